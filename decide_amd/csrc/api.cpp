@@ -1,0 +1,823 @@
+// C ABI of libdecide_hip.so: context, weights, batch layout and the forward
+// orchestration. Declarations and the reference interfaces each entry point
+// replaces are in include/decide_hip.h.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <string>
+#include <vector>
+
+#include "../../include/decide_hip.h"
+#include "common.hpp"
+
+namespace {
+
+struct DevBuf {
+  void *p = nullptr;
+  size_t cap = 0;
+};
+
+struct TensorSlot {
+  DevBuf buf;
+  int64_t n = 0;     // float32 elements expected
+  bool proj = false; // projection matrix: stored in the operand precision
+  bool wi = false;   // Wi: rows interleaved for the GeGLU epilogue
+  bool set = false;
+};
+
+struct Config {
+  int hidden = 0, inter = 0, heads = 0, layers = 0, vocab = 0;
+  float eps = 1e-5f;
+  int half_window = 64;
+  double theta_g = 160000, theta_l = 10000;
+  std::vector<uint8_t> sliding;
+  int precision = DN_PRECISION_BF16;
+};
+
+thread_local std::string g_err;  // errors without a context
+
+}  // namespace
+
+struct dn_ctx {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  hipStream_t own_stream = nullptr;
+  std::string err;
+  bool configured = false;
+  Config cfg;
+  std::map<std::string, TensorSlot> w;
+  DevBuf inv_freq;  // 32 doubles global theta, 32 local
+  // workspace
+  DevBuf h, xn, qkv, ctxb, act, rope, kinfo, ids, pos, opt, rowtok, logits, err_flag;
+  DevBuf gA, gB, gC;  // dn_gemm_f32 staging
+  // batch layout cache
+  std::vector<int> lay_len;
+  std::vector<int> h_seq_off, h_chunk_off;
+  std::vector<int4> h_chunk_desc, h_work;
+  DevBuf d_seq_off, d_seq_len, d_chunk_off, d_chunk_desc, d_work, d_chunks;
+  int lay_T = 0, lay_nchunks = 0, lay_nwork = 0;
+  // kernel probe: events[2*k], events[2*k+1] bracket launch k of one forward
+  int probe_layer = -1;
+  std::vector<hipEvent_t> probe_pool;  // 10 events per recorded forward
+  int probe_used = 0;                  // forwards recorded
+};
+
+namespace {
+
+int fail(dn_ctx *c, int code, const std::string &msg) {
+  if (c)
+    c->err = msg;
+  else
+    g_err = msg;
+  return code;
+}
+
+int hip_fail(dn_ctx *c, const char *op, hipError_t e) {
+  const int code = e == hipErrorOutOfMemory ? DN_OUT_OF_MEMORY : DN_DEVICE_ERROR;
+  return fail(c, code, std::string("hip: ") + op + " failed: " + hipGetErrorString(e) + " [code " +
+                           std::to_string((int)e) + "]");
+}
+
+#define HIPCHK(c, op, expr)                         \
+  do {                                              \
+    hipError_t e_ = (expr);                         \
+    if (e_ != hipSuccess) return hip_fail(c, op, e_); \
+  } while (0)
+
+hipError_t ensure(DevBuf &b, size_t bytes) {
+  if (bytes == 0) bytes = 16;
+  if (bytes <= b.cap) return hipSuccess;
+  if (b.p) {
+    hipError_t e = hipFree(b.p);
+    if (e != hipSuccess) return e;
+  }
+  b.p = nullptr;
+  b.cap = 0;
+  bytes = (bytes + 255) & ~(size_t)255;
+  hipError_t e = hipMalloc(&b.p, bytes);
+  if (e != hipSuccess) {
+    b.p = nullptr;
+    return e;
+  }
+  b.cap = bytes;
+  return hipSuccess;
+}
+
+void release(DevBuf &b) {
+  if (b.p) (void)hipFree(b.p);
+  b.p = nullptr;
+  b.cap = 0;
+}
+
+uint16_t f32_to_bf16_rne(float f) {
+  uint32_t u;
+  std::memcpy(&u, &f, 4);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40);  // NaN stays NaN
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+std::string layer_prefix(int l) { return "model.layers." + std::to_string(l) + "."; }
+
+void define_tensors(dn_ctx *c) {
+  const Config &g = c->cfg;
+  const int64_t H = g.hidden, I = g.inter;
+  auto add = [&](const std::string &name, int64_t n, bool proj = false, bool wi = false) {
+    TensorSlot s;
+    s.n = n;
+    s.proj = proj;
+    s.wi = wi;
+    c->w[name] = s;
+  };
+  add("model.embeddings.tok_embeddings.weight", (int64_t)g.vocab * H);
+  add("model.embeddings.norm.weight", H);
+  for (int l = 0; l < g.layers; l++) {
+    const std::string p = layer_prefix(l);
+    if (l > 0) add(p + "attn_norm.weight", H);
+    add(p + "attn.Wqkv.weight", 3 * H * H, true);
+    add(p + "attn.Wo.weight", H * H, true);
+    add(p + "mlp_norm.weight", H);
+    add(p + "mlp.Wi.weight", 2 * I * H, true, true);
+    add(p + "mlp.Wo.weight", H * I, true);
+  }
+  add("model.final_norm.weight", H);
+  add("scorer.input_norm.weight", H);
+  add("scorer.input_norm.bias", H);
+  add("scorer.dense.weight", H / 2 * H);
+  add("scorer.dense.bias", H / 2);
+  add("scorer.norm.weight", H / 2);
+  add("scorer.norm.bias", H / 2);
+  add("scorer.out_proj.weight", H / 2);
+  add("scorer.out_proj.bias", 1);
+}
+
+const void *W(dn_ctx *c, const std::string &name) { return c->w[name].buf.p; }
+
+// Batch layout: sequence offsets, 32-token chunks and 128-query work items.
+int prepare_layout(dn_ctx *c, int nseq, const int32_t *seq_len) {
+  std::vector<int> len(seq_len, seq_len + nseq);
+  if (len == c->lay_len && c->d_seq_off.p) return DN_OK;
+  HIPCHK(c, "hipStreamSynchronize", hipStreamSynchronize(c->stream));  // old host staging may be in flight
+  c->lay_len.clear();
+  c->h_seq_off.assign(nseq + 1, 0);
+  c->h_chunk_off.assign(nseq + 1, 0);
+  c->h_chunk_desc.clear();
+  c->h_work.clear();
+  int T = 0, nch = 0;
+  for (int s = 0; s < nseq; s++) {
+    const int n = len[s];
+    c->h_seq_off[s] = T;
+    c->h_chunk_off[s] = nch;
+    for (int i = 0; i < n; i += 32) c->h_chunk_desc.push_back(make_int4(T + i, std::min(32, n - i), 0, 0));
+    for (int q = 0; q < n; q += 128) c->h_work.push_back(make_int4(s, q, 0, 0));
+    nch += (n + 31) / 32;
+    T += n;
+  }
+  c->h_seq_off[nseq] = T;
+  c->h_chunk_off[nseq] = nch;
+  HIPCHK(c, "hipMalloc", ensure(c->d_seq_off, sizeof(int) * (nseq + 1)));
+  HIPCHK(c, "hipMalloc", ensure(c->d_seq_len, sizeof(int) * (nseq + 1)));
+  HIPCHK(c, "hipMalloc", ensure(c->d_chunk_off, sizeof(int) * (nseq + 1)));
+  HIPCHK(c, "hipMalloc", ensure(c->d_chunk_desc, sizeof(int4) * (nch + 1)));
+  HIPCHK(c, "hipMalloc", ensure(c->d_chunks, sizeof(ChunkInfo) * (nch + 1)));
+  HIPCHK(c, "hipMalloc", ensure(c->d_work, sizeof(int4) * (c->h_work.size() + 1)));
+  c->lay_len = len;
+  HIPCHK(c, "hipMemcpyAsync", hipMemcpyAsync(c->d_seq_off.p, c->h_seq_off.data(), sizeof(int) * (nseq + 1),
+                                             hipMemcpyHostToDevice, c->stream));
+  HIPCHK(c, "hipMemcpyAsync",
+         hipMemcpyAsync(c->d_seq_len.p, c->lay_len.data(), sizeof(int) * nseq, hipMemcpyHostToDevice, c->stream));
+  HIPCHK(c, "hipMemcpyAsync", hipMemcpyAsync(c->d_chunk_off.p, c->h_chunk_off.data(), sizeof(int) * (nseq + 1),
+                                             hipMemcpyHostToDevice, c->stream));
+  if (nch)
+    HIPCHK(c, "hipMemcpyAsync", hipMemcpyAsync(c->d_chunk_desc.p, c->h_chunk_desc.data(), sizeof(int4) * nch,
+                                               hipMemcpyHostToDevice, c->stream));
+  if (!c->h_work.empty())
+    HIPCHK(c, "hipMemcpyAsync", hipMemcpyAsync(c->d_work.p, c->h_work.data(), sizeof(int4) * c->h_work.size(),
+                                               hipMemcpyHostToDevice, c->stream));
+  c->lay_T = T;
+  c->lay_nchunks = nch;
+  c->lay_nwork = (int)c->h_work.size();
+  return DN_OK;
+}
+
+// The device-side error flag: allocated and zeroed once per context.
+int ensure_err_flag(dn_ctx *c) {
+  if (c->err_flag.p) return DN_OK;
+  HIPCHK(c, "hipMalloc", ensure(c->err_flag, sizeof(int)));
+  HIPCHK(c, "hipMemsetAsync", hipMemsetAsync(c->err_flag.p, 0, sizeof(int), c->stream));
+  return DN_OK;
+}
+
+int check_ready(dn_ctx *c) {
+  if (!c->configured) return fail(c, DN_INVALID_ARG, "decide_hip: dn_set_config has not been called");
+  if (!dn_weights_ready(c)) {
+    for (auto &kv : c->w)
+      if (!kv.second.set) return fail(c, DN_INVALID_ARG, "decide_hip: weight " + kv.first + " not uploaded");
+  }
+  return DN_OK;
+}
+
+// Returns the event pair slot for launch k of the current forward, or null
+// when the probe is off for this layer.
+hipEvent_t *probe_slot(dn_ctx *c, int l) {
+  if (c->probe_layer != l) return nullptr;
+  const size_t need = (size_t)(c->probe_used + 1) * 10;
+  while (c->probe_pool.size() < need) {
+    hipEvent_t e;
+    if (hipEventCreate(&e) != hipSuccess) return nullptr;
+    c->probe_pool.push_back(e);
+  }
+  return &c->probe_pool[(size_t)c->probe_used * 10];
+}
+
+#define PROBED(slot, k, op, call)                                              \
+  do {                                                                         \
+    if (slot) HIPCHK(c, "hipEventRecord", hipEventRecord((slot)[2 * (k)], s)); \
+    HIPCHK(c, op, call);                                                       \
+    if (slot) HIPCHK(c, "hipEventRecord", hipEventRecord((slot)[2 * (k) + 1], s)); \
+  } while (0)
+
+int forward_core(dn_ctx *c, int nseq, const int32_t *seq_len, const int32_t *d_ids, const int32_t *d_pos,
+                 const int32_t *d_opt, int R, const int32_t *d_row_tok, float *d_logits) {
+  const Config &g = c->cfg;
+  const int H = g.hidden, I = g.inter, L = g.layers;
+  const int prec = g.precision;
+  const size_t es = prec == DN_PRECISION_BF16 ? 2 : 4;
+  int rc = prepare_layout(c, nseq, seq_len);
+  if (rc) return rc;
+  const int T = c->lay_T;
+  hipStream_t s = c->stream;
+  HIPCHK(c, "hipMalloc", ensure(c->h, sizeof(float) * T * H));
+  HIPCHK(c, "hipMalloc", ensure(c->xn, es * T * H));
+  HIPCHK(c, "hipMalloc", ensure(c->qkv, es * T * 3 * H));
+  HIPCHK(c, "hipMalloc", ensure(c->ctxb, es * T * H));
+  HIPCHK(c, "hipMalloc", ensure(c->act, es * T * I));
+  HIPCHK(c, "hipMalloc", ensure(c->rope, sizeof(float) * T * 32 * 4));
+  HIPCHK(c, "hipMalloc", ensure(c->kinfo, sizeof(int) * T));
+  rc = ensure_err_flag(c);
+  if (rc) return rc;
+
+  float *h = (float *)c->h.p;
+  float *rope = (float *)c->rope.p;
+  float *cos_g = rope, *sin_g = rope + (size_t)T * 32, *cos_l = rope + (size_t)2 * T * 32,
+        *sin_l = rope + (size_t)3 * T * 32;
+  int *kinfo = (int *)c->kinfo.p;
+  const double *inv = (const double *)c->inv_freq.p;
+
+  HIPCHK(c, "token_info", launch_token_info(d_pos, d_opt, kinfo, T, s));
+  HIPCHK(c, "chunk_summary", launch_chunk_summary(kinfo, (const int4 *)c->d_chunk_desc.p,
+                                                  (ChunkInfo *)c->d_chunks.p, c->lay_nchunks, s));
+  HIPCHK(c, "rope_tables", launch_rope_tables(d_pos, T, inv, inv + 32, cos_g, sin_g, cos_l, sin_l, s));
+  HIPCHK(c, "embed_ln",
+         launch_embed_ln(prec, d_ids, T, (const float *)W(c, "model.embeddings.tok_embeddings.weight"), g.vocab,
+                         (const float *)W(c, "model.embeddings.norm.weight"), g.eps, H, h, c->xn.p,
+                         (int *)c->err_flag.p, s));
+
+  AttnArgs at{};
+  at.qkv = c->qkv.p;
+  at.ctx = c->ctxb.p;
+  at.kinfo = kinfo;
+  at.chunks = (const ChunkInfo *)c->d_chunks.p;
+  at.work = (const int4 *)c->d_work.p;
+  at.seq_off = (const int *)c->d_seq_off.p;
+  at.seq_len = (const int *)c->d_seq_len.p;
+  at.chunk_off = (const int *)c->d_chunk_off.p;
+  at.nwork = c->lay_nwork;
+  at.H = H;
+  at.heads = g.heads;
+  at.half_window = g.half_window;
+  at.scale_log2 = (float)(1.0 / std::sqrt(64.0)) * 1.44269504088896340736f;
+
+  bool probed = false;
+  for (int l = 0; l < L; l++) {
+    const std::string p = layer_prefix(l);
+    const bool sliding = g.sliding[l] != 0;
+    hipEvent_t *ev = probe_slot(c, l);
+    probed |= ev != nullptr;
+    if (l > 0)
+      HIPCHK(c, "ln(attn_norm)", launch_ln(prec, h, T, H, (const float *)W(c, p + "attn_norm.weight"), g.eps,
+                                           c->xn.p, s));
+    GemmArgs q{};
+    q.A = c->xn.p;
+    q.lda = H;
+    q.B = W(c, p + "attn.Wqkv.weight");
+    q.ldb = H;
+    q.C = c->qkv.p;
+    q.ldc = 3 * H;
+    q.M = T;
+    q.N = 3 * H;
+    q.K = H;
+    q.n_store = 3 * H;
+    q.rope_cols = 2 * H;
+    q.cos_t = sliding ? cos_l : cos_g;
+    q.sin_t = sliding ? sin_l : sin_g;
+    PROBED(ev, DN_PROBE_QKV, "gemm(Wqkv)", launch_gemm(prec, EPI_QKV, q, s));
+
+    at.sliding = sliding ? 1 : 0;
+    PROBED(ev, DN_PROBE_ATTENTION, "attention", launch_attention(prec, at, s));
+
+    GemmArgs o{};
+    o.A = c->ctxb.p;
+    o.lda = H;
+    o.B = W(c, p + "attn.Wo.weight");
+    o.ldb = H;
+    o.C = h;
+    o.ldc = H;
+    o.M = T;
+    o.N = H;
+    o.K = H;
+    o.n_store = H;
+    o.accumulate = 1;
+    PROBED(ev, DN_PROBE_WO, "gemm(Wo)", launch_gemm(prec, EPI_F32, o, s));
+
+    HIPCHK(c, "ln(mlp_norm)",
+           launch_ln(prec, h, T, H, (const float *)W(c, p + "mlp_norm.weight"), g.eps, c->xn.p, s));
+
+    GemmArgs wi{};
+    wi.A = c->xn.p;
+    wi.lda = H;
+    wi.B = W(c, p + "mlp.Wi.weight");
+    wi.ldb = H;
+    wi.C = c->act.p;
+    wi.ldc = I;
+    wi.M = T;
+    wi.N = 2 * I;
+    wi.K = H;
+    wi.n_store = 2 * I;
+    PROBED(ev, DN_PROBE_WI, "gemm(Wi)", launch_gemm(prec, EPI_GEGLU, wi, s));
+
+    GemmArgs mo{};
+    mo.A = c->act.p;
+    mo.lda = I;
+    mo.B = W(c, p + "mlp.Wo.weight");
+    mo.ldb = I;
+    mo.C = h;
+    mo.ldc = H;
+    mo.M = T;
+    mo.N = H;
+    mo.K = I;
+    mo.n_store = H;
+    mo.accumulate = 1;
+    PROBED(ev, DN_PROBE_MLPWO, "gemm(MlpWo)", launch_gemm(prec, EPI_F32, mo, s));
+  }
+  if (probed) c->probe_used++;
+
+  HeadArgs ha{};
+  ha.h = h;
+  ha.row_tok = d_row_tok;
+  ha.R = R;
+  ha.T = T;
+  ha.H = H;
+  ha.eps = g.eps;
+  ha.final_norm = (const float *)W(c, "model.final_norm.weight");
+  ha.in_w = (const float *)W(c, "scorer.input_norm.weight");
+  ha.in_b = (const float *)W(c, "scorer.input_norm.bias");
+  ha.dense_w = (const float *)W(c, "scorer.dense.weight");
+  ha.dense_b = (const float *)W(c, "scorer.dense.bias");
+  ha.norm_w = (const float *)W(c, "scorer.norm.weight");
+  ha.norm_b = (const float *)W(c, "scorer.norm.bias");
+  ha.out_w = (const float *)W(c, "scorer.out_proj.weight");
+  ha.out_b = (const float *)W(c, "scorer.out_proj.bias");
+  ha.logits = d_logits;
+  ha.err_flag = (int *)c->err_flag.p;
+  HIPCHK(c, "head", launch_head(ha, s));
+  return DN_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int dn_abi_version(void) { return DN_ABI_VERSION; }
+
+const char *dn_status_string(int status) {
+  switch (status) {
+    case DN_OK: return "ok";
+    case DN_NO_GPU: return "no GPU";
+    case DN_INVALID_ARG: return "invalid argument";
+    case DN_OUT_OF_MEMORY: return "out of memory";
+    case DN_DEVICE_ERROR: return "device error";
+    case DN_UNSUPPORTED: return "unsupported";
+  }
+  return "unknown status";
+}
+
+int dn_open(int device, dn_ctx **out) {
+  if (!out) return fail(nullptr, DN_INVALID_ARG, "decide_hip: dn_open: out is NULL");
+  *out = nullptr;
+  int count = 0;
+  hipError_t e = hipGetDeviceCount(&count);
+  if (e != hipSuccess || count == 0)
+    return fail(nullptr, DN_NO_GPU, std::string("decide_hip: no GPU (") +
+                                        (e != hipSuccess ? hipGetErrorString(e) : "0 devices") + ")");
+  if (device < 0 || device >= count)
+    return fail(nullptr, DN_INVALID_ARG, "decide_hip: device " + std::to_string(device) + " out of range");
+  e = hipSetDevice(device);
+  if (e != hipSuccess) return hip_fail(nullptr, "hipSetDevice", e);
+  dn_ctx *c = new dn_ctx;
+  c->device = device;
+  e = hipStreamCreateWithFlags(&c->own_stream, hipStreamNonBlocking);
+  if (e != hipSuccess) {
+    delete c;
+    return hip_fail(nullptr, "hipStreamCreate", e);
+  }
+  c->stream = c->own_stream;
+  *out = c;
+  return DN_OK;
+}
+
+void dn_close(dn_ctx *c) {
+  if (!c) return;
+  (void)hipSetDevice(c->device);
+  if (c->stream) (void)hipStreamSynchronize(c->stream);
+  for (auto &kv : c->w) release(kv.second.buf);
+  for (hipEvent_t e : c->probe_pool) (void)hipEventDestroy(e);
+  DevBuf *bufs[] = {&c->inv_freq, &c->h,     &c->xn,       &c->qkv,         &c->ctxb,     &c->act,
+                    &c->rope,     &c->kinfo, &c->ids,      &c->pos,         &c->opt,      &c->rowtok,
+                    &c->logits,   &c->err_flag, &c->gA,    &c->gB,          &c->gC,       &c->d_seq_off,
+                    &c->d_seq_len, &c->d_chunk_off, &c->d_chunk_desc, &c->d_work, &c->d_chunks};
+  for (DevBuf *b : bufs) release(*b);
+  if (c->own_stream) (void)hipStreamDestroy(c->own_stream);
+  delete c;
+}
+
+const char *dn_last_error(const dn_ctx *c) { return c ? c->err.c_str() : g_err.c_str(); }
+
+int dn_set_stream(dn_ctx *c, void *stream) {
+  if (!c) return DN_INVALID_ARG;
+  c->stream = stream ? (hipStream_t)stream : c->own_stream;
+  return DN_OK;
+}
+
+int dn_set_config(dn_ctx *c, int hidden, int inter, int heads, int layers, int vocab, float eps, int half_window,
+                  double theta_global, double theta_local, const uint8_t *layer_is_sliding, int precision) {
+  if (!c) return DN_INVALID_ARG;
+  c->err.clear();
+  if (hidden <= 0 || inter <= 0 || heads <= 0 || layers <= 0 || vocab <= 0 || !layer_is_sliding ||
+      hidden % heads != 0 || hidden % 2 != 0)
+    return fail(c, DN_INVALID_ARG, "nn: incomplete or inconsistent config");
+  if (precision != DN_PRECISION_FP32 && precision != DN_PRECISION_BF16)
+    return fail(c, DN_INVALID_ARG, "decide_hip: unknown precision " + std::to_string(precision));
+  if (hidden / heads != 64 || hidden % 128 != 0 || inter % 64 != 0 || hidden > 1024)
+    return fail(c, DN_UNSUPPORTED, "decide_hip: this build implements head_dim 64, hidden % 128 == 0 (<= 1024) "
+                                   "and intermediate % 64 == 0");
+  (void)hipSetDevice(c->device);
+  for (auto &kv : c->w) release(kv.second.buf);
+  c->w.clear();
+  Config &g = c->cfg;
+  g.hidden = hidden;
+  g.inter = inter;
+  g.heads = heads;
+  g.layers = layers;
+  g.vocab = vocab;
+  g.eps = eps == 0 ? 1e-5f : eps;
+  g.half_window = half_window == 0 ? 64 : half_window;
+  g.theta_g = theta_global;
+  g.theta_l = theta_local;
+  g.sliding.assign(layer_is_sliding, layer_is_sliding + layers);
+  g.precision = precision;
+  define_tensors(c);
+  // inv_freq_i = 1 / theta^(2i/64), model.go:244-247.
+  double inv[64];
+  for (int i = 0; i < 32; i++) {
+    inv[i] = 1.0 / std::pow(theta_global, (double)(2 * i) / 64.0);
+    inv[32 + i] = 1.0 / std::pow(theta_local, (double)(2 * i) / 64.0);
+  }
+  HIPCHK(c, "hipMalloc", ensure(c->inv_freq, sizeof(inv)));
+  HIPCHK(c, "hipMemcpy", hipMemcpy(c->inv_freq.p, inv, sizeof(inv), hipMemcpyHostToDevice));
+  c->configured = true;
+  return DN_OK;
+}
+
+int dn_upload_tensor(dn_ctx *c, const char *name, const float *data, int64_t n) {
+  if (!c) return DN_INVALID_ARG;
+  c->err.clear();
+  if (!c->configured) return fail(c, DN_INVALID_ARG, "decide_hip: dn_set_config has not been called");
+  if (!name || !data) return fail(c, DN_INVALID_ARG, "decide_hip: dn_upload_tensor: NULL argument");
+  auto it = c->w.find(name);
+  if (it == c->w.end()) return fail(c, DN_INVALID_ARG, std::string("decide_hip: unknown tensor ") + name);
+  TensorSlot &t = it->second;
+  if (n != t.n)
+    return fail(c, DN_INVALID_ARG, std::string("nn: ") + name + " has " + std::to_string(n) +
+                                       " values, model expects " + std::to_string(t.n));
+  (void)hipSetDevice(c->device);
+  const bool bf = t.proj && c->cfg.precision == DN_PRECISION_BF16;
+  const size_t bytes = (size_t)n * (bf ? 2 : 4);
+  HIPCHK(c, "hipMalloc", ensure(t.buf, bytes));
+  const int64_t H = c->cfg.hidden, I = c->cfg.inter;
+  // Row order: Wi's value rows [0,I) and gate rows [I,2I) are interleaved in
+  // groups of 32: stored row 64g+r is value row 32g+r (r < 32) or gate row
+  // I+32g+r-32 (r >= 32).
+  auto src_row = [&](int64_t r) -> int64_t {
+    if (!t.wi) return r;
+    const int64_t g = r / 64, k = r % 64;
+    return k < 32 ? 32 * g + k : I + 32 * g + (k - 32);
+  };
+  const int64_t rows = t.wi ? 2 * I : 0;
+  if (bf) {
+    std::vector<uint16_t> tmp((size_t)n);
+    if (t.wi) {
+      for (int64_t r = 0; r < rows; r++) {
+        const float *s = data + src_row(r) * H;
+        for (int64_t k = 0; k < H; k++) tmp[r * H + k] = f32_to_bf16_rne(s[k]);
+      }
+    } else {
+      for (int64_t i = 0; i < n; i++) tmp[i] = f32_to_bf16_rne(data[i]);
+    }
+    HIPCHK(c, "hipMemcpy", hipMemcpy(t.buf.p, tmp.data(), bytes, hipMemcpyHostToDevice));
+  } else if (t.wi) {
+    std::vector<float> tmp((size_t)n);
+    for (int64_t r = 0; r < rows; r++) std::memcpy(&tmp[r * H], data + src_row(r) * H, sizeof(float) * H);
+    HIPCHK(c, "hipMemcpy", hipMemcpy(t.buf.p, tmp.data(), bytes, hipMemcpyHostToDevice));
+  } else {
+    HIPCHK(c, "hipMemcpy", hipMemcpy(t.buf.p, data, bytes, hipMemcpyHostToDevice));
+  }
+  t.set = true;
+  return DN_OK;
+}
+
+int dn_weights_ready(const dn_ctx *c) {
+  if (!c || !c->configured) return 0;
+  for (auto &kv : c->w)
+    if (!kv.second.set) return 0;
+  return 1;
+}
+
+int dn_forward(dn_ctx *c, int nseq, const int32_t *seq_len, const int32_t *ids, const int32_t *pos,
+               const int32_t *opt_id, const int32_t *nmask, const int32_t *mask_pos, float *logits, int logits_cap) {
+  if (!c) return DN_INVALID_ARG;
+  c->err.clear();
+  int rc = check_ready(c);
+  if (rc) return rc;
+  if (nseq < 0 || (nseq > 0 && (!seq_len || !ids || !pos || !nmask)))
+    return fail(c, DN_INVALID_ARG, "decide_hip: dn_forward: NULL argument");
+  const Config &g = c->cfg;
+  // Validation, forward.go:142-196.
+  std::vector<int32_t> row_tok;
+  int64_t T = 0, mp = 0;
+  for (int si = 0; si < nseq; si++) {
+    const int n = seq_len[si];
+    if (n <= 0) return fail(c, DN_INVALID_ARG, "nn: malformed sequence " + std::to_string(si));
+    if (nmask[si] <= 0) return fail(c, DN_INVALID_ARG, "nn: sequence " + std::to_string(si) + " has no options");
+    for (int k = 0; k < nmask[si]; k++) {
+      const int m = mask_pos[mp + k];
+      if (m < 0 || m >= n)
+        return fail(c, DN_INVALID_ARG, "nn: sequence " + std::to_string(si) + " mask position " +
+                                           std::to_string(m) + " out of range");
+      row_tok.push_back((int32_t)(T + m));
+    }
+    mp += nmask[si];
+    T += n;
+  }
+  if (T > (1 << 30)) return fail(c, DN_UNSUPPORTED, "decide_hip: batch too large");
+  for (int64_t t = 0; t < T; t++)
+    if (ids[t] < 0 || ids[t] >= g.vocab)
+      return fail(c, DN_INVALID_ARG, "nn: token id " + std::to_string(ids[t]) + " out of range");
+  // The attention kernel packs (option id + 1, position) into 16 bits each.
+  for (int64_t t = 0; t < T; t++) {
+    if (pos[t] < 0 || pos[t] > 0xffff)
+      return fail(c, DN_UNSUPPORTED, "decide_hip: position id " + std::to_string(pos[t]) + " outside [0, 65535]");
+    if (opt_id && (opt_id[t] < -1 || opt_id[t] > 32765))
+      return fail(c, DN_UNSUPPORTED, "decide_hip: option id " + std::to_string(opt_id[t]) + " outside [-1, 32765]");
+  }
+  const int R = (int)row_tok.size();
+  if (logits_cap < R) return fail(c, DN_INVALID_ARG, "decide_hip: logits buffer holds fewer than " +
+                                                         std::to_string(R) + " values");
+  if (T == 0) return DN_OK;
+  (void)hipSetDevice(c->device);
+  hipStream_t s = c->stream;
+  HIPCHK(c, "hipMalloc", ensure(c->ids, sizeof(int) * T));
+  HIPCHK(c, "hipMalloc", ensure(c->pos, sizeof(int) * T));
+  HIPCHK(c, "hipMalloc", ensure(c->opt, sizeof(int) * T));
+  HIPCHK(c, "hipMalloc", ensure(c->rowtok, sizeof(int) * R));
+  HIPCHK(c, "hipMalloc", ensure(c->logits, sizeof(float) * R));
+  rc = ensure_err_flag(c);
+  if (rc) return rc;
+  HIPCHK(c, "hipMemsetAsync", hipMemsetAsync(c->err_flag.p, 0, sizeof(int), s));
+  HIPCHK(c, "hipMemcpyAsync", hipMemcpyAsync(c->ids.p, ids, sizeof(int) * T, hipMemcpyHostToDevice, s));
+  HIPCHK(c, "hipMemcpyAsync", hipMemcpyAsync(c->pos.p, pos, sizeof(int) * T, hipMemcpyHostToDevice, s));
+  if (opt_id)
+    HIPCHK(c, "hipMemcpyAsync", hipMemcpyAsync(c->opt.p, opt_id, sizeof(int) * T, hipMemcpyHostToDevice, s));
+  HIPCHK(c, "hipMemcpyAsync",
+         hipMemcpyAsync(c->rowtok.p, row_tok.data(), sizeof(int) * R, hipMemcpyHostToDevice, s));
+  rc = forward_core(c, nseq, seq_len, (const int32_t *)c->ids.p, (const int32_t *)c->pos.p,
+                    opt_id ? (const int32_t *)c->opt.p : nullptr, R, (const int32_t *)c->rowtok.p,
+                    (float *)c->logits.p);
+  if (rc) return rc;
+  HIPCHK(c, "hipMemcpyAsync", hipMemcpyAsync(logits, c->logits.p, sizeof(float) * R, hipMemcpyDeviceToHost, s));
+  int flag = 0;
+  HIPCHK(c, "hipMemcpyAsync", hipMemcpyAsync(&flag, c->err_flag.p, sizeof(int), hipMemcpyDeviceToHost, s));
+  HIPCHK(c, "hipStreamSynchronize", hipStreamSynchronize(s));
+  if (flag) return fail(c, DN_DEVICE_ERROR, "decide_hip: device saw an out-of-range index after validation");
+  return DN_OK;
+}
+
+int dn_forward_device(dn_ctx *c, int nseq, const int32_t *seq_len, const int32_t *d_ids, const int32_t *d_pos,
+                      const int32_t *d_opt_id, int nrows, const int32_t *d_row_tok, float *d_logits) {
+  if (!c) return DN_INVALID_ARG;
+  c->err.clear();
+  int rc = check_ready(c);
+  if (rc) return rc;
+  if (nseq <= 0 || !seq_len || !d_ids || !d_pos || nrows < 0 || (nrows > 0 && (!d_row_tok || !d_logits)))
+    return fail(c, DN_INVALID_ARG, "decide_hip: dn_forward_device: bad argument");
+  for (int s = 0; s < nseq; s++)
+    if (seq_len[s] <= 0) return fail(c, DN_INVALID_ARG, "nn: malformed sequence " + std::to_string(s));
+  (void)hipSetDevice(c->device);
+  return forward_core(c, nseq, seq_len, d_ids, d_pos, d_opt_id, nrows, d_row_tok, d_logits);
+}
+
+int dn_check_device_errors(dn_ctx *c) {
+  if (!c) return DN_INVALID_ARG;
+  c->err.clear();
+  if (!c->err_flag.p) return DN_OK;
+  int flag = 0;
+  HIPCHK(c, "hipMemcpyAsync", hipMemcpyAsync(&flag, c->err_flag.p, sizeof(int), hipMemcpyDeviceToHost, c->stream));
+  HIPCHK(c, "hipStreamSynchronize", hipStreamSynchronize(c->stream));
+  if (flag) {
+    HIPCHK(c, "hipMemsetAsync", hipMemsetAsync(c->err_flag.p, 0, sizeof(int), c->stream));
+    HIPCHK(c, "hipStreamSynchronize", hipStreamSynchronize(c->stream));
+    return fail(c, DN_INVALID_ARG, (flag & 1) ? "nn: token id out of range" : "nn: mask position out of range");
+  }
+  return DN_OK;
+}
+
+int dn_gemm_f32(dn_ctx *c, int transA, int transB, int M, int N, int K, const float *A, int lda, const float *B,
+                int ldb, float *C, int ldc, int accumulate) {
+  if (!c) return DN_INVALID_ARG;
+  c->err.clear();
+  if (M < 0 || N < 0 || K < 0) return fail(c, DN_INVALID_ARG, "decide_hip: negative GEMM dimension");
+  if (M == 0 || N == 0) return DN_OK;
+  if (!C || ldc < N) return fail(c, DN_INVALID_ARG, "decide_hip: bad C / ldc");
+  if (K > 0) {
+    if (!A || !B) return fail(c, DN_INVALID_ARG, "decide_hip: NULL operand");
+    if (lda < (transA ? M : K) || ldb < (transB ? K : N))
+      return fail(c, DN_INVALID_ARG, "decide_hip: leading dimension too small");
+  }
+  (void)hipSetDevice(c->device);
+  hipStream_t s = c->stream;
+  const int Kp = K == 0 ? 32 : (K + 31) / 32 * 32;
+  const int Np = (N + 127) / 128 * 128;
+  // Stage op(A) as M x Kp and op(B) as Np x Kp (zero padded), the device
+  // counterpart of packA/packB (gemm.go:147-195).
+  const size_t a_rows = transA ? K : M, a_cols = transA ? M : K;
+  const size_t b_rows = transB ? N : K, b_cols = transB ? K : N;
+  const size_t a_span = K ? (a_rows - 1) * lda + a_cols : 0, b_span = K ? (b_rows - 1) * ldb + b_cols : 0;
+  HIPCHK(c, "hipMalloc", ensure(c->gA, sizeof(float) * (a_span + (size_t)M * Kp)));
+  HIPCHK(c, "hipMalloc", ensure(c->gB, sizeof(float) * (b_span + (size_t)Np * Kp)));
+  HIPCHK(c, "hipMalloc", ensure(c->gC, sizeof(float) * (size_t)M * N));
+  float *rawA = (float *)c->gA.p, *Ap = rawA + a_span;
+  float *rawB = (float *)c->gB.p, *Bp = rawB + b_span;
+  float *Cd = (float *)c->gC.p;
+  if (K) {
+    HIPCHK(c, "hipMemcpyAsync", hipMemcpyAsync(rawA, A, sizeof(float) * a_span, hipMemcpyHostToDevice, s));
+    HIPCHK(c, "hipMemcpyAsync", hipMemcpyAsync(rawB, B, sizeof(float) * b_span, hipMemcpyHostToDevice, s));
+  }
+  // op(A) is M x K: element (i,k) = transA ? A[k*lda+i] : A[i*lda+k].
+  HIPCHK(c, "pack(A)", launch_pack(rawA, transA, M, K, lda, Ap, M, Kp, s));
+  // B operand rows are output columns: row j = op(B)[:, j], element (j,k) =
+  // transB ? B[j*ldb+k] : B[k*ldb+j].
+  HIPCHK(c, "pack(B)", launch_pack(rawB, !transB, N, K, ldb, Bp, Np, Kp, s));
+  if (accumulate) {
+    HIPCHK(c, "hipMemcpy2DAsync", hipMemcpy2DAsync(Cd, sizeof(float) * N, C, sizeof(float) * ldc,
+                                                   sizeof(float) * N, M, hipMemcpyHostToDevice, s));
+  }
+  GemmArgs a{};
+  a.A = Ap;
+  a.lda = Kp;
+  a.B = Bp;
+  a.ldb = Kp;
+  a.C = Cd;
+  a.ldc = N;
+  a.M = M;
+  a.N = Np;
+  a.K = Kp;
+  a.n_store = N;
+  a.accumulate = accumulate ? 1 : 0;
+  HIPCHK(c, "gemm", launch_gemm(DN_PRECISION_FP32, EPI_F32, a, s));
+  HIPCHK(c, "hipMemcpy2DAsync", hipMemcpy2DAsync(C, sizeof(float) * ldc, Cd, sizeof(float) * N, sizeof(float) * N,
+                                                 M, hipMemcpyDeviceToHost, s));
+  HIPCHK(c, "hipStreamSynchronize", hipStreamSynchronize(s));
+  return DN_OK;
+}
+
+int dn_gemm_device(dn_ctx *c, int precision, int M, int N, int K, const void *d_A, const void *d_B, float *d_C,
+                   int accumulate) {
+  if (!c) return DN_INVALID_ARG;
+  c->err.clear();
+  if (precision != DN_PRECISION_FP32 && precision != DN_PRECISION_BF16)
+    return fail(c, DN_INVALID_ARG, "decide_hip: unknown precision");
+  if (M < 0 || !d_A || !d_B || !d_C) return fail(c, DN_INVALID_ARG, "decide_hip: dn_gemm_device: bad argument");
+  if (!gemm_shape_ok(precision, N, K))
+    return fail(c, DN_UNSUPPORTED, "decide_hip: dn_gemm_device needs N % 128 == 0 and K % 64 (bf16) / 32 (fp32)");
+  (void)hipSetDevice(c->device);
+  GemmArgs a{};
+  a.A = d_A;
+  a.lda = K;
+  a.B = d_B;
+  a.ldb = K;
+  a.C = d_C;
+  a.ldc = N;
+  a.M = M;
+  a.N = N;
+  a.K = K;
+  a.n_store = N;
+  a.accumulate = accumulate ? 1 : 0;
+  HIPCHK(c, "gemm", launch_gemm(precision, EPI_F32, a, c->stream));
+  return DN_OK;
+}
+
+int dn_synchronize(dn_ctx *c) {
+  if (!c) return DN_INVALID_ARG;
+  HIPCHK(c, "hipStreamSynchronize", hipStreamSynchronize(c->stream));
+  return DN_OK;
+}
+
+int dn_set_probe(dn_ctx *c, int layer) {
+  if (!c) return DN_INVALID_ARG;
+  c->err.clear();
+  if (c->probe_used) HIPCHK(c, "hipStreamSynchronize", hipStreamSynchronize(c->stream));
+  c->probe_layer = layer;
+  c->probe_used = 0;
+  return DN_OK;
+}
+
+int dn_read_probe(dn_ctx *c, double *ms, int *count) {
+  if (!c || !ms || !count) return DN_INVALID_ARG;
+  c->err.clear();
+  HIPCHK(c, "hipStreamSynchronize", hipStreamSynchronize(c->stream));
+  for (int f = 0; f < c->probe_used; f++)
+    for (int k = 0; k < 5; k++) {
+      float t = 0;
+      HIPCHK(c, "hipEventElapsedTime",
+             hipEventElapsedTime(&t, c->probe_pool[(size_t)f * 10 + 2 * k], c->probe_pool[(size_t)f * 10 + 2 * k + 1]));
+      ms[k] += t;
+    }
+  *count += c->probe_used;
+  c->probe_used = 0;
+  return DN_OK;
+}
+
+int dn_build_sequence(const int32_t *ids, int n, int32_t mask_id, int independent, int32_t *pos, int32_t *opt_id,
+                      int32_t *mask_pos, int *has_opt) {
+  if (n < 0 || (n > 0 && (!ids || !pos || !mask_pos)) || !has_opt) return -1;
+  int nm = 0;
+  for (int i = 0; i < n; i++) {
+    pos[i] = i;
+    if (ids[i] == mask_id) mask_pos[nm++] = i;
+  }
+  *has_opt = 0;
+  if (!independent || nm == 0) return nm;
+  if (!opt_id) return -1;
+  // The trailing token (the final [SEP]) belongs to no option; options
+  // restart their positions right after the prefix (forward.go:39-54).
+  const int last = n - 1, prefix = mask_pos[0];
+  for (int i = 0; i < n; i++) opt_id[i] = -1;
+  for (int k = 0; k < nm; k++) {
+    const int start = mask_pos[k], end = k + 1 < nm ? mask_pos[k + 1] : last;
+    for (int i = start; i < end; i++) {
+      opt_id[i] = k;
+      pos[i] = prefix + i - start;
+    }
+  }
+  *has_opt = 1;
+  return nm;
+}
+
+double dn_round(double x, int places) {
+  const double p = std::pow(10.0, (double)places);
+  return std::nearbyint(x * p) / p;
+}
+
+int dn_answer(const double *logits, int k, double temperature, double *probs, int *choice, double *confidence) {
+  if (k <= 0 || !logits || !probs || !choice || !confidence) return DN_INVALID_ARG;
+  // calibrated + softmax (local.go:206-232).
+  const double t = std::fmax(temperature, 1e-4);
+  double maxv = -INFINITY;
+  for (int i = 0; i < k; i++) maxv = std::fmax(maxv, logits[i] / t);
+  double sum = 0;
+  for (int i = 0; i < k; i++) {
+    probs[i] = std::exp(logits[i] / t - maxv);
+    sum += probs[i];
+  }
+  for (int i = 0; i < k; i++) probs[i] /= sum;
+  // argmax of raw logits, first index wins ties (local.go:254-262).
+  int best = 0;
+  for (int i = 0; i < k; i++)
+    if (logits[i] > logits[best]) best = i;
+  *choice = best;
+  // marginConfidence (local.go:241-252).
+  if (k <= 1) {
+    *confidence = 1.0;
+  } else {
+    double pmax = 0;
+    for (int i = 0; i < k; i++) pmax = std::fmax(pmax, probs[i]);
+    const double cf = ((double)k * pmax - 1) / (double)(k - 1);
+    *confidence = dn_round(std::fmax(0.0, std::fmin(1.0, cf)), 3);
+  }
+  return DN_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,122 @@
+// Shared device-side definitions for the gfx950 encoder kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+typedef __bf16 bf16;
+typedef bf16 bf16x8 __attribute__((__vector_size__(8 * sizeof(bf16))));
+typedef bf16 bf16x4 __attribute__((__vector_size__(4 * sizeof(bf16))));
+typedef float f32x16 __attribute__((__vector_size__(16 * sizeof(float))));
+typedef float f32x4 __attribute__((__vector_size__(4 * sizeof(float))));
+
+// Per-element-type MFMA shape. Both element types use the 32x32 output
+// layout (16 fp32 accumulators per lane): lane l owns output column l%32 and
+// rows 8*(i/4) + 4*(l/32) + i%4 for accumulator i. Operand layout: lane l
+// feeds row (A) / column (B) l%32 with SLOTS consecutive k values starting at
+// (l/32)*SLOTS inside each KSTEP-wide k step.
+template <class T>
+struct Mfma;
+
+template <>
+struct Mfma<bf16> {
+  static constexpr int KSTEP = 16;  // v_mfma_f32_32x32x16_bf16
+  static constexpr int SLOTS = 8;
+  typedef bf16x8 frag;
+  static __device__ __forceinline__ f32x16 mma(frag a, frag b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  }
+};
+
+template <>
+struct Mfma<float> {
+  static constexpr int KSTEP = 2;  // v_mfma_f32_32x32x2_f32
+  static constexpr int SLOTS = 1;
+  typedef float frag;
+  static __device__ __forceinline__ f32x16 mma(frag a, frag b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+  }
+};
+
+// Row (M) index inside a 32x32 MFMA output tile of accumulator i on this lane.
+__device__ __forceinline__ int mfma_row(int i, int lane) { return 8 * (i >> 2) + 4 * (lane >> 5) + (i & 3); }
+
+template <class T>
+__device__ __forceinline__ T to_elem(float x);
+template <>
+__device__ __forceinline__ float to_elem<float>(float x) { return x; }
+template <>
+__device__ __forceinline__ bf16 to_elem<bf16>(float x) { return (bf16)x; }
+
+// GELU, exact erf form: 0.5*x*(1 + erf(x/sqrt2)) (internal/nn/ops.go:140-142).
+// The fp32 validation build evaluates erf in double as the reference does.
+template <class T>
+__device__ __forceinline__ float gelu_erf(float x);
+template <>
+__device__ __forceinline__ float gelu_erf<float>(float x) {
+  return 0.5f * x * (1.0f + (float)erf((double)x * 1.41421356237309504880 / 2.0));
+}
+template <>
+__device__ __forceinline__ float gelu_erf<bf16>(float x) {
+  return 0.5f * x * (1.0f + erff(x * 0.70710678118654752440f));
+}
+
+// Summary of up to 32 consecutive tokens of one sequence, used by the
+// attention kernel to skip (or fast-path) whole key tiles.
+struct ChunkInfo {
+  int pmin, pmax;  // position range
+  int omin, omax;  // option-id range over option tokens (omin > omax if none)
+  int nprefix;     // tokens with opt == -1
+  int nopt;        // tokens with opt >= 0
+  int len;         // valid tokens in the chunk
+  int pad;
+};
+
+// Host-side launchers (implemented in the .hip files, called by api.cpp).
+struct GemmArgs {
+  const void *A;  // M x K, row stride lda (elements)
+  const void *B;  // N x K, row stride ldb (weights, PyTorch (out,in) layout)
+  void *C;        // output
+  const float *cos_t, *sin_t;  // RoPE tables [M x 32] (QKV epilogue)
+  int M, N, K, lda, ldb, ldc;
+  int n_store;    // columns actually stored (plain epilogue)
+  int accumulate; // plain epilogue: C += result
+  int rope_cols;  // QKV epilogue: columns [0, rope_cols) are rotated
+};
+
+enum { EPI_F32 = 0, EPI_QKV = 1, EPI_GEGLU = 2 };
+
+hipError_t launch_gemm(int precision, int epi, const GemmArgs &a, hipStream_t s);
+bool gemm_shape_ok(int precision, int N, int K);
+
+struct AttnArgs {
+  const void *qkv;
+  void *ctx;
+  const int *kinfo;   // per token: ((opt+1) << 16) | pos
+  const ChunkInfo *chunks;
+  const int4 *work;   // (seq, q0, 0, 0) per workgroup
+  const int *seq_off, *seq_len, *chunk_off;
+  int nwork, H, heads, sliding, half_window;
+  float scale_log2;   // softmax scale * log2(e)
+};
+hipError_t launch_attention(int precision, const AttnArgs &a, hipStream_t s);
+
+hipError_t launch_chunk_summary(const int *kinfo, const int4 *chunk_desc, ChunkInfo *out, int nchunks, hipStream_t s);
+hipError_t launch_token_info(const int *pos, const int *opt, int *kinfo, int T, hipStream_t s);
+hipError_t launch_rope_tables(const int *pos, int T, const double *inv_g, const double *inv_l, float *cos_g,
+                              float *sin_g, float *cos_l, float *sin_l, hipStream_t s);
+hipError_t launch_embed_ln(int precision, const int *ids, int T, const float *tok, int vocab, const float *w, float eps,
+                           int H, float *h, void *xn, int *err_flag, hipStream_t s);
+hipError_t launch_ln(int precision, const float *x, int rows, int H, const float *w, float eps, void *y, hipStream_t s);
+struct HeadArgs {
+  const float *h;
+  const int *row_tok;
+  int R, T, H;
+  float eps;
+  const float *final_norm, *in_w, *in_b, *dense_w, *dense_b, *norm_w, *norm_b, *out_w, *out_b;
+  float *logits;
+  int *err_flag;
+};
+hipError_t launch_head(const HeadArgs &a, hipStream_t s);
+hipError_t launch_pack(const float *src, int trans, int rows, int cols, int ld, float *dst, int dst_rows,
+                       int dst_cols, hipStream_t s);

@@ -1,0 +1,309 @@
+// Row-wise kernels: embedding gather + LayerNorm, LayerNorm, RoPE tables,
+// the scoring head, and the operand packer used by the general GEMM entry.
+//
+// All are HBM-bound; rows are handled one wavefront per row with 128-bit
+// loads, and LayerNorm statistics are reduced in double as the reference's
+// layerNormFwd does (internal/nn/ops.go:63-92): mean = sum/dim, two-pass
+// variance, rs = f32(1/sqrt(var + eps)), y = ((x - f32(mean)) * rs) * w (+ b).
+#include "common.hpp"
+
+namespace {
+
+__device__ __forceinline__ double wave_sum(double v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+__device__ __forceinline__ float wave_sumf(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+
+constexpr int MAXV = 4;  // float4 vectors per lane: rows up to 64*4*4 = 1024 wide
+
+// One row of `dim` floats (dim % 4 == 0, dim <= 1024) held as float4 in
+// registers; returns mean and rstd with the reference's f64 statistics.
+__device__ __forceinline__ void row_stats(const float4 (&x)[MAXV], int nvec, int lane, int dim, float eps,
+                                          float &mean, float &rstd) {
+  double s = 0;
+#pragma unroll
+  for (int j = 0; j < MAXV; j++)
+    if (lane + 64 * j < nvec) s += (double)x[j].x + (double)x[j].y + (double)x[j].z + (double)x[j].w;
+  const double mu = wave_sum(s) / (double)dim;
+  double v = 0;
+#pragma unroll
+  for (int j = 0; j < MAXV; j++)
+    if (lane + 64 * j < nvec) {
+      const double a = (double)x[j].x - mu, b = (double)x[j].y - mu, c = (double)x[j].z - mu,
+                   d = (double)x[j].w - mu;
+      v += a * a + b * b + c * c + d * d;
+    }
+  const double var = wave_sum(v) / (double)dim;
+  rstd = (float)(1.0 / sqrt(var + (double)eps));
+  mean = (float)mu;
+}
+
+template <class T>
+__device__ __forceinline__ void store4(T *p, float4 v);
+template <>
+__device__ __forceinline__ void store4<float>(float *p, float4 v) {
+  *(float4 *)p = v;
+}
+template <>
+__device__ __forceinline__ void store4<bf16>(bf16 *p, float4 v) {
+  bf16x4 o = {(bf16)v.x, (bf16)v.y, (bf16)v.z, (bf16)v.w};
+  *(bf16x4 *)p = o;
+}
+
+// Embedding gather (forward.go:204-209) + emb norm (forward.go:220). Writes the
+// fp32 residual stream h and its GEMM-operand copy xn (layer 0 has no
+// attn_norm, so its QKV input is h itself).
+template <class T>
+__global__ __launch_bounds__(256) void embed_ln_kernel(const int *ids, int Tn, const float *tok, int vocab,
+                                                       const float *w, float eps, int dim, float *h, T *xn,
+                                                       int *err) {
+  const int lane = threadIdx.x & 63;
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= Tn) return;
+  int id = ids[t];
+  if (id < 0 || id >= vocab) {
+    if (lane == 0) atomicOr(err, 1);
+    id = 0;
+  }
+  const int nvec = dim / 4;
+  const float4 *src = (const float4 *)(tok + (size_t)id * dim);
+  float4 x[MAXV];
+#pragma unroll
+  for (int j = 0; j < MAXV; j++)
+    if (lane + 64 * j < nvec) x[j] = src[lane + 64 * j];
+  float mean, rs;
+  row_stats(x, nvec, lane, dim, eps, mean, rs);
+  const float4 *w4 = (const float4 *)w;
+#pragma unroll
+  for (int j = 0; j < MAXV; j++)
+    if (lane + 64 * j < nvec) {
+      const float4 ww = w4[lane + 64 * j];
+      float4 y;
+      y.x = (x[j].x - mean) * rs * ww.x;
+      y.y = (x[j].y - mean) * rs * ww.y;
+      y.z = (x[j].z - mean) * rs * ww.z;
+      y.w = (x[j].w - mean) * rs * ww.w;
+      ((float4 *)(h + (size_t)t * dim))[lane + 64 * j] = y;
+      store4<T>(xn + (size_t)t * dim + 4 * (lane + 64 * j), y);
+    }
+}
+
+// Bias-free LayerNorm of the fp32 residual stream into the GEMM operand type
+// (attn_norm forward.go:289-294, mlp_norm forward.go:324).
+template <class T>
+__global__ __launch_bounds__(256) void ln_kernel(const float *xin, int rows, int dim, const float *w, float eps,
+                                                 T *y) {
+  const int lane = threadIdx.x & 63;
+  const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= rows) return;
+  const int nvec = dim / 4;
+  const float4 *src = (const float4 *)(xin + (size_t)r * dim);
+  float4 x[MAXV];
+#pragma unroll
+  for (int j = 0; j < MAXV; j++)
+    if (lane + 64 * j < nvec) x[j] = src[lane + 64 * j];
+  float mean, rs;
+  row_stats(x, nvec, lane, dim, eps, mean, rs);
+  const float4 *w4 = (const float4 *)w;
+#pragma unroll
+  for (int j = 0; j < MAXV; j++)
+    if (lane + 64 * j < nvec) {
+      const float4 ww = w4[lane + 64 * j];
+      float4 o;
+      o.x = (x[j].x - mean) * rs * ww.x;
+      o.y = (x[j].y - mean) * rs * ww.y;
+      o.z = (x[j].z - mean) * rs * ww.z;
+      o.w = (x[j].w - mean) * rs * ww.w;
+      store4<T>(y + (size_t)r * dim + 4 * (lane + 64 * j), o);
+    }
+}
+
+// ropeTables (internal/nn/model.go:242-258): angle = f32(pos * inv_freq[i])
+// widened back to f64, then f32(cos), f32(sin). One thread per (token, i).
+__global__ void rope_tables_kernel(const int *pos, int Tn, const double *inv_g, const double *inv_l, float *cg,
+                                   float *sg, float *cl, float *sl) {
+  const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= Tn * 32) return;
+  const int t = idx >> 5, i = idx & 31;
+  const double p = (double)pos[t];
+  const double fg = (double)(float)(p * inv_g[i]);
+  const double fl = (double)(float)(p * inv_l[i]);
+  cg[idx] = (float)cos(fg);
+  sg[idx] = (float)sin(fg);
+  cl[idx] = (float)cos(fl);
+  sl[idx] = (float)sin(fl);
+}
+
+// Scoring head (HeadForward, forward.go:250-282) for RB rows per workgroup:
+// gather the [MASK] rows of the encoder output, final_norm, input_norm (+bias,
+// eps 1e-5), dense H -> H/2 (+bias), gelu, norm (+bias, eps 1e-5), dot with
+// out_proj (+bias). fp32 throughout; the dense weight is streamed once per
+// workgroup with coalesced loads and reused for all RB rows.
+constexpr int RB = 8;
+constexpr int HMAX = 1024;
+
+__global__ __launch_bounds__(256) void head_kernel(HeadArgs a) {
+  __shared__ float s1[RB][HMAX];
+  __shared__ float ge[RB][HMAX / 2];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r0 = blockIdx.x * RB;
+  const int dim = a.H, half = a.H / 2, nvec = dim / 4;
+
+  // 1. rows -> final_norm -> input_norm (+bias) into s1.
+  for (int rr = wave; rr < RB; rr += 4) {
+    const int r = r0 + rr;
+    if (r >= a.R) break;
+    int t = a.row_tok[r];
+    if (t < 0 || t >= a.T) {
+      if (lane == 0) atomicOr(a.err_flag, 2);
+      t = 0;
+    }
+    const float4 *src = (const float4 *)(a.h + (size_t)t * dim);
+    float4 x[MAXV];
+#pragma unroll
+    for (int j = 0; j < MAXV; j++)
+      if (lane + 64 * j < nvec) x[j] = src[lane + 64 * j];
+    float mean, rs;
+    row_stats(x, nvec, lane, dim, a.eps, mean, rs);
+    const float4 *fw = (const float4 *)a.final_norm;
+#pragma unroll
+    for (int j = 0; j < MAXV; j++)
+      if (lane + 64 * j < nvec) {
+        const float4 ww = fw[lane + 64 * j];
+        x[j].x = (x[j].x - mean) * rs * ww.x;
+        x[j].y = (x[j].y - mean) * rs * ww.y;
+        x[j].z = (x[j].z - mean) * rs * ww.z;
+        x[j].w = (x[j].w - mean) * rs * ww.w;
+      }
+    row_stats(x, nvec, lane, dim, 1e-5f, mean, rs);
+    const float4 *iw = (const float4 *)a.in_w, *ib = (const float4 *)a.in_b;
+#pragma unroll
+    for (int j = 0; j < MAXV; j++)
+      if (lane + 64 * j < nvec) {
+        const float4 ww = iw[lane + 64 * j], bb = ib[lane + 64 * j];
+        float4 y;
+        y.x = (x[j].x - mean) * rs * ww.x + bb.x;
+        y.y = (x[j].y - mean) * rs * ww.y + bb.y;
+        y.z = (x[j].z - mean) * rs * ww.z + bb.z;
+        y.w = (x[j].w - mean) * rs * ww.w + bb.w;
+        *(float4 *)&s1[rr][4 * (lane + 64 * j)] = y;
+      }
+  }
+  __syncthreads();
+
+  // 2. dense + bias + gelu: wave w computes outputs o = w, w+4, ...
+  for (int o = wave; o < half; o += 4) {
+    const float4 *wr = (const float4 *)(a.dense_w + (size_t)o * dim);
+    float acc[RB];
+#pragma unroll
+    for (int rr = 0; rr < RB; rr++) acc[rr] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < MAXV; j++)
+      if (lane + 64 * j < nvec) {
+        const float4 ww = wr[lane + 64 * j];
+#pragma unroll
+        for (int rr = 0; rr < RB; rr++) {
+          const float4 xv = *(const float4 *)&s1[rr][4 * (lane + 64 * j)];
+          acc[rr] += xv.x * ww.x + xv.y * ww.y + xv.z * ww.z + xv.w * ww.w;
+        }
+      }
+#pragma unroll
+    for (int rr = 0; rr < RB; rr++) {
+      const float v = wave_sumf(acc[rr]);
+      if (lane == 0) ge[rr][o] = gelu_erf<float>(v + a.dense_b[o]);
+    }
+  }
+  __syncthreads();
+
+  // 3. norm (+bias) over H/2 and the output projection: one wave per row.
+  for (int rr = wave; rr < RB; rr += 4) {
+    const int r = r0 + rr;
+    if (r >= a.R) break;
+    double s = 0;
+    for (int i = lane; i < half; i += 64) s += (double)ge[rr][i];
+    const double mu = wave_sum(s) / (double)half;
+    double v = 0;
+    for (int i = lane; i < half; i += 64) {
+      const double d = (double)ge[rr][i] - mu;
+      v += d * d;
+    }
+    const double var = wave_sum(v) / (double)half;
+    const float rs = (float)(1.0 / sqrt(var + 1e-5));
+    const float m = (float)mu;
+    float dot = 0.0f;
+    for (int i = lane; i < half; i += 64) {
+      const float y = (ge[rr][i] - m) * rs * a.norm_w[i] + a.norm_b[i];
+      dot += y * a.out_w[i];
+    }
+    dot = wave_sumf(dot);
+    if (lane == 0) a.logits[r] = dot + a.out_b[0];
+  }
+}
+
+// dst[dst_rows x dst_cols] (row-major, zero padded) = op(src) where op(src)
+// is rows x cols; src is row-major with leading dimension ld, stored
+// transposed (cols x rows) when trans is set.
+__global__ void pack_kernel(const float *src, int trans, int rows, int cols, int ld, float *dst, int dst_rows,
+                            int dst_cols) {
+  const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= (size_t)dst_rows * dst_cols) return;
+  const int r = idx / dst_cols, c = idx % dst_cols;
+  float v = 0.0f;
+  if (r < rows && c < cols) v = trans ? src[(size_t)c * ld + r] : src[(size_t)r * ld + c];
+  dst[idx] = v;
+}
+
+}  // namespace
+
+hipError_t launch_embed_ln(int precision, const int *ids, int Tn, const float *tok, int vocab, const float *w,
+                           float eps, int H, float *h, void *xn, int *err, hipStream_t s) {
+  if (Tn <= 0) return hipSuccess;
+  dim3 grid((Tn + 3) / 4), block(256);
+  if (precision == 1)
+    hipLaunchKernelGGL(embed_ln_kernel<bf16>, grid, block, 0, s, ids, Tn, tok, vocab, w, eps, H, h, (bf16 *)xn, err);
+  else
+    hipLaunchKernelGGL(embed_ln_kernel<float>, grid, block, 0, s, ids, Tn, tok, vocab, w, eps, H, h, (float *)xn,
+                       err);
+  return hipGetLastError();
+}
+
+hipError_t launch_ln(int precision, const float *x, int rows, int H, const float *w, float eps, void *y,
+                     hipStream_t s) {
+  if (rows <= 0) return hipSuccess;
+  dim3 grid((rows + 3) / 4), block(256);
+  if (precision == 1)
+    hipLaunchKernelGGL(ln_kernel<bf16>, grid, block, 0, s, x, rows, H, w, eps, (bf16 *)y);
+  else
+    hipLaunchKernelGGL(ln_kernel<float>, grid, block, 0, s, x, rows, H, w, eps, (float *)y);
+  return hipGetLastError();
+}
+
+hipError_t launch_rope_tables(const int *pos, int Tn, const double *inv_g, const double *inv_l, float *cos_g,
+                              float *sin_g, float *cos_l, float *sin_l, hipStream_t s) {
+  if (Tn <= 0) return hipSuccess;
+  const int n = Tn * 32;
+  hipLaunchKernelGGL(rope_tables_kernel, dim3((n + 255) / 256), dim3(256), 0, s, pos, Tn, inv_g, inv_l, cos_g, sin_g,
+                     cos_l, sin_l);
+  return hipGetLastError();
+}
+
+hipError_t launch_head(const HeadArgs &a, hipStream_t s) {
+  if (a.R <= 0) return hipSuccess;
+  hipLaunchKernelGGL(head_kernel, dim3((a.R + RB - 1) / RB), dim3(256), 0, s, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_pack(const float *src, int trans, int rows, int cols, int ld, float *dst, int dst_rows,
+                       int dst_cols, hipStream_t s) {
+  const size_t n = (size_t)dst_rows * dst_cols;
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(pack_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, src, trans, rows, cols, ld,
+                     dst, dst_rows, dst_cols);
+  return hipGetLastError();
+}

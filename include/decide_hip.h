@@ -1,0 +1,181 @@
+/*
+ * decide_hip.h - C ABI of libdecide_hip.so, the MI355X (gfx950) encoder
+ * forward for jmwri/decide.
+ *
+ * The library replaces the reference's GPU stack for inference
+ * (internal/cuda: purego driver FFI + NVRTC-built PTX, internal/gpunn:
+ * orchestration, cmd/ptxgen: codegen) and gives a device engine for the CPU
+ * forward in internal/nn. A host binding (the Go/purego stub is in
+ * INTEGRATION.md, the Python ctypes veneer is decide_amd/) dlopens it with
+ * RTLD_NOW|RTLD_GLOBAL as internal/cuda/lib_unix.go:7-9 does for libcuda.
+ *
+ * Conventions (mirroring internal/cuda/driver.go):
+ *   - every call returns an int status; 0 is success (driver.go:123-142);
+ *   - a missing or unusable GPU yields DN_NO_GPU, which the binding maps to
+ *     the reference's ErrNoGPU sentinel and its CPU fallback
+ *     (driver.go:19, :157-167; internal/train/engine.go:42-61);
+ *   - on failure dn_last_error() names the operation and cause;
+ *   - host arrays are caller-owned and copied synchronously; device memory
+ *     is owned by the context and freed by dn_close;
+ *   - one context is single-stream and not re-entrant: callers serialise
+ *     calls, as decide.Local does with its fmu mutex (local.go:193-194).
+ *
+ * All pointers named d_* are device pointers; all others are host pointers.
+ */
+#ifndef DECIDE_HIP_H
+#define DECIDE_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define DN_ABI_VERSION 1
+
+enum {
+  DN_OK = 0,
+  DN_NO_GPU = 1,        /* no HIP device / runtime: fall back to the CPU */
+  DN_INVALID_ARG = 2,   /* malformed input; message mirrors forward.go */
+  DN_OUT_OF_MEMORY = 3,
+  DN_DEVICE_ERROR = 4,  /* a HIP call or kernel failed */
+  DN_UNSUPPORTED = 5    /* geometry or mode this build does not implement */
+};
+
+enum { DN_PRECISION_FP32 = 0, DN_PRECISION_BF16 = 1 };
+
+typedef struct dn_ctx dn_ctx;
+
+/* ABI version of the loaded library (DN_ABI_VERSION). */
+int dn_abi_version(void);
+
+/* Human-readable name of a status code. */
+const char *dn_status_string(int status);
+
+/* Opens device `device` and creates a context.
+ * Replaces cuda.Open (internal/cuda/driver.go:157-191): DN_NO_GPU when the
+ * HIP runtime reports no device (driver.go:157-167). */
+int dn_open(int device, dn_ctx **out);
+
+/* Frees every device allocation of the context.
+ * Replaces gpunn.(*Model).Free + cuda.(*Device).Close (engine.go:166). */
+void dn_close(dn_ctx *ctx);
+
+/* Message of the last failed call on ctx ("" if none); valid until the next
+ * call on ctx. Counterpart of cuda.Error.Error (driver.go:123-136). */
+const char *dn_last_error(const dn_ctx *ctx);
+
+/* Runs the context's work on `stream` (a hipStream_t) instead of its own.
+ * No counterpart in the reference (CUDA's context stream was implicit). */
+int dn_set_stream(dn_ctx *ctx, void *stream);
+
+/* Model geometry, the fields of nn.Config (internal/nn/config.go:12-27;
+ * defaults from LoadConfig :33-95) plus the arithmetic mode:
+ * DN_PRECISION_BF16 = bf16 GEMM/attention operands, fp32 accumulate,
+ * residual stream, statistics and head; DN_PRECISION_FP32 = fp32 MFMA
+ * everywhere (the validation build). Must precede dn_upload_tensor.
+ * Replaces the config capture of gpunn.New (internal/gpunn/model.go:80-122).
+ * This build implements head_dim 64 with hidden % 128 == 0 and
+ * inter % 64 == 0 (ModernBERT-base: 768/1152/12 heads); others give
+ * DN_UNSUPPORTED. */
+int dn_set_config(dn_ctx *ctx, int hidden, int inter, int heads, int layers, int vocab, float eps,
+                  int half_window, double theta_global, double theta_local,
+                  const uint8_t *layer_is_sliding /* [layers] */, int precision);
+
+/* Uploads one parameter by its nn.Model.Tensors() name
+ * (internal/nn/model.go:51-84), as n float32 values in that tensor's layout.
+ * bf16 mode converts the four projection matrices to bf16 (round to nearest
+ * even) and interleaves the Wi rows for the fused GeGLU epilogue.
+ * Replaces the per-tensor upload loop of gpunn.New (model.go:80-122). */
+int dn_upload_tensor(dn_ctx *ctx, const char *name, const float *data, int64_t n);
+
+/* 1 when every tensor the configured model needs has been uploaded. */
+int dn_weights_ready(const dn_ctx *ctx);
+
+/* Encoder + scorer forward over a batch of packed sequences, returning one
+ * logit per mask position in batch order.
+ * Replaces nn.(*Model).Forward (internal/nn/forward.go:129-245, inference,
+ * trainFrom >= Layers) and gpunn.(*Model).Forward (internal/gpunn/model.go:204-330)
+ * including HeadForward (forward.go:250-282), which ran on the host there.
+ * The nn.Sequence slice is passed flattened:
+ *   seq_len[nseq]            len(Sequence.IDs)
+ *   ids[T], pos[T]           Sequence.IDs, Sequence.Pos (T = sum seq_len)
+ *   opt_id[T] or NULL        Sequence.OptID; -1 = prefix; a sequence with
+ *                            OptID == nil is passed as all -1; NULL = all nil
+ *   nmask[nseq], mask_pos[]  Sequence.MaskPos of each sequence, concatenated
+ *   logits[logits_cap]       output, sum(nmask) values
+ * Validation and messages follow forward.go:145-150, :181-183, :192-196
+ * (DN_INVALID_ARG). */
+int dn_forward(dn_ctx *ctx, int nseq, const int32_t *seq_len, const int32_t *ids, const int32_t *pos,
+               const int32_t *opt_id, const int32_t *nmask, const int32_t *mask_pos, float *logits,
+               int logits_cap);
+
+/* The same forward with the token arrays already resident on the device.
+ * seq_len is a host array (the batch layout); d_row_tok holds, per output
+ * row, the global token index of its mask position. Inputs are trusted to
+ * satisfy dn_forward's checks; out-of-range ids or rows are clamped by the
+ * kernels and reported by the next dn_check_device_errors. Asynchronous on
+ * the context's stream. No separate counterpart in the reference (it is the
+ * device part of gpunn.(*Model).Forward, model.go:261-328). */
+int dn_forward_device(dn_ctx *ctx, int nseq, const int32_t *seq_len, const int32_t *d_ids,
+                      const int32_t *d_pos, const int32_t *d_opt_id, int nrows, const int32_t *d_row_tok,
+                      float *d_logits);
+
+/* Synchronises the stream and reports (DN_INVALID_ARG) any out-of-range token
+ * id or row index seen by dn_forward_device since the last check. */
+int dn_check_device_errors(dn_ctx *ctx);
+
+/* C (M x N) = op(A) (M x K) . op(B) (K x N), adding into C when accumulate
+ * is set, with blas.Sgemm semantics (internal/blas/gemm.go:55-63): row-major
+ * host arrays with leading dimensions; transA means A is stored K x M,
+ * transB means B is stored N x K. Computed on the GPU with fp32 MFMA.
+ * Replaces cuda.(*Kernels).Gemm (internal/cuda/kernels.go:52-71). */
+int dn_gemm_f32(dn_ctx *ctx, int transA, int transB, int M, int N, int K, const float *A, int lda,
+                const float *B, int ldb, float *C, int ldc, int accumulate);
+
+/* Device-resident projection GEMM as the forward runs it:
+ * d_C[M x N] (fp32) (+)= d_A[M x K] . d_B[N x K]^T, with operands of the
+ * given precision (bf16 or fp32). Requires N % 128 == 0 and K a multiple of
+ * 64 (bf16) / 32 (fp32). Asynchronous. Same reference counterpart as
+ * dn_gemm_f32 (the NT case, linearFwd forward.go:122-124). */
+int dn_gemm_device(dn_ctx *ctx, int precision, int M, int N, int K, const void *d_A, const void *d_B,
+                   float *d_C, int accumulate);
+
+/* Waits for the context's stream. */
+int dn_synchronize(dn_ctx *ctx);
+
+/* Kernel probe for measurement: while enabled (layer >= 0), every forward
+ * records HIP events on the context's stream around the five per-layer
+ * launches of encoder layer `layer` (DN_PROBE_* order). dn_read_probe
+ * synchronises, adds each launch's duration to ms[5] and the number of
+ * forwards seen to *count, and resets the probe. layer < 0 disables it.
+ * No counterpart in the reference (its tests time whole calls,
+ * internal/cuda/gemm_test.go:141-181). */
+enum { DN_PROBE_QKV = 0, DN_PROBE_ATTENTION = 1, DN_PROBE_WO = 2, DN_PROBE_WI = 3, DN_PROBE_MLPWO = 4 };
+int dn_set_probe(dn_ctx *ctx, int layer);
+int dn_read_probe(dn_ctx *ctx, double *ms /* [5] */, int *count);
+
+/* ---- host-side helpers mirroring the reference's scoring glue ---------- */
+
+/* nn.BuildSequence (internal/nn/forward.go:28-56). Writes pos[n] and, when
+ * independent and at least one mask token exists, opt_id[n] (*has_opt = 1);
+ * mask_pos receives the mask token indices (capacity n). Returns their
+ * count. */
+int dn_build_sequence(const int32_t *ids, int n, int32_t mask_id, int independent, int32_t *pos,
+                      int32_t *opt_id, int32_t *mask_pos, int *has_opt);
+
+/* decide.Local answer post-processing for K logits (local.go:206-262):
+ * probs = softmax(logit / max(temperature, 1e-4)) in float64; *choice =
+ * argmax of the raw logits (first index wins ties); *confidence =
+ * marginConfidence(probs) rounded to 3 places. probs are NOT rounded. */
+int dn_answer(const double *logits, int k, double temperature, double *probs, int *choice,
+              double *confidence);
+
+/* local.go round(): math.RoundToEven(x * 10^places) / 10^places. */
+double dn_round(double x, int places);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DECIDE_HIP_H */

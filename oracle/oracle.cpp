@@ -1,0 +1,741 @@
+// CPU oracle: a C++ restatement of the reference's pure-Go encoder forward.
+//
+// TEST INFRASTRUCTURE ONLY. This file is the parity checker for the HIP
+// library and the CPU baseline timed by bench.py. Only tests/, the smoke
+// entry and bench.py's cpu_baseline leg load it; the product path never does.
+//
+// What it restates (paths relative to the reference checkout):
+//   internal/blas/gemm.go:13-220     Sgemm / Sgemm1: blocking mr=6 nr=16 kc=256
+//                                    mc=96, packA/packB, dynamic job queue
+//   internal/blas/kern_amd64.s:5-81  6x16 AVX2/FMA micro-kernel (acc := 0,
+//                                    acc = fma(a,b,acc) over one kc block in
+//                                    increasing k, then C += acc)
+//   internal/nn/ops.go:13-44         parallelFor (4*workers dynamic chunks)
+//   internal/nn/ops.go:63-92         layerNormFwd (f64 two-pass statistics)
+//   internal/nn/ops.go:140-142       gelu (exact erf form, erf in f64)
+//   internal/nn/ops.go:155-175       applyRope (rotate-half)
+//   internal/nn/model.go:242-258     ropeTables (angle rounded to f32 first)
+//   internal/nn/forward.go:28-56     BuildSequence
+//   internal/nn/forward.go:129-245   Forward (layout, masks, layers, rows)
+//   internal/nn/forward.go:250-282   HeadForward
+//   internal/nn/forward.go:284-343   layerFwd
+//   internal/nn/forward.go:347-409   attnFwd + softmaxMasked
+//   local.go:206-262                 softmax, calibrated, round, marginConfidence, argmax
+//
+// Go evaluates float32 expressions in IEEE single precision without
+// contracting a*b+c on amd64, so everything outside the explicit FMA
+// micro-kernel is compiled with -ffp-contract=off and written with Go's
+// left-to-right association.
+//
+// Parity pins (tests/test_oracle.py): the reference's own PyTorch fixture
+// (tiny_ref.safetensors: logits, hidden.0-3, l1.n1, l1.attn), naive float64
+// GEMM on the reference test's shape list with all transposes, accumulate and
+// padded leading dimensions, order invariance, and closed forms for LN, RoPE,
+// GELU and the answer post-processing.
+#include <immintrin.h>
+
+#include <atomic>
+#include <cmath>
+#include <condition_variable>
+#include <cstdint>
+#include <cstring>
+#include <functional>
+#include <map>
+#include <mutex>
+#include <string>
+#include <thread>
+#include <vector>
+
+namespace {
+
+// ---------------------------------------------------------------------------
+// Worker pool: stands in for goroutines. run(w, body) executes body on w
+// threads (the caller included); work distribution inside body is the
+// reference's atomic-counter queue.
+class Pool {
+ public:
+  ~Pool() {
+    {
+      std::lock_guard<std::mutex> g(mu_);
+      stop_ = true;
+      gen_++;
+    }
+    cv_.notify_all();
+    for (auto &t : th_) t.join();
+  }
+  void run(int w, const std::function<void()> &body) {
+    if (w <= 1) {
+      body();
+      return;
+    }
+    ensure(w - 1);
+    {
+      std::lock_guard<std::mutex> g(mu_);
+      body_ = &body;
+      active_ = w - 1;
+      pending_ = w - 1;
+      gen_++;
+    }
+    cv_.notify_all();
+    body();
+    std::unique_lock<std::mutex> g(mu_);
+    done_.wait(g, [&] { return pending_ == 0; });
+    body_ = nullptr;
+  }
+
+ private:
+  void ensure(int n) {
+    while ((int)th_.size() < n) {
+      int id = (int)th_.size();
+      // The thread starts from the current generation: work published after
+      // this point (gen_ incremented by run) is seen as new.
+      const uint64_t g0 = gen_;
+      th_.emplace_back([this, id, g0] { loop(id, g0); });
+    }
+  }
+  void loop(int id, uint64_t seen) {
+    for (;;) {
+      const std::function<void()> *b = nullptr;
+      {
+        std::unique_lock<std::mutex> g(mu_);
+        cv_.wait(g, [&] { return gen_ != seen; });
+        seen = gen_;
+        if (stop_) return;
+        if (id >= active_) continue;
+        b = body_;
+      }
+      (*b)();
+      {
+        std::lock_guard<std::mutex> g(mu_);
+        if (--pending_ == 0) done_.notify_all();
+      }
+    }
+  }
+  std::vector<std::thread> th_;
+  std::mutex mu_;
+  std::condition_variable cv_, done_;
+  const std::function<void()> *body_ = nullptr;
+  uint64_t gen_ = 0;
+  int active_ = 0, pending_ = 0;
+  bool stop_ = false;
+};
+
+Pool &pool() {
+  static Pool p;
+  return p;
+}
+
+int g_workers = 1;  // runtime.GOMAXPROCS(0) / blas.Workers
+
+// parallelFor, internal/nn/ops.go:13-44.
+void parallel_for(int n, const std::function<void(int, int)> &fn) {
+  int workers = g_workers;
+  if (n <= 0) return;
+  if (workers > n) workers = n;
+  if (workers <= 1) {
+    fn(0, n);
+    return;
+  }
+  int chunk = std::max(1, (n + 4 * workers - 1) / (4 * workers));
+  int chunks = (n + chunk - 1) / chunk;
+  std::atomic<int> next{0};
+  pool().run(std::min(workers, chunks), [&] {
+    for (;;) {
+      int c = next.fetch_add(1);
+      if (c >= chunks) return;
+      int lo = c * chunk;
+      fn(lo, std::min(lo + chunk, n));
+    }
+  });
+}
+
+// ---------------------------------------------------------------------------
+// SGEMM, internal/blas/gemm.go.
+constexpr int MR = 6, NR = 16, KC = 256, MC = 96;
+
+struct Scratch {
+  std::vector<float> a, b;
+  float tmp[MR * NR];
+};
+
+// kern6x16, kern_amd64.s:5-81. 12 accumulators start at zero, one FMA per
+// (k, i, j) in increasing k, then C += acc.
+void kern6x16(int k, const float *a, const float *b, float *c, int ldc) {
+  __m256 c00 = _mm256_setzero_ps(), c01 = _mm256_setzero_ps();
+  __m256 c10 = _mm256_setzero_ps(), c11 = _mm256_setzero_ps();
+  __m256 c20 = _mm256_setzero_ps(), c21 = _mm256_setzero_ps();
+  __m256 c30 = _mm256_setzero_ps(), c31 = _mm256_setzero_ps();
+  __m256 c40 = _mm256_setzero_ps(), c41 = _mm256_setzero_ps();
+  __m256 c50 = _mm256_setzero_ps(), c51 = _mm256_setzero_ps();
+  for (int p = 0; p < k; p++) {
+    __m256 b0 = _mm256_loadu_ps(b), b1 = _mm256_loadu_ps(b + 8);
+    __m256 a0 = _mm256_broadcast_ss(a + 0), a1 = _mm256_broadcast_ss(a + 1);
+    c00 = _mm256_fmadd_ps(b0, a0, c00);
+    c01 = _mm256_fmadd_ps(b1, a0, c01);
+    c10 = _mm256_fmadd_ps(b0, a1, c10);
+    c11 = _mm256_fmadd_ps(b1, a1, c11);
+    a0 = _mm256_broadcast_ss(a + 2);
+    a1 = _mm256_broadcast_ss(a + 3);
+    c20 = _mm256_fmadd_ps(b0, a0, c20);
+    c21 = _mm256_fmadd_ps(b1, a0, c21);
+    c30 = _mm256_fmadd_ps(b0, a1, c30);
+    c31 = _mm256_fmadd_ps(b1, a1, c31);
+    a0 = _mm256_broadcast_ss(a + 4);
+    a1 = _mm256_broadcast_ss(a + 5);
+    c40 = _mm256_fmadd_ps(b0, a0, c40);
+    c41 = _mm256_fmadd_ps(b1, a0, c41);
+    c50 = _mm256_fmadd_ps(b0, a1, c50);
+    c51 = _mm256_fmadd_ps(b1, a1, c51);
+    a += MR;
+    b += NR;
+  }
+  auto st = [&](float *row, __m256 x0, __m256 x1) {
+    _mm256_storeu_ps(row, _mm256_add_ps(x0, _mm256_loadu_ps(row)));
+    _mm256_storeu_ps(row + 8, _mm256_add_ps(x1, _mm256_loadu_ps(row + 8)));
+  };
+  st(c + 0 * ldc, c00, c01);
+  st(c + 1 * ldc, c10, c11);
+  st(c + 2 * ldc, c20, c21);
+  st(c + 3 * ldc, c30, c31);
+  st(c + 4 * ldc, c40, c41);
+  st(c + 5 * ldc, c50, c51);
+}
+
+// packA, gemm.go:147-170.
+void pack_a(Scratch &s, bool trans, const float *A, int lda, int i0, int p0, int mb, int kb) {
+  int panels = (mb + MR - 1) / MR;
+  s.a.resize((size_t)panels * MR * kb);
+  float *dst = s.a.data();
+  for (int pi = 0; pi < panels; pi++) {
+    size_t base = (size_t)pi * MR * kb;
+    int rows = std::min(MR, mb - pi * MR);
+    for (int p = 0; p < kb; p++) {
+      float *d = dst + base + (size_t)p * MR;
+      if (!trans) {
+        for (int i = 0; i < rows; i++) d[i] = A[(size_t)(i0 + pi * MR + i) * lda + p0 + p];
+      } else {
+        const float *src = A + (size_t)(p0 + p) * lda + i0 + pi * MR;
+        std::memcpy(d, src, sizeof(float) * rows);
+      }
+      for (int i = rows; i < MR; i++) d[i] = 0;
+    }
+  }
+}
+
+// packB, gemm.go:172-195.
+void pack_b(Scratch &s, bool trans, const float *B, int ldb, int p0, int j0, int kb, int nb) {
+  int panels = (nb + NR - 1) / NR;
+  s.b.resize((size_t)panels * NR * kb);
+  float *dst = s.b.data();
+  for (int pj = 0; pj < panels; pj++) {
+    size_t base = (size_t)pj * NR * kb;
+    int cols = std::min(NR, nb - pj * NR);
+    for (int p = 0; p < kb; p++) {
+      float *d = dst + base + (size_t)p * NR;
+      if (!trans) {
+        const float *src = B + (size_t)(p0 + p) * ldb + j0 + pj * NR;
+        std::memcpy(d, src, sizeof(float) * cols);
+      } else {
+        for (int j = 0; j < cols; j++) d[j] = B[(size_t)(j0 + pj * NR + j) * ldb + p0 + p];
+      }
+      for (int j = cols; j < NR; j++) d[j] = 0;
+    }
+  }
+}
+
+// macro, gemm.go:197-220.
+void macro(Scratch &s, float *C, int ldc, int mb, int nb, int kb) {
+  for (int jr = 0; jr < nb; jr += NR) {
+    const float *bp = s.b.data() + (size_t)(jr / NR) * NR * kb;
+    int cols = std::min(NR, nb - jr);
+    for (int ir = 0; ir < mb; ir += MR) {
+      const float *ap = s.a.data() + (size_t)(ir / MR) * MR * kb;
+      int rows = std::min(MR, mb - ir);
+      if (rows == MR && cols == NR) {
+        kern6x16(kb, ap, bp, C + (size_t)ir * ldc + jr, ldc);
+        continue;
+      }
+      std::memset(s.tmp, 0, sizeof(s.tmp));
+      kern6x16(kb, ap, bp, s.tmp, NR);
+      for (int i = 0; i < rows; i++) {
+        float *dst = C + (size_t)(ir + i) * ldc + jr;
+        for (int j = 0; j < cols; j++) dst[j] += s.tmp[i * NR + j];
+      }
+    }
+  }
+}
+
+int round_up(int x, int m) { return (x + m - 1) / m * m; }
+
+// sgemm, gemm.go:71-138.
+void sgemm(int workers, bool transA, bool transB, int M, int N, int K, const float *A, int lda,
+           const float *B, int ldb, float *C, int ldc, bool accumulate) {
+  if (M == 0 || N == 0) return;
+  if (!accumulate)
+    for (int i = 0; i < M; i++) std::memset(C + (size_t)i * ldc, 0, sizeof(float) * N);
+  if (K == 0) return;
+  if ((int64_t)M * N * K < (1 << 15)) workers = 1;
+  int mBlk = std::min(MC, round_up(M, MR));
+  int mBlocks = (M + mBlk - 1) / mBlk;
+  int nBlk = round_up(N, NR);
+  int want = (2 * workers + mBlocks - 1) / mBlocks;
+  if (want > 1) nBlk = std::min(nBlk, std::max(NR, round_up((N + want - 1) / want, NR)));
+  nBlk = std::min(nBlk, 256);
+  int nBlocks = (N + nBlk - 1) / nBlk;
+  int jobs = mBlocks * nBlocks;
+  auto run = [&](int job, Scratch &s) {
+    int ic = (job % mBlocks) * mBlk;
+    int jc = (job / mBlocks) * nBlk;
+    int mb = std::min(mBlk, M - ic);
+    int nb = std::min(nBlk, N - jc);
+    for (int pc = 0; pc < K; pc += KC) {
+      int kb = std::min(KC, K - pc);
+      pack_a(s, transA, A, lda, ic, pc, mb, kb);
+      pack_b(s, transB, B, ldb, pc, jc, kb, nb);
+      macro(s, C + (size_t)ic * ldc + jc, ldc, mb, nb, kb);
+    }
+  };
+  if (workers == 1 || jobs == 1) {
+    thread_local Scratch s;
+    for (int j = 0; j < jobs; j++) run(j, s);
+    return;
+  }
+  std::atomic<int> next{0};
+  pool().run(std::min(workers, jobs), [&] {
+    thread_local Scratch s;
+    for (;;) {
+      int j = next.fetch_add(1);
+      if (j >= jobs) break;
+      run(j, s);
+    }
+  });
+}
+
+// ---------------------------------------------------------------------------
+// Model, internal/nn/model.go + config.go.
+struct Config {
+  int hidden, inter, heads, layers, vocab;
+  float eps;
+  int half_window;
+  double theta_g, theta_l;
+  std::vector<uint8_t> sliding;
+};
+
+struct Model {
+  Config cfg;
+  std::map<std::string, std::vector<float>> w;
+  const float *get(const std::string &name) const {
+    auto it = w.find(name);
+    return it == w.end() ? nullptr : it->second.data();
+  }
+};
+
+// layerNormFwd, ops.go:63-92.
+void layer_norm(float *y, const float *x, int rows, int dim, const float *w, const float *b, float eps) {
+  parallel_for(rows, [&](int lo, int hi) {
+    for (int r = lo; r < hi; r++) {
+      const float *row = x + (size_t)r * dim;
+      double sum = 0;
+      for (int i = 0; i < dim; i++) sum += (double)row[i];
+      double mu = sum / (double)dim;
+      double vs = 0;
+      for (int i = 0; i < dim; i++) {
+        double d = (double)row[i] - mu;
+        vs += d * d;
+      }
+      float rs = (float)(1.0 / std::sqrt(vs / (double)dim + (double)eps));
+      float m = (float)mu;
+      float *o = y + (size_t)r * dim;
+      if (b) {
+        for (int i = 0; i < dim; i++) o[i] = (row[i] - m) * rs * w[i] + b[i];
+      } else {
+        for (int i = 0; i < dim; i++) o[i] = (row[i] - m) * rs * w[i];
+      }
+    }
+  });
+}
+
+// gelu, ops.go:140-142.
+inline float gelu(float x) {
+  const double sqrt2 = 1.41421356237309504880168872420969808;
+  return 0.5f * x * (1.0f + (float)std::erf((double)x * sqrt2 / 2.0));
+}
+
+// ropeTables, model.go:242-258.
+void rope_tables(const std::vector<int32_t> &pos, int headDim, double theta, std::vector<float> &cs,
+                 std::vector<float> &sn) {
+  int half = headDim / 2;
+  std::vector<double> inv(half);
+  for (int i = 0; i < half; i++) inv[i] = 1.0 / std::pow(theta, (double)(2 * i) / (double)headDim);
+  cs.assign(pos.size() * half, 0);
+  sn.assign(pos.size() * half, 0);
+  for (size_t s = 0; s < pos.size(); s++)
+    for (int i = 0; i < half; i++) {
+      double f = (double)(float)((double)pos[s] * inv[i]);
+      cs[s * half + i] = (float)std::cos(f);
+      sn[s * half + i] = (float)std::sin(f);
+    }
+}
+
+// applyRope, ops.go:155-175 (forward direction only).
+void apply_rope(float *qkv, int T, int H, int heads, int D, const float *cs, const float *sn) {
+  int half = D / 2, stride = 3 * H;
+  parallel_for(T, [&](int lo, int hi) {
+    for (int t = lo; t < hi; t++)
+      for (int hd = 0; hd < heads; hd++)
+        for (int off : {hd * D, H + hd * D}) {
+          float *v = qkv + (size_t)t * stride + off;
+          for (int i = 0; i < half; i++) {
+            float c = cs[(size_t)t * half + i], s = sn[(size_t)t * half + i];
+            float a = v[i], b = v[i + half];
+            v[i] = a * c - b * s;
+            v[i + half] = b * c + a * s;
+          }
+        }
+  });
+}
+
+// softmaxMasked, forward.go:382-409.
+void softmax_masked(float *P, int n, float scale, const uint8_t *mask) {
+  for (int i = 0; i < n; i++) {
+    float *row = P + (size_t)i * n;
+    float maxv = -INFINITY;
+    for (int j = 0; j < n; j++) {
+      if (mask && mask[(size_t)i * n + j] == 0) continue;
+      float v = row[j] * scale;
+      if (v > maxv) maxv = v;
+    }
+    double sum = 0;
+    for (int j = 0; j < n; j++) {
+      if (mask && mask[(size_t)i * n + j] == 0) {
+        row[j] = 0;
+        continue;
+      }
+      float e = (float)std::exp((double)(row[j] * scale - maxv));
+      row[j] = e;
+      sum += (double)e;
+    }
+    float inv = (float)(1.0 / sum);
+    for (int j = 0; j < n; j++) row[j] *= inv;
+  }
+}
+
+struct SeqInfo {
+  int off, n;
+  std::vector<uint8_t> full, slide;  // full empty == nil (all allowed)
+};
+
+struct Debug {
+  float *hs;    // (L+1) x T x H : input of each layer, then the encoder output
+  float *n1;    // L x T x H     : attention input (attn_norm output, layer 0: identity)
+  float *attn;  // L x T x H     : Wo . ctx, before the residual add
+};
+
+void linear(float *y, const float *x, int T, int K, const float *w, int N) {
+  sgemm(g_workers, false, true, T, N, K, x, K, w, K, y, N, false);
+}
+
+// attnFwd, forward.go:347-378 (inference: P in per-item scratch).
+void attn_fwd(const Config &cfg, const std::vector<SeqInfo> &seqs, float *ctx, const float *qkv, bool sliding) {
+  int H = cfg.hidden, heads = cfg.heads, D = H / heads, stride = 3 * H;
+  float scale = (float)(1.0 / std::sqrt((double)D));
+  int items = (int)seqs.size() * heads;
+  parallel_for(items, [&](int lo, int hi) {
+    std::vector<float> P;
+    for (int it = lo; it < hi; it++) {
+      int si = it / heads, hd = it % heads;
+      const SeqInfo &s = seqs[si];
+      int n = s.n;
+      P.resize((size_t)n * n);
+      const float *q = qkv + (size_t)s.off * stride + hd * D;
+      const float *k = qkv + (size_t)s.off * stride + H + hd * D;
+      const float *v = qkv + (size_t)s.off * stride + 2 * H + hd * D;
+      sgemm(1, false, true, n, n, D, q, stride, k, stride, P.data(), n, false);
+      const uint8_t *mask = sliding ? s.slide.data() : (s.full.empty() ? nullptr : s.full.data());
+      softmax_masked(P.data(), n, scale, mask);
+      sgemm(1, false, false, n, D, n, P.data(), n, v, stride, ctx + (size_t)s.off * H + hd * D, H, false);
+    }
+  });
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// C ABI used by tests/ and bench.py through ctypes.
+extern "C" {
+
+void orc_set_workers(int n) { g_workers = n < 1 ? 1 : n; }
+int orc_get_workers(void) { return g_workers; }
+
+// blas.Sgemm (gemm.go:61) with an explicit worker count (Sgemm1 == workers 1).
+void orc_sgemm(int workers, int transA, int transB, int M, int N, int K, const float *A, int lda, const float *B,
+               int ldb, float *C, int ldc, int accumulate) {
+  sgemm(workers, transA != 0, transB != 0, M, N, K, A, lda, B, ldb, C, ldc, accumulate != 0);
+}
+
+// The same summation order written per element (no blocking): C (=0 unless
+// accumulate); for each 256-wide k block: acc = 0; acc = fma(a,b,acc) in
+// increasing k; C += acc. Used to pin orc_sgemm bit-for-bit.
+void orc_sgemm_ref(int transA, int transB, int M, int N, int K, const float *A, int lda, const float *B, int ldb,
+                   float *C, int ldc, int accumulate) {
+  for (int i = 0; i < M; i++)
+    for (int j = 0; j < N; j++) {
+      float c = accumulate ? C[(size_t)i * ldc + j] : 0.0f;
+      for (int pc = 0; pc < K; pc += KC) {
+        float acc = 0.0f;
+        for (int k = pc; k < std::min(K, pc + KC); k++) {
+          float a = transA ? A[(size_t)k * lda + i] : A[(size_t)i * lda + k];
+          float b = transB ? B[(size_t)j * ldb + k] : B[(size_t)k * ldb + j];
+          acc = std::fma(a, b, acc);
+        }
+        c = c + acc;
+      }
+      C[(size_t)i * ldc + j] = c;
+    }
+}
+
+// BuildSequence, forward.go:28-56. Returns the number of mask positions
+// written to mask_pos (capacity n). *has_opt is 1 when OptID is non-nil.
+int orc_build_sequence(const int32_t *ids, int n, int32_t mask_id, int independent, int32_t *pos, int32_t *opt,
+                       int32_t *mask_pos, int *has_opt) {
+  int nm = 0;
+  for (int i = 0; i < n; i++) {
+    pos[i] = i;
+    if (ids[i] == mask_id) mask_pos[nm++] = i;
+  }
+  *has_opt = 0;
+  if (!independent || nm == 0) return nm;
+  int last = n - 1;
+  *has_opt = 1;
+  for (int i = 0; i < n; i++) opt[i] = -1;
+  int prefix = mask_pos[0];
+  for (int k = 0; k < nm; k++) {
+    int start = mask_pos[k];
+    int end = k + 1 < nm ? mask_pos[k + 1] : last;
+    for (int i = start; i < end; i++) {
+      opt[i] = k;
+      pos[i] = prefix + i - start;
+    }
+  }
+  return nm;
+}
+
+void *orc_model_new(int hidden, int inter, int heads, int layers, int vocab, float eps, int half_window,
+                    double theta_g, double theta_l, const uint8_t *sliding) {
+  Model *m = new Model;
+  m->cfg = Config{hidden, inter, heads, layers, vocab, eps, half_window, theta_g, theta_l,
+                  std::vector<uint8_t>(sliding, sliding + layers)};
+  return m;
+}
+
+void orc_model_free(void *m) { delete (Model *)m; }
+
+void orc_model_set(void *mp, const char *name, const float *data, int64_t n) {
+  Model *m = (Model *)mp;
+  m->w[name].assign(data, data + n);
+}
+
+// Model.Forward (forward.go:129-245) + HeadForward (:250-282), inference.
+// Sequences are concatenated: seq_len[nseq], ids/pos/opt[T]; has_opt[s] = 0
+// means OptID nil for that sequence. mask_pos holds each sequence's mask
+// positions (local indices), nmask[s] of them. Returns 0, or a negative code
+// mirroring the reference's validation errors:
+//   -1 malformed sequence, -2 no options, -3 mask position out of range,
+//   -4 token id out of range, -5 missing weight.
+int orc_forward(void *mp, int nseq, const int32_t *seq_len, const int32_t *ids, const int32_t *pos_in,
+                const int32_t *opt_in, const uint8_t *has_opt, const int32_t *nmask, const int32_t *mask_pos,
+                float *logits, float *dbg_hs, float *dbg_n1, float *dbg_attn) {
+  const Model &m = *(Model *)mp;
+  const Config &cfg = m.cfg;
+  int H = cfg.hidden, I = cfg.inter, D = H / cfg.heads, L = cfg.layers;
+  std::vector<SeqInfo> seqs;
+  std::vector<int32_t> pos;
+  std::vector<int> rowTok;
+  int T = 0, mp_off = 0;
+  for (int si = 0; si < nseq; si++) {
+    int n = seq_len[si];
+    if (n <= 0) return -1;
+    if (nmask[si] == 0) return -2;
+    SeqInfo info;
+    info.off = T;
+    info.n = n;
+    const int32_t *op = opt_in + T;
+    const int32_t *ps = pos_in + T;
+    if (has_opt[si]) {
+      info.full.assign((size_t)n * n, 0);
+      for (int i = 0; i < n; i++) {
+        int oi = op[i];
+        for (int j = 0; j < n; j++) {
+          int oj = op[j];
+          if ((oi == -1 && oj == -1) || (oi != -1 && (oj == -1 || oi == oj))) info.full[(size_t)i * n + j] = 1;
+        }
+      }
+    }
+    info.slide.assign((size_t)n * n, 0);
+    int w = cfg.half_window;
+    for (int i = 0; i < n; i++)
+      for (int j = 0; j < n; j++) {
+        int d = ps[i] - ps[j];
+        if (d < 0) d = -d;
+        if (d <= w && (info.full.empty() || info.full[(size_t)i * n + j] == 1)) info.slide[(size_t)i * n + j] = 1;
+      }
+    seqs.push_back(std::move(info));
+    pos.insert(pos.end(), ps, ps + n);
+    for (int k = 0; k < nmask[si]; k++) {
+      int mpos = mask_pos[mp_off + k];
+      if (mpos < 0 || mpos >= n) return -3;
+      rowTok.push_back(T + mpos);
+    }
+    mp_off += nmask[si];
+    T += n;
+  }
+  for (int t = 0; t < T; t++)
+    if (ids[t] < 0 || ids[t] >= cfg.vocab) return -4;
+  int R = (int)rowTok.size();
+
+  std::vector<float> cosG, sinG, cosL, sinL;
+  rope_tables(pos, D, cfg.theta_g, cosG, sinG);
+  rope_tables(pos, D, cfg.theta_l, cosL, sinL);
+
+  const float *tok = m.get("model.embeddings.tok_embeddings.weight");
+  const float *embNorm = m.get("model.embeddings.norm.weight");
+  if (!tok || !embNorm) return -5;
+  std::vector<float> embX((size_t)T * H);
+  parallel_for(T, [&](int lo, int hi) {
+    for (int t = lo; t < hi; t++) std::memcpy(&embX[(size_t)t * H], tok + (size_t)ids[t] * H, sizeof(float) * H);
+  });
+  std::vector<float> cur((size_t)T * H), out((size_t)T * H);
+  layer_norm(cur.data(), embX.data(), T, H, embNorm, nullptr, cfg.eps);
+  if (dbg_hs) std::memcpy(dbg_hs, cur.data(), sizeof(float) * T * H);
+
+  std::vector<float> n1((size_t)T * H), qkv((size_t)T * 3 * H), ctx((size_t)T * H), tmp((size_t)T * H),
+      h1((size_t)T * H), n2((size_t)T * H), wi((size_t)T * 2 * I), act((size_t)T * I);
+  for (int l = 0; l < L; l++) {
+    std::string p = "model.layers." + std::to_string(l) + ".";
+    const float *attnNorm = m.get(p + "attn_norm.weight");
+    const float *Wqkv = m.get(p + "attn.Wqkv.weight");
+    const float *Wo = m.get(p + "attn.Wo.weight");
+    const float *mlpNorm = m.get(p + "mlp_norm.weight");
+    const float *Wi = m.get(p + "mlp.Wi.weight");
+    const float *MlpWo = m.get(p + "mlp.Wo.weight");
+    if (!Wqkv || !Wo || !mlpNorm || !Wi || !MlpWo || (l > 0 && !attnNorm)) return -5;
+    bool sliding = cfg.sliding[l] != 0;
+    // layerFwd, forward.go:284-343.
+    const float *in = cur.data();
+    const float *x1 = in;
+    if (l > 0) {  // layer 0 has no attn_norm (model.go:13-14, forward.go:289-294)
+      layer_norm(n1.data(), in, T, H, attnNorm, nullptr, cfg.eps);
+      x1 = n1.data();
+    }
+    if (dbg_n1) std::memcpy(dbg_n1 + (size_t)l * T * H, x1, sizeof(float) * T * H);
+    linear(qkv.data(), x1, T, H, Wqkv, 3 * H);
+    apply_rope(qkv.data(), T, H, cfg.heads, D, sliding ? cosL.data() : cosG.data(),
+               sliding ? sinL.data() : sinG.data());
+    attn_fwd(cfg, seqs, ctx.data(), qkv.data(), sliding);
+    linear(tmp.data(), ctx.data(), T, H, Wo, H);
+    if (dbg_attn) std::memcpy(dbg_attn + (size_t)l * T * H, tmp.data(), sizeof(float) * T * H);
+    parallel_for(T * H, [&](int lo, int hi) {
+      for (int i = lo; i < hi; i++) h1[i] = in[i] + tmp[i];
+    });
+    layer_norm(n2.data(), h1.data(), T, H, mlpNorm, nullptr, cfg.eps);
+    linear(wi.data(), n2.data(), T, H, Wi, 2 * I);
+    parallel_for(T, [&](int lo, int hi) {
+      for (int t = lo; t < hi; t++) {
+        const float *row = &wi[(size_t)t * 2 * I];
+        float *a = &act[(size_t)t * I];
+        for (int i = 0; i < I; i++) a[i] = gelu(row[i]) * row[I + i];
+      }
+    });
+    linear(tmp.data(), act.data(), T, I, MlpWo, H);
+    parallel_for(T * H, [&](int lo, int hi) {
+      for (int i = lo; i < hi; i++) out[i] = h1[i] + tmp[i];
+    });
+    std::swap(cur, out);
+    if (dbg_hs) std::memcpy(dbg_hs + (size_t)(l + 1) * T * H, cur.data(), sizeof(float) * T * H);
+  }
+  std::vector<float> rows((size_t)R * H);
+  for (int r = 0; r < R; r++) std::memcpy(&rows[(size_t)r * H], &cur[(size_t)rowTok[r] * H], sizeof(float) * H);
+
+  // HeadForward, forward.go:250-282.
+  const float *finalNorm = m.get("model.final_norm.weight");
+  const float *inW = m.get("scorer.input_norm.weight"), *inB = m.get("scorer.input_norm.bias");
+  const float *denseW = m.get("scorer.dense.weight"), *denseB = m.get("scorer.dense.bias");
+  const float *normW = m.get("scorer.norm.weight"), *normB = m.get("scorer.norm.bias");
+  const float *outW = m.get("scorer.out_proj.weight"), *outB = m.get("scorer.out_proj.bias");
+  if (!finalNorm || !inW || !inB || !denseW || !denseB || !normW || !normB || !outW || !outB) return -5;
+  int half = H / 2;
+  std::vector<float> fN((size_t)R * H), s1((size_t)R * H), d((size_t)R * half), ge((size_t)R * half),
+      s2((size_t)R * half);
+  layer_norm(fN.data(), rows.data(), R, H, finalNorm, nullptr, cfg.eps);
+  layer_norm(s1.data(), fN.data(), R, H, inW, inB, 1e-5f);
+  linear(d.data(), s1.data(), R, H, denseW, half);
+  for (int r = 0; r < R; r++)
+    for (int i = 0; i < half; i++) {
+      d[(size_t)r * half + i] += denseB[i];
+      ge[(size_t)r * half + i] = gelu(d[(size_t)r * half + i]);
+    }
+  layer_norm(s2.data(), ge.data(), R, half, normW, normB, 1e-5f);
+  for (int r = 0; r < R; r++) {
+    float s = 0;
+    for (int i = 0; i < half; i++) s += s2[(size_t)r * half + i] * outW[i];
+    logits[r] = s + outB[0];
+  }
+  return 0;
+}
+
+// Pieces exposed for closed-form checks.
+void orc_layer_norm(float *y, const float *x, int rows, int dim, const float *w, const float *b, float eps) {
+  layer_norm(y, x, rows, dim, w, b, eps);
+}
+float orc_gelu(float x) { return gelu(x); }
+void orc_rope_tables(const int32_t *pos, int n, int headDim, double theta, float *cs, float *sn) {
+  std::vector<int32_t> p(pos, pos + n);
+  std::vector<float> c, s;
+  rope_tables(p, headDim, theta, c, s);
+  std::memcpy(cs, c.data(), sizeof(float) * c.size());
+  std::memcpy(sn, s.data(), sizeof(float) * s.size());
+}
+void orc_apply_rope(float *qkv, int T, int H, int heads, int D, const float *cs, const float *sn) {
+  apply_rope(qkv, T, H, heads, D, cs, sn);
+}
+void orc_softmax_masked(float *P, int n, float scale, const uint8_t *mask) { softmax_masked(P, n, scale, mask); }
+
+// local.go:206-262 answer post-processing, float64.
+// calibrated (local.go:225-232): p = softmax(logit / max(T, 1e-4)).
+void orc_calibrated(const double *logits, int k, double temperature, double *probs) {
+  double t = std::max(temperature, 1e-4);
+  double maxv = -INFINITY;
+  std::vector<double> sc(k);
+  for (int i = 0; i < k; i++) {
+    sc[i] = logits[i] / t;
+    maxv = std::max(maxv, sc[i]);
+  }
+  double sum = 0;
+  for (int i = 0; i < k; i++) {
+    probs[i] = std::exp(sc[i] - maxv);
+    sum += probs[i];
+  }
+  for (int i = 0; i < k; i++) probs[i] /= sum;
+}
+// round (local.go:234-237): RoundToEven(x * 10^places) / 10^places.
+double orc_round(double x, int places) {
+  double p = std::pow(10.0, (double)places);
+  return std::nearbyint(x * p) / p;
+}
+// marginConfidence (local.go:241-252).
+double orc_margin_confidence(const double *probs, int n) {
+  if (n <= 1) return 1.0;
+  double pmax = 0;
+  for (int i = 0; i < n; i++) pmax = std::max(pmax, probs[i]);
+  double c = ((double)n * pmax - 1) / (double)(n - 1);
+  return orc_round(std::max(0.0, std::min(1.0, c)), 3);
+}
+// argmax (local.go:254-262): first index wins ties.
+int orc_argmax(const double *x, int n) {
+  int best = 0;
+  for (int i = 0; i < n; i++)
+    if (x[i] > x[best]) best = i;
+  return best;
+}
+
+}  // extern "C"

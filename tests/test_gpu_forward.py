@@ -1,0 +1,216 @@
+"""Forward parity on the GPU: libdecide_hip.so against the CPU oracle on
+identical seeded weights and token ids.
+
+Bars: per-option probabilities (softmax over each
+question's logits, T = 1) within max |dp| <= 1e-5 in the fp32 validation
+mode and <= 2e-3 in bf16, argmax agreement; logits are also compared
+directly (fp32: |dlogit| <= 1e-4 * (1 + |logit|))."""
+import os
+
+import numpy as np
+import pytest
+
+import oracle
+
+pytestmark = pytest.mark.gpu
+
+WORKERS = max(1, min(16, os.cpu_count() or 1))
+
+
+def probs_per_seq(logits, batch):
+    out, off = [], 0
+    for s in batch:
+        k = len(s.mask_pos)
+        z = np.asarray(logits[off: off + k], np.float64)
+        e = np.exp(z - z.max())
+        out.append(e / e.sum())
+        off += k
+    return out
+
+
+def compare(got, want, batch, prec):
+    pg, pw = probs_per_seq(got, batch), probs_per_seq(want, batch)
+    dp = max(float(np.max(np.abs(a - b))) for a, b in zip(pg, pw))
+    agree = np.mean([int(np.argmax(a) == np.argmax(b)) for a, b in zip(pg, pw)])
+    dl = float(np.max(np.abs(np.asarray(got, np.float64) - want)))
+    print(f"{prec}: max|dp| {dp:.3g} max|dlogit| {dl:.3g} argmax agree {agree:.4f} "
+          f"(logit range {float(np.min(want)):.4g}..{float(np.max(want)):.4g})", flush=True)
+    assert np.all(np.isfinite(got))
+    if prec == "fp32":
+        assert dp <= 1e-5
+        assert np.all(np.abs(np.asarray(got, np.float64) - want) <= 1e-4 * (1 + np.abs(want)))
+        assert agree == 1.0
+    else:
+        assert dp <= 2e-3
+        assert agree >= 0.999 or len(batch) < 1000 and agree == 1.0
+
+
+# ---------------------------------------------------------------- small geometry
+def small_cfg():
+    from decide_amd.nn import Config
+
+    return Config(hidden=128, intermediate=192, heads=2, layers=4, vocab=300, half_window=4,
+                  layer_types=["full_attention", "sliding_attention", "sliding_attention", "full_attention"])
+
+
+def ragged_batch(vocab, mask_id, seed=0):
+    """Lengths straddling the 32/64/128 tile edges; independent and plain
+    sequences mixed; a one-token sequence; options of length 1."""
+    from decide_amd.nn import build_sequence
+
+    rng = np.random.default_rng(seed)
+    out = []
+    specs = [(1, []), (9, [1, 5]), (30, [4, 3]), (33, [16, 15]), (64, [8] * 3), (65, [20, 1, 7]),
+             (127, [40, 30]), (128, [64, 64]), (129, [10] * 6), (200, [30, 30, 30])]
+    for i, (prem, opts) in enumerate(specs):
+        ids = list(rng.integers(2, mask_id, size=prem))
+        for ln in opts:
+            ids += [mask_id] + list(rng.integers(2, mask_id, size=ln - 1))
+        if not opts:
+            ids = [mask_id]
+        else:
+            ids.append(1)
+        out.append(build_sequence(np.array(ids, np.int32), mask_id, independent=(i % 3 != 2)))
+    return out
+
+
+@pytest.fixture(scope="module")
+def small():
+    from decide_amd.synth import random_weights
+
+    cfg = small_cfg()
+    w = random_weights(cfg, seed=5, std=0.1)
+    return cfg, w, oracle.OracleModel(cfg, w)
+
+
+@pytest.mark.parametrize("prec", ["fp32", "bf16"])
+def test_small_geometry_ragged(small, prec):
+    from decide_amd import Engine, NoGPUError
+
+    cfg, w, orc = small
+    batch = ragged_batch(cfg.vocab, mask_id=cfg.vocab - 1)
+    oracle.set_workers(WORKERS)
+    want = orc.forward(batch)
+    try:
+        eng = Engine(cfg, w, precision=prec)
+    except NoGPUError:
+        pytest.skip("no GPU")
+    with eng:
+        got = eng.forward(batch)
+        compare(got, want, batch, prec)
+        # one sequence at a time gives the same logits as the batch
+        off = 0
+        for s in batch:
+            one = eng.forward([s])
+            k = len(s.mask_pos)
+            assert np.allclose(one, got[off: off + k], rtol=1e-5, atol=1e-6)
+            off += k
+
+
+# ---------------------------------------------------------------- ModernBERT-base
+@pytest.fixture(scope="module")
+def base():
+    from decide_amd import modernbert_base
+    from decide_amd.synth import random_weights
+
+    cfg = modernbert_base()
+    w = random_weights(cfg, seed=0)
+    return cfg, w, oracle.OracleModel(cfg, w)
+
+
+@pytest.fixture(scope="module")
+def engines(base):
+    from decide_amd import Engine, NoGPUError
+
+    cfg, w, _ = base
+    try:
+        e = {p: Engine(cfg, w, precision=p) for p in ("fp32", "bf16")}
+    except NoGPUError:
+        pytest.skip("no GPU")
+    yield e
+    for x in e.values():
+        x.close()
+
+
+@pytest.mark.parametrize("name,nseq", [("cfg2", None), ("cfg5", None), ("cfg3", 2), ("cfg4", 1)])
+@pytest.mark.parametrize("prec", ["fp32", "bf16"])
+def test_base_config_matches_oracle(base, engines, name, nseq, prec):
+    from decide_amd.synth import config_batch
+
+    cfg, _, orc = base
+    batch = config_batch(name, vocab=cfg.vocab, nseq=nseq)
+    oracle.set_workers(WORKERS)
+    want = orc.forward(batch)
+    got = engines[prec].forward(batch)
+    compare(got, want, batch, prec)
+
+
+def test_cfg3_full_batch_properties(base, engines):
+    """Full cfg3 (64 x 512) in bf16: each sequence's logits do not depend on the
+    rest of the batch, and permuting a sequence's options permutes its logits."""
+    from decide_amd.nn import build_sequence
+    from decide_amd.synth import config_batch
+
+    cfg = base[0]
+    eng = engines["bf16"]
+    batch = config_batch("cfg3", vocab=cfg.vocab)
+    full = eng.forward(batch)
+    assert full.shape == (512,) and np.all(np.isfinite(full))
+    for i in (0, 37, 63):
+        one = eng.forward([batch[i]])
+        assert np.allclose(one, full[8 * i: 8 * i + 8], rtol=1e-5, atol=1e-6)
+    s = batch[5]
+    ids = s.ids.copy()
+    starts = list(s.mask_pos)
+    last = len(ids) - 1
+    spans = [ids[a: (starts[k + 1] if k + 1 < len(starts) else last)] for k, a in enumerate(starts)]
+    perm = [3, 7, 0, 1, 6, 2, 5, 4]
+    pids = np.concatenate([ids[: starts[0]]] + [spans[k] for k in perm] + [ids[last:]]).astype(np.int32)
+    got = eng.forward([build_sequence(pids, 50284, True)])
+    for slot, k in enumerate(perm):
+        assert abs(float(got[slot]) - float(full[8 * 5 + k])) <= 1e-3 * (1 + abs(float(full[8 * 5 + k])))
+
+
+def test_forward_device_matches_host_entry(base, engines):
+    import torch
+
+    from decide_amd.nn import flatten, row_tokens
+    from decide_amd.synth import config_batch
+
+    eng = engines["bf16"]
+    batch = config_batch("cfg3", vocab=base[0].vocab, nseq=3)
+    host = eng.forward(batch)
+    seq_len, ids, pos, opt, nmask, _ = flatten(batch)
+    d = {k: torch.from_numpy(v).cuda() for k, v in dict(ids=ids, pos=pos, opt=opt, rt=row_tokens(batch)).items()}
+    out = torch.zeros(len(host), dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+    eng.forward_device(seq_len, d["ids"].data_ptr(), d["pos"].data_ptr(), d["opt"].data_ptr(), len(host),
+                       d["rt"].data_ptr(), out.data_ptr())
+    eng.check_device_errors()
+    assert np.array_equal(out.cpu().numpy(), host)
+
+
+def test_forward_validation_errors(base, engines):
+    """Model.Forward's input validation (forward.go:145-150, 181-183, 192-196)."""
+    from decide_amd import InvalidArgument
+    from decide_amd.nn import Sequence
+
+    eng = engines["bf16"]
+    good = Sequence(ids=np.array([50281, 7, 50284, 9, 50282], np.int32), pos=np.arange(5, dtype=np.int32),
+                    opt=None, mask_pos=np.array([2], np.int32))
+    assert eng.forward([good]).shape == (1,)
+    cases = [
+        (Sequence(ids=np.zeros(0, np.int32), pos=np.zeros(0, np.int32), opt=None, mask_pos=np.array([0], np.int32)),
+         "nn: malformed sequence 0"),
+        (Sequence(ids=good.ids, pos=good.pos, opt=None, mask_pos=np.zeros(0, np.int32)),
+         "nn: sequence 0 has no options"),
+        (Sequence(ids=good.ids, pos=good.pos, opt=None, mask_pos=np.array([5], np.int32)),
+         "nn: sequence 0 mask position 5 out of range"),
+        (Sequence(ids=np.array([50281, 50368, 50284], np.int32), pos=np.arange(3, dtype=np.int32), opt=None,
+                  mask_pos=np.array([2], np.int32)), "nn: token id 50368 out of range"),
+    ]
+    for seq, msg in cases:
+        with pytest.raises(InvalidArgument) as ei:
+            eng.forward([good, seq] if "sequence 0" not in msg else [seq])
+        assert ei.value.message == msg
+    assert np.isfinite(eng.forward([good])).all()  # the context stays usable

@@ -1,0 +1,113 @@
+"""GEMM parity on the GPU: dn_gemm_f32 (blas.Sgemm semantics, fp32 MFMA)
+against the oracle's Go-order sgemm, and the bf16 device GEMM against a
+float64 product of the same bf16 operands."""
+import math
+
+import numpy as np
+import pytest
+
+import oracle
+from test_oracle import SHAPES, naive
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def eng():
+    from decide_amd import Engine, NoGPUError
+    from decide_amd.nn import Config
+
+    cfg = Config(hidden=128, intermediate=192, heads=2, layers=1, vocab=8, layer_types=["full_attention"])
+    try:
+        e = Engine(cfg, None, precision="fp32")
+    except NoGPUError:
+        pytest.skip("no GPU")
+    yield e
+    e.close()
+
+
+def abs_bound(ta, tb, M, N, K, A, lda, B, ldb):
+    """sum_k |a_ik * b_kj|: the scale of the rounding error of any fp32 summation order."""
+    return naive(ta, tb, M, N, K, np.abs(A), lda, np.abs(B), ldb)
+
+
+@pytest.mark.parametrize("shape", SHAPES)
+def test_gemm_f32_matches_oracle(eng, shape):
+    """TestSgemm / TestGemmMatchesCPU shapes, all transposes x accumulate.
+    Bar: |gpu - oracle| <= 1e-5 * sum_k |a b| (+ |C0| * 2^-23 when accumulating)."""
+    rng = np.random.default_rng(11)
+    M, N, K = shape
+    for ta in (False, True):
+        for tb in (False, True):
+            lda = M if ta else K
+            ldb = K if tb else N
+            A = rng.standard_normal(M * K, dtype=np.float32)
+            B = rng.standard_normal(K * N, dtype=np.float32)
+            bound = abs_bound(ta, tb, M, N, K, A, lda, B, ldb).reshape(-1)
+            for acc in (False, True):
+                C0 = rng.standard_normal(M * N, dtype=np.float32)
+                want = C0.copy()
+                oracle.sgemm(ta, tb, M, N, K, A, lda, B, ldb, want, N, acc, workers=8)
+                got = C0.copy()
+                eng.gemm_f32(ta, tb, M, N, K, A, lda, B, ldb, got, N, acc)
+                tol = 1e-5 * bound + (np.abs(C0) * 2.0 ** -23 if acc else 0) + 1e-30
+                err = np.abs(got.astype(np.float64) - want)
+                assert np.all(err <= tol), (shape, ta, tb, acc, float(np.max(err / tol)))
+                # and the reference test's own bar against exact float64
+                exact = naive(ta, tb, M, N, K, A, lda, B, ldb).reshape(-1) + (C0 if acc else 0)
+                assert np.max(np.abs(got - exact)) <= 1e-3 * math.sqrt(K + 1)
+
+
+def test_gemm_f32_leading_dims_untouched(eng):
+    """TestSgemmLeadingDims / cuda gemm_test.go:78-83: padding columns untouched."""
+    rng = np.random.default_rng(4)
+    M, N, K = 20, 30, 40
+    lda, ldb, ldc = K + 3, N + 5, N + 7
+    A = rng.standard_normal(M * lda, dtype=np.float32)
+    B = rng.standard_normal(K * ldb, dtype=np.float32)
+    C = np.full(M * ldc, 7.0, np.float32)
+    eng.gemm_f32(False, False, M, N, K, A, lda, B, ldb, C, ldc, False)
+    C2 = C.reshape(M, ldc)
+    assert np.max(np.abs(C2[:, :N] - naive(False, False, M, N, K, A, lda, B, ldb))) <= 1e-3
+    assert np.all(C2[:, N:] == 7.0)
+
+
+def test_gemm_cfg1(eng):
+    """cfg1: fp32 X[512x768] . W^T, W[2304x768]; X ~ N(0,1), W ~ N(0,0.02), seed 0,
+    against the Go-order AVX2 sgemm: error-bound rtol 1e-5, and max relative
+    error 1e-5 on entries with |ref| > 1e-3 * max|ref|."""
+    rng = np.random.default_rng(0)
+    M, N, K = 512, 2304, 768
+    X = rng.standard_normal(M * K, dtype=np.float32)
+    W = (rng.standard_normal(N * K, dtype=np.float32) * np.float32(0.02)).astype(np.float32)
+    want = np.zeros(M * N, np.float32)
+    oracle.sgemm(False, True, M, N, K, X, K, W, K, want, N, False, workers=8)
+    got = np.zeros(M * N, np.float32)
+    eng.gemm_f32(False, True, M, N, K, X, K, W, K, got, N, False)
+    bound = (np.abs(X.reshape(M, K)).astype(np.float64) @ np.abs(W.reshape(N, K)).T.astype(np.float64)).reshape(-1)
+    err = np.abs(got.astype(np.float64) - want)
+    ratio = float(np.max(err / (1e-5 * bound)))
+    big = np.abs(want) > 1e-3 * np.abs(want).max()
+    rel = float(np.max(err[big] / np.abs(want[big])))
+    print(f"cfg1: max err/(1e-5*sum|xw|) = {ratio:.3f}, max rel (|ref| large) = {rel:.3g}")
+    assert ratio <= 1.0 and rel <= 1e-5
+
+
+@pytest.mark.parametrize("M", [64, 112, 1000, 2048])
+def test_gemm_bf16_device(eng, M):
+    """bf16 operands, fp32 accumulate: against float64 of the same bf16 values."""
+    import torch
+
+    N, K = 2304, 768
+    g = torch.Generator().manual_seed(M)
+    A = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    B = (torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16)
+    exact = A.double() @ B.double().T
+    bound = A.double().abs() @ B.double().abs().T
+    dA, dB = A.cuda(), B.cuda()
+    dC = torch.zeros(M, N, dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+    eng.gemm_device("bf16", M, N, K, dA.data_ptr(), dB.data_ptr(), dC.data_ptr())
+    eng.synchronize()
+    err = (dC.cpu().double() - exact).abs()
+    assert float((err / (1e-5 * bound + 1e-30)).max()) <= 1.0
