@@ -80,6 +80,8 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=12.0)
     ap.add_argument("--probe-layer", type=int, default=1)
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="run one device copy of MIB MiB first (reference kernel for HBM counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
@@ -115,6 +117,16 @@ def main() -> int:
     def step():
         eng.forward_device(seq_len, d_ids.data_ptr(), d_pos.data_ptr(), d_opt.data_ptr(), R, d_rt.data_ptr(),
                            d_out.data_ptr())
+
+    if args.copy_calibration:
+        nbytes = args.copy_calibration << 20
+        src = torch.ones(nbytes // 4, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"copy calibration: {nbytes} bytes read + {nbytes} bytes written")
+        del src, dst
 
     log(f"warmup {args.warmup}")
     for _ in range(args.warmup):

@@ -448,7 +448,7 @@ const char *dn_last_error(const dn_ctx *c) { return c ? c->err.c_str() : g_err.c
 
 int dn_set_stream(dn_ctx *c, void *stream) {
   if (!c) return DN_INVALID_ARG;
-  c->stream = stream ? (hipStream_t)stream : c->own_stream;
+  c->stream = (hipStream_t)stream;
   return DN_OK;
 }
 

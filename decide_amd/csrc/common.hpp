@@ -56,9 +56,19 @@ template <>
 __device__ __forceinline__ float gelu_erf<float>(float x) {
   return 0.5f * x * (1.0f + (float)erf((double)x * 1.41421356237309504880 / 2.0));
 }
+// erf(x) for the bf16 path, whose result is rounded to bf16 (2^-9 relative)
+// anyway: the rational approximation 7.1.26 of Abramowitz & Stegun,
+// |error| <= 1.5e-7, evaluated with one exp2 and one reciprocal.
+__device__ __forceinline__ float erf_as(float x) {
+  const float ax = fabsf(x);
+  const float t = __frcp_rn(1.0f + 0.3275911f * ax);
+  const float p = t * (0.254829592f + t * (-0.284496736f + t * (1.421413741f + t * (-1.453152027f + t * 1.061405429f))));
+  const float y = 1.0f - p * exp2f(-ax * ax * 1.44269504088896341f);
+  return copysignf(y, x);
+}
 template <>
 __device__ __forceinline__ float gelu_erf<bf16>(float x) {
-  return 0.5f * x * (1.0f + erff(x * 0.70710678118654752440f));
+  return 0.5f * x * (1.0f + erf_as(x * 0.70710678118654752440f));
 }
 
 // Summary of up to 32 consecutive tokens of one sequence, used by the
@@ -82,6 +92,8 @@ struct GemmArgs {
   int n_store;    // columns actually stored (plain epilogue)
   int accumulate; // plain epilogue: C += result
   int rope_cols;  // QKV epilogue: columns [0, rope_cols) are rotated
+  int ngroups;    // N-tile groups per XCD sweep (set by launch_gemm)
+  int order;      // workgroup -> tile order (0: XCD-aware groups)
 };
 
 enum { EPI_F32 = 0, EPI_QKV = 1, EPI_GEGLU = 2 };

@@ -10,80 +10,109 @@
 //               interleaved at upload so each 64-column group holds 32 value
 //               rows followed by the 32 matching gate rows
 //
-// Both operands are K-contiguous (token-major activations, (out,in) weights),
-// so each lane's MFMA operand is one contiguous LDS read. Tiles of BM x BN x
-// (128 bytes of K) are staged through LDS, double buffered, with 16 bytes of
-// padding per 128-byte row so the 32 rows read by one MFMA operand land in
-// distinct bank groups.
+// Design (gfx950):
+//   * Both operands are K-contiguous (token-major activations, (out,in)
+//     weights): every MFMA operand is one contiguous 16-byte LDS read.
+//   * K is staged 128 bytes at a time through an NSTAGE-deep ring of LDS
+//     buffers filled by direct global->LDS loads (global_load_lds_dwordx4), so
+//     NSTAGE-1 stages are in flight while one is consumed and no registers are
+//     spent on staging. Each wave-wide load writes 1 KB = 8 tile rows.
+//   * LDS rows are 128 bytes with the 16-byte chunks XOR-swizzled by
+//     (row >> 1) & 7, so the 16 rows read by a quarter-wave fall in distinct
+//     banks (the swizzle is applied on the global side of the DMA).
+//   * Workgroup -> tile order is XCD-aware: consecutive workgroup ids go
+//     round-robin over the 8 XCDs; each XCD owns a contiguous range of M
+//     panels and sweeps the N tiles in groups small enough that the group's
+//     slice of B stays in that XCD's 4 MB L2 while its A panels stream.
+//   * The epilogue stages the finished tile through LDS so global stores are
+//     full 16-byte-per-lane rows.
+#include <cstdlib>
+
 #include "common.hpp"
 
 namespace {
 
-constexpr int ROWB = 144;  // bytes per LDS tile row: 128 of K + 16 padding
+constexpr int NTHREADS = 256;  // 4 waves, 2 x 2 over the output tile
 
-template <class T, int BM, int BN, int WAVES_M, int WAVES_N, int EPI>
-__global__ __launch_bounds__(WAVES_M *WAVES_N * 64) void gemm_nt_kernel(GemmArgs g) {
+__device__ __forceinline__ int swz(int row) { return (row >> 1) & 7; }
+
+typedef __attribute__((address_space(3))) void lds_void;
+typedef const __attribute__((address_space(1))) void gbl_void;
+
+// s_waitcnt vmcnt(n) with the other counters left alone (gfx9 encoding:
+// vmcnt[3:0] in bits 3:0, vmcnt[5:4] in bits 15:14, expcnt 6:4, lgkmcnt 11:8).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+template <int BM, int BN>
+struct TileOrder {
+  int m0, n0;
+  __device__ __forceinline__ TileOrder(int bid, int tiles_m, int tiles_n, int ngroups, int order) {
+    int tm, tn;
+    const int nt = tiles_m * tiles_n;
+    if (order != 1 && tiles_m % 8 == 0 && tiles_n % ngroups == 0 && nt == (int)gridDim.x) {
+      const int xcd = order == 2 ? bid / (nt / 8) : bid % 8, j = order == 2 ? bid % (nt / 8) : bid / 8;
+      const int pm = tiles_m / 8, gn = tiles_n / ngroups;
+      const int grp = j / (pm * gn), rem = j % (pm * gn);
+      tm = xcd * pm + rem / gn;
+      tn = grp * gn + rem % gn;
+    } else {
+      tm = bid / tiles_n;
+      tn = bid % tiles_n;
+    }
+    m0 = tm * BM;
+    n0 = tn * BN;
+  }
+};
+
+template <class T, int BM, int BN, int NSTAGE, int EPI>
+__global__ __launch_bounds__(NTHREADS) void gemm_nt_kernel(GemmArgs g) {
   using MF = Mfma<T>;
   typedef typename MF::frag frag;
-  constexpr int NT = WAVES_M * WAVES_N * 64;
-  constexpr int KT = 128 / sizeof(T);  // K elements per stage
-  constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;
+  constexpr int KT = 128 / sizeof(T);  // K elements per stage (128-byte rows)
+  constexpr int WM = BM / 2, WN = BN / 2;
   constexpr int TM = WM / 32, TN = WN / 32;
-  constexpr int A_CH = BM * 8 / NT, B_CH = BN * 8 / NT;  // 16-byte chunks per thread
-  static_assert(A_CH * NT == BM * 8 && B_CH * NT == BN * 8, "tile/thread mismatch");
+  constexpr int STAGE = (BM + BN) * 128;
+  constexpr int LOADS = (BM + BN) * 8 / NTHREADS;  // 16-byte DMA loads per thread per stage
+  static_assert(LOADS * NTHREADS == (BM + BN) * 8, "tile rows must be a multiple of 32");
   static_assert(EPI == EPI_F32 || TN % 2 == 0, "paired epilogues need 64-column wave tiles");
+  static_assert(NSTAGE >= 2 && LOADS * (NSTAGE - 2) < 64, "pipeline depth");
+  constexpr int EPI_BYTES = (EPI == EPI_F32) ? BM * (BN + 4) * 4
+                                             : BM * ((EPI == EPI_GEGLU ? BN / 2 : BN) + 8) * (int)sizeof(T);
+  constexpr int SMEM = NSTAGE * STAGE > EPI_BYTES ? NSTAGE * STAGE : EPI_BYTES;
+  __shared__ __attribute__((aligned(1024))) char smem[SMEM];
 
-  __shared__ __attribute__((aligned(16))) char smem[2][(BM + BN) * ROWB];
-
-  const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
-  const int wm = wave / WAVES_N, wn = wave % WAVES_N;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
   const int lr = lane & 31, lh = lane >> 5;
 
-  // XCD-aware tile order: consecutive workgroups go round-robin over the 8
-  // XCDs; give each XCD a contiguous range of tiles (N fastest) so an A row
-  // panel is reused out of that XCD's L2.
-  const int tiles_n = g.N / BN;
-  const int ntiles = gridDim.x;
-  int bid = blockIdx.x;
-  int tile = (ntiles % 8 == 0) ? (bid % 8) * (ntiles / 8) + bid / 8 : bid;
-  const int m0 = (tile / tiles_n) * BM, n0 = (tile % tiles_n) * BN;
+  const TileOrder<BM, BN> to(blockIdx.x, (g.M + BM - 1) / BM, g.N / BN, g.ngroups, g.order);
+  const int m0 = to.m0, n0 = to.n0;
 
-  const char *Ab = (const char *)g.A;
-  const char *Bb = (const char *)g.B;
-  const size_t lda_b = (size_t)g.lda * sizeof(T), ldb_b = (size_t)g.ldb * sizeof(T);
-
-  // Global -> register staging of one K stage (16-byte chunks; 8 threads per
-  // 128-byte row), then register -> LDS. Rows past M re-read row M-1 (their
-  // results are never stored).
-  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-  u32x4 ra[A_CH], rb[B_CH];
-  const char *a_src[A_CH];
-  const char *b_src[B_CH];
-  int a_dst[A_CH], b_dst[B_CH];
+  // DMA sources: load i of this wave fills tile rows 8*(wave + 4i) .. +7;
+  // lane l writes row 8*(wave+4i) + l/8, LDS chunk slot l%8, which holds the
+  // row's logical 16-byte chunk (l%8) ^ swz(row).
+  const char *src[LOADS];
 #pragma unroll
-  for (int i = 0; i < A_CH; i++) {
-    const int c = tid + i * NT, r = c >> 3, cc = c & 7;
-    a_src[i] = Ab + (size_t)min(m0 + r, g.M - 1) * lda_b + cc * 16;
-    a_dst[i] = r * ROWB + cc * 16;
+  for (int i = 0; i < LOADS; i++) {
+    const int r = 8 * (wave + 4 * i) + (lane >> 3);
+    const int c = (lane & 7) ^ swz(r);
+    if (r < BM)
+      src[i] = (const char *)g.A + (size_t)min(m0 + r, g.M - 1) * g.lda * sizeof(T) + c * 16;
+    else
+      src[i] = (const char *)g.B + (size_t)(n0 + r - BM) * g.ldb * sizeof(T) + c * 16;
   }
+  auto issue_part = [&](int stage, int k0, int i0, int i1) {
+    char *dst = smem + stage * STAGE + wave * 1024;
+    const size_t kb = (size_t)k0 * sizeof(T);
 #pragma unroll
-  for (int i = 0; i < B_CH; i++) {
-    const int c = tid + i * NT, r = c >> 3, cc = c & 7;
-    b_src[i] = Bb + (size_t)(n0 + r) * ldb_b + cc * 16;
-    b_dst[i] = (BM + r) * ROWB + cc * 16;
-  }
-#define GEMM_GLOAD(k0)                                                                       \
-  do {                                                                                       \
-    const size_t kb_ = (size_t)(k0) * sizeof(T);                                             \
-    _Pragma("unroll") for (int i = 0; i < A_CH; i++) ra[i] = *(const u32x4 *)(a_src[i] + kb_); \
-    _Pragma("unroll") for (int i = 0; i < B_CH; i++) rb[i] = *(const u32x4 *)(b_src[i] + kb_); \
-  } while (0)
-#define GEMM_SSTORE(buf)                                                                        \
-  do {                                                                                          \
-    _Pragma("unroll") for (int i = 0; i < A_CH; i++) *(u32x4 *)(smem[buf] + a_dst[i]) = ra[i]; \
-    _Pragma("unroll") for (int i = 0; i < B_CH; i++) *(u32x4 *)(smem[buf] + b_dst[i]) = rb[i]; \
-  } while (0)
+    for (int i = i0; i < i1; i++)
+      __builtin_amdgcn_global_load_lds((gbl_void *)(src[i] + kb), (lds_void *)(dst + i * 4096), 16, 0, 0);
+  };
+  auto issue = [&](int stage, int k0) { issue_part(stage, k0, 0, LOADS); };
 
   f32x16 acc[TM][TN];
 #pragma unroll
@@ -93,112 +122,232 @@ __global__ __launch_bounds__(WAVES_M *WAVES_N * 64) void gemm_nt_kernel(GemmArgs
 #pragma unroll
       for (int e = 0; e < 16; e++) acc[i][j][e] = 0.0f;
 
-  const int nk = g.K / KT;
-  GEMM_GLOAD(0);
-  GEMM_SSTORE(0);
-  __syncthreads();
-  for (int kt = 0; kt < nk; kt++) {
-    const int buf = kt & 1;
-    if (kt + 1 < nk) GEMM_GLOAD((kt + 1) * KT);
-    const char *sa = smem[buf] + (wm * WM + lr) * ROWB;
-    const char *sb = smem[buf] + (BM + wn * WN + lr) * ROWB;
-#pragma unroll
-    for (int ks = 0; ks < KT / MF::KSTEP; ks++) {
-      const int kof = (ks * MF::KSTEP + lh * MF::SLOTS) * (int)sizeof(T);
-      frag a[TM], b[TN];
-#pragma unroll
-      for (int i = 0; i < TM; i++) a[i] = *(const frag *)(sa + i * 32 * ROWB + kof);
-#pragma unroll
-      for (int j = 0; j < TN; j++) b[j] = *(const frag *)(sb + j * 32 * ROWB + kof);
+  const int rw = wm * WM, cw = wn * WN;  // wave tile origin inside the block tile
+
+  // QKV: the RoPE factors of this lane's rows (column lr of every 64-wide
+  // head slice) are loaded before the main loop so their latency hides
+  // behind it. They depend on the row and the pair index only.
+  // Wide (TN >= 4) tiles have no registers to spare: they load the factors
+  // per 32-row block in the epilogue instead, one batch of 32 loads each.
+  constexpr bool PREFETCH = EPI == EPI_QKV && TN <= 2;
+  float rcos[PREFETCH ? TM : 1][16], rsin[PREFETCH ? TM : 1][16];
+  if constexpr (PREFETCH) {
+    if (n0 + cw < g.rope_cols) {
 #pragma unroll
       for (int i = 0; i < TM; i++)
 #pragma unroll
-        for (int j = 0; j < TN; j++) acc[i][j] = MF::mma(a[i], b[j], acc[i][j]);
+        for (int e = 0; e < 16; e++) {
+          const size_t tr = (size_t)min(m0 + rw + i * 32 + mfma_row(e, lane), g.M - 1);
+          rcos[i][e] = g.cos_t[tr * 32 + lr];
+          rsin[i][e] = g.sin_t[tr * 32 + lr];
+        }
     }
-    if (kt + 1 < nk) GEMM_SSTORE(buf ^ 1);
-    __syncthreads();
   }
 
-#undef GEMM_GLOAD
-#undef GEMM_SSTORE
+  const int nk = g.K / KT;
+#pragma unroll
+  for (int s = 0; s < NSTAGE - 1; s++)
+    if (s < nk) issue(s, s * KT);
 
-  // Epilogue.
-  const int row_base = m0 + wm * WM;
-  const int col_base = n0 + wn * WN;
+  constexpr int NKS = KT / MF::KSTEP;                  // MFMA k steps per stage
+  constexpr int PER_KS = (LOADS + NKS - 1) / NKS;      // next-stage loads issued per k step
+  static_assert(NKS % 2 == 0, "operand double buffering alternates per k step");
+
+  // MFMA operands are double buffered across k steps: the fragments of step
+  // ks+1 (or of the next stage's step 0) are read from LDS while the MFMAs of
+  // step ks run. The next stage's readiness (vmcnt + barrier) is established
+  // at the end of each stage, after the last MFMAs of the stage are issued.
+  frag fa[2][TM], fb[2][TN];
+  auto load_frags = [&](int buf, int stage, int ks) {
+    const char *sa = smem + stage * STAGE;
+    const char *sb = sa + BM * 128;
+    const int ke = ks * MF::KSTEP + lh * MF::SLOTS;  // first k element of this lane's operand
+    const int chunk = ke * (int)sizeof(T) / 16, within = ke * (int)sizeof(T) % 16;
+#pragma unroll
+    for (int i = 0; i < TM; i++) {
+      const int r = wm * WM + i * 32 + lr;
+      fa[buf][i] = *(const frag *)(sa + r * 128 + ((chunk ^ swz(r)) << 4) + within);
+    }
+#pragma unroll
+    for (int j = 0; j < TN; j++) {
+      const int r = wn * WN + j * 32 + lr;
+      fb[buf][j] = *(const frag *)(sb + r * 128 + ((chunk ^ swz(r)) << 4) + within);
+    }
+  };
+  // Waits until stage kt has landed for every wave. The RoPE prefetch shares
+  // the vector-memory counter with the LDS DMA and the two kinds may complete
+  // out of order, so the first stage waits for everything.
+  auto stage_ready = [&](int kt) {
+    if (kt + NSTAGE - 2 < nk && !(PREFETCH && kt == 0))
+      wait_vmcnt<LOADS * (NSTAGE - 2)>();
+    else
+      wait_vmcnt<0>();
+    __builtin_amdgcn_s_barrier();
+  };
+
+  stage_ready(0);
+  load_frags(0, 0, 0);
+  for (int kt = 0; kt < nk; kt++) {
+    // Refill the buffer of stage kt-1 (every wave finished reading it before
+    // the barrier that made stage kt visible) with stage kt + NSTAGE - 1.
+    const bool refill = kt + NSTAGE - 1 < nk;
+    const int rstage = (kt + NSTAGE - 1) % NSTAGE, rk = (kt + NSTAGE - 1) * KT;
+#pragma unroll
+    for (int ks = 0; ks < NKS; ks++) {
+      const int cur = ks & 1;
+      // Program order: next step's operand reads, this step's share of the
+      // DMA refill (the DMA writes LDS, so reads placed after it could not be
+      // hoisted above it), then this step's MFMAs.
+      if (ks + 1 < NKS) load_frags(cur ^ 1, kt % NSTAGE, ks + 1);
+      if (refill) {
+        const int i0 = ks * PER_KS < LOADS ? ks * PER_KS : LOADS;
+        const int i1 = (ks + 1) * PER_KS < LOADS ? (ks + 1) * PER_KS : LOADS;
+        issue_part(rstage, rk, i0, i1);
+      }
+#pragma unroll
+      for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++) acc[i][j] = MF::mma(fa[cur][i], fb[cur][j], acc[i][j]);
+      // One MFMA, then all of the next step's operand reads (they get the
+      // rest of the step to land), then the DMA issues, then the MFMAs.
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      if (ks + 1 < NKS) __builtin_amdgcn_sched_group_barrier(0x100, TM + TN, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x020, PER_KS, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, TM * TN - 2, 0);
+      if (ks + 1 == NKS && kt + 1 < nk) {
+        stage_ready(kt + 1);
+        load_frags(cur ^ 1, (kt + 1) % NSTAGE, 0);
+      }
+    }
+  }
+  __builtin_amdgcn_s_barrier();  // all waves done with the ring: reuse it for the epilogue
   if constexpr (EPI == EPI_F32) {
-    float *C = (float *)g.C;
+    constexpr int LD = BN + 4;  // floats per staged row
+    float *st = (float *)smem;
 #pragma unroll
     for (int i = 0; i < TM; i++)
 #pragma unroll
-      for (int j = 0; j < TN; j++) {
-        const int col = col_base + j * 32 + lr;
-        if (col >= g.n_store) continue;
+      for (int j = 0; j < TN; j++)
 #pragma unroll
-        for (int e = 0; e < 16; e++) {
-          const int row = row_base + i * 32 + mfma_row(e, lane);
-          if (row < g.M) {
-            float *p = C + (size_t)row * g.ldc + col;
-            *p = g.accumulate ? *p + acc[i][j][e] : acc[i][j][e];
+        for (int e = 0; e < 16; e++) st[(rw + i * 32 + mfma_row(e, lane)) * LD + cw + j * 32 + lr] = acc[i][j][e];
+    __syncthreads();
+    float *C = (float *)g.C;
+    constexpr int V = BN / 4;  // float4 per row
+    constexpr int ITER = BM * V / NTHREADS;
+    constexpr int BATCH = ITER < 8 ? ITER : 8;
+    static_assert(ITER % BATCH == 0, "epilogue batching");
+    const bool vec = (g.ldc & 3) == 0;
+    // All loads of a batch are issued before its stores (C is read and
+    // written here, so the compiler would otherwise serialise each pair).
+    for (int b0 = 0; b0 < ITER; b0 += BATCH) {
+      float4 old[BATCH];
+#pragma unroll
+      for (int u = 0; u < BATCH; u++) {
+        const int c = tid + (b0 + u) * NTHREADS, r = c / V, c4 = (c % V) * 4;
+        const int row = m0 + r, col = n0 + c4;
+        old[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (g.accumulate && vec && row < g.M && col + 4 <= g.n_store)
+          old[u] = *(const float4 *)(C + (size_t)row * g.ldc + col);
+      }
+#pragma unroll
+      for (int u = 0; u < BATCH; u++) {
+        const int c = tid + (b0 + u) * NTHREADS, r = c / V, c4 = (c % V) * 4;
+        const int row = m0 + r, col = n0 + c4;
+        if (row >= g.M || col >= g.n_store) continue;
+        const float4 v = *(const float4 *)(st + r * LD + c4);
+        float *p = C + (size_t)row * g.ldc + col;
+        if (vec && col + 4 <= g.n_store) {
+          *(float4 *)p = make_float4(v.x + old[u].x, v.y + old[u].y, v.z + old[u].z, v.w + old[u].w);
+        } else {
+          const float vv[4] = {v.x, v.y, v.z, v.w};
+          for (int q = 0; q < 4 && col + q < g.n_store; q++) p[q] = g.accumulate ? p[q] + vv[q] : vv[q];
+        }
+      }
+    }
+  } else {
+    constexpr int OC = EPI == EPI_GEGLU ? BN / 2 : BN;  // output columns of the block tile
+    constexpr int LD = OC + 8;                          // staged row length (elements)
+    T *st = (T *)smem;
+    const bool rot = EPI == EPI_QKV && n0 + cw < g.rope_cols;  // whole wave tile is q/k or v
+#pragma unroll
+    for (int i = 0; i < TM; i++) {
+      float cs[16], sn[16];
+      if constexpr (EPI == EPI_QKV) {
+        if constexpr (PREFETCH) {
+#pragma unroll
+          for (int e = 0; e < 16; e++) {
+            cs[e] = rcos[i][e];
+            sn[e] = rsin[i][e];
+          }
+        } else if (rot) {
+#pragma unroll
+          for (int e = 0; e < 16; e++) {
+            const size_t tr = (size_t)min(m0 + rw + i * 32 + mfma_row(e, lane), g.M - 1);
+            cs[e] = g.cos_t[tr * 32 + lr];
+            sn[e] = g.sin_t[tr * 32 + lr];
           }
         }
       }
-  } else if constexpr (EPI == EPI_QKV) {
-    T *C = (T *)g.C;
 #pragma unroll
-    for (int jp = 0; jp < TN / 2; jp++) {
-      const int c0 = col_base + jp * 64;  // start of one 64-wide head slice
-      const bool rot = c0 < g.rope_cols;
-#pragma unroll
-      for (int i = 0; i < TM; i++)
+      for (int jp = 0; jp < TN / 2; jp++) {
 #pragma unroll
         for (int e = 0; e < 16; e++) {
-          const int row = row_base + i * 32 + mfma_row(e, lane);
-          float a = acc[i][2 * jp][e], b = acc[i][2 * jp + 1][e];
-          if (rot) {
-            const int tr = min(row, g.M - 1);
-            const float c = g.cos_t[(size_t)tr * 32 + lr], s = g.sin_t[(size_t)tr * 32 + lr];
-            const float a2 = a * c - b * s;
-            const float b2 = b * c + a * s;
-            a = a2;
-            b = b2;
-          }
-          if (row < g.M) {
-            T *p = C + (size_t)row * g.ldc + c0 + lr;
-            p[0] = to_elem<T>(a);
-            p[32] = to_elem<T>(b);
+          const int r = rw + i * 32 + mfma_row(e, lane);
+          const float a = acc[i][2 * jp][e], b = acc[i][2 * jp + 1][e];
+          if constexpr (EPI == EPI_QKV) {
+            float x = a, y = b;
+            if (rot) {
+              // Unfused, as the reference's applyRope (ops.go:169-170).
+#pragma clang fp contract(off)
+              x = a * cs[e] - b * sn[e];
+              y = b * cs[e] + a * sn[e];
+            }
+            st[r * LD + cw + jp * 64 + lr] = to_elem<T>(x);
+            st[r * LD + cw + jp * 64 + 32 + lr] = to_elem<T>(y);
+          } else {
+            st[r * LD + (cw + jp * 64) / 2 + lr] = to_elem<T>(gelu_erf<T>(a) * b);
           }
         }
+      }
     }
-  } else {  // EPI_GEGLU
+    __syncthreads();
     T *C = (T *)g.C;
-#pragma unroll
-    for (int jp = 0; jp < TN / 2; jp++) {
-      const int oc = (col_base + jp * 64) / 2 + lr;
-#pragma unroll
-      for (int i = 0; i < TM; i++)
-#pragma unroll
-        for (int e = 0; e < 16; e++) {
-          const int row = row_base + i * 32 + mfma_row(e, lane);
-          const float v = acc[i][2 * jp][e], gt = acc[i][2 * jp + 1][e];
-          if (row < g.M) C[(size_t)row * g.ldc + oc] = to_elem<T>(gelu_erf<T>(v) * gt);
-        }
+    const int oc0 = EPI == EPI_GEGLU ? n0 / 2 : n0;
+    constexpr int EPV = 16 / sizeof(T);  // elements per 16-byte vector
+    constexpr int V = OC / EPV;
+    for (int c = tid; c < BM * V; c += NTHREADS) {
+      const int r = c / V, cc = (c % V) * EPV;
+      const int row = m0 + r;
+      if (row >= g.M) continue;
+      *(uint4 *)(C + (size_t)row * g.ldc + oc0 + cc) = *(const uint4 *)(st + r * LD + cc);
     }
   }
 }
 
-template <class T, int BM, int BN, int WM_, int WN_>
+// fp32 epilogue staging of a BN = 256 tile would exceed LDS; such configs are
+// only used for the bf16 paired epilogues.
+template <class T, int BM, int BN>
+constexpr bool f32_epilogue_fits() {
+  return BM * (BN + 4) * 4 <= 160 * 1024;
+}
+
+template <class T, int BM, int BN, int NSTAGE>
 hipError_t launch_cfg(int epi, const GemmArgs &a, hipStream_t s) {
   const int tiles = ((a.M + BM - 1) / BM) * (a.N / BN);
-  dim3 grid(tiles), block(WM_ * WN_ * 64);
+  dim3 grid(tiles), block(NTHREADS);
   switch (epi) {
     case EPI_F32:
-      hipLaunchKernelGGL((gemm_nt_kernel<T, BM, BN, WM_, WN_, EPI_F32>), grid, block, 0, s, a);
+      if constexpr (f32_epilogue_fits<T, BM, BN>())
+        hipLaunchKernelGGL((gemm_nt_kernel<T, BM, BN, NSTAGE, EPI_F32>), grid, block, 0, s, a);
+      else
+        return hipErrorInvalidValue;
       break;
     case EPI_QKV:
-      hipLaunchKernelGGL((gemm_nt_kernel<T, BM, BN, WM_, WN_, EPI_QKV>), grid, block, 0, s, a);
+      hipLaunchKernelGGL((gemm_nt_kernel<T, BM, BN, NSTAGE, EPI_QKV>), grid, block, 0, s, a);
       break;
     default:
-      hipLaunchKernelGGL((gemm_nt_kernel<T, BM, BN, WM_, WN_, EPI_GEGLU>), grid, block, 0, s, a);
+      hipLaunchKernelGGL((gemm_nt_kernel<T, BM, BN, NSTAGE, EPI_GEGLU>), grid, block, 0, s, a);
       break;
   }
   return hipGetLastError();
@@ -212,13 +361,35 @@ bool gemm_shape_ok(int precision, int N, int K) {
   return N > 0 && K > 0 && N % 128 == 0 && K % kt == 0;
 }
 
-hipError_t launch_gemm(int precision, int epi, const GemmArgs &a, hipStream_t s) {
-  if (a.M <= 0) return hipSuccess;
+hipError_t launch_gemm(int precision, int epi, const GemmArgs &a0, hipStream_t s) {
+  if (a0.M <= 0) return hipSuccess;
+  GemmArgs a = a0;
+  // N groups per XCD sweep: keep the group's slice of B (N/groups rows of
+  // K elements) within about 2 MB of L2.
+  const size_t b_bytes = (size_t)a.N * a.K * (precision == 1 ? 2 : 4);
+  const int tiles_n = a.N / 128;
+  int groups = 1;
+  while (b_bytes / groups > (2u << 20) && groups < tiles_n) {
+    groups++;
+    while (tiles_n % groups) groups++;
+  }
+  a.ngroups = groups;
+  static const int order = getenv("DECIDE_GEMM_ORDER") ? atoi(getenv("DECIDE_GEMM_ORDER")) : 0;
+  a.order = order;
   const bool small = a.M <= 1024;
   if (precision == 1) {
-    if (small) return launch_cfg<bf16, 64, 128, 1, 2>(epi, a, s);
-    return launch_cfg<bf16, 256, 128, 2, 2>(epi, a, s);
+    if (small) return launch_cfg<bf16, 64, 128, 4>(epi, a, s);
+    static const int wide = getenv("DECIDE_GEMM_WIDE") ? atoi(getenv("DECIDE_GEMM_WIDE")) : 0;
+    if (wide && epi != EPI_F32 && a.N % 256 == 0) {
+      a.ngroups = 1;
+      while ((size_t)a.N / a.ngroups * a.K * 2 > (2u << 20) && a.ngroups < a.N / 256) {
+        a.ngroups++;
+        while ((a.N / 256) % a.ngroups) a.ngroups++;
+      }
+      return launch_cfg<bf16, 256, 256, 2>(epi, a, s);
+    }
+    return launch_cfg<bf16, 256, 128, 3>(epi, a, s);
   }
-  if (small) return launch_cfg<float, 64, 128, 1, 2>(epi, a, s);
-  return launch_cfg<float, 256, 128, 2, 2>(epi, a, s);
+  if (small) return launch_cfg<float, 64, 128, 4>(epi, a, s);
+  return launch_cfg<float, 256, 128, 3>(epi, a, s);
 }

@@ -65,7 +65,8 @@ void dn_close(dn_ctx *ctx);
  * call on ctx. Counterpart of cuda.Error.Error (driver.go:123-136). */
 const char *dn_last_error(const dn_ctx *ctx);
 
-/* Runs the context's work on `stream` (a hipStream_t) instead of its own.
+/* Runs the context's work on `stream` (a hipStream_t; NULL is the default
+ * stream) instead of the context's own non-blocking stream.
  * No counterpart in the reference (CUDA's context stream was implicit). */
 int dn_set_stream(dn_ctx *ctx, void *stream);
 
