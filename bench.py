@@ -157,8 +157,17 @@ def main() -> int:
     log("per-launch ms (layer %d): %s" % (args.probe_layer, {k: round(v, 4) for k, v in avg.items()}))
 
     prec = args.precision
-    qkv_flop = 2.0 * T * (3 * H) * H
-    qkv_ach = qkv_flop / (avg["gemm_qkv"] * 1e-3)
+    # Roofline kernel: the Wi projection with the fused GeGLU epilogue, the
+    # largest projection GEMM (N = 2I = 2304, K = H = 768); every launch of its
+    # kernel symbol has this shape, so rocprof's per-symbol average is the
+    # per-launch duration measured here.
+    wi_flop = 2.0 * T * (2 * I) * H
+    wi_ach = wi_flop / (avg["gemm_wi"] * 1e-3)
+    traffic = None
+    tpath = os.path.join(HERE, "profiles", "gemm_wi_geglu_cfg3_traffic.json")
+    if args.config == "cfg3" and prec == "bf16" and os.path.exists(tpath):
+        with open(tpath) as fh:
+            traffic = json.load(fh).get("hbm_bytes_per_launch")
     gemm_ms = avg["gemm_qkv"] + avg["gemm_wo"] + avg["gemm_wi"] + avg["gemm_mlpwo"]
     gemm_tflops = PROJ_FLOP_PER_TOKEN_LAYER * T / (gemm_ms * 1e-3) / 1e12
     result = {
@@ -183,10 +192,11 @@ def main() -> int:
         "projection_gemm_tflops": round(gemm_tflops, 2),
         "projection_gemm_frac_peak": round(gemm_tflops * 1e12 / PEAK[prec], 4),
         "per_launch_ms": {k: round(v, 5) for k, v in avg.items()},
-        "roofline": {"kernel": "gemm_nt_kernel (QKV projection, RoPE epilogue), layer %d" % args.probe_layer,
-                     "bound": "mfma", "achieved": round(qkv_ach / 1e12, 2), "peak": PEAK[prec] / 1e12,
-                     "unit": "TFLOP/s", "frac": round(qkv_ach / PEAK[prec], 4), "traffic": None,
-                     "flop_per_launch": qkv_flop},
+        "roofline": {"kernel": "gemm_nt_kernel<bf16,256,128,3,EPI_GEGLU> (Wi projection + GeGLU), layer %d"
+                               % args.probe_layer,
+                     "bound": "mfma", "achieved": round(wi_ach / 1e12, 2), "peak": PEAK[prec] / 1e12,
+                     "unit": "TFLOP/s", "frac": round(wi_ach / PEAK[prec], 4), "traffic": traffic,
+                     "flop_per_launch": wi_flop, "algorithmic_bytes_per_launch": 2 * (T * H + 2 * I * H + T * I)},
     }
     if not args.no_cpu_baseline:
         log("cpu baseline")

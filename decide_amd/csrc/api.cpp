@@ -51,7 +51,7 @@ struct dn_ctx {
   std::map<std::string, TensorSlot> w;
   DevBuf inv_freq;  // 32 doubles global theta, 32 local
   // workspace
-  DevBuf h, xn, qkv, ctxb, act, rope, kinfo, ids, pos, opt, rowtok, logits, err_flag;
+  DevBuf h, xn, qkv, ctxb, act, rope, kinfo, ids, pos, opt, rowtok, logits, err_flag, head_s1, head_d;
   DevBuf gA, gB, gC;  // dn_gemm_f32 staging
   // batch layout cache
   std::vector<int> lay_len;
@@ -311,12 +311,11 @@ int forward_core(dn_ctx *c, int nseq, const int32_t *seq_len, const int32_t *d_i
     q.N = 3 * H;
     q.K = H;
     q.n_store = 3 * H;
-    q.rope_cols = 2 * H;
-    q.cos_t = sliding ? cos_l : cos_g;
-    q.sin_t = sliding ? sin_l : sin_g;
-    PROBED(ev, DN_PROBE_QKV, "gemm(Wqkv)", launch_gemm(prec, EPI_QKV, q, s));
+    PROBED(ev, DN_PROBE_QKV, "gemm(Wqkv)", launch_gemm(prec, EPI_STORE, q, s));
 
     at.sliding = sliding ? 1 : 0;
+    at.cos_t = sliding ? cos_l : cos_g;
+    at.sin_t = sliding ? sin_l : sin_g;
     PROBED(ev, DN_PROBE_ATTENTION, "attention", launch_attention(prec, at, s));
 
     GemmArgs o{};
@@ -383,7 +382,9 @@ int forward_core(dn_ctx *c, int nseq, const int32_t *seq_len, const int32_t *d_i
   ha.out_b = (const float *)W(c, "scorer.out_proj.bias");
   ha.logits = d_logits;
   ha.err_flag = (int *)c->err_flag.p;
-  HIPCHK(c, "head", launch_head(ha, s));
+  HIPCHK(c, "hipMalloc", ensure(c->head_s1, sizeof(float) * (size_t)std::max(R, 1) * H));
+  HIPCHK(c, "hipMalloc", ensure(c->head_d, sizeof(float) * (size_t)std::max(R, 1) * (H / 2)));
+  HIPCHK(c, "head", launch_head(ha, (float *)c->head_s1.p, (float *)c->head_d.p, s));
   return DN_OK;
 }
 
@@ -437,7 +438,7 @@ void dn_close(dn_ctx *c) {
   for (hipEvent_t e : c->probe_pool) (void)hipEventDestroy(e);
   DevBuf *bufs[] = {&c->inv_freq, &c->h,     &c->xn,       &c->qkv,         &c->ctxb,     &c->act,
                     &c->rope,     &c->kinfo, &c->ids,      &c->pos,         &c->opt,      &c->rowtok,
-                    &c->logits,   &c->err_flag, &c->gA,    &c->gB,          &c->gC,       &c->d_seq_off,
+                    &c->logits,   &c->err_flag, &c->gA,    &c->gB,          &c->gC,       &c->d_seq_off, &c->head_s1, &c->head_d,
                     &c->d_seq_len, &c->d_chunk_off, &c->d_chunk_desc, &c->d_work, &c->d_chunks};
   for (DevBuf *b : bufs) release(*b);
   if (c->own_stream) (void)hipStreamDestroy(c->own_stream);
@@ -461,8 +462,8 @@ int dn_set_config(dn_ctx *c, int hidden, int inter, int heads, int layers, int v
     return fail(c, DN_INVALID_ARG, "nn: incomplete or inconsistent config");
   if (precision != DN_PRECISION_FP32 && precision != DN_PRECISION_BF16)
     return fail(c, DN_INVALID_ARG, "decide_hip: unknown precision " + std::to_string(precision));
-  if (hidden / heads != 64 || hidden % 128 != 0 || inter % 64 != 0 || hidden > 1024)
-    return fail(c, DN_UNSUPPORTED, "decide_hip: this build implements head_dim 64, hidden % 128 == 0 (<= 1024) "
+  if (hidden / heads != 64 || hidden % 256 != 0 || inter % 64 != 0 || hidden > 1024)
+    return fail(c, DN_UNSUPPORTED, "decide_hip: this build implements head_dim 64, hidden % 256 == 0 (<= 1024) "
                                    "and intermediate % 64 == 0");
   (void)hipSetDevice(c->device);
   for (auto &kv : c->w) release(kv.second.buf);
@@ -561,6 +562,7 @@ int dn_forward(dn_ctx *c, int nseq, const int32_t *seq_len, const int32_t *ids, 
   for (int si = 0; si < nseq; si++) {
     const int n = seq_len[si];
     if (n <= 0) return fail(c, DN_INVALID_ARG, "nn: malformed sequence " + std::to_string(si));
+    if (n > 8192) return fail(c, DN_UNSUPPORTED, "decide_hip: sequence " + std::to_string(si) + " is longer than 8192 tokens");
     if (nmask[si] <= 0) return fail(c, DN_INVALID_ARG, "nn: sequence " + std::to_string(si) + " has no options");
     for (int k = 0; k < nmask[si]; k++) {
       const int m = mask_pos[mp + k];
@@ -623,8 +625,11 @@ int dn_forward_device(dn_ctx *c, int nseq, const int32_t *seq_len, const int32_t
   if (rc) return rc;
   if (nseq <= 0 || !seq_len || !d_ids || !d_pos || nrows < 0 || (nrows > 0 && (!d_row_tok || !d_logits)))
     return fail(c, DN_INVALID_ARG, "decide_hip: dn_forward_device: bad argument");
-  for (int s = 0; s < nseq; s++)
+  for (int s = 0; s < nseq; s++) {
     if (seq_len[s] <= 0) return fail(c, DN_INVALID_ARG, "nn: malformed sequence " + std::to_string(s));
+    if (seq_len[s] > 8192)
+      return fail(c, DN_UNSUPPORTED, "decide_hip: sequence " + std::to_string(s) + " is longer than 8192 tokens");
+  }
   (void)hipSetDevice(c->device);
   return forward_core(c, nseq, seq_len, d_ids, d_pos, d_opt_id, nrows, d_row_tok, d_logits);
 }

@@ -1,9 +1,11 @@
-// Fused masked multi-head attention (forward only).
+// Fused masked multi-head attention (forward only), with RoPE applied to q
+// and k on the way in.
 //
 // Replaces the reference's per-(sequence, head) attnFwd
 // (internal/nn/forward.go:347-378): Sgemm1 Q.K^T, softmaxMasked
-// (forward.go:382-409), Sgemm1 P.V; and its dense n x n uint8 masks
-// (forward.go:152-176). Here nothing n x n is materialised:
+// (forward.go:382-409), Sgemm1 P.V; its dense n x n uint8 masks
+// (forward.go:152-176); and applyRope on q and k (internal/nn/ops.go:155-175,
+// forward.go:297-301). Nothing n x n is materialised:
 //   * the mask is evaluated per element from each token's (option id,
 //     position): allowed(i,j) = block(opt_i, opt_j) && (global || |pos_i-pos_j| <= W),
 //     block(a,b) = (a == -1 && b == -1) || (a != -1 && (b == -1 || a == b));
@@ -18,13 +20,23 @@
 // tile: the row max and row sum are in-register plus one exchange with the
 // partner lane. The same register layout is directly the B operand of
 // O^T = V^T . P^T (keys permuted consistently in both operands), so P never
-// leaves registers. V is staged transposed in LDS for that product.
+// leaves registers.
+//
+// Key tiles (64 keys) are visited in a list of the tiles some wave needs; the
+// next tile's K, V and RoPE factors are loaded into registers while the
+// current one is computed. K is rotated and stored key-major; V is stored
+// transposed (d-major) with two keys packed per 32-bit word so each wave's
+// LDS writes are contiguous.
 #include "common.hpp"
 
 namespace {
 
 constexpr int KTILE = 64;   // keys per tile
 constexpr int D = 64;       // head dim
+constexpr int MAXKT = 8192 / KTILE;
+#ifndef WAVES_PER_EU
+#define WAVES_PER_EU 3
+#endif
 
 __device__ __forceinline__ int tile_class(const ChunkInfo &q, const ChunkInfo &k, int sliding, int W) {
   // 0: no allowed pair; 1: every pair allowed; 2: test per element.
@@ -44,7 +56,130 @@ __device__ __forceinline__ int combine(int a, int b) {
 }
 
 template <class T>
-__global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
+struct Staging;
+
+// bf16: a thread stages one (key, 8-element chunk pair (c, c+4)) of K and one
+// (key pair, 8-d group) of V.
+template <>
+struct Staging<bf16> {
+  uint4 k_lo, k_hi, v0, v1;
+  float4 c_lo, c_hi, s_lo, s_hi;
+  int info;
+};
+
+// fp32: two (key, 4-element chunk pair) of K and four (key, 4-d group) of V.
+template <>
+struct Staging<float> {
+  uint4 k_lo[2], k_hi[2], v[4];
+  float4 c[2], s[2];
+  int info;
+};
+
+template <class T>
+__device__ __forceinline__ void stage_load(Staging<T> &st, const T *qkv, int ld, int H, int head, int base, int n,
+                                           int k0, const float *cos_t, const float *sin_t, const int *kinfo,
+                                           int tid) {
+  const uint4 z = {0, 0, 0, 0};
+  const float4 one = {1.f, 1.f, 1.f, 1.f}, zero = {0.f, 0.f, 0.f, 0.f};
+  if constexpr (sizeof(T) == 2) {
+    {  // K: key = tid / 4, chunk c = tid % 4 (elements 8c..8c+7 and 32+8c..)
+      const int key = tid >> 2, c = tid & 3;
+      const bool ok = k0 + key < n;
+      const size_t tok = (size_t)(base + k0 + key);
+      const T *row = qkv + tok * ld + H + head * D;
+      st.k_lo = ok ? *(const uint4 *)(row + 8 * c) : z;
+      st.k_hi = ok ? *(const uint4 *)(row + 32 + 8 * c) : z;
+      st.c_lo = ok ? *(const float4 *)(cos_t + tok * 32 + 8 * c) : one;
+      st.c_hi = ok ? *(const float4 *)(cos_t + tok * 32 + 8 * c + 4) : one;
+      st.s_lo = ok ? *(const float4 *)(sin_t + tok * 32 + 8 * c) : zero;
+      st.s_hi = ok ? *(const float4 *)(sin_t + tok * 32 + 8 * c + 4) : zero;
+    }
+    {  // V: key pair p = tid % 32, d group g = tid / 32
+      const int p = tid & 31, g = tid >> 5;
+      const int k = k0 + 2 * p;
+      st.v0 = k < n ? *(const uint4 *)(qkv + (size_t)(base + k) * ld + 2 * H + head * D + 8 * g) : z;
+      st.v1 = k + 1 < n ? *(const uint4 *)(qkv + (size_t)(base + k + 1) * ld + 2 * H + head * D + 8 * g) : z;
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < 2; j++) {  // K: (key, chunk c in 0..7) = item tid + 256 j
+      const int it = tid + 256 * j, key = it >> 3, c = it & 7;
+      const bool ok = k0 + key < n;
+      const size_t tok = (size_t)(base + k0 + key);
+      const T *row = qkv + tok * ld + H + head * D;
+      st.k_lo[j] = ok ? *(const uint4 *)(row + 4 * c) : z;
+      st.k_hi[j] = ok ? *(const uint4 *)(row + 32 + 4 * c) : z;
+      st.c[j] = ok ? *(const float4 *)(cos_t + tok * 32 + 4 * c) : one;
+      st.s[j] = ok ? *(const float4 *)(sin_t + tok * 32 + 4 * c) : zero;
+    }
+#pragma unroll
+    for (int j = 0; j < 4; j++) {  // V: key = tid % 64, d group g = tid / 64 + 4 j
+      const int key = tid & 63, g = (tid >> 6) + 4 * j;
+      st.v[j] = k0 + key < n ? *(const uint4 *)(qkv + (size_t)(base + k0 + key) * ld + 2 * H + head * D + 4 * g) : z;
+    }
+  }
+  st.info = (tid < KTILE && k0 + tid < n) ? kinfo[base + k0 + tid] : 0;
+}
+
+// RoPE on one chunk pair, unfused like applyRope (ops.go:169-170).
+__device__ __forceinline__ void rope4(float *lo, float *hi, const float *c, const float *s) {
+#pragma clang fp contract(off)
+#pragma unroll
+  for (int e = 0; e < 4; e++) {
+    const float a = lo[e], b = hi[e];
+    lo[e] = a * c[e] - b * s[e];
+    hi[e] = b * c[e] + a * s[e];
+  }
+}
+
+template <class T>
+__device__ __forceinline__ void stage_store(const Staging<T> &st, char *sK, char *sV, int *sInfo, int tid, int ROWK,
+                                            int ROWV) {
+  if constexpr (sizeof(T) == 2) {
+    const int key = tid >> 2, c = tid & 3;
+    const bf16 *lo = (const bf16 *)&st.k_lo, *hi = (const bf16 *)&st.k_hi;
+    float flo[8], fhi[8];
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+      flo[e] = (float)lo[e];
+      fhi[e] = (float)hi[e];
+    }
+    rope4(flo, fhi, (const float *)&st.c_lo, (const float *)&st.s_lo);
+    rope4(flo + 4, fhi + 4, (const float *)&st.c_hi, (const float *)&st.s_hi);
+    bf16x8 olo, ohi;
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+      olo[e] = (bf16)flo[e];
+      ohi[e] = (bf16)fhi[e];
+    }
+    *(bf16x8 *)(sK + key * ROWK + 16 * c) = olo;
+    *(bf16x8 *)(sK + key * ROWK + 64 + 16 * c) = ohi;
+    const int p = tid & 31, g = tid >> 5;
+    const uint16_t *a = (const uint16_t *)&st.v0, *b = (const uint16_t *)&st.v1;
+#pragma unroll
+    for (int e = 0; e < 8; e++) *(uint32_t *)(sV + (8 * g + e) * ROWV + 4 * p) = (uint32_t)a[e] | ((uint32_t)b[e] << 16);
+  } else {
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+      const int it = tid + 256 * j, key = it >> 3, c = it & 7;
+      float4 lo = *(const float4 *)&st.k_lo[j], hi = *(const float4 *)&st.k_hi[j];
+      rope4((float *)&lo, (float *)&hi, (const float *)&st.c[j], (const float *)&st.s[j]);
+      *(float4 *)(sK + key * ROWK + 16 * c) = lo;
+      *(float4 *)(sK + key * ROWK + 128 + 16 * c) = hi;
+    }
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const int key = tid & 63, g = (tid >> 6) + 4 * j;
+      const float *v = (const float *)&st.v[j];
+#pragma unroll
+      for (int e = 0; e < 4; e++) *(float *)(sV + (4 * g + e) * ROWV + 4 * key) = v[e];
+    }
+  }
+  if (tid < KTILE) sInfo[tid] = st.info;
+}
+
+template <class T>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_PER_EU))) void attention_kernel(AttnArgs a) {
   using MF = Mfma<T>;
   typedef typename MF::frag frag;
   constexpr int ROWK = D * sizeof(T) + 16;       // K tile row bytes (key-major)
@@ -52,38 +187,89 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) char sK[KTILE * ROWK];
   __shared__ __attribute__((aligned(16))) char sV[D * ROWV];
   __shared__ __attribute__((aligned(16))) int sInfo[KTILE];
+  __shared__ uint8_t sCode[MAXKT];  // per key tile: 2-bit class of each wave
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int lr = lane & 31, lh = lane >> 5;
-  const int4 wk = a.work[blockIdx.x];
-  const int s = wk.x, q0 = wk.y, head = blockIdx.y;
+  // Linear grid, XCD-aware: workgroup ids go round-robin over the 8 XCDs, so
+  // XCD x gets the contiguous range [x*per, (x+1)*per) of the logical order
+  // (work item, head) with the q blocks of one sequence and its 12 heads
+  // adjacent: the K/V rows, RoPE factors and chunk summaries they share are
+  // reused out of that XCD's L2.
+  const int total = a.nwork * a.heads;
+  const int bid = blockIdx.x;
+  int logical = bid;
+  if (total % 8 == 0) logical = (bid % 8) * (total / 8) + bid / 8;
+  const int4 wk = a.work[logical / a.heads];
+  const int s = wk.x, q0 = wk.y, head = logical % a.heads;
   const int n = a.seq_len[s], base = a.seq_off[s], cbase = a.chunk_off[s];
   const int nch = (n + 31) / 32;
   const int H = a.H, ld = 3 * H;
   const T *qkv = (const T *)a.qkv;
+  const int nkt = (n + KTILE - 1) / KTILE;
 
-  ChunkInfo empty = {0, 0, 1, 0, 0, 0, 0, 0};
-  ChunkInfo qc[4];
+  // Classify every key tile against the 4 query chunks of this workgroup.
+  {
+    const ChunkInfo empty = {0, 0, 1, 0, 0, 0, 0, 0};
+    ChunkInfo qc[4];
 #pragma unroll
-  for (int w = 0; w < 4; w++) {
-    const int c = q0 / 32 + w;
-    qc[w] = c < nch ? a.chunks[cbase + c] : empty;
+    for (int w = 0; w < 4; w++) {
+      const int c = q0 / 32 + w;
+      qc[w] = c < nch ? a.chunks[cbase + c] : empty;
+    }
+    for (int kt = tid; kt < nkt; kt += 256) {
+      const ChunkInfo kc0 = a.chunks[cbase + 2 * kt];
+      const ChunkInfo kc1 = (2 * kt + 1 < nch) ? a.chunks[cbase + 2 * kt + 1] : empty;
+      int code = 0;
+#pragma unroll
+      for (int w = 0; w < 4; w++)
+        code |= combine(tile_class(qc[w], kc0, a.sliding, a.half_window),
+                        tile_class(qc[w], kc1, a.sliding, a.half_window))
+                << (2 * w);
+      sCode[kt] = (uint8_t)code;
+    }
   }
 
-  // This lane's query.
+  // This lane's query, its RoPE factors and the rotated Q^T operand
+  // (B operand: column = query, k = head dim).
   const int q = q0 + wave * 32 + lr;
   const bool qvalid = q < n;
   const int qq = qvalid ? q : n - 1;
   const int qinfo = a.kinfo[base + qq];
   const int qopt = (qinfo >> 16) - 1, qpos = qinfo & 0xffff;
-
-  // Q^T operand fragments (B operand: column = query, k = head dim).
   constexpr int NKS = D / MF::KSTEP;
   frag qf[NKS];
   {
     const T *qrow = qkv + (size_t)(base + qq) * ld + head * D;
+    const float *cq = a.cos_t + (size_t)(base + qq) * 32, *sq = a.sin_t + (size_t)(base + qq) * 32;
 #pragma unroll
     for (int ks = 0; ks < NKS; ks++) qf[ks] = *(const frag *)(qrow + ks * MF::KSTEP + lh * MF::SLOTS);
+    // Pairs (i, i+32): step ks holds i = ks*KSTEP + lh*SLOTS + u, its partner
+    // is in step ks + NKS/2 at the same slot.
+#pragma unroll
+    for (int ks = 0; ks < NKS / 2; ks++)
+#pragma unroll
+      for (int u = 0; u < MF::SLOTS; u++) {
+#pragma clang fp contract(off)
+        const int i = ks * MF::KSTEP + lh * MF::SLOTS + u;
+        const float c = cq[i], sn = sq[i];
+        float x, y;
+        if constexpr (sizeof(T) == 2) {
+          x = (float)qf[ks][u];
+          y = (float)qf[ks + NKS / 2][u];
+        } else {
+          x = qf[ks];
+          y = qf[ks + NKS / 2];
+        }
+        const float x2 = x * c - y * sn, y2 = y * c + x * sn;
+        if constexpr (sizeof(T) == 2) {
+          qf[ks][u] = (bf16)x2;
+          qf[ks + NKS / 2][u] = (bf16)y2;
+        } else {
+          qf[ks] = x2;
+          qf[ks + NKS / 2] = y2;
+        }
+      }
   }
 
   f32x16 ot[2];
@@ -93,136 +279,118 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
     for (int e = 0; e < 16; e++) ot[i][e] = 0.0f;
   float m_run = -INFINITY, l_run = 0.0f;
 
-  const int nkt = (n + KTILE - 1) / KTILE;
-  for (int kt = 0; kt < nkt; kt++) {
+  __syncthreads();  // sCode visible
+  auto next_tile = [&](int kt) {
+    while (kt < nkt && sCode[kt] == 0) kt++;
+    return kt;
+  };
+  int kt = next_tile(0);
+  Staging<T> st;
+  if (kt < nkt) stage_load<T>(st, qkv, ld, H, head, base, n, kt * KTILE, a.cos_t, a.sin_t, a.kinfo, tid);
+
+  while (kt < nkt) {
     const int k0 = kt * KTILE;
-    const ChunkInfo kc0 = a.chunks[cbase + 2 * kt];
-    const ChunkInfo kc1 = (2 * kt + 1 < nch) ? a.chunks[cbase + 2 * kt + 1] : empty;
-    int cls[4];
-    bool need = false;
-#pragma unroll
-    for (int w = 0; w < 4; w++) {
-      cls[w] = combine(tile_class(qc[w], kc0, a.sliding, a.half_window),
-                       tile_class(qc[w], kc1, a.sliding, a.half_window));
-      need |= cls[w] != 0;
-    }
-    if (!need) continue;  // uniform over the workgroup
-
+    const int mycls = (sCode[kt] >> (2 * wave)) & 3;
     __syncthreads();  // previous tile fully consumed
-    // Stage K (key-major) and V^T (d-major) for keys k0..k0+63; zero beyond n.
-    constexpr int CPR = D * sizeof(T) / 16;  // 16-byte chunks per key row
-    constexpr int EPC = 16 / sizeof(T);      // elements per chunk
-#pragma unroll
-    for (int c = tid; c < KTILE * CPR; c += 256) {
-      const int key = c / CPR, cc = c % CPR;
-      uint4 kv = {0, 0, 0, 0}, vv = {0, 0, 0, 0};
-      if (k0 + key < n) {
-        const T *row = qkv + (size_t)(base + k0 + key) * ld + head * D + cc * EPC;
-        kv = *(const uint4 *)(row + H);
-        vv = *(const uint4 *)(row + 2 * H);
-      }
-      *(uint4 *)(sK + key * ROWK + cc * 16) = kv;
-      const T *ve = (const T *)&vv;
-#pragma unroll
-      for (int e = 0; e < EPC; e++) *(T *)(sV + (cc * EPC + e) * ROWV + key * sizeof(T)) = ve[e];
-    }
-    if (tid < KTILE) sInfo[tid] = (k0 + tid < n) ? a.kinfo[base + k0 + tid] : 0;
+    stage_store<T>(st, sK, sV, sInfo, tid, ROWK, ROWV);
     __syncthreads();
+    const int kn = next_tile(kt + 1);
+    if (kn < nkt) stage_load<T>(st, qkv, ld, H, head, base, n, kn * KTILE, a.cos_t, a.sin_t, a.kinfo, tid);
 
-    const int mycls = cls[wave];
-    if (mycls == 0) continue;
-
-    // S^T = K . Q^T for 64 keys x 32 queries (two 32x32 tiles).
-    f32x16 st[2];
+    if (mycls != 0) {
+      // S^T = K . Q^T for 64 keys x 32 queries (two 32x32 tiles).
+      f32x16 sT[2];
 #pragma unroll
-    for (int i = 0; i < 2; i++)
+      for (int i = 0; i < 2; i++)
 #pragma unroll
-      for (int e = 0; e < 16; e++) st[i][e] = 0.0f;
+        for (int e = 0; e < 16; e++) sT[i][e] = 0.0f;
 #pragma unroll
-    for (int ks = 0; ks < NKS; ks++) {
-      const int kof = (ks * MF::KSTEP + lh * MF::SLOTS) * (int)sizeof(T);
+      for (int ks = 0; ks < NKS; ks++) {
+        const int kof = (ks * MF::KSTEP + lh * MF::SLOTS) * (int)sizeof(T);
 #pragma unroll
-      for (int i = 0; i < 2; i++) {
-        frag kf = *(const frag *)(sK + (i * 32 + lr) * ROWK + kof);
-        st[i] = MF::mma(kf, qf[ks], st[i]);
+        for (int i = 0; i < 2; i++) {
+          frag kf = *(const frag *)(sK + (i * 32 + lr) * ROWK + kof);
+          sT[i] = MF::mma(kf, qf[ks], sT[i]);
+        }
       }
-    }
 
-    // Scale, mask, running max.
-    float mx = -INFINITY;
+      // Scale, mask, running max.
+      float mx = -INFINITY;
 #pragma unroll
-    for (int i = 0; i < 2; i++)
+      for (int i = 0; i < 2; i++)
 #pragma unroll
-      for (int g = 0; g < 4; g++) {
-        const int kl = i * 32 + 8 * g + 4 * lh;  // 4 consecutive keys kl..kl+3
-        int4 inf4 = {0, 0, 0, 0};
-        if (mycls == 2) inf4 = *(const int4 *)(sInfo + kl);
-        const int *inf = (const int *)&inf4;
+        for (int g = 0; g < 4; g++) {
+          const int kl = i * 32 + 8 * g + 4 * lh;  // 4 consecutive keys kl..kl+3
+          int4 inf4 = {0, 0, 0, 0};
+          if (mycls == 2) inf4 = *(const int4 *)(sInfo + kl);
+          const int *inf = (const int *)&inf4;
 #pragma unroll
-        for (int u = 0; u < 4; u++) {
-          float x = st[i][4 * g + u] * a.scale_log2;
-          if (mycls == 2) {
-            const int ko = (inf[u] >> 16) - 1, kp = inf[u] & 0xffff;
-            bool ok = k0 + kl + u < n;
-            ok = ok && (qopt == -1 ? ko == -1 : (ko == -1 || ko == qopt));
-            ok = ok && (!a.sliding || abs(qpos - kp) <= a.half_window);
-            x = ok ? x : -INFINITY;
+          for (int u = 0; u < 4; u++) {
+            float x = sT[i][4 * g + u] * a.scale_log2;
+            if (mycls == 2) {
+              const int ko = (inf[u] >> 16) - 1, kp = inf[u] & 0xffff;
+              bool ok = k0 + kl + u < n;
+              ok = ok && (qopt == -1 ? ko == -1 : (ko == -1 || ko == qopt));
+              ok = ok && (!a.sliding || abs(qpos - kp) <= a.half_window);
+              x = ok ? x : -INFINITY;
+            }
+            sT[i][4 * g + u] = x;
+            mx = fmaxf(mx, x);
           }
-          st[i][4 * g + u] = x;
-          mx = fmaxf(mx, x);
         }
-      }
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
-    const float m_new = fmaxf(m_run, mx);
-    const float m_use = m_new == -INFINITY ? 0.0f : m_new;
-    const float alpha = exp2f(m_run - m_use);
-    float psum = 0.0f;
+      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      const float m_new = fmaxf(m_run, mx);
+      const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+      const float alpha = exp2f(m_run - m_use);
+      float psum = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 2; i++)
+      for (int i = 0; i < 2; i++)
 #pragma unroll
-      for (int e = 0; e < 16; e++) {
-        const float p = exp2f(st[i][e] - m_use);
-        st[i][e] = p;
-        psum += p;
-      }
-    l_run = l_run * alpha + psum;
-    m_run = m_new;
+        for (int e = 0; e < 16; e++) {
+          const float p = exp2f(sT[i][e] - m_use);
+          sT[i][e] = p;
+          psum += p;
+        }
+      l_run = l_run * alpha + psum;
+      m_run = m_new;
 #pragma unroll
-    for (int i = 0; i < 2; i++)
+      for (int i = 0; i < 2; i++)
 #pragma unroll
-      for (int e = 0; e < 16; e++) ot[i][e] *= alpha;
+        for (int e = 0; e < 16; e++) ot[i][e] *= alpha;
 
-    // O^T += V^T . P^T. k step ks covers accumulator registers
-    // [ks*SLOTS, ks*SLOTS + SLOTS) of the flattened S^T tiles; accumulator r
-    // of tile i on lane half lh is key 32*i + 8*((r%16)/4) + 4*lh + r%4.
-    constexpr int NPV = KTILE / MF::KSTEP;
+      // O^T += V^T . P^T. k step ks covers accumulator registers
+      // [ks*SLOTS, ks*SLOTS + SLOTS) of the flattened S^T tiles; accumulator r
+      // of tile i on lane half lh is key 32*i + 8*((r%16)/4) + 4*lh + r%4.
+      constexpr int NPV = KTILE / MF::KSTEP;
 #pragma unroll
-    for (int ks = 0; ks < NPV; ks++) {
-      frag pf;
-      if constexpr (sizeof(T) == 2) {
-        const int ti = ks >> 1, r0 = (ks & 1) * 8;
-#pragma unroll
-        for (int u = 0; u < 8; u++) pf[u] = (bf16)st[ti][r0 + u];
-      } else {
-        pf = st[ks >> 4][ks & 15];
-      }
-#pragma unroll
-      for (int i = 0; i < 2; i++) {
-        const char *vrow = sV + (i * 32 + lr) * ROWV;
-        frag vf;
+      for (int ks = 0; ks < NPV; ks++) {
+        frag pf;
         if constexpr (sizeof(T) == 2) {
-          const int kb = 32 * (ks >> 1) + 16 * (ks & 1) + 4 * lh;
-          bf16x4 lo = *(const bf16x4 *)(vrow + kb * 2);
-          bf16x4 hi = *(const bf16x4 *)(vrow + (kb + 8) * 2);
-          vf = (bf16x8){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+          const int ti = ks >> 1, r0 = (ks & 1) * 8;
+#pragma unroll
+          for (int u = 0; u < 8; u++) pf[u] = (bf16)sT[ti][r0 + u];
         } else {
-          const int r = ks & 15;
-          const int key = 32 * (ks >> 4) + 8 * (r >> 2) + 4 * lh + (r & 3);
-          vf = *(const float *)(vrow + key * 4);
+          pf = sT[ks >> 4][ks & 15];
         }
-        ot[i] = MF::mma(vf, pf, ot[i]);
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+          const char *vrow = sV + (i * 32 + lr) * ROWV;
+          frag vf;
+          if constexpr (sizeof(T) == 2) {
+            const int kb = 32 * (ks >> 1) + 16 * (ks & 1) + 4 * lh;
+            bf16x4 lo = *(const bf16x4 *)(vrow + kb * 2);
+            bf16x4 hi = *(const bf16x4 *)(vrow + (kb + 8) * 2);
+            vf = (bf16x8){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+          } else {
+            const int r = ks & 15;
+            const int key = 32 * (ks >> 4) + 8 * (r >> 2) + 4 * lh + (r & 3);
+            vf = *(const float *)(vrow + key * 4);
+          }
+          ot[i] = MF::mma(vf, pf, ot[i]);
+        }
       }
     }
+    kt = kn;
   }
 
   // Normalise and store ctx[token][head*64 + d].
@@ -235,8 +403,14 @@ __global__ __launch_bounds__(256) void attention_kernel(AttnArgs a) {
 #pragma unroll
       for (int g = 0; g < 4; g++) {
         const int d0 = i * 32 + 8 * g + 4 * lh;
-#pragma unroll
-        for (int u = 0; u < 4; u++) out[d0 + u] = to_elem<T>(ot[i][4 * g + u] * inv);
+        if constexpr (sizeof(T) == 2) {
+          bf16x4 o = {(bf16)(ot[i][4 * g] * inv), (bf16)(ot[i][4 * g + 1] * inv), (bf16)(ot[i][4 * g + 2] * inv),
+                      (bf16)(ot[i][4 * g + 3] * inv)};
+          *(bf16x4 *)(out + d0) = o;
+        } else {
+          *(float4 *)(out + d0) = make_float4(ot[i][4 * g] * inv, ot[i][4 * g + 1] * inv, ot[i][4 * g + 2] * inv,
+                                              ot[i][4 * g + 3] * inv);
+        }
       }
   }
 }
@@ -271,7 +445,7 @@ __global__ void chunk_summary_kernel(const int *kinfo, const int4 *desc, ChunkIn
 
 hipError_t launch_attention(int precision, const AttnArgs &a, hipStream_t s) {
   if (a.nwork <= 0) return hipSuccess;
-  dim3 grid(a.nwork, a.heads), block(256);
+  dim3 grid(a.nwork * a.heads), block(256);
   if (precision == 1)
     hipLaunchKernelGGL(attention_kernel<bf16>, grid, block, 0, s, a);
   else

@@ -87,16 +87,14 @@ struct GemmArgs {
   const void *A;  // M x K, row stride lda (elements)
   const void *B;  // N x K, row stride ldb (weights, PyTorch (out,in) layout)
   void *C;        // output
-  const float *cos_t, *sin_t;  // RoPE tables [M x 32] (QKV epilogue)
   int M, N, K, lda, ldb, ldc;
-  int n_store;    // columns actually stored (plain epilogue)
-  int accumulate; // plain epilogue: C += result
-  int rope_cols;  // QKV epilogue: columns [0, rope_cols) are rotated
+  int n_store;    // columns actually stored (fp32 epilogue)
+  int accumulate; // fp32 epilogue: C += result
   int ngroups;    // N-tile groups per XCD sweep (set by launch_gemm)
   int order;      // workgroup -> tile order (0: XCD-aware groups)
 };
 
-enum { EPI_F32 = 0, EPI_QKV = 1, EPI_GEGLU = 2 };
+enum { EPI_F32 = 0, EPI_STORE = 1, EPI_GEGLU = 2 };
 
 hipError_t launch_gemm(int precision, int epi, const GemmArgs &a, hipStream_t s);
 bool gemm_shape_ok(int precision, int N, int K);
@@ -107,6 +105,7 @@ struct AttnArgs {
   const int *kinfo;   // per token: ((opt+1) << 16) | pos
   const ChunkInfo *chunks;
   const int4 *work;   // (seq, q0, 0, 0) per workgroup
+  const float *cos_t, *sin_t;  // RoPE tables [T x 32] of this layer's theta
   const int *seq_off, *seq_len, *chunk_off;
   int nwork, H, heads, sliding, half_window;
   float scale_log2;   // softmax scale * log2(e)
@@ -129,6 +128,6 @@ struct HeadArgs {
   float *logits;
   int *err_flag;
 };
-hipError_t launch_head(const HeadArgs &a, hipStream_t s);
+hipError_t launch_head(const HeadArgs &a, float *s1, float *d, hipStream_t s);
 hipError_t launch_pack(const float *src, int trans, int rows, int cols, int ld, float *dst, int dst_rows,
                        int dst_cols, hipStream_t s);

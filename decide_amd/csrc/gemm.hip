@@ -4,7 +4,8 @@
 // (internal/nn/forward.go:122-124, internal/blas/gemm.go:61-138) for the four
 // per-layer projections, with the elementwise work that follows each of them
 // fused into the epilogue:
-//   EPI_QKV   : RoPE on the q/k columns (internal/nn/ops.go:155-175), store qkv
+//   EPI_STORE : store in the operand type (qkv; RoPE is applied by the
+//               attention kernel as it loads q and k)
 //   EPI_F32   : store fp32, optionally C += (the residual adds, forward.go:318-322, 338-342)
 //   EPI_GEGLU : act = gelu(value) * gate (forward.go:327-336); the Wi rows are
 //               interleaved at upload so each 64-column group holds 32 value
@@ -124,26 +125,6 @@ __global__ __launch_bounds__(NTHREADS) void gemm_nt_kernel(GemmArgs g) {
 
   const int rw = wm * WM, cw = wn * WN;  // wave tile origin inside the block tile
 
-  // QKV: the RoPE factors of this lane's rows (column lr of every 64-wide
-  // head slice) are loaded before the main loop so their latency hides
-  // behind it. They depend on the row and the pair index only.
-  // Wide (TN >= 4) tiles have no registers to spare: they load the factors
-  // per 32-row block in the epilogue instead, one batch of 32 loads each.
-  constexpr bool PREFETCH = EPI == EPI_QKV && TN <= 2;
-  float rcos[PREFETCH ? TM : 1][16], rsin[PREFETCH ? TM : 1][16];
-  if constexpr (PREFETCH) {
-    if (n0 + cw < g.rope_cols) {
-#pragma unroll
-      for (int i = 0; i < TM; i++)
-#pragma unroll
-        for (int e = 0; e < 16; e++) {
-          const size_t tr = (size_t)min(m0 + rw + i * 32 + mfma_row(e, lane), g.M - 1);
-          rcos[i][e] = g.cos_t[tr * 32 + lr];
-          rsin[i][e] = g.sin_t[tr * 32 + lr];
-        }
-    }
-  }
-
   const int nk = g.K / KT;
 #pragma unroll
   for (int s = 0; s < NSTAGE - 1; s++)
@@ -174,11 +155,9 @@ __global__ __launch_bounds__(NTHREADS) void gemm_nt_kernel(GemmArgs g) {
       fb[buf][j] = *(const frag *)(sb + r * 128 + ((chunk ^ swz(r)) << 4) + within);
     }
   };
-  // Waits until stage kt has landed for every wave. The RoPE prefetch shares
-  // the vector-memory counter with the LDS DMA and the two kinds may complete
-  // out of order, so the first stage waits for everything.
+  // Waits until stage kt has landed for every wave.
   auto stage_ready = [&](int kt) {
-    if (kt + NSTAGE - 2 < nk && !(PREFETCH && kt == 0))
+    if (kt + NSTAGE - 2 < nk)
       wait_vmcnt<LOADS * (NSTAGE - 2)>();
     else
       wait_vmcnt<0>();
@@ -269,48 +248,21 @@ __global__ __launch_bounds__(NTHREADS) void gemm_nt_kernel(GemmArgs g) {
     constexpr int OC = EPI == EPI_GEGLU ? BN / 2 : BN;  // output columns of the block tile
     constexpr int LD = OC + 8;                          // staged row length (elements)
     T *st = (T *)smem;
-    const bool rot = EPI == EPI_QKV && n0 + cw < g.rope_cols;  // whole wave tile is q/k or v
 #pragma unroll
-    for (int i = 0; i < TM; i++) {
-      float cs[16], sn[16];
-      if constexpr (EPI == EPI_QKV) {
-        if constexpr (PREFETCH) {
+    for (int i = 0; i < TM; i++)
 #pragma unroll
-          for (int e = 0; e < 16; e++) {
-            cs[e] = rcos[i][e];
-            sn[e] = rsin[i][e];
-          }
-        } else if (rot) {
-#pragma unroll
-          for (int e = 0; e < 16; e++) {
-            const size_t tr = (size_t)min(m0 + rw + i * 32 + mfma_row(e, lane), g.M - 1);
-            cs[e] = g.cos_t[tr * 32 + lr];
-            sn[e] = g.sin_t[tr * 32 + lr];
-          }
-        }
-      }
-#pragma unroll
-      for (int jp = 0; jp < TN / 2; jp++) {
+      for (int jp = 0; jp < TN / 2; jp++)
 #pragma unroll
         for (int e = 0; e < 16; e++) {
           const int r = rw + i * 32 + mfma_row(e, lane);
           const float a = acc[i][2 * jp][e], b = acc[i][2 * jp + 1][e];
-          if constexpr (EPI == EPI_QKV) {
-            float x = a, y = b;
-            if (rot) {
-              // Unfused, as the reference's applyRope (ops.go:169-170).
-#pragma clang fp contract(off)
-              x = a * cs[e] - b * sn[e];
-              y = b * cs[e] + a * sn[e];
-            }
-            st[r * LD + cw + jp * 64 + lr] = to_elem<T>(x);
-            st[r * LD + cw + jp * 64 + 32 + lr] = to_elem<T>(y);
+          if constexpr (EPI == EPI_STORE) {
+            st[r * LD + cw + jp * 64 + lr] = to_elem<T>(a);
+            st[r * LD + cw + jp * 64 + 32 + lr] = to_elem<T>(b);
           } else {
             st[r * LD + (cw + jp * 64) / 2 + lr] = to_elem<T>(gelu_erf<T>(a) * b);
           }
         }
-      }
-    }
     __syncthreads();
     T *C = (T *)g.C;
     const int oc0 = EPI == EPI_GEGLU ? n0 / 2 : n0;
@@ -343,8 +295,8 @@ hipError_t launch_cfg(int epi, const GemmArgs &a, hipStream_t s) {
       else
         return hipErrorInvalidValue;
       break;
-    case EPI_QKV:
-      hipLaunchKernelGGL((gemm_nt_kernel<T, BM, BN, NSTAGE, EPI_QKV>), grid, block, 0, s, a);
+    case EPI_STORE:
+      hipLaunchKernelGGL((gemm_nt_kernel<T, BM, BN, NSTAGE, EPI_STORE>), grid, block, 0, s, a);
       break;
     default:
       hipLaunchKernelGGL((gemm_nt_kernel<T, BM, BN, NSTAGE, EPI_GEGLU>), grid, block, 0, s, a);

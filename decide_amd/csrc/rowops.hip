@@ -140,110 +140,90 @@ __global__ void rope_tables_kernel(const int *pos, int Tn, const double *inv_g, 
   sl[idx] = (float)sin(fl);
 }
 
-// Scoring head (HeadForward, forward.go:250-282) for RB rows per workgroup:
-// gather the [MASK] rows of the encoder output, final_norm, input_norm (+bias,
-// eps 1e-5), dense H -> H/2 (+bias), gelu, norm (+bias, eps 1e-5), dot with
-// out_proj (+bias). fp32 throughout; the dense weight is streamed once per
-// workgroup with coalesced loads and reused for all RB rows.
-constexpr int RB = 8;
-constexpr int HMAX = 1024;
-
-__global__ __launch_bounds__(256) void head_kernel(HeadArgs a) {
-  __shared__ float s1[RB][HMAX];
-  __shared__ float ge[RB][HMAX / 2];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int r0 = blockIdx.x * RB;
-  const int dim = a.H, half = a.H / 2, nvec = dim / 4;
-
-  // 1. rows -> final_norm -> input_norm (+bias) into s1.
-  for (int rr = wave; rr < RB; rr += 4) {
-    const int r = r0 + rr;
-    if (r >= a.R) break;
-    int t = a.row_tok[r];
-    if (t < 0 || t >= a.T) {
-      if (lane == 0) atomicOr(a.err_flag, 2);
-      t = 0;
-    }
-    const float4 *src = (const float4 *)(a.h + (size_t)t * dim);
-    float4 x[MAXV];
-#pragma unroll
-    for (int j = 0; j < MAXV; j++)
-      if (lane + 64 * j < nvec) x[j] = src[lane + 64 * j];
-    float mean, rs;
-    row_stats(x, nvec, lane, dim, a.eps, mean, rs);
-    const float4 *fw = (const float4 *)a.final_norm;
-#pragma unroll
-    for (int j = 0; j < MAXV; j++)
-      if (lane + 64 * j < nvec) {
-        const float4 ww = fw[lane + 64 * j];
-        x[j].x = (x[j].x - mean) * rs * ww.x;
-        x[j].y = (x[j].y - mean) * rs * ww.y;
-        x[j].z = (x[j].z - mean) * rs * ww.z;
-        x[j].w = (x[j].w - mean) * rs * ww.w;
-      }
-    row_stats(x, nvec, lane, dim, 1e-5f, mean, rs);
-    const float4 *iw = (const float4 *)a.in_w, *ib = (const float4 *)a.in_b;
-#pragma unroll
-    for (int j = 0; j < MAXV; j++)
-      if (lane + 64 * j < nvec) {
-        const float4 ww = iw[lane + 64 * j], bb = ib[lane + 64 * j];
-        float4 y;
-        y.x = (x[j].x - mean) * rs * ww.x + bb.x;
-        y.y = (x[j].y - mean) * rs * ww.y + bb.y;
-        y.z = (x[j].z - mean) * rs * ww.z + bb.z;
-        y.w = (x[j].w - mean) * rs * ww.w + bb.w;
-        *(float4 *)&s1[rr][4 * (lane + 64 * j)] = y;
-      }
+// Scoring head (HeadForward, forward.go:250-282), in three launches:
+//   head_pre  : gather the [MASK] rows of the encoder output, final_norm, then
+//               input_norm (+bias, eps 1e-5) -> s1 [R x H]            (one wave per row)
+//   GEMM      : d = s1 . dense^T [R x H/2] on fp32 MFMA (the reference's linearFwd)
+//   head_post : +bias, gelu, norm (+bias, eps 1e-5), dot with out_proj, +bias
+//                                                                     (one wave per row)
+__global__ __launch_bounds__(256) void head_pre_kernel(HeadArgs a, float *s1) {
+  const int lane = threadIdx.x & 63;
+  const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= a.R) return;
+  const int dim = a.H, nvec = dim / 4;
+  int t = a.row_tok[r];
+  if (t < 0 || t >= a.T) {
+    if (lane == 0) atomicOr(a.err_flag, 2);
+    t = 0;
   }
-  __syncthreads();
+  const float4 *src = (const float4 *)(a.h + (size_t)t * dim);
+  float4 x[MAXV];
+#pragma unroll
+  for (int j = 0; j < MAXV; j++)
+    if (lane + 64 * j < nvec) x[j] = src[lane + 64 * j];
+  float mean, rs;
+  row_stats(x, nvec, lane, dim, a.eps, mean, rs);
+  const float4 *fw = (const float4 *)a.final_norm;
+#pragma unroll
+  for (int j = 0; j < MAXV; j++)
+    if (lane + 64 * j < nvec) {
+      const float4 ww = fw[lane + 64 * j];
+      x[j].x = (x[j].x - mean) * rs * ww.x;
+      x[j].y = (x[j].y - mean) * rs * ww.y;
+      x[j].z = (x[j].z - mean) * rs * ww.z;
+      x[j].w = (x[j].w - mean) * rs * ww.w;
+    }
+  row_stats(x, nvec, lane, dim, 1e-5f, mean, rs);
+  const float4 *iw = (const float4 *)a.in_w, *ib = (const float4 *)a.in_b;
+#pragma unroll
+  for (int j = 0; j < MAXV; j++)
+    if (lane + 64 * j < nvec) {
+      const float4 ww = iw[lane + 64 * j], bb = ib[lane + 64 * j];
+      float4 y;
+      y.x = (x[j].x - mean) * rs * ww.x + bb.x;
+      y.y = (x[j].y - mean) * rs * ww.y + bb.y;
+      y.z = (x[j].z - mean) * rs * ww.z + bb.z;
+      y.w = (x[j].w - mean) * rs * ww.w + bb.w;
+      ((float4 *)(s1 + (size_t)r * dim))[lane + 64 * j] = y;
+    }
+}
 
-  // 2. dense + bias + gelu: wave w computes outputs o = w, w+4, ...
-  for (int o = wave; o < half; o += 4) {
-    const float4 *wr = (const float4 *)(a.dense_w + (size_t)o * dim);
-    float acc[RB];
+__global__ __launch_bounds__(256) void head_post_kernel(HeadArgs a, const float *d) {
+  const int lane = threadIdx.x & 63;
+  const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= a.R) return;
+  const int half = a.H / 2;
+  constexpr int MAXE = 8;  // half <= 512
+  float g[MAXE];
+  double s = 0;
 #pragma unroll
-    for (int rr = 0; rr < RB; rr++) acc[rr] = 0.0f;
-#pragma unroll
-    for (int j = 0; j < MAXV; j++)
-      if (lane + 64 * j < nvec) {
-        const float4 ww = wr[lane + 64 * j];
-#pragma unroll
-        for (int rr = 0; rr < RB; rr++) {
-          const float4 xv = *(const float4 *)&s1[rr][4 * (lane + 64 * j)];
-          acc[rr] += xv.x * ww.x + xv.y * ww.y + xv.z * ww.z + xv.w * ww.w;
-        }
-      }
-#pragma unroll
-    for (int rr = 0; rr < RB; rr++) {
-      const float v = wave_sumf(acc[rr]);
-      if (lane == 0) ge[rr][o] = gelu_erf<float>(v + a.dense_b[o]);
+  for (int j = 0; j < MAXE; j++) {
+    const int i = lane + 64 * j;
+    g[j] = 0.0f;
+    if (i < half) {
+      g[j] = gelu_erf<float>(d[(size_t)r * half + i] + a.dense_b[i]);
+      s += (double)g[j];
     }
   }
-  __syncthreads();
-
-  // 3. norm (+bias) over H/2 and the output projection: one wave per row.
-  for (int rr = wave; rr < RB; rr += 4) {
-    const int r = r0 + rr;
-    if (r >= a.R) break;
-    double s = 0;
-    for (int i = lane; i < half; i += 64) s += (double)ge[rr][i];
-    const double mu = wave_sum(s) / (double)half;
-    double v = 0;
-    for (int i = lane; i < half; i += 64) {
-      const double d = (double)ge[rr][i] - mu;
-      v += d * d;
+  const double mu = wave_sum(s) / (double)half;
+  double v = 0;
+#pragma unroll
+  for (int j = 0; j < MAXE; j++)
+    if (lane + 64 * j < half) {
+      const double dd = (double)g[j] - mu;
+      v += dd * dd;
     }
-    const double var = wave_sum(v) / (double)half;
-    const float rs = (float)(1.0 / sqrt(var + 1e-5));
-    const float m = (float)mu;
-    float dot = 0.0f;
-    for (int i = lane; i < half; i += 64) {
-      const float y = (ge[rr][i] - m) * rs * a.norm_w[i] + a.norm_b[i];
-      dot += y * a.out_w[i];
-    }
-    dot = wave_sumf(dot);
-    if (lane == 0) a.logits[r] = dot + a.out_b[0];
+  const double var = wave_sum(v) / (double)half;
+  const float rs = (float)(1.0 / sqrt(var + 1e-5));
+  const float m = (float)mu;
+  float dot = 0.0f;
+#pragma unroll
+  for (int j = 0; j < MAXE; j++) {
+    const int i = lane + 64 * j;
+    if (i < half) dot += ((g[j] - m) * rs * a.norm_w[i] + a.norm_b[i]) * a.out_w[i];
   }
+  dot = wave_sumf(dot);
+  if (lane == 0) a.logits[r] = dot + a.out_b[0];
 }
 
 // dst[dst_rows x dst_cols] (row-major, zero padded) = op(src) where op(src)
@@ -293,9 +273,27 @@ hipError_t launch_rope_tables(const int *pos, int Tn, const double *inv_g, const
   return hipGetLastError();
 }
 
-hipError_t launch_head(const HeadArgs &a, hipStream_t s) {
+hipError_t launch_head(const HeadArgs &a, float *s1, float *d, hipStream_t s) {
   if (a.R <= 0) return hipSuccess;
-  hipLaunchKernelGGL(head_kernel, dim3((a.R + RB - 1) / RB), dim3(256), 0, s, a);
+  if (a.H > 1024 || a.H % 256 != 0) return hipErrorInvalidValue;
+  const dim3 grid((a.R + 3) / 4), block(256);
+  hipLaunchKernelGGL(head_pre_kernel, grid, block, 0, s, a, s1);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  GemmArgs g{};
+  g.A = s1;
+  g.lda = a.H;
+  g.B = a.dense_w;
+  g.ldb = a.H;
+  g.C = d;
+  g.ldc = a.H / 2;
+  g.M = a.R;
+  g.N = a.H / 2;
+  g.K = a.H;
+  g.n_store = a.H / 2;
+  e = launch_gemm(0, EPI_F32, g, s);
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(head_post_kernel, grid, block, 0, s, a, d);
   return hipGetLastError();
 }
 

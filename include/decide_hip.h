@@ -76,7 +76,7 @@ int dn_set_stream(dn_ctx *ctx, void *stream);
  * residual stream, statistics and head; DN_PRECISION_FP32 = fp32 MFMA
  * everywhere (the validation build). Must precede dn_upload_tensor.
  * Replaces the config capture of gpunn.New (internal/gpunn/model.go:80-122).
- * This build implements head_dim 64 with hidden % 128 == 0 and
+ * This build implements head_dim 64 with hidden % 256 == 0 (<= 1024) and
  * inter % 64 == 0 (ModernBERT-base: 768/1152/12 heads); others give
  * DN_UNSUPPORTED. */
 int dn_set_config(dn_ctx *ctx, int hidden, int inter, int heads, int layers, int vocab, float eps,

@@ -49,7 +49,7 @@ def compare(got, want, batch, prec, bf16_dp=2e-3):
 def small_cfg():
     from decide_amd.nn import Config
 
-    return Config(hidden=128, intermediate=192, heads=2, layers=4, vocab=300, half_window=4,
+    return Config(hidden=256, intermediate=384, heads=4, layers=4, vocab=300, half_window=4,
                   layer_types=["full_attention", "sliding_attention", "sliding_attention", "full_attention"])
 
 
@@ -79,7 +79,7 @@ def small():
     from decide_amd.synth import random_weights
 
     cfg = small_cfg()
-    w = random_weights(cfg, seed=5, std=0.1)
+    w = random_weights(cfg, seed=5, std=0.05)
     return cfg, w, oracle.OracleModel(cfg, w)
 
 
@@ -97,8 +97,8 @@ def test_small_geometry_ragged(small, prec):
         pytest.skip("no GPU")
     with eng:
         got = eng.forward(batch)
-        # This geometry uses std 0.1 weights (logits spread ~2 units, 5x the
-        # N(0,0.02) base configs), which amplifies bf16 operand rounding; its
+        # This geometry uses std 0.05 weights (logits spread several times the
+        # N(0,0.02) base configs'), which amplifies bf16 operand rounding; its
         # bf16 bar is 1e-2. The fp32 run holds the 1e-5 bar on the same batch.
         compare(got, want, batch, prec, bf16_dp=1e-2)
         # one sequence at a time gives the same logits as the batch

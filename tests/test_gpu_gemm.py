@@ -17,7 +17,7 @@ def eng():
     from decide_amd import Engine, NoGPUError
     from decide_amd.nn import Config
 
-    cfg = Config(hidden=128, intermediate=192, heads=2, layers=1, vocab=8, layer_types=["full_attention"])
+    cfg = Config(hidden=256, intermediate=384, heads=4, layers=1, vocab=8, layer_types=["full_attention"])
     try:
         e = Engine(cfg, None, precision="fp32")
     except NoGPUError:
