@@ -80,56 +80,69 @@ __device__ __forceinline__ void stage_load(Staging<T> &st, const T *qkv, int ld,
                                            int k0, const float *cos_t, const float *sin_t, const int *kinfo,
                                            int tid) {
   const uint4 z = {0, 0, 0, 0};
-  const float4 one = {1.f, 1.f, 1.f, 1.f}, zero = {0.f, 0.f, 0.f, 0.f};
+  // Keys past the sequence end read the last key's row (in bounds) and are
+  // zeroed; their RoPE factors are whatever that row has (results unused).
   if constexpr (sizeof(T) == 2) {
     {  // K: key = tid / 4, chunk c = tid % 4 (elements 8c..8c+7 and 32+8c..)
       const int key = tid >> 2, c = tid & 3;
       const bool ok = k0 + key < n;
-      const size_t tok = (size_t)(base + k0 + key);
+      const size_t tok = (size_t)(base + min(k0 + key, n - 1));
       const T *row = qkv + tok * ld + H + head * D;
-      st.k_lo = ok ? *(const uint4 *)(row + 8 * c) : z;
-      st.k_hi = ok ? *(const uint4 *)(row + 32 + 8 * c) : z;
-      st.c_lo = ok ? *(const float4 *)(cos_t + tok * 32 + 8 * c) : one;
-      st.c_hi = ok ? *(const float4 *)(cos_t + tok * 32 + 8 * c + 4) : one;
-      st.s_lo = ok ? *(const float4 *)(sin_t + tok * 32 + 8 * c) : zero;
-      st.s_hi = ok ? *(const float4 *)(sin_t + tok * 32 + 8 * c + 4) : zero;
+      const uint4 lo = *(const uint4 *)(row + 8 * c), hi = *(const uint4 *)(row + 32 + 8 * c);
+      st.k_lo = ok ? lo : z;
+      st.k_hi = ok ? hi : z;
+      st.c_lo = *(const float4 *)(cos_t + tok * 32 + 8 * c);
+      st.c_hi = *(const float4 *)(cos_t + tok * 32 + 8 * c + 4);
+      st.s_lo = *(const float4 *)(sin_t + tok * 32 + 8 * c);
+      st.s_hi = *(const float4 *)(sin_t + tok * 32 + 8 * c + 4);
     }
     {  // V: key pair p = tid % 32, d group g = tid / 32
       const int p = tid & 31, g = tid >> 5;
       const int k = k0 + 2 * p;
-      st.v0 = k < n ? *(const uint4 *)(qkv + (size_t)(base + k) * ld + 2 * H + head * D + 8 * g) : z;
-      st.v1 = k + 1 < n ? *(const uint4 *)(qkv + (size_t)(base + k + 1) * ld + 2 * H + head * D + 8 * g) : z;
+      const uint4 a = *(const uint4 *)(qkv + (size_t)(base + min(k, n - 1)) * ld + 2 * H + head * D + 8 * g);
+      const uint4 b = *(const uint4 *)(qkv + (size_t)(base + min(k + 1, n - 1)) * ld + 2 * H + head * D + 8 * g);
+      st.v0 = k < n ? a : z;
+      st.v1 = k + 1 < n ? b : z;
     }
   } else {
 #pragma unroll
     for (int j = 0; j < 2; j++) {  // K: (key, chunk c in 0..7) = item tid + 256 j
       const int it = tid + 256 * j, key = it >> 3, c = it & 7;
       const bool ok = k0 + key < n;
-      const size_t tok = (size_t)(base + k0 + key);
+      const size_t tok = (size_t)(base + min(k0 + key, n - 1));
       const T *row = qkv + tok * ld + H + head * D;
-      st.k_lo[j] = ok ? *(const uint4 *)(row + 4 * c) : z;
-      st.k_hi[j] = ok ? *(const uint4 *)(row + 32 + 4 * c) : z;
-      st.c[j] = ok ? *(const float4 *)(cos_t + tok * 32 + 4 * c) : one;
-      st.s[j] = ok ? *(const float4 *)(sin_t + tok * 32 + 4 * c) : zero;
+      const uint4 lo = *(const uint4 *)(row + 4 * c), hi = *(const uint4 *)(row + 32 + 4 * c);
+      st.k_lo[j] = ok ? lo : z;
+      st.k_hi[j] = ok ? hi : z;
+      st.c[j] = *(const float4 *)(cos_t + tok * 32 + 4 * c);
+      st.s[j] = *(const float4 *)(sin_t + tok * 32 + 4 * c);
     }
 #pragma unroll
     for (int j = 0; j < 4; j++) {  // V: key = tid % 64, d group g = tid / 64 + 4 j
       const int key = tid & 63, g = (tid >> 6) + 4 * j;
-      st.v[j] = k0 + key < n ? *(const uint4 *)(qkv + (size_t)(base + k0 + key) * ld + 2 * H + head * D + 4 * g) : z;
+      const uint4 v = *(const uint4 *)(qkv + (size_t)(base + min(k0 + key, n - 1)) * ld + 2 * H + head * D + 4 * g);
+      st.v[j] = k0 + key < n ? v : z;
     }
   }
   st.info = (tid < KTILE && k0 + tid < n) ? kinfo[base + k0 + tid] : 0;
 }
 
-// RoPE on one chunk pair, unfused like applyRope (ops.go:169-170).
-__device__ __forceinline__ void rope4(float *lo, float *hi, const float *c, const float *s) {
+__device__ __forceinline__ float bf_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+// RoPE of one (a, b) pair, unfused like applyRope (ops.go:169-170).
+__device__ __forceinline__ void rope1(float &a, float &b, float c, float s) {
 #pragma clang fp contract(off)
-#pragma unroll
-  for (int e = 0; e < 4; e++) {
-    const float a = lo[e], b = hi[e];
-    lo[e] = a * c[e] - b * s[e];
-    hi[e] = b * c[e] + a * s[e];
-  }
+  const float x = a * c - b * s;
+  const float y = b * c + a * s;
+  a = x;
+  b = y;
+}
+
+// Round-to-nearest-even fp32 -> bf16 pair packed in one word (lo in bits 0..15).
+__device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
+  bf16x2_t v = {(bf16)lo, (bf16)hi};
+  return __builtin_bit_cast(uint32_t, v);
 }
 
 template <class T>
@@ -137,42 +150,52 @@ __device__ __forceinline__ void stage_store(const Staging<T> &st, char *sK, char
                                             int ROWV) {
   if constexpr (sizeof(T) == 2) {
     const int key = tid >> 2, c = tid & 3;
-    const bf16 *lo = (const bf16 *)&st.k_lo, *hi = (const bf16 *)&st.k_hi;
-    float flo[8], fhi[8];
+    const uint32_t klo[4] = {st.k_lo.x, st.k_lo.y, st.k_lo.z, st.k_lo.w};
+    const uint32_t khi[4] = {st.k_hi.x, st.k_hi.y, st.k_hi.z, st.k_hi.w};
+    const float cs[8] = {st.c_lo.x, st.c_lo.y, st.c_lo.z, st.c_lo.w, st.c_hi.x, st.c_hi.y, st.c_hi.z, st.c_hi.w};
+    const float sn[8] = {st.s_lo.x, st.s_lo.y, st.s_lo.z, st.s_lo.w, st.s_hi.x, st.s_hi.y, st.s_hi.z, st.s_hi.w};
+    uint4 olo, ohi;
+    uint32_t *po = (uint32_t *)&olo, *ph = (uint32_t *)&ohi;
 #pragma unroll
-    for (int e = 0; e < 8; e++) {
-      flo[e] = (float)lo[e];
-      fhi[e] = (float)hi[e];
+    for (int w = 0; w < 4; w++) {
+      float a0 = bf_lo(klo[w]), a1 = bf_hi(klo[w]), b0 = bf_lo(khi[w]), b1 = bf_hi(khi[w]);
+      rope1(a0, b0, cs[2 * w], sn[2 * w]);
+      rope1(a1, b1, cs[2 * w + 1], sn[2 * w + 1]);
+      po[w] = pack_bf16(a0, a1);
+      ph[w] = pack_bf16(b0, b1);
     }
-    rope4(flo, fhi, (const float *)&st.c_lo, (const float *)&st.s_lo);
-    rope4(flo + 4, fhi + 4, (const float *)&st.c_hi, (const float *)&st.s_hi);
-    bf16x8 olo, ohi;
-#pragma unroll
-    for (int e = 0; e < 8; e++) {
-      olo[e] = (bf16)flo[e];
-      ohi[e] = (bf16)fhi[e];
-    }
-    *(bf16x8 *)(sK + key * ROWK + 16 * c) = olo;
-    *(bf16x8 *)(sK + key * ROWK + 64 + 16 * c) = ohi;
+    *(uint4 *)(sK + key * ROWK + 16 * c) = olo;
+    *(uint4 *)(sK + key * ROWK + 64 + 16 * c) = ohi;
+    // V^T: word e of row (8g + e) holds (key 2p, key 2p+1) for d = 8g + e.
     const int p = tid & 31, g = tid >> 5;
-    const uint16_t *a = (const uint16_t *)&st.v0, *b = (const uint16_t *)&st.v1;
+    const uint32_t va[4] = {st.v0.x, st.v0.y, st.v0.z, st.v0.w};
+    const uint32_t vb[4] = {st.v1.x, st.v1.y, st.v1.z, st.v1.w};
 #pragma unroll
-    for (int e = 0; e < 8; e++) *(uint32_t *)(sV + (8 * g + e) * ROWV + 4 * p) = (uint32_t)a[e] | ((uint32_t)b[e] << 16);
+    for (int w = 0; w < 4; w++) {
+      *(uint32_t *)(sV + (8 * g + 2 * w) * ROWV + 4 * p) = (va[w] & 0xffffu) | (vb[w] << 16);
+      *(uint32_t *)(sV + (8 * g + 2 * w + 1) * ROWV + 4 * p) = (va[w] >> 16) | (vb[w] & 0xffff0000u);
+    }
   } else {
 #pragma unroll
     for (int j = 0; j < 2; j++) {
       const int it = tid + 256 * j, key = it >> 3, c = it & 7;
       float4 lo = *(const float4 *)&st.k_lo[j], hi = *(const float4 *)&st.k_hi[j];
-      rope4((float *)&lo, (float *)&hi, (const float *)&st.c[j], (const float *)&st.s[j]);
+      const float4 cs = st.c[j], sn = st.s[j];
+      rope1(lo.x, hi.x, cs.x, sn.x);
+      rope1(lo.y, hi.y, cs.y, sn.y);
+      rope1(lo.z, hi.z, cs.z, sn.z);
+      rope1(lo.w, hi.w, cs.w, sn.w);
       *(float4 *)(sK + key * ROWK + 16 * c) = lo;
       *(float4 *)(sK + key * ROWK + 128 + 16 * c) = hi;
     }
 #pragma unroll
     for (int j = 0; j < 4; j++) {
       const int key = tid & 63, g = (tid >> 6) + 4 * j;
-      const float *v = (const float *)&st.v[j];
-#pragma unroll
-      for (int e = 0; e < 4; e++) *(float *)(sV + (4 * g + e) * ROWV + 4 * key) = v[e];
+      const uint4 v = st.v[j];
+      *(uint32_t *)(sV + (4 * g + 0) * ROWV + 4 * key) = v.x;
+      *(uint32_t *)(sV + (4 * g + 1) * ROWV + 4 * key) = v.y;
+      *(uint32_t *)(sV + (4 * g + 2) * ROWV + 4 * key) = v.z;
+      *(uint32_t *)(sV + (4 * g + 3) * ROWV + 4 * key) = v.w;
     }
   }
   if (tid < KTILE) sInfo[tid] = st.info;
@@ -341,13 +364,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_PER_E
       mx = fmaxf(mx, __shfl_xor(mx, 32));
       const float m_new = fmaxf(m_run, mx);
       const float m_use = m_new == -INFINITY ? 0.0f : m_new;
-      const float alpha = exp2f(m_run - m_use);
+      const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
       float psum = 0.0f;
 #pragma unroll
       for (int i = 0; i < 2; i++)
 #pragma unroll
         for (int e = 0; e < 16; e++) {
-          const float p = exp2f(sT[i][e] - m_use);
+          const float p = __builtin_amdgcn_exp2f(sT[i][e] - m_use);
           sT[i][e] = p;
           psum += p;
         }

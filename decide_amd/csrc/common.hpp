@@ -7,6 +7,7 @@
 typedef __bf16 bf16;
 typedef bf16 bf16x8 __attribute__((__vector_size__(8 * sizeof(bf16))));
 typedef bf16 bf16x4 __attribute__((__vector_size__(4 * sizeof(bf16))));
+typedef bf16 bf16x2_t __attribute__((__vector_size__(2 * sizeof(bf16))));
 typedef float f32x16 __attribute__((__vector_size__(16 * sizeof(float))));
 typedef float f32x4 __attribute__((__vector_size__(4 * sizeof(float))));
 
