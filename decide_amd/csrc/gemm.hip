@@ -27,15 +27,19 @@
 //     slice of B stays in that XCD's 4 MB L2 while its A panels stream.
 //   * The epilogue stages the finished tile through LDS so global stores are
 //     full 16-byte-per-lane rows.
-#include <cstdlib>
-
 #include "common.hpp"
 
 namespace {
 
 constexpr int NTHREADS = 256;  // 4 waves, 2 x 2 over the output tile
 
-__device__ __forceinline__ int swz(int row) { return (row >> 1) & 7; }
+// XOR swizzle of the 16-byte chunks of an LDS tile row: with RB-byte rows,
+// the 16 rows read by a quarter-wave at one logical chunk land in 16
+// distinct 4-bank groups.
+template <int RB>
+__device__ __forceinline__ int swz(int row) {
+  return RB == 128 ? (row >> 1) & 7 : (row >> 2) & 3;
+}
 
 typedef __attribute__((address_space(3))) void lds_void;
 typedef const __attribute__((address_space(1))) void gbl_void;
@@ -69,19 +73,22 @@ struct TileOrder {
   }
 };
 
-template <class T, int BM, int BN, int NSTAGE, int EPI>
-__global__ __launch_bounds__(NTHREADS) void gemm_nt_kernel(GemmArgs g) {
+template <class T, int BM, int BN, int RB, int NSTAGE, int EPI, int WPE>
+__global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(WPE))) void gemm_nt_kernel(GemmArgs g) {
   using MF = Mfma<T>;
   typedef typename MF::frag frag;
-  constexpr int KT = 128 / sizeof(T);  // K elements per stage (128-byte rows)
+  constexpr int KT = RB / sizeof(T);   // K elements per stage (RB-byte rows)
+  constexpr int CPR = RB / 16;         // 16-byte chunks per row
+  constexpr int RPI = 1024 / RB;       // rows per wave-wide DMA instruction
   constexpr int WM = BM / 2, WN = BN / 2;
   constexpr int TM = WM / 32, TN = WN / 32;
-  constexpr int STAGE = (BM + BN) * 128;
-  constexpr int LOADS = (BM + BN) * 8 / NTHREADS;  // 16-byte DMA loads per thread per stage
-  static_assert(LOADS * NTHREADS == (BM + BN) * 8, "tile rows must be a multiple of 32");
+  constexpr int STAGE = (BM + BN) * RB;
+  constexpr int LOADS = (BM + BN) * CPR / NTHREADS;  // 16-byte DMA loads per thread per stage
+  static_assert(LOADS * NTHREADS == (BM + BN) * CPR, "tile rows must fill whole DMA instructions");
   static_assert(EPI == EPI_F32 || TN % 2 == 0, "paired epilogues need 64-column wave tiles");
   static_assert(NSTAGE >= 2 && LOADS * (NSTAGE - 2) < 64, "pipeline depth");
-  constexpr int EPI_BYTES = (EPI == EPI_F32) ? BM * (BN + 4) * 4
+  // fp32 epilogue staged in two halves of BM/2 rows; the others in one pass.
+  constexpr int EPI_BYTES = (EPI == EPI_F32) ? (BM / 2) * (BN + 4) * 4
                                              : BM * ((EPI == EPI_GEGLU ? BN / 2 : BN) + 8) * (int)sizeof(T);
   constexpr int SMEM = NSTAGE * STAGE > EPI_BYTES ? NSTAGE * STAGE : EPI_BYTES;
   __shared__ __attribute__((aligned(1024))) char smem[SMEM];
@@ -93,14 +100,14 @@ __global__ __launch_bounds__(NTHREADS) void gemm_nt_kernel(GemmArgs g) {
   const TileOrder<BM, BN> to(blockIdx.x, (g.M + BM - 1) / BM, g.N / BN, g.ngroups, g.order);
   const int m0 = to.m0, n0 = to.n0;
 
-  // DMA sources: load i of this wave fills tile rows 8*(wave + 4i) .. +7;
-  // lane l writes row 8*(wave+4i) + l/8, LDS chunk slot l%8, which holds the
-  // row's logical 16-byte chunk (l%8) ^ swz(row).
+  // DMA sources: load i of this wave fills tile rows RPI*(wave + 4i) .. +RPI-1;
+  // lane l writes row RPI*(wave+4i) + l/CPR, LDS chunk slot l%CPR, which holds
+  // the row's logical 16-byte chunk (l%CPR) ^ swz(row).
   const char *src[LOADS];
 #pragma unroll
   for (int i = 0; i < LOADS; i++) {
-    const int r = 8 * (wave + 4 * i) + (lane >> 3);
-    const int c = (lane & 7) ^ swz(r);
+    const int r = RPI * (wave + 4 * i) + lane / CPR;
+    const int c = (lane % CPR) ^ swz<RB>(r);
     if (r < BM)
       src[i] = (const char *)g.A + (size_t)min(m0 + r, g.M - 1) * g.lda * sizeof(T) + c * 16;
     else
@@ -141,18 +148,18 @@ __global__ __launch_bounds__(NTHREADS) void gemm_nt_kernel(GemmArgs g) {
   frag fa[2][TM], fb[2][TN];
   auto load_frags = [&](int buf, int stage, int ks) {
     const char *sa = smem + stage * STAGE;
-    const char *sb = sa + BM * 128;
+    const char *sb = sa + BM * RB;
     const int ke = ks * MF::KSTEP + lh * MF::SLOTS;  // first k element of this lane's operand
     const int chunk = ke * (int)sizeof(T) / 16, within = ke * (int)sizeof(T) % 16;
 #pragma unroll
     for (int i = 0; i < TM; i++) {
       const int r = wm * WM + i * 32 + lr;
-      fa[buf][i] = *(const frag *)(sa + r * 128 + ((chunk ^ swz(r)) << 4) + within);
+      fa[buf][i] = *(const frag *)(sa + r * RB + ((chunk ^ swz<RB>(r)) << 4) + within);
     }
 #pragma unroll
     for (int j = 0; j < TN; j++) {
       const int r = wn * WN + j * 32 + lr;
-      fb[buf][j] = *(const frag *)(sb + r * 128 + ((chunk ^ swz(r)) << 4) + within);
+      fb[buf][j] = *(const frag *)(sb + r * RB + ((chunk ^ swz<RB>(r)) << 4) + within);
     }
   };
   // Waits until stage kt has landed for every wave.
@@ -203,46 +210,53 @@ __global__ __launch_bounds__(NTHREADS) void gemm_nt_kernel(GemmArgs g) {
   __builtin_amdgcn_s_barrier();  // all waves done with the ring: reuse it for the epilogue
   if constexpr (EPI == EPI_F32) {
     constexpr int LD = BN + 4;  // floats per staged row
+    constexpr int HM = BM / 2;  // rows per pass: the waves with wm == pass stage theirs
     float *st = (float *)smem;
-#pragma unroll
-    for (int i = 0; i < TM; i++)
-#pragma unroll
-      for (int j = 0; j < TN; j++)
-#pragma unroll
-        for (int e = 0; e < 16; e++) st[(rw + i * 32 + mfma_row(e, lane)) * LD + cw + j * 32 + lr] = acc[i][j][e];
-    __syncthreads();
     float *C = (float *)g.C;
     constexpr int V = BN / 4;  // float4 per row
-    constexpr int ITER = BM * V / NTHREADS;
+    constexpr int ITER = HM * V / NTHREADS;
     constexpr int BATCH = ITER < 8 ? ITER : 8;
     static_assert(ITER % BATCH == 0, "epilogue batching");
     const bool vec = (g.ldc & 3) == 0;
-    // All loads of a batch are issued before its stores (C is read and
-    // written here, so the compiler would otherwise serialise each pair).
-    for (int b0 = 0; b0 < ITER; b0 += BATCH) {
-      float4 old[BATCH];
 #pragma unroll
-      for (int u = 0; u < BATCH; u++) {
-        const int c = tid + (b0 + u) * NTHREADS, r = c / V, c4 = (c % V) * 4;
-        const int row = m0 + r, col = n0 + c4;
-        old[u] = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (g.accumulate && vec && row < g.M && col + 4 <= g.n_store)
-          old[u] = *(const float4 *)(C + (size_t)row * g.ldc + col);
+    for (int pass = 0; pass < 2; pass++) {
+      if (wm == pass) {
+#pragma unroll
+        for (int i = 0; i < TM; i++)
+#pragma unroll
+          for (int j = 0; j < TN; j++)
+#pragma unroll
+            for (int e = 0; e < 16; e++) st[(i * 32 + mfma_row(e, lane)) * LD + cw + j * 32 + lr] = acc[i][j][e];
       }
+      __syncthreads();
+      // All loads of a batch are issued before its stores (C is read and
+      // written here, so the compiler would otherwise serialise each pair).
+      for (int b0 = 0; b0 < ITER; b0 += BATCH) {
+        float4 old[BATCH];
 #pragma unroll
-      for (int u = 0; u < BATCH; u++) {
-        const int c = tid + (b0 + u) * NTHREADS, r = c / V, c4 = (c % V) * 4;
-        const int row = m0 + r, col = n0 + c4;
-        if (row >= g.M || col >= g.n_store) continue;
-        const float4 v = *(const float4 *)(st + r * LD + c4);
-        float *p = C + (size_t)row * g.ldc + col;
-        if (vec && col + 4 <= g.n_store) {
-          *(float4 *)p = make_float4(v.x + old[u].x, v.y + old[u].y, v.z + old[u].z, v.w + old[u].w);
-        } else {
-          const float vv[4] = {v.x, v.y, v.z, v.w};
-          for (int q = 0; q < 4 && col + q < g.n_store; q++) p[q] = g.accumulate ? p[q] + vv[q] : vv[q];
+        for (int u = 0; u < BATCH; u++) {
+          const int c = tid + (b0 + u) * NTHREADS, r = c / V, c4 = (c % V) * 4;
+          const int row = m0 + pass * HM + r, col = n0 + c4;
+          old[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+          if (g.accumulate && vec && row < g.M && col + 4 <= g.n_store)
+            old[u] = *(const float4 *)(C + (size_t)row * g.ldc + col);
+        }
+#pragma unroll
+        for (int u = 0; u < BATCH; u++) {
+          const int c = tid + (b0 + u) * NTHREADS, r = c / V, c4 = (c % V) * 4;
+          const int row = m0 + pass * HM + r, col = n0 + c4;
+          if (row >= g.M || col >= g.n_store) continue;
+          const float4 v = *(const float4 *)(st + r * LD + c4);
+          float *p = C + (size_t)row * g.ldc + col;
+          if (vec && col + 4 <= g.n_store) {
+            *(float4 *)p = make_float4(v.x + old[u].x, v.y + old[u].y, v.z + old[u].z, v.w + old[u].w);
+          } else {
+            const float vv[4] = {v.x, v.y, v.z, v.w};
+            for (int q = 0; q < 4 && col + q < g.n_store; q++) p[q] = g.accumulate ? p[q] + vv[q] : vv[q];
+          }
         }
       }
+      if (pass == 0) __syncthreads();
     }
   } else {
     constexpr int OC = EPI == EPI_GEGLU ? BN / 2 : BN;  // output columns of the block tile
@@ -277,29 +291,19 @@ __global__ __launch_bounds__(NTHREADS) void gemm_nt_kernel(GemmArgs g) {
   }
 }
 
-// fp32 epilogue staging of a BN = 256 tile would exceed LDS; such configs are
-// only used for the bf16 paired epilogues.
-template <class T, int BM, int BN>
-constexpr bool f32_epilogue_fits() {
-  return BM * (BN + 4) * 4 <= 160 * 1024;
-}
-
-template <class T, int BM, int BN, int NSTAGE>
+template <class T, int BM, int BN, int RB, int NSTAGE, int WPE>
 hipError_t launch_cfg(int epi, const GemmArgs &a, hipStream_t s) {
   const int tiles = ((a.M + BM - 1) / BM) * (a.N / BN);
   dim3 grid(tiles), block(NTHREADS);
   switch (epi) {
     case EPI_F32:
-      if constexpr (f32_epilogue_fits<T, BM, BN>())
-        hipLaunchKernelGGL((gemm_nt_kernel<T, BM, BN, NSTAGE, EPI_F32>), grid, block, 0, s, a);
-      else
-        return hipErrorInvalidValue;
+      hipLaunchKernelGGL((gemm_nt_kernel<T, BM, BN, RB, NSTAGE, EPI_F32, WPE>), grid, block, 0, s, a);
       break;
     case EPI_STORE:
-      hipLaunchKernelGGL((gemm_nt_kernel<T, BM, BN, NSTAGE, EPI_STORE>), grid, block, 0, s, a);
+      hipLaunchKernelGGL((gemm_nt_kernel<T, BM, BN, RB, NSTAGE, EPI_STORE, WPE>), grid, block, 0, s, a);
       break;
     default:
-      hipLaunchKernelGGL((gemm_nt_kernel<T, BM, BN, NSTAGE, EPI_GEGLU>), grid, block, 0, s, a);
+      hipLaunchKernelGGL((gemm_nt_kernel<T, BM, BN, RB, NSTAGE, EPI_GEGLU, WPE>), grid, block, 0, s, a);
       break;
   }
   return hipGetLastError();
@@ -307,7 +311,7 @@ hipError_t launch_cfg(int epi, const GemmArgs &a, hipStream_t s) {
 
 }  // namespace
 
-// All tile configs use BN = 128 and stage 128 bytes of K per step.
+// All tile configs use BN = 128; K is staged 64 or 128 bytes per step.
 bool gemm_shape_ok(int precision, int N, int K) {
   const int kt = precision == 1 ? 64 : 32;
   return N > 0 && K > 0 && N % 128 == 0 && K % kt == 0;
@@ -326,22 +330,20 @@ hipError_t launch_gemm(int precision, int epi, const GemmArgs &a0, hipStream_t s
     while (tiles_n % groups) groups++;
   }
   a.ngroups = groups;
-  static const int order = getenv("DECIDE_GEMM_ORDER") ? atoi(getenv("DECIDE_GEMM_ORDER")) : 0;
-  a.order = order;
+  a.order = 0;
+  // Tile configs (measured on cfg3 shapes, 2304- and 768-wide outputs):
+  //  * M <= 1024: 64 x 128, 128-byte K stages, 4 stages, 1 workgroup per CU;
+  //  * paired / store epilogues (N = 2304): 256 x 128, 64-byte stages x 3
+  //    (72 KB LDS), two workgroups per CU so one tile's epilogue and DMA
+  //    stalls overlap the other's MFMAs;
+  //  * fp32 residual epilogue (N = 768): 128 x 128, 64-byte stages x 3
+  //    (48 KB), three workgroups per CU.
   const bool small = a.M <= 1024;
   if (precision == 1) {
-    if (small) return launch_cfg<bf16, 64, 128, 4>(epi, a, s);
-    static const int wide = getenv("DECIDE_GEMM_WIDE") ? atoi(getenv("DECIDE_GEMM_WIDE")) : 0;
-    if (wide && epi != EPI_F32 && a.N % 256 == 0) {
-      a.ngroups = 1;
-      while ((size_t)a.N / a.ngroups * a.K * 2 > (2u << 20) && a.ngroups < a.N / 256) {
-        a.ngroups++;
-        while ((a.N / 256) % a.ngroups) a.ngroups++;
-      }
-      return launch_cfg<bf16, 256, 256, 2>(epi, a, s);
-    }
-    return launch_cfg<bf16, 256, 128, 3>(epi, a, s);
+    if (small) return launch_cfg<bf16, 64, 128, 128, 4, 1>(epi, a, s);
+    if (epi == EPI_F32) return launch_cfg<bf16, 128, 128, 64, 3, 3>(epi, a, s);
+    return launch_cfg<bf16, 256, 128, 64, 3, 2>(epi, a, s);
   }
-  if (small) return launch_cfg<float, 64, 128, 4>(epi, a, s);
-  return launch_cfg<float, 256, 128, 3>(epi, a, s);
+  if (small) return launch_cfg<float, 64, 128, 128, 4, 1>(epi, a, s);
+  return launch_cfg<float, 256, 128, 128, 3, 1>(epi, a, s);
 }
