@@ -309,6 +309,228 @@ hipError_t launch_cfg(int epi, const GemmArgs &a, hipStream_t s) {
   return hipGetLastError();
 }
 
+// Small-M GEMM (M <= 128: one request, the scorer's dense layer). Such
+// launches are bound by streaming the weights and by latency, and the
+// 128-wide tiles above would give only N/128 workgroups. Here a workgroup
+// owns a TR x TC output tile (TR = 32*MB rows, TC = 32*NB columns) and all
+// of K:
+//   * K is walked in groups of GK elements (four 16-byte loads per lane and
+//     operand row); the W waves take the groups round-robin and load their
+//     MFMA operands straight from global memory into registers (every
+//     operand is used by one wave only, so LDS staging buys nothing),
+//     prefetching the next group while the current one is multiplied.
+//   * The waves' partial tiles are summed through LDS in a fixed order, so
+//     results do not depend on timing. (Splitting K across workgroups would
+//     need a device-scope release/acquire per workgroup, which on gfx950 is
+//     an L2 writeback + invalidate and costs more than it saves.)
+// Operand layout: in load j of a group, lane l reads the 16 bytes of row
+// l%32 at group offset 2*VPL*j + VPL*(l/32); for bf16 that is exactly the
+// k step j operand of v_mfma_f32_32x32x16_bf16, for fp32 the four values
+// feed four v_mfma_f32_32x32x2f32 (A and B use the same k order).
+template <class T, int MB, int NB, int EPI, int W>
+__global__ __launch_bounds__(64 * W) void gemm_skinny_kernel(GemmArgs g) {
+  using MF = Mfma<T>;
+  typedef typename MF::frag frag;
+  constexpr int NT = 64 * W;
+  constexpr int VPL = 16 / (int)sizeof(T);  // elements per 16-byte load
+  constexpr int GK = 8 * VPL;               // k elements per group
+  constexpr int TR = 32 * MB, TC = 32 * NB, TE = TR * TC;
+  static_assert(EPI != EPI_GEGLU || NB == 2, "GeGLU tiles pair 32 value and 32 gate columns");
+  static_assert(W == 4 || W == 8, "wave count");
+  __shared__ __attribute__((aligned(16))) float red[4 * TE];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, lr = lane & 31, lh = lane >> 5;
+  const int n0 = blockIdx.x * TC, m0 = blockIdx.y * TR;
+
+  const T *ap[MB], *bp[NB];
+#pragma unroll
+  for (int i = 0; i < MB; i++) ap[i] = (const T *)g.A + (size_t)min(m0 + 32 * i + lr, g.M - 1) * g.lda + lh * VPL;
+#pragma unroll
+  for (int j = 0; j < NB; j++) bp[j] = (const T *)g.B + (size_t)(n0 + 32 * j + lr) * g.ldb + lh * VPL;
+
+  f32x16 acc[MB][NB];
+#pragma unroll
+  for (int i = 0; i < MB; i++)
+#pragma unroll
+    for (int j = 0; j < NB; j++)
+#pragma unroll
+      for (int e = 0; e < 16; e++) acc[i][j][e] = 0.0f;
+
+#define SKINNY_LOAD(XA, XB, GRP)                                                                  \
+  do {                                                                                            \
+    const int k_ = (GRP) * GK;                                                                    \
+    _Pragma("unroll") for (int i = 0; i < MB; i++) _Pragma("unroll") for (int q = 0; q < 4; q++) \
+        XA[i][q] = *(const uint4 *)(ap[i] + k_ + 2 * VPL * q);                                    \
+    _Pragma("unroll") for (int j = 0; j < NB; j++) _Pragma("unroll") for (int q = 0; q < 4; q++) \
+        XB[j][q] = *(const uint4 *)(bp[j] + k_ + 2 * VPL * q);                                    \
+  } while (0)
+
+  const int ngrp = g.K / GK;
+  uint4 la[MB][4], lb[NB][4];
+  int grp = wave;
+  if (grp < ngrp) SKINNY_LOAD(la, lb, grp);
+  for (; grp < ngrp; grp += W) {
+    uint4 na[MB][4], nb[NB][4];
+    const bool more = grp + W < ngrp;
+    if (more) SKINNY_LOAD(na, nb, grp + W);
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      if constexpr (sizeof(T) == 2) {
+#pragma unroll
+        for (int i = 0; i < MB; i++)
+#pragma unroll
+          for (int j = 0; j < NB; j++)
+            acc[i][j] = MF::mma(__builtin_bit_cast(frag, la[i][q]), __builtin_bit_cast(frag, lb[j][q]), acc[i][j]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+#pragma unroll
+          for (int i = 0; i < MB; i++)
+#pragma unroll
+            for (int j = 0; j < NB; j++) {
+              const uint4 a4 = la[i][q], b4 = lb[j][q];
+              const unsigned ua = e == 0 ? a4.x : e == 1 ? a4.y : e == 2 ? a4.z : a4.w;
+              const unsigned ub = e == 0 ? b4.x : e == 1 ? b4.y : e == 2 ? b4.z : b4.w;
+              acc[i][j] = MF::mma(__builtin_bit_cast(frag, ua), __builtin_bit_cast(frag, ub), acc[i][j]);
+            }
+      }
+    }
+    if (more) {
+#pragma unroll
+      for (int i = 0; i < MB; i++)
+#pragma unroll
+        for (int q = 0; q < 4; q++) la[i][q] = na[i][q];
+#pragma unroll
+      for (int j = 0; j < NB; j++)
+#pragma unroll
+        for (int q = 0; q < 4; q++) lb[j][q] = nb[j][q];
+    }
+  }
+#undef SKINNY_LOAD
+
+  // Reduce the W partial tiles (row-major TR x TC): with 8 waves, waves 4..7
+  // hand theirs to waves 0..3 first; then the four are summed in wave order.
+  if constexpr (W == 8) {
+    if (wave >= 4) {
+      float *mine = red + (wave - 4) * TE;
+#pragma unroll
+      for (int i = 0; i < MB; i++)
+#pragma unroll
+        for (int j = 0; j < NB; j++)
+#pragma unroll
+          for (int e = 0; e < 16; e++) mine[(32 * i + mfma_row(e, lane)) * TC + 32 * j + lr] = acc[i][j][e];
+    }
+    __syncthreads();
+    if (wave < 4) {
+      const float *theirs = red + wave * TE;
+#pragma unroll
+      for (int i = 0; i < MB; i++)
+#pragma unroll
+        for (int j = 0; j < NB; j++)
+#pragma unroll
+          for (int e = 0; e < 16; e++) acc[i][j][e] += theirs[(32 * i + mfma_row(e, lane)) * TC + 32 * j + lr];
+    }
+    __syncthreads();
+  }
+  if (wave < 4) {
+    float *mine = red + wave * TE;
+#pragma unroll
+    for (int i = 0; i < MB; i++)
+#pragma unroll
+      for (int j = 0; j < NB; j++)
+#pragma unroll
+        for (int e = 0; e < 16; e++) mine[(32 * i + mfma_row(e, lane)) * TC + 32 * j + lr] = acc[i][j][e];
+  }
+  __syncthreads();
+  float4 *red4 = (float4 *)red;
+  constexpr int TE4 = TE / 4;
+  for (int q = tid; q < TE4; q += NT) {
+    float4 v = red4[q];
+#pragma unroll
+    for (int w = 1; w < 4; w++) {
+      const float4 u = red4[w * TE4 + q];
+      v.x += u.x;
+      v.y += u.y;
+      v.z += u.z;
+      v.w += u.w;
+    }
+    red4[q] = v;  // each index is read and written by one thread only
+  }
+  __syncthreads();
+
+  if constexpr (EPI == EPI_F32) {
+    float *C = (float *)g.C;
+    const bool vec = (g.ldc & 3) == 0;
+    for (int q = tid; q < TE4; q += NT) {
+      const int r = q / (TC / 4), c4 = (q % (TC / 4)) * 4, col = n0 + c4;
+      if (m0 + r >= g.M || col >= g.n_store) continue;
+      const float4 v = red4[q];
+      float *p = C + (size_t)(m0 + r) * g.ldc + col;
+      if (vec && col + 4 <= g.n_store) {
+        float4 o = g.accumulate ? *(const float4 *)p : make_float4(0.f, 0.f, 0.f, 0.f);
+        *(float4 *)p = make_float4(o.x + v.x, o.y + v.y, o.z + v.z, o.w + v.w);
+      } else {
+        const float vv[4] = {v.x, v.y, v.z, v.w};
+        for (int u = 0; u < 4 && col + u < g.n_store; u++) p[u] = g.accumulate ? p[u] + vv[u] : vv[u];
+      }
+    }
+  } else {
+    constexpr int EPV = 16 / (int)sizeof(T);            // elements per 16-byte store
+    constexpr int OC = EPI == EPI_GEGLU ? TC / 2 : TC;  // output columns of the tile
+    T *C = (T *)g.C;
+    const int oc0 = EPI == EPI_GEGLU ? n0 / 2 : n0;
+    for (int q = tid; q < TR * (OC / EPV); q += NT) {
+      const int r = q / (OC / EPV), c = (q % (OC / EPV)) * EPV;
+      if (m0 + r >= g.M) continue;
+      unsigned w[4];
+#pragma unroll
+      for (int u = 0; u < EPV; u++) {
+        float v;
+        if constexpr (EPI == EPI_STORE)
+          v = red[r * TC + c + u];
+        else
+          v = gelu_erf<T>(red[r * TC + c + u]) * red[r * TC + 32 + c + u];
+        if constexpr (sizeof(T) == 2) {
+          const unsigned b = __builtin_bit_cast(unsigned short, (bf16)v);
+          w[u / 2] = (u & 1) ? (w[u / 2] | (b << 16)) : b;
+        } else {
+          w[u] = __float_as_uint(v);
+        }
+      }
+      *(uint4 *)(C + (size_t)(m0 + r) * g.ldc + oc0 + c) = make_uint4(w[0], w[1], w[2], w[3]);
+    }
+  }
+}
+
+template <class T, int MB, int NB, int W>
+hipError_t launch_skinny_cfg(int epi, const GemmArgs &a, hipStream_t s) {
+  dim3 grid(a.N / (32 * NB), (a.M + 32 * MB - 1) / (32 * MB)), block(64 * W);
+  switch (epi) {
+    case EPI_F32:
+      hipLaunchKernelGGL((gemm_skinny_kernel<T, MB, NB, EPI_F32, W>), grid, block, 0, s, a);
+      break;
+    case EPI_STORE:
+      hipLaunchKernelGGL((gemm_skinny_kernel<T, MB, NB, EPI_STORE, W>), grid, block, 0, s, a);
+      break;
+    default:
+      if constexpr (NB == 2) hipLaunchKernelGGL((gemm_skinny_kernel<T, MB, 2, EPI_GEGLU, W>), grid, block, 0, s, a);
+      else return hipErrorInvalidValue;
+      break;
+  }
+  return hipGetLastError();
+}
+
+// 32- or 64-row tiles, 32 columns (64 for GeGLU's value/gate pairs), 8 waves.
+template <class T>
+hipError_t launch_skinny(int epi, const GemmArgs &a, hipStream_t s) {
+  if (epi == EPI_GEGLU) {
+    if (a.M <= 32) return launch_skinny_cfg<T, 1, 2, 8>(epi, a, s);
+    return launch_skinny_cfg<T, 2, 2, 8>(epi, a, s);
+  }
+  if (a.M <= 32) return launch_skinny_cfg<T, 1, 1, 8>(epi, a, s);
+  return launch_skinny_cfg<T, 2, 1, 8>(epi, a, s);
+}
+
 }  // namespace
 
 // All tile configs use BN = 128; K is staged 64 or 128 bytes per step.
@@ -319,6 +541,7 @@ bool gemm_shape_ok(int precision, int N, int K) {
 
 hipError_t launch_gemm(int precision, int epi, const GemmArgs &a0, hipStream_t s) {
   if (a0.M <= 0) return hipSuccess;
+  if (a0.M <= 128) return precision == 1 ? launch_skinny<bf16>(epi, a0, s) : launch_skinny<float>(epi, a0, s);
   GemmArgs a = a0;
   // N groups per XCD sweep: keep the group's slice of B (N/groups rows of
   // K elements) within about 2 MB of L2.

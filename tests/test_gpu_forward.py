@@ -101,12 +101,19 @@ def test_small_geometry_ragged(small, prec):
         # N(0,0.02) base configs'), which amplifies bf16 operand rounding; its
         # bf16 bar is 1e-2. The fp32 run holds the 1e-5 bar on the same batch.
         compare(got, want, batch, prec, bf16_dp=1e-2)
-        # one sequence at a time gives the same logits as the batch
+        # One sequence at a time: up to 128 tokens run the split-K small-M
+        # GEMM (another fp32 summation order than the batch's tiles). fp32
+        # still gives the batch's logits to 1e-5; bf16 rounds the activations
+        # after each GEMM, so each single-sequence run is held to the oracle
+        # bar instead.
         off = 0
         for s in batch:
             one = eng.forward([s])
             k = len(s.mask_pos)
-            assert np.allclose(one, got[off: off + k], rtol=1e-5, atol=1e-6)
+            if prec == "fp32":
+                assert np.allclose(one, got[off: off + k], rtol=1e-5, atol=1e-6)
+            else:
+                compare(one, want[off: off + k], [s], prec, bf16_dp=1e-2)
             off += k
 
 

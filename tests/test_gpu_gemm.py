@@ -116,3 +116,33 @@ def test_gemm_bf16_device(eng, M):
     eng.synchronize()
     err = (dC.cpu().double() - exact).abs()
     assert float((err / (1e-5 * bound + 1e-30)).max()) <= 1.0
+
+
+@pytest.mark.parametrize("prec", ["bf16", "fp32"])
+@pytest.mark.parametrize("M,N,K", [(1, 2304, 768), (31, 768, 1152), (33, 384, 768), (64, 2304, 768),
+                                   (65, 768, 768), (112, 768, 1152), (128, 2304, 64), (100, 128, 4096)])
+def test_gemm_small_m(eng, prec, M, N, K):
+    """M <= 128 runs the split-K small-M kernel (K slices reduced by the last
+    workgroup of each tile). Same bar as above, C += accumulate checked, and
+    two calls in a row must agree bit for bit (the arrival counters reset
+    themselves and the slice sum order is fixed)."""
+    import torch
+
+    dt = torch.bfloat16 if prec == "bf16" else torch.float32
+    g = torch.Generator().manual_seed(M * 7 + N + K)
+    A = torch.randn(M, K, generator=g).to(dt)
+    B = (torch.randn(N, K, generator=g) * 0.02).to(dt)
+    C0 = torch.randn(M, N, generator=g)
+    exact = A.double() @ B.double().T + C0.double()
+    bound = A.double().abs() @ B.double().abs().T + C0.double().abs() * 2.0 ** -23
+    dA, dB = A.cuda(), B.cuda()
+    outs = []
+    for _ in range(2):
+        dC = C0.clone().cuda()
+        torch.cuda.synchronize()
+        eng.gemm_device(prec, M, N, K, dA.data_ptr(), dB.data_ptr(), dC.data_ptr(), accumulate=True)
+        eng.synchronize()
+        outs.append(dC.cpu())
+    err = (outs[0].double() - exact).abs()
+    assert float((err / (1e-5 * bound + 1e-30)).max()) <= 1.0
+    assert torch.equal(outs[0], outs[1])
