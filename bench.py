@@ -192,7 +192,7 @@ def main() -> int:
         "projection_gemm_tflops": round(gemm_tflops, 2),
         "projection_gemm_frac_peak": round(gemm_tflops * 1e12 / PEAK[prec], 4),
         "per_launch_ms": {k: round(v, 5) for k, v in avg.items()},
-        "roofline": {"kernel": "gemm_nt_kernel<bf16,256,128,3,EPI_GEGLU> (Wi projection + GeGLU), layer %d"
+        "roofline": {"kernel": "gemm_nt_kernel, EPI_GEGLU (Wi projection + fused GeGLU), layer %d"
                                % args.probe_layer,
                      "bound": "mfma", "achieved": round(wi_ach / 1e12, 2), "peak": PEAK[prec] / 1e12,
                      "unit": "TFLOP/s", "frac": round(wi_ach / PEAK[prec], 4), "traffic": traffic,

@@ -31,7 +31,6 @@
 
 namespace {
 
-constexpr int NTHREADS = 256;  // 4 waves, 2 x 2 over the output tile
 
 // XOR swizzle of the 16-byte chunks of an LDS tile row: with RB-byte rows,
 // the 16 rows read by a quarter-wave at one logical chunk land in 16
@@ -73,40 +72,42 @@ struct TileOrder {
   }
 };
 
-template <class T, int BM, int BN, int RB, int NSTAGE, int EPI, int WPE>
-__global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(WPE))) void gemm_nt_kernel(GemmArgs g) {
+// WGM x WGN waves tile the BM x BN block; each wave owns a WM x WN sub-tile.
+template <class T, int BM, int BN, int RB, int NSTAGE, int EPI, int WPE, int WGM, int WGN>
+__global__ __launch_bounds__(64 * WGM * WGN) __attribute__((amdgpu_waves_per_eu(WPE))) void gemm_nt_kernel(GemmArgs g) {
   using MF = Mfma<T>;
   typedef typename MF::frag frag;
+  constexpr int NW = WGM * WGN, NT = 64 * NW;
   constexpr int KT = RB / sizeof(T);   // K elements per stage (RB-byte rows)
   constexpr int CPR = RB / 16;         // 16-byte chunks per row
   constexpr int RPI = 1024 / RB;       // rows per wave-wide DMA instruction
-  constexpr int WM = BM / 2, WN = BN / 2;
+  constexpr int WM = BM / WGM, WN = BN / WGN;
   constexpr int TM = WM / 32, TN = WN / 32;
   constexpr int STAGE = (BM + BN) * RB;
-  constexpr int LOADS = (BM + BN) * CPR / NTHREADS;  // 16-byte DMA loads per thread per stage
-  static_assert(LOADS * NTHREADS == (BM + BN) * CPR, "tile rows must fill whole DMA instructions");
+  constexpr int LOADS = (BM + BN) * CPR / NT;  // 16-byte DMA loads per thread per stage
+  static_assert(LOADS * NT == (BM + BN) * CPR, "tile rows must fill whole DMA instructions");
   static_assert(EPI == EPI_F32 || TN % 2 == 0, "paired epilogues need 64-column wave tiles");
   static_assert(NSTAGE >= 2 && LOADS * (NSTAGE - 2) < 64, "pipeline depth");
-  // fp32 epilogue staged in two halves of BM/2 rows; the others in one pass.
-  constexpr int EPI_BYTES = (EPI == EPI_F32) ? (BM / 2) * (BN + 4) * 4
+  // fp32 epilogue staged in WGM passes of WM rows; the others in one pass.
+  constexpr int EPI_BYTES = (EPI == EPI_F32) ? WM * (BN + 4) * 4
                                              : BM * ((EPI == EPI_GEGLU ? BN / 2 : BN) + 8) * (int)sizeof(T);
   constexpr int SMEM = NSTAGE * STAGE > EPI_BYTES ? NSTAGE * STAGE : EPI_BYTES;
   __shared__ __attribute__((aligned(1024))) char smem[SMEM];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave / WGN, wn = wave % WGN;
   const int lr = lane & 31, lh = lane >> 5;
 
   const TileOrder<BM, BN> to(blockIdx.x, (g.M + BM - 1) / BM, g.N / BN, g.ngroups, g.order);
   const int m0 = to.m0, n0 = to.n0;
 
-  // DMA sources: load i of this wave fills tile rows RPI*(wave + 4i) .. +RPI-1;
-  // lane l writes row RPI*(wave+4i) + l/CPR, LDS chunk slot l%CPR, which holds
-  // the row's logical 16-byte chunk (l%CPR) ^ swz(row).
+  // DMA sources: load i of this wave fills tile rows RPI*(wave + NW*i) .. +RPI-1;
+  // lane l writes row RPI*(wave+NW*i) + l/CPR, LDS chunk slot l%CPR, which
+  // holds the row's logical 16-byte chunk (l%CPR) ^ swz(row).
   const char *src[LOADS];
 #pragma unroll
   for (int i = 0; i < LOADS; i++) {
-    const int r = RPI * (wave + 4 * i) + lane / CPR;
+    const int r = RPI * (wave + NW * i) + lane / CPR;
     const int c = (lane % CPR) ^ swz<RB>(r);
     if (r < BM)
       src[i] = (const char *)g.A + (size_t)min(m0 + r, g.M - 1) * g.lda * sizeof(T) + c * 16;
@@ -118,7 +119,7 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(WPE)))
     const size_t kb = (size_t)k0 * sizeof(T);
 #pragma unroll
     for (int i = i0; i < i1; i++)
-      __builtin_amdgcn_global_load_lds((gbl_void *)(src[i] + kb), (lds_void *)(dst + i * 4096), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds((gbl_void *)(src[i] + kb), (lds_void *)(dst + i * NW * 1024), 16, 0, 0);
   };
   auto issue = [&](int stage, int k0) { issue_part(stage, k0, 0, LOADS); };
 
@@ -132,10 +133,12 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(WPE)))
 
   const int rw = wm * WM, cw = wn * WN;  // wave tile origin inside the block tile
 
+  // Every stage issues the same number of DMA loads (past the end of K the
+  // last stage is re-read into a ring slot nothing reads again), so the
+  // vmcnt arithmetic below is exact and no branch surrounds a DMA issue.
   const int nk = g.K / KT;
 #pragma unroll
-  for (int s = 0; s < NSTAGE - 1; s++)
-    if (s < nk) issue(s, s * KT);
+  for (int s = 0; s < NSTAGE - 1; s++) issue(s, min(s, nk - 1) * KT);
 
   constexpr int NKS = KT / MF::KSTEP;                  // MFMA k steps per stage
   constexpr int PER_KS = (LOADS + NKS - 1) / NKS;      // next-stage loads issued per k step
@@ -162,22 +165,19 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(WPE)))
       fb[buf][j] = *(const frag *)(sb + r * RB + ((chunk ^ swz<RB>(r)) << 4) + within);
     }
   };
-  // Waits until stage kt has landed for every wave.
-  auto stage_ready = [&](int kt) {
-    if (kt + NSTAGE - 2 < nk)
-      wait_vmcnt<LOADS * (NSTAGE - 2)>();
-    else
-      wait_vmcnt<0>();
+  // Waits until stage kt has landed for every wave: NSTAGE-2 later stages'
+  // loads may still be in flight.
+  auto stage_ready = [&]() {
+    wait_vmcnt<LOADS * (NSTAGE - 2)>();
     __builtin_amdgcn_s_barrier();
   };
 
-  stage_ready(0);
+  stage_ready();
   load_frags(0, 0, 0);
   for (int kt = 0; kt < nk; kt++) {
     // Refill the buffer of stage kt-1 (every wave finished reading it before
     // the barrier that made stage kt visible) with stage kt + NSTAGE - 1.
-    const bool refill = kt + NSTAGE - 1 < nk;
-    const int rstage = (kt + NSTAGE - 1) % NSTAGE, rk = (kt + NSTAGE - 1) * KT;
+    const int rstage = (kt + NSTAGE - 1) % NSTAGE, rk = min(kt + NSTAGE - 1, nk - 1) * KT;
 #pragma unroll
     for (int ks = 0; ks < NKS; ks++) {
       const int cur = ks & 1;
@@ -185,7 +185,7 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(WPE)))
       // DMA refill (the DMA writes LDS, so reads placed after it could not be
       // hoisted above it), then this step's MFMAs.
       if (ks + 1 < NKS) load_frags(cur ^ 1, kt % NSTAGE, ks + 1);
-      if (refill) {
+      {
         const int i0 = ks * PER_KS < LOADS ? ks * PER_KS : LOADS;
         const int i1 = (ks + 1) * PER_KS < LOADS ? (ks + 1) * PER_KS : LOADS;
         issue_part(rstage, rk, i0, i1);
@@ -202,24 +202,26 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(WPE)))
       __builtin_amdgcn_sched_group_barrier(0x020, PER_KS, 0);
       __builtin_amdgcn_sched_group_barrier(0x008, TM * TN - 2, 0);
       if (ks + 1 == NKS && kt + 1 < nk) {
-        stage_ready(kt + 1);
+        stage_ready();
         load_frags(cur ^ 1, (kt + 1) % NSTAGE, 0);
       }
     }
   }
-  __builtin_amdgcn_s_barrier();  // all waves done with the ring: reuse it for the epilogue
+  // All waves done with the ring and every DMA landed: reuse it for the epilogue.
+  wait_vmcnt<0>();
+  __builtin_amdgcn_s_barrier();
   if constexpr (EPI == EPI_F32) {
     constexpr int LD = BN + 4;  // floats per staged row
-    constexpr int HM = BM / 2;  // rows per pass: the waves with wm == pass stage theirs
+    constexpr int HM = WM;      // rows per pass: the waves with wm == pass stage theirs
     float *st = (float *)smem;
     float *C = (float *)g.C;
     constexpr int V = BN / 4;  // float4 per row
-    constexpr int ITER = HM * V / NTHREADS;
+    constexpr int ITER = HM * V / NT;
     constexpr int BATCH = ITER < 8 ? ITER : 8;
     static_assert(ITER % BATCH == 0, "epilogue batching");
     const bool vec = (g.ldc & 3) == 0;
 #pragma unroll
-    for (int pass = 0; pass < 2; pass++) {
+    for (int pass = 0; pass < WGM; pass++) {
       if (wm == pass) {
 #pragma unroll
         for (int i = 0; i < TM; i++)
@@ -235,7 +237,7 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(WPE)))
         float4 old[BATCH];
 #pragma unroll
         for (int u = 0; u < BATCH; u++) {
-          const int c = tid + (b0 + u) * NTHREADS, r = c / V, c4 = (c % V) * 4;
+          const int c = tid + (b0 + u) * NT, r = c / V, c4 = (c % V) * 4;
           const int row = m0 + pass * HM + r, col = n0 + c4;
           old[u] = make_float4(0.f, 0.f, 0.f, 0.f);
           if (g.accumulate && vec && row < g.M && col + 4 <= g.n_store)
@@ -243,7 +245,7 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(WPE)))
         }
 #pragma unroll
         for (int u = 0; u < BATCH; u++) {
-          const int c = tid + (b0 + u) * NTHREADS, r = c / V, c4 = (c % V) * 4;
+          const int c = tid + (b0 + u) * NT, r = c / V, c4 = (c % V) * 4;
           const int row = m0 + pass * HM + r, col = n0 + c4;
           if (row >= g.M || col >= g.n_store) continue;
           const float4 v = *(const float4 *)(st + r * LD + c4);
@@ -256,7 +258,7 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(WPE)))
           }
         }
       }
-      if (pass == 0) __syncthreads();
+      if (pass + 1 < WGM) __syncthreads();
     }
   } else {
     constexpr int OC = EPI == EPI_GEGLU ? BN / 2 : BN;  // output columns of the block tile
@@ -282,7 +284,7 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(WPE)))
     const int oc0 = EPI == EPI_GEGLU ? n0 / 2 : n0;
     constexpr int EPV = 16 / sizeof(T);  // elements per 16-byte vector
     constexpr int V = OC / EPV;
-    for (int c = tid; c < BM * V; c += NTHREADS) {
+    for (int c = tid; c < BM * V; c += NT) {
       const int r = c / V, cc = (c % V) * EPV;
       const int row = m0 + r;
       if (row >= g.M) continue;
@@ -291,19 +293,19 @@ __global__ __launch_bounds__(NTHREADS) __attribute__((amdgpu_waves_per_eu(WPE)))
   }
 }
 
-template <class T, int BM, int BN, int RB, int NSTAGE, int WPE>
+template <class T, int BM, int BN, int RB, int NSTAGE, int WPE, int WGM = 2, int WGN = 2>
 hipError_t launch_cfg(int epi, const GemmArgs &a, hipStream_t s) {
   const int tiles = ((a.M + BM - 1) / BM) * (a.N / BN);
-  dim3 grid(tiles), block(NTHREADS);
+  dim3 grid(tiles), block(64 * WGM * WGN);
   switch (epi) {
     case EPI_F32:
-      hipLaunchKernelGGL((gemm_nt_kernel<T, BM, BN, RB, NSTAGE, EPI_F32, WPE>), grid, block, 0, s, a);
+      hipLaunchKernelGGL((gemm_nt_kernel<T, BM, BN, RB, NSTAGE, EPI_F32, WPE, WGM, WGN>), grid, block, 0, s, a);
       break;
     case EPI_STORE:
-      hipLaunchKernelGGL((gemm_nt_kernel<T, BM, BN, RB, NSTAGE, EPI_STORE, WPE>), grid, block, 0, s, a);
+      hipLaunchKernelGGL((gemm_nt_kernel<T, BM, BN, RB, NSTAGE, EPI_STORE, WPE, WGM, WGN>), grid, block, 0, s, a);
       break;
     default:
-      hipLaunchKernelGGL((gemm_nt_kernel<T, BM, BN, RB, NSTAGE, EPI_GEGLU, WPE>), grid, block, 0, s, a);
+      hipLaunchKernelGGL((gemm_nt_kernel<T, BM, BN, RB, NSTAGE, EPI_GEGLU, WPE, WGM, WGN>), grid, block, 0, s, a);
       break;
   }
   return hipGetLastError();
