@@ -51,7 +51,11 @@ struct dn_ctx {
   std::map<std::string, TensorSlot> w;
   DevBuf inv_freq;  // 32 doubles global theta, 32 local
   // workspace
-  DevBuf h, xn, qkv, ctxb, act, rope, kinfo, ids, pos, opt, rowtok, logits, err_flag, head_s1, head_d;
+  DevBuf h, xn, qkv, ctxb, act, kinfo, ids, pos, opt, rowtok, logits, err_flag, head_s1, head_d;
+  // RoPE cos/sin per position 0..65535 (global theta, then local), built once
+  // per configuration at the first forward.
+  DevBuf rope;
+  bool rope_ready = false;
   DevBuf gA, gB, gC;  // dn_gemm_f32 staging
   // batch layout cache
   std::vector<int> lay_len;
@@ -255,22 +259,28 @@ int forward_core(dn_ctx *c, int nseq, const int32_t *seq_len, const int32_t *d_i
   HIPCHK(c, "hipMalloc", ensure(c->qkv, es * T * 3 * H));
   HIPCHK(c, "hipMalloc", ensure(c->ctxb, es * T * H));
   HIPCHK(c, "hipMalloc", ensure(c->act, es * T * I));
-  HIPCHK(c, "hipMalloc", ensure(c->rope, sizeof(float) * T * 32 * 4));
   HIPCHK(c, "hipMalloc", ensure(c->kinfo, sizeof(int) * T));
   rc = ensure_err_flag(c);
   if (rc) return rc;
 
+  constexpr int kPositions = 65536;  // positions are validated / flagged to this range
   float *h = (float *)c->h.p;
-  float *rope = (float *)c->rope.p;
-  float *cos_g = rope, *sin_g = rope + (size_t)T * 32, *cos_l = rope + (size_t)2 * T * 32,
-        *sin_l = rope + (size_t)3 * T * 32;
-  int *kinfo = (int *)c->kinfo.p;
   const double *inv = (const double *)c->inv_freq.p;
+  if (!c->rope_ready) {
+    HIPCHK(c, "hipMalloc", ensure(c->rope, sizeof(float) * kPositions * 32 * 4));
+    float *r = (float *)c->rope.p;
+    HIPCHK(c, "rope_tables", launch_rope_tables(nullptr, kPositions, inv, inv + 32, r, r + (size_t)kPositions * 32,
+                                                r + (size_t)2 * kPositions * 32, r + (size_t)3 * kPositions * 32, s));
+    c->rope_ready = true;
+  }
+  const float *rope = (const float *)c->rope.p;
+  const float *cos_g = rope, *sin_g = rope + (size_t)kPositions * 32, *cos_l = rope + (size_t)2 * kPositions * 32,
+              *sin_l = rope + (size_t)3 * kPositions * 32;
+  int *kinfo = (int *)c->kinfo.p;
 
-  HIPCHK(c, "token_info", launch_token_info(d_pos, d_opt, kinfo, T, s));
+  HIPCHK(c, "token_info", launch_token_info(d_pos, d_opt, kinfo, T, (int *)c->err_flag.p, s));
   HIPCHK(c, "chunk_summary", launch_chunk_summary(kinfo, (const int4 *)c->d_chunk_desc.p,
                                                   (ChunkInfo *)c->d_chunks.p, c->lay_nchunks, s));
-  HIPCHK(c, "rope_tables", launch_rope_tables(d_pos, T, inv, inv + 32, cos_g, sin_g, cos_l, sin_l, s));
   HIPCHK(c, "embed_ln",
          launch_embed_ln(prec, d_ids, T, (const float *)W(c, "model.embeddings.tok_embeddings.weight"), g.vocab,
                          (const float *)W(c, "model.embeddings.norm.weight"), g.eps, H, h, c->xn.p,
@@ -314,7 +324,7 @@ int forward_core(dn_ctx *c, int nseq, const int32_t *seq_len, const int32_t *d_i
     PROBED(ev, DN_PROBE_QKV, "gemm(Wqkv)", launch_gemm(prec, EPI_STORE, q, s));
 
     at.sliding = sliding ? 1 : 0;
-    at.cos_t = sliding ? cos_l : cos_g;
+    at.cos_t = sliding ? cos_l : cos_g;  // the layer type picks the table (forward.go:297-301)
     at.sin_t = sliding ? sin_l : sin_g;
     PROBED(ev, DN_PROBE_ATTENTION, "attention", launch_attention(prec, at, s));
 
@@ -489,6 +499,7 @@ int dn_set_config(dn_ctx *c, int hidden, int inter, int heads, int layers, int v
   }
   HIPCHK(c, "hipMalloc", ensure(c->inv_freq, sizeof(inv)));
   HIPCHK(c, "hipMemcpy", hipMemcpy(c->inv_freq.p, inv, sizeof(inv), hipMemcpyHostToDevice));
+  c->rope_ready = false;  // tables follow the new thetas at the next forward
   c->configured = true;
   return DN_OK;
 }
@@ -644,6 +655,7 @@ int dn_check_device_errors(dn_ctx *c) {
   if (flag) {
     HIPCHK(c, "hipMemsetAsync", hipMemsetAsync(c->err_flag.p, 0, sizeof(int), c->stream));
     HIPCHK(c, "hipStreamSynchronize", hipStreamSynchronize(c->stream));
+    if (flag & 4) return fail(c, DN_UNSUPPORTED, "decide_hip: position outside [0, 65535] or option id outside [-1, 32766]");
     return fail(c, DN_INVALID_ARG, (flag & 1) ? "nn: token id out of range" : "nn: mask position out of range");
   }
   return DN_OK;

@@ -75,13 +75,19 @@ struct Staging<float> {
   int info;
 };
 
+// ok ? v : 0, per component (a select of the whole vector can end up as an
+// indexed scratch access).
+__device__ __forceinline__ uint4 keep_if(bool ok, uint4 v) {
+  return make_uint4(ok ? v.x : 0u, ok ? v.y : 0u, ok ? v.z : 0u, ok ? v.w : 0u);
+}
+
 template <class T>
 __device__ __forceinline__ void stage_load(Staging<T> &st, const T *qkv, int ld, int H, int head, int base, int n,
                                            int k0, const float *cos_t, const float *sin_t, const int *kinfo,
                                            int tid) {
-  const uint4 z = {0, 0, 0, 0};
   // Keys past the sequence end read the last key's row (in bounds) and are
   // zeroed; their RoPE factors are whatever that row has (results unused).
+  // The RoPE tables are indexed by position (low 16 bits of the key's info).
   if constexpr (sizeof(T) == 2) {
     {  // K: key = tid / 4, chunk c = tid % 4 (elements 8c..8c+7 and 32+8c..)
       const int key = tid >> 2, c = tid & 3;
@@ -89,20 +95,21 @@ __device__ __forceinline__ void stage_load(Staging<T> &st, const T *qkv, int ld,
       const size_t tok = (size_t)(base + min(k0 + key, n - 1));
       const T *row = qkv + tok * ld + H + head * D;
       const uint4 lo = *(const uint4 *)(row + 8 * c), hi = *(const uint4 *)(row + 32 + 8 * c);
-      st.k_lo = ok ? lo : z;
-      st.k_hi = ok ? hi : z;
-      st.c_lo = *(const float4 *)(cos_t + tok * 32 + 8 * c);
-      st.c_hi = *(const float4 *)(cos_t + tok * 32 + 8 * c + 4);
-      st.s_lo = *(const float4 *)(sin_t + tok * 32 + 8 * c);
-      st.s_hi = *(const float4 *)(sin_t + tok * 32 + 8 * c + 4);
+      st.k_lo = keep_if(ok, lo);
+      st.k_hi = keep_if(ok, hi);
+      const size_t p = (size_t)(kinfo[tok] & 0xffff);
+      st.c_lo = *(const float4 *)(cos_t + p * 32 + 8 * c);
+      st.c_hi = *(const float4 *)(cos_t + p * 32 + 8 * c + 4);
+      st.s_lo = *(const float4 *)(sin_t + p * 32 + 8 * c);
+      st.s_hi = *(const float4 *)(sin_t + p * 32 + 8 * c + 4);
     }
     {  // V: key pair p = tid % 32, d group g = tid / 32
       const int p = tid & 31, g = tid >> 5;
       const int k = k0 + 2 * p;
       const uint4 a = *(const uint4 *)(qkv + (size_t)(base + min(k, n - 1)) * ld + 2 * H + head * D + 8 * g);
       const uint4 b = *(const uint4 *)(qkv + (size_t)(base + min(k + 1, n - 1)) * ld + 2 * H + head * D + 8 * g);
-      st.v0 = k < n ? a : z;
-      st.v1 = k + 1 < n ? b : z;
+      st.v0 = keep_if(k < n, a);
+      st.v1 = keep_if(k + 1 < n, b);
     }
   } else {
 #pragma unroll
@@ -112,16 +119,17 @@ __device__ __forceinline__ void stage_load(Staging<T> &st, const T *qkv, int ld,
       const size_t tok = (size_t)(base + min(k0 + key, n - 1));
       const T *row = qkv + tok * ld + H + head * D;
       const uint4 lo = *(const uint4 *)(row + 4 * c), hi = *(const uint4 *)(row + 32 + 4 * c);
-      st.k_lo[j] = ok ? lo : z;
-      st.k_hi[j] = ok ? hi : z;
-      st.c[j] = *(const float4 *)(cos_t + tok * 32 + 4 * c);
-      st.s[j] = *(const float4 *)(sin_t + tok * 32 + 4 * c);
+      st.k_lo[j] = keep_if(ok, lo);
+      st.k_hi[j] = keep_if(ok, hi);
+      const size_t p = (size_t)(kinfo[tok] & 0xffff);
+      st.c[j] = *(const float4 *)(cos_t + p * 32 + 4 * c);
+      st.s[j] = *(const float4 *)(sin_t + p * 32 + 4 * c);
     }
 #pragma unroll
     for (int j = 0; j < 4; j++) {  // V: key = tid % 64, d group g = tid / 64 + 4 j
       const int key = tid & 63, g = (tid >> 6) + 4 * j;
       const uint4 v = *(const uint4 *)(qkv + (size_t)(base + min(k0 + key, n - 1)) * ld + 2 * H + head * D + 4 * g);
-      st.v[j] = k0 + key < n ? v : z;
+      st.v[j] = keep_if(k0 + key < n, v);
     }
   }
   st.info = (tid < KTILE && k0 + tid < n) ? kinfo[base + k0 + tid] : 0;
@@ -264,7 +272,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_PER_E
   frag qf[NKS];
   {
     const T *qrow = qkv + (size_t)(base + qq) * ld + head * D;
-    const float *cq = a.cos_t + (size_t)(base + qq) * 32, *sq = a.sin_t + (size_t)(base + qq) * 32;
+    const float *cq = a.cos_t + (size_t)qpos * 32, *sq = a.sin_t + (size_t)qpos * 32;
 #pragma unroll
     for (int ks = 0; ks < NKS; ks++) qf[ks] = *(const frag *)(qrow + ks * MF::KSTEP + lh * MF::SLOTS);
     // Pairs (i, i+32): step ks holds i = ks*KSTEP + lh*SLOTS + u, its partner
@@ -438,9 +446,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_PER_E
   }
 }
 
-__global__ void token_info_kernel(const int *pos, const int *opt, int *kinfo, int T) {
+// Packs (option id + 1, position) per token; positions outside [0, 65535] or
+// option ids outside [-1, 32766] set bit 4 of the error flag (the packed
+// form and the per-position RoPE tables cover that range only).
+__global__ void token_info_kernel(const int *pos, const int *opt, int *kinfo, int T, int *err_flag) {
   const int t = blockIdx.x * blockDim.x + threadIdx.x;
-  if (t < T) kinfo[t] = (((opt ? opt[t] : -1) + 1) << 16) | (pos[t] & 0xffff);
+  if (t >= T) return;
+  const int o = opt ? opt[t] : -1, p = pos[t];
+  if (p < 0 || p > 65535 || o < -1 || o > 32766) atomicOr(err_flag, 4);
+  kinfo[t] = ((o + 1) << 16) | (p & 0xffff);
 }
 
 __global__ void chunk_summary_kernel(const int *kinfo, const int4 *desc, ChunkInfo *out, int nchunks) {
@@ -476,9 +490,9 @@ hipError_t launch_attention(int precision, const AttnArgs &a, hipStream_t s) {
   return hipGetLastError();
 }
 
-hipError_t launch_token_info(const int *pos, const int *opt, int *kinfo, int T, hipStream_t s) {
+hipError_t launch_token_info(const int *pos, const int *opt, int *kinfo, int T, int *err_flag, hipStream_t s) {
   if (T <= 0) return hipSuccess;
-  hipLaunchKernelGGL(token_info_kernel, dim3((T + 255) / 256), dim3(256), 0, s, pos, opt, kinfo, T);
+  hipLaunchKernelGGL(token_info_kernel, dim3((T + 255) / 256), dim3(256), 0, s, pos, opt, kinfo, T, err_flag);
   return hipGetLastError();
 }
 

@@ -105,8 +105,8 @@ struct AttnArgs {
   void *ctx;
   const int *kinfo;   // per token: ((opt+1) << 16) | pos
   const ChunkInfo *chunks;
+  const float *cos_t, *sin_t;  // RoPE tables [65536 x 32] of this layer's theta, row = position
   const int4 *work;   // (seq, q0, 0, 0) per workgroup
-  const float *cos_t, *sin_t;  // RoPE tables [T x 32] of this layer's theta
   const int *seq_off, *seq_len, *chunk_off;
   int nwork, H, heads, sliding, half_window;
   float scale_log2;   // softmax scale * log2(e)
@@ -114,7 +114,7 @@ struct AttnArgs {
 hipError_t launch_attention(int precision, const AttnArgs &a, hipStream_t s);
 
 hipError_t launch_chunk_summary(const int *kinfo, const int4 *chunk_desc, ChunkInfo *out, int nchunks, hipStream_t s);
-hipError_t launch_token_info(const int *pos, const int *opt, int *kinfo, int T, hipStream_t s);
+hipError_t launch_token_info(const int *pos, const int *opt, int *kinfo, int T, int *err_flag, hipStream_t s);
 hipError_t launch_rope_tables(const int *pos, int T, const double *inv_g, const double *inv_l, float *cos_g,
                               float *sin_g, float *cos_l, float *sin_l, hipStream_t s);
 hipError_t launch_embed_ln(int precision, const int *ids, int T, const float *tok, int vocab, const float *w, float eps,

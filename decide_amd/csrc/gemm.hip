@@ -190,10 +190,13 @@ __global__ __launch_bounds__(64 * WGM * WGN) __attribute__((amdgpu_waves_per_eu(
         const int i1 = (ks + 1) * PER_KS < LOADS ? (ks + 1) * PER_KS : LOADS;
         issue_part(rstage, rk, i0, i1);
       }
+      // B is the MFMA's first operand: acc[i][j] holds the transposed
+      // 32x32 block, so lane l owns token row l%32 and four runs of four
+      // consecutive output columns (vector stores in the epilogue).
 #pragma unroll
       for (int i = 0; i < TM; i++)
 #pragma unroll
-        for (int j = 0; j < TN; j++) acc[i][j] = MF::mma(fa[cur][i], fb[cur][j], acc[i][j]);
+        for (int j = 0; j < TN; j++) acc[i][j] = MF::mma(fb[cur][j], fa[cur][i], acc[i][j]);
       // One MFMA, then all of the next step's operand reads (they get the
       // rest of the step to land), then the DMA issues, then the MFMAs.
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
@@ -228,7 +231,9 @@ __global__ __launch_bounds__(64 * WGM * WGN) __attribute__((amdgpu_waves_per_eu(
 #pragma unroll
           for (int j = 0; j < TN; j++)
 #pragma unroll
-            for (int e = 0; e < 16; e++) st[(i * 32 + mfma_row(e, lane)) * LD + cw + j * 32 + lr] = acc[i][j][e];
+            for (int q = 0; q < 4; q++)
+              *(float4 *)(st + (i * 32 + lr) * LD + cw + j * 32 + mfma_row(4 * q, lane)) =
+                  make_float4(acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]);
       }
       __syncthreads();
       // All loads of a batch are issued before its stores (C is read and
@@ -263,22 +268,29 @@ __global__ __launch_bounds__(64 * WGM * WGN) __attribute__((amdgpu_waves_per_eu(
   } else {
     constexpr int OC = EPI == EPI_GEGLU ? BN / 2 : BN;  // output columns of the block tile
     constexpr int LD = OC + 8;                          // staged row length (elements)
+    typedef T T4 __attribute__((ext_vector_type(4)));
     T *st = (T *)smem;
 #pragma unroll
-    for (int i = 0; i < TM; i++)
+    for (int i = 0; i < TM; i++) {
 #pragma unroll
       for (int jp = 0; jp < TN / 2; jp++)
 #pragma unroll
-        for (int e = 0; e < 16; e++) {
-          const int r = rw + i * 32 + mfma_row(e, lane);
-          const float a = acc[i][2 * jp][e], b = acc[i][2 * jp + 1][e];
+        for (int q = 0; q < 4; q++) {
+          const int r = rw + i * 32 + lr, c = mfma_row(4 * q, lane);  // 4 consecutive columns from c
+          const f32x16 &a = acc[i][2 * jp], &b = acc[i][2 * jp + 1];
           if constexpr (EPI == EPI_STORE) {
-            st[r * LD + cw + jp * 64 + lr] = to_elem<T>(a);
-            st[r * LD + cw + jp * 64 + 32 + lr] = to_elem<T>(b);
+            *(T4 *)(st + r * LD + cw + jp * 64 + c) =
+                T4{to_elem<T>(a[4 * q]), to_elem<T>(a[4 * q + 1]), to_elem<T>(a[4 * q + 2]), to_elem<T>(a[4 * q + 3])};
+            *(T4 *)(st + r * LD + cw + jp * 64 + 32 + c) =
+                T4{to_elem<T>(b[4 * q]), to_elem<T>(b[4 * q + 1]), to_elem<T>(b[4 * q + 2]), to_elem<T>(b[4 * q + 3])};
           } else {
-            st[r * LD + (cw + jp * 64) / 2 + lr] = to_elem<T>(gelu_erf<T>(a) * b);
+            T4 o;
+#pragma unroll
+            for (int t = 0; t < 4; t++) o[t] = to_elem<T>(gelu_erf<T>(a[4 * q + t]) * b[4 * q + t]);
+            *(T4 *)(st + r * LD + (cw + jp * 64) / 2 + c) = o;
           }
         }
+    }
     __syncthreads();
     T *C = (T *)g.C;
     const int oc0 = EPI == EPI_GEGLU ? n0 / 2 : n0;
@@ -488,10 +500,11 @@ __global__ __launch_bounds__(64 * W) void gemm_skinny_kernel(GemmArgs g) {
 #pragma unroll
       for (int u = 0; u < EPV; u++) {
         float v;
-        if constexpr (EPI == EPI_STORE)
+        if constexpr (EPI == EPI_STORE) {
           v = red[r * TC + c + u];
-        else
+        } else {
           v = gelu_erf<T>(red[r * TC + c + u]) * red[r * TC + 32 + c + u];
+        }
         if constexpr (sizeof(T) == 2) {
           const unsigned b = __builtin_bit_cast(unsigned short, (bf16)v);
           w[u / 2] = (u & 1) ? (w[u / 2] | (b << 16)) : b;

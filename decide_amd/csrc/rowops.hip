@@ -125,13 +125,15 @@ __global__ __launch_bounds__(256) void ln_kernel(const float *xin, int rows, int
 }
 
 // ropeTables (internal/nn/model.go:242-258): angle = f32(pos * inv_freq[i])
-// widened back to f64, then f32(cos), f32(sin). One thread per (token, i).
+// widened back to f64, then f32(cos), f32(sin). One thread per (row, i); row
+// t is token t's position, or position t itself when pos is null (the
+// per-position tables the QKV epilogue indexes).
 __global__ void rope_tables_kernel(const int *pos, int Tn, const double *inv_g, const double *inv_l, float *cg,
                                    float *sg, float *cl, float *sl) {
   const int idx = blockIdx.x * blockDim.x + threadIdx.x;
   if (idx >= Tn * 32) return;
   const int t = idx >> 5, i = idx & 31;
-  const double p = (double)pos[t];
+  const double p = (double)(pos ? pos[t] : t);
   const double fg = (double)(float)(p * inv_g[i]);
   const double fl = (double)(float)(p * inv_l[i]);
   cg[idx] = (float)cos(fg);

@@ -236,3 +236,33 @@ def test_forward_validation_errors(base, engines):
             eng.forward([good, seq] if "sequence 0" not in msg else [seq])
         assert ei.value.message == msg
     assert np.isfinite(eng.forward([good])).all()  # the context stays usable
+
+
+def test_forward_device_position_range_flagged(base, engines):
+    """The device-resident entry point cannot validate positions on the host:
+    a position past the RoPE tables' range (65535) is flagged by the kernels
+    and reported by dn_check_device_errors as unsupported; the context stays
+    usable and the next valid batch is correct."""
+    import torch
+    from decide_amd import Unsupported
+    from decide_amd.nn import Sequence, flatten, row_tokens
+
+    eng = engines["bf16"]
+    good = Sequence(ids=np.array([50281, 7, 50284, 9, 50282], np.int32), pos=np.arange(5, dtype=np.int32),
+                    opt=None, mask_pos=np.array([2], np.int32))
+    want = eng.forward([good])
+    bad_pos = np.array([0, 1, 70000, 3, 4], np.int32)
+    for pos in (bad_pos, good.pos):
+        seq_len, ids, _, _, _, _ = flatten([good])
+        opt = np.full(len(ids), -1, np.int32)
+        d = {k: torch.from_numpy(v).cuda() for k, v in dict(ids=ids, pos=pos, opt=opt, rt=row_tokens([good])).items()}
+        out = torch.zeros(1, dtype=torch.float32, device="cuda")
+        torch.cuda.synchronize()
+        eng.forward_device(seq_len, d["ids"].data_ptr(), d["pos"].data_ptr(), d["opt"].data_ptr(), 1,
+                           d["rt"].data_ptr(), out.data_ptr())
+        if pos is bad_pos:
+            with pytest.raises(Unsupported):
+                eng.check_device_errors()
+        else:
+            eng.check_device_errors()
+            assert np.array_equal(out.cpu().numpy(), want)
