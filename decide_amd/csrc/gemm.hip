@@ -323,7 +323,8 @@ hipError_t launch_cfg(int epi, const GemmArgs &a, hipStream_t s) {
   return hipGetLastError();
 }
 
-// Small-M GEMM (M <= 128: one request, the scorer's dense layer). Such
+// Small-M GEMM (M <= 128 in bf16: one request; M <= 1024 in fp32: the
+// scorer's dense layer over every [MASK] row of a batch). Such
 // launches are bound by streaming the weights and by latency, and the
 // 128-wide tiles above would give only N/128 workgroups. Here a workgroup
 // owns a TR x TC output tile (TR = 32*MB rows, TC = 32*NB columns) and all
@@ -556,7 +557,12 @@ bool gemm_shape_ok(int precision, int N, int K) {
 
 hipError_t launch_gemm(int precision, int epi, const GemmArgs &a0, hipStream_t s) {
   if (a0.M <= 0) return hipSuccess;
+  // Small M goes to the whole-K kernel (grid: N/32 x M/64 workgroups). In
+  // fp32 (the scorer's dense layer over all [MASK] rows, the fp32 validation
+  // build) that pays up to M = 1024: the 64 x 128 tiles below would leave
+  // most CUs idle with a 24-step fp32 K loop each.
   if (a0.M <= 128) return precision == 1 ? launch_skinny<bf16>(epi, a0, s) : launch_skinny<float>(epi, a0, s);
+  if (precision == 0 && a0.M <= 1024) return launch_skinny<float>(epi, a0, s);
   GemmArgs a = a0;
   // N groups per XCD sweep: keep the group's slice of B (N/groups rows of
   // K elements) within about 2 MB of L2.
