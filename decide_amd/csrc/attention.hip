@@ -220,7 +220,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_PER_E
   __shared__ __attribute__((aligned(16))) int sInfo[KTILE];
   __shared__ uint8_t sCode[MAXKT];  // per key tile: 2-bit class of each wave
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lr = lane & 31, lh = lane >> 5;
   // Linear grid, XCD-aware: workgroup ids go round-robin over the 8 XCDs, so
   // XCD x gets the contiguous range [x*per, (x+1)*per) of the logical order
