@@ -176,7 +176,7 @@ int prepare_layout(dn_ctx *c, int nseq, const int32_t *seq_len) {
     c->h_seq_off[s] = T;
     c->h_chunk_off[s] = nch;
     for (int i = 0; i < n; i += 32) c->h_chunk_desc.push_back(make_int4(T + i, std::min(32, n - i), 0, 0));
-    for (int q = 0; q < n; q += 128) c->h_work.push_back(make_int4(s, q, 0, 0));
+    for (int q = 0; q < n; q += 32 * ATTN_WAVES) c->h_work.push_back(make_int4(s, q, 0, 0));
     nch += (n + 31) / 32;
     T += n;
   }

@@ -55,23 +55,25 @@ __device__ __forceinline__ int combine(int a, int b) {
   return 2;
 }
 
-template <class T>
+template <class T, int R>
 struct Staging;
 
-// bf16: a thread stages one (key, 8-element chunk pair (c, c+4)) of K and one
-// (key pair, 8-d group) of V.
-template <>
-struct Staging<bf16> {
-  uint4 k_lo, k_hi, v0, v1;
-  float4 c_lo, c_hi, s_lo, s_hi;
+// bf16: each of a thread's R items is one (key, 16-byte chunk pair (c, c+4))
+// of K with its RoPE factors and one (key pair, 8-d group) of V; the
+// workgroup's threads cover the tile's 256 K items and 256 V items.
+template <int R>
+struct Staging<bf16, R> {
+  uint4 k_lo[R], k_hi[R], v0[R], v1[R];
+  float4 c_lo[R], c_hi[R], s_lo[R], s_hi[R];
   int info;
 };
 
-// fp32: two (key, 4-element chunk pair) of K and four (key, 4-d group) of V.
-template <>
-struct Staging<float> {
-  uint4 k_lo[2], k_hi[2], v[4];
-  float4 c[2], s[2];
+// fp32: 512 (key, 16-byte chunk pair) K items and 1024 (key, 4-d group) V
+// items per tile.
+template <int R>
+struct Staging<float, R> {
+  uint4 k_lo[2 * R], k_hi[2 * R], v[4 * R];
+  float4 c[2 * R], s[2 * R];
   int info;
 };
 
@@ -81,40 +83,44 @@ __device__ __forceinline__ uint4 keep_if(bool ok, uint4 v) {
   return make_uint4(ok ? v.x : 0u, ok ? v.y : 0u, ok ? v.z : 0u, ok ? v.w : 0u);
 }
 
-template <class T>
-__device__ __forceinline__ void stage_load(Staging<T> &st, const T *qkv, int ld, int H, int head, int base, int n,
+// Loads one key tile (keys k0 .. k0+63) into registers; NT threads, R = 256/NT.
+template <class T, int R>
+__device__ __forceinline__ void stage_load(Staging<T, R> &st, const T *qkv, int ld, int H, int head, int base, int n,
                                            int k0, const float *cos_t, const float *sin_t, const int *kinfo,
                                            int tid) {
+  constexpr int NT = 256 / R;
   // Keys past the sequence end read the last key's row (in bounds) and are
   // zeroed; their RoPE factors are whatever that row has (results unused).
   // The RoPE tables are indexed by position (low 16 bits of the key's info).
   if constexpr (sizeof(T) == 2) {
-    {  // K: key = tid / 4, chunk c = tid % 4 (elements 8c..8c+7 and 32+8c..)
-      const int key = tid >> 2, c = tid & 3;
+#pragma unroll
+    for (int j = 0; j < R; j++) {  // K: key = it / 4, chunk c = it % 4 (elements 8c..8c+7 and 32+8c..)
+      const int it = tid + NT * j, key = it >> 2, c = it & 3;
       const bool ok = k0 + key < n;
       const size_t tok = (size_t)(base + min(k0 + key, n - 1));
       const T *row = qkv + tok * ld + H + head * D;
       const uint4 lo = *(const uint4 *)(row + 8 * c), hi = *(const uint4 *)(row + 32 + 8 * c);
-      st.k_lo = keep_if(ok, lo);
-      st.k_hi = keep_if(ok, hi);
+      st.k_lo[j] = keep_if(ok, lo);
+      st.k_hi[j] = keep_if(ok, hi);
       const size_t p = (size_t)(kinfo[tok] & 0xffff);
-      st.c_lo = *(const float4 *)(cos_t + p * 32 + 8 * c);
-      st.c_hi = *(const float4 *)(cos_t + p * 32 + 8 * c + 4);
-      st.s_lo = *(const float4 *)(sin_t + p * 32 + 8 * c);
-      st.s_hi = *(const float4 *)(sin_t + p * 32 + 8 * c + 4);
+      st.c_lo[j] = *(const float4 *)(cos_t + p * 32 + 8 * c);
+      st.c_hi[j] = *(const float4 *)(cos_t + p * 32 + 8 * c + 4);
+      st.s_lo[j] = *(const float4 *)(sin_t + p * 32 + 8 * c);
+      st.s_hi[j] = *(const float4 *)(sin_t + p * 32 + 8 * c + 4);
     }
-    {  // V: key pair p = tid % 32, d group g = tid / 32
-      const int p = tid & 31, g = tid >> 5;
+#pragma unroll
+    for (int j = 0; j < R; j++) {  // V: key pair p = it % 32, d group g = it / 32
+      const int it = tid + NT * j, p = it & 31, g = it >> 5;
       const int k = k0 + 2 * p;
       const uint4 a = *(const uint4 *)(qkv + (size_t)(base + min(k, n - 1)) * ld + 2 * H + head * D + 8 * g);
       const uint4 b = *(const uint4 *)(qkv + (size_t)(base + min(k + 1, n - 1)) * ld + 2 * H + head * D + 8 * g);
-      st.v0 = keep_if(k < n, a);
-      st.v1 = keep_if(k + 1 < n, b);
+      st.v0[j] = keep_if(k < n, a);
+      st.v1[j] = keep_if(k + 1 < n, b);
     }
   } else {
 #pragma unroll
-    for (int j = 0; j < 2; j++) {  // K: (key, chunk c in 0..7) = item tid + 256 j
-      const int it = tid + 256 * j, key = it >> 3, c = it & 7;
+    for (int j = 0; j < 2 * R; j++) {  // K: (key, chunk c in 0..7) = item tid + NT j
+      const int it = tid + NT * j, key = it >> 3, c = it & 7;
       const bool ok = k0 + key < n;
       const size_t tok = (size_t)(base + min(k0 + key, n - 1));
       const T *row = qkv + tok * ld + H + head * D;
@@ -126,8 +132,8 @@ __device__ __forceinline__ void stage_load(Staging<T> &st, const T *qkv, int ld,
       st.s[j] = *(const float4 *)(sin_t + p * 32 + 4 * c);
     }
 #pragma unroll
-    for (int j = 0; j < 4; j++) {  // V: key = tid % 64, d group g = tid / 64 + 4 j
-      const int key = tid & 63, g = (tid >> 6) + 4 * j;
+    for (int j = 0; j < 4 * R; j++) {  // V: key = it % 64, d group g = it / 64
+      const int it = tid + NT * j, key = it & 63, g = it >> 6;
       const uint4 v = *(const uint4 *)(qkv + (size_t)(base + min(k0 + key, n - 1)) * ld + 2 * H + head * D + 4 * g);
       st.v[j] = keep_if(k0 + key < n, v);
     }
@@ -153,40 +159,48 @@ __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, v);
 }
 
-template <class T>
-__device__ __forceinline__ void stage_store(const Staging<T> &st, char *sK, char *sV, int *sInfo, int tid, int ROWK,
-                                            int ROWV) {
+template <class T, int R>
+__device__ __forceinline__ void stage_store(const Staging<T, R> &st, char *sK, char *sV, int *sInfo, int tid,
+                                            int ROWK, int ROWV) {
+  constexpr int NT = 256 / R;
   if constexpr (sizeof(T) == 2) {
-    const int key = tid >> 2, c = tid & 3;
-    const uint32_t klo[4] = {st.k_lo.x, st.k_lo.y, st.k_lo.z, st.k_lo.w};
-    const uint32_t khi[4] = {st.k_hi.x, st.k_hi.y, st.k_hi.z, st.k_hi.w};
-    const float cs[8] = {st.c_lo.x, st.c_lo.y, st.c_lo.z, st.c_lo.w, st.c_hi.x, st.c_hi.y, st.c_hi.z, st.c_hi.w};
-    const float sn[8] = {st.s_lo.x, st.s_lo.y, st.s_lo.z, st.s_lo.w, st.s_hi.x, st.s_hi.y, st.s_hi.z, st.s_hi.w};
-    uint4 olo, ohi;
-    uint32_t *po = (uint32_t *)&olo, *ph = (uint32_t *)&ohi;
 #pragma unroll
-    for (int w = 0; w < 4; w++) {
-      float a0 = bf_lo(klo[w]), a1 = bf_hi(klo[w]), b0 = bf_lo(khi[w]), b1 = bf_hi(khi[w]);
-      rope1(a0, b0, cs[2 * w], sn[2 * w]);
-      rope1(a1, b1, cs[2 * w + 1], sn[2 * w + 1]);
-      po[w] = pack_bf16(a0, a1);
-      ph[w] = pack_bf16(b0, b1);
+    for (int j = 0; j < R; j++) {
+      const int it = tid + NT * j, key = it >> 2, c = it & 3;
+      const uint32_t klo[4] = {st.k_lo[j].x, st.k_lo[j].y, st.k_lo[j].z, st.k_lo[j].w};
+      const uint32_t khi[4] = {st.k_hi[j].x, st.k_hi[j].y, st.k_hi[j].z, st.k_hi[j].w};
+      const float cs[8] = {st.c_lo[j].x, st.c_lo[j].y, st.c_lo[j].z, st.c_lo[j].w,
+                           st.c_hi[j].x, st.c_hi[j].y, st.c_hi[j].z, st.c_hi[j].w};
+      const float sn[8] = {st.s_lo[j].x, st.s_lo[j].y, st.s_lo[j].z, st.s_lo[j].w,
+                           st.s_hi[j].x, st.s_hi[j].y, st.s_hi[j].z, st.s_hi[j].w};
+      uint32_t po[4], ph[4];
+#pragma unroll
+      for (int w = 0; w < 4; w++) {
+        float a0 = bf_lo(klo[w]), a1 = bf_hi(klo[w]), b0 = bf_lo(khi[w]), b1 = bf_hi(khi[w]);
+        rope1(a0, b0, cs[2 * w], sn[2 * w]);
+        rope1(a1, b1, cs[2 * w + 1], sn[2 * w + 1]);
+        po[w] = pack_bf16(a0, a1);
+        ph[w] = pack_bf16(b0, b1);
+      }
+      *(uint4 *)(sK + key * ROWK + 16 * c) = make_uint4(po[0], po[1], po[2], po[3]);
+      *(uint4 *)(sK + key * ROWK + 64 + 16 * c) = make_uint4(ph[0], ph[1], ph[2], ph[3]);
     }
-    *(uint4 *)(sK + key * ROWK + 16 * c) = olo;
-    *(uint4 *)(sK + key * ROWK + 64 + 16 * c) = ohi;
     // V^T: word e of row (8g + e) holds (key 2p, key 2p+1) for d = 8g + e.
-    const int p = tid & 31, g = tid >> 5;
-    const uint32_t va[4] = {st.v0.x, st.v0.y, st.v0.z, st.v0.w};
-    const uint32_t vb[4] = {st.v1.x, st.v1.y, st.v1.z, st.v1.w};
 #pragma unroll
-    for (int w = 0; w < 4; w++) {
-      *(uint32_t *)(sV + (8 * g + 2 * w) * ROWV + 4 * p) = (va[w] & 0xffffu) | (vb[w] << 16);
-      *(uint32_t *)(sV + (8 * g + 2 * w + 1) * ROWV + 4 * p) = (va[w] >> 16) | (vb[w] & 0xffff0000u);
+    for (int j = 0; j < R; j++) {
+      const int it = tid + NT * j, p = it & 31, g = it >> 5;
+      const uint32_t va[4] = {st.v0[j].x, st.v0[j].y, st.v0[j].z, st.v0[j].w};
+      const uint32_t vb[4] = {st.v1[j].x, st.v1[j].y, st.v1[j].z, st.v1[j].w};
+#pragma unroll
+      for (int w = 0; w < 4; w++) {
+        *(uint32_t *)(sV + (8 * g + 2 * w) * ROWV + 4 * p) = (va[w] & 0xffffu) | (vb[w] << 16);
+        *(uint32_t *)(sV + (8 * g + 2 * w + 1) * ROWV + 4 * p) = (va[w] >> 16) | (vb[w] & 0xffff0000u);
+      }
     }
   } else {
 #pragma unroll
-    for (int j = 0; j < 2; j++) {
-      const int it = tid + 256 * j, key = it >> 3, c = it & 7;
+    for (int j = 0; j < 2 * R; j++) {
+      const int it = tid + NT * j, key = it >> 3, c = it & 7;
       float4 lo = *(const float4 *)&st.k_lo[j], hi = *(const float4 *)&st.k_hi[j];
       const float4 cs = st.c[j], sn = st.s[j];
       rope1(lo.x, hi.x, cs.x, sn.x);
@@ -197,8 +211,8 @@ __device__ __forceinline__ void stage_store(const Staging<T> &st, char *sK, char
       *(float4 *)(sK + key * ROWK + 128 + 16 * c) = hi;
     }
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-      const int key = tid & 63, g = (tid >> 6) + 4 * j;
+    for (int j = 0; j < 4 * R; j++) {
+      const int it = tid + NT * j, key = it & 63, g = it >> 6;
       const uint4 v = st.v[j];
       *(uint32_t *)(sV + (4 * g + 0) * ROWV + 4 * key) = v.x;
       *(uint32_t *)(sV + (4 * g + 1) * ROWV + 4 * key) = v.y;
@@ -209,8 +223,12 @@ __device__ __forceinline__ void stage_store(const Staging<T> &st, char *sK, char
   if (tid < KTILE) sInfo[tid] = st.info;
 }
 
-template <class T>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_PER_EU))) void attention_kernel(AttnArgs a) {
+template <class T, int QW>
+__global__ __launch_bounds__(64 * QW) __attribute__((amdgpu_waves_per_eu(WAVES_PER_EU))) void attention_kernel(AttnArgs a) {
+  // R staging items per thread; with more than 4 waves only the first 256
+  // threads stage.
+  constexpr int NT = 64 * QW, R = QW >= 4 ? 1 : 4 / QW;
+  static_assert(QW == 1 || QW == 2 || QW == 4 || QW == 8, "waves per workgroup");
   using MF = Mfma<T>;
   typedef typename MF::frag frag;
   constexpr int ROWK = D * sizeof(T) + 16;       // K tile row bytes (key-major)
@@ -218,7 +236,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_PER_E
   __shared__ __attribute__((aligned(16))) char sK[KTILE * ROWK];
   __shared__ __attribute__((aligned(16))) char sV[D * ROWV];
   __shared__ __attribute__((aligned(16))) int sInfo[KTILE];
-  __shared__ uint8_t sCode[MAXKT];  // per key tile: 2-bit class of each wave
+  __shared__ uint16_t sCode[MAXKT];  // per key tile: 2-bit class of each wave
 
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lr = lane & 31, lh = lane >> 5;
@@ -242,22 +260,22 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_PER_E
   // Classify every key tile against the 4 query chunks of this workgroup.
   {
     const ChunkInfo empty = {0, 0, 1, 0, 0, 0, 0, 0};
-    ChunkInfo qc[4];
+    ChunkInfo qc[QW];
 #pragma unroll
-    for (int w = 0; w < 4; w++) {
+    for (int w = 0; w < QW; w++) {
       const int c = q0 / 32 + w;
       qc[w] = c < nch ? a.chunks[cbase + c] : empty;
     }
-    for (int kt = tid; kt < nkt; kt += 256) {
+    for (int kt = tid; kt < nkt; kt += NT) {
       const ChunkInfo kc0 = a.chunks[cbase + 2 * kt];
       const ChunkInfo kc1 = (2 * kt + 1 < nch) ? a.chunks[cbase + 2 * kt + 1] : empty;
       int code = 0;
 #pragma unroll
-      for (int w = 0; w < 4; w++)
+      for (int w = 0; w < QW; w++)
         code |= combine(tile_class(qc[w], kc0, a.sliding, a.half_window),
                         tile_class(qc[w], kc1, a.sliding, a.half_window))
                 << (2 * w);
-      sCode[kt] = (uint8_t)code;
+      sCode[kt] = (uint16_t)code;
     }
   }
 
@@ -316,17 +334,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_PER_E
     return kt;
   };
   int kt = next_tile(0);
-  Staging<T> st;
-  if (kt < nkt) stage_load<T>(st, qkv, ld, H, head, base, n, kt * KTILE, a.cos_t, a.sin_t, a.kinfo, tid);
+  Staging<T, R> st;
+  const bool stager = tid < 256;
+  if (kt < nkt && stager) stage_load<T, R>(st, qkv, ld, H, head, base, n, kt * KTILE, a.cos_t, a.sin_t, a.kinfo, tid);
 
   while (kt < nkt) {
     const int k0 = kt * KTILE;
     const int mycls = (sCode[kt] >> (2 * wave)) & 3;
     __syncthreads();  // previous tile fully consumed
-    stage_store<T>(st, sK, sV, sInfo, tid, ROWK, ROWV);
+    if (stager) stage_store<T, R>(st, sK, sV, sInfo, tid, ROWK, ROWV);
     __syncthreads();
     const int kn = next_tile(kt + 1);
-    if (kn < nkt) stage_load<T>(st, qkv, ld, H, head, base, n, kn * KTILE, a.cos_t, a.sin_t, a.kinfo, tid);
+    if (kn < nkt && stager) stage_load<T, R>(st, qkv, ld, H, head, base, n, kn * KTILE, a.cos_t, a.sin_t, a.kinfo, tid);
 
     if (mycls != 0) {
       // S^T = K . Q^T for 64 keys x 32 queries (two 32x32 tiles).
@@ -345,7 +364,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_PER_E
         }
       }
 
-      // Scale, mask, running max.
+      // Mask and running max on the raw scores; the softmax scale (times
+      // log2 e, > 0) is applied inside the exponent: p = 2^(s*c - m*c).
       float mx = -INFINITY;
 #pragma unroll
       for (int i = 0; i < 2; i++)
@@ -357,12 +377,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_PER_E
           const int *inf = (const int *)&inf4;
 #pragma unroll
           for (int u = 0; u < 4; u++) {
-            float x = sT[i][4 * g + u] * a.scale_log2;
+            float x = sT[i][4 * g + u];
             if (mycls == 2) {
+              // Block mask: a prefix query sees prefix keys; an option query
+              // sees prefix keys and its own option, i.e. ko in {-1, qopt}.
               const int ko = (inf[u] >> 16) - 1, kp = inf[u] & 0xffff;
-              bool ok = k0 + kl + u < n;
-              ok = ok && (qopt == -1 ? ko == -1 : (ko == -1 || ko == qopt));
-              ok = ok && (!a.sliding || abs(qpos - kp) <= a.half_window);
+              bool ok = k0 + kl + u < n && (ko == -1 || ko == qopt);
+              ok = ok && (!a.sliding || (unsigned)(kp - qpos + a.half_window) <= (unsigned)(2 * a.half_window));
               x = ok ? x : -INFINITY;
             }
             sT[i][4 * g + u] = x;
@@ -372,22 +393,25 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WAVES_PER_E
       mx = fmaxf(mx, __shfl_xor(mx, 32));
       const float m_new = fmaxf(m_run, mx);
       const float m_use = m_new == -INFINITY ? 0.0f : m_new;
-      const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
+      const float c = a.scale_log2, mc = -m_use * c;
+      const float alpha = __builtin_amdgcn_exp2f((m_run - m_use) * c);
       float psum = 0.0f;
 #pragma unroll
       for (int i = 0; i < 2; i++)
 #pragma unroll
         for (int e = 0; e < 16; e++) {
-          const float p = __builtin_amdgcn_exp2f(sT[i][e] - m_use);
+          const float p = __builtin_amdgcn_exp2f(fmaf(sT[i][e], c, mc));
           sT[i][e] = p;
           psum += p;
         }
       l_run = l_run * alpha + psum;
       m_run = m_new;
+      if (__ballot(alpha != 1.0f)) {  // no lane's maximum moved: nothing to rescale
 #pragma unroll
-      for (int i = 0; i < 2; i++)
+        for (int i = 0; i < 2; i++)
 #pragma unroll
-        for (int e = 0; e < 16; e++) ot[i][e] *= alpha;
+          for (int e = 0; e < 16; e++) ot[i][e] *= alpha;
+      }
 
       // O^T += V^T . P^T. k step ks covers accumulator registers
       // [ks*SLOTS, ks*SLOTS + SLOTS) of the flattened S^T tiles; accumulator r
@@ -482,11 +506,11 @@ __global__ void chunk_summary_kernel(const int *kinfo, const int4 *desc, ChunkIn
 
 hipError_t launch_attention(int precision, const AttnArgs &a, hipStream_t s) {
   if (a.nwork <= 0) return hipSuccess;
-  dim3 grid(a.nwork * a.heads), block(256);
+  dim3 grid(a.nwork * a.heads), block(64 * ATTN_WAVES);
   if (precision == 1)
-    hipLaunchKernelGGL(attention_kernel<bf16>, grid, block, 0, s, a);
+    hipLaunchKernelGGL((attention_kernel<bf16, ATTN_WAVES>), grid, block, 0, s, a);
   else
-    hipLaunchKernelGGL(attention_kernel<float>, grid, block, 0, s, a);
+    hipLaunchKernelGGL((attention_kernel<float, ATTN_WAVES>), grid, block, 0, s, a);
   return hipGetLastError();
 }
 

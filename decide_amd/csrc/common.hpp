@@ -100,6 +100,10 @@ enum { EPI_F32 = 0, EPI_STORE = 1, EPI_GEGLU = 2 };
 hipError_t launch_gemm(int precision, int epi, const GemmArgs &a, hipStream_t s);
 bool gemm_shape_ok(int precision, int N, int K);
 
+// Attention work item: 32 * ATTN_WAVES queries of one sequence (one wave per
+// 32 queries), for every head.
+constexpr int ATTN_WAVES = 4;
+
 struct AttnArgs {
   const void *qkv;
   void *ctx;
