@@ -366,30 +366,33 @@ __global__ __launch_bounds__(64 * QW) __attribute__((amdgpu_waves_per_eu(WAVES_P
 
       // Mask and running max on the raw scores; the softmax scale (times
       // log2 e, > 0) is applied inside the exponent: p = 2^(s*c - m*c).
+      // The per-element test is branch-free (bitwise and + select).
+      if (mycls == 2) {
+        const unsigned win2 = a.sliding ? (unsigned)(2 * a.half_window) : 0xffffffffu;
+#pragma unroll
+        for (int i = 0; i < 2; i++)
+#pragma unroll
+          for (int g = 0; g < 4; g++) {
+            const int kl = i * 32 + 8 * g + 4 * lh;  // 4 consecutive keys kl..kl+3
+            const int4 inf4 = *(const int4 *)(sInfo + kl);
+            const int inf[4] = {inf4.x, inf4.y, inf4.z, inf4.w};
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+              // Block mask: a prefix query sees prefix keys; an option query
+              // sees prefix keys and its own option, i.e. ko in {-1, qopt}.
+              // Window: |kpos - qpos| <= W on local layers.
+              const int ko = (inf[u] >> 16) - 1, kp = inf[u] & 0xffff;
+              const bool ok = (k0 + kl + u < n) & ((ko == -1) | (ko == qopt)) &
+                              ((unsigned)(kp - qpos + a.half_window) <= win2);
+              sT[i][4 * g + u] = ok ? sT[i][4 * g + u] : -INFINITY;
+            }
+          }
+      }
       float mx = -INFINITY;
 #pragma unroll
       for (int i = 0; i < 2; i++)
 #pragma unroll
-        for (int g = 0; g < 4; g++) {
-          const int kl = i * 32 + 8 * g + 4 * lh;  // 4 consecutive keys kl..kl+3
-          int4 inf4 = {0, 0, 0, 0};
-          if (mycls == 2) inf4 = *(const int4 *)(sInfo + kl);
-          const int *inf = (const int *)&inf4;
-#pragma unroll
-          for (int u = 0; u < 4; u++) {
-            float x = sT[i][4 * g + u];
-            if (mycls == 2) {
-              // Block mask: a prefix query sees prefix keys; an option query
-              // sees prefix keys and its own option, i.e. ko in {-1, qopt}.
-              const int ko = (inf[u] >> 16) - 1, kp = inf[u] & 0xffff;
-              bool ok = k0 + kl + u < n && (ko == -1 || ko == qopt);
-              ok = ok && (!a.sliding || (unsigned)(kp - qpos + a.half_window) <= (unsigned)(2 * a.half_window));
-              x = ok ? x : -INFINITY;
-            }
-            sT[i][4 * g + u] = x;
-            mx = fmaxf(mx, x);
-          }
-        }
+        for (int e = 0; e < 16; e++) mx = fmaxf(mx, sT[i][e]);
       mx = fmaxf(mx, __shfl_xor(mx, 32));
       const float m_new = fmaxf(m_run, mx);
       const float m_use = m_new == -INFINITY ? 0.0f : m_new;
