@@ -9,11 +9,12 @@
 //   * the mask is evaluated per element from each token's (option id,
 //     position): allowed(i,j) = block(opt_i, opt_j) && (global || |pos_i-pos_j| <= W),
 //     block(a,b) = (a == -1 && b == -1) || (a != -1 && (b == -1 || a == b));
-//   * 32-token chunk summaries let a workgroup skip key tiles with no allowed
-//     pair and drop the per-element test on tiles where every pair is allowed;
+//   * 32-token chunk summaries classify each (32-query chunk, 32-key half
+//     tile) pair as empty, full or mixed: a wave skips the MFMAs, softmax and
+//     P.V of empty halves, and the per-element test of full ones;
 //   * softmax is the online (running max / running sum) form in fp32.
 //
-// Work decomposition: one workgroup = 4 waves = 128 queries of one
+// Work decomposition: one workgroup = ATTN_WAVES (4) waves = 128 queries of one
 // (sequence, head); wave w owns queries q0+32w .. q0+32w+31, one per lane
 // pair (lane l and l^32 share query l%32). Scores are computed transposed,
 // S^T = K . Q^T, so that each lane holds 16 keys of ONE query per 32x32
@@ -47,12 +48,6 @@ __device__ __forceinline__ int tile_class(const ChunkInfo &q, const ChunkInfo &k
   const bool block_full = !ko || (!qp && q.omin == q.omax && k.omin == k.omax && q.omin == k.omin);
   const bool win_full = !sliding || max(q.pmax - k.pmin, k.pmax - q.pmin) <= W;
   return (block_full && win_full && k.len == 32) ? 1 : 2;
-}
-
-__device__ __forceinline__ int combine(int a, int b) {
-  if (a == 0 && b == 0) return 0;
-  if (a == 1 && b == 1) return 1;
-  return 2;
 }
 
 template <class T, int R>
@@ -236,7 +231,9 @@ __global__ __launch_bounds__(64 * QW) __attribute__((amdgpu_waves_per_eu(WAVES_P
   __shared__ __attribute__((aligned(16))) char sK[KTILE * ROWK];
   __shared__ __attribute__((aligned(16))) char sV[D * ROWV];
   __shared__ __attribute__((aligned(16))) int sInfo[KTILE];
-  __shared__ uint16_t sCode[MAXKT];  // per key tile: 2-bit class of each wave
+  // Per key tile: for each wave, the 2-bit class of each 32-key half (bits
+  // 4w..4w+1 keys 0-31, 4w+2..4w+3 keys 32-63).
+  __shared__ uint32_t sCode[MAXKT];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lr = lane & 31, lh = lane >> 5;
@@ -257,7 +254,7 @@ __global__ __launch_bounds__(64 * QW) __attribute__((amdgpu_waves_per_eu(WAVES_P
   const T *qkv = (const T *)a.qkv;
   const int nkt = (n + KTILE - 1) / KTILE;
 
-  // Classify every key tile against the 4 query chunks of this workgroup.
+  // Classify every 32-key half tile against each wave's 32-query chunk.
   {
     const ChunkInfo empty = {0, 0, 1, 0, 0, 0, 0, 0};
     ChunkInfo qc[QW];
@@ -269,13 +266,13 @@ __global__ __launch_bounds__(64 * QW) __attribute__((amdgpu_waves_per_eu(WAVES_P
     for (int kt = tid; kt < nkt; kt += NT) {
       const ChunkInfo kc0 = a.chunks[cbase + 2 * kt];
       const ChunkInfo kc1 = (2 * kt + 1 < nch) ? a.chunks[cbase + 2 * kt + 1] : empty;
-      int code = 0;
+      uint32_t code = 0;
 #pragma unroll
       for (int w = 0; w < QW; w++)
-        code |= combine(tile_class(qc[w], kc0, a.sliding, a.half_window),
-                        tile_class(qc[w], kc1, a.sliding, a.half_window))
-                << (2 * w);
-      sCode[kt] = (uint16_t)code;
+        code |= (uint32_t)(tile_class(qc[w], kc0, a.sliding, a.half_window) |
+                           (tile_class(qc[w], kc1, a.sliding, a.half_window) << 2))
+                << (4 * w);
+      sCode[kt] = code;
     }
   }
 
@@ -340,25 +337,29 @@ __global__ __launch_bounds__(64 * QW) __attribute__((amdgpu_waves_per_eu(WAVES_P
 
   while (kt < nkt) {
     const int k0 = kt * KTILE;
-    const int mycls = (sCode[kt] >> (2 * wave)) & 3;
+    // This wave's classes of the two halves (uniform across the wave).
+    const int mycode = __builtin_amdgcn_readfirstlane((sCode[kt] >> (4 * wave)) & 15);
+    const int hcls[2] = {mycode & 3, mycode >> 2};
     __syncthreads();  // previous tile fully consumed
     if (stager) stage_store<T, R>(st, sK, sV, sInfo, tid, ROWK, ROWV);
     __syncthreads();
     const int kn = next_tile(kt + 1);
     if (kn < nkt && stager) stage_load<T, R>(st, qkv, ld, H, head, base, n, kn * KTILE, a.cos_t, a.sin_t, a.kinfo, tid);
 
-    if (mycls != 0) {
-      // S^T = K . Q^T for 64 keys x 32 queries (two 32x32 tiles).
+    if (mycode != 0) {
+      // S^T = K . Q^T for 64 keys x 32 queries (two 32x32 tiles); a half with
+      // no allowed pair is skipped here and in P.V, and scores -inf.
       f32x16 sT[2];
 #pragma unroll
       for (int i = 0; i < 2; i++)
 #pragma unroll
-        for (int e = 0; e < 16; e++) sT[i][e] = 0.0f;
+        for (int e = 0; e < 16; e++) sT[i][e] = hcls[i] ? 0.0f : -INFINITY;
 #pragma unroll
-      for (int ks = 0; ks < NKS; ks++) {
-        const int kof = (ks * MF::KSTEP + lh * MF::SLOTS) * (int)sizeof(T);
+      for (int i = 0; i < 2; i++) {
+        if (hcls[i] == 0) continue;
 #pragma unroll
-        for (int i = 0; i < 2; i++) {
+        for (int ks = 0; ks < NKS; ks++) {
+          const int kof = (ks * MF::KSTEP + lh * MF::SLOTS) * (int)sizeof(T);
           frag kf = *(const frag *)(sK + (i * 32 + lr) * ROWK + kof);
           sT[i] = MF::mma(kf, qf[ks], sT[i]);
         }
@@ -367,12 +368,12 @@ __global__ __launch_bounds__(64 * QW) __attribute__((amdgpu_waves_per_eu(WAVES_P
       // Mask and running max on the raw scores; the softmax scale (times
       // log2 e, > 0) is applied inside the exponent: p = 2^(s*c - m*c).
       // The per-element test is branch-free (bitwise and + select).
-      if (mycls == 2) {
-        const unsigned win2 = a.sliding ? (unsigned)(2 * a.half_window) : 0xffffffffu;
+      const unsigned win2 = a.sliding ? (unsigned)(2 * a.half_window) : 0xffffffffu;
 #pragma unroll
-        for (int i = 0; i < 2; i++)
+      for (int i = 0; i < 2; i++) {
+        if (hcls[i] != 2) continue;
 #pragma unroll
-          for (int g = 0; g < 4; g++) {
+        for (int g = 0; g < 4; g++) {
             const int kl = i * 32 + 8 * g + 4 * lh;  // 4 consecutive keys kl..kl+3
             const int4 inf4 = *(const int4 *)(sInfo + kl);
             const int inf[4] = {inf4.x, inf4.y, inf4.z, inf4.w};
@@ -386,7 +387,7 @@ __global__ __launch_bounds__(64 * QW) __attribute__((amdgpu_waves_per_eu(WAVES_P
                               ((unsigned)(kp - qpos + a.half_window) <= win2);
               sT[i][4 * g + u] = ok ? sT[i][4 * g + u] : -INFINITY;
             }
-          }
+        }
       }
       float mx = -INFINITY;
 #pragma unroll
@@ -400,13 +401,15 @@ __global__ __launch_bounds__(64 * QW) __attribute__((amdgpu_waves_per_eu(WAVES_P
       const float alpha = __builtin_amdgcn_exp2f((m_run - m_use) * c);
       float psum = 0.0f;
 #pragma unroll
-      for (int i = 0; i < 2; i++)
+      for (int i = 0; i < 2; i++) {
+        if (hcls[i] == 0) continue;  // all -inf: p = 0, and P.V skips the half
 #pragma unroll
         for (int e = 0; e < 16; e++) {
           const float p = __builtin_amdgcn_exp2f(fmaf(sT[i][e], c, mc));
           sT[i][e] = p;
           psum += p;
         }
+      }
       l_run = l_run * alpha + psum;
       m_run = m_new;
       if (__ballot(alpha != 1.0f)) {  // no lane's maximum moved: nothing to rescale
@@ -422,6 +425,7 @@ __global__ __launch_bounds__(64 * QW) __attribute__((amdgpu_waves_per_eu(WAVES_P
       constexpr int NPV = KTILE / MF::KSTEP;
 #pragma unroll
       for (int ks = 0; ks < NPV; ks++) {
+        if (hcls[ks / (NPV / 2)] == 0) continue;
         frag pf;
         if constexpr (sizeof(T) == 2) {
           const int ti = ks >> 1, r0 = (ks & 1) * 8;
