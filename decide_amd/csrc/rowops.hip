@@ -96,32 +96,40 @@ __global__ __launch_bounds__(256) void embed_ln_kernel(const int *ids, int Tn, c
 
 // Bias-free LayerNorm of the fp32 residual stream into the GEMM operand type
 // (attn_norm forward.go:289-294, mlp_norm forward.go:324).
-template <class T>
+// RPW rows per wave (their loads and reductions interleave).
+template <class T, int RPW>
 __global__ __launch_bounds__(256) void ln_kernel(const float *xin, int rows, int dim, const float *w, float eps,
                                                  T *y) {
   const int lane = threadIdx.x & 63;
-  const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (r >= rows) return;
+  const int r0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * RPW;
   const int nvec = dim / 4;
-  const float4 *src = (const float4 *)(xin + (size_t)r * dim);
-  float4 x[MAXV];
+  float4 x[RPW][MAXV];
 #pragma unroll
-  for (int j = 0; j < MAXV; j++)
-    if (lane + 64 * j < nvec) x[j] = src[lane + 64 * j];
-  float mean, rs;
-  row_stats(x, nvec, lane, dim, eps, mean, rs);
+  for (int rr = 0; rr < RPW; rr++) {
+    const float4 *src = (const float4 *)(xin + (size_t)min(r0 + rr, rows - 1) * dim);
+#pragma unroll
+    for (int j = 0; j < MAXV; j++)
+      if (lane + 64 * j < nvec) x[rr][j] = src[lane + 64 * j];
+  }
   const float4 *w4 = (const float4 *)w;
 #pragma unroll
-  for (int j = 0; j < MAXV; j++)
-    if (lane + 64 * j < nvec) {
-      const float4 ww = w4[lane + 64 * j];
-      float4 o;
-      o.x = (x[j].x - mean) * rs * ww.x;
-      o.y = (x[j].y - mean) * rs * ww.y;
-      o.z = (x[j].z - mean) * rs * ww.z;
-      o.w = (x[j].w - mean) * rs * ww.w;
-      store4<T>(y + (size_t)r * dim + 4 * (lane + 64 * j), o);
-    }
+  for (int rr = 0; rr < RPW; rr++) {
+    const int r = r0 + rr;
+    float mean, rs;
+    row_stats(x[rr], nvec, lane, dim, eps, mean, rs);
+    if (r >= rows) continue;
+#pragma unroll
+    for (int j = 0; j < MAXV; j++)
+      if (lane + 64 * j < nvec) {
+        const float4 ww = w4[lane + 64 * j];
+        float4 o;
+        o.x = (x[rr][j].x - mean) * rs * ww.x;
+        o.y = (x[rr][j].y - mean) * rs * ww.y;
+        o.z = (x[rr][j].z - mean) * rs * ww.z;
+        o.w = (x[rr][j].w - mean) * rs * ww.w;
+        store4<T>(y + (size_t)r * dim + 4 * (lane + 64 * j), o);
+      }
+  }
 }
 
 // ropeTables (internal/nn/model.go:242-258): angle = f32(pos * inv_freq[i])
@@ -258,11 +266,12 @@ hipError_t launch_embed_ln(int precision, const int *ids, int Tn, const float *t
 hipError_t launch_ln(int precision, const float *x, int rows, int H, const float *w, float eps, void *y,
                      hipStream_t s) {
   if (rows <= 0) return hipSuccess;
-  dim3 grid((rows + 3) / 4), block(256);
+  constexpr int RPW = 1;
+  dim3 grid((rows + 4 * RPW - 1) / (4 * RPW)), block(256);
   if (precision == 1)
-    hipLaunchKernelGGL(ln_kernel<bf16>, grid, block, 0, s, x, rows, H, w, eps, (bf16 *)y);
+    hipLaunchKernelGGL((ln_kernel<bf16, RPW>), grid, block, 0, s, x, rows, H, w, eps, (bf16 *)y);
   else
-    hipLaunchKernelGGL(ln_kernel<float>, grid, block, 0, s, x, rows, H, w, eps, (float *)y);
+    hipLaunchKernelGGL((ln_kernel<float, RPW>), grid, block, 0, s, x, rows, H, w, eps, (float *)y);
   return hipGetLastError();
 }
 
