@@ -160,14 +160,25 @@ def main() -> int:
     # Roofline kernel: the Wi projection with the fused GeGLU epilogue, the
     # largest projection GEMM (N = 2I = 2304, K = H = 768); every launch of its
     # kernel symbol has this shape, so rocprof's per-symbol average is the
-    # per-launch duration measured here.
+    # per-launch duration measured here. With few tokens (cfg2, cfg5: the
+    # small-M kernel) the launch streams the weights and is bounded by HBM:
+    # achieved = algorithmic bytes (weights + activations in + out) / time.
     wi_flop = 2.0 * T * (2 * I) * H
-    wi_ach = wi_flop / (avg["gemm_wi"] * 1e-3)
+    esz = 2 if prec == "bf16" else 4
+    wi_bytes = esz * (T * H + 2 * I * H + T * I)
+    wi_s = avg["gemm_wi"] * 1e-3
+    hbm_bound = T <= 128
     traffic = None
     tpath = os.path.join(HERE, "profiles", "gemm_wi_geglu_cfg3_traffic.json")
     if args.config == "cfg3" and prec == "bf16" and os.path.exists(tpath):
         with open(tpath) as fh:
             traffic = json.load(fh).get("hbm_bytes_per_launch")
+    if hbm_bound:
+        roof = {"bound": "hbm", "achieved": round(wi_bytes / wi_s / 1e9, 1), "peak": 8000.0, "unit": "GB/s",
+                "frac": round(wi_bytes / wi_s / 8e12, 4)}
+    else:
+        roof = {"bound": "mfma", "achieved": round(wi_flop / wi_s / 1e12, 2), "peak": PEAK[prec] / 1e12,
+                "unit": "TFLOP/s", "frac": round(wi_flop / wi_s / PEAK[prec], 4)}
     gemm_ms = avg["gemm_qkv"] + avg["gemm_wo"] + avg["gemm_wi"] + avg["gemm_mlpwo"]
     gemm_tflops = PROJ_FLOP_PER_TOKEN_LAYER * T / (gemm_ms * 1e-3) / 1e12
     result = {
@@ -192,11 +203,9 @@ def main() -> int:
         "projection_gemm_tflops": round(gemm_tflops, 2),
         "projection_gemm_frac_peak": round(gemm_tflops * 1e12 / PEAK[prec], 4),
         "per_launch_ms": {k: round(v, 5) for k, v in avg.items()},
-        "roofline": {"kernel": "gemm_nt_kernel, EPI_GEGLU (Wi projection + fused GeGLU), layer %d"
-                               % args.probe_layer,
-                     "bound": "mfma", "achieved": round(wi_ach / 1e12, 2), "peak": PEAK[prec] / 1e12,
-                     "unit": "TFLOP/s", "frac": round(wi_ach / PEAK[prec], 4), "traffic": traffic,
-                     "flop_per_launch": wi_flop, "algorithmic_bytes_per_launch": 2 * (T * H + 2 * I * H + T * I)},
+        "roofline": dict({"kernel": "%s, EPI_GEGLU (Wi projection + fused GeGLU), layer %d"
+                                    % ("gemm_skinny_kernel" if hbm_bound else "gemm_nt_kernel", args.probe_layer)},
+                         **roof, traffic=traffic, flop_per_launch=wi_flop, algorithmic_bytes_per_launch=wi_bytes),
     }
     if not args.no_cpu_baseline:
         log("cpu baseline")
