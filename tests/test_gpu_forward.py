@@ -266,3 +266,25 @@ def test_forward_device_position_range_flagged(base, engines):
         else:
             eng.check_device_errors()
             assert np.array_equal(out.cpu().numpy(), want)
+
+
+def test_max_length_sequence(base, engines):
+    """The longest sequence this build accepts (8192 tokens, the reference's
+    Local limit: 8000-token premise + 4 options x 48) against the oracle in
+    both modes; one token more is refused as unsupported."""
+    from decide_amd import Unsupported
+    from decide_amd.nn import build_sequence
+    from decide_amd.synth import pack_request
+
+    cfg, _, orc = base
+    rng = np.random.default_rng(8192)
+    ids = pack_request(rng, 8000, [48] * 4, cfg.vocab)
+    assert len(ids) == 8192
+    batch = [build_sequence(ids, 50284, True)]
+    oracle.set_workers(WORKERS)
+    want = orc.forward(batch)
+    for prec in ("fp32", "bf16"):
+        compare(engines[prec].forward(batch), want, batch, prec)
+    long_ids = pack_request(rng, 8001, [48] * 4, cfg.vocab)
+    with pytest.raises(Unsupported):
+        engines["bf16"].forward([build_sequence(long_ids, 50284, True)])
