@@ -62,6 +62,7 @@ struct dn_ctx {
   std::vector<int> h_seq_off, h_chunk_off;
   std::vector<int4> h_chunk_desc, h_work;
   DevBuf d_seq_off, d_seq_len, d_chunk_off, d_chunk_desc, d_work, d_chunks;
+  DevBuf d_codes, d_first;  // attention tile classes per work item: [global | local]
   int lay_T = 0, lay_nchunks = 0, lay_nwork = 0;
   // kernel probe: events[2*k], events[2*k+1] bracket launch k of one forward
   int probe_layer = -1;
@@ -160,7 +161,7 @@ void define_tensors(dn_ctx *c) {
 
 const void *W(dn_ctx *c, const std::string &name) { return c->w[name].buf.p; }
 
-// Batch layout: sequence offsets, 32-token chunks and 128-query work items.
+// Batch layout: sequence offsets, 32-token chunks and (32 * ATTN_WAVES)-query work items.
 int prepare_layout(dn_ctx *c, int nseq, const int32_t *seq_len) {
   std::vector<int> len(seq_len, seq_len + nseq);
   if (len == c->lay_len && c->d_seq_off.p) return DN_OK;
@@ -188,6 +189,8 @@ int prepare_layout(dn_ctx *c, int nseq, const int32_t *seq_len) {
   HIPCHK(c, "hipMalloc", ensure(c->d_chunk_desc, sizeof(int4) * (nch + 1)));
   HIPCHK(c, "hipMalloc", ensure(c->d_chunks, sizeof(ChunkInfo) * (nch + 1)));
   HIPCHK(c, "hipMalloc", ensure(c->d_work, sizeof(int4) * (c->h_work.size() + 1)));
+  HIPCHK(c, "hipMalloc", ensure(c->d_codes, sizeof(uint32_t) * 2 * ATTN_MAXKT * (c->h_work.size() + 1)));
+  HIPCHK(c, "hipMalloc", ensure(c->d_first, sizeof(int) * 2 * (c->h_work.size() + 1)));
   c->lay_len = len;
   HIPCHK(c, "hipMemcpyAsync", hipMemcpyAsync(c->d_seq_off.p, c->h_seq_off.data(), sizeof(int) * (nseq + 1),
                                              hipMemcpyHostToDevice, c->stream));
@@ -281,6 +284,15 @@ int forward_core(dn_ctx *c, int nseq, const int32_t *seq_len, const int32_t *d_i
   HIPCHK(c, "token_info", launch_token_info(d_pos, d_opt, kinfo, T, (int *)c->err_flag.p, s));
   HIPCHK(c, "chunk_summary", launch_chunk_summary(kinfo, (const int4 *)c->d_chunk_desc.p,
                                                   (ChunkInfo *)c->d_chunks.p, c->lay_nchunks, s));
+  // Attention tile classes for the two layer types (global, then local).
+  uint32_t *codes = (uint32_t *)c->d_codes.p;
+  int *first = (int *)c->d_first.p;
+  const size_t nw = (size_t)c->lay_nwork;
+  for (int sl = 0; sl < 2; sl++)
+    HIPCHK(c, "tile_codes", launch_tile_codes((const ChunkInfo *)c->d_chunks.p, (const int4 *)c->d_work.p,
+                                              (const int *)c->d_seq_len.p, (const int *)c->d_chunk_off.p,
+                                              c->lay_nwork, sl, g.half_window, codes + sl * nw * ATTN_MAXKT,
+                                              first + sl * nw, s));
   HIPCHK(c, "embed_ln",
          launch_embed_ln(prec, d_ids, T, (const float *)W(c, "model.embeddings.tok_embeddings.weight"), g.vocab,
                          (const float *)W(c, "model.embeddings.norm.weight"), g.eps, H, h, c->xn.p,
@@ -290,11 +302,9 @@ int forward_core(dn_ctx *c, int nseq, const int32_t *seq_len, const int32_t *d_i
   at.qkv = c->qkv.p;
   at.ctx = c->ctxb.p;
   at.kinfo = kinfo;
-  at.chunks = (const ChunkInfo *)c->d_chunks.p;
   at.work = (const int4 *)c->d_work.p;
   at.seq_off = (const int *)c->d_seq_off.p;
   at.seq_len = (const int *)c->d_seq_len.p;
-  at.chunk_off = (const int *)c->d_chunk_off.p;
   at.nwork = c->lay_nwork;
   at.H = H;
   at.heads = g.heads;
@@ -324,6 +334,8 @@ int forward_core(dn_ctx *c, int nseq, const int32_t *seq_len, const int32_t *d_i
     PROBED(ev, DN_PROBE_QKV, "gemm(Wqkv)", launch_gemm(prec, EPI_STORE, q, s));
 
     at.sliding = sliding ? 1 : 0;
+    at.codes = codes + (sliding ? nw * ATTN_MAXKT : 0);
+    at.first = first + (sliding ? nw : 0);
     at.cos_t = sliding ? cos_l : cos_g;  // the layer type picks the table (forward.go:297-301)
     at.sin_t = sliding ? sin_l : sin_g;
     PROBED(ev, DN_PROBE_ATTENTION, "attention", launch_attention(prec, at, s));
@@ -449,7 +461,8 @@ void dn_close(dn_ctx *c) {
   DevBuf *bufs[] = {&c->inv_freq, &c->h,     &c->xn,       &c->qkv,         &c->ctxb,     &c->act,
                     &c->rope,     &c->kinfo, &c->ids,      &c->pos,         &c->opt,      &c->rowtok,
                     &c->logits,   &c->err_flag, &c->gA,    &c->gB,          &c->gC,       &c->d_seq_off, &c->head_s1, &c->head_d,
-                    &c->d_seq_len, &c->d_chunk_off, &c->d_chunk_desc, &c->d_work, &c->d_chunks};
+                    &c->d_seq_len, &c->d_chunk_off, &c->d_chunk_desc, &c->d_work, &c->d_chunks,
+                    &c->d_codes,   &c->d_first};
   for (DevBuf *b : bufs) release(*b);
   if (c->own_stream) (void)hipStreamDestroy(c->own_stream);
   delete c;

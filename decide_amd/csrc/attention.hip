@@ -34,7 +34,7 @@ namespace {
 
 constexpr int KTILE = 64;   // keys per tile
 constexpr int D = 64;       // head dim
-constexpr int MAXKT = 8192 / KTILE;
+static_assert(ATTN_MAXKT * KTILE == 8192, "tile codes cover sequences up to 8192 tokens");
 #ifndef WAVES_PER_EU
 #define WAVES_PER_EU 3
 #endif
@@ -233,7 +233,7 @@ __global__ __launch_bounds__(64 * QW) __attribute__((amdgpu_waves_per_eu(WAVES_P
   __shared__ __attribute__((aligned(16))) int sInfo[KTILE];
   // Per key tile: for each wave, the 2-bit class of each 32-key half (bits
   // 4w..4w+1 keys 0-31, 4w+2..4w+3 keys 32-63).
-  __shared__ uint32_t sCode[MAXKT];
+  __shared__ uint32_t sCode[ATTN_MAXKT];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lr = lane & 31, lh = lane >> 5;
@@ -248,33 +248,21 @@ __global__ __launch_bounds__(64 * QW) __attribute__((amdgpu_waves_per_eu(WAVES_P
   if (total % 8 == 0) logical = (bid % 8) * (total / 8) + bid / 8;
   const int4 wk = a.work[logical / a.heads];
   const int s = wk.x, q0 = wk.y, head = logical % a.heads;
-  const int n = a.seq_len[s], base = a.seq_off[s], cbase = a.chunk_off[s];
-  const int nch = (n + 31) / 32;
+  const int n = a.seq_len[s], base = a.seq_off[s];
   const int H = a.H, ld = 3 * H;
   const T *qkv = (const T *)a.qkv;
   const int nkt = (n + KTILE - 1) / KTILE;
 
-  // Classify every 32-key half tile against each wave's 32-query chunk.
-  {
-    const ChunkInfo empty = {0, 0, 1, 0, 0, 0, 0, 0};
-    ChunkInfo qc[QW];
-#pragma unroll
-    for (int w = 0; w < QW; w++) {
-      const int c = q0 / 32 + w;
-      qc[w] = c < nch ? a.chunks[cbase + c] : empty;
-    }
-    for (int kt = tid; kt < nkt; kt += NT) {
-      const ChunkInfo kc0 = a.chunks[cbase + 2 * kt];
-      const ChunkInfo kc1 = (2 * kt + 1 < nch) ? a.chunks[cbase + 2 * kt + 1] : empty;
-      uint32_t code = 0;
-#pragma unroll
-      for (int w = 0; w < QW; w++)
-        code |= (uint32_t)(tile_class(qc[w], kc0, a.sliding, a.half_window) |
-                           (tile_class(qc[w], kc1, a.sliding, a.half_window) << 2))
-                << (4 * w);
-      sCode[kt] = code;
-    }
-  }
+  // This work item's tile classes (computed once per forward and layer type
+  // by tile_codes_kernel) and its first needed tile: the first tile's loads
+  // are issued before the classes reach LDS.
+  const int wi = logical / a.heads;
+  const uint32_t *codes = a.codes + (size_t)wi * ATTN_MAXKT;
+  for (int kt = tid; kt < nkt; kt += NT) sCode[kt] = codes[kt];
+  int kt = a.first[wi];
+  Staging<T, R> st;
+  const bool stager = tid < 256;
+  if (kt < nkt && stager) stage_load<T, R>(st, qkv, ld, H, head, base, n, kt * KTILE, a.cos_t, a.sin_t, a.kinfo, tid);
 
   // This lane's query, its RoPE factors and the rotated Q^T operand
   // (B operand: column = query, k = head dim).
@@ -330,10 +318,6 @@ __global__ __launch_bounds__(64 * QW) __attribute__((amdgpu_waves_per_eu(WAVES_P
     while (kt < nkt && sCode[kt] == 0) kt++;
     return kt;
   };
-  int kt = next_tile(0);
-  Staging<T, R> st;
-  const bool stager = tid < 256;
-  if (kt < nkt && stager) stage_load<T, R>(st, qkv, ld, H, head, base, n, kt * KTILE, a.cos_t, a.sin_t, a.kinfo, tid);
 
   while (kt < nkt) {
     const int k0 = kt * KTILE;
@@ -477,6 +461,47 @@ __global__ __launch_bounds__(64 * QW) __attribute__((amdgpu_waves_per_eu(WAVES_P
   }
 }
 
+// Tile classes of one work item (32 * QW queries of one sequence) for one
+// layer type: for every 64-key tile and wave w, the 2-bit class (0 none, 1
+// all, 2 per-element) of each 32-key half against the wave's 32-query chunk,
+// packed as bits 4w..4w+3; and the first tile with any allowed pair (nkt if
+// none). The classes depend only on the batch layout and the layer type, so
+// every layer of that type reuses them.
+template <int QW>
+__global__ __launch_bounds__(64) void tile_codes_kernel(const ChunkInfo *chunks, const int4 *work, const int *seq_len,
+                                                        const int *chunk_off, int sliding, int half_window,
+                                                        uint32_t *codes, int *first) {
+  __shared__ int s_first;
+  const int wi = blockIdx.x, tid = threadIdx.x;
+  const int4 wk = work[wi];
+  const int s = wk.x, q0 = wk.y;
+  const int n = seq_len[s], cbase = chunk_off[s];
+  const int nch = (n + 31) / 32, nkt = (n + KTILE - 1) / KTILE;
+  if (tid == 0) s_first = nkt;
+  __syncthreads();
+  const ChunkInfo empty = {0, 0, 1, 0, 0, 0, 0, 0};
+  ChunkInfo qc[QW];
+#pragma unroll
+  for (int w = 0; w < QW; w++) {
+    const int c = q0 / 32 + w;
+    qc[w] = c < nch ? chunks[cbase + c] : empty;
+  }
+  for (int kt = tid; kt < nkt; kt += 64) {
+    const ChunkInfo kc0 = chunks[cbase + 2 * kt];
+    const ChunkInfo kc1 = (2 * kt + 1 < nch) ? chunks[cbase + 2 * kt + 1] : empty;
+    uint32_t code = 0;
+#pragma unroll
+    for (int w = 0; w < QW; w++)
+      code |= (uint32_t)(tile_class(qc[w], kc0, sliding, half_window) |
+                         (tile_class(qc[w], kc1, sliding, half_window) << 2))
+              << (4 * w);
+    codes[(size_t)wi * ATTN_MAXKT + kt] = code;
+    if (code) atomicMin(&s_first, kt);
+  }
+  __syncthreads();
+  if (tid == 0) first[wi] = s_first;
+}
+
 // Packs (option id + 1, position) per token; positions outside [0, 65535] or
 // option ids outside [-1, 32766] set bit 4 of the error flag (the packed
 // form and the per-position RoPE tables cover that range only).
@@ -518,6 +543,14 @@ hipError_t launch_attention(int precision, const AttnArgs &a, hipStream_t s) {
     hipLaunchKernelGGL((attention_kernel<bf16, ATTN_WAVES>), grid, block, 0, s, a);
   else
     hipLaunchKernelGGL((attention_kernel<float, ATTN_WAVES>), grid, block, 0, s, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_tile_codes(const ChunkInfo *chunks, const int4 *work, const int *seq_len, const int *chunk_off,
+                             int nwork, int sliding, int half_window, uint32_t *codes, int *first, hipStream_t s) {
+  if (nwork <= 0) return hipSuccess;
+  hipLaunchKernelGGL(tile_codes_kernel<ATTN_WAVES>, dim3(nwork), dim3(64), 0, s, chunks, work, seq_len, chunk_off,
+                     sliding, half_window, codes, first);
   return hipGetLastError();
 }
 

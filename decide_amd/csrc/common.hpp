@@ -103,20 +103,25 @@ bool gemm_shape_ok(int precision, int N, int K);
 // Attention work item: 32 * ATTN_WAVES queries of one sequence (one wave per
 // 32 queries), for every head.
 constexpr int ATTN_WAVES = 4;
+// Key tiles (64 keys) per sequence: sequences up to 8192 tokens.
+constexpr int ATTN_MAXKT = 128;
 
 struct AttnArgs {
   const void *qkv;
   void *ctx;
   const int *kinfo;   // per token: ((opt+1) << 16) | pos
-  const ChunkInfo *chunks;
   const float *cos_t, *sin_t;  // RoPE tables [65536 x 32] of this layer's theta, row = position
   const int4 *work;   // (seq, q0, 0, 0) per workgroup
-  const int *seq_off, *seq_len, *chunk_off;
+  const uint32_t *codes;  // [nwork][ATTN_MAXKT] tile classes of this layer type (tile_codes_kernel)
+  const int *first;       // [nwork] first tile with an allowed pair
+  const int *seq_off, *seq_len;
   int nwork, H, heads, sliding, half_window;
   float scale_log2;   // softmax scale * log2(e)
 };
 hipError_t launch_attention(int precision, const AttnArgs &a, hipStream_t s);
 
+hipError_t launch_tile_codes(const ChunkInfo *chunks, const int4 *work, const int *seq_len, const int *chunk_off,
+                             int nwork, int sliding, int half_window, uint32_t *codes, int *first, hipStream_t s);
 hipError_t launch_chunk_summary(const int *kinfo, const int4 *chunk_desc, ChunkInfo *out, int nchunks, hipStream_t s);
 hipError_t launch_token_info(const int *pos, const int *opt, int *kinfo, int T, int *err_flag, hipStream_t s);
 hipError_t launch_rope_tables(const int *pos, int T, const double *inv_g, const double *inv_l, float *cos_g,
