@@ -410,6 +410,57 @@ int forward_core(dn_ctx *c, int nseq, const int32_t *seq_len, const int32_t *d_i
   return DN_OK;
 }
 
+// The tensor slot `name` when it exists and expects n values; else fails.
+int find_slot(dn_ctx *c, const char *name, const void *data, int64_t n, TensorSlot **out) {
+  if (!c->configured) return fail(c, DN_INVALID_ARG, "decide_hip: dn_set_config has not been called");
+  if (!name || !data) return fail(c, DN_INVALID_ARG, "decide_hip: dn_upload_tensor: NULL argument");
+  auto it = c->w.find(name);
+  if (it == c->w.end()) return fail(c, DN_INVALID_ARG, std::string("decide_hip: unknown tensor ") + name);
+  TensorSlot &t = it->second;
+  if (n != t.n)
+    return fail(c, DN_INVALID_ARG, std::string("nn: ") + name + " has " + std::to_string(n) +
+                                       " values, model expects " + std::to_string(t.n));
+  *out = &t;
+  return DN_OK;
+}
+
+// Wi's value rows [0,I) and gate rows [I,2I) are interleaved in groups of 32:
+// stored row 64g+r is value row 32g+r (r < 32) or gate row I+32g+r-32
+// (r >= 32).
+int64_t wi_src_row(int64_t r, int64_t I) {
+  const int64_t g = r / 64, k = r % 64;
+  return k < 32 ? 32 * g + k : I + 32 * g + (k - 32);
+}
+
+int upload_f32(dn_ctx *c, TensorSlot &t, const float *data, int64_t n) {
+  (void)hipSetDevice(c->device);
+  const bool bf = t.proj && c->cfg.precision == DN_PRECISION_BF16;
+  const size_t bytes = (size_t)n * (bf ? 2 : 4);
+  HIPCHK(c, "hipMalloc", ensure(t.buf, bytes));
+  const int64_t H = c->cfg.hidden, I = c->cfg.inter;
+  auto src_row = [&](int64_t r) -> int64_t { return t.wi ? wi_src_row(r, I) : r; };
+  const int64_t rows = t.wi ? 2 * I : 0;
+  if (bf) {
+    std::vector<uint16_t> tmp((size_t)n);
+    if (t.wi) {
+      for (int64_t r = 0; r < rows; r++) {
+        const float *s = data + src_row(r) * H;
+        for (int64_t k = 0; k < H; k++) tmp[r * H + k] = f32_to_bf16_rne(s[k]);
+      }
+    } else {
+      for (int64_t i = 0; i < n; i++) tmp[i] = f32_to_bf16_rne(data[i]);
+    }
+    HIPCHK(c, "hipMemcpy", hipMemcpy(t.buf.p, tmp.data(), bytes, hipMemcpyHostToDevice));
+  } else if (t.wi) {
+    std::vector<float> tmp((size_t)n);
+    for (int64_t r = 0; r < rows; r++) std::memcpy(&tmp[r * H], data + src_row(r) * H, sizeof(float) * H);
+    HIPCHK(c, "hipMemcpy", hipMemcpy(t.buf.p, tmp.data(), bytes, hipMemcpyHostToDevice));
+  } else {
+    HIPCHK(c, "hipMemcpy", hipMemcpy(t.buf.p, data, bytes, hipMemcpyHostToDevice));
+  }
+  t.set = true;
+  return DN_OK;
+}
 }  // namespace
 
 extern "C" {
@@ -517,51 +568,42 @@ int dn_set_config(dn_ctx *c, int hidden, int inter, int heads, int layers, int v
   return DN_OK;
 }
 
+int dn_upload_tensor_bf16(dn_ctx *c, const char *name, const uint16_t *bits, int64_t n) {
+  if (!c) return DN_INVALID_ARG;
+  c->err.clear();
+  TensorSlot *t = nullptr;
+  int rc = find_slot(c, name, bits, n, &t);
+  if (rc) return rc;
+  if (!(t->proj && c->cfg.precision == DN_PRECISION_BF16)) {
+    // Stored as float32: widen exactly (safetensors.go:113-124).
+    std::vector<float> f((size_t)n);
+    for (int64_t i = 0; i < n; i++) {
+      const uint32_t u = (uint32_t)bits[i] << 16;
+      std::memcpy(&f[i], &u, 4);
+    }
+    return upload_f32(c, *t, f.data(), n);
+  }
+  (void)hipSetDevice(c->device);
+  HIPCHK(c, "hipMalloc", ensure(t->buf, (size_t)n * 2));
+  if (t->wi) {
+    const int64_t H = c->cfg.hidden, I = c->cfg.inter;
+    std::vector<uint16_t> tmp((size_t)n);
+    for (int64_t r = 0; r < 2 * I; r++) std::memcpy(&tmp[r * H], bits + wi_src_row(r, I) * H, 2 * H);
+    HIPCHK(c, "hipMemcpy", hipMemcpy(t->buf.p, tmp.data(), (size_t)n * 2, hipMemcpyHostToDevice));
+  } else {
+    HIPCHK(c, "hipMemcpy", hipMemcpy(t->buf.p, bits, (size_t)n * 2, hipMemcpyHostToDevice));
+  }
+  t->set = true;
+  return DN_OK;
+}
+
 int dn_upload_tensor(dn_ctx *c, const char *name, const float *data, int64_t n) {
   if (!c) return DN_INVALID_ARG;
   c->err.clear();
-  if (!c->configured) return fail(c, DN_INVALID_ARG, "decide_hip: dn_set_config has not been called");
-  if (!name || !data) return fail(c, DN_INVALID_ARG, "decide_hip: dn_upload_tensor: NULL argument");
-  auto it = c->w.find(name);
-  if (it == c->w.end()) return fail(c, DN_INVALID_ARG, std::string("decide_hip: unknown tensor ") + name);
-  TensorSlot &t = it->second;
-  if (n != t.n)
-    return fail(c, DN_INVALID_ARG, std::string("nn: ") + name + " has " + std::to_string(n) +
-                                       " values, model expects " + std::to_string(t.n));
-  (void)hipSetDevice(c->device);
-  const bool bf = t.proj && c->cfg.precision == DN_PRECISION_BF16;
-  const size_t bytes = (size_t)n * (bf ? 2 : 4);
-  HIPCHK(c, "hipMalloc", ensure(t.buf, bytes));
-  const int64_t H = c->cfg.hidden, I = c->cfg.inter;
-  // Row order: Wi's value rows [0,I) and gate rows [I,2I) are interleaved in
-  // groups of 32: stored row 64g+r is value row 32g+r (r < 32) or gate row
-  // I+32g+r-32 (r >= 32).
-  auto src_row = [&](int64_t r) -> int64_t {
-    if (!t.wi) return r;
-    const int64_t g = r / 64, k = r % 64;
-    return k < 32 ? 32 * g + k : I + 32 * g + (k - 32);
-  };
-  const int64_t rows = t.wi ? 2 * I : 0;
-  if (bf) {
-    std::vector<uint16_t> tmp((size_t)n);
-    if (t.wi) {
-      for (int64_t r = 0; r < rows; r++) {
-        const float *s = data + src_row(r) * H;
-        for (int64_t k = 0; k < H; k++) tmp[r * H + k] = f32_to_bf16_rne(s[k]);
-      }
-    } else {
-      for (int64_t i = 0; i < n; i++) tmp[i] = f32_to_bf16_rne(data[i]);
-    }
-    HIPCHK(c, "hipMemcpy", hipMemcpy(t.buf.p, tmp.data(), bytes, hipMemcpyHostToDevice));
-  } else if (t.wi) {
-    std::vector<float> tmp((size_t)n);
-    for (int64_t r = 0; r < rows; r++) std::memcpy(&tmp[r * H], data + src_row(r) * H, sizeof(float) * H);
-    HIPCHK(c, "hipMemcpy", hipMemcpy(t.buf.p, tmp.data(), bytes, hipMemcpyHostToDevice));
-  } else {
-    HIPCHK(c, "hipMemcpy", hipMemcpy(t.buf.p, data, bytes, hipMemcpyHostToDevice));
-  }
-  t.set = true;
-  return DN_OK;
+  TensorSlot *t = nullptr;
+  int rc = find_slot(c, name, data, n, &t);
+  if (rc) return rc;
+  return upload_f32(c, *t, data, n);
 }
 
 int dn_weights_ready(const dn_ctx *c) {
@@ -846,6 +888,89 @@ int dn_answer(const double *logits, int k, double temperature, double *probs, in
     for (int i = 0; i < k; i++) pmax = std::fmax(pmax, probs[i]);
     const double cf = ((double)k * pmax - 1) / (double)(k - 1);
     *confidence = dn_round(std::fmax(0.0, std::fmin(1.0, cf)), 3);
+  }
+  return DN_OK;
+}
+
+int dn_evaluate(dn_ctx *c, int nq, const int32_t *kind, const int32_t *n_opt, const int32_t *q_len,
+                const int32_t *ids, const double *temperature, int32_t mask_id, int independent, double *probs,
+                int32_t *choice, double *confidence, double *value) {
+  if (!c) return DN_INVALID_ARG;
+  c->err.clear();
+  if (nq < 0 || (nq > 0 && (!kind || !n_opt || !q_len || !temperature || !choice || !confidence || !value)))
+    return fail(c, DN_INVALID_ARG, "decide_hip: dn_evaluate: NULL argument");
+  // Pass 1, in question order as Local.Evaluate walks them (local.go:126-150):
+  // the checks of rawLogits (local.go:185-192) and the batch layout.
+  std::vector<int32_t> seq_len, bpos, bopt, nmask, mpos, bids;
+  std::vector<int> fwd_q;  // question of each forwarded sequence
+  int64_t off = 0, nprob = 0;
+  for (int q = 0; q < nq; q++) {
+    const int k = n_opt[q], kd = kind[q], n = q_len[q];
+    const std::string where = "decide: question " + std::to_string(q) + ": ";
+    if (kd < DN_KIND_CHOICE || kd > DN_KIND_NOUL) return fail(c, DN_INVALID_ARG, where + "unsupported question kind");
+    if (k < 0 || n < 0) return fail(c, DN_INVALID_ARG, where + "negative option or token count");
+    if (kd == DN_KIND_NOUL && k != 2) return fail(c, DN_INVALID_ARG, where + "a Noul has exactly two options");
+    if (n > 0 && !ids) return fail(c, DN_INVALID_ARG, "decide_hip: dn_evaluate: NULL argument");
+    if (kd == DN_KIND_NOUL || k >= 2) {  // k <= 1 skips the model (local.go:285-287, :310-312)
+      if (n > 8192)
+        return fail(c, DN_INVALID_ARG, where + "input is " + std::to_string(n) + " tokens; the limit is 8192");
+      const size_t t0 = bpos.size(), m0 = mpos.size();
+      bpos.resize(t0 + n);
+      bopt.resize(t0 + n, -1);
+      mpos.resize(m0 + n);
+      int has_opt = 0;
+      const int nm = dn_build_sequence(ids + off, n, mask_id, independent, bpos.data() + t0, bopt.data() + t0,
+                                       mpos.data() + m0, &has_opt);
+      if (nm != k) return fail(c, DN_INVALID_ARG, where + "input contains the reserved [MASK] token");
+      mpos.resize(m0 + nm);
+      bids.insert(bids.end(), ids + off, ids + off + n);
+      seq_len.push_back(n);
+      nmask.push_back(nm);
+      fwd_q.push_back(q);
+    }
+    off += n;
+    nprob += k;
+  }
+  if (nprob > 0 && !probs) return fail(c, DN_INVALID_ARG, "decide_hip: dn_evaluate: NULL argument");
+  // One forward for every question that needs the model.
+  std::vector<float> logits(mpos.size());
+  if (!seq_len.empty()) {
+    const int rc = dn_forward(c, (int)seq_len.size(), seq_len.data(), bids.data(), bpos.data(),
+                              independent ? bopt.data() : nullptr, nmask.data(), mpos.data(), logits.data(),
+                              (int)logits.size());
+    if (rc) return rc;
+  }
+  // Pass 2: evalChoice / evalScore / evalNoul after the forward
+  // (local.go:264-356), logits widened to float64 (local.go:199-203).
+  std::vector<int64_t> lg_off((size_t)nq, -1);
+  for (size_t i = 0, r = 0; i < fwd_q.size(); r += nmask[i], i++) lg_off[fwd_q[i]] = (int64_t)r;
+  std::vector<double> lg, pr;
+  for (int q = 0, po = 0; q < nq; po += n_opt[q], q++) {
+    const int k = n_opt[q], kd = kind[q];
+    double *pq = probs ? probs + po : nullptr;
+    choice[q] = -1;
+    confidence[q] = 0;
+    value[q] = 0;
+    if (k == 0) continue;  // empty answer
+    pr.assign((size_t)k, 1.0);
+    int ch = 0;
+    double cf = 1.0;
+    if (lg_off[q] >= 0) {
+      lg.assign(logits.begin() + lg_off[q], logits.begin() + lg_off[q] + k);
+      dn_answer(lg.data(), k, temperature[q], pr.data(), &ch, &cf);
+    }
+    if (kd == DN_KIND_CHOICE) {
+      choice[q] = ch;
+      confidence[q] = cf;
+    } else if (kd == DN_KIND_SCORE) {
+      double expect = 0;
+      for (int i = 0; i < k; i++) expect += (double)i * pr[i];
+      value[q] = dn_round(expect, 2);
+      confidence[q] = cf;
+    } else {
+      value[q] = dn_round(std::fmax(0.0, std::fmin(1.0, pr[0])), 4);
+    }
+    for (int i = 0; i < k; i++) pq[i] = dn_round(pr[i], 4);
   }
   return DN_OK;
 }

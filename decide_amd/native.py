@@ -55,6 +55,7 @@ _SIGS = {
     "dn_set_stream": ([_vp, _vp], _i),
     "dn_set_config": ([_vp, _i, _i, _i, _i, _i, _c.c_float, _i, _c.c_double, _c.c_double, _vp, _i], _i),
     "dn_upload_tensor": ([_vp, _c.c_char_p, _f32p, _c.c_int64], _i),
+    "dn_upload_tensor_bf16": ([_vp, _c.c_char_p, _vp, _c.c_int64], _i),
     "dn_weights_ready": ([_vp], _i),
     "dn_forward": ([_vp, _i, _i32p, _i32p, _i32p, _i32p, _i32p, _i32p, _f32p, _i], _i),
     "dn_forward_device": ([_vp, _i, _i32p, _vp, _vp, _vp, _i, _vp, _vp], _i),
@@ -67,6 +68,7 @@ _SIGS = {
     "dn_build_sequence": ([_i32p, _i, _c.c_int32, _i, _i32p, _i32p, _i32p, _c.POINTER(_i)], _i),
     "dn_answer": ([_f64p, _i, _c.c_double, _f64p, _c.POINTER(_i), _c.POINTER(_c.c_double)], _i),
     "dn_round": ([_c.c_double, _i], _c.c_double),
+    "dn_evaluate": ([_vp, _i, _vp, _vp, _vp, _vp, _f64p, _c.c_int32, _i, _f64p, _vp, _f64p, _f64p], _i),
 }
 for _name, (_args, _res) in _SIGS.items():
     _fn = getattr(lib, _name)

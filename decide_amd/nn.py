@@ -191,6 +191,11 @@ class Engine:
         a = np.ascontiguousarray(data, dtype=np.float32).reshape(-1)
         check(lib.dn_upload_tensor(self._h, name.encode(), _ptr(a), a.size), self._h)
 
+    def upload_bf16(self, name: str, bits: np.ndarray) -> None:
+        """Upload bfloat16 bit patterns (uint16), as a BF16 safetensors entry stores them."""
+        a = np.ascontiguousarray(bits, dtype=np.uint16).reshape(-1)
+        check(lib.dn_upload_tensor_bf16(self._h, name.encode(), _ptr(a), a.size), self._h)
+
     @property
     def handle(self):
         return self._h

@@ -90,6 +90,14 @@ int dn_set_config(dn_ctx *ctx, int hidden, int inter, int heads, int layers, int
  * Replaces the per-tensor upload loop of gpunn.New (model.go:80-122). */
 int dn_upload_tensor(dn_ctx *ctx, const char *name, const float *data, int64_t n);
 
+/* The same upload from bfloat16 bits, as a BF16 entry of a safetensors
+ * bundle holds them (n uint16 values, little-endian bit patterns). bf16 mode
+ * stores the projection matrices' bits as given (no float32 round trip);
+ * every other tensor, and every tensor in fp32 mode, is widened exactly to
+ * float32. Replaces the BF16 branch of safetensors.(*File).Float32
+ * (internal/safetensors/safetensors.go:113-124) followed by the upload. */
+int dn_upload_tensor_bf16(dn_ctx *ctx, const char *name, const uint16_t *bits, int64_t n);
+
 /* 1 when every tensor the configured model needs has been uploaded. */
 int dn_weights_ready(const dn_ctx *ctx);
 
@@ -174,6 +182,37 @@ int dn_answer(const double *logits, int k, double temperature, double *probs, in
 
 /* local.go round(): math.RoundToEven(x * 10^places) / 10^places. */
 double dn_round(double x, int places);
+
+/* Question kinds of decide.Local (local.go:264-356). */
+enum { DN_KIND_CHOICE = 0, DN_KIND_SCORE = 1, DN_KIND_NOUL = 2 };
+
+/* Answers every question of one SystemOne call with ONE forward over all of
+ * them. decide.Local.Evaluate (local.go:126-150) runs evalChoice / evalScore /
+ * evalNoul (local.go:264-356) one question at a time, one Forward each; the
+ * answers here are those, computed from a single batched Forward.
+ * Per question q (inputs):
+ *   kind[q]         DN_KIND_*
+ *   n_opt[q]        number of options (Choice criteria, Score levels; 2 for
+ *                   a Noul)
+ *   q_len[q], ids   the tokenizer's ids of bundle.PackText(state,
+ *                   instructions, options) with [CLS]/[SEP] (local.go:185-186),
+ *                   concatenated over questions; questions that skip the
+ *                   model (Choice/Score with n_opt <= 1) may pass q_len 0
+ *   temperature[q]  Calibration.TemperatureFor(kind) (bundle.go:39-50)
+ *   mask_id, independent: as nn.BuildSequence (Tokenizer.MaskID,
+ *                   Meta.IndependentOptions)
+ * Outputs: probs[sum n_opt] calibrated probabilities rounded to 4 places
+ * (question q's at offset sum of n_opt[<q]); choice[q] argmax of the raw
+ * logits for a Choice, else -1; confidence[q] marginConfidence for a Choice
+ * or Score, else 0; value[q] the Score's expectation rounded to 2 places or
+ * the Noul's p(first option) clamped and rounded to 4 places, else 0. A
+ * question with n_opt == 0 gets no probabilities, choice -1, confidence 0.
+ * Errors (DN_INVALID_ARG) name the first failing question in order, with
+ * rawLogits' messages ("input is N tokens; the limit is 8192", "input
+ * contains the reserved [MASK] token"); then nothing is computed. */
+int dn_evaluate(dn_ctx *ctx, int nq, const int32_t *kind, const int32_t *n_opt, const int32_t *q_len,
+                const int32_t *ids, const double *temperature, int32_t mask_id, int independent, double *probs,
+                int32_t *choice, double *confidence, double *value);
 
 #ifdef __cplusplus
 }

@@ -208,3 +208,46 @@ def margin_confidence(probs):
 
 def argmax(x):
     return lib().orc_argmax(np.ascontiguousarray(x, np.float64), len(x))
+
+
+def evaluate_question(model, kind: str, n_opt: int, ids, mask_id: int, independent: bool, temperature: float):
+    """One question answered as decide.Local does it: rawLogits runs ONE
+    Forward over the question's own packed sequence (local.go:182-204), then
+    evalChoice / evalScore / evalNoul (local.go:264-356) post-process.
+    ids are the tokenizer's Encode(PackText(...), true). Returns
+    {"probs": rounded to 4 places, "choice", "confidence", "value"} with the
+    conventions of dn_evaluate (choice -1 unless a Choice; value = Score
+    expectation to 2 places or Noul p(first) to 4 places)."""
+    out = {"probs": [], "choice": -1, "confidence": 0.0, "value": 0.0}
+    if n_opt == 0:
+        return out
+    if kind != "noul" and n_opt == 1:  # local.go:285-287, :310-312: the model is skipped
+        probs = np.ones(1)
+        logits = np.zeros(1)
+    else:
+        ids = np.asarray(ids, np.int32)
+        if len(ids) > 8192:
+            raise ValueError(f"input is {len(ids)} tokens; the limit is 8192")
+        pos, opt, mp = build_sequence(ids, mask_id, independent)
+        if len(mp) != n_opt:
+            raise ValueError("input contains the reserved [MASK] token")
+
+        class _Seq:
+            pass
+        s = _Seq()
+        s.ids, s.pos, s.opt, s.mask_pos = ids, pos, opt, mp
+        logits = model.forward([s]).astype(np.float64)
+        probs = calibrated(logits, temperature)
+    if kind == "choice":
+        out["choice"] = argmax(logits)
+        out["confidence"] = margin_confidence(probs)
+    elif kind == "score":
+        expect = 0.0
+        for i, p in enumerate(probs):
+            expect += float(i) * p
+        out["value"] = round_even(expect, 2)
+        out["confidence"] = margin_confidence(probs)
+    else:
+        out["value"] = round_even(max(0.0, min(1.0, probs[0])), 4)
+    out["probs"] = [round_even(p, 4) for p in probs]
+    return out
