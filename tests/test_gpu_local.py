@@ -5,8 +5,9 @@ Also: BF16 bundles (bf16 bits uploaded as stored) and the error paths.
 
 Bars: fp32 mode, rounded probabilities within 1e-4 (one unit of the
 4th place, since a 1e-6 difference can cross a rounding boundary), Score
-expectation within 0.01, confidence within 0.001, the same choice;
-bf16 mode, probabilities within 2e-3 plus one rounding unit."""
+expectation within 0.01, confidence within 0.001, the same choice; bf16
+mode, probabilities within 2e-3 plus one rounding unit. The fp32 cases pin
+the batching itself."""
 import json
 import os
 
@@ -49,7 +50,7 @@ def bundles(tmp_path_factory):
     from decide_amd.synth import random_weights
 
     cfg = nn.config_from_dict(TINY)
-    w = random_weights(cfg, seed=7, std=0.1)
+    w = random_weights(cfg, seed=7, std=0.05)
     out = {}
     for dt in ("F32", "BF16"):
         d = tmp_path_factory.mktemp("bundle_" + dt)
@@ -102,8 +103,10 @@ def check_answers(resp, want, qs, prec):
     print(f"{prec}: worst |dp| (rounded) {worst:.3g}", flush=True)
 
 
-@pytest.mark.parametrize("prec,dt", [("fp32", "F32"), ("bf16", "BF16"), ("bf16", "F32")])
+@pytest.mark.parametrize("prec,dt", [("fp32", "F32"), ("bf16", "BF16"), ("fp32", "BF16")])
 def test_system_one_matches_serial_oracle(bundles, prec, dt):
+    """The oracle runs the weights the bundle stores (BF16 widened exactly),
+    so in bf16 mode only the activation rounding differs."""
     from decide_amd import bundle
     from decide_amd.local import format_state
 
@@ -131,7 +134,7 @@ def test_many_questions_long_state(bundles, prec):
     from decide_amd import bundle
     from decide_amd.local import Choice, Noul, Option, Score, levels
 
-    d, cfg, om = bundles["F32"]
+    d, cfg, om = bundles["BF16" if prec == "bf16" else "F32"]
     rng = np.random.default_rng(3)
     words = ["alpha", "beta", "gamma", "delta", "payment", "failed", "error", "login", "refund", "urgent"]
     state = " ".join(rng.choice(words, size=250))
@@ -189,8 +192,10 @@ def test_evaluate_errors(bundles):
     d, _, _ = bundles["F32"]
     loc = bundle.load_bundle(d, precision="bf16", encoder=(byte_encode, MIN_MASK))
     with pytest.raises(InvalidArgument, match="question 'q': input contains the reserved \\[MASK\\] token"):
-        loc.system_one("text with [MASK] injected", [("ok", Noul("fine")), ("q", Choice("i", [Option("a"),
-                                                                                               Option("b")]))])
+        # 'one' skips the model, so 'q' is the first question whose input is checked.
+        loc.system_one("text with [MASK] injected", [("one", Choice("i", [Option("only")])),
+                                                     ("q", Choice("i", [Option("a"), Option("b")])),
+                                                     ("n", Noul("fine"))])
     with pytest.raises(InvalidArgument, match="duplicate choice"):
         loc.system_one("s", [("q", Choice("i", [Option("a"), Option("a")]))])
     with pytest.raises(InvalidArgument, match="duplicate question id"):
