@@ -8,6 +8,7 @@ below). Synthetic data: weights N(0, 0.02) with InitRandom semantics and
 seeded token ids; see decide_amd/synth.py.
 
   python bench.py [--steps K] [--warmup W] [--config cfg3] [--precision bf16]
+  python bench.py --systemone [--steps K]   one SystemOne call, batched vs serial
 """
 from __future__ import annotations
 
@@ -70,6 +71,115 @@ def cpu_baseline(cfg, weights, name: str, budget_s: float = 12.0):
                       f"{secs:.1f} s; C++ restatement of the reference Go AVX2 path (oracle/)"}
 
 
+SYSTEMONE_METRIC = ("SystemOne call: 24 questions (cfg4 mix) over a 2048-token state, answered with one "
+                    "batched forward vs one forward per question, ModernBERT-base, 1 MI355X")
+
+
+def systemone(args) -> int:
+    """Times Local.Evaluate's work for one SystemOne call through the C ABI
+    (host ids in, answers out, validation and post-processing included):
+    dn_evaluate over all 24 questions (one forward) against 24 dn_evaluate
+    calls of one question each (one forward per question, as local.go:126-150
+    runs them). Prints one JSON line."""
+    import ctypes
+
+    from decide_amd import Engine, modernbert_base
+    from decide_amd.native import check, lib
+    from decide_amd.nn import MASK_ID
+    from decide_amd.synth import random_weights, systemone_call
+
+    cfg = modernbert_base()
+    weights = random_weights(cfg, seed=0)
+    kinds, nopt, qids = systemone_call(cfg.vocab)
+    nq = len(kinds)
+    eng = Engine(cfg, weights, precision=args.precision)
+    h = eng.handle
+    vp = lambda a: a.ctypes.data_as(ctypes.c_void_p)  # noqa: E731
+
+    def call(sel):
+        k = np.array([kinds[i] for i in sel], np.int32)
+        n = np.array([nopt[i] for i in sel], np.int32)
+        ql = np.array([len(qids[i]) for i in sel], np.int32)
+        ids = np.concatenate([qids[i] for i in sel]).astype(np.int32)
+        t = np.ones(len(sel), np.float64)
+        pr = np.zeros(int(n.sum()), np.float64)
+        ch = np.zeros(len(sel), np.int32)
+        cf = np.zeros(len(sel), np.float64)
+        va = np.zeros(len(sel), np.float64)
+        check(lib.dn_evaluate(h, len(sel), vp(k), vp(n), vp(ql), vp(ids), vp(t), MASK_ID, 1, vp(pr), vp(ch), vp(cf),
+                              vp(va)), h)
+        return pr, ch
+
+    def batched():
+        return call(list(range(nq)))
+
+    def serial():
+        outs = [call([i]) for i in range(nq)]
+        return np.concatenate([o[0] for o in outs]), np.concatenate([o[1] for o in outs])
+
+    T = sum(len(q) for q in qids)
+    log(f"systemone: {nq} questions, {T} tokens per call")
+    for _ in range(args.warmup):
+        batched()
+        serial()
+    tb, ts = [], []
+    for _ in range(args.steps):
+        t0 = time.perf_counter()
+        pb, cb = batched()
+        tb.append(time.perf_counter() - t0)
+        t0 = time.perf_counter()
+        ps, cs = serial()
+        ts.append(time.perf_counter() - t0)
+    agree = float(np.mean(cb == cs))
+    dp = float(np.max(np.abs(pb - ps)))
+    mb, ms = float(np.median(tb)), float(np.median(ts))
+    result = {
+        "metric": SYSTEMONE_METRIC,
+        "value": round(1.0 / mb, 3),
+        "unit": "calls/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(mb * 1e3, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": args.precision,
+        "data": "synthetic: random-init weights N(0,0.02) (numpy PCG64 seed 0); 24 packed questions "
+                "[CLS] 16 instruction ids + 2030 state ids [SEP] ([MASK] option)*K [SEP] (decide_amd/synth.py)",
+        "config": {"workload": "systemone: 24 questions (Choice K=4 x6+, Noul K=2, Score K=5; cfg4 order) over one "
+                               "2048-token state", "questions": nq, "tokens_per_call": T, "precision": args.precision},
+        "batched_ms_per_call_p50": round(mb * 1e3, 3),
+        "serial_ms_per_call_p50": round(ms * 1e3, 3),
+        "speedup_batched_vs_serial": round(ms / mb, 3),
+        "batched_tokens_per_s": round(T / mb, 1),
+        "answers_agree_batched_vs_serial": {"choice_equal": agree, "max_abs_dprob_rounded": dp},
+    }
+    if not args.no_cpu_baseline:
+        import oracle
+
+        threads = cpu_threads()
+        oracle.set_workers(threads)
+        model = oracle.OracleModel(cfg, weights)
+        secs, done = 0.0, 0
+        while secs < args.cpu_budget and done < nq:
+            i = done
+            t0 = time.perf_counter()
+            oracle.evaluate_question(model, {0: "choice", 1: "score", 2: "noul"}[kinds[i]], nopt[i], qids[i], MASK_ID,
+                                     True, 1.0)
+            secs += time.perf_counter() - t0
+            done += 1
+        per_q = secs / done
+        result["cpu_baseline"] = {"value": round(1.0 / (per_q * nq), 5), "unit": "calls/s", "cores": threads,
+                                  "kind": "port",
+                                  "sample": f"{done} of the call's {nq} questions, one oracle forward each "
+                                            f"({secs:.1f} s), scaled to the whole call; C++ restatement of the "
+                                            "reference Go AVX2 path (oracle/)"}
+    eng.close()
+    print(json.dumps(result), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -82,11 +192,16 @@ def main() -> int:
     ap.add_argument("--probe-layer", type=int, default=1)
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="run one device copy of MIB MiB first (reference kernel for HBM counters)")
+    ap.add_argument("--systemone", action="store_true",
+                    help="time one SystemOne call (24 questions) batched into one forward vs one forward each")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
               "(the forward shards by sequence with no collective; see DESIGN.md)", file=sys.stderr)
         return 2
+
+    if args.systemone:
+        return systemone(args)
 
     import torch
 

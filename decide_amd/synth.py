@@ -96,3 +96,26 @@ def cfg4_question_groups() -> List[tuple]:
         out.append((kind, off, k))
         off += k
     return out
+
+
+def systemone_call(vocab: int = 50368, seed: int = 0, state_tokens: int = 2030, instr_tokens: int = 16):
+    """One SystemOne call of 24 questions over one state, as Local packs it
+    (PackText + Encode: [CLS] instructions state [SEP] ([MASK] option)*K
+    [SEP], bundle.go:81-93): the cfg4 question mix (Choice K=4, Noul K=2,
+    Score K=5, 32 option tokens each), the same state in every question and
+    16 instruction tokens of its own. Returns (kinds, n_opt, per-question
+    ids) with kinds 0 = Choice, 1 = Score, 2 = Noul."""
+    rng = np.random.default_rng(2000 + seed)
+    state = random_ids(rng, state_tokens, vocab)
+    code = {"choice": 0, "score": 1, "noul": 2}
+    kinds, nopt, qids = [], [], []
+    for kind in CFG4_ORDER:
+        parts = [np.array([CLS_ID], np.int32), random_ids(rng, instr_tokens, vocab), state,
+                 np.array([SEP_ID], np.int32)]
+        for ln in SEGMENTS[kind]:
+            parts += [np.array([MASK_ID], np.int32), random_ids(rng, ln - 1, vocab)]
+        parts.append(np.array([SEP_ID], np.int32))
+        kinds.append(code[kind])
+        nopt.append(len(SEGMENTS[kind]))
+        qids.append(np.concatenate(parts).astype(np.int32))
+    return kinds, nopt, qids
