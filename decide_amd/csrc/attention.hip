@@ -228,9 +228,14 @@ __global__ __launch_bounds__(64 * QW) __attribute__((amdgpu_waves_per_eu(WAVES_P
   typedef typename MF::frag frag;
   constexpr int ROWK = D * sizeof(T) + 16;       // K tile row bytes (key-major)
   constexpr int ROWV = KTILE * sizeof(T) + 16;   // V^T tile row bytes (d-major)
-  __shared__ __attribute__((aligned(16))) char sK[KTILE * ROWK];
-  __shared__ __attribute__((aligned(16))) char sV[D * ROWV];
-  __shared__ __attribute__((aligned(16))) int sInfo[KTILE];
+  // bf16: two buffers, tile t is computed from one while tile t+1 is stored
+  // into the other, with one barrier per tile. fp32 (the validation mode,
+  // twice the bytes) keeps one buffer and a second barrier so that three
+  // workgroups fit a CU.
+  constexpr int NBUF = sizeof(T) == 2 ? 2 : 1;
+  __shared__ __attribute__((aligned(16))) char sK[NBUF][KTILE * ROWK];
+  __shared__ __attribute__((aligned(16))) char sV[NBUF][D * ROWV];
+  __shared__ __attribute__((aligned(16))) int sInfo[NBUF][KTILE];
   // Per key tile: for each wave, the 2-bit class of each 32-key half (bits
   // 4w..4w+1 keys 0-31, 4w+2..4w+3 keys 32-63).
   __shared__ uint32_t sCode[ATTN_MAXKT];
@@ -319,16 +324,24 @@ __global__ __launch_bounds__(64 * QW) __attribute__((amdgpu_waves_per_eu(WAVES_P
     return kt;
   };
 
+  // Pipeline: the first tile is stored, the second one's loads are issued;
+  // then per tile: compute it from buffer b, store the next tile (loaded
+  // during the compute) into buffer b^1, issue the loads of the one after,
+  // one barrier.
+  int kn = nkt, b = 0;
+  if (kt < nkt) {
+    if (stager) stage_store<T, R>(st, sK[0], sV[0], sInfo[0], tid, ROWK, ROWV);
+    kn = next_tile(kt + 1);
+    if (kn < nkt && stager) stage_load<T, R>(st, qkv, ld, H, head, base, n, kn * KTILE, a.cos_t, a.sin_t, a.kinfo, tid);
+    __syncthreads();
+  }
   while (kt < nkt) {
     const int k0 = kt * KTILE;
+    const char *sKb = sK[b], *sVb = sV[b];
+    const int *sInfob = sInfo[b];
     // This wave's classes of the two halves (uniform across the wave).
     const int mycode = __builtin_amdgcn_readfirstlane((sCode[kt] >> (4 * wave)) & 15);
     const int hcls[2] = {mycode & 3, mycode >> 2};
-    __syncthreads();  // previous tile fully consumed
-    if (stager) stage_store<T, R>(st, sK, sV, sInfo, tid, ROWK, ROWV);
-    __syncthreads();
-    const int kn = next_tile(kt + 1);
-    if (kn < nkt && stager) stage_load<T, R>(st, qkv, ld, H, head, base, n, kn * KTILE, a.cos_t, a.sin_t, a.kinfo, tid);
 
     if (mycode != 0) {
       // S^T = K . Q^T for 64 keys x 32 queries (two 32x32 tiles); a half with
@@ -344,7 +357,7 @@ __global__ __launch_bounds__(64 * QW) __attribute__((amdgpu_waves_per_eu(WAVES_P
 #pragma unroll
         for (int ks = 0; ks < NKS; ks++) {
           const int kof = (ks * MF::KSTEP + lh * MF::SLOTS) * (int)sizeof(T);
-          frag kf = *(const frag *)(sK + (i * 32 + lr) * ROWK + kof);
+          frag kf = *(const frag *)(sKb + (i * 32 + lr) * ROWK + kof);
           sT[i] = MF::mma(kf, qf[ks], sT[i]);
         }
       }
@@ -359,7 +372,7 @@ __global__ __launch_bounds__(64 * QW) __attribute__((amdgpu_waves_per_eu(WAVES_P
 #pragma unroll
         for (int g = 0; g < 4; g++) {
             const int kl = i * 32 + 8 * g + 4 * lh;  // 4 consecutive keys kl..kl+3
-            const int4 inf4 = *(const int4 *)(sInfo + kl);
+            const int4 inf4 = *(const int4 *)(sInfob + kl);
             const int inf[4] = {inf4.x, inf4.y, inf4.z, inf4.w};
 #pragma unroll
             for (int u = 0; u < 4; u++) {
@@ -420,7 +433,7 @@ __global__ __launch_bounds__(64 * QW) __attribute__((amdgpu_waves_per_eu(WAVES_P
         }
 #pragma unroll
         for (int i = 0; i < 2; i++) {
-          const char *vrow = sV + (i * 32 + lr) * ROWV;
+          const char *vrow = sVb + (i * 32 + lr) * ROWV;
           frag vf;
           if constexpr (sizeof(T) == 2) {
             const int kb = 32 * (ks >> 1) + 16 * (ks & 1) + 4 * lh;
@@ -436,7 +449,19 @@ __global__ __launch_bounds__(64 * QW) __attribute__((amdgpu_waves_per_eu(WAVES_P
         }
       }
     }
+    int kn2 = nkt;
+    if (kn < nkt) {
+      const int nb = NBUF == 2 ? b ^ 1 : 0;
+      if constexpr (NBUF == 1) __syncthreads();  // every wave is done with the one buffer
+      if (stager) stage_store<T, R>(st, sK[nb], sV[nb], sInfo[nb], tid, ROWK, ROWV);
+      kn2 = next_tile(kn + 1);
+      if (kn2 < nkt && stager)
+        stage_load<T, R>(st, qkv, ld, H, head, base, n, kn2 * KTILE, a.cos_t, a.sin_t, a.kinfo, tid);
+    }
+    __syncthreads();  // the next tile's buffer is complete; buffer b is free
     kt = kn;
+    kn = kn2;
+    b = NBUF == 2 ? b ^ 1 : 0;
   }
 
   // Normalise and store ctx[token][head*64 + d].
