@@ -161,7 +161,7 @@ void define_tensors(dn_ctx *c) {
 
 const void *W(dn_ctx *c, const std::string &name) { return c->w[name].buf.p; }
 
-// Batch layout: sequence offsets, 32-token chunks and (32 * ATTN_WAVES)-query work items.
+// Batch layout: sequence offsets, 32-token chunks and ATTN_QUERIES-query work items.
 int prepare_layout(dn_ctx *c, int nseq, const int32_t *seq_len) {
   std::vector<int> len(seq_len, seq_len + nseq);
   if (len == c->lay_len && c->d_seq_off.p) return DN_OK;
@@ -177,7 +177,7 @@ int prepare_layout(dn_ctx *c, int nseq, const int32_t *seq_len) {
     c->h_seq_off[s] = T;
     c->h_chunk_off[s] = nch;
     for (int i = 0; i < n; i += 32) c->h_chunk_desc.push_back(make_int4(T + i, std::min(32, n - i), 0, 0));
-    for (int q = 0; q < n; q += 32 * ATTN_WAVES) c->h_work.push_back(make_int4(s, q, 0, 0));
+    for (int q = 0; q < n; q += ATTN_QUERIES) c->h_work.push_back(make_int4(s, q, 0, 0));
     nch += (n + 31) / 32;
     T += n;
   }

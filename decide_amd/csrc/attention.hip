@@ -35,9 +35,6 @@ namespace {
 constexpr int KTILE = 64;   // keys per tile
 constexpr int D = 64;       // head dim
 static_assert(ATTN_MAXKT * KTILE == 8192, "tile codes cover sequences up to 8192 tokens");
-#ifndef WAVES_PER_EU
-#define WAVES_PER_EU 3
-#endif
 
 __device__ __forceinline__ int tile_class(const ChunkInfo &q, const ChunkInfo &k, int sliding, int W) {
   // 0: no allowed pair; 1: every pair allowed; 2: test per element.
@@ -180,16 +177,22 @@ __device__ __forceinline__ void stage_store(const Staging<T, R> &st, char *sK, c
       *(uint4 *)(sK + key * ROWK + 16 * c) = make_uint4(po[0], po[1], po[2], po[3]);
       *(uint4 *)(sK + key * ROWK + 64 + 16 * c) = make_uint4(ph[0], ph[1], ph[2], ph[3]);
     }
-    // V^T: word e of row (8g + e) holds (key 2p, key 2p+1) for d = 8g + e.
+    // V^T: row d = 8g + e holds key pairs (2p, 2p+1), one per 32-bit word.
+    // Within each 16-key group the 4-key runs are stored in the order
+    // 0-3, 8-11, 4-7, 12-15: the eight keys one lane feeds to a P.V step
+    // (runs 4lh.. and 8+4lh.., the S^T accumulator order) are then one
+    // contiguous 16-byte read.
 #pragma unroll
     for (int j = 0; j < R; j++) {
       const int it = tid + NT * j, p = it & 31, g = it >> 5;
+      const int lp = p & 7, q4 = lp >> 1;
+      const int pw = (p & ~7) + ((((q4 & 1) << 1) | (q4 >> 1)) << 1) + (lp & 1);
       const uint32_t va[4] = {st.v0[j].x, st.v0[j].y, st.v0[j].z, st.v0[j].w};
       const uint32_t vb[4] = {st.v1[j].x, st.v1[j].y, st.v1[j].z, st.v1[j].w};
 #pragma unroll
       for (int w = 0; w < 4; w++) {
-        *(uint32_t *)(sV + (8 * g + 2 * w) * ROWV + 4 * p) = (va[w] & 0xffffu) | (vb[w] << 16);
-        *(uint32_t *)(sV + (8 * g + 2 * w + 1) * ROWV + 4 * p) = (va[w] >> 16) | (vb[w] & 0xffff0000u);
+        *(uint32_t *)(sV + (8 * g + 2 * w) * ROWV + 4 * pw) = (va[w] & 0xffffu) | (vb[w] << 16);
+        *(uint32_t *)(sV + (8 * g + 2 * w + 1) * ROWV + 4 * pw) = (va[w] >> 16) | (vb[w] & 0xffff0000u);
       }
     }
   } else {
@@ -218,26 +221,27 @@ __device__ __forceinline__ void stage_store(const Staging<T, R> &st, char *sK, c
   if (tid < KTILE) sInfo[tid] = st.info;
 }
 
-template <class T, int QW>
-__global__ __launch_bounds__(64 * QW) __attribute__((amdgpu_waves_per_eu(WAVES_PER_EU))) void attention_kernel(AttnArgs a) {
+template <class T, int QW, int QT>
+__global__ __launch_bounds__(64 * QW) __attribute__((amdgpu_waves_per_eu(QT == 1 ? 3 : 2))) void attention_kernel(
+    AttnArgs a) {
   // R staging items per thread; with more than 4 waves only the first 256
-  // threads stage.
+  // threads stage. Each wave owns QT 32-query tiles.
   constexpr int NT = 64 * QW, R = QW >= 4 ? 1 : 4 / QW;
   static_assert(QW == 1 || QW == 2 || QW == 4 || QW == 8, "waves per workgroup");
+  static_assert(QT * QW <= 8, "tile codes hold 8 query chunks");
   using MF = Mfma<T>;
   typedef typename MF::frag frag;
   constexpr int ROWK = D * sizeof(T) + 16;       // K tile row bytes (key-major)
   constexpr int ROWV = KTILE * sizeof(T) + 16;   // V^T tile row bytes (d-major)
   // bf16: two buffers, tile t is computed from one while tile t+1 is stored
   // into the other, with one barrier per tile. fp32 (the validation mode,
-  // twice the bytes) keeps one buffer and a second barrier so that three
-  // workgroups fit a CU.
+  // twice the bytes) keeps one buffer and a second barrier.
   constexpr int NBUF = sizeof(T) == 2 ? 2 : 1;
   __shared__ __attribute__((aligned(16))) char sK[NBUF][KTILE * ROWK];
   __shared__ __attribute__((aligned(16))) char sV[NBUF][D * ROWV];
   __shared__ __attribute__((aligned(16))) int sInfo[NBUF][KTILE];
-  // Per key tile: for each wave, the 2-bit class of each 32-key half (bits
-  // 4w..4w+1 keys 0-31, 4w+2..4w+3 keys 32-63).
+  // Per key tile: for each 32-query chunk c of the work item, the 2-bit class
+  // of each 32-key half (bits 4c..4c+1 keys 0-31, 4c+2..4c+3 keys 32-63).
   __shared__ uint32_t sCode[ATTN_MAXKT];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -269,20 +273,24 @@ __global__ __launch_bounds__(64 * QW) __attribute__((amdgpu_waves_per_eu(WAVES_P
   const bool stager = tid < 256;
   if (kt < nkt && stager) stage_load<T, R>(st, qkv, ld, H, head, base, n, kt * KTILE, a.cos_t, a.sin_t, a.kinfo, tid);
 
-  // This lane's query, its RoPE factors and the rotated Q^T operand
-  // (B operand: column = query, k = head dim).
-  const int q = q0 + wave * 32 + lr;
-  const bool qvalid = q < n;
-  const int qq = qvalid ? q : n - 1;
-  const int qinfo = a.kinfo[base + qq];
-  const int qopt = (qinfo >> 16) - 1, qpos = qinfo & 0xffff;
+  // This lane's queries (one per query tile), their RoPE factors and the
+  // rotated Q^T operands (B operand: column = query, k = head dim).
   constexpr int NKS = D / MF::KSTEP;
-  frag qf[NKS];
-  {
-    const T *qrow = qkv + (size_t)(base + qq) * ld + head * D;
-    const float *cq = a.cos_t + (size_t)qpos * 32, *sq = a.sin_t + (size_t)qpos * 32;
+  frag qf[QT][NKS];
+  int qopt[QT], qpos[QT];
+  bool qvalid[QT];
 #pragma unroll
-    for (int ks = 0; ks < NKS; ks++) qf[ks] = *(const frag *)(qrow + ks * MF::KSTEP + lh * MF::SLOTS);
+  for (int t = 0; t < QT; t++) {
+    const int q = q0 + (wave * QT + t) * 32 + lr;
+    qvalid[t] = q < n;
+    const int qq = qvalid[t] ? q : n - 1;
+    const int qinfo = a.kinfo[base + qq];
+    qopt[t] = (qinfo >> 16) - 1;
+    qpos[t] = qinfo & 0xffff;
+    const T *qrow = qkv + (size_t)(base + qq) * ld + head * D;
+    const float *cq = a.cos_t + (size_t)qpos[t] * 32, *sq = a.sin_t + (size_t)qpos[t] * 32;
+#pragma unroll
+    for (int ks = 0; ks < NKS; ks++) qf[t][ks] = *(const frag *)(qrow + ks * MF::KSTEP + lh * MF::SLOTS);
     // Pairs (i, i+32): step ks holds i = ks*KSTEP + lh*SLOTS + u, its partner
     // is in step ks + NKS/2 at the same slot.
 #pragma unroll
@@ -294,29 +302,34 @@ __global__ __launch_bounds__(64 * QW) __attribute__((amdgpu_waves_per_eu(WAVES_P
         const float c = cq[i], sn = sq[i];
         float x, y;
         if constexpr (sizeof(T) == 2) {
-          x = (float)qf[ks][u];
-          y = (float)qf[ks + NKS / 2][u];
+          x = (float)qf[t][ks][u];
+          y = (float)qf[t][ks + NKS / 2][u];
         } else {
-          x = qf[ks];
-          y = qf[ks + NKS / 2];
+          x = qf[t][ks];
+          y = qf[t][ks + NKS / 2];
         }
         const float x2 = x * c - y * sn, y2 = y * c + x * sn;
         if constexpr (sizeof(T) == 2) {
-          qf[ks][u] = (bf16)x2;
-          qf[ks + NKS / 2][u] = (bf16)y2;
+          qf[t][ks][u] = (bf16)x2;
+          qf[t][ks + NKS / 2][u] = (bf16)y2;
         } else {
-          qf[ks] = x2;
-          qf[ks + NKS / 2] = y2;
+          qf[t][ks] = x2;
+          qf[t][ks + NKS / 2] = y2;
         }
       }
   }
 
-  f32x16 ot[2];
+  f32x16 ot[QT][2];
+  float m_run[QT], l_run[QT];
 #pragma unroll
-  for (int i = 0; i < 2; i++)
+  for (int t = 0; t < QT; t++) {
+    m_run[t] = -INFINITY;
+    l_run[t] = 0.0f;
 #pragma unroll
-    for (int e = 0; e < 16; e++) ot[i][e] = 0.0f;
-  float m_run = -INFINITY, l_run = 0.0f;
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+      for (int e = 0; e < 16; e++) ot[t][i][e] = 0.0f;
+  }
 
   __syncthreads();  // sCode visible
   auto next_tile = [&](int kt) {
@@ -335,42 +348,60 @@ __global__ __launch_bounds__(64 * QW) __attribute__((amdgpu_waves_per_eu(WAVES_P
     if (kn < nkt && stager) stage_load<T, R>(st, qkv, ld, H, head, base, n, kn * KTILE, a.cos_t, a.sin_t, a.kinfo, tid);
     __syncthreads();
   }
+  const unsigned win2 = a.sliding ? (unsigned)(2 * a.half_window) : 0xffffffffu;
   while (kt < nkt) {
     const int k0 = kt * KTILE;
     const char *sKb = sK[b], *sVb = sV[b];
     const int *sInfob = sInfo[b];
-    // This wave's classes of the two halves (uniform across the wave).
-    const int mycode = __builtin_amdgcn_readfirstlane((sCode[kt] >> (4 * wave)) & 15);
-    const int hcls[2] = {mycode & 3, mycode >> 2};
+    // This wave's classes: per query tile t and 32-key half i (uniform
+    // across the wave).
+    const int mycode =
+        __builtin_amdgcn_readfirstlane((sCode[kt] >> (4 * QT * wave)) & ((1u << (4 * QT)) - 1));
+    int hcls[QT][2];
+#pragma unroll
+    for (int t = 0; t < QT; t++) {
+      hcls[t][0] = (mycode >> (4 * t)) & 3;
+      hcls[t][1] = (mycode >> (4 * t + 2)) & 3;
+    }
 
     if (mycode != 0) {
-      // S^T = K . Q^T for 64 keys x 32 queries (two 32x32 tiles); a half with
-      // no allowed pair is skipped here and in P.V, and scores -inf.
-      f32x16 sT[2];
+      // S^T = K . Q^T per query tile for 64 keys (two 32x32 tiles); a K
+      // fragment read from LDS feeds every query tile that needs its half.
+      f32x16 sT[QT][2];
 #pragma unroll
-      for (int i = 0; i < 2; i++)
+      for (int t = 0; t < QT; t++)
 #pragma unroll
-        for (int e = 0; e < 16; e++) sT[i][e] = hcls[i] ? 0.0f : -INFINITY;
+        for (int i = 0; i < 2; i++)
+#pragma unroll
+          for (int e = 0; e < 16; e++) sT[t][i][e] = hcls[t][i] ? 0.0f : -INFINITY;
 #pragma unroll
       for (int i = 0; i < 2; i++) {
-        if (hcls[i] == 0) continue;
+        int any = 0;
+#pragma unroll
+        for (int t = 0; t < QT; t++) any |= hcls[t][i];
+        if (any == 0) continue;
 #pragma unroll
         for (int ks = 0; ks < NKS; ks++) {
           const int kof = (ks * MF::KSTEP + lh * MF::SLOTS) * (int)sizeof(T);
           frag kf = *(const frag *)(sKb + (i * 32 + lr) * ROWK + kof);
-          sT[i] = MF::mma(kf, qf[ks], sT[i]);
+#pragma unroll
+          for (int t = 0; t < QT; t++)
+            if (hcls[t][i]) sT[t][i] = MF::mma(kf, qf[t][ks], sT[t][i]);
         }
       }
 
-      // Mask and running max on the raw scores; the softmax scale (times
-      // log2 e, > 0) is applied inside the exponent: p = 2^(s*c - m*c).
-      // The per-element test is branch-free (bitwise and + select).
-      const unsigned win2 = a.sliding ? (unsigned)(2 * a.half_window) : 0xffffffffu;
+      // Per query tile: mask and running max on the raw scores; the softmax
+      // scale (times log2 e, > 0) is applied inside the exponent:
+      // p = 2^(s*c - m*c). The per-element test is branch-free (bitwise and +
+      // select).
 #pragma unroll
-      for (int i = 0; i < 2; i++) {
-        if (hcls[i] != 2) continue;
+      for (int t = 0; t < QT; t++) {
+        if ((hcls[t][0] | hcls[t][1]) == 0) continue;
 #pragma unroll
-        for (int g = 0; g < 4; g++) {
+        for (int i = 0; i < 2; i++) {
+          if (hcls[t][i] != 2) continue;
+#pragma unroll
+          for (int g = 0; g < 4; g++) {
             const int kl = i * 32 + 8 * g + 4 * lh;  // 4 consecutive keys kl..kl+3
             const int4 inf4 = *(const int4 *)(sInfob + kl);
             const int inf[4] = {inf4.x, inf4.y, inf4.z, inf4.w};
@@ -380,72 +411,80 @@ __global__ __launch_bounds__(64 * QW) __attribute__((amdgpu_waves_per_eu(WAVES_P
               // sees prefix keys and its own option, i.e. ko in {-1, qopt}.
               // Window: |kpos - qpos| <= W on local layers.
               const int ko = (inf[u] >> 16) - 1, kp = inf[u] & 0xffff;
-              const bool ok = (k0 + kl + u < n) & ((ko == -1) | (ko == qopt)) &
-                              ((unsigned)(kp - qpos + a.half_window) <= win2);
-              sT[i][4 * g + u] = ok ? sT[i][4 * g + u] : -INFINITY;
+              const bool ok = (k0 + kl + u < n) & ((ko == -1) | (ko == qopt[t])) &
+                              ((unsigned)(kp - qpos[t] + a.half_window) <= win2);
+              sT[t][i][4 * g + u] = ok ? sT[t][i][4 * g + u] : -INFINITY;
             }
+          }
         }
-      }
-      float mx = -INFINITY;
-#pragma unroll
-      for (int i = 0; i < 2; i++)
-#pragma unroll
-        for (int e = 0; e < 16; e++) mx = fmaxf(mx, sT[i][e]);
-      mx = fmaxf(mx, __shfl_xor(mx, 32));
-      const float m_new = fmaxf(m_run, mx);
-      const float m_use = m_new == -INFINITY ? 0.0f : m_new;
-      const float c = a.scale_log2, mc = -m_use * c;
-      const float alpha = __builtin_amdgcn_exp2f((m_run - m_use) * c);
-      float psum = 0.0f;
-#pragma unroll
-      for (int i = 0; i < 2; i++) {
-        if (hcls[i] == 0) continue;  // all -inf: p = 0, and P.V skips the half
-#pragma unroll
-        for (int e = 0; e < 16; e++) {
-          const float p = __builtin_amdgcn_exp2f(fmaf(sT[i][e], c, mc));
-          sT[i][e] = p;
-          psum += p;
-        }
-      }
-      l_run = l_run * alpha + psum;
-      m_run = m_new;
-      if (__ballot(alpha != 1.0f)) {  // no lane's maximum moved: nothing to rescale
+        float mx = -INFINITY;
 #pragma unroll
         for (int i = 0; i < 2; i++)
 #pragma unroll
-          for (int e = 0; e < 16; e++) ot[i][e] *= alpha;
+          for (int e = 0; e < 16; e++) mx = fmaxf(mx, sT[t][i][e]);
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        const float m_new = fmaxf(m_run[t], mx);
+        const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+        const float c = a.scale_log2, mc = -m_use * c;
+        const float alpha = __builtin_amdgcn_exp2f((m_run[t] - m_use) * c);
+        float psum = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+          if (hcls[t][i] == 0) continue;  // all -inf: p = 0, and P.V skips the half
+#pragma unroll
+          for (int e = 0; e < 16; e++) {
+            const float p = __builtin_amdgcn_exp2f(fmaf(sT[t][i][e], c, mc));
+            sT[t][i][e] = p;
+            psum += p;
+          }
+        }
+        l_run[t] = l_run[t] * alpha + psum;
+        m_run[t] = m_new;
+        if (__ballot(alpha != 1.0f)) {  // no lane's maximum moved: nothing to rescale
+#pragma unroll
+          for (int i = 0; i < 2; i++)
+#pragma unroll
+            for (int e = 0; e < 16; e++) ot[t][i][e] *= alpha;
+        }
       }
 
       // O^T += V^T . P^T. k step ks covers accumulator registers
       // [ks*SLOTS, ks*SLOTS + SLOTS) of the flattened S^T tiles; accumulator r
-      // of tile i on lane half lh is key 32*i + 8*((r%16)/4) + 4*lh + r%4.
+      // of tile i on lane half lh is key 32*i + 8*((r%16)/4) + 4*lh + r%4. A V
+      // fragment read from LDS feeds every query tile that needs its half.
       constexpr int NPV = KTILE / MF::KSTEP;
 #pragma unroll
       for (int ks = 0; ks < NPV; ks++) {
-        if (hcls[ks / (NPV / 2)] == 0) continue;
-        frag pf;
-        if constexpr (sizeof(T) == 2) {
-          const int ti = ks >> 1, r0 = (ks & 1) * 8;
+        const int half = ks / (NPV / 2);
+        int any = 0;
 #pragma unroll
-          for (int u = 0; u < 8; u++) pf[u] = (bf16)sT[ti][r0 + u];
-        } else {
-          pf = sT[ks >> 4][ks & 15];
+        for (int t = 0; t < QT; t++) any |= hcls[t][half];
+        if (any == 0) continue;
+        frag pf[QT];
+#pragma unroll
+        for (int t = 0; t < QT; t++) {
+          if constexpr (sizeof(T) == 2) {
+            const int ti = ks >> 1, r0 = (ks & 1) * 8;
+#pragma unroll
+            for (int u = 0; u < 8; u++) pf[t][u] = (bf16)sT[t][ti][r0 + u];
+          } else {
+            pf[t] = sT[t][ks >> 4][ks & 15];
+          }
         }
 #pragma unroll
         for (int i = 0; i < 2; i++) {
           const char *vrow = sVb + (i * 32 + lr) * ROWV;
           frag vf;
           if constexpr (sizeof(T) == 2) {
-            const int kb = 32 * (ks >> 1) + 16 * (ks & 1) + 4 * lh;
-            bf16x4 lo = *(const bf16x4 *)(vrow + kb * 2);
-            bf16x4 hi = *(const bf16x4 *)(vrow + (kb + 8) * 2);
-            vf = (bf16x8){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+            vf = *(const frag *)(vrow + 32 * ks + 16 * lh);  // keys 16ks + {4lh..4lh+3, 8+4lh..8+4lh+3}
           } else {
             const int r = ks & 15;
             const int key = 32 * (ks >> 4) + 8 * (r >> 2) + 4 * lh + (r & 3);
             vf = *(const float *)(vrow + key * 4);
           }
-          ot[i] = MF::mma(vf, pf, ot[i]);
+#pragma unroll
+          for (int t = 0; t < QT; t++)
+            if (hcls[t][half]) ot[t][i] = MF::mma(vf, pf[t], ot[t][i]);
         }
       }
     }
@@ -465,37 +504,42 @@ __global__ __launch_bounds__(64 * QW) __attribute__((amdgpu_waves_per_eu(WAVES_P
   }
 
   // Normalise and store ctx[token][head*64 + d].
-  const float l_tot = l_run + __shfl_xor(l_run, 32);
-  const float inv = 1.0f / l_tot;
-  if (qvalid) {
-    T *out = (T *)a.ctx + (size_t)(base + q) * H + head * D;
 #pragma unroll
-    for (int i = 0; i < 2; i++)
+  for (int t = 0; t < QT; t++) {
+    const float l_tot = l_run[t] + __shfl_xor(l_run[t], 32);
+    const float inv = 1.0f / l_tot;
+    if (qvalid[t]) {
+      const int q = q0 + (wave * QT + t) * 32 + lr;
+      T *out = (T *)a.ctx + (size_t)(base + q) * H + head * D;
 #pragma unroll
-      for (int g = 0; g < 4; g++) {
-        const int d0 = i * 32 + 8 * g + 4 * lh;
-        if constexpr (sizeof(T) == 2) {
-          bf16x4 o = {(bf16)(ot[i][4 * g] * inv), (bf16)(ot[i][4 * g + 1] * inv), (bf16)(ot[i][4 * g + 2] * inv),
-                      (bf16)(ot[i][4 * g + 3] * inv)};
-          *(bf16x4 *)(out + d0) = o;
-        } else {
-          *(float4 *)(out + d0) = make_float4(ot[i][4 * g] * inv, ot[i][4 * g + 1] * inv, ot[i][4 * g + 2] * inv,
-                                              ot[i][4 * g + 3] * inv);
+      for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+          const int d0 = i * 32 + 8 * g + 4 * lh;
+          if constexpr (sizeof(T) == 2) {
+            bf16x4 o = {(bf16)(ot[t][i][4 * g] * inv), (bf16)(ot[t][i][4 * g + 1] * inv),
+                        (bf16)(ot[t][i][4 * g + 2] * inv), (bf16)(ot[t][i][4 * g + 3] * inv)};
+            *(bf16x4 *)(out + d0) = o;
+          } else {
+            *(float4 *)(out + d0) = make_float4(ot[t][i][4 * g] * inv, ot[t][i][4 * g + 1] * inv,
+                                                ot[t][i][4 * g + 2] * inv, ot[t][i][4 * g + 3] * inv);
+          }
         }
-      }
+    }
   }
 }
 
-// Tile classes of one work item (32 * QW queries of one sequence) for one
-// layer type: for every 64-key tile and wave w, the 2-bit class (0 none, 1
-// all, 2 per-element) of each 32-key half against the wave's 32-query chunk,
-// packed as bits 4w..4w+3; and the first tile with any allowed pair (nkt if
-// none). The classes depend only on the batch layout and the layer type, so
-// every layer of that type reuses them.
-template <int QW>
+// Tile classes of one work item (32 * NC queries of one sequence) for one
+// layer type: for every 64-key tile and 32-query chunk c, the 2-bit class (0
+// none, 1 all, 2 per-element) of each 32-key half against the chunk, packed
+// as bits 4c..4c+3; and the first tile with any allowed pair (nkt if none).
+// The classes depend only on the batch layout and the layer type, so every
+// layer of that type reuses them.
+template <int NC>
 __global__ __launch_bounds__(64) void tile_codes_kernel(const ChunkInfo *chunks, const int4 *work, const int *seq_len,
                                                         const int *chunk_off, int sliding, int half_window,
                                                         uint32_t *codes, int *first) {
+  static_assert(NC <= 8, "32-bit codes");
   __shared__ int s_first;
   const int wi = blockIdx.x, tid = threadIdx.x;
   const int4 wk = work[wi];
@@ -505,9 +549,9 @@ __global__ __launch_bounds__(64) void tile_codes_kernel(const ChunkInfo *chunks,
   if (tid == 0) s_first = nkt;
   __syncthreads();
   const ChunkInfo empty = {0, 0, 1, 0, 0, 0, 0, 0};
-  ChunkInfo qc[QW];
+  ChunkInfo qc[NC];
 #pragma unroll
-  for (int w = 0; w < QW; w++) {
+  for (int w = 0; w < NC; w++) {
     const int c = q0 / 32 + w;
     qc[w] = c < nch ? chunks[cbase + c] : empty;
   }
@@ -516,7 +560,7 @@ __global__ __launch_bounds__(64) void tile_codes_kernel(const ChunkInfo *chunks,
     const ChunkInfo kc1 = (2 * kt + 1 < nch) ? chunks[cbase + 2 * kt + 1] : empty;
     uint32_t code = 0;
 #pragma unroll
-    for (int w = 0; w < QW; w++)
+    for (int w = 0; w < NC; w++)
       code |= (uint32_t)(tile_class(qc[w], kc0, sliding, half_window) |
                          (tile_class(qc[w], kc1, sliding, half_window) << 2))
               << (4 * w);
@@ -565,16 +609,16 @@ hipError_t launch_attention(int precision, const AttnArgs &a, hipStream_t s) {
   if (a.nwork <= 0) return hipSuccess;
   dim3 grid(a.nwork * a.heads), block(64 * ATTN_WAVES);
   if (precision == 1)
-    hipLaunchKernelGGL((attention_kernel<bf16, ATTN_WAVES>), grid, block, 0, s, a);
+    hipLaunchKernelGGL((attention_kernel<bf16, ATTN_WAVES, ATTN_QT>), grid, block, 0, s, a);
   else
-    hipLaunchKernelGGL((attention_kernel<float, ATTN_WAVES>), grid, block, 0, s, a);
+    hipLaunchKernelGGL((attention_kernel<float, ATTN_WAVES, ATTN_QT>), grid, block, 0, s, a);
   return hipGetLastError();
 }
 
 hipError_t launch_tile_codes(const ChunkInfo *chunks, const int4 *work, const int *seq_len, const int *chunk_off,
                              int nwork, int sliding, int half_window, uint32_t *codes, int *first, hipStream_t s) {
   if (nwork <= 0) return hipSuccess;
-  hipLaunchKernelGGL(tile_codes_kernel<ATTN_WAVES>, dim3(nwork), dim3(64), 0, s, chunks, work, seq_len, chunk_off,
+  hipLaunchKernelGGL(tile_codes_kernel<ATTN_WAVES * ATTN_QT>, dim3(nwork), dim3(64), 0, s, chunks, work, seq_len, chunk_off,
                      sliding, half_window, codes, first);
   return hipGetLastError();
 }

@@ -100,9 +100,16 @@ enum { EPI_F32 = 0, EPI_STORE = 1, EPI_GEGLU = 2 };
 hipError_t launch_gemm(int precision, int epi, const GemmArgs &a, hipStream_t s);
 bool gemm_shape_ok(int precision, int N, int K);
 
-// Attention work item: 32 * ATTN_WAVES queries of one sequence (one wave per
-// 32 queries), for every head.
+// Attention work item: 32 * ATTN_QT * ATTN_WAVES queries of one sequence
+// (each wave owns ATTN_QT tiles of 32 queries), for every head. ATTN_QT = 2
+// halves the LDS fragment reads per MFMA but needs 250 VGPRs (2 waves per
+// SIMD instead of 3); measured slower (cfg3 local layers 90 -> 111 us), so 1.
 constexpr int ATTN_WAVES = 4;
+#ifndef ATTN_QT_SETTING
+#define ATTN_QT_SETTING 1
+#endif
+constexpr int ATTN_QT = ATTN_QT_SETTING;
+constexpr int ATTN_QUERIES = 32 * ATTN_QT * ATTN_WAVES;
 // Key tiles (64 keys) per sequence: sequences up to 8192 tokens.
 constexpr int ATTN_MAXKT = 128;
 
