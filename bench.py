@@ -9,6 +9,7 @@ seeded token ids; see decide_amd/synth.py.
 
   python bench.py [--steps K] [--warmup W] [--config cfg3] [--precision bf16]
   python bench.py --systemone [--steps K]   one SystemOne call, batched vs serial
+  python bench.py --tokenizer               host tokenizer throughput (CPU only)
 """
 from __future__ import annotations
 
@@ -180,6 +181,102 @@ def systemone(args) -> int:
     return 0
 
 
+def synthetic_prose(seed: int, n_docs: int, doc_words: int):
+    """Pseudo-English documents: syllable words, capitals, digits,
+    punctuation, contractions, some accented words and line breaks."""
+    import random
+
+    rng = random.Random(seed)
+    syl = ["ta", "ke", "ri", "on", "mar", "sel", "ing", "pre", "con", "tion", "ab", "ly", "de", "ver", "st", "ou",
+           "fi", "na", "lo", "gu", "ment", "er", "qu", "ist", "re", "ca", "pol", "ex", "un", "im"]
+    extra = ["don't", "it's", "we're", "café", "naïve", "2026", "1,234.56", "(approx.)", "e.g.", "--", "%"]
+    docs = []
+    for _ in range(n_docs):
+        words = []
+        for i in range(doc_words):
+            if rng.random() < 0.05:
+                w = rng.choice(extra)
+            else:
+                w = "".join(rng.choice(syl) for _ in range(rng.randint(1, 4)))
+                if rng.random() < 0.1:
+                    w = w.capitalize()
+            words.append(w + (rng.choice([",", ".", ":", "?"]) if rng.random() < 0.08 else ""))
+            if rng.random() < 0.02:
+                words.append("\n")
+        docs.append(" ".join(words))
+    return docs
+
+
+def tokenizer_bench(args) -> int:
+    """Host tokenizer throughput (dn_tokenize, one thread) on a byte-level BPE
+    vocabulary of 8000 trained here, against HuggingFace `tokenizers` (one
+    thread) and the oracle's pure-Python restatement. Prints one JSON line."""
+    os.environ["TOKENIZERS_PARALLELISM"] = "false"
+    from tokenizers import AddedToken, Tokenizer as HFTokenizer, models, normalizers, pre_tokenizers, processors, \
+        trainers
+
+    import oracle.tokenizer as ot
+    from decide_amd.tokenizer import Tokenizer
+
+    hf = HFTokenizer(models.BPE())
+    hf.normalizer = normalizers.NFC()
+    hf.pre_tokenizer = pre_tokenizers.ByteLevel(add_prefix_space=False, use_regex=True)
+    hf.train_from_iterator(synthetic_prose(1, 4000, 200), trainers.BpeTrainer(
+        vocab_size=8000, initial_alphabet=pre_tokenizers.ByteLevel.alphabet(), show_progress=False))
+    hf.add_special_tokens([AddedToken(t, special=True, normalized=False, lstrip=(t == "[MASK]"))
+                           for t in ("[CLS]", "[SEP]", "[MASK]", "[PAD]", "[UNK]")])
+    hf.post_processor = processors.TemplateProcessing(
+        single="[CLS] $A [SEP]", special_tokens=[("[CLS]", hf.token_to_id("[CLS]")), ("[SEP]", hf.token_to_id("[SEP]"))])
+    raw = hf.to_str().encode()
+    tok = Tokenizer.parse(raw)
+    docs = synthetic_prose(2, 400, 400)
+    nbytes = sum(len(d.encode()) for d in docs)
+
+    def timed(fn, budget):
+        n_tok, secs, k = 0, 0.0, 0
+        while secs < budget:
+            d = docs[k % len(docs)]
+            t0 = time.perf_counter()
+            n_tok += len(fn(d))
+            secs += time.perf_counter() - t0
+            k += 1
+        return n_tok / secs, k, secs
+
+    for d in docs:  # warm the word caches once (both implementations keep one)
+        tok.encode(d)
+        hf.encode(d)
+    lib_tps, lib_docs, lib_s = timed(tok.encode, 3.0)
+    hf_tps, _, _ = timed(lambda d: hf.encode(d).ids, 3.0)
+    orc = ot.Tokenizer(raw)
+    orc_tps, orc_docs, orc_s = timed(orc.encode, args.cpu_budget / 2)
+    same = all(tok.encode(d) == hf.encode(d).ids for d in docs[:50])
+    avg_bytes_per_tok = nbytes / sum(len(tok.encode(d)) for d in docs)
+    result = {
+        "metric": "host tokenizer throughput: byte-level BPE (NFC, GPT-2 pre-tokenizer), vocab 8000, one thread",
+        "value": round(lib_tps, 1),
+        "unit": "tokens/s",
+        "n_gpus": 0,
+        "steps": lib_docs,
+        "warmup": len(docs),
+        "ms_per_step": round(lib_s * 1e3 / lib_docs, 4),
+        "higher_is_better": True,
+        "scaling": "strong",
+        "vs_baseline": None,
+        "dtype": "u8",
+        "data": "synthetic pseudo-English documents of 400 words (bench.py synthetic_prose), vocabulary trained "
+                "here with HuggingFace tokenizers",
+        "config": {"workload": "tokenize 400 documents (%d bytes) one at a time" % nbytes, "vocab": 8000},
+        "mb_per_s": round(lib_tps * avg_bytes_per_tok / 1e6, 2),
+        "huggingface_tokenizers_tokens_per_s": round(hf_tps, 1),
+        "ids_equal_huggingface": same,
+        "cpu_baseline": {"value": round(orc_tps, 1), "unit": "tokens/s", "cores": 1, "kind": "port",
+                         "sample": f"{orc_docs} documents, {orc_s:.1f} s; the oracle's pure-Python restatement of "
+                                   "internal/tokenizer/tokenizer.go"},
+    }
+    print(json.dumps(result), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -192,6 +289,8 @@ def main() -> int:
     ap.add_argument("--probe-layer", type=int, default=1)
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="run one device copy of MIB MiB first (reference kernel for HBM counters)")
+    ap.add_argument("--tokenizer", action="store_true",
+                    help="time the host tokenizer (dn_tokenize) against HuggingFace tokenizers; no GPU")
     ap.add_argument("--systemone", action="store_true",
                     help="time one SystemOne call (24 questions) batched into one forward vs one forward each")
     args = ap.parse_args()
@@ -200,6 +299,8 @@ def main() -> int:
               "(the forward shards by sequence with no collective; see DESIGN.md)", file=sys.stderr)
         return 2
 
+    if args.tokenizer:
+        return tokenizer_bench(args)
     if args.systemone:
         return systemone(args)
 

@@ -119,28 +119,25 @@ def read_meta(bundle_dir: str) -> dict:
     return meta
 
 
-def hf_encoder(tokenizer_json: str) -> Tuple[Callable[[str], Sequence[int]], int]:
-    """Encode(text, addSpecial=True) and the [MASK] id from a HuggingFace
-    tokenizer.json via the ``tokenizers`` package (the library whose output
-    the reference's Go tokenizer is tested against, tokenizer_test.go:11-38)."""
-    from tokenizers import Tokenizer  # optional dependency of bundle loading only
+def bundle_encoder(tokenizer_json: str) -> Tuple[Callable[[str], Sequence[int]], int]:
+    """Encode(text, addSpecial=True) and the [MASK] id of a bundle's
+    tokenizer.json, through the library's host tokenizer (dn_tokenizer_*)."""
+    from .tokenizer import Tokenizer
 
-    tok = Tokenizer.from_file(tokenizer_json)
-    mask = tok.token_to_id("[MASK]")
-    if mask is None:
-        raise ValueError("tokenizer: missing [CLS]/[SEP]/[MASK] added tokens")
-    return (lambda text: tok.encode(text, add_special_tokens=True).ids), int(mask)
+    tok = Tokenizer.load(tokenizer_json)
+    return tok.encode, tok.mask_id
 
 
 def load_bundle(bundle_dir: str, precision: str = "bf16", device: int = 0,
                 encoder: Optional[Tuple[Callable[[str], Sequence[int]], int]] = None) -> Local:
     """bundle.Load (bundle.go:95-125) onto the device: a Local whose weights are
-    resident. ``encoder`` = (encode, mask_id) overrides tokenizer.json."""
+    resident and whose tokenizer is the bundle's tokenizer.json.
+    ``encoder`` = (encode, mask_id) replaces that tokenizer."""
     meta = read_meta(bundle_dir)
     cfg = nn.load_config(os.path.join(bundle_dir, "config.json"))
     engine = nn.Engine(cfg, precision=precision, device=device)
     upload_weights(engine, os.path.join(bundle_dir, "model.safetensors"))
-    encode, mask_id = encoder if encoder is not None else hf_encoder(os.path.join(bundle_dir, "tokenizer.json"))
+    encode, mask_id = encoder if encoder is not None else bundle_encoder(os.path.join(bundle_dir, "tokenizer.json"))
     cal = meta.get("calibration") or {}
     return Local(engine, encode, mask_id, model_id=meta.get("model_id") or "decide-0.2.0",
                  independent_options=bool(meta.get("independent_options", False)),

@@ -41,6 +41,11 @@ thread_local std::string g_err;  // errors without a context
 
 }  // namespace
 
+int set_host_error(int code, const std::string &msg) {
+  g_err = msg;
+  return code;
+}
+
 struct dn_ctx {
   int device = 0;
   hipStream_t stream = nullptr;

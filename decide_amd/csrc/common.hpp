@@ -4,6 +4,12 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <string>
+
+// Records msg as the error of calls made without a context (dn_last_error(NULL))
+// and returns code.
+int set_host_error(int code, const std::string &msg);
+
 typedef __bf16 bf16;
 typedef bf16 bf16x8 __attribute__((__vector_size__(8 * sizeof(bf16))));
 typedef bf16 bf16x4 __attribute__((__vector_size__(4 * sizeof(bf16))));

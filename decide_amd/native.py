@@ -69,6 +69,12 @@ _SIGS = {
     "dn_answer": ([_f64p, _i, _c.c_double, _f64p, _c.POINTER(_i), _c.POINTER(_c.c_double)], _i),
     "dn_round": ([_c.c_double, _i], _c.c_double),
     "dn_evaluate": ([_vp, _i, _vp, _vp, _vp, _vp, _f64p, _c.c_int32, _i, _f64p, _vp, _f64p, _f64p], _i),
+    "dn_tokenizer_parse": ([_vp, _c.c_int64, _c.POINTER(_vp)], _i),
+    "dn_tokenizer_free": ([_vp], None),
+    "dn_tokenizer_special_ids": ([_vp, _vp, _vp, _vp, _vp], _i),
+    "dn_tokenize": ([_vp, _vp, _c.c_int64, _i, _vp, _c.c_int64, _c.POINTER(_c.c_int64)], _i),
+    "dn_pretokenize": ([_vp, _c.c_int64, _vp, _c.c_int64, _c.POINTER(_c.c_int64)], _i),
+    "dn_nfc": ([_vp, _c.c_int64, _vp, _c.c_int64, _c.POINTER(_c.c_int64)], _i),
 }
 for _name, (_args, _res) in _SIGS.items():
     _fn = getattr(lib, _name)

@@ -214,6 +214,42 @@ int dn_evaluate(dn_ctx *ctx, int nq, const int32_t *kind, const int32_t *n_opt, 
                 const int32_t *ids, const double *temperature, int32_t mask_id, int independent, double *probs,
                 int32_t *choice, double *confidence, double *value);
 
+/* ---- host tokenizer (internal/tokenizer/tokenizer.go) ------------------ */
+
+/* ModernBERT's byte-level BPE tokenizer: NFC, the GPT-2 pre-tokenizer,
+ * added tokens, [CLS] $A [SEP]. Host code only; a tokenizer is safe for
+ * concurrent use (as tokenizer.Tokenizer is). Errors are reported through
+ * dn_last_error(NULL). */
+typedef struct dn_tokenizer dn_tokenizer;
+
+/* Parses tokenizer.json contents (len bytes). Replaces tokenizer.Parse
+ * (internal/tokenizer/tokenizer.go:60-130): BPE models only; merges as
+ * ["a","b"] pairs or "a b" strings, the first occurrence of a pair keeping
+ * its rank; special, non-normalized added tokens match the raw text, the
+ * others the normalized text; [CLS], [SEP] and [MASK] must exist. */
+int dn_tokenizer_parse(const char *json, int64_t len, dn_tokenizer **out);
+
+void dn_tokenizer_free(dn_tokenizer *tok);
+
+/* Ids of [CLS], [SEP], [MASK] and [PAD] (Tokenizer.ClsID / SepID / MaskID,
+ * tokenizer.go:40-50); any pointer may be NULL. */
+int dn_tokenizer_special_ids(const dn_tokenizer *tok, int32_t *cls, int32_t *sep, int32_t *mask, int32_t *pad);
+
+/* Tokenizer.Encode (tokenizer.go:133-160) of len bytes of UTF-8 text, with
+ * [CLS] ... [SEP] when add_special. *n receives the id count; the ids are
+ * written when it is <= cap, else DN_INVALID_ARG (call again with *n). */
+int dn_tokenize(dn_tokenizer *tok, const char *text, int64_t len, int add_special, int32_t *ids, int64_t cap,
+                int64_t *n);
+
+/* preTokenize (tokenizer.go:214-272): the pieces of text under the GPT-2
+ * split rule, as end offsets into the text (invalid UTF-8 bytes count as
+ * U+FFFD, three bytes, as Go's []rune conversion makes them). */
+int dn_pretokenize(const char *text, int64_t len, int64_t *ends, int64_t cap, int64_t *n);
+
+/* Unicode NFC of UTF-8 text (norm.NFC.String in Encode, tokenizer.go:147),
+ * invalid bytes passed through; same output-capacity convention. */
+int dn_nfc(const char *text, int64_t len, char *out, int64_t cap, int64_t *n);
+
 #ifdef __cplusplus
 }
 #endif

@@ -15,6 +15,7 @@ import numpy as np
 import pytest
 
 import oracle
+import oracle.tokenizer
 from test_local import MIN_MASK, byte_encode
 
 pytestmark = pytest.mark.gpu
@@ -60,6 +61,7 @@ def bundles(tmp_path_factory):
             json.dump({"name": "decide", "model_id": "decide-test-0", "format": 1, "independent_options": True,
                        "max_tokens": 8192, "calibration": CAL}, fh)
         bundle.write_safetensors(str(d / "model.safetensors"), w, dtype=dt, metadata={"format": "pt"})
+        (d / "tokenizer.json").write_bytes(oracle.tokenizer.minimal_json())
         stored, _ = bundle.read_safetensors(str(d / "model.safetensors"))
         wf = {k: bundle.to_float32(*stored[k][::2]).reshape(stored[k][1]) for k in w}
         out[dt] = (str(d), cfg, oracle.OracleModel(cfg, wf))
@@ -207,3 +209,19 @@ def test_evaluate_errors(bundles):
     r = loc.system_one("s", [("q", Noul("i"))])
     assert 0 <= r["answers"]["q"]["noul"] <= 1
     loc.engine.close()
+
+
+def test_system_one_with_bundle_tokenizer(bundles):
+    """load_bundle without an encoder tokenizes with the library's tokenizer
+    (the bundle's tokenizer.json, here tokenizer.MinimalJSON): the same
+    answers as with the test's byte-level encoder."""
+    from decide_amd import bundle
+
+    d, _, _ = bundles["F32"]
+    qs = questions()
+    a = bundle.load_bundle(d, precision="fp32")
+    b = bundle.load_bundle(d, precision="fp32", encoder=(byte_encode, MIN_MASK))
+    assert a.mask_id == MIN_MASK
+    assert a.system_one(STATE, qs)["answers"] == b.system_one(STATE, qs)["answers"]
+    a.engine.close()
+    b.engine.close()
