@@ -164,7 +164,13 @@ void define_tensors(dn_ctx *c) {
   add("scorer.out_proj.bias", 1);
 }
 
-const void *W(dn_ctx *c, const std::string &name) { return c->w[name].buf.p; }
+// Device pointer of an uploaded weight (check_ready has verified that every
+// tensor of the configured model is set; a name outside the model is a bug
+// here, not an input error, and gives a null pointer rather than a new slot).
+const void *W(dn_ctx *c, const std::string &name) {
+  auto it = c->w.find(name);
+  return it == c->w.end() ? nullptr : it->second.buf.p;
+}
 
 // Batch layout: sequence offsets, 32-token chunks and ATTN_QUERIES-query work items.
 int prepare_layout(dn_ctx *c, int nseq, const int32_t *seq_len) {
