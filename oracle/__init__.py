@@ -9,6 +9,7 @@ Every function restates reference code; the citations are in oracle.cpp.
 from __future__ import annotations
 
 import ctypes
+import math
 import os
 import subprocess
 
@@ -52,10 +53,31 @@ def lib():
         L.orc_forward.argtypes = [ctypes.c_void_p, ctypes.c_int, _i32p, _i32p, _i32p, _i32p, _u8p, _i32p, _i32p,
                                   _f32p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]
         L.orc_forward.restype = ctypes.c_int
+        L.orc_forward_train.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, _i32p, _i32p, _i32p, _i32p, _u8p,
+                                        _i32p, _i32p, _f32p]
+        L.orc_forward_train.restype = ctypes.c_int
+        L.orc_backward.argtypes = [ctypes.c_void_p, _f32p, ctypes.c_void_p, ctypes.c_int]
+        L.orc_backward.restype = ctypes.c_int
+        L.orc_model_zero_like.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+        L.orc_model_get.argtypes = [ctypes.c_void_p, ctypes.c_char_p, _f32p, ctypes.c_int64]
+        L.orc_model_get.restype = ctypes.c_int
+        L.orc_adamw_new.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_float, ctypes.c_int, ctypes.c_int,
+                                    ctypes.c_int]
+        L.orc_adamw_new.restype = ctypes.c_void_p
+        L.orc_adamw_free.argtypes = [ctypes.c_void_p]
+        L.orc_adamw_grad_norm.argtypes = [ctypes.c_void_p]
+        L.orc_adamw_grad_norm.restype = ctypes.c_double
+        L.orc_adamw_update.argtypes = [ctypes.c_void_p, ctypes.c_float, ctypes.c_float, ctypes.c_float]
+        L.orc_adamw_get.argtypes = [ctypes.c_void_p, ctypes.c_char_p, ctypes.c_int, _f32p, ctypes.c_int64]
+        L.orc_adamw_get.restype = ctypes.c_int
         L.orc_layer_norm.argtypes = [_f32p, _f32p, ctypes.c_int, ctypes.c_int, _f32p, ctypes.c_void_p,
                                      ctypes.c_float]
         L.orc_gelu.argtypes = [ctypes.c_float]
         L.orc_gelu.restype = ctypes.c_float
+        L.orc_gelu_grad.argtypes = [ctypes.c_float]
+        L.orc_gelu_grad.restype = ctypes.c_float
+        L.orc_apply_rope_inverse.argtypes = [_f32p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, _f32p,
+                                             _f32p]
         L.orc_rope_tables.argtypes = [_i32p, ctypes.c_int, ctypes.c_int, ctypes.c_double, _f32p, _f32p]
         L.orc_apply_rope.argtypes = [_f32p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, _f32p, _f32p]
         L.orc_softmax_masked.argtypes = [_f32p, ctypes.c_int, ctypes.c_float, ctypes.c_void_p]
@@ -125,9 +147,8 @@ class OracleModel:
             lib().orc_model_free(self._h)
             self._h = None
 
-    def forward(self, batch, debug: bool = False):
-        """batch: list of objects with ids, pos, opt (None = plain), mask_pos."""
-        cfg = self.cfg
+    @staticmethod
+    def _flat(batch):
         seq_len = np.array([len(s.ids) for s in batch], np.int32)
         ids = np.concatenate([np.asarray(s.ids, np.int32) for s in batch]).astype(np.int32)
         pos = np.concatenate([np.asarray(s.pos, np.int32) for s in batch]).astype(np.int32)
@@ -139,6 +160,12 @@ class OracleModel:
         mp = np.ascontiguousarray(mp, dtype=np.int32)
         if mp.size == 0:
             mp = np.zeros(1, np.int32)
+        return seq_len, ids, pos, opt, has_opt, nmask, mp
+
+    def forward(self, batch, debug: bool = False):
+        """batch: list of objects with ids, pos, opt (None = plain), mask_pos."""
+        cfg = self.cfg
+        seq_len, ids, pos, opt, has_opt, nmask, mp = self._flat(batch)
         R = int(nmask.sum())
         T = int(seq_len.sum())
         logits = np.zeros(max(R, 1), np.float32)
@@ -156,6 +183,87 @@ class OracleModel:
         if debug:
             return logits[:R], {"hs": hs, "n1": n1, "attn": attn}
         return logits[:R]
+
+    def forward_train(self, batch, train_from: int = 0):
+        """Forward(c, batch, trainFrom): keeps the activations Backward needs."""
+        seq_len, ids, pos, opt, has_opt, nmask, mp = self._flat(batch)
+        R = int(nmask.sum())
+        logits = np.zeros(max(R, 1), np.float32)
+        rc = lib().orc_forward_train(self._h, int(train_from), len(batch), seq_len, ids, pos, opt, has_opt, nmask,
+                                     mp, logits)
+        if rc != 0:
+            raise ValueError("oracle: " + ERRORS.get(rc, str(rc)))
+        self._R = R
+        return logits[:R]
+
+    def backward(self, dlogits, grads: "OracleModel", train_emb: bool = True) -> None:
+        """Model.Backward: accumulates into grads (see zeros_like)."""
+        dl = np.ascontiguousarray(dlogits, np.float32)
+        assert dl.size == self._R
+        if lib().orc_backward(self._h, dl if dl.size else np.zeros(1, np.float32), grads._h, int(train_emb)) != 0:
+            raise ValueError("oracle: backward without a training forward")
+
+    def zeros_like(self) -> "OracleModel":
+        """NewLike: a model of the same configuration with every tensor zero."""
+        g = OracleModel(self.cfg, {})
+        lib().orc_model_zero_like(g._h, self._h)
+        return g
+
+    def get(self, name: str, n: int) -> np.ndarray:
+        out = np.zeros(n, np.float32)
+        if lib().orc_model_get(self._h, name.encode(), out, n) != 0:
+            raise KeyError(name)
+        return out
+
+
+class OracleAdamW:
+    """AdamW of internal/train/optim.go over an OracleModel and its gradients."""
+
+    def __init__(self, model: OracleModel, grads: OracleModel, weight_decay: float, train_from: int = 0,
+                 train_emb: bool = True, head_only: bool = False):
+        self._model, self._grads = model, grads
+        self._h = lib().orc_adamw_new(model._h, grads._h, weight_decay, train_from, int(train_emb), int(head_only))
+
+    def __del__(self):
+        if getattr(self, "_h", None):
+            lib().orc_adamw_free(self._h)
+            self._h = None
+
+    def grad_norm(self) -> float:
+        return lib().orc_adamw_grad_norm(self._h)
+
+    def update(self, lr: float, head_lr: float, grad_scale: float = 1.0) -> None:
+        lib().orc_adamw_update(self._h, lr, head_lr, grad_scale)
+
+    def moment(self, name: str, which: int, n: int) -> np.ndarray:
+        out = np.zeros(n, np.float32)
+        if lib().orc_adamw_get(self._h, name.encode(), which, out, n) != 0:
+            raise KeyError(name)
+        return out
+
+
+def loss_and_grad(logits, batch, targets):
+    """lossAndGrad of internal/nn/nn_test.go:60-86: mean cross-entropy over
+    sequences (one target option each) and dLoss/dlogits."""
+    d = np.zeros(len(logits), np.float32)
+    loss = 0.0
+    off = 0
+    nb = len(batch)
+    for si, s in enumerate(batch):
+        k = len(s.mask_pos)
+        l = np.asarray(logits[off:off + k], np.float32)
+        maxv = float(np.max(l))
+        ssum = 0.0
+        for v in l:
+            ssum += math.exp(float(np.float32(v - np.float32(maxv))))
+        for i, v in enumerate(l):
+            p = math.exp(float(np.float32(v - np.float32(maxv)))) / ssum
+            d[off + i] = np.float32(p) / np.float32(nb)
+            if i == targets[si]:
+                loss -= math.log(p) / nb
+                d[off + i] = np.float32(d[off + i] - np.float32(1) / np.float32(nb))
+        off += k
+    return loss, d
 
 
 def layer_norm(x, w, b, eps):

@@ -41,6 +41,7 @@
 #include <cstring>
 #include <functional>
 #include <map>
+#include <memory>
 #include <mutex>
 #include <string>
 #include <thread>
@@ -321,8 +322,11 @@ struct Config {
   std::vector<uint8_t> sliding;
 };
 
+struct TrainCache;
+
 struct Model {
   Config cfg;
+  std::shared_ptr<TrainCache> tc;  // activations of the last training forward
   std::map<std::string, std::vector<float>> w;
   const float *get(const std::string &name) const {
     auto it = w.find(name);
@@ -331,7 +335,10 @@ struct Model {
 };
 
 // layerNormFwd, ops.go:63-92.
-void layer_norm(float *y, const float *x, int rows, int dim, const float *w, const float *b, float eps) {
+// mean / rstd (when non-null) receive the row statistics, as the reference
+// records them for the backward pass.
+void layer_norm(float *y, const float *x, int rows, int dim, const float *w, const float *b, float eps,
+                float *mean = nullptr, float *rstd = nullptr) {
   parallel_for(rows, [&](int lo, int hi) {
     for (int r = lo; r < hi; r++) {
       const float *row = x + (size_t)r * dim;
@@ -345,6 +352,8 @@ void layer_norm(float *y, const float *x, int rows, int dim, const float *w, con
       }
       float rs = (float)(1.0 / std::sqrt(vs / (double)dim + (double)eps));
       float m = (float)mu;
+      if (mean) mean[r] = m;
+      if (rstd) rstd[r] = rs;
       float *o = y + (size_t)r * dim;
       if (b) {
         for (int i = 0; i < dim; i++) o[i] = (row[i] - m) * rs * w[i] + b[i];
@@ -377,8 +386,18 @@ void rope_tables(const std::vector<int32_t> &pos, int headDim, double theta, std
     }
 }
 
-// applyRope, ops.go:155-175 (forward direction only).
-void apply_rope(float *qkv, int T, int H, int heads, int D, const float *cs, const float *sn) {
+// geluGrad, ops.go:145-150: d gelu(x) / dx with erf and exp in float64.
+inline float gelu_grad(float x) {
+  const double sqrt2 = 1.41421356237309504880168872420969808;
+  const double pi = 3.14159265358979323846264338327950288;
+  double xf = (double)x;
+  double cdf = 0.5 * (1 + std::erf(xf * sqrt2 / 2));
+  double pdf = std::exp(-0.5 * xf * xf) / std::sqrt(2 * pi);
+  return (float)(cdf + xf * pdf);
+}
+
+// applyRope, ops.go:155-175; inverse transposes the rotation (backward pass).
+void apply_rope(float *qkv, int T, int H, int heads, int D, const float *cs, const float *sn, bool inverse = false) {
   int half = D / 2, stride = 3 * H;
   parallel_for(T, [&](int lo, int hi) {
     for (int t = lo; t < hi; t++)
@@ -387,6 +406,7 @@ void apply_rope(float *qkv, int T, int H, int heads, int D, const float *cs, con
           float *v = qkv + (size_t)t * stride + off;
           for (int i = 0; i < half; i++) {
             float c = cs[(size_t)t * half + i], s = sn[(size_t)t * half + i];
+            if (inverse) s = -s;
             float a = v[i], b = v[i + half];
             v[i] = a * c - b * s;
             v[i + half] = b * c + a * s;
@@ -422,6 +442,7 @@ void softmax_masked(float *P, int n, float scale, const uint8_t *mask) {
 
 struct SeqInfo {
   int off, n;
+  size_t pOff = 0;  // offset of this sequence's kept attention probabilities
   std::vector<uint8_t> full, slide;  // full empty == nil (all allowed)
 };
 
@@ -435,8 +456,11 @@ void linear(float *y, const float *x, int T, int K, const float *w, int N) {
   sgemm(g_workers, false, true, T, N, K, x, K, w, K, y, N, false);
 }
 
-// attnFwd, forward.go:347-378 (inference: P in per-item scratch).
-void attn_fwd(const Config &cfg, const std::vector<SeqInfo> &seqs, float *ctx, const float *qkv, bool sliding) {
+// attnFwd, forward.go:347-378. With pkeep (training) the probabilities are
+// kept there, n x n per (sequence, head) at pOff + head*n*n; otherwise P is
+// per-item scratch.
+void attn_fwd(const Config &cfg, const std::vector<SeqInfo> &seqs, float *ctx, const float *qkv, bool sliding,
+              float *pkeep = nullptr) {
   int H = cfg.hidden, heads = cfg.heads, D = H / heads, stride = 3 * H;
   float scale = (float)(1.0 / std::sqrt((double)D));
   int items = (int)seqs.size() * heads;
@@ -446,14 +470,20 @@ void attn_fwd(const Config &cfg, const std::vector<SeqInfo> &seqs, float *ctx, c
       int si = it / heads, hd = it % heads;
       const SeqInfo &s = seqs[si];
       int n = s.n;
-      P.resize((size_t)n * n);
+      float *Pp;
+      if (pkeep) {
+        Pp = pkeep + s.pOff + (size_t)hd * n * n;
+      } else {
+        P.resize((size_t)n * n);
+        Pp = P.data();
+      }
       const float *q = qkv + (size_t)s.off * stride + hd * D;
       const float *k = qkv + (size_t)s.off * stride + H + hd * D;
       const float *v = qkv + (size_t)s.off * stride + 2 * H + hd * D;
-      sgemm(1, false, true, n, n, D, q, stride, k, stride, P.data(), n, false);
+      sgemm(1, false, true, n, n, D, q, stride, k, stride, Pp, n, false);
       const uint8_t *mask = sliding ? s.slide.data() : (s.full.empty() ? nullptr : s.full.data());
-      softmax_masked(P.data(), n, scale, mask);
-      sgemm(1, false, false, n, D, n, P.data(), n, v, stride, ctx + (size_t)s.off * H + hd * D, H, false);
+      softmax_masked(Pp, n, scale, mask);
+      sgemm(1, false, false, n, D, n, Pp, n, v, stride, ctx + (size_t)s.off * H + hd * D, H, false);
     }
   });
 }
@@ -535,23 +565,50 @@ void orc_model_set(void *mp, const char *name, const float *data, int64_t n) {
   m->w[name].assign(data, data + n);
 }
 
-// Model.Forward (forward.go:129-245) + HeadForward (:250-282), inference.
-// Sequences are concatenated: seq_len[nseq], ids/pos/opt[T]; has_opt[s] = 0
-// means OptID nil for that sequence. mask_pos holds each sequence's mask
-// positions (local indices), nmask[s] of them. Returns 0, or a negative code
+}  // extern "C"
+
+namespace {
+
+// Per-layer activations a training forward keeps (layerCache, forward.go:65-73).
+struct LayerCache {
+  std::vector<float> n1, mean1, rstd1, qkv, ctx, h1, n2, mean2, rstd2, wi, act, P;
+};
+
+// The parts of nn.Cache (forward.go:77-110) that Backward reads.
+struct TrainCache {
+  int trainFrom = 0, T = 0, R = 0;
+  std::vector<SeqInfo> seqs;
+  std::vector<int32_t> ids;
+  std::vector<float> cosG, sinG, cosL, sinL;
+  std::vector<float> embX, embMean, embRstd;
+  std::vector<std::vector<float>> hs;  // hs[l] = input of layer l (kept for l >= trainFrom), hs[L] = output
+  std::vector<LayerCache> lc;
+  std::vector<int> rowTok;
+  std::vector<float> fN, fMean, fRstd, s1, m1, r1, d, ge, s2, m2, r2;
+};
+
+// Model.Forward (forward.go:129-245) + layerFwd (:284-343) + HeadForward
+// (:250-282). Sequences are concatenated: seq_len[nseq], ids/pos/opt[T];
+// has_opt[s] = 0 means OptID nil for that sequence. mask_pos holds each
+// sequence's mask positions (local indices), nmask[s] of them. With tc
+// (training) the activations of layers >= trainFrom, the attention
+// probabilities and the head's intermediates are kept there; layers below
+// trainFrom keep nothing (forward.go:226-236). Returns 0, or a negative code
 // mirroring the reference's validation errors:
 //   -1 malformed sequence, -2 no options, -3 mask position out of range,
 //   -4 token id out of range, -5 missing weight.
-int orc_forward(void *mp, int nseq, const int32_t *seq_len, const int32_t *ids, const int32_t *pos_in,
-                const int32_t *opt_in, const uint8_t *has_opt, const int32_t *nmask, const int32_t *mask_pos,
-                float *logits, float *dbg_hs, float *dbg_n1, float *dbg_attn) {
-  const Model &m = *(Model *)mp;
+int forward_impl(const Model &m, int nseq, const int32_t *seq_len, const int32_t *ids, const int32_t *pos_in,
+                 const int32_t *opt_in, const uint8_t *has_opt, const int32_t *nmask, const int32_t *mask_pos,
+                 float *logits, float *dbg_hs, float *dbg_n1, float *dbg_attn, TrainCache *tc, int trainFrom) {
   const Config &cfg = m.cfg;
   int H = cfg.hidden, I = cfg.inter, D = H / cfg.heads, L = cfg.layers;
+  if (tc) trainFrom = std::min(std::max(trainFrom, 0), L + 1);
+  else trainFrom = L + 1;
   std::vector<SeqInfo> seqs;
   std::vector<int32_t> pos;
   std::vector<int> rowTok;
   int T = 0, mp_off = 0;
+  size_t pTotal = 0;
   for (int si = 0; si < nseq; si++) {
     int n = seq_len[si];
     if (n <= 0) return -1;
@@ -559,6 +616,7 @@ int orc_forward(void *mp, int nseq, const int32_t *seq_len, const int32_t *ids, 
     SeqInfo info;
     info.off = T;
     info.n = n;
+    info.pOff = pTotal;
     const int32_t *op = opt_in + T;
     const int32_t *ps = pos_in + T;
     if (has_opt[si]) {
@@ -588,28 +646,42 @@ int orc_forward(void *mp, int nseq, const int32_t *seq_len, const int32_t *ids, 
     }
     mp_off += nmask[si];
     T += n;
+    pTotal += (size_t)n * n * cfg.heads;
   }
   for (int t = 0; t < T; t++)
     if (ids[t] < 0 || ids[t] >= cfg.vocab) return -4;
   int R = (int)rowTok.size();
 
-  std::vector<float> cosG, sinG, cosL, sinL;
-  rope_tables(pos, D, cfg.theta_g, cosG, sinG);
-  rope_tables(pos, D, cfg.theta_l, cosL, sinL);
+  TrainCache scratch;
+  TrainCache &c = tc ? *tc : scratch;
+  c.trainFrom = trainFrom;
+  c.T = T;
+  c.R = R;
+  c.ids.assign(ids, ids + T);
+  c.rowTok = rowTok;
+  rope_tables(pos, D, cfg.theta_g, c.cosG, c.sinG);
+  rope_tables(pos, D, cfg.theta_l, c.cosL, c.sinL);
 
   const float *tok = m.get("model.embeddings.tok_embeddings.weight");
   const float *embNorm = m.get("model.embeddings.norm.weight");
   if (!tok || !embNorm) return -5;
-  std::vector<float> embX((size_t)T * H);
+  c.embX.assign((size_t)T * H, 0);
+  c.embMean.assign(T, 0);
+  c.embRstd.assign(T, 0);
   parallel_for(T, [&](int lo, int hi) {
-    for (int t = lo; t < hi; t++) std::memcpy(&embX[(size_t)t * H], tok + (size_t)ids[t] * H, sizeof(float) * H);
+    for (int t = lo; t < hi; t++) std::memcpy(&c.embX[(size_t)t * H], tok + (size_t)ids[t] * H, sizeof(float) * H);
   });
-  std::vector<float> cur((size_t)T * H), out((size_t)T * H);
-  layer_norm(cur.data(), embX.data(), T, H, embNorm, nullptr, cfg.eps);
-  if (dbg_hs) std::memcpy(dbg_hs, cur.data(), sizeof(float) * T * H);
+  c.hs.assign(L + 1, {});
+  c.lc.assign(L, {});
+  for (int l = 0; l <= L; l++)
+    if (l >= trainFrom || l == L) c.hs[l].assign((size_t)T * H, 0);
+  std::vector<float> ping((size_t)T * H), pong((size_t)T * H);
+  float *cur = trainFrom == 0 ? c.hs[0].data() : ping.data();
+  layer_norm(cur, c.embX.data(), T, H, embNorm, nullptr, cfg.eps, c.embMean.data(), c.embRstd.data());
+  if (dbg_hs) std::memcpy(dbg_hs, cur, sizeof(float) * T * H);
 
-  std::vector<float> n1((size_t)T * H), qkv((size_t)T * 3 * H), ctx((size_t)T * H), tmp((size_t)T * H),
-      h1((size_t)T * H), n2((size_t)T * H), wi((size_t)T * 2 * I), act((size_t)T * I);
+  LayerCache frozen;
+  std::vector<float> tmp((size_t)T * H);
   for (int l = 0; l < L; l++) {
     std::string p = "model.layers." + std::to_string(l) + ".";
     const float *attnNorm = m.get(p + "attn_norm.weight");
@@ -619,40 +691,58 @@ int orc_forward(void *mp, int nseq, const int32_t *seq_len, const int32_t *ids, 
     const float *Wi = m.get(p + "mlp.Wi.weight");
     const float *MlpWo = m.get(p + "mlp.Wo.weight");
     if (!Wqkv || !Wo || !mlpNorm || !Wi || !MlpWo || (l > 0 && !attnNorm)) return -5;
+    float *out;
+    if (l + 1 >= trainFrom || l + 1 == L) out = c.hs[l + 1].data();
+    else out = cur == ping.data() ? pong.data() : ping.data();
+    const bool keep = l >= trainFrom;
+    LayerCache &lc = keep ? c.lc[l] : frozen;
     bool sliding = cfg.sliding[l] != 0;
     // layerFwd, forward.go:284-343.
-    const float *in = cur.data();
+    const float *in = cur;
     const float *x1 = in;
     if (l > 0) {  // layer 0 has no attn_norm (model.go:13-14, forward.go:289-294)
-      layer_norm(n1.data(), in, T, H, attnNorm, nullptr, cfg.eps);
-      x1 = n1.data();
+      lc.n1.resize((size_t)T * H);
+      lc.mean1.resize(T);
+      lc.rstd1.resize(T);
+      layer_norm(lc.n1.data(), in, T, H, attnNorm, nullptr, cfg.eps, lc.mean1.data(), lc.rstd1.data());
+      x1 = lc.n1.data();
     }
     if (dbg_n1) std::memcpy(dbg_n1 + (size_t)l * T * H, x1, sizeof(float) * T * H);
-    linear(qkv.data(), x1, T, H, Wqkv, 3 * H);
-    apply_rope(qkv.data(), T, H, cfg.heads, D, sliding ? cosL.data() : cosG.data(),
-               sliding ? sinL.data() : sinG.data());
-    attn_fwd(cfg, seqs, ctx.data(), qkv.data(), sliding);
-    linear(tmp.data(), ctx.data(), T, H, Wo, H);
+    lc.qkv.resize((size_t)T * 3 * H);
+    linear(lc.qkv.data(), x1, T, H, Wqkv, 3 * H);
+    apply_rope(lc.qkv.data(), T, H, cfg.heads, D, sliding ? c.cosL.data() : c.cosG.data(),
+               sliding ? c.sinL.data() : c.sinG.data());
+    lc.ctx.resize((size_t)T * H);
+    if (keep) lc.P.assign(pTotal, 0);
+    attn_fwd(cfg, seqs, lc.ctx.data(), lc.qkv.data(), sliding, keep ? lc.P.data() : nullptr);
+    linear(tmp.data(), lc.ctx.data(), T, H, Wo, H);
     if (dbg_attn) std::memcpy(dbg_attn + (size_t)l * T * H, tmp.data(), sizeof(float) * T * H);
+    lc.h1.resize((size_t)T * H);
     parallel_for(T * H, [&](int lo, int hi) {
-      for (int i = lo; i < hi; i++) h1[i] = in[i] + tmp[i];
+      for (int i = lo; i < hi; i++) lc.h1[i] = in[i] + tmp[i];
     });
-    layer_norm(n2.data(), h1.data(), T, H, mlpNorm, nullptr, cfg.eps);
-    linear(wi.data(), n2.data(), T, H, Wi, 2 * I);
+    lc.n2.resize((size_t)T * H);
+    lc.mean2.resize(T);
+    lc.rstd2.resize(T);
+    layer_norm(lc.n2.data(), lc.h1.data(), T, H, mlpNorm, nullptr, cfg.eps, lc.mean2.data(), lc.rstd2.data());
+    lc.wi.resize((size_t)T * 2 * I);
+    linear(lc.wi.data(), lc.n2.data(), T, H, Wi, 2 * I);
+    lc.act.resize((size_t)T * I);
     parallel_for(T, [&](int lo, int hi) {
       for (int t = lo; t < hi; t++) {
-        const float *row = &wi[(size_t)t * 2 * I];
-        float *a = &act[(size_t)t * I];
+        const float *row = &lc.wi[(size_t)t * 2 * I];
+        float *a = &lc.act[(size_t)t * I];
         for (int i = 0; i < I; i++) a[i] = gelu(row[i]) * row[I + i];
       }
     });
-    linear(tmp.data(), act.data(), T, I, MlpWo, H);
+    linear(tmp.data(), lc.act.data(), T, I, MlpWo, H);
     parallel_for(T * H, [&](int lo, int hi) {
-      for (int i = lo; i < hi; i++) out[i] = h1[i] + tmp[i];
+      for (int i = lo; i < hi; i++) out[i] = lc.h1[i] + tmp[i];
     });
-    std::swap(cur, out);
-    if (dbg_hs) std::memcpy(dbg_hs + (size_t)(l + 1) * T * H, cur.data(), sizeof(float) * T * H);
+    cur = out;
+    if (dbg_hs) std::memcpy(dbg_hs + (size_t)(l + 1) * T * H, cur, sizeof(float) * T * H);
   }
+  c.seqs = std::move(seqs);
   std::vector<float> rows((size_t)R * H);
   for (int r = 0; r < R; r++) std::memcpy(&rows[(size_t)r * H], &cur[(size_t)rowTok[r] * H], sizeof(float) * H);
 
@@ -664,23 +754,412 @@ int orc_forward(void *mp, int nseq, const int32_t *seq_len, const int32_t *ids, 
   const float *outW = m.get("scorer.out_proj.weight"), *outB = m.get("scorer.out_proj.bias");
   if (!finalNorm || !inW || !inB || !denseW || !denseB || !normW || !normB || !outW || !outB) return -5;
   int half = H / 2;
-  std::vector<float> fN((size_t)R * H), s1((size_t)R * H), d((size_t)R * half), ge((size_t)R * half),
-      s2((size_t)R * half);
-  layer_norm(fN.data(), rows.data(), R, H, finalNorm, nullptr, cfg.eps);
-  layer_norm(s1.data(), fN.data(), R, H, inW, inB, 1e-5f);
-  linear(d.data(), s1.data(), R, H, denseW, half);
+  c.fN.assign((size_t)R * H, 0);
+  c.fMean.assign(R, 0);
+  c.fRstd.assign(R, 0);
+  c.s1.assign((size_t)R * H, 0);
+  c.m1.assign(R, 0);
+  c.r1.assign(R, 0);
+  c.d.assign((size_t)R * half, 0);
+  c.ge.assign((size_t)R * half, 0);
+  c.s2.assign((size_t)R * half, 0);
+  c.m2.assign(R, 0);
+  c.r2.assign(R, 0);
+  layer_norm(c.fN.data(), rows.data(), R, H, finalNorm, nullptr, cfg.eps, c.fMean.data(), c.fRstd.data());
+  layer_norm(c.s1.data(), c.fN.data(), R, H, inW, inB, 1e-5f, c.m1.data(), c.r1.data());
+  linear(c.d.data(), c.s1.data(), R, H, denseW, half);
   for (int r = 0; r < R; r++)
     for (int i = 0; i < half; i++) {
-      d[(size_t)r * half + i] += denseB[i];
-      ge[(size_t)r * half + i] = gelu(d[(size_t)r * half + i]);
+      c.d[(size_t)r * half + i] += denseB[i];
+      c.ge[(size_t)r * half + i] = gelu(c.d[(size_t)r * half + i]);
     }
-  layer_norm(s2.data(), ge.data(), R, half, normW, normB, 1e-5f);
+  layer_norm(c.s2.data(), c.ge.data(), R, half, normW, normB, 1e-5f, c.m2.data(), c.r2.data());
   for (int r = 0; r < R; r++) {
     float s = 0;
-    for (int i = 0; i < half; i++) s += s2[(size_t)r * half + i] * outW[i];
+    for (int i = 0; i < half; i++) s += c.s2[(size_t)r * half + i] * outW[i];
     logits[r] = s + outB[0];
   }
   return 0;
+}
+
+// layerNormBwd, ops.go:94-135: ADDS the input gradient into dx and
+// accumulates dw (and db when non-null); per-chunk partial sums are merged
+// under a lock as the reference does.
+void layer_norm_bwd(float *dx, const float *dy, const float *x, int rows, int dim, const float *w, const float *mean,
+                    const float *rstd, float *dw, float *db) {
+  std::mutex mu;
+  parallel_for(rows, [&](int lo, int hi) {
+    std::vector<float> pw(dim, 0.0f), pb(db ? dim : 0, 0.0f), xh(dim);
+    for (int r = lo; r < hi; r++) {
+      const float *row = x + (size_t)r * dim;
+      const float *g = dy + (size_t)r * dim;
+      float m = mean[r], rs = rstd[r];
+      double s1 = 0, s2 = 0;
+      for (int i = 0; i < dim; i++) {
+        xh[i] = (row[i] - m) * rs;
+        float gw = g[i] * w[i];
+        s1 += (double)gw;
+        s2 += (double)(gw * xh[i]);
+        pw[i] += g[i] * xh[i];
+        if (db) pb[i] += g[i];
+      }
+      float a = (float)(s1 / (double)dim), b = (float)(s2 / (double)dim);
+      float *o = dx + (size_t)r * dim;
+      for (int i = 0; i < dim; i++) o[i] += rs * (g[i] * w[i] - a - xh[i] * b);
+    }
+    std::lock_guard<std::mutex> lk(mu);
+    for (int i = 0; i < dim; i++) dw[i] += pw[i];
+    if (db)
+      for (int i = 0; i < dim; i++) db[i] += pb[i];
+  });
+}
+
+// attnBwd, backward.go:117-159: dqkv (before the RoPE inverse) from dctx,
+// the rotated qkv and the kept probabilities.
+void attn_bwd(const Config &cfg, const std::vector<SeqInfo> &seqs, float *dqkv, const float *dctx, const float *qkv,
+              const float *P) {
+  int H = cfg.hidden, D = H / cfg.heads, heads = cfg.heads, stride = 3 * H;
+  float scale = (float)(1.0 / std::sqrt((double)D));
+  int items = (int)seqs.size() * heads;
+  parallel_for(items, [&](int lo, int hi) {
+    std::vector<float> dP;
+    for (int it = lo; it < hi; it++) {
+      int si = it / heads, hd = it % heads;
+      const SeqInfo &s = seqs[si];
+      int n = s.n;
+      const float *p = P + s.pOff + (size_t)hd * n * n;
+      dP.assign((size_t)n * n, 0);
+      const float *q = qkv + (size_t)s.off * stride + hd * D;
+      const float *k = qkv + (size_t)s.off * stride + H + hd * D;
+      const float *v = qkv + (size_t)s.off * stride + 2 * H + hd * D;
+      const float *dc = dctx + (size_t)s.off * H + hd * D;
+      sgemm(1, false, true, n, n, D, dc, H, v, stride, dP.data(), n, false);  // dP = dctx . V^T
+      for (int i = 0; i < n; i++) {
+        const float *pr = p + (size_t)i * n;
+        float *dr = dP.data() + (size_t)i * n;
+        float dot = 0;
+        for (int j = 0; j < n; j++) dot += pr[j] * dr[j];
+        for (int j = 0; j < n; j++) dr[j] = pr[j] * (dr[j] - dot) * scale;
+      }
+      float *dq = dqkv + (size_t)s.off * stride + hd * D;
+      float *dk = dqkv + (size_t)s.off * stride + H + hd * D;
+      float *dv = dqkv + (size_t)s.off * stride + 2 * H + hd * D;
+      sgemm(1, true, false, n, D, n, p, n, dc, H, dv, stride, false);         // dV = P^T . dctx
+      sgemm(1, false, false, n, D, n, dP.data(), n, k, stride, dq, stride, false);  // dQ = dS . K
+      sgemm(1, true, false, n, D, n, dP.data(), n, q, stride, dk, stride, false);   // dK = dS^T . Q
+    }
+  });
+}
+
+float *grad_of(Model &g, const std::string &name) {
+  auto it = g.w.find(name);
+  return it == g.w.end() ? nullptr : it->second.data();
+}
+
+// HeadBackward, backward.go:161-196: dlogits through the scorer head and the
+// final norm; returns dRows (R x H).
+std::vector<float> head_backward(const Model &m, const TrainCache &c, const float *rows, const float *dlogits,
+                                 Model &g) {
+  const Config &cfg = m.cfg;
+  int H = cfg.hidden, R = c.R, half = H / 2;
+  const float *outW = m.get("scorer.out_proj.weight"), *denseW = m.get("scorer.dense.weight");
+  std::vector<float> ds2((size_t)R * half);
+  float *gOutB = grad_of(g, "scorer.out_proj.bias"), *gOutW = grad_of(g, "scorer.out_proj.weight");
+  for (int r = 0; r < R; r++) {
+    float dl = dlogits[r];
+    gOutB[0] += dl;
+    const float *row = &c.s2[(size_t)r * half];
+    for (int i = 0; i < half; i++) {
+      gOutW[i] += dl * row[i];
+      ds2[(size_t)r * half + i] = dl * outW[i];
+    }
+  }
+  std::vector<float> dge((size_t)R * half, 0.0f);
+  layer_norm_bwd(dge.data(), ds2.data(), c.ge.data(), R, half, m.get("scorer.norm.weight"), c.m2.data(), c.r2.data(),
+                 grad_of(g, "scorer.norm.weight"), grad_of(g, "scorer.norm.bias"));
+  std::vector<float> dd((size_t)R * half);
+  float *gDenseB = grad_of(g, "scorer.dense.bias");
+  for (int r = 0; r < R; r++)
+    for (int i = 0; i < half; i++) {
+      float v = dge[(size_t)r * half + i] * gelu_grad(c.d[(size_t)r * half + i]);
+      dd[(size_t)r * half + i] = v;
+      gDenseB[i] += v;
+    }
+  sgemm(g_workers, true, false, half, H, R, dd.data(), half, c.s1.data(), H, grad_of(g, "scorer.dense.weight"), H,
+        true);
+  std::vector<float> ds1((size_t)R * H);
+  sgemm(g_workers, false, false, R, H, half, dd.data(), half, denseW, H, ds1.data(), H, false);
+  std::vector<float> dfN((size_t)R * H, 0.0f);
+  layer_norm_bwd(dfN.data(), ds1.data(), c.fN.data(), R, H, m.get("scorer.input_norm.weight"), c.m1.data(),
+                 c.r1.data(), grad_of(g, "scorer.input_norm.weight"), grad_of(g, "scorer.input_norm.bias"));
+  std::vector<float> dRows((size_t)R * H, 0.0f);
+  layer_norm_bwd(dRows.data(), dfN.data(), rows, R, H, m.get("model.final_norm.weight"), c.fMean.data(),
+                 c.fRstd.data(), grad_of(g, "model.final_norm.weight"), nullptr);
+  return dRows;
+}
+
+// Model.Backward, backward.go:19-115: accumulates into g the gradient of a
+// loss whose derivative with respect to the option logits is dlogits.
+void backward_impl(const Model &m, const TrainCache &c, const float *dlogits, Model &g, bool trainEmb) {
+  const Config &cfg = m.cfg;
+  int H = cfg.hidden, I = cfg.inter, D = H / cfg.heads, L = cfg.layers;
+  int T = c.T, R = c.R;
+  const float *hL = c.hs[L].data();
+  std::vector<float> rows((size_t)R * H);
+  for (int r = 0; r < R; r++) std::memcpy(&rows[(size_t)r * H], hL + (size_t)c.rowTok[r] * H, sizeof(float) * H);
+  std::vector<float> dRows = head_backward(m, c, rows.data(), dlogits, g);
+  std::vector<float> dcur((size_t)T * H, 0.0f);
+  for (int r = 0; r < R; r++)
+    std::memcpy(&dcur[(size_t)c.rowTok[r] * H], &dRows[(size_t)r * H], sizeof(float) * H);
+
+  std::vector<float> dh1((size_t)T * H), dact((size_t)T * I), dwi((size_t)T * 2 * I), dn2((size_t)T * H, 0.0f),
+      dctx((size_t)T * H), dqkv((size_t)T * 3 * H), dn1((size_t)T * H), dprev((size_t)T * H);
+  for (int l = L - 1; l >= c.trainFrom && l >= 0; l--) {
+    std::string p = "model.layers." + std::to_string(l) + ".";
+    const LayerCache &lc = c.lc[l];
+    const float *in = c.hs[l].data();
+    const float *dout = dcur.data();
+    const float *attnNorm = m.get(p + "attn_norm.weight");
+
+    // MLP: out = h1 + Wo(act)
+    sgemm(g_workers, false, false, T, I, H, dout, H, m.get(p + "mlp.Wo.weight"), I, dact.data(), I, false);
+    sgemm(g_workers, true, false, H, I, T, dout, H, lc.act.data(), I, grad_of(g, p + "mlp.Wo.weight"), I, true);
+    parallel_for(T, [&](int lo, int hi) {
+      for (int t = lo; t < hi; t++) {
+        const float *row = &lc.wi[(size_t)t * 2 * I];
+        const float *da = &dact[(size_t)t * I];
+        float *dw = &dwi[(size_t)t * 2 * I];
+        for (int i = 0; i < I; i++) {
+          float a = row[i], gt = row[I + i];
+          dw[i] = da[i] * gt * gelu_grad(a);
+          dw[I + i] = da[i] * gelu(a);
+        }
+      }
+    });
+    sgemm(g_workers, true, false, 2 * I, H, T, dwi.data(), 2 * I, lc.n2.data(), H, grad_of(g, p + "mlp.Wi.weight"), H,
+          true);
+    sgemm(g_workers, false, false, T, H, 2 * I, dwi.data(), 2 * I, m.get(p + "mlp.Wi.weight"), H, dn2.data(), H,
+          false);
+    dh1 = dcur;  // residual path
+    layer_norm_bwd(dh1.data(), dn2.data(), lc.h1.data(), T, H, m.get(p + "mlp_norm.weight"), lc.mean2.data(),
+                   lc.rstd2.data(), grad_of(g, p + "mlp_norm.weight"), nullptr);
+
+    // Attention: h1 = in + Wo(ctx)
+    sgemm(g_workers, false, false, T, H, H, dh1.data(), H, m.get(p + "attn.Wo.weight"), H, dctx.data(), H, false);
+    sgemm(g_workers, true, false, H, H, T, dh1.data(), H, lc.ctx.data(), H, grad_of(g, p + "attn.Wo.weight"), H, true);
+    attn_bwd(cfg, c.seqs, dqkv.data(), dctx.data(), lc.qkv.data(), lc.P.data());
+    const bool sliding = cfg.sliding[l] != 0;
+    apply_rope(dqkv.data(), T, H, cfg.heads, D, sliding ? c.cosL.data() : c.cosG.data(),
+               sliding ? c.sinL.data() : c.sinG.data(), true);
+    const float *n1 = attnNorm ? lc.n1.data() : in;
+    sgemm(g_workers, true, false, 3 * H, H, T, dqkv.data(), 3 * H, n1, H, grad_of(g, p + "attn.Wqkv.weight"), H, true);
+    sgemm(g_workers, false, false, T, H, 3 * H, dqkv.data(), 3 * H, m.get(p + "attn.Wqkv.weight"), H, dn1.data(), H,
+          false);
+    dprev = dh1;  // residual path
+    if (attnNorm) {
+      layer_norm_bwd(dprev.data(), dn1.data(), in, T, H, attnNorm, lc.mean1.data(), lc.rstd1.data(),
+                     grad_of(g, p + "attn_norm.weight"), nullptr);
+    } else {
+      parallel_for(T * H, [&](int lo, int hi) {
+        for (int i = lo; i < hi; i++) dprev[i] += dn1[i];
+      });
+    }
+    std::swap(dcur, dprev);
+    std::fill(dn2.begin(), dn2.end(), 0.0f);
+  }
+
+  // Embeddings.
+  if (trainEmb && c.trainFrom == 0) {
+    std::vector<float> dE((size_t)T * H, 0.0f);
+    layer_norm_bwd(dE.data(), dcur.data(), c.embX.data(), T, H, m.get("model.embeddings.norm.weight"),
+                   c.embMean.data(), c.embRstd.data(), grad_of(g, "model.embeddings.norm.weight"), nullptr);
+    float *gTok = grad_of(g, "model.embeddings.tok_embeddings.weight");
+    for (int t = 0; t < T; t++) {
+      float *dst = gTok + (size_t)c.ids[t] * H;
+      const float *src = &dE[(size_t)t * H];
+      for (int i = 0; i < H; i++) dst[i] += src[i];
+    }
+  }
+}
+
+// Tensor order and shapes of nn.Model.Tensors() (model.go:51-84): name,
+// element count, rank.
+struct TensorDesc {
+  std::string name;
+  size_t n;
+  int rank;
+};
+std::vector<TensorDesc> tensor_list(const Config &cfg) {
+  size_t H = cfg.hidden, I = cfg.inter;
+  std::vector<TensorDesc> t = {{"model.embeddings.tok_embeddings.weight", (size_t)cfg.vocab * H, 2},
+                               {"model.embeddings.norm.weight", H, 1}};
+  for (int l = 0; l < cfg.layers; l++) {
+    std::string p = "model.layers." + std::to_string(l) + ".";
+    if (l > 0) t.push_back({p + "attn_norm.weight", H, 1});
+    t.push_back({p + "attn.Wqkv.weight", 3 * H * H, 2});
+    t.push_back({p + "attn.Wo.weight", H * H, 2});
+    t.push_back({p + "mlp_norm.weight", H, 1});
+    t.push_back({p + "mlp.Wi.weight", 2 * I * H, 2});
+    t.push_back({p + "mlp.Wo.weight", H * I, 2});
+  }
+  t.push_back({"model.final_norm.weight", H, 1});
+  t.push_back({"scorer.input_norm.weight", H, 1});
+  t.push_back({"scorer.input_norm.bias", H, 1});
+  t.push_back({"scorer.dense.weight", H / 2 * H, 2});
+  t.push_back({"scorer.dense.bias", H / 2, 1});
+  t.push_back({"scorer.norm.weight", H / 2, 1});
+  t.push_back({"scorer.norm.bias", H / 2, 1});
+  t.push_back({"scorer.out_proj.weight", H / 2, 2});
+  t.push_back({"scorer.out_proj.bias", 1, 1});
+  return t;
+}
+
+// AdamW, internal/train/optim.go:11-145.
+struct AdamW {
+  float beta1 = 0.9f, beta2 = 0.999f, eps = 1e-8f, weightDecay = 0;
+  Model *model = nullptr, *grads = nullptr;
+  std::vector<TensorDesc> list;
+  std::vector<std::vector<float>> m, v;
+  std::vector<bool> frozen, head, decay;
+  int step = 0;
+};
+
+// NewAdamW, optim.go:31-65.
+AdamW *adamw_new(Model *model, Model *grads, float wd, int trainFrom, bool trainEmb, bool headOnly) {
+  AdamW *o = new AdamW;
+  o->weightDecay = wd;
+  o->model = model;
+  o->grads = grads;
+  o->list = tensor_list(model->cfg);
+  for (const TensorDesc &t : o->list) {
+    bool frozen = false, head = t.name.rfind("scorer.", 0) == 0, decay = t.rank == 2;
+    if (t.name == "model.embeddings.tok_embeddings.weight") {
+      frozen = !trainEmb || trainFrom > 0;
+      decay = false;
+    } else if (t.name == "model.embeddings.norm.weight") {
+      frozen = trainFrom > 0;
+    } else if (t.name.rfind("model.layers.", 0) == 0) {
+      int l = 0;
+      for (size_t i = 13; i < t.name.size() && t.name[i] >= '0' && t.name[i] <= '9'; i++) l = l * 10 + (t.name[i] - '0');
+      frozen = l < trainFrom;
+    }
+    if (headOnly && (t.name.rfind("model.embeddings.", 0) == 0 || t.name.rfind("model.layers.", 0) == 0))
+      frozen = true;
+    o->frozen.push_back(frozen);
+    o->head.push_back(head);
+    o->decay.push_back(decay);
+    o->m.emplace_back(t.n, 0.0f);
+    o->v.emplace_back(t.n, 0.0f);
+  }
+  return o;
+}
+
+// GradNorm, optim.go:68-90 (per-tensor float64 sums of squares).
+double adamw_grad_norm(const AdamW &o) {
+  double total = 0;
+  for (size_t i = 0; i < o.list.size(); i++) {
+    if (o.frozen[i]) continue;
+    const std::vector<float> &d = o.grads->w.at(o.list[i].name);
+    double s = 0;
+    for (float v : d) s += (double)v * (double)v;
+    total += s;
+  }
+  return std::sqrt(total);
+}
+
+// Update, optim.go:94-145.
+void adamw_update(AdamW &o, float lr, float headLR, float gradScale) {
+  o.step++;
+  double b1c = 1 - std::pow((double)o.beta1, (double)o.step);
+  double b2c = 1 - std::pow((double)o.beta2, (double)o.step);
+  float stepSize = (float)(1 / b1c);
+  float invSqrtB2c = (float)(1 / std::sqrt(b2c));
+  for (size_t i = 0; i < o.list.size(); i++) {
+    if (o.frozen[i]) continue;
+    float rate = o.head[i] ? headLR : lr;
+    float wd = o.decay[i] ? o.weightDecay * rate : 0.0f;
+    std::vector<float> &p = o.model->w.at(o.list[i].name);
+    const std::vector<float> &g = o.grads->w.at(o.list[i].name);
+    std::vector<float> &m = o.m[i], &v = o.v[i];
+    parallel_for((int)p.size(), [&](int lo, int hi) {
+      for (int k = lo; k < hi; k++) {
+        float gr = g[k] * gradScale;
+        m[k] = o.beta1 * m[k] + (1 - o.beta1) * gr;
+        v[k] = o.beta2 * v[k] + (1 - o.beta2) * gr * gr;
+        float den = (float)std::sqrt((double)v[k]) * invSqrtB2c + o.eps;
+        p[k] -= rate * stepSize * m[k] / den + wd * p[k];
+      }
+    });
+  }
+}
+
+}  // namespace
+
+extern "C" {
+
+// Inference forward (Forward with trainFrom >= Layers); the dbg_* arrays, when
+// non-null, receive each layer's input, attention input and Wo output.
+int orc_forward(void *mp, int nseq, const int32_t *seq_len, const int32_t *ids, const int32_t *pos_in,
+                const int32_t *opt_in, const uint8_t *has_opt, const int32_t *nmask, const int32_t *mask_pos,
+                float *logits, float *dbg_hs, float *dbg_n1, float *dbg_attn) {
+  return forward_impl(*(Model *)mp, nseq, seq_len, ids, pos_in, opt_in, has_opt, nmask, mask_pos, logits, dbg_hs,
+                      dbg_n1, dbg_attn, nullptr, 0);
+}
+
+// Training forward: Forward(c, batch, trainFrom) with the model's own cache.
+int orc_forward_train(void *mp, int trainFrom, int nseq, const int32_t *seq_len, const int32_t *ids,
+                      const int32_t *pos_in, const int32_t *opt_in, const uint8_t *has_opt, const int32_t *nmask,
+                      const int32_t *mask_pos, float *logits) {
+  Model &m = *(Model *)mp;
+  if (!m.tc) m.tc = std::make_shared<TrainCache>();
+  return forward_impl(m, nseq, seq_len, ids, pos_in, opt_in, has_opt, nmask, mask_pos, logits, nullptr, nullptr,
+                      nullptr, m.tc.get(), trainFrom);
+}
+
+// Backward of the last orc_forward_train into the gradient model g (a model
+// of the same configuration whose tensors accumulate). Returns -1 without a
+// training forward.
+int orc_backward(void *mp, const float *dlogits, void *gp, int trainEmb) {
+  Model &m = *(Model *)mp;
+  if (!m.tc) return -1;
+  backward_impl(m, *m.tc, dlogits, *(Model *)gp, trainEmb != 0);
+  return 0;
+}
+
+// NewLike + Zero (model.go:123-130): every tensor of the configuration, zeroed.
+void orc_model_zero_like(void *dst, void *src) {
+  Model &d = *(Model *)dst;
+  for (const TensorDesc &t : tensor_list(((Model *)src)->cfg)) d.w[t.name].assign(t.n, 0.0f);
+}
+
+// Copies tensor name into out (n values); -1 if absent or of another size.
+int orc_model_get(void *mp, const char *name, float *out, int64_t n) {
+  Model &m = *(Model *)mp;
+  auto it = m.w.find(name);
+  if (it == m.w.end() || (int64_t)it->second.size() != n) return -1;
+  std::memcpy(out, it->second.data(), sizeof(float) * n);
+  return 0;
+}
+
+void *orc_adamw_new(void *model, void *grads, float wd, int trainFrom, int trainEmb, int headOnly) {
+  return adamw_new((Model *)model, (Model *)grads, wd, trainFrom, trainEmb != 0, headOnly != 0);
+}
+void orc_adamw_free(void *o) { delete (AdamW *)o; }
+double orc_adamw_grad_norm(void *o) { return adamw_grad_norm(*(AdamW *)o); }
+void orc_adamw_update(void *o, float lr, float headLR, float gradScale) {
+  adamw_update(*(AdamW *)o, lr, headLR, gradScale);
+}
+// Moment tensor (which 0 = m, 1 = v) of name; -1 if absent.
+int orc_adamw_get(void *op, const char *name, int which, float *out, int64_t n) {
+  AdamW &o = *(AdamW *)op;
+  for (size_t i = 0; i < o.list.size(); i++)
+    if (o.list[i].name == name) {
+      const std::vector<float> &src = which ? o.v[i] : o.m[i];
+      if ((int64_t)src.size() != n) return -1;
+      std::memcpy(out, src.data(), sizeof(float) * n);
+      return 0;
+    }
+  return -1;
 }
 
 // Pieces exposed for closed-form checks.
@@ -688,6 +1167,10 @@ void orc_layer_norm(float *y, const float *x, int rows, int dim, const float *w,
   layer_norm(y, x, rows, dim, w, b, eps);
 }
 float orc_gelu(float x) { return gelu(x); }
+float orc_gelu_grad(float x) { return gelu_grad(x); }
+void orc_apply_rope_inverse(float *qkv, int T, int H, int heads, int D, const float *cs, const float *sn) {
+  apply_rope(qkv, T, H, heads, D, cs, sn, true);
+}
 void orc_rope_tables(const int32_t *pos, int n, int headDim, double theta, float *cs, float *sn) {
   std::vector<int32_t> p(pos, pos + n);
   std::vector<float> c, s;
