@@ -10,35 +10,10 @@
 #include <string>
 #include <vector>
 
-#include "../../include/decide_hip.h"
-#include "common.hpp"
+#include "ctx.hpp"
 
 namespace {
-
-struct DevBuf {
-  void *p = nullptr;
-  size_t cap = 0;
-};
-
-struct TensorSlot {
-  DevBuf buf;
-  int64_t n = 0;     // float32 elements expected
-  bool proj = false; // projection matrix: stored in the operand precision
-  bool wi = false;   // Wi: rows interleaved for the GeGLU epilogue
-  bool set = false;
-};
-
-struct Config {
-  int hidden = 0, inter = 0, heads = 0, layers = 0, vocab = 0;
-  float eps = 1e-5f;
-  int half_window = 64;
-  double theta_g = 160000, theta_l = 10000;
-  std::vector<uint8_t> sliding;
-  int precision = DN_PRECISION_BF16;
-};
-
 thread_local std::string g_err;  // errors without a context
-
 }  // namespace
 
 int set_host_error(int code, const std::string &msg) {
@@ -46,36 +21,9 @@ int set_host_error(int code, const std::string &msg) {
   return code;
 }
 
-struct dn_ctx {
-  int device = 0;
-  hipStream_t stream = nullptr;
-  hipStream_t own_stream = nullptr;
-  std::string err;
-  bool configured = false;
-  Config cfg;
-  std::map<std::string, TensorSlot> w;
-  DevBuf inv_freq;  // 32 doubles global theta, 32 local
-  // workspace
-  DevBuf h, xn, qkv, ctxb, act, kinfo, ids, pos, opt, rowtok, logits, err_flag, head_s1, head_d;
-  // RoPE cos/sin per position 0..65535 (global theta, then local), built once
-  // per configuration at the first forward.
-  DevBuf rope;
-  bool rope_ready = false;
-  DevBuf gA, gB, gC;  // dn_gemm_f32 staging
-  // batch layout cache
-  std::vector<int> lay_len;
-  std::vector<int> h_seq_off, h_chunk_off;
-  std::vector<int4> h_chunk_desc, h_work;
-  DevBuf d_seq_off, d_seq_len, d_chunk_off, d_chunk_desc, d_work, d_chunks;
-  DevBuf d_codes, d_first;  // attention tile classes per work item: [global | local]
-  int lay_T = 0, lay_nchunks = 0, lay_nwork = 0;
-  // kernel probe: events[2*k], events[2*k+1] bracket launch k of one forward
-  int probe_layer = -1;
-  std::vector<hipEvent_t> probe_pool;  // 10 events per recorded forward
-  int probe_used = 0;                  // forwards recorded
-};
+using namespace dnh;
 
-namespace {
+namespace dnh {
 
 int fail(dn_ctx *c, int code, const std::string &msg) {
   if (c)
@@ -90,12 +38,6 @@ int hip_fail(dn_ctx *c, const char *op, hipError_t e) {
   return fail(c, code, std::string("hip: ") + op + " failed: " + hipGetErrorString(e) + " [code " +
                            std::to_string((int)e) + "]");
 }
-
-#define HIPCHK(c, op, expr)                         \
-  do {                                              \
-    hipError_t e_ = (expr);                         \
-    if (e_ != hipSuccess) return hip_fail(c, op, e_); \
-  } while (0)
 
 hipError_t ensure(DevBuf &b, size_t bytes) {
   if (bytes == 0) bytes = 16;
@@ -122,6 +64,24 @@ void release(DevBuf &b) {
   b.cap = 0;
 }
 
+void release_slot(TensorSlot &t) {
+  DevBuf *bufs[] = {&t.buf, &t.train.master, &t.train.grad, &t.train.m, &t.train.v, &t.train.wt};
+  for (DevBuf *b : bufs) release(*b);
+}
+
+void release_train(TrainState &tr) {
+  for (LayerSave &S : tr.layers) {
+    DevBuf *bufs[] = {&S.hs, &S.h1, &S.n1, &S.qkv, &S.ctx, &S.n2, &S.wi, &S.act, &S.lse};
+    for (DevBuf *b : bufs) release(*b);
+  }
+  tr.layers.clear();
+  DevBuf *bufs[] = {&tr.dcur, &tr.dprev, &tr.dh1, &tr.dact, &tr.dwi, &tr.dn2, &tr.dctx, &tr.dqkv, &tr.dn1,
+                    &tr.dyop, &tr.dyT, &tr.xT, &tr.dsum, &tr.part, &tr.lnpart, &tr.dE, &tr.dl, &tr.contrib,
+                    &tr.emb_order, &tr.emb_seg, &tr.emb_id, &tr.sq_part, &tr.sq_out};
+  for (DevBuf *b : bufs) release(*b);
+  tr.have_forward = false;
+}
+
 uint16_t f32_to_bf16_rne(float f) {
   uint32_t u;
   std::memcpy(&u, &f, 4);
@@ -135,33 +95,34 @@ std::string layer_prefix(int l) { return "model.layers." + std::to_string(l) + "
 void define_tensors(dn_ctx *c) {
   const Config &g = c->cfg;
   const int64_t H = g.hidden, I = g.inter;
-  auto add = [&](const std::string &name, int64_t n, bool proj = false, bool wi = false) {
+  auto add = [&](const std::string &name, int64_t n, int rank, bool proj = false, bool wi = false) {
     TensorSlot s;
     s.n = n;
+    s.rank = rank;
     s.proj = proj;
     s.wi = wi;
     c->w[name] = s;
   };
-  add("model.embeddings.tok_embeddings.weight", (int64_t)g.vocab * H);
-  add("model.embeddings.norm.weight", H);
+  add("model.embeddings.tok_embeddings.weight", (int64_t)g.vocab * H, 2);
+  add("model.embeddings.norm.weight", H, 1);
   for (int l = 0; l < g.layers; l++) {
     const std::string p = layer_prefix(l);
-    if (l > 0) add(p + "attn_norm.weight", H);
-    add(p + "attn.Wqkv.weight", 3 * H * H, true);
-    add(p + "attn.Wo.weight", H * H, true);
-    add(p + "mlp_norm.weight", H);
-    add(p + "mlp.Wi.weight", 2 * I * H, true, true);
-    add(p + "mlp.Wo.weight", H * I, true);
+    if (l > 0) add(p + "attn_norm.weight", H, 1);
+    add(p + "attn.Wqkv.weight", 3 * H * H, 2, true);
+    add(p + "attn.Wo.weight", H * H, 2, true);
+    add(p + "mlp_norm.weight", H, 1);
+    add(p + "mlp.Wi.weight", 2 * I * H, 2, true, true);
+    add(p + "mlp.Wo.weight", H * I, 2, true);
   }
-  add("model.final_norm.weight", H);
-  add("scorer.input_norm.weight", H);
-  add("scorer.input_norm.bias", H);
-  add("scorer.dense.weight", H / 2 * H);
-  add("scorer.dense.bias", H / 2);
-  add("scorer.norm.weight", H / 2);
-  add("scorer.norm.bias", H / 2);
-  add("scorer.out_proj.weight", H / 2);
-  add("scorer.out_proj.bias", 1);
+  add("model.final_norm.weight", H, 1);
+  add("scorer.input_norm.weight", H, 1);
+  add("scorer.input_norm.bias", H, 1);
+  add("scorer.dense.weight", H / 2 * H, 2);
+  add("scorer.dense.bias", H / 2, 1);
+  add("scorer.norm.weight", H / 2, 1);
+  add("scorer.norm.bias", H / 2, 1);
+  add("scorer.out_proj.weight", H / 2, 2);
+  add("scorer.out_proj.bias", 1, 1);
 }
 
 // Device pointer of an uploaded weight (check_ready has verified that every
@@ -259,15 +220,32 @@ hipEvent_t *probe_slot(dn_ctx *c, int l) {
   } while (0)
 
 int forward_core(dn_ctx *c, int nseq, const int32_t *seq_len, const int32_t *d_ids, const int32_t *d_pos,
-                 const int32_t *d_opt, int R, const int32_t *d_row_tok, float *d_logits) {
+                 const int32_t *d_opt, int R, const int32_t *d_row_tok, float *d_logits, bool train) {
   const Config &g = c->cfg;
   const int H = g.hidden, I = g.inter, L = g.layers;
   const int prec = g.precision;
   const size_t es = prec == DN_PRECISION_BF16 ? 2 : 4;
+  TrainState &tr = c->tr;
+  tr.have_forward = false;  // any forward replaces the layout and the encoder output
   int rc = prepare_layout(c, nseq, seq_len);
   if (rc) return rc;
   const int T = c->lay_T;
   hipStream_t s = c->stream;
+  if (train) {
+    tr.layers.resize(L);
+    for (int l = tr.train_from; l < L; l++) {
+      LayerSave &S = tr.layers[l];
+      HIPCHK(c, "hipMalloc", ensure(S.hs, sizeof(float) * T * H));
+      HIPCHK(c, "hipMalloc", ensure(S.h1, sizeof(float) * T * H));
+      HIPCHK(c, "hipMalloc", ensure(S.n1, es * T * H));
+      HIPCHK(c, "hipMalloc", ensure(S.qkv, es * T * 3 * H));
+      HIPCHK(c, "hipMalloc", ensure(S.ctx, es * T * H));
+      HIPCHK(c, "hipMalloc", ensure(S.n2, es * T * H));
+      HIPCHK(c, "hipMalloc", ensure(S.wi, es * T * 2 * I));
+      HIPCHK(c, "hipMalloc", ensure(S.act, es * T * I));
+      HIPCHK(c, "hipMalloc", ensure(S.lse, sizeof(float) * T * g.heads));
+    }
+  }
   HIPCHK(c, "hipMalloc", ensure(c->h, sizeof(float) * T * H));
   HIPCHK(c, "hipMalloc", ensure(c->xn, es * T * H));
   HIPCHK(c, "hipMalloc", ensure(c->qkv, es * T * 3 * H));
@@ -277,7 +255,6 @@ int forward_core(dn_ctx *c, int nseq, const int32_t *seq_len, const int32_t *d_i
   rc = ensure_err_flag(c);
   if (rc) return rc;
 
-  constexpr int kPositions = 65536;  // positions are validated / flagged to this range
   float *h = (float *)c->h.p;
   const double *inv = (const double *)c->inv_freq.p;
   if (!c->rope_ready) {
@@ -310,8 +287,6 @@ int forward_core(dn_ctx *c, int nseq, const int32_t *seq_len, const int32_t *d_i
                          (int *)c->err_flag.p, s));
 
   AttnArgs at{};
-  at.qkv = c->qkv.p;
-  at.ctx = c->ctxb.p;
   at.kinfo = kinfo;
   at.work = (const int4 *)c->d_work.p;
   at.seq_off = (const int *)c->d_seq_off.p;
@@ -328,15 +303,24 @@ int forward_core(dn_ctx *c, int nseq, const int32_t *seq_len, const int32_t *d_i
     const bool sliding = g.sliding[l] != 0;
     hipEvent_t *ev = probe_slot(c, l);
     probed |= ev != nullptr;
-    if (l > 0)
-      HIPCHK(c, "ln(attn_norm)", launch_ln(prec, h, T, H, (const float *)W(c, p + "attn_norm.weight"), g.eps,
-                                           c->xn.p, s));
+    // Training keeps this layer's activations (layers >= train_from).
+    LayerSave *S = train && l >= tr.train_from ? &tr.layers[l] : nullptr;
+    if (S) HIPCHK(c, "hipMemcpyAsync", hipMemcpyAsync(S->hs.p, h, sizeof(float) * T * H, hipMemcpyDeviceToDevice, s));
+    void *x1 = c->xn.p;  // QKV input: attn_norm(h), or for layer 0 the embedding output
+    if (l > 0) {
+      if (S) x1 = S->n1.p;
+      HIPCHK(c, "ln(attn_norm)",
+             launch_ln(prec, h, T, H, (const float *)W(c, p + "attn_norm.weight"), g.eps, x1, s));
+    } else if (S) {
+      HIPCHK(c, "hipMemcpyAsync", hipMemcpyAsync(S->n1.p, c->xn.p, es * T * H, hipMemcpyDeviceToDevice, s));
+      x1 = S->n1.p;
+    }
     GemmArgs q{};
-    q.A = c->xn.p;
+    q.A = x1;
     q.lda = H;
     q.B = W(c, p + "attn.Wqkv.weight");
     q.ldb = H;
-    q.C = c->qkv.p;
+    q.C = S ? S->qkv.p : c->qkv.p;
     q.ldc = 3 * H;
     q.M = T;
     q.N = 3 * H;
@@ -344,6 +328,9 @@ int forward_core(dn_ctx *c, int nseq, const int32_t *seq_len, const int32_t *d_i
     q.n_store = 3 * H;
     PROBED(ev, DN_PROBE_QKV, "gemm(Wqkv)", launch_gemm(prec, EPI_STORE, q, s));
 
+    at.qkv = q.C;
+    at.ctx = S ? S->ctx.p : c->ctxb.p;
+    at.lse = S ? (float *)S->lse.p : nullptr;
     at.sliding = sliding ? 1 : 0;
     at.codes = codes + (sliding ? nw * ATTN_MAXKT : 0);
     at.first = first + (sliding ? nw : 0);
@@ -352,7 +339,7 @@ int forward_core(dn_ctx *c, int nseq, const int32_t *seq_len, const int32_t *d_i
     PROBED(ev, DN_PROBE_ATTENTION, "attention", launch_attention(prec, at, s));
 
     GemmArgs o{};
-    o.A = c->ctxb.p;
+    o.A = at.ctx;
     o.lda = H;
     o.B = W(c, p + "attn.Wo.weight");
     o.ldb = H;
@@ -364,25 +351,33 @@ int forward_core(dn_ctx *c, int nseq, const int32_t *seq_len, const int32_t *d_i
     o.n_store = H;
     o.accumulate = 1;
     PROBED(ev, DN_PROBE_WO, "gemm(Wo)", launch_gemm(prec, EPI_F32, o, s));
+    if (S) HIPCHK(c, "hipMemcpyAsync", hipMemcpyAsync(S->h1.p, h, sizeof(float) * T * H, hipMemcpyDeviceToDevice, s));
 
-    HIPCHK(c, "ln(mlp_norm)",
-           launch_ln(prec, h, T, H, (const float *)W(c, p + "mlp_norm.weight"), g.eps, c->xn.p, s));
+    void *x2 = S ? S->n2.p : c->xn.p;
+    HIPCHK(c, "ln(mlp_norm)", launch_ln(prec, h, T, H, (const float *)W(c, p + "mlp_norm.weight"), g.eps, x2, s));
 
     GemmArgs wi{};
-    wi.A = c->xn.p;
+    wi.A = x2;
     wi.lda = H;
     wi.B = W(c, p + "mlp.Wi.weight");
     wi.ldb = H;
-    wi.C = c->act.p;
-    wi.ldc = I;
     wi.M = T;
     wi.N = 2 * I;
     wi.K = H;
     wi.n_store = 2 * I;
-    PROBED(ev, DN_PROBE_WI, "gemm(Wi)", launch_gemm(prec, EPI_GEGLU, wi, s));
+    if (S) {  // training keeps the pre-activation: plain store, then GeGLU
+      wi.C = S->wi.p;
+      wi.ldc = 2 * I;
+      PROBED(ev, DN_PROBE_WI, "gemm(Wi)", launch_gemm(prec, EPI_STORE, wi, s));
+      HIPCHK(c, "geglu", launch_geglu_fwd(prec, S->wi.p, S->act.p, T, I, s));
+    } else {
+      wi.C = c->act.p;
+      wi.ldc = I;
+      PROBED(ev, DN_PROBE_WI, "gemm(Wi)", launch_gemm(prec, EPI_GEGLU, wi, s));
+    }
 
     GemmArgs mo{};
-    mo.A = c->act.p;
+    mo.A = S ? S->act.p : c->act.p;
     mo.lda = I;
     mo.B = W(c, p + "mlp.Wo.weight");
     mo.ldb = I;
@@ -418,6 +413,11 @@ int forward_core(dn_ctx *c, int nseq, const int32_t *seq_len, const int32_t *d_i
   HIPCHK(c, "hipMalloc", ensure(c->head_s1, sizeof(float) * (size_t)std::max(R, 1) * H));
   HIPCHK(c, "hipMalloc", ensure(c->head_d, sizeof(float) * (size_t)std::max(R, 1) * (H / 2)));
   HIPCHK(c, "head", launch_head(ha, (float *)c->head_s1.p, (float *)c->head_d.p, s));
+  if (train) {
+    tr.have_forward = true;
+    tr.T = T;
+    tr.R = R;
+  }
   return DN_OK;
 }
 
@@ -451,17 +451,25 @@ int upload_f32(dn_ctx *c, TensorSlot &t, const float *data, int64_t n) {
   const int64_t H = c->cfg.hidden, I = c->cfg.inter;
   auto src_row = [&](int64_t r) -> int64_t { return t.wi ? wi_src_row(r, I) : r; };
   const int64_t rows = t.wi ? 2 * I : 0;
+  t.train.wt_valid = false;
   if (bf) {
     std::vector<uint16_t> tmp((size_t)n);
+    std::vector<float> master(c->tr.enabled ? (size_t)n : 0);
     if (t.wi) {
       for (int64_t r = 0; r < rows; r++) {
         const float *s = data + src_row(r) * H;
         for (int64_t k = 0; k < H; k++) tmp[r * H + k] = f32_to_bf16_rne(s[k]);
+        if (!master.empty()) std::memcpy(&master[r * H], s, sizeof(float) * H);
       }
     } else {
       for (int64_t i = 0; i < n; i++) tmp[i] = f32_to_bf16_rne(data[i]);
+      if (!master.empty()) std::memcpy(master.data(), data, sizeof(float) * n);
     }
     HIPCHK(c, "hipMemcpy", hipMemcpy(t.buf.p, tmp.data(), bytes, hipMemcpyHostToDevice));
+    if (!master.empty()) {  // training keeps the fp32 weights the bf16 copy is rounded from
+      HIPCHK(c, "hipMalloc", ensure(t.train.master, sizeof(float) * n));
+      HIPCHK(c, "hipMemcpy", hipMemcpy(t.train.master.p, master.data(), sizeof(float) * n, hipMemcpyHostToDevice));
+    }
   } else if (t.wi) {
     std::vector<float> tmp((size_t)n);
     for (int64_t r = 0; r < rows; r++) std::memcpy(&tmp[r * H], data + src_row(r) * H, sizeof(float) * H);
@@ -472,7 +480,78 @@ int upload_f32(dn_ctx *c, TensorSlot &t, const float *data, int64_t n) {
   t.set = true;
   return DN_OK;
 }
-}  // namespace
+// Validation (forward.go:142-196) and staging of a host batch.
+int stage_batch(dn_ctx *c, int nseq, const int32_t *seq_len, const int32_t *ids, const int32_t *pos,
+                const int32_t *opt_id, const int32_t *nmask, const int32_t *mask_pos, int logits_cap, int *R_out,
+                int64_t *T_out) {
+  if (nseq < 0 || (nseq > 0 && (!seq_len || !ids || !pos || !nmask)))
+    return fail(c, DN_INVALID_ARG, "decide_hip: dn_forward: NULL argument");
+  const Config &g = c->cfg;
+  // Validation, forward.go:142-196.
+  std::vector<int32_t> row_tok;
+  int64_t T = 0, mp = 0;
+  for (int si = 0; si < nseq; si++) {
+    const int n = seq_len[si];
+    if (n <= 0) return fail(c, DN_INVALID_ARG, "nn: malformed sequence " + std::to_string(si));
+    if (n > 8192) return fail(c, DN_UNSUPPORTED, "decide_hip: sequence " + std::to_string(si) + " is longer than 8192 tokens");
+    if (nmask[si] <= 0) return fail(c, DN_INVALID_ARG, "nn: sequence " + std::to_string(si) + " has no options");
+    for (int k = 0; k < nmask[si]; k++) {
+      const int m = mask_pos[mp + k];
+      if (m < 0 || m >= n)
+        return fail(c, DN_INVALID_ARG, "nn: sequence " + std::to_string(si) + " mask position " +
+                                           std::to_string(m) + " out of range");
+      row_tok.push_back((int32_t)(T + m));
+    }
+    mp += nmask[si];
+    T += n;
+  }
+  if (T > (1 << 30)) return fail(c, DN_UNSUPPORTED, "decide_hip: batch too large");
+  for (int64_t t = 0; t < T; t++)
+    if (ids[t] < 0 || ids[t] >= g.vocab)
+      return fail(c, DN_INVALID_ARG, "nn: token id " + std::to_string(ids[t]) + " out of range");
+  // The attention kernel packs (option id + 1, position) into 16 bits each.
+  for (int64_t t = 0; t < T; t++) {
+    if (pos[t] < 0 || pos[t] > 0xffff)
+      return fail(c, DN_UNSUPPORTED, "decide_hip: position id " + std::to_string(pos[t]) + " outside [0, 65535]");
+    if (opt_id && (opt_id[t] < -1 || opt_id[t] > 32765))
+      return fail(c, DN_UNSUPPORTED, "decide_hip: option id " + std::to_string(opt_id[t]) + " outside [-1, 32765]");
+  }
+  const int R = (int)row_tok.size();
+  *R_out = R;
+  if (logits_cap < R) return fail(c, DN_INVALID_ARG, "decide_hip: logits buffer holds fewer than " +
+                                                         std::to_string(R) + " values");
+  *T_out = T;
+  if (T == 0) return DN_OK;
+  (void)hipSetDevice(c->device);
+  hipStream_t s = c->stream;
+  HIPCHK(c, "hipMalloc", ensure(c->ids, sizeof(int) * T));
+  HIPCHK(c, "hipMalloc", ensure(c->pos, sizeof(int) * T));
+  HIPCHK(c, "hipMalloc", ensure(c->opt, sizeof(int) * T));
+  HIPCHK(c, "hipMalloc", ensure(c->rowtok, sizeof(int) * R));
+  HIPCHK(c, "hipMalloc", ensure(c->logits, sizeof(float) * R));
+  int rc = ensure_err_flag(c);
+  if (rc) return rc;
+  HIPCHK(c, "hipMemsetAsync", hipMemsetAsync(c->err_flag.p, 0, sizeof(int), s));
+  HIPCHK(c, "hipMemcpyAsync", hipMemcpyAsync(c->ids.p, ids, sizeof(int) * T, hipMemcpyHostToDevice, s));
+  HIPCHK(c, "hipMemcpyAsync", hipMemcpyAsync(c->pos.p, pos, sizeof(int) * T, hipMemcpyHostToDevice, s));
+  if (opt_id)
+    HIPCHK(c, "hipMemcpyAsync", hipMemcpyAsync(c->opt.p, opt_id, sizeof(int) * T, hipMemcpyHostToDevice, s));
+  HIPCHK(c, "hipMemcpyAsync",
+         hipMemcpyAsync(c->rowtok.p, row_tok.data(), sizeof(int) * R, hipMemcpyHostToDevice, s));
+  return DN_OK;
+}
+
+int finish_forward(dn_ctx *c, int R, float *logits) {
+  hipStream_t s = c->stream;
+  HIPCHK(c, "hipMemcpyAsync", hipMemcpyAsync(logits, c->logits.p, sizeof(float) * R, hipMemcpyDeviceToHost, s));
+  int flag = 0;
+  HIPCHK(c, "hipMemcpyAsync", hipMemcpyAsync(&flag, c->err_flag.p, sizeof(int), hipMemcpyDeviceToHost, s));
+  HIPCHK(c, "hipStreamSynchronize", hipStreamSynchronize(s));
+  if (flag) return fail(c, DN_DEVICE_ERROR, "decide_hip: device saw an out-of-range index after validation");
+  return DN_OK;
+}
+
+}  // namespace dnh
 
 extern "C" {
 
@@ -518,7 +597,8 @@ void dn_close(dn_ctx *c) {
   if (!c) return;
   (void)hipSetDevice(c->device);
   if (c->stream) (void)hipStreamSynchronize(c->stream);
-  for (auto &kv : c->w) release(kv.second.buf);
+  for (auto &kv : c->w) release_slot(kv.second);
+  release_train(c->tr);
   for (hipEvent_t e : c->probe_pool) (void)hipEventDestroy(e);
   DevBuf *bufs[] = {&c->inv_freq, &c->h,     &c->xn,       &c->qkv,         &c->ctxb,     &c->act,
                     &c->rope,     &c->kinfo, &c->ids,      &c->pos,         &c->opt,      &c->rowtok,
@@ -551,8 +631,10 @@ int dn_set_config(dn_ctx *c, int hidden, int inter, int heads, int layers, int v
     return fail(c, DN_UNSUPPORTED, "decide_hip: this build implements head_dim 64, hidden % 256 == 0 (<= 1024) "
                                    "and intermediate % 64 == 0");
   (void)hipSetDevice(c->device);
-  for (auto &kv : c->w) release(kv.second.buf);
+  for (auto &kv : c->w) release_slot(kv.second);
   c->w.clear();
+  release_train(c->tr);
+  c->tr = TrainState();
   Config &g = c->cfg;
   g.hidden = hidden;
   g.inter = inter;
@@ -594,7 +676,17 @@ int dn_upload_tensor_bf16(dn_ctx *c, const char *name, const uint16_t *bits, int
     }
     return upload_f32(c, *t, f.data(), n);
   }
+  if (c->tr.enabled) {
+    // Training keeps fp32 masters: widen exactly and take the float path.
+    std::vector<float> f((size_t)n);
+    for (int64_t i = 0; i < n; i++) {
+      const uint32_t u = (uint32_t)bits[i] << 16;
+      std::memcpy(&f[i], &u, 4);
+    }
+    return upload_f32(c, *t, f.data(), n);
+  }
   (void)hipSetDevice(c->device);
+  t->train.wt_valid = false;
   HIPCHK(c, "hipMalloc", ensure(t->buf, (size_t)n * 2));
   if (t->wi) {
     const int64_t H = c->cfg.hidden, I = c->cfg.inter;
@@ -630,68 +722,15 @@ int dn_forward(dn_ctx *c, int nseq, const int32_t *seq_len, const int32_t *ids, 
   c->err.clear();
   int rc = check_ready(c);
   if (rc) return rc;
-  if (nseq < 0 || (nseq > 0 && (!seq_len || !ids || !pos || !nmask)))
-    return fail(c, DN_INVALID_ARG, "decide_hip: dn_forward: NULL argument");
-  const Config &g = c->cfg;
-  // Validation, forward.go:142-196.
-  std::vector<int32_t> row_tok;
-  int64_t T = 0, mp = 0;
-  for (int si = 0; si < nseq; si++) {
-    const int n = seq_len[si];
-    if (n <= 0) return fail(c, DN_INVALID_ARG, "nn: malformed sequence " + std::to_string(si));
-    if (n > 8192) return fail(c, DN_UNSUPPORTED, "decide_hip: sequence " + std::to_string(si) + " is longer than 8192 tokens");
-    if (nmask[si] <= 0) return fail(c, DN_INVALID_ARG, "nn: sequence " + std::to_string(si) + " has no options");
-    for (int k = 0; k < nmask[si]; k++) {
-      const int m = mask_pos[mp + k];
-      if (m < 0 || m >= n)
-        return fail(c, DN_INVALID_ARG, "nn: sequence " + std::to_string(si) + " mask position " +
-                                           std::to_string(m) + " out of range");
-      row_tok.push_back((int32_t)(T + m));
-    }
-    mp += nmask[si];
-    T += n;
-  }
-  if (T > (1 << 30)) return fail(c, DN_UNSUPPORTED, "decide_hip: batch too large");
-  for (int64_t t = 0; t < T; t++)
-    if (ids[t] < 0 || ids[t] >= g.vocab)
-      return fail(c, DN_INVALID_ARG, "nn: token id " + std::to_string(ids[t]) + " out of range");
-  // The attention kernel packs (option id + 1, position) into 16 bits each.
-  for (int64_t t = 0; t < T; t++) {
-    if (pos[t] < 0 || pos[t] > 0xffff)
-      return fail(c, DN_UNSUPPORTED, "decide_hip: position id " + std::to_string(pos[t]) + " outside [0, 65535]");
-    if (opt_id && (opt_id[t] < -1 || opt_id[t] > 32765))
-      return fail(c, DN_UNSUPPORTED, "decide_hip: option id " + std::to_string(opt_id[t]) + " outside [-1, 32765]");
-  }
-  const int R = (int)row_tok.size();
-  if (logits_cap < R) return fail(c, DN_INVALID_ARG, "decide_hip: logits buffer holds fewer than " +
-                                                         std::to_string(R) + " values");
-  if (T == 0) return DN_OK;
-  (void)hipSetDevice(c->device);
-  hipStream_t s = c->stream;
-  HIPCHK(c, "hipMalloc", ensure(c->ids, sizeof(int) * T));
-  HIPCHK(c, "hipMalloc", ensure(c->pos, sizeof(int) * T));
-  HIPCHK(c, "hipMalloc", ensure(c->opt, sizeof(int) * T));
-  HIPCHK(c, "hipMalloc", ensure(c->rowtok, sizeof(int) * R));
-  HIPCHK(c, "hipMalloc", ensure(c->logits, sizeof(float) * R));
-  rc = ensure_err_flag(c);
-  if (rc) return rc;
-  HIPCHK(c, "hipMemsetAsync", hipMemsetAsync(c->err_flag.p, 0, sizeof(int), s));
-  HIPCHK(c, "hipMemcpyAsync", hipMemcpyAsync(c->ids.p, ids, sizeof(int) * T, hipMemcpyHostToDevice, s));
-  HIPCHK(c, "hipMemcpyAsync", hipMemcpyAsync(c->pos.p, pos, sizeof(int) * T, hipMemcpyHostToDevice, s));
-  if (opt_id)
-    HIPCHK(c, "hipMemcpyAsync", hipMemcpyAsync(c->opt.p, opt_id, sizeof(int) * T, hipMemcpyHostToDevice, s));
-  HIPCHK(c, "hipMemcpyAsync",
-         hipMemcpyAsync(c->rowtok.p, row_tok.data(), sizeof(int) * R, hipMemcpyHostToDevice, s));
+  int R = 0;
+  int64_t T = 0;
+  rc = stage_batch(c, nseq, seq_len, ids, pos, opt_id, nmask, mask_pos, logits_cap, &R, &T);
+  if (rc || T == 0) return rc;
   rc = forward_core(c, nseq, seq_len, (const int32_t *)c->ids.p, (const int32_t *)c->pos.p,
                     opt_id ? (const int32_t *)c->opt.p : nullptr, R, (const int32_t *)c->rowtok.p,
-                    (float *)c->logits.p);
+                    (float *)c->logits.p, false);
   if (rc) return rc;
-  HIPCHK(c, "hipMemcpyAsync", hipMemcpyAsync(logits, c->logits.p, sizeof(float) * R, hipMemcpyDeviceToHost, s));
-  int flag = 0;
-  HIPCHK(c, "hipMemcpyAsync", hipMemcpyAsync(&flag, c->err_flag.p, sizeof(int), hipMemcpyDeviceToHost, s));
-  HIPCHK(c, "hipStreamSynchronize", hipStreamSynchronize(s));
-  if (flag) return fail(c, DN_DEVICE_ERROR, "decide_hip: device saw an out-of-range index after validation");
-  return DN_OK;
+  return finish_forward(c, R, logits);
 }
 
 int dn_forward_device(dn_ctx *c, int nseq, const int32_t *seq_len, const int32_t *d_ids, const int32_t *d_pos,
@@ -708,7 +747,7 @@ int dn_forward_device(dn_ctx *c, int nseq, const int32_t *seq_len, const int32_t
       return fail(c, DN_UNSUPPORTED, "decide_hip: sequence " + std::to_string(s) + " is longer than 8192 tokens");
   }
   (void)hipSetDevice(c->device);
-  return forward_core(c, nseq, seq_len, d_ids, d_pos, d_opt_id, nrows, d_row_tok, d_logits);
+  return forward_core(c, nseq, seq_len, d_ids, d_pos, d_opt_id, nrows, d_row_tok, d_logits, false);
 }
 
 int dn_check_device_errors(dn_ctx *c) {

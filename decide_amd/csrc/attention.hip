@@ -503,11 +503,16 @@ __global__ __launch_bounds__(64 * QW) __attribute__((amdgpu_waves_per_eu(QT == 1
     b = NBUF == 2 ? b ^ 1 : 0;
   }
 
-  // Normalise and store ctx[token][head*64 + d].
+  // Normalise and store ctx[token][head*64 + d]; in training also the
+  // softmax denominator in log2 form (the backward recomputes P from it).
 #pragma unroll
   for (int t = 0; t < QT; t++) {
     const float l_tot = l_run[t] + __shfl_xor(l_run[t], 32);
     const float inv = 1.0f / l_tot;
+    if (a.lse && qvalid[t] && lh == 0) {
+      const int q = q0 + (wave * QT + t) * 32 + lr;
+      a.lse[(size_t)(base + q) * a.heads + head] = m_run[t] * a.scale_log2 + log2f(l_tot);
+    }
     if (qvalid[t]) {
       const int q = q0 + (wave * QT + t) * 32 + lr;
       T *out = (T *)a.ctx + (size_t)(base + q) * H + head * D;
@@ -603,6 +608,538 @@ __global__ void chunk_summary_kernel(const int *kinfo, const int4 *desc, ChunkIn
   out[c] = ci;
 }
 
+// ---------------------------------------------------------------------------
+// Attention backward: the reference's attnBwd (backward.go:117-159) with the
+// RoPE inverse (backward.go:77-81), recomputing P instead of keeping it:
+//   P = 2^(s*c - lse) (c = scale*log2 e; lse from the forward), masked -> 0
+//   dP = dO . V^T,  D = rowsum(dO * O) (= sum_j P dP),  dS = P * (dP - D) * scale
+//   dQ = dS . K,    dK = dS^T . Q,    dV = P^T . dO
+// Two kernels, neither with atomics:
+//   * attn_bwd_dq_kernel is query-major (the forward's work items, tile list
+//     and tile classes): S^T = K.Q^T and dP^T = V.dO^T put one query per lane
+//     pair, so lse and D are per-lane scalars; dQ^T += K^T . dS^T uses dS^T
+//     straight from registers (keys permuted in the staged K^T, as the forward
+//     does for V^T). It also writes D for the second kernel.
+//   * attn_bwd_dkdv_kernel is key-major (128 keys of one (sequence, head) per
+//     workgroup, one key per lane pair): S = Q.K^T and dP = dO.V^T put one key
+//     per lane, and dV^T += dO^T . P, dK^T += Q^T . dS take P and dS from
+//     registers. Query tiles with no allowed pair for any wave are skipped by
+//     the same chunk classes as the forward.
+// Every tile is staged row-major (RoPE applied to q and k), and the
+// transposed, key-permuted copy an MFMA operand needs is built from it in LDS.
+
+
+// One 64-row x 64-d tile of rows r0.. of a row-major [tokens x ld] array, in
+// registers between load and store. Item it of the 256 threads is (row,
+// 16-byte chunk c and its RoPE partner c + 32 elements): bf16 4 chunks per
+// half row, fp32 8.
+template <class T>
+struct RowStage {
+  static constexpr int NI = sizeof(T) == 2 ? 1 : 2;
+  uint4 lo[NI], hi[NI];
+  float4 c0[NI], c1[NI], s0[NI], s1[NI];
+};
+
+template <class T, bool ROT>
+__device__ __forceinline__ void rows_load(RowStage<T> &st, const T *src, int ld, int base, int r0, int n,
+                                          const float *cos_t, const float *sin_t, const int *kinfo, int tid) {
+  constexpr int EL = 16 / sizeof(T), CPH = 32 / EL;  // elements per chunk, chunks per half row
+#pragma unroll
+  for (int j = 0; j < RowStage<T>::NI; j++) {
+    const int it = tid + 256 * j, row = it / CPH, c = it % CPH;
+    const bool ok = r0 + row < n;
+    const size_t tok = (size_t)(base + min(r0 + row, n - 1));
+    const T *p = src + tok * ld;
+    st.lo[j] = keep_if(ok, *(const uint4 *)(p + EL * c));
+    st.hi[j] = keep_if(ok, *(const uint4 *)(p + 32 + EL * c));
+    if constexpr (ROT) {
+      const size_t pos = (size_t)(kinfo[tok] & 0xffff);
+      st.c0[j] = *(const float4 *)(cos_t + pos * 32 + EL * c);
+      st.s0[j] = *(const float4 *)(sin_t + pos * 32 + EL * c);
+      if constexpr (sizeof(T) == 2) {
+        st.c1[j] = *(const float4 *)(cos_t + pos * 32 + EL * c + 4);
+        st.s1[j] = *(const float4 *)(sin_t + pos * 32 + EL * c + 4);
+      }
+    }
+  }
+}
+
+// Stores the tile row-major: row r at dst + r*ROW, d-contiguous.
+template <class T, bool ROT>
+__device__ __forceinline__ void rows_store(const RowStage<T> &st, char *dst, int tid) {
+  constexpr int EL = 16 / sizeof(T), CPH = 32 / EL, ROW = D * sizeof(T) + 16;
+#pragma unroll
+  for (int j = 0; j < RowStage<T>::NI; j++) {
+    const int it = tid + 256 * j, row = it / CPH, c = it % CPH;
+    uint4 lo = st.lo[j], hi = st.hi[j];
+    if constexpr (ROT) {
+      if constexpr (sizeof(T) == 2) {
+        const uint32_t l[4] = {lo.x, lo.y, lo.z, lo.w}, h[4] = {hi.x, hi.y, hi.z, hi.w};
+        const float cs[8] = {st.c0[j].x, st.c0[j].y, st.c0[j].z, st.c0[j].w,
+                             st.c1[j].x, st.c1[j].y, st.c1[j].z, st.c1[j].w};
+        const float sn[8] = {st.s0[j].x, st.s0[j].y, st.s0[j].z, st.s0[j].w,
+                             st.s1[j].x, st.s1[j].y, st.s1[j].z, st.s1[j].w};
+        uint32_t po[4], ph[4];
+#pragma unroll
+        for (int w = 0; w < 4; w++) {
+          float a0 = bf_lo(l[w]), a1 = bf_hi(l[w]), b0 = bf_lo(h[w]), b1 = bf_hi(h[w]);
+          rope1(a0, b0, cs[2 * w], sn[2 * w]);
+          rope1(a1, b1, cs[2 * w + 1], sn[2 * w + 1]);
+          po[w] = pack_bf16(a0, a1);
+          ph[w] = pack_bf16(b0, b1);
+        }
+        lo = make_uint4(po[0], po[1], po[2], po[3]);
+        hi = make_uint4(ph[0], ph[1], ph[2], ph[3]);
+      } else {
+        float4 a = *(const float4 *)&lo, b = *(const float4 *)&hi;
+        rope1(a.x, b.x, st.c0[j].x, st.s0[j].x);
+        rope1(a.y, b.y, st.c0[j].y, st.s0[j].y);
+        rope1(a.z, b.z, st.c0[j].z, st.s0[j].z);
+        rope1(a.w, b.w, st.c0[j].w, st.s0[j].w);
+        lo = *(const uint4 *)&a;
+        hi = *(const uint4 *)&b;
+      }
+    }
+    *(uint4 *)(dst + row * ROW + 16 * c) = lo;
+    *(uint4 *)(dst + row * ROW + (32 * sizeof(T)) + 16 * c) = hi;
+  }
+}
+
+// Builds the transposed copy TT[d][row] of a row-major tile R (both with
+// D*sizeof(T)+16-byte rows). bf16: rows (2p, 2p+1) share a 32-bit word, and
+// within each 16-row group the 4-row runs are in the order 0-3, 8-11, 4-7,
+// 12-15 (the order one lane feeds a k step from the S^T / S accumulators).
+// fp32: plain row order; the reader permutes per k step.
+template <class T>
+__device__ __forceinline__ void build_transposed(const char *R, char *TT, int tid) {
+  constexpr int ROW = D * sizeof(T) + 16;
+  if constexpr (sizeof(T) == 2) {
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      const int it = tid + 256 * j, p = it & 31, d = it >> 5;
+      const uint32_t lo = *(const uint16_t *)(R + (2 * p) * ROW + 2 * d);
+      const uint32_t hi = *(const uint16_t *)(R + (2 * p + 1) * ROW + 2 * d);
+      const int lp = p & 7, q4 = lp >> 1;
+      const int pw = (p & ~7) + ((((q4 & 1) << 1) | (q4 >> 1)) << 1) + (lp & 1);
+      *(uint32_t *)(TT + d * ROW + 4 * pw) = lo | (hi << 16);
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < 16; j++) {
+      const int it = tid + 256 * j, r = it & 63, d = it >> 6;
+      *(float *)(TT + d * ROW + 4 * r) = *(const float *)(R + r * ROW + 4 * d);
+    }
+  }
+}
+
+// MFMA operand of k step ks from the row-major tile (row `row`, k = d).
+template <class T>
+__device__ __forceinline__ typename Mfma<T>::frag row_frag(const char *R, int row, int ks, int lh) {
+  using MF = Mfma<T>;
+  constexpr int ROW = D * sizeof(T) + 16;
+  return *(const typename MF::frag *)(R + row * ROW + (ks * MF::KSTEP + lh * MF::SLOTS) * (int)sizeof(T));
+}
+
+// MFMA operand of k step ks (over the 64 tile rows) from the transposed tile
+// (row d), matching the register order of an S^T / S accumulator pair.
+template <class T>
+__device__ __forceinline__ typename Mfma<T>::frag t_frag(const char *TT, int d, int ks, int lh) {
+  using MF = Mfma<T>;
+  constexpr int ROW = D * sizeof(T) + 16;
+  const char *row = TT + d * ROW;
+  if constexpr (sizeof(T) == 2) {
+    return *(const typename MF::frag *)(row + 32 * ks + 16 * lh);
+  } else {
+    const int r = ks & 15;
+    return *(const float *)(row + 4 * (32 * (ks >> 4) + 8 * (r >> 2) + 4 * lh + (r & 3)));
+  }
+}
+
+// The B operand of k step ks taken from a pair of 32x32 accumulators (the 64
+// tile rows of the k dimension).
+template <class T>
+__device__ __forceinline__ typename Mfma<T>::frag acc_frag(const f32x16 (&x)[2], int ks) {
+  typename Mfma<T>::frag f;
+  if constexpr (sizeof(T) == 2) {
+    const int ti = ks >> 1, r0 = (ks & 1) * 8;
+#pragma unroll
+    for (int u = 0; u < 8; u++) f[u] = (bf16)x[ti][r0 + u];
+  } else {
+    f = x[ks >> 4][ks & 15];
+  }
+  return f;
+}
+
+// Writes a lane's 64-d row (two 32-d accumulator blocks of one token, d =
+// 32*blk + mfma_row(e)) to dst[d], with the inverse RoPE rotation of the
+// token's position when cs is given (pairs (d, d+32) are the same register
+// of the two blocks).
+template <class T>
+__device__ __forceinline__ void store_row64(f32x16 (&x)[2], T *dst, const float *cs, const float *sn, int lh) {
+  if (cs) {
+#pragma unroll
+    for (int e = 0; e < 16; e++) {
+      const int d = 8 * (e >> 2) + 4 * lh + (e & 3);
+      float u = x[0][e], v = x[1][e];
+      rope1(u, v, cs[d], -sn[d]);
+      x[0][e] = u;
+      x[1][e] = v;
+    }
+  }
+#pragma unroll
+  for (int b = 0; b < 2; b++)
+#pragma unroll
+    for (int g = 0; g < 4; g++) {
+      const int d0 = b * 32 + 8 * g + 4 * lh;
+      if constexpr (sizeof(T) == 2) {
+        bf16x4 o = {(bf16)x[b][4 * g], (bf16)x[b][4 * g + 1], (bf16)x[b][4 * g + 2], (bf16)x[b][4 * g + 3]};
+        *(bf16x4 *)(dst + d0) = o;
+      } else {
+        *(float4 *)(dst + d0) = make_float4(x[b][4 * g], x[b][4 * g + 1], x[b][4 * g + 2], x[b][4 * g + 3]);
+      }
+    }
+}
+
+template <class T>
+__global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnBwdArgs a) {
+  using MF = Mfma<T>;
+  typedef typename MF::frag frag;
+  constexpr int ROW = D * sizeof(T) + 16, NKS = D / MF::KSTEP, NPV = KTILE / MF::KSTEP;
+  __shared__ __attribute__((aligned(16))) char sK[KTILE * ROW];
+  __shared__ __attribute__((aligned(16))) char sV[KTILE * ROW];
+  __shared__ __attribute__((aligned(16))) char sKT[D * ROW];
+  __shared__ __attribute__((aligned(16))) int sInfo[KTILE];
+  __shared__ uint32_t sCode[ATTN_MAXKT];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lr = lane & 31, lh = lane >> 5;
+  const int total = a.nwork * a.heads, bid = blockIdx.x;
+  const int logical = total % 8 == 0 ? (bid % 8) * (total / 8) + bid / 8 : bid;
+  const int wi = logical / a.heads, head = logical % a.heads;
+  const int4 wk = a.work[wi];
+  const int s = wk.x, q0 = wk.y;
+  const int n = a.seq_len[s], base = a.seq_off[s];
+  const int H = a.H, ld = 3 * H;
+  const T *qkv = (const T *)a.qkv;
+  const int nkt = (n + KTILE - 1) / KTILE;
+  const uint32_t *codes = a.codes + (size_t)wi * ATTN_MAXKT;
+  for (int kt = tid; kt < nkt; kt += 256) sCode[kt] = codes[kt];
+
+  // The lane's query: rotated Q^T and dO^T operands, lse, D.
+  const int q = q0 + wave * 32 + lr;
+  const bool qvalid = q < n;
+  const size_t qtok = (size_t)(base + (qvalid ? q : n - 1));
+  const int qinfo = a.kinfo[qtok], qopt = (qinfo >> 16) - 1, qpos = qinfo & 0xffff;
+  const float *cq = a.cos_t + (size_t)qpos * 32, *sq = a.sin_t + (size_t)qpos * 32;
+  frag qf[NKS], dof[NKS];
+  float dsum = 0.0f;
+  {
+    const T *qrow = qkv + qtok * ld + head * D;
+    const T *orow = (const T *)a.ctx + qtok * H + head * D;
+    const T *drow = (const T *)a.dctx + qtok * H + head * D;
+#pragma unroll
+    for (int ks = 0; ks < NKS; ks++) {
+      const int k0 = ks * MF::KSTEP + lh * MF::SLOTS;
+      qf[ks] = *(const frag *)(qrow + k0);
+      dof[ks] = *(const frag *)(drow + k0);
+      const frag of = *(const frag *)(orow + k0);
+      if constexpr (sizeof(T) == 2) {
+#pragma unroll
+        for (int u = 0; u < 8; u++) dsum += (float)dof[ks][u] * (float)of[u];
+      } else {
+        dsum += dof[ks] * of;
+      }
+    }
+#pragma unroll
+    for (int ks = 0; ks < NKS / 2; ks++)
+#pragma unroll
+      for (int u = 0; u < MF::SLOTS; u++) {
+        const int i = ks * MF::KSTEP + lh * MF::SLOTS + u;
+        float x, y;
+        if constexpr (sizeof(T) == 2) {
+          x = (float)qf[ks][u];
+          y = (float)qf[ks + NKS / 2][u];
+        } else {
+          x = qf[ks];
+          y = qf[ks + NKS / 2];
+        }
+        rope1(x, y, cq[i], sq[i]);
+        if constexpr (sizeof(T) == 2) {
+          qf[ks][u] = (bf16)x;
+          qf[ks + NKS / 2][u] = (bf16)y;
+        } else {
+          qf[ks] = x;
+          qf[ks + NKS / 2] = y;
+        }
+      }
+  }
+  dsum += __shfl_xor(dsum, 32);
+  if (qvalid && lh == 0) a.dsum[qtok * a.heads + head] = dsum;
+  const float lse = a.lse[qtok * a.heads + head];
+  const float c = a.scale_log2;
+
+  f32x16 dq[2];
+#pragma unroll
+  for (int b = 0; b < 2; b++)
+#pragma unroll
+    for (int e = 0; e < 16; e++) dq[b][e] = 0.0f;
+
+  __syncthreads();  // sCode
+  const unsigned win2 = a.sliding ? (unsigned)(2 * a.half_window) : 0xffffffffu;
+  for (int kt = a.first[wi]; kt < nkt; kt++) {
+    if (sCode[kt] == 0) continue;
+    const int k0 = kt * KTILE;
+    {
+      RowStage<T> sk, sv;
+      rows_load<T, true>(sk, qkv + H + head * D, ld, base, k0, n, a.cos_t, a.sin_t, a.kinfo, tid);
+      rows_load<T, false>(sv, qkv + 2 * H + head * D, ld, base, k0, n, nullptr, nullptr, nullptr, tid);
+      const int info = (tid < KTILE && k0 + tid < n) ? a.kinfo[base + k0 + tid] : 0;
+      __syncthreads();  // the previous tile's reads are done
+      rows_store<T, true>(sk, sK, tid);
+      rows_store<T, false>(sv, sV, tid);
+      if (tid < KTILE) sInfo[tid] = info;
+    }
+    __syncthreads();
+    build_transposed<T>(sK, sKT, tid);
+    __syncthreads();
+
+    const int mycode = __builtin_amdgcn_readfirstlane((sCode[kt] >> (4 * wave)) & 15);
+    if (mycode == 0) continue;
+    const int hcls[2] = {mycode & 3, (mycode >> 2) & 3};
+    f32x16 sT[2], dpT[2];
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+      for (int e = 0; e < 16; e++) {
+        sT[i][e] = 0.0f;
+        dpT[i][e] = 0.0f;
+      }
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+      if (hcls[i] == 0) continue;
+#pragma unroll
+      for (int ks = 0; ks < NKS; ks++) {
+        sT[i] = MF::mma(row_frag<T>(sK, i * 32 + lr, ks, lh), qf[ks], sT[i]);
+        dpT[i] = MF::mma(row_frag<T>(sV, i * 32 + lr, ks, lh), dof[ks], dpT[i]);
+      }
+    }
+    // P^T and dS^T in place of sT (per element: key 32i + 8(e/4) + 4lh + e%4).
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+      if (hcls[i] == 0) continue;
+#pragma unroll
+      for (int g = 0; g < 4; g++) {
+        const int kl = i * 32 + 8 * g + 4 * lh;
+        const int4 inf4 = *(const int4 *)(sInfo + kl);
+        const int inf[4] = {inf4.x, inf4.y, inf4.z, inf4.w};
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+          const int ko = (inf[u] >> 16) - 1, kp = inf[u] & 0xffff;
+          const bool ok = qvalid & (k0 + kl + u < n) & ((ko == -1) | (ko == qopt)) &
+                          ((unsigned)(kp - qpos + a.half_window) <= win2);
+          const int e = 4 * g + u;
+          const float p = ok ? __builtin_amdgcn_exp2f(fmaf(sT[i][e], c, -lse)) : 0.0f;
+          sT[i][e] = p * (dpT[i][e] - dsum) * a.scale;
+        }
+      }
+    }
+    // dQ^T += K^T . dS^T
+#pragma unroll
+    for (int ks = 0; ks < NPV; ks++) {
+      if (hcls[ks / (NPV / 2)] == 0) continue;
+      const frag df = acc_frag<T>(sT, ks);
+#pragma unroll
+      for (int b = 0; b < 2; b++) dq[b] = MF::mma(t_frag<T>(sKT, b * 32 + lr, ks, lh), df, dq[b]);
+    }
+  }
+  if (qvalid) store_row64<T>(dq, (T *)a.dqkv + qtok * ld + head * D, cq, sq, lh);
+}
+
+template <class T>
+__global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(AttnBwdArgs a) {
+  using MF = Mfma<T>;
+  typedef typename MF::frag frag;
+  constexpr int ROW = D * sizeof(T) + 16, NKS = D / MF::KSTEP, NPV = KTILE / MF::KSTEP;
+  __shared__ __attribute__((aligned(16))) char sQ[KTILE * ROW];
+  __shared__ __attribute__((aligned(16))) char sQT[D * ROW];
+  __shared__ __attribute__((aligned(16))) char sO[KTILE * ROW];
+  __shared__ __attribute__((aligned(16))) char sOT[D * ROW];
+  __shared__ __attribute__((aligned(16))) int sInfo[KTILE];
+  __shared__ __attribute__((aligned(16))) float sL[KTILE], sD[KTILE];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lr = lane & 31, lh = lane >> 5;
+  const int total = a.nwork * a.heads, bid = blockIdx.x;
+  const int logical = total % 8 == 0 ? (bid % 8) * (total / 8) + bid / 8 : bid;
+  const int wi = logical / a.heads, head = logical % a.heads;
+  const int4 wk = a.work[wi];
+  const int s = wk.x, kw0 = wk.y;  // this workgroup's 128 keys start at kw0
+  const int n = a.seq_len[s], base = a.seq_off[s];
+  const int H = a.H, ld = 3 * H;
+  const T *qkv = (const T *)a.qkv;
+  const int nch = (n + 31) / 32, cbase = a.chunk_off[s];
+
+  // The lane's key: rotated K and V operands (B operands: column = key).
+  const int k = kw0 + wave * 32 + lr;
+  const bool kvalid = k < n;
+  const size_t ktok = (size_t)(base + (kvalid ? k : n - 1));
+  const int kinfo = a.kinfo[ktok], kopt = (kinfo >> 16) - 1, kpos = kinfo & 0xffff;
+  const float *ck = a.cos_t + (size_t)kpos * 32, *sk = a.sin_t + (size_t)kpos * 32;
+  frag kf[NKS], vf[NKS];
+  {
+    const T *krow = qkv + ktok * ld + H + head * D;
+    const T *vrow = qkv + ktok * ld + 2 * H + head * D;
+#pragma unroll
+    for (int ks = 0; ks < NKS; ks++) {
+      const int k0 = ks * MF::KSTEP + lh * MF::SLOTS;
+      kf[ks] = *(const frag *)(krow + k0);
+      vf[ks] = *(const frag *)(vrow + k0);
+    }
+#pragma unroll
+    for (int ks = 0; ks < NKS / 2; ks++)
+#pragma unroll
+      for (int u = 0; u < MF::SLOTS; u++) {
+        const int i = ks * MF::KSTEP + lh * MF::SLOTS + u;
+        float x, y;
+        if constexpr (sizeof(T) == 2) {
+          x = (float)kf[ks][u];
+          y = (float)kf[ks + NKS / 2][u];
+        } else {
+          x = kf[ks];
+          y = kf[ks + NKS / 2];
+        }
+        rope1(x, y, ck[i], sk[i]);
+        if constexpr (sizeof(T) == 2) {
+          kf[ks][u] = (bf16)x;
+          kf[ks + NKS / 2][u] = (bf16)y;
+        } else {
+          kf[ks] = x;
+          kf[ks + NKS / 2] = y;
+        }
+      }
+  }
+  // Key chunk of each wave (empty past the sequence end).
+  const ChunkInfo empty = {0, 0, 1, 0, 0, 0, 0, 0};
+  ChunkInfo kc[4];
+#pragma unroll
+  for (int w = 0; w < 4; w++) {
+    const int ch = kw0 / 32 + w;
+    kc[w] = ch < nch ? a.chunks[cbase + ch] : empty;
+  }
+
+  f32x16 dk[2], dv[2];
+#pragma unroll
+  for (int b = 0; b < 2; b++)
+#pragma unroll
+    for (int e = 0; e < 16; e++) {
+      dk[b][e] = 0.0f;
+      dv[b][e] = 0.0f;
+    }
+  const float c = a.scale_log2;
+  const unsigned win2 = a.sliding ? (unsigned)(2 * a.half_window) : 0xffffffffu;
+  const int nqt = (n + KTILE - 1) / KTILE;
+  for (int qt = 0; qt < nqt; qt++) {
+    const int q0 = qt * KTILE;
+    const ChunkInfo qc0 = a.chunks[cbase + 2 * qt];
+    const ChunkInfo qc1 = 2 * qt + 1 < nch ? a.chunks[cbase + 2 * qt + 1] : empty;
+    int any = 0, hcls[2] = {0, 0};
+#pragma unroll
+    for (int w = 0; w < 4; w++) {
+      const int c0 = tile_class(qc0, kc[w], a.sliding, a.half_window);
+      const int c1 = tile_class(qc1, kc[w], a.sliding, a.half_window);
+      any |= c0 | c1;
+      if (w == wave) {
+        hcls[0] = c0;
+        hcls[1] = c1;
+      }
+    }
+    if (any == 0) continue;
+    {
+      RowStage<T> sq, so;
+      rows_load<T, true>(sq, qkv + head * D, ld, base, q0, n, a.cos_t, a.sin_t, a.kinfo, tid);
+      rows_load<T, false>(so, (const T *)a.dctx + head * D, H, base, q0, n, nullptr, nullptr, nullptr, tid);
+      int info = 0;
+      float lse = INFINITY, dd = 0.0f;  // rows past the end: P = 2^-inf = 0
+      if (tid < KTILE && q0 + tid < n) {
+        const size_t t = (size_t)(base + q0 + tid);
+        info = a.kinfo[t];
+        lse = a.lse[t * a.heads + head];
+        dd = a.dsum[t * a.heads + head];
+      }
+      __syncthreads();  // the previous tile's reads are done
+      rows_store<T, true>(sq, sQ, tid);
+      rows_store<T, false>(so, sO, tid);
+      if (tid < KTILE) {
+        sInfo[tid] = info;
+        sL[tid] = lse;
+        sD[tid] = dd;
+      }
+    }
+    __syncthreads();
+    build_transposed<T>(sQ, sQT, tid);
+    build_transposed<T>(sO, sOT, tid);
+    __syncthreads();
+    if ((hcls[0] | hcls[1]) == 0) continue;
+
+    f32x16 sc[2], dp[2];
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+      for (int e = 0; e < 16; e++) {
+        sc[i][e] = 0.0f;
+        dp[i][e] = 0.0f;
+      }
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+      if (hcls[i] == 0) continue;
+#pragma unroll
+      for (int ks = 0; ks < NKS; ks++) {
+        sc[i] = MF::mma(row_frag<T>(sQ, i * 32 + lr, ks, lh), kf[ks], sc[i]);
+        dp[i] = MF::mma(row_frag<T>(sO, i * 32 + lr, ks, lh), vf[ks], dp[i]);
+      }
+    }
+    // P (in sc) and dS (in dp); element e is query 32i + 8(e/4) + 4lh + e%4.
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+      if (hcls[i] == 0) continue;
+#pragma unroll
+      for (int g = 0; g < 4; g++) {
+        const int ql = i * 32 + 8 * g + 4 * lh;
+        const int4 inf4 = *(const int4 *)(sInfo + ql);
+        const float4 l4 = *(const float4 *)(sL + ql), d4 = *(const float4 *)(sD + ql);
+        const int inf[4] = {inf4.x, inf4.y, inf4.z, inf4.w};
+        const float lq[4] = {l4.x, l4.y, l4.z, l4.w}, dq4[4] = {d4.x, d4.y, d4.z, d4.w};
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+          const int qo = (inf[u] >> 16) - 1, qp = inf[u] & 0xffff;
+          const bool ok = kvalid & (q0 + ql + u < n) & ((kopt == -1) | (kopt == qo)) &
+                          ((unsigned)(kpos - qp + a.half_window) <= win2);
+          const int e = 4 * g + u;
+          const float p = ok ? __builtin_amdgcn_exp2f(fmaf(sc[i][e], c, -lq[u])) : 0.0f;
+          sc[i][e] = p;
+          dp[i][e] = p * (dp[i][e] - dq4[u]) * a.scale;
+        }
+      }
+    }
+    // dV^T += dO^T . P, dK^T += Q^T . dS
+#pragma unroll
+    for (int ks = 0; ks < NPV; ks++) {
+      if (hcls[ks / (NPV / 2)] == 0) continue;
+      const frag pf = acc_frag<T>(sc, ks), df = acc_frag<T>(dp, ks);
+#pragma unroll
+      for (int b = 0; b < 2; b++) {
+        dv[b] = MF::mma(t_frag<T>(sOT, b * 32 + lr, ks, lh), pf, dv[b]);
+        dk[b] = MF::mma(t_frag<T>(sQT, b * 32 + lr, ks, lh), df, dk[b]);
+      }
+    }
+  }
+  if (kvalid) {
+    T *row = (T *)a.dqkv + ktok * ld + head * D;
+    store_row64<T>(dk, row + H, ck, sk, lh);
+    store_row64<T>(dv, row + 2 * H, nullptr, nullptr, lh);
+  }
+}
+
 }  // namespace
 
 hipError_t launch_attention(int precision, const AttnArgs &a, hipStream_t s) {
@@ -632,5 +1169,19 @@ hipError_t launch_token_info(const int *pos, const int *opt, int *kinfo, int T, 
 hipError_t launch_chunk_summary(const int *kinfo, const int4 *desc, ChunkInfo *out, int nchunks, hipStream_t s) {
   if (nchunks <= 0) return hipSuccess;
   hipLaunchKernelGGL(chunk_summary_kernel, dim3((nchunks + 127) / 128), dim3(128), 0, s, kinfo, desc, out, nchunks);
+  return hipGetLastError();
+}
+
+hipError_t launch_attention_bwd(int precision, const AttnBwdArgs &a, hipStream_t s) {
+  if (a.nwork <= 0) return hipSuccess;
+  static_assert(ATTN_QUERIES == 128 && ATTN_WAVES == 4, "backward kernels use 4-wave, 128-token work items");
+  dim3 grid(a.nwork * a.heads), block(256);
+  if (precision == 1) {
+    hipLaunchKernelGGL(attn_bwd_dq_kernel<bf16>, grid, block, 0, s, a);
+    hipLaunchKernelGGL(attn_bwd_dkdv_kernel<bf16>, grid, block, 0, s, a);
+  } else {
+    hipLaunchKernelGGL(attn_bwd_dq_kernel<float>, grid, block, 0, s, a);
+    hipLaunchKernelGGL(attn_bwd_dkdv_kernel<float>, grid, block, 0, s, a);
+  }
   return hipGetLastError();
 }

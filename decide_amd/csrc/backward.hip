@@ -1,0 +1,581 @@
+// Training kernels other than attention and the GEMMs: the GeGLU forward
+// that keeps the Wi pre-activation, the backward of GeGLU, LayerNorm, the
+// embedding gather and the scoring head, operand transposes for the
+// weight-gradient GEMMs, gradient sums of squares and AdamW.
+//
+// Reference (internal/nn/backward.go, ops.go; internal/train/optim.go):
+//   geglu backward  backward.go:49-61   dwi = [da*gate*gelu'(a) | da*gelu(a)]
+//   layerNormBwd    ops.go:94-135        dx += rs*(g*w - mean(g*w) - xh*mean(g*w*xh)), dw += sum g*xh (+ db)
+//   embeddings      backward.go:96-109   dTok[id] += LN backward of the emb norm, in token order
+//   HeadBackward    backward.go:161-196
+//   GradNorm        optim.go:68-90       float64 sums of squares
+//   Update          optim.go:94-145      AdamW with decoupled weight decay
+// Reductions over rows are two-stage with fixed order (per-block partials,
+// then a sum in block order), so results do not depend on scheduling.
+#include "common.hpp"
+
+namespace {
+
+__device__ __forceinline__ double wave_sum_d(double v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+
+template <class T>
+__device__ __forceinline__ float ld_elem(const T *p) {
+  return (float)*p;
+}
+
+// d gelu(x)/dx = Phi(x) + x phi(x) (geluGrad, ops.go:145-150): float64 in the
+// fp32 build; the bf16 build uses the same erf approximation as its forward.
+template <class T>
+__device__ __forceinline__ float gelu_grad(float x);
+template <>
+__device__ __forceinline__ float gelu_grad<float>(float x) {
+  const double xf = (double)x;
+  const double cdf = 0.5 * (1 + erf(xf * 1.41421356237309504880 / 2));
+  const double pdf = exp(-0.5 * xf * xf) / sqrt(2 * 3.14159265358979323846);
+  return (float)(cdf + xf * pdf);
+}
+template <>
+__device__ __forceinline__ float gelu_grad<bf16>(float x) {
+  const float cdf = 0.5f * (1.0f + erf_as(x * 0.70710678118654752440f));
+  const float pdf = exp2f(-0.5f * x * x * 1.44269504088896341f) * 0.39894228040143267794f;
+  return cdf + x * pdf;
+}
+
+// ---------------------------------------------------------------------------
+// 64 x 64 tiles through LDS: dstT[c][r] = src[r][c] for r < rows_pad (zero
+// for r >= rows), converted to TO; when copy is set also copy[r][c] = src[r][c]
+// (r < rows) in TO. Grid (cols/64, rows_pad/64), 256 threads.
+template <class TI, class TO>
+__global__ __launch_bounds__(256) void transpose_kernel(const TI *src, int rows, int cols, int lds, TO *dstT, int ldt,
+                                                        int rows_pad, TO *copy) {
+  __shared__ float tile[64][65];
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  const int c0 = blockIdx.x * 64, r0 = blockIdx.y * 64;
+#pragma unroll 4
+  for (int j = 0; j < 16; j++) {
+    const int r = r0 + ty + 4 * j, c = c0 + tx;
+    float v = 0.0f;
+    if (r < rows && c < cols) {
+      v = ld_elem(src + (size_t)r * lds + c);
+      if (copy) copy[(size_t)r * cols + c] = (TO)v;
+    }
+    tile[ty + 4 * j][tx] = v;
+  }
+  __syncthreads();
+#pragma unroll 4
+  for (int j = 0; j < 16; j++) {
+    const int c = c0 + ty + 4 * j, r = r0 + tx;
+    if (c < cols && r < rows_pad) dstT[(size_t)c * ldt + r] = (TO)tile[tx][ty + 4 * j];
+  }
+}
+
+// GeGLU on the stored Wi output (rows interleaved in 64-column groups: 32
+// value columns, then the 32 matching gate columns): act[t][32g+r] =
+// gelu(wi[t][64g+r]) * wi[t][64g+32+r] (forward.go:327-336).
+template <class T>
+__global__ void geglu_fwd_kernel(const T *wi, T *act, int rows, int I) {
+  const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= (size_t)rows * I) return;
+  const size_t t = idx / I;
+  const int i = (int)(idx % I), g = i >> 5, r = i & 31;
+  const T *row = wi + t * 2 * I + 64 * g;
+  act[idx] = (T)(gelu_erf<T>(ld_elem(row + r)) * ld_elem(row + 32 + r));
+}
+
+// GeGLU backward (backward.go:49-61) in the interleaved layout.
+template <class T>
+__global__ void geglu_bwd_kernel(const float *dact, const T *wi, T *dwi, int rows, int I) {
+  const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= (size_t)rows * I) return;
+  const size_t t = idx / I;
+  const int i = (int)(idx % I), g = i >> 5, r = i & 31;
+  const T *row = wi + t * 2 * I + 64 * g;
+  T *out = dwi + t * 2 * I + 64 * g;
+  const float a = ld_elem(row + r), gt = ld_elem(row + 32 + r), da = dact[idx];
+  out[r] = (T)(da * gt * gelu_grad<T>(a));
+  out[32 + r] = (T)(da * gelu_erf<T>(a));
+}
+
+// ---------------------------------------------------------------------------
+// LayerNorm backward (layerNormBwd, ops.go:94-135) for bias-free norms over
+// rows of dim <= 1024 (dim % 256 == 0): one wave per row; dx[r] += ..., and
+// this block's partial of dw (sum over its rows of dy*xh) into part[block].
+// The row statistics are recomputed from x as the forward computes them (f64).
+// x rows are x[r] or, with ids, the embedding row tok[ids[r]].
+constexpr int LNB_WAVES = 4;
+__global__ __launch_bounds__(256) void ln_bwd_kernel(float *dx, const float *dy, const float *x, const int *ids,
+                                                     const float *w, float eps, int rows, int dim, float *part) {
+  constexpr int MAXE = 16;  // dim <= 1024: 16 elements per lane
+  __shared__ float sw[LNB_WAVES][1024];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int ne = dim / 64;
+  float pw[MAXE];
+#pragma unroll
+  for (int j = 0; j < MAXE; j++) pw[j] = 0.0f;
+  for (int r = blockIdx.x * LNB_WAVES + wave; r < rows; r += gridDim.x * LNB_WAVES) {
+    const float *xr = ids ? x + (size_t)ids[r] * dim : x + (size_t)r * dim;
+    const float *g = dy + (size_t)r * dim;
+    float xv[MAXE], gv[MAXE];
+    double s = 0;
+#pragma unroll
+    for (int j = 0; j < MAXE; j++)
+      if (j < ne) {
+        xv[j] = xr[lane + 64 * j];
+        gv[j] = g[lane + 64 * j];
+        s += (double)xv[j];
+      }
+    const double mu = wave_sum_d(s) / (double)dim;
+    double v = 0;
+#pragma unroll
+    for (int j = 0; j < MAXE; j++)
+      if (j < ne) {
+        const double d = (double)xv[j] - mu;
+        v += d * d;
+      }
+    const float rs = (float)(1.0 / sqrt(wave_sum_d(v) / (double)dim + (double)eps));
+    const float m = (float)mu;
+    double s1 = 0, s2 = 0;
+#pragma unroll
+    for (int j = 0; j < MAXE; j++)
+      if (j < ne) {
+#pragma clang fp contract(off)
+        const float xh = (xv[j] - m) * rs;
+        const float gw = gv[j] * w[lane + 64 * j];
+        s1 += (double)gw;
+        s2 += (double)(gw * xh);
+        pw[j] += gv[j] * xh;
+        xv[j] = xh;
+      }
+    const float a = (float)(wave_sum_d(s1) / (double)dim), b = (float)(wave_sum_d(s2) / (double)dim);
+    float *o = dx + (size_t)r * dim;
+#pragma unroll
+    for (int j = 0; j < MAXE; j++)
+      if (j < ne) {
+#pragma clang fp contract(off)
+        o[lane + 64 * j] += rs * (gv[j] * w[lane + 64 * j] - a - xv[j] * b);
+      }
+  }
+#pragma unroll
+  for (int j = 0; j < MAXE; j++)
+    if (j < ne) sw[wave][lane + 64 * j] = pw[j];
+  __syncthreads();
+  for (int i = threadIdx.x; i < dim; i += 256) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int q = 0; q < LNB_WAVES; q++) acc += sw[q][i];
+    part[(size_t)blockIdx.x * dim + i] = acc;
+  }
+}
+
+// out[i] += sum over p of part[p * n + i], in p order.
+__global__ void sum_partials_kernel(const float *part, int nparts, int n, float *out) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  float acc = 0.0f;
+  for (int p = 0; p < nparts; p++) acc += part[(size_t)p * n + i];
+  out[i] += acc;
+}
+
+// dst[i] += src[i].
+__global__ void add_kernel(float *dst, const float *src, size_t n) {
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) dst[i] += src[i];
+}
+
+// Embedding gradient: one block per distinct token id; the rows of dE whose
+// token has that id are added to dTok[id] in token order (backward.go:102-108).
+__global__ __launch_bounds__(256) void embed_bwd_kernel(const float *dE, const int *order, const int *seg_start,
+                                                        const int *seg_id, int dim, float *gtok) {
+  const int sgi = blockIdx.x;
+  const int b = seg_start[sgi], e = seg_start[sgi + 1];
+  float *dst = gtok + (size_t)seg_id[sgi] * dim;
+  for (int i = threadIdx.x; i < dim; i += 256) {
+    float acc = dst[i];
+    for (int k = b; k < e; k++) acc += dE[(size_t)order[k] * dim + i];
+    dst[i] = acc;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// HeadBackward (backward.go:161-196), fp32. One 256-thread block per row r:
+// recomputes final_norm (fN), the input_norm statistics, gelu and the scorer
+// norm from the encoder row and the forward's s1 and d (dense output before
+// its bias), then back-propagates dl = dlogits[r]:
+//   ds2 = dl*OutW; dge = LNbwd(ds2); dd = dge*gelu'(d+b); ds1 = dd.DenseW;
+//   dfN = LNbwd(ds1); dRows = LNbwd(dfN) -> dcur[rowTok[r]].
+// Per-row parameter-gradient terms go to contrib (summed over rows by
+// head_param_kernel): [dl*s2 | ds2*xh2 | ds2 | dd | ds1*xh1 | ds1 | dfN*xhF].
+struct HeadBwdArgs {
+  const float *h;         // encoder output [T x H]
+  const int *row_tok;     // [R]
+  const float *s1, *d;    // forward's input_norm output [R x H] and dense output [R x H/2]
+  const float *dlogits;   // [R]
+  int R, H;
+  float eps;
+  const float *final_norm, *in_w, *dense_w, *dense_b, *norm_w, *norm_b, *out_w;
+  float *dcur;            // [T x H], zero except the rows written here
+  float *contrib;         // [R x (4*half + 3*H)]
+};
+
+__device__ __forceinline__ double block_sum(double v, double *red) {
+  v = wave_sum_d(v);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  __syncthreads();
+  if (lane == 0) red[wave] = v;
+  __syncthreads();
+  return red[0] + red[1] + red[2] + red[3];
+}
+
+// LN backward of one row held 3 (or 2 for half rows) elements per thread:
+// returns dx (no accumulate), with xh the normalized input and w the weight.
+template <int E>
+__device__ __forceinline__ void row_ln_bwd(const float (&g)[E], const float (&xh)[E], const float (&w)[E],
+                                           const bool (&ok)[E], float rs, int dim, double *red, float (&dx)[E]) {
+  double s1 = 0, s2 = 0;
+#pragma unroll
+  for (int j = 0; j < E; j++)
+    if (ok[j]) {
+#pragma clang fp contract(off)
+      const float gw = g[j] * w[j];
+      s1 += (double)gw;
+      s2 += (double)(gw * xh[j]);
+    }
+  const float a = (float)(block_sum(s1, red) / (double)dim);
+  const float b = (float)(block_sum(s2, red) / (double)dim);
+#pragma unroll
+  for (int j = 0; j < E; j++) {
+#pragma clang fp contract(off)
+    dx[j] = ok[j] ? rs * (g[j] * w[j] - a - xh[j] * b) : 0.0f;
+  }
+}
+
+template <int E>
+__device__ __forceinline__ void row_stats_block(const float (&x)[E], const bool (&ok)[E], int dim, float eps,
+                                                double *red, float &mean, float &rstd) {
+  double s = 0;
+#pragma unroll
+  for (int j = 0; j < E; j++)
+    if (ok[j]) s += (double)x[j];
+  const double mu = block_sum(s, red) / (double)dim;
+  double v = 0;
+#pragma unroll
+  for (int j = 0; j < E; j++)
+    if (ok[j]) {
+      const double d = (double)x[j] - mu;
+      v += d * d;
+    }
+  rstd = (float)(1.0 / sqrt(block_sum(v, red) / (double)dim + (double)eps));
+  mean = (float)mu;
+}
+
+__global__ __launch_bounds__(256) void head_bwd_row_kernel(HeadBwdArgs a) {
+  constexpr int EH = 4;  // H <= 1024
+  constexpr int EF = 2;  // half <= 512
+  __shared__ double red[4];
+  __shared__ float sdd[512];
+  const int r = blockIdx.x, tid = threadIdx.x;
+  const int H = a.H, half = H / 2;
+  const int t = a.row_tok[r];
+  const float dl = a.dlogits[r];
+  const size_t cw = (size_t)4 * half + 3 * H;
+  float *ct = a.contrib + (size_t)r * cw;
+  // Half rows: gelu input, scorer norm.
+  float dv[EF], ge[EF], nw[EF], xh2[EF], ds2[EF];
+  bool okf[EF];
+#pragma unroll
+  for (int j = 0; j < EF; j++) {
+    const int i = tid + 256 * j;
+    okf[j] = i < half;
+    dv[j] = okf[j] ? a.d[(size_t)r * half + i] + a.dense_b[i] : 0.0f;
+    ge[j] = okf[j] ? gelu_erf<float>(dv[j]) : 0.0f;
+    nw[j] = okf[j] ? a.norm_w[i] : 0.0f;
+  }
+  float m2, r2;
+  row_stats_block(ge, okf, half, 1e-5f, red, m2, r2);
+#pragma unroll
+  for (int j = 0; j < EF; j++) {
+    const int i = tid + 256 * j;
+    {
+#pragma clang fp contract(off)
+      xh2[j] = (ge[j] - m2) * r2;
+    }
+    ds2[j] = okf[j] ? dl * a.out_w[i] : 0.0f;
+    if (okf[j]) {
+      ct[i] = dl * (xh2[j] * nw[j] + a.norm_b[i]);  // OutW: dl * s2
+      ct[half + i] = ds2[j] * xh2[j];               // norm weight
+      ct[2 * half + i] = ds2[j];                    // norm bias
+    }
+  }
+  float dge[EF];
+  row_ln_bwd(ds2, xh2, nw, okf, r2, half, red, dge);
+#pragma unroll
+  for (int j = 0; j < EF; j++) {
+    const int i = tid + 256 * j;
+    if (okf[j]) {
+      const float v = dge[j] * gelu_grad<float>(dv[j]);
+      sdd[i] = v;
+      ct[3 * half + i] = v;  // dense bias (and, with s1, the dense weight)
+    }
+  }
+  __syncthreads();
+  // Full rows: ds1 = dd . DenseW, input_norm and final_norm backward.
+  float x[EH], fn[EH], xhF[EH], xh1[EH], wF[EH], wI[EH], ds1[EH];
+  bool ok[EH];
+#pragma unroll
+  for (int j = 0; j < EH; j++) {
+    const int i = tid + 256 * j;
+    ok[j] = i < H;
+    x[j] = ok[j] ? a.h[(size_t)t * H + i] : 0.0f;
+    wF[j] = ok[j] ? a.final_norm[i] : 0.0f;
+    wI[j] = ok[j] ? a.in_w[i] : 0.0f;
+    float acc = 0.0f;
+    if (ok[j])
+      for (int k = 0; k < half; k++) acc += sdd[k] * a.dense_w[(size_t)k * H + i];
+    ds1[j] = acc;
+  }
+  float mF, rF;
+  row_stats_block(x, ok, H, a.eps, red, mF, rF);
+#pragma unroll
+  for (int j = 0; j < EH; j++) {
+    {
+#pragma clang fp contract(off)
+      xhF[j] = (x[j] - mF) * rF;
+    }
+    fn[j] = ok[j] ? xhF[j] * wF[j] : 0.0f;
+  }
+  float m1, r1;
+  row_stats_block(fn, ok, H, 1e-5f, red, m1, r1);
+#pragma unroll
+  for (int j = 0; j < EH; j++) {
+    const int i = tid + 256 * j;
+    {
+#pragma clang fp contract(off)
+      xh1[j] = (fn[j] - m1) * r1;
+    }
+    if (ok[j]) {
+      ct[4 * half + i] = ds1[j] * xh1[j];  // input_norm weight
+      ct[4 * half + H + i] = ds1[j];       // input_norm bias
+    }
+  }
+  float dfN[EH], dRow[EH];
+  row_ln_bwd(ds1, xh1, wI, ok, r1, H, red, dfN);
+  row_ln_bwd(dfN, xhF, wF, ok, rF, H, red, dRow);
+#pragma unroll
+  for (int j = 0; j < EH; j++) {
+    const int i = tid + 256 * j;
+    if (ok[j]) {
+      ct[4 * half + 2 * H + i] = dfN[j] * xhF[j];  // final_norm weight
+      a.dcur[(size_t)t * H + i] = dRow[j];
+    }
+  }
+}
+
+// Head parameter gradients from the per-row terms, summed over rows in row
+// order: thread i < half*H is DenseW[i/H][i%H] += sum_r dd[r][i/H]*s1[r][i%H];
+// the rest add the column sums of contrib and the out_proj bias.
+__global__ void head_param_kernel(HeadBwdArgs a, float *g_outw, float *g_normw, float *g_normb, float *g_denseb,
+                                  float *g_densew, float *g_inw, float *g_inb, float *g_final, float *g_outb) {
+  const int H = a.H, half = H / 2;
+  const size_t cw = (size_t)4 * half + 3 * H;
+  const size_t nd = (size_t)half * H;
+  const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx < nd) {
+    const int k = (int)(idx / H), i = (int)(idx % H);
+    float acc = 0.0f;
+    for (int r = 0; r < a.R; r++) acc += a.contrib[(size_t)r * cw + 3 * half + k] * a.s1[(size_t)r * H + i];
+    g_densew[idx] += acc;
+    return;
+  }
+  const size_t c = idx - nd;
+  if (c < cw) {
+    float acc = 0.0f;
+    for (int r = 0; r < a.R; r++) acc += a.contrib[(size_t)r * cw + c];
+    float *dst;
+    size_t off;
+    if (c < (size_t)half) dst = g_outw, off = c;
+    else if (c < (size_t)2 * half) dst = g_normw, off = c - half;
+    else if (c < (size_t)3 * half) dst = g_normb, off = c - 2 * half;
+    else if (c < (size_t)4 * half) dst = g_denseb, off = c - 3 * half;
+    else if (c < (size_t)4 * half + H) dst = g_inw, off = c - 4 * half;
+    else if (c < (size_t)4 * half + 2 * H) dst = g_inb, off = c - 4 * half - H;
+    else dst = g_final, off = c - 4 * half - 2 * H;
+    dst[off] += acc;
+    return;
+  }
+  if (c == cw) {
+    float acc = 0.0f;
+    for (int r = 0; r < a.R; r++) acc += a.dlogits[r];
+    g_outb[0] += acc;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Sum of squares in float64: block partials (fixed grid), then one sum in
+// partial order.
+__global__ __launch_bounds__(256) void sumsq_kernel(const float *x, size_t n, double *part) {
+  __shared__ double red[4];
+  double s = 0;
+  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) {
+    const double v = (double)x[i];
+    s += v * v;
+  }
+  s = wave_sum_d(s);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (lane == 0) red[wave] = s;
+  __syncthreads();
+  if (threadIdx.x == 0) part[blockIdx.x] = red[0] + red[1] + red[2] + red[3];
+}
+
+__global__ void sum_doubles_kernel(const double *part, int n, double *out) {
+  if (threadIdx.x != 0 || blockIdx.x != 0) return;
+  double s = 0;
+  for (int i = 0; i < n; i++) s += part[i];
+  *out = s;
+}
+
+// AdamW (Update, optim.go:118-141), written unfused as the reference
+// evaluates it. With wq (bf16 projections) the new weight is also stored in
+// the operand copy, rounded to nearest even.
+__global__ void adamw_kernel(float *p, const float *g, float *m, float *v, size_t n, float lr, float wd, float b1,
+                             float b2, float eps, float scale, float step_size, float inv_sqrt_b2c, bf16 *wq) {
+  const size_t k = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (k >= n) return;
+  {
+#pragma clang fp contract(off)
+    const float gr = g[k] * scale;
+    const float mk = b1 * m[k] + (1 - b1) * gr;
+    const float vk = b2 * v[k] + (1 - b2) * gr * gr;
+    m[k] = mk;
+    v[k] = vk;
+    const float den = (float)sqrt((double)vk) * inv_sqrt_b2c + eps;
+    const float pk = p[k] - (lr * step_size * mk / den + wd * p[k]);
+    p[k] = pk;
+    if (wq) wq[k] = (bf16)pk;
+  }
+}
+
+__global__ void widen_bf16_kernel(const bf16 *src, float *dst, size_t n) {
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) dst[i] = (float)src[i];
+}
+
+inline unsigned blocks(size_t n, int per = 256) { return (unsigned)((n + per - 1) / per); }
+
+}  // namespace
+
+hipError_t launch_transpose(int precision_in, int precision_out, const void *src, int rows, int cols, int lds,
+                            void *dstT, int ldt, int rows_pad, void *copy, hipStream_t s) {
+  if (rows_pad <= 0 || cols <= 0) return hipSuccess;
+  const dim3 grid((cols + 63) / 64, (rows_pad + 63) / 64), block(256);
+  if (precision_in == 0 && precision_out == 1)
+    hipLaunchKernelGGL((transpose_kernel<float, bf16>), grid, block, 0, s, (const float *)src, rows, cols, lds,
+                       (bf16 *)dstT, ldt, rows_pad, (bf16 *)copy);
+  else if (precision_in == 0 && precision_out == 0)
+    hipLaunchKernelGGL((transpose_kernel<float, float>), grid, block, 0, s, (const float *)src, rows, cols, lds,
+                       (float *)dstT, ldt, rows_pad, (float *)copy);
+  else if (precision_in == 1 && precision_out == 1)
+    hipLaunchKernelGGL((transpose_kernel<bf16, bf16>), grid, block, 0, s, (const bf16 *)src, rows, cols, lds,
+                       (bf16 *)dstT, ldt, rows_pad, (bf16 *)copy);
+  else
+    return hipErrorInvalidValue;
+  return hipGetLastError();
+}
+
+hipError_t launch_geglu_fwd(int precision, const void *wi, void *act, int rows, int I, hipStream_t s) {
+  const size_t n = (size_t)rows * I;
+  if (n == 0) return hipSuccess;
+  if (precision == 1)
+    hipLaunchKernelGGL(geglu_fwd_kernel<bf16>, dim3(blocks(n)), dim3(256), 0, s, (const bf16 *)wi, (bf16 *)act, rows, I);
+  else
+    hipLaunchKernelGGL(geglu_fwd_kernel<float>, dim3(blocks(n)), dim3(256), 0, s, (const float *)wi, (float *)act, rows,
+                       I);
+  return hipGetLastError();
+}
+
+hipError_t launch_geglu_bwd(int precision, const float *dact, const void *wi, void *dwi, int rows, int I,
+                            hipStream_t s) {
+  const size_t n = (size_t)rows * I;
+  if (n == 0) return hipSuccess;
+  if (precision == 1)
+    hipLaunchKernelGGL(geglu_bwd_kernel<bf16>, dim3(blocks(n)), dim3(256), 0, s, dact, (const bf16 *)wi, (bf16 *)dwi,
+                       rows, I);
+  else
+    hipLaunchKernelGGL(geglu_bwd_kernel<float>, dim3(blocks(n)), dim3(256), 0, s, dact, (const float *)wi,
+                       (float *)dwi, rows, I);
+  return hipGetLastError();
+}
+
+int ln_bwd_blocks(int rows) { return std::max(1, std::min(512, (rows + LNB_WAVES - 1) / LNB_WAVES)); }
+
+hipError_t launch_ln_bwd(float *dx, const float *dy, const float *x, const int *ids, const float *w, float eps, int rows,
+                         int dim, float *part, float *dw, hipStream_t s) {
+  if (rows <= 0) return hipSuccess;
+  if (dim % 64 != 0 || dim > 1024) return hipErrorInvalidValue;
+  const int nb = ln_bwd_blocks(rows);
+  hipLaunchKernelGGL(ln_bwd_kernel, dim3(nb), dim3(256), 0, s, dx, dy, x, ids, w, eps, rows, dim, part);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || !dw) return e;
+  hipLaunchKernelGGL(sum_partials_kernel, dim3(blocks(dim)), dim3(256), 0, s, part, nb, dim, dw);
+  return hipGetLastError();
+}
+
+hipError_t launch_add(float *dst, const float *src, size_t n, hipStream_t s) {
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(add_kernel, dim3(blocks(n)), dim3(256), 0, s, dst, src, n);
+  return hipGetLastError();
+}
+
+hipError_t launch_embed_bwd(const float *dE, const int *order, const int *seg_start, const int *seg_id, int nseg,
+                            int dim, float *gtok, hipStream_t s) {
+  if (nseg <= 0) return hipSuccess;
+  hipLaunchKernelGGL(embed_bwd_kernel, dim3(nseg), dim3(256), 0, s, dE, order, seg_start, seg_id, dim, gtok);
+  return hipGetLastError();
+}
+
+hipError_t launch_head_bwd(const float *h, const int *row_tok, const float *s1, const float *d, const float *dlogits,
+                           int R, int H, float eps, const float *const *w, float *dcur, float *contrib,
+                           float *const *g, hipStream_t s) {
+  if (R <= 0) return hipSuccess;
+  if (H > 1024 || H % 256 != 0) return hipErrorInvalidValue;
+  // w: final_norm, in_w, dense_w, dense_b, norm_w, norm_b, out_w
+  HeadBwdArgs a{h, row_tok, s1, d, dlogits, R, H, eps, w[0], w[1], w[2], w[3], w[4], w[5], w[6], dcur, contrib};
+  hipLaunchKernelGGL(head_bwd_row_kernel, dim3(R), dim3(256), 0, s, a);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  // g: out_w, norm_w, norm_b, dense_b, dense_w, in_w, in_b, final_norm, out_b
+  const size_t n = (size_t)(H / 2) * H + (size_t)4 * (H / 2) + 3 * H + 1;
+  hipLaunchKernelGGL(head_param_kernel, dim3(blocks(n)), dim3(256), 0, s, a, g[0], g[1], g[2], g[3], g[4], g[5], g[6],
+                     g[7], g[8]);
+  return hipGetLastError();
+}
+
+int sumsq_blocks(size_t n) { return (int)std::max<size_t>(1, std::min<size_t>(256, (n + 4095) / 4096)); }
+
+hipError_t launch_sumsq(const float *x, size_t n, double *part, hipStream_t s) {
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(sumsq_kernel, dim3(sumsq_blocks(n)), dim3(256), 0, s, x, n, part);
+  return hipGetLastError();
+}
+
+hipError_t launch_sum_doubles(const double *part, int n, double *out, hipStream_t s) {
+  hipLaunchKernelGGL(sum_doubles_kernel, dim3(1), dim3(64), 0, s, part, n, out);
+  return hipGetLastError();
+}
+
+hipError_t launch_adamw(float *p, const float *g, float *m, float *v, size_t n, float lr, float wd, float b1, float b2,
+                        float eps, float scale, float step_size, float inv_sqrt_b2c, void *wq_bf16, hipStream_t s) {
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(adamw_kernel, dim3(blocks(n)), dim3(256), 0, s, p, g, m, v, n, lr, wd, b1, b2, eps, scale,
+                     step_size, inv_sqrt_b2c, (bf16 *)wq_bf16);
+  return hipGetLastError();
+}
+
+hipError_t launch_widen_bf16(const void *src, float *dst, size_t n, hipStream_t s) {
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(widen_bf16_kernel, dim3(blocks(n)), dim3(256), 0, s, (const bf16 *)src, dst, n);
+  return hipGetLastError();
+}

@@ -99,11 +99,17 @@ struct GemmArgs {
   int accumulate; // fp32 epilogue: C += result
   int ngroups;    // N-tile groups per XCD sweep (set by launch_gemm)
   int order;      // workgroup -> tile order (0: XCD-aware groups)
+  size_t c_split; // split-K: elements between the partial outputs of blockIdx.y (0: one split)
 };
 
 enum { EPI_F32 = 0, EPI_STORE = 1, EPI_GEGLU = 2 };
 
 hipError_t launch_gemm(int precision, int epi, const GemmArgs &a, hipStream_t s);
+// Split-K fp32-output GEMM: `splits` partial products, each over a.K / splits
+// of K (a.K % (splits * 64) == 0), written to partial + split * M * N
+// (row-major, ldc = N), then added in split order into C (M x N, ldc = N,
+// accumulated into). partial holds splits * M * N floats.
+hipError_t launch_gemm_splitk(int precision, const GemmArgs &a, int splits, float *partial, hipStream_t s);
 bool gemm_shape_ok(int precision, int N, int K);
 
 // Attention work item: 32 * ATTN_QT * ATTN_WAVES queries of one sequence
@@ -130,8 +136,34 @@ struct AttnArgs {
   const int *seq_off, *seq_len;
   int nwork, H, heads, sliding, half_window;
   float scale_log2;   // softmax scale * log2(e)
+  float *lse;         // training: per (token, head) log2 of the softmax denominator of the
+                      // scaled scores, lse[t*heads + head] = max*scale_log2 + log2(sum); null otherwise
 };
 hipError_t launch_attention(int precision, const AttnArgs &a, hipStream_t s);
+
+// Attention backward (the reference's attnBwd + the RoPE inverse,
+// backward.go:117-159 and :77-81): dqkv from dctx, the un-rotated qkv, ctx and
+// the forward's lse. The batch layout fields are the forward's.
+struct AttnBwdArgs {
+  const void *qkv;     // [T x 3H] un-rotated, operand type
+  const void *ctx;     // [T x H] forward output O, operand type
+  const void *dctx;    // [T x H] dO, operand type
+  const float *lse;    // [T x heads] from the forward
+  float *dsum;         // [T x heads] scratch: D = rowsum(dO * O)
+  void *dqkv;          // [T x 3H] out (dq, dk after the RoPE inverse; dv), operand type
+  const int *kinfo;
+  const float *cos_t, *sin_t;
+  const int4 *work;
+  const uint32_t *codes;
+  const int *first;
+  const int *seq_off, *seq_len;
+  const ChunkInfo *chunks;
+  const int *chunk_off;
+  int nwork, H, heads, sliding, half_window;
+  float scale;         // 1/sqrt(64)
+  float scale_log2;    // scale * log2(e)
+};
+hipError_t launch_attention_bwd(int precision, const AttnBwdArgs &a, hipStream_t s);
 
 hipError_t launch_tile_codes(const ChunkInfo *chunks, const int4 *work, const int *seq_len, const int *chunk_off,
                              int nwork, int sliding, int half_window, uint32_t *codes, int *first, hipStream_t s);
@@ -154,3 +186,28 @@ struct HeadArgs {
 hipError_t launch_head(const HeadArgs &a, float *s1, float *d, hipStream_t s);
 hipError_t launch_pack(const float *src, int trans, int rows, int cols, int ld, float *dst, int dst_rows,
                        int dst_cols, hipStream_t s);
+
+// Training kernels (backward.hip). Precision codes: 0 fp32, 1 bf16.
+hipError_t launch_transpose(int precision_in, int precision_out, const void *src, int rows, int cols, int lds,
+                            void *dstT, int ldt, int rows_pad, void *copy, hipStream_t s);
+hipError_t launch_geglu_fwd(int precision, const void *wi, void *act, int rows, int I, hipStream_t s);
+hipError_t launch_geglu_bwd(int precision, const float *dact, const void *wi, void *dwi, int rows, int I,
+                            hipStream_t s);
+int ln_bwd_blocks(int rows);  // partial rows of dw written by launch_ln_bwd (part holds ln_bwd_blocks x dim)
+hipError_t launch_ln_bwd(float *dx, const float *dy, const float *x, const int *ids, const float *w, float eps, int rows,
+                         int dim, float *part, float *dw, hipStream_t s);
+hipError_t launch_add(float *dst, const float *src, size_t n, hipStream_t s);
+hipError_t launch_embed_bwd(const float *dE, const int *order, const int *seg_start, const int *seg_id, int nseg,
+                            int dim, float *gtok, hipStream_t s);
+// w: final_norm, in_w, dense_w, dense_b, norm_w, norm_b, out_w;
+// g: out_w, norm_w, norm_b, dense_b, dense_w, in_w, in_b, final_norm, out_b.
+// contrib holds R x (2H + 3H) floats.
+hipError_t launch_head_bwd(const float *h, const int *row_tok, const float *s1, const float *d, const float *dlogits,
+                           int R, int H, float eps, const float *const *w, float *dcur, float *contrib,
+                           float *const *g, hipStream_t s);
+int sumsq_blocks(size_t n);
+hipError_t launch_sumsq(const float *x, size_t n, double *part, hipStream_t s);
+hipError_t launch_sum_doubles(const double *part, int n, double *out, hipStream_t s);
+hipError_t launch_adamw(float *p, const float *g, float *m, float *v, size_t n, float lr, float wd, float b1, float b2,
+                        float eps, float scale, float step_size, float inv_sqrt_b2c, void *wq_bf16, hipStream_t s);
+hipError_t launch_widen_bf16(const void *src, float *dst, size_t n, hipStream_t s);

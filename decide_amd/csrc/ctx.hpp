@@ -1,0 +1,131 @@
+// Library-internal state of a dn_ctx and the helpers shared by the C ABI
+// translation units (api.cpp: context, weights, forward; train.cpp: training).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <map>
+#include <string>
+#include <vector>
+
+#include "../../include/decide_hip.h"
+#include "common.hpp"
+
+struct DevBuf {
+  void *p = nullptr;
+  size_t cap = 0;
+};
+
+// Per-tensor training state, in the slot's stored layout (Wi rows interleaved).
+struct ParamTrain {
+  DevBuf master;   // fp32 weights when the slot holds bf16 (projections in bf16 mode)
+  DevBuf grad, m, v;
+  DevBuf wt;       // projections: transposed operand copy [in x out] for the input-gradient GEMMs
+  bool wt_valid = false;
+};
+
+struct TensorSlot {
+  DevBuf buf;
+  int64_t n = 0;     // float32 elements expected
+  int rank = 1;      // rank of the reference tensor (model.go:51-84)
+  bool proj = false; // projection matrix: stored in the operand precision
+  bool wi = false;   // Wi: rows interleaved for the GeGLU epilogue
+  bool set = false;
+  ParamTrain train;  // allocated by the training entry points
+};
+
+struct Config {
+  int hidden = 0, inter = 0, heads = 0, layers = 0, vocab = 0;
+  float eps = 1e-5f;
+  int half_window = 64;
+  double theta_g = 160000, theta_l = 10000;
+  std::vector<uint8_t> sliding;
+  int precision = DN_PRECISION_BF16;
+};
+
+// Activations of one layer kept by a training forward (the reference's
+// layerCache, internal/nn/forward.go:65-73, without the n x n probabilities:
+// the backward recomputes them from lse).
+struct LayerSave {
+  DevBuf hs, h1;                      // fp32 [T x H]: layer input, residual after attention
+  DevBuf n1, qkv, ctx, n2, wi, act;   // operand type: QKV input, un-rotated qkv, ctx, Wi input, Wi output, GeGLU
+  DevBuf lse;                         // fp32 [T x heads]
+};
+
+struct TrainState {
+  bool enabled = false;
+  int train_from = 0;
+  bool train_emb = true;
+  int adam_step = 0;
+  std::vector<LayerSave> layers;
+  bool have_forward = false;  // the activations of the last dn_forward_train are intact
+  int T = 0, R = 0;
+  std::vector<int32_t> ids;   // token ids of the last training forward
+  DevBuf dcur, dprev, dh1, dact, dwi, dn2, dctx, dqkv, dn1, dyop, dyT, xT, dsum, part, lnpart, dE, dl, contrib;
+  DevBuf emb_order, emb_seg, emb_id, sq_part, sq_out;
+};
+
+struct dn_ctx {
+  int device = 0;
+  hipStream_t stream = nullptr;
+  hipStream_t own_stream = nullptr;
+  std::string err;
+  bool configured = false;
+  Config cfg;
+  std::map<std::string, TensorSlot> w;
+  DevBuf inv_freq;  // 32 doubles global theta, 32 local
+  // workspace
+  DevBuf h, xn, qkv, ctxb, act, kinfo, ids, pos, opt, rowtok, logits, err_flag, head_s1, head_d;
+  // RoPE cos/sin per position 0..65535 (global theta, then local), built once
+  // per configuration at the first forward.
+  DevBuf rope;
+  bool rope_ready = false;
+  DevBuf gA, gB, gC;  // dn_gemm_f32 staging
+  // batch layout cache
+  std::vector<int> lay_len;
+  std::vector<int> h_seq_off, h_chunk_off;
+  std::vector<int4> h_chunk_desc, h_work;
+  DevBuf d_seq_off, d_seq_len, d_chunk_off, d_chunk_desc, d_work, d_chunks;
+  DevBuf d_codes, d_first;  // attention tile classes per work item: [global | local]
+  int lay_T = 0, lay_nchunks = 0, lay_nwork = 0;
+  // kernel probe: events[2*k], events[2*k+1] bracket launch k of one forward
+  int probe_layer = -1;
+  std::vector<hipEvent_t> probe_pool;  // 10 events per recorded forward
+  int probe_used = 0;                  // forwards recorded
+  TrainState tr;
+};
+
+namespace dnh {
+
+constexpr int kPositions = 65536;  // RoPE table rows: positions are validated / flagged to this range
+
+int fail(dn_ctx *c, int code, const std::string &msg);
+int hip_fail(dn_ctx *c, const char *op, hipError_t e);
+hipError_t ensure(DevBuf &b, size_t bytes);
+void release(DevBuf &b);
+void release_slot(TensorSlot &t);
+void release_train(TrainState &tr);
+uint16_t f32_to_bf16_rne(float f);
+std::string layer_prefix(int l);
+const void *W(dn_ctx *c, const std::string &name);
+int check_ready(dn_ctx *c);
+int64_t wi_src_row(int64_t r, int64_t I);
+// Validates a host batch as dn_forward does and stages it on the device
+// (ids, pos, opt, row_tok); *R receives the number of option rows.
+int stage_batch(dn_ctx *c, int nseq, const int32_t *seq_len, const int32_t *ids, const int32_t *pos,
+                const int32_t *opt_id, const int32_t *nmask, const int32_t *mask_pos, int logits_cap, int *R,
+                int64_t *T);
+// The forward on device-resident token arrays; with train, the activations of
+// layers >= c->tr.train_from are kept in c->tr.layers.
+int forward_core(dn_ctx *c, int nseq, const int32_t *seq_len, const int32_t *d_ids, const int32_t *d_pos,
+                 const int32_t *d_opt, int R, const int32_t *d_row_tok, float *d_logits, bool train);
+// Finishes a host-array forward: logits to the host and the device error flag.
+int finish_forward(dn_ctx *c, int R, float *logits);
+
+}  // namespace dnh
+
+#define HIPCHK(c, op, expr)                                     \
+  do {                                                          \
+    hipError_t e_ = (expr);                                     \
+    if (e_ != hipSuccess) return dnh::hip_fail(c, op, e_);      \
+  } while (0)

@@ -102,6 +102,11 @@ __global__ __launch_bounds__(64 * WGM * WGN) __attribute__((amdgpu_waves_per_eu(
 
   const TileOrder<BM, BN> to(blockIdx.x, (g.M + BM - 1) / BM, g.N / BN, g.ngroups, g.order);
   const int m0 = to.m0, n0 = to.n0;
+  // Split-K: blockIdx.y takes K elements [y*K, (y+1)*K) of A and B and writes
+  // its own partial output.
+  const size_t koff = (size_t)blockIdx.y * g.K;
+  const T *gA = (const T *)g.A + koff, *gB = (const T *)g.B + koff;
+  char *gC = (char *)g.C + (size_t)blockIdx.y * g.c_split * (EPI == EPI_F32 ? 4 : sizeof(T));
 
   // DMA sources: load i of this wave fills tile rows RPI*(wave + NW*i) .. +RPI-1;
   // lane l writes row RPI*(wave+NW*i) + l/CPR, LDS chunk slot l%CPR, which
@@ -112,9 +117,9 @@ __global__ __launch_bounds__(64 * WGM * WGN) __attribute__((amdgpu_waves_per_eu(
     const int r = RPI * (wave + NW * i) + lane / CPR;
     const int c = (lane % CPR) ^ swz<RB>(r);
     if (r < BM)
-      src[i] = (const char *)g.A + (size_t)min(m0 + r, g.M - 1) * g.lda * sizeof(T) + c * 16;
+      src[i] = (const char *)gA + (size_t)min(m0 + r, g.M - 1) * g.lda * sizeof(T) + c * 16;
     else
-      src[i] = (const char *)g.B + (size_t)(n0 + r - BM) * g.ldb * sizeof(T) + c * 16;
+      src[i] = (const char *)gB + (size_t)(n0 + r - BM) * g.ldb * sizeof(T) + c * 16;
   }
   auto issue_part = [&](int stage, int k0, int i0, int i1) {
     char *dst = smem + stage * STAGE + wave * 1024;
@@ -219,7 +224,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) __attribute__((amdgpu_waves_per_eu(
     constexpr int LD = BN + 4;  // floats per staged row
     constexpr int HM = WM;      // rows per pass: the waves with wm == pass stage theirs
     float *st = (float *)smem;
-    float *C = (float *)g.C;
+    float *C = (float *)gC;
     constexpr int V = BN / 4;  // float4 per row
     constexpr int ITER = HM * V / NT;
     constexpr int BATCH = ITER < 8 ? ITER : 8;
@@ -294,7 +299,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) __attribute__((amdgpu_waves_per_eu(
         }
     }
     __syncthreads();
-    T *C = (T *)g.C;
+    T *C = (T *)gC;
     const int oc0 = EPI == EPI_GEGLU ? n0 / 2 : n0;
     constexpr int EPV = 16 / sizeof(T);  // elements per 16-byte vector
     constexpr int V = OC / EPV;
@@ -308,9 +313,9 @@ __global__ __launch_bounds__(64 * WGM * WGN) __attribute__((amdgpu_waves_per_eu(
 }
 
 template <class T, int BM, int BN, int RB, int NSTAGE, int WPE, int WGM = 2, int WGN = 2>
-hipError_t launch_cfg(int epi, const GemmArgs &a, hipStream_t s) {
+hipError_t launch_cfg(int epi, const GemmArgs &a, hipStream_t s, int splits = 1) {
   const int tiles = ((a.M + BM - 1) / BM) * (a.N / BN);
-  dim3 grid(tiles), block(64 * WGM * WGN);
+  dim3 grid(tiles, splits), block(64 * WGM * WGN);
   switch (epi) {
     case EPI_F32:
       hipLaunchKernelGGL((gemm_nt_kernel<T, BM, BN, RB, NSTAGE, EPI_F32, WPE, WGM, WGN>), grid, block, 0, s, a);
@@ -551,7 +556,37 @@ hipError_t launch_skinny(int epi, const GemmArgs &a, hipStream_t s) {
   return launch_skinny_cfg<T, 2, 1, 8>(epi, a, s);
 }
 
+// C[i] += sum over splits of part[s * n + i], in split order.
+__global__ void splitk_reduce_kernel(const float *part, int splits, size_t n, float *C) {
+  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  float acc = 0.0f;
+  for (int s = 0; s < splits; s++) acc += part[(size_t)s * n + i];
+  C[i] += acc;
+}
+
 }  // namespace
+
+hipError_t launch_gemm_splitk(int precision, const GemmArgs &a0, int splits, float *partial, hipStream_t s) {
+  if (a0.M <= 0) return hipSuccess;
+  if (splits < 1 || a0.K % (splits * 64) != 0 || a0.N % 128 != 0) return hipErrorInvalidValue;
+  GemmArgs a = a0;
+  a.K = a0.K / splits;
+  a.C = partial;
+  a.ldc = a0.N;
+  a.n_store = a0.N;
+  a.accumulate = 0;
+  a.c_split = (size_t)a0.M * a0.N;
+  a.ngroups = 1;
+  a.order = 1;  // row-major tile order: the grid is (tiles, splits)
+  hipError_t e = precision == 1 ? launch_cfg<bf16, 128, 128, 64, 3, 3>(EPI_F32, a, s, splits)
+                                : launch_cfg<float, 128, 128, 128, 3, 1>(EPI_F32, a, s, splits);
+  if (e != hipSuccess) return e;
+  const size_t n = (size_t)a0.M * a0.N;
+  hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, partial, splits, n,
+                     (float *)a0.C);
+  return hipGetLastError();
+}
 
 // All tile configs use BN = 128; K is staged 64 or 128 bytes per step.
 bool gemm_shape_ok(int precision, int N, int K) {

@@ -15,6 +15,7 @@ LIB_PATH = os.path.join(HERE, "libdecide_hip.so")
 
 DN_OK, DN_NO_GPU, DN_INVALID_ARG, DN_OUT_OF_MEMORY, DN_DEVICE_ERROR, DN_UNSUPPORTED = range(6)
 DN_PRECISION_FP32, DN_PRECISION_BF16 = 0, 1
+DN_STATE_WEIGHT, DN_STATE_GRAD, DN_STATE_M, DN_STATE_V = range(4)
 
 
 class DecideError(RuntimeError):
@@ -69,6 +70,16 @@ _SIGS = {
     "dn_answer": ([_f64p, _i, _c.c_double, _f64p, _c.POINTER(_i), _c.POINTER(_c.c_double)], _i),
     "dn_round": ([_c.c_double, _i], _c.c_double),
     "dn_evaluate": ([_vp, _i, _vp, _vp, _vp, _vp, _f64p, _c.c_int32, _i, _f64p, _vp, _f64p, _f64p], _i),
+    "dn_enable_training": ([_vp], _i),
+    "dn_set_trainable": ([_vp, _i, _i], _i),
+    "dn_forward_train": ([_vp, _i, _i32p, _i32p, _i32p, _i32p, _i32p, _i32p, _f32p, _i], _i),
+    "dn_backward": ([_vp, _f32p, _i], _i),
+    "dn_zero_grad": ([_vp], _i),
+    "dn_grad_sumsq": ([_vp, _c.POINTER(_c.c_double)], _i),
+    "dn_adamw_step": ([_vp, _c.c_float, _c.c_float, _c.c_float, _c.c_float], _i),
+    "dn_download_tensor": ([_vp, _c.c_char_p, _i, _f32p, _c.c_int64], _i),
+    "dn_upload_state": ([_vp, _c.c_char_p, _i, _f32p, _c.c_int64], _i),
+    "dn_set_adam_step": ([_vp, _i], _i),
     "dn_tokenizer_parse": ([_vp, _c.c_int64, _c.POINTER(_vp)], _i),
     "dn_tokenizer_free": ([_vp], None),
     "dn_tokenizer_special_ids": ([_vp, _vp, _vp, _vp, _vp], _i),

@@ -250,6 +250,71 @@ int dn_pretokenize(const char *text, int64_t len, int64_t *ends, int64_t cap, in
  * invalid bytes passed through; same output-capacity convention. */
 int dn_nfc(const char *text, int64_t len, char *out, int64_t cap, int64_t *n);
 
+/* ---- Training (the device half of internal/gpunn + internal/train's engine).
+ * Weights, gradients and AdamW moments of every tensor (encoder and scorer
+ * head) live on the device; the loss and learning-rate schedule stay with
+ * the caller, as in internal/train/trainer.go:300-330. Gradient and moment
+ * tensors use the same names and layouts as dn_upload_tensor. */
+
+/* Enables training on a configured context: from here on, uploads in bf16
+ * mode also keep fp32 master weights (AdamW updates them and re-rounds the
+ * bf16 operand copy). Must precede the weight uploads. Gradients and
+ * moments start at zero. Replaces gpunn.New's per-parameter w/g/m/v
+ * buffers (internal/gpunn/model.go:80-121). */
+int dn_enable_training(dn_ctx *ctx);
+
+/* Freezes encoder layers below train_from and, unless train_emb, the token
+ * embeddings (always frozen when train_from > 0); the embedding norm is
+ * frozen when train_from > 0. Replaces gpunn.(*Model).SetTrainable
+ * (internal/gpunn/model.go:155-171); the same rules as NewAdamW
+ * (internal/train/optim.go:31-65). */
+int dn_set_trainable(dn_ctx *ctx, int train_from, int train_emb);
+
+/* Forward that keeps the activations dn_backward needs (for layers >=
+ * train_from). Arguments and validation as dn_forward. Replaces
+ * gpunn.(*Model).Forward (internal/gpunn/model.go:204-330) and
+ * nn.(*Model).Forward with trainFrom < Layers (internal/nn/forward.go:129). */
+int dn_forward_train(dn_ctx *ctx, int nseq, const int32_t *seq_len, const int32_t *ids, const int32_t *pos,
+                     const int32_t *opt_id, const int32_t *nmask, const int32_t *mask_pos, float *logits,
+                     int logits_cap);
+
+/* Accumulates into the device gradients the gradient of a loss whose
+ * derivative with respect to the last dn_forward_train's logits is dlogits
+ * [nrows]. Head and final norm included; layers below train_from get none;
+ * the token embeddings only with train_emb and train_from == 0. Replaces
+ * gpunn.(*Model).Backward (internal/gpunn/model.go:384-477) and
+ * nn.(*Model).Backward (internal/nn/backward.go:19-115). DN_INVALID_ARG
+ * without a preceding dn_forward_train (any other forward invalidates it). */
+int dn_backward(dn_ctx *ctx, const float *dlogits, int nrows);
+
+/* Clears every gradient. Replaces gpunn.(*Model).ZeroGrad (model.go:479-486). */
+int dn_zero_grad(dn_ctx *ctx);
+
+/* Sum of squares (float64) of the gradients of all trainable tensors;
+ * sqrt of it is AdamW.GradNorm (optim.go:68-90) over the whole model.
+ * Replaces gpunn.(*Model).GradSumSq (model.go:488-505). */
+int dn_grad_sumsq(dn_ctx *ctx, double *out);
+
+/* One AdamW step (beta1 0.9, beta2 0.999, eps 1e-8) on every trainable
+ * tensor, gradients first scaled by grad_scale: encoder tensors at lr,
+ * scorer tensors at head_lr; decoupled weight decay weight_decay*rate on
+ * 2-D tensors except the token embeddings. Replaces
+ * gpunn.(*Model).Update (model.go:507-529) + AdamW.Update (optim.go:94-145). */
+int dn_adamw_step(dn_ctx *ctx, float lr, float head_lr, float weight_decay, float grad_scale);
+
+enum { DN_STATE_WEIGHT = 0, DN_STATE_GRAD = 1, DN_STATE_M = 2, DN_STATE_V = 3 };
+
+/* Copies one tensor's weights (fp32 masters when training in bf16),
+ * gradient or moment into out [n]. Replaces SyncToHost / DownloadGrads /
+ * DownloadAdam (internal/gpunn/model.go:531-600). */
+int dn_download_tensor(dn_ctx *ctx, const char *name, int which, float *out, int64_t n);
+
+/* Sets one tensor's gradient or moment (DN_STATE_GRAD/M/V) from data [n];
+ * with dn_set_adam_step, restores a checkpoint's optimizer state. Replaces
+ * UploadAdam (internal/gpunn/model.go:578-593). */
+int dn_upload_state(dn_ctx *ctx, const char *name, int which, const float *data, int64_t n);
+int dn_set_adam_step(dn_ctx *ctx, int step);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,331 @@
+"""Training parity on the GPU: dn_forward_train / dn_backward / dn_adamw_step
+through the C ABI against the CPU oracle's restatement of nn.Forward,
+nn.Backward and AdamW (itself pinned to the reference's PyTorch gradients in
+test_oracle_train.py).
+
+Bars: logits as the forward tests (fp32 |dlogit| <= 1e-4 (1 + |logit|));
+every gradient tensor within relErr (nn_test.go:95-103) <= 5e-4 in the fp32
+validation mode and <= 1e-1 in bf16 (bf16 operands, fp32 accumulation), the
+median over tensors <= 1e-4 / 5e-2; the
+same dlogits drive both sides so the backward is compared alone. AdamW is
+checked against its closed form and against the oracle's AdamW fed the
+device's gradients (fp32 arithmetic on both sides, same order)."""
+import os
+
+import numpy as np
+import pytest
+
+import oracle
+from conftest import rel_err
+
+pytestmark = pytest.mark.gpu
+
+WORKERS = max(1, min(16, os.cpu_count() or 1))
+# fp32: rounding level (the scorer norm-bias gradient is a sum over rows of
+# terms that cancel, since softmax cross-entropy gradients sum to zero per
+# sequence; relErr's 1e-4 floor then measures absolute noise of ~1e-8).
+# bf16: bf16 activations and GEMM / attention operands (the oracle gets the
+# same bf16-rounded projection weights). Measured on ModernBERT-base: the
+# MLP-output weight gradients 5-6.5%, QKV 1.4-1.8%, median 3.3%, the same at
+# layer 21 as at layer 0 (no compounding through depth); an indexing or sign
+# error gives O(1).
+GRAD_TOL = {"fp32": 5e-4, "bf16": 1e-1}
+GRAD_MEDIAN_TOL = {"fp32": 1e-4, "bf16": 5e-2}
+
+
+def small_cfg(layers=3):
+    from decide_amd.nn import Config
+
+    types = ["full_attention", "sliding_attention", "sliding_attention"] * 3
+    return Config(hidden=256, intermediate=384, heads=4, layers=layers, vocab=400, half_window=8,
+                  layer_types=types[:layers])
+
+
+def train_batch(vocab, mask_id, seed=0, specs=None):
+    """Independent-option sequences and a plain one, lengths across the
+    32/64/128-token tile edges; options of a few tokens each."""
+    from decide_amd.nn import build_sequence
+
+    rng = np.random.default_rng(seed)
+    specs = specs or [(20, [5, 6, 7], True), (100, [10, 12], False), (150, [20, 20, 21], True), (9, [1, 3], True)]
+    out = []
+    for prem, opts, indep in specs:
+        ids = [1] + list(rng.integers(3, mask_id, size=prem - 2)) + [2]
+        for ln in opts:
+            ids += [mask_id] + list(rng.integers(3, mask_id, size=ln - 1))
+        ids.append(2)
+        out.append(build_sequence(np.array(ids, np.int32), mask_id, independent=indep))
+    return out
+
+
+def weights_for(cfg, seed=3, std=0.05):
+    from decide_amd.synth import random_weights
+
+    w = random_weights(cfg, seed=seed, std=std)
+    rng = np.random.default_rng(seed + 1)
+    for name in w:  # norm weights and biases away from 1 / 0 so their gradients matter
+        if name.endswith("norm.weight"):
+            w[name] = (1 + 0.1 * rng.standard_normal(w[name].shape)).astype(np.float32)
+        elif name.endswith(".bias"):
+            w[name] = (0.05 * rng.standard_normal(w[name].shape)).astype(np.float32)
+    return w
+
+
+PROJ = ("attn.Wqkv.weight", "attn.Wo.weight", "mlp.Wi.weight", "mlp.Wo.weight")
+
+
+def bf16_round(a):
+    """Round-to-nearest-even to bfloat16, widened back to float32."""
+    u = np.ascontiguousarray(a, np.float32).view(np.uint32).astype(np.uint64)
+    u = (u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000
+    return u.astype(np.uint32).view(np.float32).reshape(np.shape(a))
+
+
+def effective_weights(w, prec):
+    """The weights the device computes with: in bf16 the four projection
+    matrices are rounded to bfloat16 at upload."""
+    if prec != "bf16":
+        return w
+    return {n: (bf16_round(a) if n.endswith(PROJ) else a) for n, a in w.items()}
+
+
+def oracle_grads(cfg, w, batch, train_from=0, train_emb=True, seed=5):
+    from decide_amd.nn import tensor_shapes
+
+    oracle.set_workers(WORKERS)
+    m = oracle.OracleModel(cfg, w)
+    logits = m.forward_train(batch, train_from)
+    rng = np.random.default_rng(seed)
+    targets = [int(rng.integers(0, len(s.mask_pos))) for s in batch]
+    _, dl = oracle.loss_and_grad(logits, batch, targets)
+    g = m.zeros_like()
+    m.backward(dl, g, train_emb=train_emb)
+    grads = {n: g.get(n, int(np.prod(s))).reshape(s) for n, s in tensor_shapes(cfg).items()}
+    return logits, dl, grads
+
+
+def frozen(name, train_from, train_emb):
+    if name == "model.embeddings.tok_embeddings.weight":
+        return not train_emb or train_from > 0
+    if name == "model.embeddings.norm.weight":
+        return train_from > 0
+    return any(name.startswith(f"model.layers.{l}.") for l in range(train_from))
+
+
+def check_grads(eng, want, prec, train_from=0, train_emb=True, label=""):
+    worst, worst_name, errs = 0.0, "", []
+    for name, g_want in want.items():
+        got = eng.download(name, "grad")
+        if frozen(name, train_from, train_emb):
+            assert np.all(got == 0), name
+            continue
+        if name == "model.embeddings.tok_embeddings.weight" and not train_emb:
+            continue
+        e = rel_err(got, g_want)
+        errs.append(e)
+        if e > worst:
+            worst, worst_name = e, name
+        assert np.all(np.isfinite(got)), name
+        assert e <= GRAD_TOL[prec], (label, prec, name, e)
+    if os.environ.get("DN_GRAD_REPORT"):
+        for name in want:
+            if name.startswith("model.layers.") and name.endswith(("Wqkv.weight", "mlp.Wo.weight")):
+                print(f"  {name}: {rel_err(eng.download(name, 'grad'), want[name]):.3g}", flush=True)
+    med = float(np.median(errs))
+    print(f"{label} {prec}: grad relErr worst {worst:.3g} ({worst_name}), median {med:.3g} over {len(errs)} "
+          f"tensors", flush=True)
+    assert med <= GRAD_MEDIAN_TOL[prec], (label, prec, med)
+    return worst
+
+
+@pytest.mark.parametrize("prec", ["fp32", "bf16"])
+def test_backward_matches_oracle_small(prec):
+    from decide_amd.train import TrainEngine
+
+    cfg = small_cfg()
+    w = weights_for(cfg)
+    batch = train_batch(cfg.vocab, cfg.vocab - 1)
+    print(f"case: small backward {prec}, T={sum(len(s.ids) for s in batch)}", flush=True)
+    want_logits, dl, want = oracle_grads(cfg, effective_weights(w, prec), batch)
+    with TrainEngine(cfg, w, precision=prec) as eng:
+        logits = eng.forward(batch)
+        if prec == "fp32":
+            assert np.all(np.abs(logits.astype(np.float64) - want_logits) <= 1e-4 * (1 + np.abs(want_logits)))
+        eng.backward(dl)
+        check_grads(eng, want, prec, label="small")
+
+
+def test_backward_frozen_layers_fp32():
+    """trainFrom = 2 without embeddings: layers 0-1 and the embeddings get
+    exactly zero, the rest match (TestForwardBackwardMatchesPyTorch's frozen
+    rule, nn_test.go:139-150)."""
+    from decide_amd.train import TrainEngine
+
+    cfg = small_cfg()
+    w = weights_for(cfg)
+    batch = train_batch(cfg.vocab, cfg.vocab - 1, seed=1)
+    print("case: frozen layers fp32", flush=True)
+    _, dl, want = oracle_grads(cfg, w, batch, train_from=2, train_emb=False)
+    with TrainEngine(cfg, w, precision="fp32", train_from=2, train_emb=False) as eng:
+        eng.forward(batch)
+        eng.backward(dl)
+        check_grads(eng, want, "fp32", train_from=2, train_emb=False, label="frozen")
+
+
+def test_backward_accumulates_and_zero_grad():
+    """Two backward passes add (the kernels are deterministic, so exactly
+    2x); dn_zero_grad clears every gradient."""
+    from decide_amd.nn import tensor_shapes
+    from decide_amd.train import TrainEngine
+
+    cfg = small_cfg(layers=2)
+    w = weights_for(cfg)
+    batch = train_batch(cfg.vocab, cfg.vocab - 1, seed=2)
+    print("case: accumulate bf16", flush=True)
+    _, dl, _ = oracle_grads(cfg, w, batch)
+    with TrainEngine(cfg, w, precision="bf16") as eng:
+        eng.forward(batch)
+        eng.backward(dl)
+        once = {n: eng.download(n, "grad") for n in tensor_shapes(cfg)}
+        eng.forward(batch)
+        eng.backward(dl)
+        for n, g in once.items():
+            got = eng.download(n, "grad")
+            if n == "model.embeddings.tok_embeddings.weight":
+                # dTok[id] += dE[t] per token, in token order (backward.go:102-108):
+                # a repeated id's second pass adds onto the first pass's sum.
+                assert rel_err(got, 2 * g) <= 1e-6, n
+            else:
+                assert np.array_equal(got, 2 * g), n
+        eng.zero_grad()
+        assert all(not np.any(eng.download(n, "grad")) for n in once)
+        assert eng.grad_sumsq() == 0.0
+
+
+@pytest.mark.parametrize("prec", ["fp32", "bf16"])
+def test_adamw_matches_closed_form_and_oracle(prec):
+    """Step 1 from zero moments equals p - (rate*g'/(|g'|+eps) + wd*rate*p)
+    with g' = scale*g; grad_sumsq equals the float64 sum of the downloaded
+    gradients; two steps equal the oracle's AdamW run on the same
+    gradients; after an update the inference forward uses the new weights
+    (its logits equal a fresh engine's loaded with them)."""
+    from decide_amd.nn import Engine, tensor_shapes
+    from decide_amd.train import TrainEngine
+
+    cfg = small_cfg(layers=2)
+    w = weights_for(cfg)
+    batch = train_batch(cfg.vocab, cfg.vocab - 1, seed=3)
+    print(f"case: adamw {prec}", flush=True)
+    _, dl, _ = oracle_grads(cfg, w, batch)
+    shapes = tensor_shapes(cfg)
+    lr, head_lr, wd, scale = 1e-3, 3e-3, 0.01, 0.5
+    with TrainEngine(cfg, w, precision=prec, train_from=1, train_emb=False) as eng:
+        eng.forward(batch)
+        eng.backward(dl)
+        grads = {n: eng.download(n, "grad") for n in shapes}
+        trainable = [n for n in shapes if not frozen(n, 1, False)]
+        ss = sum(float((grads[n].astype(np.float64) ** 2).sum()) for n in trainable)
+        assert abs(eng.grad_sumsq() - ss) <= 1e-12 * ss
+        eng.update(lr, head_lr, wd, scale)
+        for n, shape in shapes.items():
+            p0, p1 = w[n].astype(np.float64), eng.download(n).astype(np.float64)
+            if n not in trainable:
+                assert np.array_equal(p1, p0), n
+                continue
+            rate = head_lr if n.startswith("scorer.") else lr
+            decay = len(shape) == 2 and n != "model.embeddings.tok_embeddings.weight"
+            gs = grads[n].astype(np.float64) * scale
+            want = p0 - (rate * gs / (np.abs(gs) + 1e-8) + (wd * rate if decay else 0.0) * p0)
+            assert np.allclose(p1, want, rtol=0, atol=2e-6 * max(1.0, float(np.abs(p0).max()))), n
+            assert np.allclose(eng.download(n, "m"), 0.1 * gs, rtol=1e-5, atol=1e-12), n
+        eng.update(lr, head_lr, wd, scale)  # second step on the same gradients
+        # The oracle's AdamW on the device's gradients, two steps.
+        om = oracle.OracleModel(cfg, w)
+        og = oracle.OracleModel(cfg, grads)
+        opt = oracle.OracleAdamW(om, og, weight_decay=wd, train_from=1, train_emb=False)
+        opt.update(lr, head_lr, scale)
+        opt.update(lr, head_lr, scale)
+        for n, shape in shapes.items():
+            got = eng.download(n).reshape(-1)
+            ref = om.get(n, got.size)
+            assert np.max(np.abs(got - ref)) <= 1e-7 * max(1.0, float(np.abs(ref).max())), n
+        new_w = {n: eng.download(n) for n in shapes}
+        after = eng.infer(batch)
+    with Engine(cfg, new_w, precision=prec) as fresh:
+        assert np.array_equal(fresh.forward(batch), after)
+
+
+@pytest.mark.parametrize("prec", ["fp32", "bf16"])
+def test_backward_matches_oracle_modernbert_base(prec):
+    """ModernBERT-base geometry (22 layers, hidden 768, window 64): a cfg2
+    Choice request (112 tokens) and a 300-token plain sequence."""
+    from decide_amd import modernbert_base
+    from decide_amd.synth import config_batch, pack_request
+    from decide_amd.nn import build_sequence, MASK_ID
+    from decide_amd.train import TrainEngine
+
+    cfg = modernbert_base()
+    w = weights_for(cfg, seed=7, std=0.02)
+    rng = np.random.default_rng(9)
+    batch = config_batch("cfg2", vocab=cfg.vocab) + [
+        build_sequence(pack_request(rng, 260, [20, 20], cfg.vocab), MASK_ID, independent=False)]
+    print(f"case: modernbert-base backward {prec}, T={sum(len(s.ids) for s in batch)}", flush=True)
+    want_logits, dl, want = oracle_grads(cfg, effective_weights(w, prec), batch)
+    with TrainEngine(cfg, w, precision=prec) as eng:
+        logits = eng.forward(batch)
+        if prec == "fp32":
+            assert np.all(np.abs(logits.astype(np.float64) - want_logits) <= 1e-4 * (1 + np.abs(want_logits)))
+        eng.backward(dl)
+        check_grads(eng, want, prec, label="base")
+
+
+def test_training_errors():
+    """Backward needs a training forward (an inference forward invalidates
+    it) and the forward's row count; training must be enabled before bf16
+    weights are uploaded."""
+    from decide_amd import native
+    from decide_amd.nn import Engine
+    from decide_amd.train import TrainEngine
+
+    cfg = small_cfg(layers=2)
+    w = weights_for(cfg)
+    batch = train_batch(cfg.vocab, cfg.vocab - 1)
+    R = sum(len(s.mask_pos) for s in batch)
+    with TrainEngine(cfg, w, precision="bf16") as eng:
+        with pytest.raises(native.InvalidArgument):
+            eng.backward(np.zeros(R, np.float32))
+        eng.forward(batch)
+        with pytest.raises(native.InvalidArgument):
+            eng.backward(np.zeros(R + 1, np.float32))
+        eng.infer(batch)
+        with pytest.raises(native.InvalidArgument):
+            eng.backward(np.zeros(R, np.float32))
+        eng.forward(batch)
+        eng.backward(np.zeros(R, np.float32))
+    with Engine(cfg, w, precision="bf16") as eng:
+        rc = native.lib.dn_enable_training(eng.handle)
+        assert rc == native.DN_INVALID_ARG
+
+
+def test_training_reduces_loss():
+    """Five AdamW steps on one batch lower the trainer's soft cross-entropy
+    (internal/train/trainer.go:308-321) in bf16."""
+    from decide_amd.train import TrainEngine, soft_cross_entropy
+
+    cfg = small_cfg()
+    w = weights_for(cfg, std=0.05)
+    batch = train_batch(cfg.vocab, cfg.vocab - 1, seed=4)
+    rng = np.random.default_rng(0)
+    targets = [np.eye(len(s.mask_pos))[int(rng.integers(0, len(s.mask_pos)))] for s in batch]
+    losses = []
+    with TrainEngine(cfg, w, precision="bf16") as eng:
+        for _ in range(6):
+            logits = eng.forward(batch)
+            loss, dl = soft_cross_entropy(logits, targets, len(batch))
+            losses.append(loss)
+            eng.backward(dl)
+            gn = eng.grad_norm()
+            eng.update(1e-3, 1e-3, 0.01, min(1.0, 1.0 / (gn + 1e-6)))
+            eng.zero_grad()
+    print("losses", [round(x, 4) for x in losses], flush=True)
+    assert losses[-1] < losses[0]
