@@ -9,6 +9,7 @@ seeded token ids; see decide_amd/synth.py.
 
   python bench.py [--steps K] [--warmup W] [--config cfg3] [--precision bf16]
   python bench.py --systemone [--steps K]   one SystemOne call, batched vs serial
+  python bench.py --train [--steps K]       one training step (forward, backward, AdamW)
   python bench.py --tokenizer               host tokenizer throughput (CPU only)
 """
 from __future__ import annotations
@@ -181,6 +182,131 @@ def systemone(args) -> int:
     return 0
 
 
+TRAIN_METRIC = ("training tokens/sec: one AdamW step over 32 examples (micro-batches within the trainer's 4000-token "
+                "GPU budget), ModernBERT-base, 1 MI355X")
+
+
+def train_batches(cfg, n_examples=32, token_budget=4000, seed=0):
+    """The trainer's step shape (internal/train/trainer.go:61-90, :270-330):
+    BatchExamples 32 examples per optimizer step, packed to MaxLen 384
+    (256-token premise + 8 options x 16), micro-batches of whole examples
+    within TokenBudget (4000 by default on a GPU); one-hot targets."""
+    from decide_amd.nn import MASK_ID, build_sequence
+    from decide_amd.synth import pack_request
+
+    rng = np.random.default_rng(2000 + seed)
+    ex = [build_sequence(pack_request(rng, 256, [16] * 8, cfg.vocab), MASK_ID, True) for _ in range(n_examples)]
+    targets = [np.eye(8)[int(rng.integers(0, 8))] for _ in range(n_examples)]
+    per_micro = max(1, token_budget // 384)
+    micro = [(ex[i:i + per_micro], targets[i:i + per_micro]) for i in range(0, n_examples, per_micro)]
+    return ex, micro
+
+
+def train_bench(args) -> int:
+    """Times one optimizer step of the trainer's loop on the device
+    (trainer.go:290-330): per micro-batch dn_forward_train, the soft
+    cross-entropy on the host, dn_backward; then the gradient norm, clipping,
+    dn_adamw_step and dn_zero_grad. Prints one JSON line."""
+    import torch
+
+    from decide_amd import modernbert_base
+    from decide_amd.synth import random_weights
+    from decide_amd.train import TrainEngine, soft_cross_entropy
+
+    cfg = modernbert_base()
+    log("generating weights")
+    weights = random_weights(cfg, seed=0)
+    ex, micro = train_batches(cfg, token_budget=args.token_budget)
+    T = sum(len(s.ids) for s in ex)
+    log(f"train: {len(ex)} examples, {T} tokens per step, {len(micro)} micro-batches")
+    torch.cuda.init()
+    eng = TrainEngine(cfg, weights, precision=args.precision, train_from=0, train_emb=False)
+    n_items = len(ex)
+
+    phases = {"forward": 0.0, "backward": 0.0, "update": 0.0}
+
+    def step(timed=False):
+        loss = 0.0
+        for batch, targets in micro:
+            t0 = time.perf_counter()
+            logits = eng.forward(batch)
+            t1 = time.perf_counter()
+            l, dl = soft_cross_entropy(logits, targets, n_items)
+            loss += l
+            eng.backward(dl)
+            t2 = time.perf_counter()
+            if timed:
+                phases["forward"] += t1 - t0
+                phases["backward"] += t2 - t1
+        t0 = time.perf_counter()
+        gn = eng.grad_norm()
+        scale = 1.0 if gn <= 1.0 else 1.0 / (gn + 1e-6)
+        eng.update(4e-5, 3e-4, 0.01, scale)
+        eng.zero_grad()
+        if timed:
+            phases["update"] += time.perf_counter() - t0
+        return loss / n_items
+
+    log(f"warmup {args.warmup}")
+    for _ in range(args.warmup):
+        step()
+    log(f"timing {args.steps} steps")
+    losses, per_step = [], []
+    for _ in range(args.steps):
+        t0 = time.perf_counter()
+        losses.append(step(timed=True))
+        per_step.append(time.perf_counter() - t0)
+    wall = sum(per_step)
+    result = {
+        "metric": TRAIN_METRIC,
+        "value": round(T * args.steps / wall, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall * 1e3 / args.steps, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": args.precision,
+        "data": "synthetic: random-init weights N(0,0.02) (numpy PCG64 seed 0), 32 packed examples "
+                "[CLS] 254 ids [SEP] ([MASK] 15 ids)x8, one-hot targets (bench.py train_batches)",
+        "config": {"workload": "train: 32 examples x 384 tokens per AdamW step, micro-batches of %d examples "
+                               "(TokenBudget %d), all 22 layers trainable, embeddings frozen (trainer defaults)"
+                               % (len(micro[0][0]), args.token_budget),
+                   "examples_per_step": len(ex), "tokens_per_step": T, "micro_batches": len(micro),
+                   "token_budget": args.token_budget, "precision": args.precision},
+        "phase_ms_per_step": {k: round(v * 1e3 / args.steps, 3) for k, v in phases.items()},
+        "loss_first_last": [round(losses[0], 5), round(losses[-1], 5)],
+    }
+    if not args.no_cpu_baseline:
+        import oracle
+
+        log("cpu baseline")
+        threads = cpu_threads()
+        oracle.set_workers(threads)
+        model = oracle.OracleModel(cfg, weights)
+        secs, toks, done = 0.0, 0, 0
+        while secs < args.cpu_budget and done < len(ex):
+            s = ex[done]
+            t0 = time.perf_counter()
+            logits = model.forward_train([s], 0)
+            _, dl = soft_cross_entropy(logits, [micro[0][1][0]], 1)
+            g = model.zeros_like()
+            model.backward(dl, g, train_emb=False)
+            secs += time.perf_counter() - t0
+            toks += len(s.ids)
+            done += 1
+        result["cpu_baseline"] = {"value": round(toks / secs, 2), "unit": "tokens/s", "cores": threads,
+                                  "kind": "port",
+                                  "sample": f"{done} example(s) of 384 tokens, training forward + backward each "
+                                            f"({secs:.1f} s; the optimizer step is not included); C++ restatement "
+                                            "of the reference Go path (oracle/)"}
+    eng.close()
+    print(json.dumps(result), flush=True)
+    return 0
+
+
 def synthetic_prose(seed: int, n_docs: int, doc_words: int):
     """Pseudo-English documents: syllable words, capitals, digits,
     punctuation, contractions, some accented words and line breaks."""
@@ -293,6 +419,10 @@ def main() -> int:
                     help="time the host tokenizer (dn_tokenize) against HuggingFace tokenizers; no GPU")
     ap.add_argument("--systemone", action="store_true",
                     help="time one SystemOne call (24 questions) batched into one forward vs one forward each")
+    ap.add_argument("--train", action="store_true",
+                    help="time one training step (forward, backward, AdamW) at the trainer's GPU shape")
+    ap.add_argument("--token-budget", type=int, default=4000,
+                    help="--train: tokens per micro-batch (the trainer's TokenBudget; 4000 is its GPU default)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
@@ -303,6 +433,8 @@ def main() -> int:
         return tokenizer_bench(args)
     if args.systemone:
         return systemone(args)
+    if args.train:
+        return train_bench(args)
 
     import torch
 

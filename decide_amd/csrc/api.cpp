@@ -76,9 +76,17 @@ void release_train(TrainState &tr) {
   }
   tr.layers.clear();
   DevBuf *bufs[] = {&tr.dcur, &tr.dprev, &tr.dh1, &tr.dact, &tr.dwi, &tr.dn2, &tr.dctx, &tr.dqkv, &tr.dn1,
-                    &tr.dyop, &tr.dyT, &tr.xT, &tr.dsum, &tr.part, &tr.lnpart, &tr.dE, &tr.dl, &tr.contrib,
-                    &tr.emb_order, &tr.emb_seg, &tr.emb_id, &tr.sq_part, &tr.sq_out};
+                    &tr.dyop, &tr.dsum, &tr.part, &tr.lnpart, &tr.dE, &tr.dl, &tr.contrib, &tr.emb_order,
+                    &tr.emb_seg, &tr.emb_id, &tr.sq_part, &tr.sq_out, &tr.opT[0], &tr.opT[1]};
+  if (tr.side) (void)hipStreamSynchronize(tr.side);
   for (DevBuf *b : bufs) release(*b);
+  for (int i = 0; i < 2; i++) {
+    if (tr.ev_ready[i]) (void)hipEventDestroy(tr.ev_ready[i]);
+    if (tr.ev_done[i]) (void)hipEventDestroy(tr.ev_done[i]);
+    tr.ev_ready[i] = tr.ev_done[i] = nullptr;
+  }
+  if (tr.side) (void)hipStreamDestroy(tr.side);
+  tr.side = nullptr;
   tr.have_forward = false;
 }
 

@@ -73,6 +73,69 @@ __global__ __launch_bounds__(256) void transpose_kernel(const TI *src, int rows,
   }
 }
 
+// The same with 8-element vectors (16 bytes of bf16, 32 of fp32) on both
+// sides: needs cols, lds and ldt multiples of 8 and rows_pad a multiple of 64.
+template <class T>
+struct Vec8;
+template <>
+struct Vec8<bf16> {
+  static __device__ __forceinline__ void load(const bf16 *p, float (&v)[8]) {
+    const uint4 u = *(const uint4 *)p;
+    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      v[2 * i] = __uint_as_float(w[i] << 16);
+      v[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+    }
+  }
+  static __device__ __forceinline__ void store(bf16 *p, const float (&v)[8]) {
+    bf16x8 o;
+#pragma unroll
+    for (int i = 0; i < 8; i++) o[i] = (bf16)v[i];
+    *(bf16x8 *)p = o;
+  }
+};
+template <>
+struct Vec8<float> {
+  static __device__ __forceinline__ void load(const float *p, float (&v)[8]) {
+    const float4 a = *(const float4 *)p, b = *(const float4 *)(p + 4);
+    v[0] = a.x, v[1] = a.y, v[2] = a.z, v[3] = a.w, v[4] = b.x, v[5] = b.y, v[6] = b.z, v[7] = b.w;
+  }
+  static __device__ __forceinline__ void store(float *p, const float (&v)[8]) {
+    *(float4 *)p = make_float4(v[0], v[1], v[2], v[3]);
+    *(float4 *)(p + 4) = make_float4(v[4], v[5], v[6], v[7]);
+  }
+};
+
+template <class TI, class TO>
+__global__ __launch_bounds__(256) void transpose8_kernel(const TI *src, int rows, int cols, int lds, TO *dstT,
+                                                         int ldt, int rows_pad, TO *copy) {
+  __shared__ float tile[64][65];
+  const int tid = threadIdx.x;
+  const int c0 = blockIdx.x * 64, r0 = blockIdx.y * 64;
+#pragma unroll
+  for (int j = 0; j < 2; j++) {
+    const int it = tid + 256 * j, r = it >> 3, cg = (it & 7) * 8;
+    float v[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+    if (r0 + r < rows && c0 + cg < cols) {
+      Vec8<TI>::load(src + (size_t)(r0 + r) * lds + c0 + cg, v);
+      if (copy) Vec8<TO>::store(copy + (size_t)(r0 + r) * cols + c0 + cg, v);
+    }
+#pragma unroll
+    for (int u = 0; u < 8; u++) tile[r][cg + u] = v[u];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < 2; j++) {
+    const int it = tid + 256 * j, c = it >> 3, rg = (it & 7) * 8;
+    if (c0 + c >= cols || r0 + rg >= rows_pad) continue;
+    float v[8];
+#pragma unroll
+    for (int u = 0; u < 8; u++) v[u] = tile[rg + u][c];
+    Vec8<TO>::store(dstT + (size_t)(c0 + c) * ldt + r0 + rg, v);
+  }
+}
+
 // GeGLU on the stored Wi output (rows interleaved in 64-column groups: 32
 // value columns, then the 32 matching gate columns): act[t][32g+r] =
 // gelu(wi[t][64g+r]) * wi[t][64g+32+r] (forward.go:327-336).
@@ -107,8 +170,9 @@ __global__ void geglu_bwd_kernel(const float *dact, const T *wi, T *dwi, int row
 // The row statistics are recomputed from x as the forward computes them (f64).
 // x rows are x[r] or, with ids, the embedding row tok[ids[r]].
 constexpr int LNB_WAVES = 4;
-__global__ __launch_bounds__(256) void ln_bwd_kernel(float *dx, const float *dy, const float *x, const int *ids,
-                                                     const float *w, float eps, int rows, int dim, float *part) {
+__global__ __launch_bounds__(256) void ln_bwd_kernel(float *dx, const float *res, const float *dy, const float *x,
+                                                     const int *ids, const float *w, float eps, int rows, int dim,
+                                                     float *part) {
   constexpr int MAXE = 16;  // dim <= 1024: 16 elements per lane
   __shared__ float sw[LNB_WAVES][1024];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -152,11 +216,12 @@ __global__ __launch_bounds__(256) void ln_bwd_kernel(float *dx, const float *dy,
       }
     const float a = (float)(wave_sum_d(s1) / (double)dim), b = (float)(wave_sum_d(s2) / (double)dim);
     float *o = dx + (size_t)r * dim;
+    const float *base = res ? res + (size_t)r * dim : o;  // dx = res + ... (res given) or dx += ...
 #pragma unroll
     for (int j = 0; j < MAXE; j++)
       if (j < ne) {
 #pragma clang fp contract(off)
-        o[lane + 64 * j] += rs * (gv[j] * w[lane + 64 * j] - a - xv[j] * b);
+        o[lane + 64 * j] = base[lane + 64 * j] + rs * (gv[j] * w[lane + 64 * j] - a - xv[j] * b);
       }
   }
 #pragma unroll
@@ -171,12 +236,38 @@ __global__ __launch_bounds__(256) void ln_bwd_kernel(float *dx, const float *dy,
   }
 }
 
-// out[i] += sum over p of part[p * n + i], in p order.
-__global__ void sum_partials_kernel(const float *part, int nparts, int n, float *out) {
+// Column sums of part [nparts x n] in two launches with a fixed order:
+// colsum_kernel: block (x, y) sums rows y*per .. y*per+per-1 of columns
+// 64x .. 64x+63 (each wave every 4th row, 4 independent loads in flight per
+// lane, then the 4 waves in order) into part2[y][col]; colsum_final_kernel
+// adds the NG partial rows, in order, into out.
+constexpr int COLSUM_NG = 16;
+__global__ __launch_bounds__(256) void colsum_kernel(const float *part, int nparts, int n, float *part2) {
+  __shared__ float red[4][64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int c = blockIdx.x * 64 + lane;
+  const int per = (nparts + COLSUM_NG - 1) / COLSUM_NG;
+  const int p0 = blockIdx.y * per, p1 = min(nparts, p0 + per);
+  float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  if (c < n) {
+    int p = p0 + wave;
+    for (; p + 12 < p1; p += 16) {
+#pragma unroll
+      for (int u = 0; u < 4; u++) acc[u] += part[(size_t)(p + 4 * u) * n + c];
+    }
+    for (; p < p1; p += 4) acc[0] += part[(size_t)p * n + c];
+  }
+  red[wave][lane] = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+  __syncthreads();
+  if (wave == 0 && c < n) part2[(size_t)blockIdx.y * n + c] = ((red[0][lane] + red[1][lane]) + red[2][lane]) + red[3][lane];
+}
+
+__global__ void colsum_final_kernel(const float *part2, int n, float *out) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n) return;
   float acc = 0.0f;
-  for (int p = 0; p < nparts; p++) acc += part[(size_t)p * n + i];
+#pragma unroll
+  for (int y = 0; y < COLSUM_NG; y++) acc += part2[(size_t)y * n + i];
   out[i] += acc;
 }
 
@@ -430,11 +521,19 @@ __global__ __launch_bounds__(256) void sumsq_kernel(const float *x, size_t n, do
   if (threadIdx.x == 0) part[blockIdx.x] = red[0] + red[1] + red[2] + red[3];
 }
 
-__global__ void sum_doubles_kernel(const double *part, int n, double *out) {
-  if (threadIdx.x != 0 || blockIdx.x != 0) return;
+// One block of 256 threads: strided per-thread sums, then the 256 sums in a
+// fixed tree order.
+__global__ __launch_bounds__(256) void sum_doubles_kernel(const double *part, int n, double *out) {
+  __shared__ double red[256];
   double s = 0;
-  for (int i = 0; i < n; i++) s += part[i];
-  *out = s;
+  for (int i = threadIdx.x; i < n; i += 256) s += part[i];
+  red[threadIdx.x] = s;
+  __syncthreads();
+  for (int w = 128; w > 0; w >>= 1) {
+    if ((int)threadIdx.x < w) red[threadIdx.x] += red[threadIdx.x + w];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) *out = red[0];
 }
 
 // AdamW (Update, optim.go:118-141), written unfused as the reference
@@ -471,6 +570,20 @@ hipError_t launch_transpose(int precision_in, int precision_out, const void *src
                             void *dstT, int ldt, int rows_pad, void *copy, hipStream_t s) {
   if (rows_pad <= 0 || cols <= 0) return hipSuccess;
   const dim3 grid((cols + 63) / 64, (rows_pad + 63) / 64), block(256);
+  if (cols % 8 == 0 && lds % 8 == 0 && ldt % 8 == 0 && rows_pad % 64 == 0) {
+    if (precision_in == 0 && precision_out == 1)
+      hipLaunchKernelGGL((transpose8_kernel<float, bf16>), grid, block, 0, s, (const float *)src, rows, cols, lds,
+                         (bf16 *)dstT, ldt, rows_pad, (bf16 *)copy);
+    else if (precision_in == 0 && precision_out == 0)
+      hipLaunchKernelGGL((transpose8_kernel<float, float>), grid, block, 0, s, (const float *)src, rows, cols, lds,
+                         (float *)dstT, ldt, rows_pad, (float *)copy);
+    else if (precision_in == 1 && precision_out == 1)
+      hipLaunchKernelGGL((transpose8_kernel<bf16, bf16>), grid, block, 0, s, (const bf16 *)src, rows, cols, lds,
+                         (bf16 *)dstT, ldt, rows_pad, (bf16 *)copy);
+    else
+      return hipErrorInvalidValue;
+    return hipGetLastError();
+  }
   if (precision_in == 0 && precision_out == 1)
     hipLaunchKernelGGL((transpose_kernel<float, bf16>), grid, block, 0, s, (const float *)src, rows, cols, lds,
                        (bf16 *)dstT, ldt, rows_pad, (bf16 *)copy);
@@ -509,17 +622,21 @@ hipError_t launch_geglu_bwd(int precision, const float *dact, const void *wi, vo
   return hipGetLastError();
 }
 
-int ln_bwd_blocks(int rows) { return std::max(1, std::min(512, (rows + LNB_WAVES - 1) / LNB_WAVES)); }
+int ln_bwd_blocks(int rows) { return std::max(1, std::min(1024, (rows + LNB_WAVES - 1) / LNB_WAVES)) + COLSUM_NG; }
 
-hipError_t launch_ln_bwd(float *dx, const float *dy, const float *x, const int *ids, const float *w, float eps, int rows,
-                         int dim, float *part, float *dw, hipStream_t s) {
+hipError_t launch_ln_bwd(float *dx, const float *res, const float *dy, const float *x, const int *ids, const float *w,
+                         float eps, int rows, int dim, float *part, float *dw, hipStream_t s) {
   if (rows <= 0) return hipSuccess;
   if (dim % 64 != 0 || dim > 1024) return hipErrorInvalidValue;
-  const int nb = ln_bwd_blocks(rows);
-  hipLaunchKernelGGL(ln_bwd_kernel, dim3(nb), dim3(256), 0, s, dx, dy, x, ids, w, eps, rows, dim, part);
+  const int nb = ln_bwd_blocks(rows) - COLSUM_NG;
+  hipLaunchKernelGGL(ln_bwd_kernel, dim3(nb), dim3(256), 0, s, dx, res, dy, x, ids, w, eps, rows, dim, part);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || !dw) return e;
-  hipLaunchKernelGGL(sum_partials_kernel, dim3(blocks(dim)), dim3(256), 0, s, part, nb, dim, dw);
+  float *part2 = part + (size_t)nb * dim;
+  hipLaunchKernelGGL(colsum_kernel, dim3((dim + 63) / 64, COLSUM_NG), dim3(256), 0, s, part, nb, dim, part2);
+  e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  hipLaunchKernelGGL(colsum_final_kernel, dim3(blocks(dim)), dim3(256), 0, s, part2, dim, dw);
   return hipGetLastError();
 }
 
@@ -562,7 +679,7 @@ hipError_t launch_sumsq(const float *x, size_t n, double *part, hipStream_t s) {
 }
 
 hipError_t launch_sum_doubles(const double *part, int n, double *out, hipStream_t s) {
-  hipLaunchKernelGGL(sum_doubles_kernel, dim3(1), dim3(64), 0, s, part, n, out);
+  hipLaunchKernelGGL(sum_doubles_kernel, dim3(1), dim3(256), 0, s, part, n, out);
   return hipGetLastError();
 }
 

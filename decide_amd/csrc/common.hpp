@@ -107,8 +107,8 @@ enum { EPI_F32 = 0, EPI_STORE = 1, EPI_GEGLU = 2 };
 hipError_t launch_gemm(int precision, int epi, const GemmArgs &a, hipStream_t s);
 // Split-K fp32-output GEMM: `splits` partial products, each over a.K / splits
 // of K (a.K % (splits * 64) == 0), written to partial + split * M * N
-// (row-major, ldc = N), then added in split order into C (M x N, ldc = N,
-// accumulated into). partial holds splits * M * N floats.
+// (row-major, ldc = N), then summed in split order into C (M x N, ldc = N;
+// added to C when a.accumulate, else stored). partial holds splits * M * N floats.
 hipError_t launch_gemm_splitk(int precision, const GemmArgs &a, int splits, float *partial, hipStream_t s);
 bool gemm_shape_ok(int precision, int N, int K);
 
@@ -193,9 +193,11 @@ hipError_t launch_transpose(int precision_in, int precision_out, const void *src
 hipError_t launch_geglu_fwd(int precision, const void *wi, void *act, int rows, int I, hipStream_t s);
 hipError_t launch_geglu_bwd(int precision, const float *dact, const void *wi, void *dwi, int rows, int I,
                             hipStream_t s);
-int ln_bwd_blocks(int rows);  // partial rows of dw written by launch_ln_bwd (part holds ln_bwd_blocks x dim)
-hipError_t launch_ln_bwd(float *dx, const float *dy, const float *x, const int *ids, const float *w, float eps, int rows,
-                         int dim, float *part, float *dw, hipStream_t s);
+// LayerNorm backward: dx = res + LNbwd(dy) when res is given, else dx += LNbwd(dy);
+// dw += the weight gradient (part holds ln_bwd_blocks(rows) x dim floats of scratch).
+int ln_bwd_blocks(int rows);
+hipError_t launch_ln_bwd(float *dx, const float *res, const float *dy, const float *x, const int *ids, const float *w,
+                         float eps, int rows, int dim, float *part, float *dw, hipStream_t s);
 hipError_t launch_add(float *dst, const float *src, size_t n, hipStream_t s);
 hipError_t launch_embed_bwd(const float *dE, const int *order, const int *seg_start, const int *seg_id, int nseg,
                             int dim, float *gtok, hipStream_t s);

@@ -61,8 +61,14 @@ struct TrainState {
   bool have_forward = false;  // the activations of the last dn_forward_train are intact
   int T = 0, R = 0;
   std::vector<int32_t> ids;   // token ids of the last training forward
-  DevBuf dcur, dprev, dh1, dact, dwi, dn2, dctx, dqkv, dn1, dyop, dyT, xT, dsum, part, lnpart, dE, dl, contrib;
+  DevBuf dcur, dprev, dh1, dact, dwi, dn2, dctx, dqkv, dn1, dyop, dsum, part, lnpart, dE, dl, contrib;
   DevBuf emb_order, emb_seg, emb_id, sq_part, sq_out;
+  // Weight-gradient GEMMs run on a second stream: per layer parity, the
+  // transposed operands of the layer's four GEMMs, and the events that order
+  // them against the main stream (operands ready / arena free again).
+  DevBuf opT[2];
+  hipStream_t side = nullptr;
+  hipEvent_t ev_ready[2] = {nullptr, nullptr}, ev_done[2] = {nullptr, nullptr};
 };
 
 struct dn_ctx {

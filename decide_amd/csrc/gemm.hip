@@ -556,13 +556,13 @@ hipError_t launch_skinny(int epi, const GemmArgs &a, hipStream_t s) {
   return launch_skinny_cfg<T, 2, 1, 8>(epi, a, s);
 }
 
-// C[i] += sum over splits of part[s * n + i], in split order.
-__global__ void splitk_reduce_kernel(const float *part, int splits, size_t n, float *C) {
+// C (+)= sum over splits of part[s * n + i], in split order.
+__global__ void splitk_reduce_kernel(const float *part, int splits, size_t n, float *C, int accumulate) {
   const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n) return;
   float acc = 0.0f;
   for (int s = 0; s < splits; s++) acc += part[(size_t)s * n + i];
-  C[i] += acc;
+  C[i] = accumulate ? C[i] + acc : acc;
 }
 
 }  // namespace
@@ -584,7 +584,7 @@ hipError_t launch_gemm_splitk(int precision, const GemmArgs &a0, int splits, flo
   if (e != hipSuccess) return e;
   const size_t n = (size_t)a0.M * a0.N;
   hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, partial, splits, n,
-                     (float *)a0.C);
+                     (float *)a0.C, a0.accumulate);
   return hipGetLastError();
 }
 

@@ -91,11 +91,14 @@ int refresh_wt(dn_ctx *c, const std::string &name, TensorSlot &t) {
   return DN_OK;
 }
 
+// Splits of the token (K) dimension for a weight-gradient GEMM: enough
+// workgroups for two per CU (about 512 tiles in all) while each split keeps
+// at least 512 tokens of K; the partial outputs cost splits x M x N floats
+// of extra traffic.
 int split_count(int M, int N, int Tp) {
   const int tiles = ((M + 127) / 128) * (N / 128);
-  const int want = std::min(16, std::max(1, (1024 + tiles - 1) / tiles));
   const int kb = Tp / 64;
-  int s = std::min(want, kb);
+  int s = std::min({16, std::max(1, (512 + tiles - 1) / tiles), std::max(1, kb / 8)});
   while (s > 1 && kb % s) s--;
   return s;
 }
@@ -123,8 +126,8 @@ struct Bwd {
     return DN_OK;
   }
   // G[M x N] += A^T . B over the tokens, from the transposed copies At [M x Tp]
-  // and Bt [N x Tp].
-  int wgrad(int M, int N, const void *At, const void *Bt, float *G) {
+  // and Bt [N x Tp], on stream ws.
+  int wgrad(int M, int N, const void *At, const void *Bt, float *G, hipStream_t ws) {
     GemmArgs a{};
     a.A = At;
     a.lda = Tp;
@@ -134,7 +137,8 @@ struct Bwd {
     a.M = M;
     a.N = N;
     a.K = Tp;
-    HIPCHK(c, "gemm(split-K)", launch_gemm_splitk(prec, a, split_count(M, N, Tp), (float *)c->tr.part.p, s));
+    a.accumulate = 1;
+    HIPCHK(c, "gemm(split-K)", launch_gemm_splitk(prec, a, split_count(M, N, Tp), (float *)c->tr.part.p, ws));
     return DN_OK;
   }
   // dst [cols x Tp] = src[T x cols]^T in the operand type (zero past T); with
@@ -175,11 +179,25 @@ int backward_impl(dn_ctx *c, const float *dlogits) {
   HIPCHK(c, "hipMalloc", ensure(tr.dctx, es * TH));
   HIPCHK(c, "hipMalloc", ensure(tr.dqkv, es * T * 3 * H));
   HIPCHK(c, "hipMalloc", ensure(tr.dyop, es * TH));
-  HIPCHK(c, "hipMalloc", ensure(tr.dyT, es * (size_t)std::max(3 * H, 2 * I) * Tp));
-  HIPCHK(c, "hipMalloc", ensure(tr.xT, es * (size_t)std::max(H, I) * Tp));
+  // Transposed operands of one layer's weight-gradient GEMMs: dout, act, dwi,
+  // n2, dh1, ctx, dqkv, n1 (rows of Tp tokens), one arena per layer parity.
+  const size_t opT_rows = (size_t)8 * H + 3 * I;
+  for (int q = 0; q < 2; q++) HIPCHK(c, "hipMalloc", ensure(tr.opT[q], es * opT_rows * Tp));
+  if (!tr.side) {
+    HIPCHK(c, "hipStreamCreate", hipStreamCreateWithFlags(&tr.side, hipStreamNonBlocking));
+    for (int q = 0; q < 2; q++) {
+      HIPCHK(c, "hipEventCreate", hipEventCreateWithFlags(&tr.ev_ready[q], hipEventDisableTiming));
+      HIPCHK(c, "hipEventCreate", hipEventCreateWithFlags(&tr.ev_done[q], hipEventDisableTiming));
+    }
+  }
+  // Nothing of an earlier call may still use the arenas or the partials.
+  HIPCHK(c, "hipEventRecord", hipEventRecord(tr.ev_done[0], tr.side));
+  HIPCHK(c, "hipEventRecord", hipEventRecord(tr.ev_done[1], tr.side));
   HIPCHK(c, "hipMalloc", ensure(tr.dsum, 4 * (size_t)T * g.heads));
-  HIPCHK(c, "hipMalloc",
-         ensure(tr.part, 4 * (size_t)16 * std::max({(size_t)3 * H * H, (size_t)2 * I * H, (size_t)H * I})));
+  // split-K partials: weight gradients (<= 16 splits) and input gradients (<= 4 splits of T x max(H, I))
+  HIPCHK(c, "hipMalloc", ensure(tr.part, 4 * std::max((size_t)16 * std::max({(size_t)3 * H * H, (size_t)2 * I * H,
+                                                                             (size_t)H * I}),
+                                                        (size_t)4 * T * std::max(H, I))));
   HIPCHK(c, "hipMalloc", ensure(tr.lnpart, 4 * (size_t)ln_bwd_blocks(std::max(T, R)) * H));
   HIPCHK(c, "hipMalloc", ensure(tr.dl, 4 * (size_t)std::max(R, 1)));
   HIPCHK(c, "hipMalloc", ensure(tr.contrib, 4 * (size_t)std::max(R, 1) * 5 * H));
@@ -213,30 +231,38 @@ int backward_impl(dn_ctx *c, const float *dlogits) {
     const std::string p = layer_prefix(l);
     const LayerSave &S = tr.layers[l];
     const bool sliding = g.sliding[l] != 0;
+    const int par = l & 1;
+    // This parity's arena is free once the weight-gradient GEMMs of layer l+2 are done.
+    HIPCHK(c, "hipStreamWaitEvent", hipStreamWaitEvent(s, tr.ev_done[par], 0));
+    char *arena = (char *)tr.opT[par].p;
+    size_t row0 = 0;
+    auto slice = [&](int rows) {
+      void *q = arena + es * row0 * Tp;
+      row0 += rows;
+      return q;
+    };
+    void *doutT = slice(H), *actT = slice(I), *dwiT = slice(2 * I), *n2T = slice(H), *dh1T = slice(H),
+         *ctxT = slice(H), *dqkvT = slice(3 * H), *n1T = slice(H);
     // dout (fp32) as an operand: its transpose, and in bf16 its rounded copy.
-    RC(b.transpose(0, dcur, H, tr.dyT.p, prec == DN_PRECISION_BF16 ? tr.dyop.p : nullptr));
+    RC(b.transpose(0, dcur, H, doutT, prec == DN_PRECISION_BF16 ? tr.dyop.p : nullptr));
     const void *dout_op = prec == DN_PRECISION_BF16 ? tr.dyop.p : (const void *)dcur;
 
     // MLP: out = h1 + MlpWo(act)
     RC(b.gemm(EPI_F32, T, I, H, dout_op, H, wt(p + "mlp.Wo.weight"), H, dact, I));
-    RC(b.transpose(prec, S.act.p, I, tr.xT.p));
-    RC(b.wgrad(H, I, tr.dyT.p, tr.xT.p, grad(p + "mlp.Wo.weight")));
+    RC(b.transpose(prec, S.act.p, I, actT));
     HIPCHK(c, "geglu_bwd", launch_geglu_bwd(prec, dact, S.wi.p, tr.dwi.p, T, I, s));
-    RC(b.transpose(prec, tr.dwi.p, 2 * I, tr.dyT.p));
-    RC(b.transpose(prec, S.n2.p, H, tr.xT.p));
-    RC(b.wgrad(2 * I, H, tr.dyT.p, tr.xT.p, grad(p + "mlp.Wi.weight")));
+    RC(b.transpose(prec, tr.dwi.p, 2 * I, dwiT));
+    RC(b.transpose(prec, S.n2.p, H, n2T));
     RC(b.gemm(EPI_F32, T, H, 2 * I, tr.dwi.p, 2 * I, wt(p + "mlp.Wi.weight"), 2 * I, dn2, H));
-    HIPCHK(c, "hipMemcpyAsync", hipMemcpyAsync(dh1, dcur, 4 * TH, hipMemcpyDeviceToDevice, s));
-    HIPCHK(c, "ln_bwd(mlp_norm)", launch_ln_bwd(dh1, dn2, (const float *)S.h1.p, nullptr,
+    HIPCHK(c, "ln_bwd(mlp_norm)", launch_ln_bwd(dh1, dcur, dn2, (const float *)S.h1.p, nullptr,
                                                 (const float *)W(c, p + "mlp_norm.weight"), g.eps, T, H, lnpart,
                                                 grad(p + "mlp_norm.weight"), s));
 
     // Attention: h1 = in + Wo(ctx)
-    RC(b.transpose(0, dh1, H, tr.dyT.p, prec == DN_PRECISION_BF16 ? tr.dyop.p : nullptr));
+    RC(b.transpose(0, dh1, H, dh1T, prec == DN_PRECISION_BF16 ? tr.dyop.p : nullptr));
     const void *dh1_op = prec == DN_PRECISION_BF16 ? tr.dyop.p : (const void *)dh1;
     RC(b.gemm(EPI_STORE, T, H, H, dh1_op, H, wt(p + "attn.Wo.weight"), H, tr.dctx.p, H));
-    RC(b.transpose(prec, S.ctx.p, H, tr.xT.p));
-    RC(b.wgrad(H, H, tr.dyT.p, tr.xT.p, grad(p + "attn.Wo.weight")));
+    RC(b.transpose(prec, S.ctx.p, H, ctxT));
 
     AttnBwdArgs at{};
     at.qkv = S.qkv.p;
@@ -264,27 +290,38 @@ int backward_impl(dn_ctx *c, const float *dlogits) {
     at.scale_log2 = at.scale * 1.44269504088896340736f;
     HIPCHK(c, "attention_bwd", launch_attention_bwd(prec, at, s));
 
-    RC(b.transpose(prec, tr.dqkv.p, 3 * H, tr.dyT.p));
-    RC(b.transpose(prec, S.n1.p, H, tr.xT.p));
-    RC(b.wgrad(3 * H, H, tr.dyT.p, tr.xT.p, grad(p + "attn.Wqkv.weight")));
+    RC(b.transpose(prec, tr.dqkv.p, 3 * H, dqkvT));
+    RC(b.transpose(prec, S.n1.p, H, n1T));
     RC(b.gemm(EPI_F32, T, H, 3 * H, tr.dqkv.p, 3 * H, wt(p + "attn.Wqkv.weight"), 3 * H, dn1, H));
-    HIPCHK(c, "hipMemcpyAsync", hipMemcpyAsync(dprev, dh1, 4 * TH, hipMemcpyDeviceToDevice, s));
     if (l > 0) {
-      HIPCHK(c, "ln_bwd(attn_norm)", launch_ln_bwd(dprev, dn1, (const float *)S.hs.p, nullptr,
+      HIPCHK(c, "ln_bwd(attn_norm)", launch_ln_bwd(dprev, dh1, dn1, (const float *)S.hs.p, nullptr,
                                                    (const float *)W(c, p + "attn_norm.weight"), g.eps, T, H, lnpart,
                                                    grad(p + "attn_norm.weight"), s));
     } else {
+      HIPCHK(c, "hipMemcpyAsync", hipMemcpyAsync(dprev, dh1, 4 * TH, hipMemcpyDeviceToDevice, s));
       HIPCHK(c, "add", launch_add(dprev, dn1, TH, s));
     }
+    // The layer's weight gradients on the side stream, overlapping the next
+    // layer's input-gradient chain.
+    HIPCHK(c, "hipEventRecord", hipEventRecord(tr.ev_ready[par], s));
+    HIPCHK(c, "hipStreamWaitEvent", hipStreamWaitEvent(tr.side, tr.ev_ready[par], 0));
+    RC(b.wgrad(H, I, doutT, actT, grad(p + "mlp.Wo.weight"), tr.side));
+    RC(b.wgrad(2 * I, H, dwiT, n2T, grad(p + "mlp.Wi.weight"), tr.side));
+    RC(b.wgrad(H, H, dh1T, ctxT, grad(p + "attn.Wo.weight"), tr.side));
+    RC(b.wgrad(3 * H, H, dqkvT, n1T, grad(p + "attn.Wqkv.weight"), tr.side));
+    HIPCHK(c, "hipEventRecord", hipEventRecord(tr.ev_done[par], tr.side));
     std::swap(dcur, dprev);
   }
+  // Every weight gradient is in place before the call returns.
+  HIPCHK(c, "hipStreamWaitEvent", hipStreamWaitEvent(s, tr.ev_done[0], 0));
+  HIPCHK(c, "hipStreamWaitEvent", hipStreamWaitEvent(s, tr.ev_done[1], 0));
 
   // Embeddings (backward.go:96-109): LN backward of the emb norm from the
   // gathered rows, then the rows added into dTok in token order.
   if (tr.train_emb && tr.train_from == 0) {
     HIPCHK(c, "hipMalloc", ensure(tr.dE, 4 * TH));
     HIPCHK(c, "hipMemsetAsync", hipMemsetAsync(tr.dE.p, 0, 4 * TH, s));
-    HIPCHK(c, "ln_bwd(emb)", launch_ln_bwd((float *)tr.dE.p, dcur, (const float *)W(c, kTok),
+    HIPCHK(c, "ln_bwd(emb)", launch_ln_bwd((float *)tr.dE.p, nullptr, dcur, (const float *)W(c, kTok),
                                            (const int *)c->ids.p, (const float *)W(c, kEmbNorm), g.eps, T, H, lnpart,
                                            grad(kEmbNorm), s));
     std::vector<int> order(T);
