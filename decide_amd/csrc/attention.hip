@@ -801,7 +801,7 @@ __device__ __forceinline__ void store_row64(f32x16 (&x)[2], T *dst, const float 
 }
 
 template <class T>
-__global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnBwdArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void attn_bwd_dq_kernel(AttnBwdArgs a) {
   using MF = Mfma<T>;
   typedef typename MF::frag frag;
   constexpr int ROW = D * sizeof(T) + 16, NKS = D / MF::KSTEP, NPV = KTILE / MF::KSTEP;
@@ -956,7 +956,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnBwdArgs a) {
 }
 
 template <class T>
-__global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(AttnBwdArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void attn_bwd_dkdv_kernel(AttnBwdArgs a) {
   using MF = Mfma<T>;
   typedef typename MF::frag frag;
   constexpr int ROW = D * sizeof(T) + 16, NKS = D / MF::KSTEP, NPV = KTILE / MF::KSTEP;
@@ -1054,26 +1054,31 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(AttnBwdArgs a) {
       }
     }
     if (any == 0) continue;
+    // Staged one operand at a time after the barrier (fewer live registers:
+    // two workgroups per CU hide the load latency).
+    __syncthreads();  // the previous tile's reads are done
     {
-      RowStage<T> sq, so;
+      RowStage<T> sq;
       rows_load<T, true>(sq, qkv + head * D, ld, base, q0, n, a.cos_t, a.sin_t, a.kinfo, tid);
+      rows_store<T, true>(sq, sQ, tid);
+    }
+    {
+      RowStage<T> so;
       rows_load<T, false>(so, (const T *)a.dctx + head * D, H, base, q0, n, nullptr, nullptr, nullptr, tid);
+      rows_store<T, false>(so, sO, tid);
+    }
+    if (tid < KTILE) {
       int info = 0;
       float lse = INFINITY, dd = 0.0f;  // rows past the end: P = 2^-inf = 0
-      if (tid < KTILE && q0 + tid < n) {
+      if (q0 + tid < n) {
         const size_t t = (size_t)(base + q0 + tid);
         info = a.kinfo[t];
         lse = a.lse[t * a.heads + head];
         dd = a.dsum[t * a.heads + head];
       }
-      __syncthreads();  // the previous tile's reads are done
-      rows_store<T, true>(sq, sQ, tid);
-      rows_store<T, false>(so, sO, tid);
-      if (tid < KTILE) {
-        sInfo[tid] = info;
-        sL[tid] = lse;
-        sD[tid] = dd;
-      }
+      sInfo[tid] = info;
+      sL[tid] = lse;
+      sD[tid] = dd;
     }
     __syncthreads();
     build_transposed<T>(sQ, sQT, tid);
@@ -1081,27 +1086,24 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(AttnBwdArgs a) {
     __syncthreads();
     if ((hcls[0] | hcls[1]) == 0) continue;
 
-    f32x16 sc[2], dp[2];
+    // One 32-query half at a time (fewer live accumulators): S = Q.K^T and
+    // dP = dO.V^T, then P and dS in place, then that half's k steps of
+    // dV^T += dO^T . P and dK^T += Q^T . dS. Element e of the half's
+    // accumulators is query 32i + 8(e/4) + 4lh + e%4.
 #pragma unroll
-    for (int i = 0; i < 2; i++)
+    for (int i = 0; i < 2; i++) {
+      if (hcls[i] == 0) continue;
+      f32x16 sc, dp;
 #pragma unroll
       for (int e = 0; e < 16; e++) {
-        sc[i][e] = 0.0f;
-        dp[i][e] = 0.0f;
+        sc[e] = 0.0f;
+        dp[e] = 0.0f;
       }
-#pragma unroll
-    for (int i = 0; i < 2; i++) {
-      if (hcls[i] == 0) continue;
 #pragma unroll
       for (int ks = 0; ks < NKS; ks++) {
-        sc[i] = MF::mma(row_frag<T>(sQ, i * 32 + lr, ks, lh), kf[ks], sc[i]);
-        dp[i] = MF::mma(row_frag<T>(sO, i * 32 + lr, ks, lh), vf[ks], dp[i]);
+        sc = MF::mma(row_frag<T>(sQ, i * 32 + lr, ks, lh), kf[ks], sc);
+        dp = MF::mma(row_frag<T>(sO, i * 32 + lr, ks, lh), vf[ks], dp);
       }
-    }
-    // P (in sc) and dS (in dp); element e is query 32i + 8(e/4) + 4lh + e%4.
-#pragma unroll
-    for (int i = 0; i < 2; i++) {
-      if (hcls[i] == 0) continue;
 #pragma unroll
       for (int g = 0; g < 4; g++) {
         const int ql = i * 32 + 8 * g + 4 * lh;
@@ -1115,21 +1117,30 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(AttnBwdArgs a) {
           const bool ok = kvalid & (q0 + ql + u < n) & ((kopt == -1) | (kopt == qo)) &
                           ((unsigned)(kpos - qp + a.half_window) <= win2);
           const int e = 4 * g + u;
-          const float p = ok ? __builtin_amdgcn_exp2f(fmaf(sc[i][e], c, -lq[u])) : 0.0f;
-          sc[i][e] = p;
-          dp[i][e] = p * (dp[i][e] - dq4[u]) * a.scale;
+          const float p = ok ? __builtin_amdgcn_exp2f(fmaf(sc[e], c, -lq[u])) : 0.0f;
+          sc[e] = p;
+          dp[e] = p * (dp[e] - dq4[u]) * a.scale;
         }
       }
-    }
-    // dV^T += dO^T . P, dK^T += Q^T . dS
 #pragma unroll
-    for (int ks = 0; ks < NPV; ks++) {
-      if (hcls[ks / (NPV / 2)] == 0) continue;
-      const frag pf = acc_frag<T>(sc, ks), df = acc_frag<T>(dp, ks);
+      for (int kl = 0; kl < NPV / 2; kl++) {
+        const int ks = i * (NPV / 2) + kl;
+        frag pf, df;
+        if constexpr (sizeof(T) == 2) {
 #pragma unroll
-      for (int b = 0; b < 2; b++) {
-        dv[b] = MF::mma(t_frag<T>(sOT, b * 32 + lr, ks, lh), pf, dv[b]);
-        dk[b] = MF::mma(t_frag<T>(sQT, b * 32 + lr, ks, lh), df, dk[b]);
+          for (int u = 0; u < 8; u++) {
+            pf[u] = (bf16)sc[kl * 8 + u];
+            df[u] = (bf16)dp[kl * 8 + u];
+          }
+        } else {
+          pf = sc[kl];
+          df = dp[kl];
+        }
+#pragma unroll
+        for (int b = 0; b < 2; b++) {
+          dv[b] = MF::mma(t_frag<T>(sOT, b * 32 + lr, ks, lh), pf, dv[b]);
+          dk[b] = MF::mma(t_frag<T>(sQT, b * 32 + lr, ks, lh), df, dk[b]);
+        }
       }
     }
   }
