@@ -71,13 +71,15 @@ void release_slot(TensorSlot &t) {
 
 void release_train(TrainState &tr) {
   for (LayerSave &S : tr.layers) {
-    DevBuf *bufs[] = {&S.hs, &S.h1, &S.n1, &S.qkv, &S.ctx, &S.n2, &S.wi, &S.act, &S.lse};
+    DevBuf *bufs[] = {&S.hs, &S.h1, &S.n1, &S.qkv, &S.ctx, &S.n2, &S.wi, &S.act, &S.lse,
+                      &S.mean1, &S.rstd1, &S.mean2, &S.rstd2};
     for (DevBuf *b : bufs) release(*b);
   }
   tr.layers.clear();
   DevBuf *bufs[] = {&tr.dcur, &tr.dprev, &tr.dh1, &tr.dact, &tr.dwi, &tr.dn2, &tr.dctx, &tr.dqkv, &tr.dn1,
                     &tr.dyop, &tr.dsum, &tr.part, &tr.lnpart, &tr.dE, &tr.dl, &tr.contrib, &tr.emb_order,
-                    &tr.emb_seg, &tr.emb_id, &tr.sq_part, &tr.sq_out, &tr.opT[0], &tr.opT[1]};
+                    &tr.emb_seg, &tr.emb_id, &tr.sq_part, &tr.sq_out, &tr.opT[0], &tr.opT[1],
+                    &tr.emb_mean, &tr.emb_rstd};
   if (tr.side) (void)hipStreamSynchronize(tr.side);
   for (DevBuf *b : bufs) release(*b);
   for (int i = 0; i < 2; i++) {
@@ -252,7 +254,10 @@ int forward_core(dn_ctx *c, int nseq, const int32_t *seq_len, const int32_t *d_i
       HIPCHK(c, "hipMalloc", ensure(S.wi, es * T * 2 * I));
       HIPCHK(c, "hipMalloc", ensure(S.act, es * T * I));
       HIPCHK(c, "hipMalloc", ensure(S.lse, sizeof(float) * T * g.heads));
+      for (DevBuf *b : {&S.mean1, &S.rstd1, &S.mean2, &S.rstd2}) HIPCHK(c, "hipMalloc", ensure(*b, sizeof(float) * T));
     }
+    HIPCHK(c, "hipMalloc", ensure(tr.emb_mean, sizeof(float) * T));
+    HIPCHK(c, "hipMalloc", ensure(tr.emb_rstd, sizeof(float) * T));
   }
   HIPCHK(c, "hipMalloc", ensure(c->h, sizeof(float) * T * H));
   HIPCHK(c, "hipMalloc", ensure(c->xn, es * T * H));
@@ -289,10 +294,18 @@ int forward_core(dn_ctx *c, int nseq, const int32_t *seq_len, const int32_t *d_i
                                               (const int *)c->d_seq_len.p, (const int *)c->d_chunk_off.p,
                                               c->lay_nwork, sl, g.half_window, codes + sl * nw * ATTN_MAXKT,
                                               first + sl * nw, s));
+  // Training keeps each saved layer's input in its own buffer (LayerSave::hs)
+  // and its post-attention residual in LayerSave::h1: the residual GEMMs read
+  // one and write the next, so the residual stream moves through the saved
+  // buffers without copies; unsaved layers update c->h in place.
+  auto saved = [&](int l) -> LayerSave * { return train && l >= tr.train_from && l < L ? &tr.layers[l] : nullptr; };
+  float *cur = saved(0) ? (float *)saved(0)->hs.p : h;  // the residual stream entering layer 0
+  void *xn0 = saved(0) ? saved(0)->n1.p : c->xn.p;      // layer 0's QKV input (no attn_norm)
   HIPCHK(c, "embed_ln",
          launch_embed_ln(prec, d_ids, T, (const float *)W(c, "model.embeddings.tok_embeddings.weight"), g.vocab,
-                         (const float *)W(c, "model.embeddings.norm.weight"), g.eps, H, h, c->xn.p,
-                         (int *)c->err_flag.p, s));
+                         (const float *)W(c, "model.embeddings.norm.weight"), g.eps, H, cur, xn0,
+                         (int *)c->err_flag.p, s, train ? (float *)tr.emb_mean.p : nullptr,
+                         train ? (float *)tr.emb_rstd.p : nullptr));
 
   AttnArgs at{};
   at.kinfo = kinfo;
@@ -312,16 +325,16 @@ int forward_core(dn_ctx *c, int nseq, const int32_t *seq_len, const int32_t *d_i
     hipEvent_t *ev = probe_slot(c, l);
     probed |= ev != nullptr;
     // Training keeps this layer's activations (layers >= train_from).
-    LayerSave *S = train && l >= tr.train_from ? &tr.layers[l] : nullptr;
-    if (S) HIPCHK(c, "hipMemcpyAsync", hipMemcpyAsync(S->hs.p, h, sizeof(float) * T * H, hipMemcpyDeviceToDevice, s));
-    void *x1 = c->xn.p;  // QKV input: attn_norm(h), or for layer 0 the embedding output
+    LayerSave *S = saved(l);
+    float *in = cur;                                // this layer's input (S->hs when saved)
+    float *h1 = S ? (float *)S->h1.p : in;          // residual after attention
+    float *out = saved(l + 1) ? (float *)saved(l + 1)->hs.p : h;  // the layer's output
+    void *x1 = xn0;  // QKV input: attn_norm(in), or for layer 0 the embedding output
     if (l > 0) {
-      if (S) x1 = S->n1.p;
+      x1 = S ? S->n1.p : c->xn.p;
       HIPCHK(c, "ln(attn_norm)",
-             launch_ln(prec, h, T, H, (const float *)W(c, p + "attn_norm.weight"), g.eps, x1, s));
-    } else if (S) {
-      HIPCHK(c, "hipMemcpyAsync", hipMemcpyAsync(S->n1.p, c->xn.p, es * T * H, hipMemcpyDeviceToDevice, s));
-      x1 = S->n1.p;
+             launch_ln(prec, in, T, H, (const float *)W(c, p + "attn_norm.weight"), g.eps, x1, s,
+                       S ? (float *)S->mean1.p : nullptr, S ? (float *)S->rstd1.p : nullptr));
     }
     GemmArgs q{};
     q.A = x1;
@@ -351,7 +364,8 @@ int forward_core(dn_ctx *c, int nseq, const int32_t *seq_len, const int32_t *d_i
     o.lda = H;
     o.B = W(c, p + "attn.Wo.weight");
     o.ldb = H;
-    o.C = h;
+    o.C = h1;
+    o.res = h1 == in ? nullptr : in;
     o.ldc = H;
     o.M = T;
     o.N = H;
@@ -359,10 +373,10 @@ int forward_core(dn_ctx *c, int nseq, const int32_t *seq_len, const int32_t *d_i
     o.n_store = H;
     o.accumulate = 1;
     PROBED(ev, DN_PROBE_WO, "gemm(Wo)", launch_gemm(prec, EPI_F32, o, s));
-    if (S) HIPCHK(c, "hipMemcpyAsync", hipMemcpyAsync(S->h1.p, h, sizeof(float) * T * H, hipMemcpyDeviceToDevice, s));
 
     void *x2 = S ? S->n2.p : c->xn.p;
-    HIPCHK(c, "ln(mlp_norm)", launch_ln(prec, h, T, H, (const float *)W(c, p + "mlp_norm.weight"), g.eps, x2, s));
+    HIPCHK(c, "ln(mlp_norm)", launch_ln(prec, h1, T, H, (const float *)W(c, p + "mlp_norm.weight"), g.eps, x2, s,
+                                        S ? (float *)S->mean2.p : nullptr, S ? (float *)S->rstd2.p : nullptr));
 
     GemmArgs wi{};
     wi.A = x2;
@@ -373,11 +387,12 @@ int forward_core(dn_ctx *c, int nseq, const int32_t *seq_len, const int32_t *d_i
     wi.N = 2 * I;
     wi.K = H;
     wi.n_store = 2 * I;
-    if (S) {  // training keeps the pre-activation: plain store, then GeGLU
+    if (S) {  // training keeps the pre-activation as well as the GeGLU output
       wi.C = S->wi.p;
       wi.ldc = 2 * I;
-      PROBED(ev, DN_PROBE_WI, "gemm(Wi)", launch_gemm(prec, EPI_STORE, wi, s));
-      HIPCHK(c, "geglu", launch_geglu_fwd(prec, S->wi.p, S->act.p, T, I, s));
+      wi.C2 = S->act.p;
+      wi.ldc2 = I;
+      PROBED(ev, DN_PROBE_WI, "gemm(Wi)", launch_gemm(prec, EPI_GEGLU_KEEP, wi, s));
     } else {
       wi.C = c->act.p;
       wi.ldc = I;
@@ -389,7 +404,8 @@ int forward_core(dn_ctx *c, int nseq, const int32_t *seq_len, const int32_t *d_i
     mo.lda = I;
     mo.B = W(c, p + "mlp.Wo.weight");
     mo.ldb = I;
-    mo.C = h;
+    mo.C = out;
+    mo.res = out == h1 ? nullptr : h1;
     mo.ldc = H;
     mo.M = T;
     mo.N = H;
@@ -397,6 +413,7 @@ int forward_core(dn_ctx *c, int nseq, const int32_t *seq_len, const int32_t *d_i
     mo.n_store = H;
     mo.accumulate = 1;
     PROBED(ev, DN_PROBE_MLPWO, "gemm(MlpWo)", launch_gemm(prec, EPI_F32, mo, s));
+    cur = out;
   }
   if (probed) c->probe_used++;
 

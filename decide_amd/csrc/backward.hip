@@ -149,84 +149,112 @@ __global__ void geglu_fwd_kernel(const T *wi, T *act, int rows, int I) {
   act[idx] = (T)(gelu_erf<T>(ld_elem(row + r)) * ld_elem(row + 32 + r));
 }
 
-// GeGLU backward (backward.go:49-61) in the interleaved layout.
+// GeGLU backward (backward.go:49-61) in the interleaved layout: each thread
+// takes 8 consecutive act columns (16-byte bf16 / 32-byte fp32 accesses).
 template <class T>
 __global__ void geglu_bwd_kernel(const float *dact, const T *wi, T *dwi, int rows, int I) {
-  const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const size_t idx = ((size_t)blockIdx.x * blockDim.x + threadIdx.x) * 8;
   if (idx >= (size_t)rows * I) return;
   const size_t t = idx / I;
-  const int i = (int)(idx % I), g = i >> 5, r = i & 31;
+  const int i = (int)(idx % I), g = i >> 5, r = i & 31;  // r is a multiple of 8
   const T *row = wi + t * 2 * I + 64 * g;
   T *out = dwi + t * 2 * I + 64 * g;
-  const float a = ld_elem(row + r), gt = ld_elem(row + 32 + r), da = dact[idx];
-  out[r] = (T)(da * gt * gelu_grad<T>(a));
-  out[32 + r] = (T)(da * gelu_erf<T>(a));
+  float a[8], gt[8], da[8], dv[8], dg[8];
+  Vec8<T>::load(row + r, a);
+  Vec8<T>::load(row + 32 + r, gt);
+  Vec8<float>::load(dact + idx, da);
+#pragma unroll
+  for (int u = 0; u < 8; u++) {
+    dv[u] = da[u] * gt[u] * gelu_grad<T>(a[u]);
+    dg[u] = da[u] * gelu_erf<T>(a[u]);
+  }
+  Vec8<T>::store(out + r, dv);
+  Vec8<T>::store(out + 32 + r, dg);
 }
 
 // ---------------------------------------------------------------------------
 // LayerNorm backward (layerNormBwd, ops.go:94-135) for bias-free norms over
-// rows of dim <= 1024 (dim % 256 == 0): one wave per row; dx[r] += ..., and
-// this block's partial of dw (sum over its rows of dy*xh) into part[block].
-// The row statistics are recomputed from x as the forward computes them (f64).
-// x rows are x[r] or, with ids, the embedding row tok[ids[r]].
-constexpr int LNB_WAVES = 4;
+// rows of dim = 64*NE: one wave per row, RPW rows per wave with their loads
+// issued together; dx = res + ... (res given) or dx += ...; this block's
+// partial of dw (sum over its rows of dy*xh) goes to part[block]. mean and
+// rstd are the forward's statistics (when null they are recomputed from x
+// as the forward computes them, f64). x rows are x[r] or, with ids, the
+// embedding row tok[ids[r]].
+constexpr int LNB_WAVES = 4, LNB_RPW = 4;
+template <int NE>
 __global__ __launch_bounds__(256) void ln_bwd_kernel(float *dx, const float *res, const float *dy, const float *x,
-                                                     const int *ids, const float *w, float eps, int rows, int dim,
-                                                     float *part) {
-  constexpr int MAXE = 16;  // dim <= 1024: 16 elements per lane
-  __shared__ float sw[LNB_WAVES][1024];
+                                                     const int *ids, const float *mean, const float *rstd,
+                                                     const float *w, float eps, int rows, float *part) {
+  constexpr int dim = 64 * NE;
+  __shared__ float sw[LNB_WAVES][dim];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int ne = dim / 64;
-  float pw[MAXE];
+  float wv[NE], pw[NE];
 #pragma unroll
-  for (int j = 0; j < MAXE; j++) pw[j] = 0.0f;
-  for (int r = blockIdx.x * LNB_WAVES + wave; r < rows; r += gridDim.x * LNB_WAVES) {
-    const float *xr = ids ? x + (size_t)ids[r] * dim : x + (size_t)r * dim;
-    const float *g = dy + (size_t)r * dim;
-    float xv[MAXE], gv[MAXE];
-    double s = 0;
+  for (int j = 0; j < NE; j++) {
+    wv[j] = w[lane + 64 * j];
+    pw[j] = 0.0f;
+  }
+  constexpr int RB = LNB_WAVES * LNB_RPW;  // rows per block and pass
+  for (int r0 = blockIdx.x * RB + wave * LNB_RPW; r0 < rows; r0 += gridDim.x * RB) {
+    float xv[LNB_RPW][NE], gv[LNB_RPW][NE], m[LNB_RPW], rs[LNB_RPW];
 #pragma unroll
-    for (int j = 0; j < MAXE; j++)
-      if (j < ne) {
-        xv[j] = xr[lane + 64 * j];
-        gv[j] = g[lane + 64 * j];
-        s += (double)xv[j];
+    for (int q = 0; q < LNB_RPW; q++) {
+      const int r = min(r0 + q, rows - 1);
+      const float *xr = ids ? x + (size_t)ids[r] * dim : x + (size_t)r * dim;
+#pragma unroll
+      for (int j = 0; j < NE; j++) {
+        xv[q][j] = xr[lane + 64 * j];
+        gv[q][j] = dy[(size_t)r * dim + lane + 64 * j];
       }
-    const double mu = wave_sum_d(s) / (double)dim;
-    double v = 0;
-#pragma unroll
-    for (int j = 0; j < MAXE; j++)
-      if (j < ne) {
-        const double d = (double)xv[j] - mu;
-        v += d * d;
+      if (mean) {
+        m[q] = mean[r];
+        rs[q] = rstd[r];
       }
-    const float rs = (float)(1.0 / sqrt(wave_sum_d(v) / (double)dim + (double)eps));
-    const float m = (float)mu;
-    double s1 = 0, s2 = 0;
+    }
+    if (!mean) {
 #pragma unroll
-    for (int j = 0; j < MAXE; j++)
-      if (j < ne) {
+      for (int q = 0; q < LNB_RPW; q++) {
+        double s = 0;
+#pragma unroll
+        for (int j = 0; j < NE; j++) s += (double)xv[q][j];
+        const double mu = wave_sum_d(s) / (double)dim;
+        double v = 0;
+#pragma unroll
+        for (int j = 0; j < NE; j++) {
+          const double d = (double)xv[q][j] - mu;
+          v += d * d;
+        }
+        rs[q] = (float)(1.0 / sqrt(wave_sum_d(v) / (double)dim + (double)eps));
+        m[q] = (float)mu;
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < LNB_RPW; q++) {
+      const int r = r0 + q;
+      double s1 = 0, s2 = 0;
+#pragma unroll
+      for (int j = 0; j < NE; j++) {
 #pragma clang fp contract(off)
-        const float xh = (xv[j] - m) * rs;
-        const float gw = gv[j] * w[lane + 64 * j];
+        const float xh = (xv[q][j] - m[q]) * rs[q];
+        const float gw = gv[q][j] * wv[j];
         s1 += (double)gw;
         s2 += (double)(gw * xh);
-        pw[j] += gv[j] * xh;
-        xv[j] = xh;
+        if (r < rows) pw[j] += gv[q][j] * xh;
+        xv[q][j] = xh;
       }
-    const float a = (float)(wave_sum_d(s1) / (double)dim), b = (float)(wave_sum_d(s2) / (double)dim);
-    float *o = dx + (size_t)r * dim;
-    const float *base = res ? res + (size_t)r * dim : o;  // dx = res + ... (res given) or dx += ...
+      const float a = (float)(wave_sum_d(s1) / (double)dim), b = (float)(wave_sum_d(s2) / (double)dim);
+      if (r >= rows) continue;
+      float *o = dx + (size_t)r * dim;
+      const float *base = res ? res + (size_t)r * dim : o;  // dx = res + ... (res given) or dx += ...
 #pragma unroll
-    for (int j = 0; j < MAXE; j++)
-      if (j < ne) {
+      for (int j = 0; j < NE; j++) {
 #pragma clang fp contract(off)
-        o[lane + 64 * j] = base[lane + 64 * j] + rs * (gv[j] * w[lane + 64 * j] - a - xv[j] * b);
+        o[lane + 64 * j] = base[lane + 64 * j] + rs[q] * (gv[q][j] * wv[j] - a - xv[q][j] * b);
       }
+    }
   }
 #pragma unroll
-  for (int j = 0; j < MAXE; j++)
-    if (j < ne) sw[wave][lane + 64 * j] = pw[j];
+  for (int j = 0; j < NE; j++) sw[wave][lane + 64 * j] = pw[j];
   __syncthreads();
   for (int i = threadIdx.x; i < dim; i += 256) {
     float acc = 0.0f;
@@ -613,23 +641,41 @@ hipError_t launch_geglu_bwd(int precision, const float *dact, const void *wi, vo
                             hipStream_t s) {
   const size_t n = (size_t)rows * I;
   if (n == 0) return hipSuccess;
+  if (I % 32 != 0) return hipErrorInvalidValue;
   if (precision == 1)
-    hipLaunchKernelGGL(geglu_bwd_kernel<bf16>, dim3(blocks(n)), dim3(256), 0, s, dact, (const bf16 *)wi, (bf16 *)dwi,
-                       rows, I);
+    hipLaunchKernelGGL(geglu_bwd_kernel<bf16>, dim3(blocks(n / 8)), dim3(256), 0, s, dact, (const bf16 *)wi,
+                       (bf16 *)dwi, rows, I);
   else
-    hipLaunchKernelGGL(geglu_bwd_kernel<float>, dim3(blocks(n)), dim3(256), 0, s, dact, (const float *)wi,
+    hipLaunchKernelGGL(geglu_bwd_kernel<float>, dim3(blocks(n / 8)), dim3(256), 0, s, dact, (const float *)wi,
                        (float *)dwi, rows, I);
   return hipGetLastError();
 }
 
-int ln_bwd_blocks(int rows) { return std::max(1, std::min(1024, (rows + LNB_WAVES - 1) / LNB_WAVES)) + COLSUM_NG; }
+int ln_bwd_blocks(int rows) {
+  constexpr int RB = LNB_WAVES * LNB_RPW;
+  return std::max(1, std::min(1024, (rows + RB - 1) / RB)) + COLSUM_NG;
+}
 
-hipError_t launch_ln_bwd(float *dx, const float *res, const float *dy, const float *x, const int *ids, const float *w,
-                         float eps, int rows, int dim, float *part, float *dw, hipStream_t s) {
+hipError_t launch_ln_bwd(float *dx, const float *res, const float *dy, const float *x, const int *ids,
+                         const float *mean, const float *rstd, const float *w, float eps, int rows, int dim,
+                         float *part, float *dw, hipStream_t s) {
   if (rows <= 0) return hipSuccess;
-  if (dim % 64 != 0 || dim > 1024) return hipErrorInvalidValue;
   const int nb = ln_bwd_blocks(rows) - COLSUM_NG;
-  hipLaunchKernelGGL(ln_bwd_kernel, dim3(nb), dim3(256), 0, s, dx, res, dy, x, ids, w, eps, rows, dim, part);
+  switch (dim) {
+#define LNB_CASE(NE)                                                                                               \
+  case 64 * NE:                                                                                                    \
+    hipLaunchKernelGGL(ln_bwd_kernel<NE>, dim3(nb), dim3(256), 0, s, dx, res, dy, x, ids, mean, rstd, w, eps, rows, \
+                       part);                                                                                      \
+    break;
+    LNB_CASE(4)
+    LNB_CASE(6)
+    LNB_CASE(8)
+    LNB_CASE(12)
+    LNB_CASE(16)
+#undef LNB_CASE
+    default:
+      return hipErrorInvalidValue;
+  }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || !dw) return e;
   float *part2 = part + (size_t)nb * dim;

@@ -100,9 +100,14 @@ struct GemmArgs {
   int ngroups;    // N-tile groups per XCD sweep (set by launch_gemm)
   int order;      // workgroup -> tile order (0: XCD-aware groups)
   size_t c_split; // split-K: elements between the partial outputs of blockIdx.y (0: one split)
+  const float *res; // EPI_F32 with accumulate: C = res + result (res has C's layout); null: C += result
+  void *C2;         // EPI_GEGLU_KEEP: the GeGLU output (ldc2), C receives the plain product
+  int ldc2;
 };
 
-enum { EPI_F32 = 0, EPI_STORE = 1, EPI_GEGLU = 2 };
+// GEMM epilogues: fp32 store / accumulate, store in the operand type, GeGLU of
+// value/gate column pairs, and (training) both the plain product and its GeGLU.
+enum { EPI_F32 = 0, EPI_STORE = 1, EPI_GEGLU = 2, EPI_GEGLU_KEEP = 3 };
 
 hipError_t launch_gemm(int precision, int epi, const GemmArgs &a, hipStream_t s);
 // Split-K fp32-output GEMM: `splits` partial products, each over a.K / splits
@@ -171,9 +176,12 @@ hipError_t launch_chunk_summary(const int *kinfo, const int4 *chunk_desc, ChunkI
 hipError_t launch_token_info(const int *pos, const int *opt, int *kinfo, int T, int *err_flag, hipStream_t s);
 hipError_t launch_rope_tables(const int *pos, int T, const double *inv_g, const double *inv_l, float *cos_g,
                               float *sin_g, float *cos_l, float *sin_l, hipStream_t s);
+// LayerNorm launchers; mean / rstd (optional, [rows]) receive the row statistics.
 hipError_t launch_embed_ln(int precision, const int *ids, int T, const float *tok, int vocab, const float *w, float eps,
-                           int H, float *h, void *xn, int *err_flag, hipStream_t s);
-hipError_t launch_ln(int precision, const float *x, int rows, int H, const float *w, float eps, void *y, hipStream_t s);
+                           int H, float *h, void *xn, int *err_flag, hipStream_t s, float *mean = nullptr,
+                           float *rstd = nullptr);
+hipError_t launch_ln(int precision, const float *x, int rows, int H, const float *w, float eps, void *y, hipStream_t s,
+                     float *mean = nullptr, float *rstd = nullptr);
 struct HeadArgs {
   const float *h;
   const int *row_tok;
@@ -195,9 +203,11 @@ hipError_t launch_geglu_bwd(int precision, const float *dact, const void *wi, vo
                             hipStream_t s);
 // LayerNorm backward: dx = res + LNbwd(dy) when res is given, else dx += LNbwd(dy);
 // dw += the weight gradient (part holds ln_bwd_blocks(rows) x dim floats of scratch).
+// mean / rstd: the forward's row statistics (recomputed from x when null).
 int ln_bwd_blocks(int rows);
-hipError_t launch_ln_bwd(float *dx, const float *res, const float *dy, const float *x, const int *ids, const float *w,
-                         float eps, int rows, int dim, float *part, float *dw, hipStream_t s);
+hipError_t launch_ln_bwd(float *dx, const float *res, const float *dy, const float *x, const int *ids,
+                         const float *mean, const float *rstd, const float *w, float eps, int rows, int dim,
+                         float *part, float *dw, hipStream_t s);
 hipError_t launch_add(float *dst, const float *src, size_t n, hipStream_t s);
 hipError_t launch_embed_bwd(const float *dE, const int *order, const int *seg_start, const int *seg_id, int nseg,
                             int dim, float *gtok, hipStream_t s);

@@ -50,6 +50,7 @@ struct LayerSave {
   DevBuf hs, h1;                      // fp32 [T x H]: layer input, residual after attention
   DevBuf n1, qkv, ctx, n2, wi, act;   // operand type: QKV input, un-rotated qkv, ctx, Wi input, Wi output, GeGLU
   DevBuf lse;                         // fp32 [T x heads]
+  DevBuf mean1, rstd1, mean2, rstd2;  // fp32 [T]: attn_norm and mlp_norm row statistics
 };
 
 struct TrainState {
@@ -61,6 +62,7 @@ struct TrainState {
   bool have_forward = false;  // the activations of the last dn_forward_train are intact
   int T = 0, R = 0;
   std::vector<int32_t> ids;   // token ids of the last training forward
+  DevBuf emb_mean, emb_rstd;  // emb norm row statistics of the last training forward
   DevBuf dcur, dprev, dh1, dact, dwi, dn2, dctx, dqkv, dn1, dyop, dsum, part, lnpart, dE, dl, contrib;
   DevBuf emb_order, emb_seg, emb_id, sq_part, sq_out;
   // Weight-gradient GEMMs run on a second stream: per layer parity, the

@@ -27,6 +27,8 @@
 //     slice of B stays in that XCD's 4 MB L2 while its A panels stream.
 //   * The epilogue stages the finished tile through LDS so global stores are
 //     full 16-byte-per-lane rows.
+#include <type_traits>
+
 #include "common.hpp"
 
 namespace {
@@ -225,6 +227,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) __attribute__((amdgpu_waves_per_eu(
     constexpr int HM = WM;      // rows per pass: the waves with wm == pass stage theirs
     float *st = (float *)smem;
     float *C = (float *)gC;
+    const float *R = g.res ? g.res : C;  // residual input of the accumulate
     constexpr int V = BN / 4;  // float4 per row
     constexpr int ITER = HM * V / NT;
     constexpr int BATCH = ITER < 8 ? ITER : 8;
@@ -253,7 +256,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) __attribute__((amdgpu_waves_per_eu(
           const int row = m0 + pass * HM + r, col = n0 + c4;
           old[u] = make_float4(0.f, 0.f, 0.f, 0.f);
           if (g.accumulate && vec && row < g.M && col + 4 <= g.n_store)
-            old[u] = *(const float4 *)(C + (size_t)row * g.ldc + col);
+            old[u] = *(const float4 *)(R + (size_t)row * g.ldc + col);
         }
 #pragma unroll
         for (int u = 0; u < BATCH; u++) {
@@ -266,48 +269,63 @@ __global__ __launch_bounds__(64 * WGM * WGN) __attribute__((amdgpu_waves_per_eu(
             *(float4 *)p = make_float4(v.x + old[u].x, v.y + old[u].y, v.z + old[u].z, v.w + old[u].w);
           } else {
             const float vv[4] = {v.x, v.y, v.z, v.w};
-            for (int q = 0; q < 4 && col + q < g.n_store; q++) p[q] = g.accumulate ? p[q] + vv[q] : vv[q];
+            const float *pr = R + (size_t)row * g.ldc + col;
+            for (int q = 0; q < 4 && col + q < g.n_store; q++) p[q] = g.accumulate ? pr[q] + vv[q] : vv[q];
           }
         }
       }
       if (pass + 1 < WGM) __syncthreads();
     }
   } else {
-    constexpr int OC = EPI == EPI_GEGLU ? BN / 2 : BN;  // output columns of the block tile
-    constexpr int LD = OC + 8;                          // staged row length (elements)
-    typedef T T4 __attribute__((ext_vector_type(4)));
-    T *st = (T *)smem;
+    // Operand-type epilogue: the plain product (gated false) or the GeGLU of
+    // each value/gate column pair (gated true), staged in LDS and stored as
+    // 16-byte rows. EPI_GEGLU_KEEP writes both (training keeps the Wi output).
+    auto emit = [&](auto gated, T *Cout, int ldo) {
+      constexpr bool G = decltype(gated)::value;
+      constexpr int OC = G ? BN / 2 : BN;  // output columns of the block tile
+      constexpr int LD = OC + 8;           // staged row length (elements)
+      typedef T T4 __attribute__((ext_vector_type(4)));
+      T *st = (T *)smem;
 #pragma unroll
-    for (int i = 0; i < TM; i++) {
+      for (int i = 0; i < TM; i++) {
 #pragma unroll
-      for (int jp = 0; jp < TN / 2; jp++)
+        for (int jp = 0; jp < TN / 2; jp++)
 #pragma unroll
-        for (int q = 0; q < 4; q++) {
-          const int r = rw + i * 32 + lr, c = mfma_row(4 * q, lane);  // 4 consecutive columns from c
-          const f32x16 &a = acc[i][2 * jp], &b = acc[i][2 * jp + 1];
-          if constexpr (EPI == EPI_STORE) {
-            *(T4 *)(st + r * LD + cw + jp * 64 + c) =
-                T4{to_elem<T>(a[4 * q]), to_elem<T>(a[4 * q + 1]), to_elem<T>(a[4 * q + 2]), to_elem<T>(a[4 * q + 3])};
-            *(T4 *)(st + r * LD + cw + jp * 64 + 32 + c) =
-                T4{to_elem<T>(b[4 * q]), to_elem<T>(b[4 * q + 1]), to_elem<T>(b[4 * q + 2]), to_elem<T>(b[4 * q + 3])};
-          } else {
-            T4 o;
+          for (int q = 0; q < 4; q++) {
+            const int r = rw + i * 32 + lr, c = mfma_row(4 * q, lane);  // 4 consecutive columns from c
+            const f32x16 &a = acc[i][2 * jp], &b = acc[i][2 * jp + 1];
+            if constexpr (!G) {
+              *(T4 *)(st + r * LD + cw + jp * 64 + c) =
+                  T4{to_elem<T>(a[4 * q]), to_elem<T>(a[4 * q + 1]), to_elem<T>(a[4 * q + 2]), to_elem<T>(a[4 * q + 3])};
+              *(T4 *)(st + r * LD + cw + jp * 64 + 32 + c) =
+                  T4{to_elem<T>(b[4 * q]), to_elem<T>(b[4 * q + 1]), to_elem<T>(b[4 * q + 2]), to_elem<T>(b[4 * q + 3])};
+            } else {
+              T4 o;
 #pragma unroll
-            for (int t = 0; t < 4; t++) o[t] = to_elem<T>(gelu_erf<T>(a[4 * q + t]) * b[4 * q + t]);
-            *(T4 *)(st + r * LD + (cw + jp * 64) / 2 + c) = o;
+              for (int t = 0; t < 4; t++) o[t] = to_elem<T>(gelu_erf<T>(a[4 * q + t]) * b[4 * q + t]);
+              *(T4 *)(st + r * LD + (cw + jp * 64) / 2 + c) = o;
+            }
           }
-        }
-    }
-    __syncthreads();
-    T *C = (T *)gC;
-    const int oc0 = EPI == EPI_GEGLU ? n0 / 2 : n0;
-    constexpr int EPV = 16 / sizeof(T);  // elements per 16-byte vector
-    constexpr int V = OC / EPV;
-    for (int c = tid; c < BM * V; c += NT) {
-      const int r = c / V, cc = (c % V) * EPV;
-      const int row = m0 + r;
-      if (row >= g.M) continue;
-      *(uint4 *)(C + (size_t)row * g.ldc + oc0 + cc) = *(const uint4 *)(st + r * LD + cc);
+      }
+      __syncthreads();
+      const int oc0 = G ? n0 / 2 : n0;
+      constexpr int EPV = 16 / sizeof(T);  // elements per 16-byte vector
+      constexpr int V = OC / EPV;
+      for (int c = tid; c < BM * V; c += NT) {
+        const int r = c / V, cc = (c % V) * EPV;
+        const int row = m0 + r;
+        if (row >= g.M) continue;
+        *(uint4 *)(Cout + (size_t)row * ldo + oc0 + cc) = *(const uint4 *)(st + r * LD + cc);
+      }
+    };
+    if constexpr (EPI == EPI_STORE) {
+      emit(std::false_type{}, (T *)gC, g.ldc);
+    } else if constexpr (EPI == EPI_GEGLU) {
+      emit(std::true_type{}, (T *)gC, g.ldc);
+    } else {
+      emit(std::false_type{}, (T *)gC, g.ldc);
+      __syncthreads();  // the staging area is reused
+      emit(std::true_type{}, (T *)g.C2, g.ldc2);
     }
   }
 }
@@ -323,8 +341,11 @@ hipError_t launch_cfg(int epi, const GemmArgs &a, hipStream_t s, int splits = 1)
     case EPI_STORE:
       hipLaunchKernelGGL((gemm_nt_kernel<T, BM, BN, RB, NSTAGE, EPI_STORE, WPE, WGM, WGN>), grid, block, 0, s, a);
       break;
-    default:
+    case EPI_GEGLU:
       hipLaunchKernelGGL((gemm_nt_kernel<T, BM, BN, RB, NSTAGE, EPI_GEGLU, WPE, WGM, WGN>), grid, block, 0, s, a);
+      break;
+    default:
+      hipLaunchKernelGGL((gemm_nt_kernel<T, BM, BN, RB, NSTAGE, EPI_GEGLU_KEEP, WPE, WGM, WGN>), grid, block, 0, s, a);
       break;
   }
   return hipGetLastError();
@@ -357,7 +378,7 @@ __global__ __launch_bounds__(64 * W) void gemm_skinny_kernel(GemmArgs g) {
   constexpr int VPL = 16 / (int)sizeof(T);  // elements per 16-byte load
   constexpr int GK = 8 * VPL;               // k elements per group
   constexpr int TR = 32 * MB, TC = 32 * NB, TE = TR * TC;
-  static_assert(EPI != EPI_GEGLU || NB == 2, "GeGLU tiles pair 32 value and 32 gate columns");
+  static_assert((EPI != EPI_GEGLU && EPI != EPI_GEGLU_KEEP) || NB == 2, "GeGLU tiles pair 32 value and 32 gate columns");
   static_assert(W == 4 || W == 8, "wave count");
   __shared__ __attribute__((aligned(16))) float red[4 * TE];
 
@@ -488,39 +509,50 @@ __global__ __launch_bounds__(64 * W) void gemm_skinny_kernel(GemmArgs g) {
       if (m0 + r >= g.M || col >= g.n_store) continue;
       const float4 v = red4[q];
       float *p = C + (size_t)(m0 + r) * g.ldc + col;
+      const float *pr = (g.res ? g.res : C) + (size_t)(m0 + r) * g.ldc + col;  // residual input
       if (vec && col + 4 <= g.n_store) {
-        float4 o = g.accumulate ? *(const float4 *)p : make_float4(0.f, 0.f, 0.f, 0.f);
+        float4 o = g.accumulate ? *(const float4 *)pr : make_float4(0.f, 0.f, 0.f, 0.f);
         *(float4 *)p = make_float4(o.x + v.x, o.y + v.y, o.z + v.z, o.w + v.w);
       } else {
         const float vv[4] = {v.x, v.y, v.z, v.w};
-        for (int u = 0; u < 4 && col + u < g.n_store; u++) p[u] = g.accumulate ? p[u] + vv[u] : vv[u];
+        for (int u = 0; u < 4 && col + u < g.n_store; u++) p[u] = g.accumulate ? pr[u] + vv[u] : vv[u];
       }
     }
   } else {
-    constexpr int EPV = 16 / (int)sizeof(T);            // elements per 16-byte store
-    constexpr int OC = EPI == EPI_GEGLU ? TC / 2 : TC;  // output columns of the tile
-    T *C = (T *)g.C;
-    const int oc0 = EPI == EPI_GEGLU ? n0 / 2 : n0;
-    for (int q = tid; q < TR * (OC / EPV); q += NT) {
-      const int r = q / (OC / EPV), c = (q % (OC / EPV)) * EPV;
-      if (m0 + r >= g.M) continue;
-      unsigned w[4];
+    auto emit = [&](auto gated, T *C, int ldo) {
+      constexpr bool G = decltype(gated)::value;
+      constexpr int EPV = 16 / (int)sizeof(T);  // elements per 16-byte store
+      constexpr int OC = G ? TC / 2 : TC;       // output columns of the tile
+      const int oc0 = G ? n0 / 2 : n0;
+      for (int q = tid; q < TR * (OC / EPV); q += NT) {
+        const int r = q / (OC / EPV), c = (q % (OC / EPV)) * EPV;
+        if (m0 + r >= g.M) continue;
+        unsigned w[4];
 #pragma unroll
-      for (int u = 0; u < EPV; u++) {
-        float v;
-        if constexpr (EPI == EPI_STORE) {
-          v = red[r * TC + c + u];
-        } else {
-          v = gelu_erf<T>(red[r * TC + c + u]) * red[r * TC + 32 + c + u];
+        for (int u = 0; u < EPV; u++) {
+          float v;
+          if constexpr (!G) {
+            v = red[r * TC + c + u];
+          } else {
+            v = gelu_erf<T>(red[r * TC + c + u]) * red[r * TC + 32 + c + u];
+          }
+          if constexpr (sizeof(T) == 2) {
+            const unsigned b = __builtin_bit_cast(unsigned short, (bf16)v);
+            w[u / 2] = (u & 1) ? (w[u / 2] | (b << 16)) : b;
+          } else {
+            w[u] = __float_as_uint(v);
+          }
         }
-        if constexpr (sizeof(T) == 2) {
-          const unsigned b = __builtin_bit_cast(unsigned short, (bf16)v);
-          w[u / 2] = (u & 1) ? (w[u / 2] | (b << 16)) : b;
-        } else {
-          w[u] = __float_as_uint(v);
-        }
+        *(uint4 *)(C + (size_t)(m0 + r) * ldo + oc0 + c) = make_uint4(w[0], w[1], w[2], w[3]);
       }
-      *(uint4 *)(C + (size_t)(m0 + r) * g.ldc + oc0 + c) = make_uint4(w[0], w[1], w[2], w[3]);
+    };
+    if constexpr (EPI == EPI_STORE) {
+      emit(std::false_type{}, (T *)g.C, g.ldc);
+    } else if constexpr (EPI == EPI_GEGLU) {
+      emit(std::true_type{}, (T *)g.C, g.ldc);
+    } else {
+      emit(std::false_type{}, (T *)g.C, g.ldc);
+      emit(std::true_type{}, (T *)g.C2, g.ldc2);
     }
   }
 }
@@ -535,8 +567,12 @@ hipError_t launch_skinny_cfg(int epi, const GemmArgs &a, hipStream_t s) {
     case EPI_STORE:
       hipLaunchKernelGGL((gemm_skinny_kernel<T, MB, NB, EPI_STORE, W>), grid, block, 0, s, a);
       break;
-    default:
+    case EPI_GEGLU:
       if constexpr (NB == 2) hipLaunchKernelGGL((gemm_skinny_kernel<T, MB, 2, EPI_GEGLU, W>), grid, block, 0, s, a);
+      else return hipErrorInvalidValue;
+      break;
+    default:
+      if constexpr (NB == 2) hipLaunchKernelGGL((gemm_skinny_kernel<T, MB, 2, EPI_GEGLU_KEEP, W>), grid, block, 0, s, a);
       else return hipErrorInvalidValue;
       break;
   }
@@ -548,7 +584,7 @@ hipError_t launch_skinny_cfg(int epi, const GemmArgs &a, hipStream_t s) {
 // above; 32 columns (64 for GeGLU's value/gate pairs), 8 waves.
 template <class T>
 hipError_t launch_skinny(int epi, const GemmArgs &a, hipStream_t s) {
-  if (epi == EPI_GEGLU) {
+  if (epi == EPI_GEGLU || epi == EPI_GEGLU_KEEP) {
     if (a.M <= 128) return launch_skinny_cfg<T, 1, 2, 8>(epi, a, s);
     return launch_skinny_cfg<T, 2, 2, 8>(epi, a, s);
   }

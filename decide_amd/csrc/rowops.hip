@@ -62,7 +62,7 @@ __device__ __forceinline__ void store4<bf16>(bf16 *p, float4 v) {
 template <class T>
 __global__ __launch_bounds__(256) void embed_ln_kernel(const int *ids, int Tn, const float *tok, int vocab,
                                                        const float *w, float eps, int dim, float *h, T *xn,
-                                                       int *err) {
+                                                       int *err, float *mean_out, float *rstd_out) {
   const int lane = threadIdx.x & 63;
   const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= Tn) return;
@@ -79,6 +79,10 @@ __global__ __launch_bounds__(256) void embed_ln_kernel(const int *ids, int Tn, c
     if (lane + 64 * j < nvec) x[j] = src[lane + 64 * j];
   float mean, rs;
   row_stats(x, nvec, lane, dim, eps, mean, rs);
+  if (mean_out && lane == 0) {  // training keeps the statistics (forward.go:220, layerNormFwd's mean/rstd)
+    mean_out[t] = mean;
+    rstd_out[t] = rs;
+  }
   const float4 *w4 = (const float4 *)w;
 #pragma unroll
   for (int j = 0; j < MAXV; j++)
@@ -99,7 +103,7 @@ __global__ __launch_bounds__(256) void embed_ln_kernel(const int *ids, int Tn, c
 // RPW rows per wave (their loads and reductions interleave).
 template <class T, int RPW>
 __global__ __launch_bounds__(256) void ln_kernel(const float *xin, int rows, int dim, const float *w, float eps,
-                                                 T *y) {
+                                                 T *y, float *mean_out, float *rstd_out) {
   const int lane = threadIdx.x & 63;
   const int r0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * RPW;
   const int nvec = dim / 4;
@@ -118,6 +122,10 @@ __global__ __launch_bounds__(256) void ln_kernel(const float *xin, int rows, int
     float mean, rs;
     row_stats(x[rr], nvec, lane, dim, eps, mean, rs);
     if (r >= rows) continue;
+    if (mean_out && lane == 0) {
+      mean_out[r] = mean;
+      rstd_out[r] = rs;
+    }
 #pragma unroll
     for (int j = 0; j < MAXV; j++)
       if (lane + 64 * j < nvec) {
@@ -252,26 +260,28 @@ __global__ void pack_kernel(const float *src, int trans, int rows, int cols, int
 }  // namespace
 
 hipError_t launch_embed_ln(int precision, const int *ids, int Tn, const float *tok, int vocab, const float *w,
-                           float eps, int H, float *h, void *xn, int *err, hipStream_t s) {
+                           float eps, int H, float *h, void *xn, int *err, hipStream_t s, float *mean,
+                           float *rstd) {
   if (Tn <= 0) return hipSuccess;
   dim3 grid((Tn + 3) / 4), block(256);
   if (precision == 1)
-    hipLaunchKernelGGL(embed_ln_kernel<bf16>, grid, block, 0, s, ids, Tn, tok, vocab, w, eps, H, h, (bf16 *)xn, err);
+    hipLaunchKernelGGL(embed_ln_kernel<bf16>, grid, block, 0, s, ids, Tn, tok, vocab, w, eps, H, h, (bf16 *)xn, err,
+                       mean, rstd);
   else
     hipLaunchKernelGGL(embed_ln_kernel<float>, grid, block, 0, s, ids, Tn, tok, vocab, w, eps, H, h, (float *)xn,
-                       err);
+                       err, mean, rstd);
   return hipGetLastError();
 }
 
 hipError_t launch_ln(int precision, const float *x, int rows, int H, const float *w, float eps, void *y,
-                     hipStream_t s) {
+                     hipStream_t s, float *mean, float *rstd) {
   if (rows <= 0) return hipSuccess;
   constexpr int RPW = 1;
   dim3 grid((rows + 4 * RPW - 1) / (4 * RPW)), block(256);
   if (precision == 1)
-    hipLaunchKernelGGL((ln_kernel<bf16, RPW>), grid, block, 0, s, x, rows, H, w, eps, (bf16 *)y);
+    hipLaunchKernelGGL((ln_kernel<bf16, RPW>), grid, block, 0, s, x, rows, H, w, eps, (bf16 *)y, mean, rstd);
   else
-    hipLaunchKernelGGL((ln_kernel<float, RPW>), grid, block, 0, s, x, rows, H, w, eps, (float *)y);
+    hipLaunchKernelGGL((ln_kernel<float, RPW>), grid, block, 0, s, x, rows, H, w, eps, (float *)y, mean, rstd);
   return hipGetLastError();
 }
 

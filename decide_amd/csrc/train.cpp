@@ -143,8 +143,8 @@ struct Bwd {
   }
   // dst [cols x Tp] = src[T x cols]^T in the operand type (zero past T); with
   // copy, also the operand-type copy of an fp32 src.
-  int transpose(int prec_in, const void *src, int cols, void *dst, void *copy = nullptr) {
-    HIPCHK(c, "transpose", launch_transpose(prec_in, prec, src, T, cols, cols, dst, Tp, Tp, copy, s));
+  int transpose(int prec_in, const void *src, int cols, void *dst, void *copy = nullptr, hipStream_t ts = nullptr) {
+    HIPCHK(c, "transpose", launch_transpose(prec_in, prec, src, T, cols, cols, dst, Tp, Tp, copy, ts ? ts : s));
     return DN_OK;
   }
 };
@@ -249,12 +249,11 @@ int backward_impl(dn_ctx *c, const float *dlogits) {
 
     // MLP: out = h1 + MlpWo(act)
     RC(b.gemm(EPI_F32, T, I, H, dout_op, H, wt(p + "mlp.Wo.weight"), H, dact, I));
-    RC(b.transpose(prec, S.act.p, I, actT));
     HIPCHK(c, "geglu_bwd", launch_geglu_bwd(prec, dact, S.wi.p, tr.dwi.p, T, I, s));
     RC(b.transpose(prec, tr.dwi.p, 2 * I, dwiT));
-    RC(b.transpose(prec, S.n2.p, H, n2T));
     RC(b.gemm(EPI_F32, T, H, 2 * I, tr.dwi.p, 2 * I, wt(p + "mlp.Wi.weight"), 2 * I, dn2, H));
     HIPCHK(c, "ln_bwd(mlp_norm)", launch_ln_bwd(dh1, dcur, dn2, (const float *)S.h1.p, nullptr,
+                                                (const float *)S.mean2.p, (const float *)S.rstd2.p,
                                                 (const float *)W(c, p + "mlp_norm.weight"), g.eps, T, H, lnpart,
                                                 grad(p + "mlp_norm.weight"), s));
 
@@ -262,7 +261,6 @@ int backward_impl(dn_ctx *c, const float *dlogits) {
     RC(b.transpose(0, dh1, H, dh1T, prec == DN_PRECISION_BF16 ? tr.dyop.p : nullptr));
     const void *dh1_op = prec == DN_PRECISION_BF16 ? tr.dyop.p : (const void *)dh1;
     RC(b.gemm(EPI_STORE, T, H, H, dh1_op, H, wt(p + "attn.Wo.weight"), H, tr.dctx.p, H));
-    RC(b.transpose(prec, S.ctx.p, H, ctxT));
 
     AttnBwdArgs at{};
     at.qkv = S.qkv.p;
@@ -291,10 +289,10 @@ int backward_impl(dn_ctx *c, const float *dlogits) {
     HIPCHK(c, "attention_bwd", launch_attention_bwd(prec, at, s));
 
     RC(b.transpose(prec, tr.dqkv.p, 3 * H, dqkvT));
-    RC(b.transpose(prec, S.n1.p, H, n1T));
     RC(b.gemm(EPI_F32, T, H, 3 * H, tr.dqkv.p, 3 * H, wt(p + "attn.Wqkv.weight"), 3 * H, dn1, H));
     if (l > 0) {
       HIPCHK(c, "ln_bwd(attn_norm)", launch_ln_bwd(dprev, dh1, dn1, (const float *)S.hs.p, nullptr,
+                                                   (const float *)S.mean1.p, (const float *)S.rstd1.p,
                                                    (const float *)W(c, p + "attn_norm.weight"), g.eps, T, H, lnpart,
                                                    grad(p + "attn_norm.weight"), s));
     } else {
@@ -305,6 +303,12 @@ int backward_impl(dn_ctx *c, const float *dlogits) {
     // layer's input-gradient chain.
     HIPCHK(c, "hipEventRecord", hipEventRecord(tr.ev_ready[par], s));
     HIPCHK(c, "hipStreamWaitEvent", hipStreamWaitEvent(tr.side, tr.ev_ready[par], 0));
+    // The saved activations' transposes need nothing from this backward: they
+    // run on the side stream too.
+    RC(b.transpose(prec, S.act.p, I, actT, nullptr, tr.side));
+    RC(b.transpose(prec, S.n2.p, H, n2T, nullptr, tr.side));
+    RC(b.transpose(prec, S.ctx.p, H, ctxT, nullptr, tr.side));
+    RC(b.transpose(prec, S.n1.p, H, n1T, nullptr, tr.side));
     RC(b.wgrad(H, I, doutT, actT, grad(p + "mlp.Wo.weight"), tr.side));
     RC(b.wgrad(2 * I, H, dwiT, n2T, grad(p + "mlp.Wi.weight"), tr.side));
     RC(b.wgrad(H, H, dh1T, ctxT, grad(p + "attn.Wo.weight"), tr.side));
@@ -322,7 +326,9 @@ int backward_impl(dn_ctx *c, const float *dlogits) {
     HIPCHK(c, "hipMalloc", ensure(tr.dE, 4 * TH));
     HIPCHK(c, "hipMemsetAsync", hipMemsetAsync(tr.dE.p, 0, 4 * TH, s));
     HIPCHK(c, "ln_bwd(emb)", launch_ln_bwd((float *)tr.dE.p, nullptr, dcur, (const float *)W(c, kTok),
-                                           (const int *)c->ids.p, (const float *)W(c, kEmbNorm), g.eps, T, H, lnpart,
+                                           (const int *)c->ids.p, (const float *)tr.emb_mean.p,
+                                           (const float *)tr.emb_rstd.p, (const float *)W(c, kEmbNorm), g.eps, T, H,
+                                           lnpart,
                                            grad(kEmbNorm), s));
     std::vector<int> order(T);
     std::iota(order.begin(), order.end(), 0);
