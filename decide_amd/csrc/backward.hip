@@ -196,15 +196,17 @@ __global__ __launch_bounds__(256) void ln_bwd_kernel(float *dx, const float *res
   }
   constexpr int RB = LNB_WAVES * LNB_RPW;  // rows per block and pass
   for (int r0 = blockIdx.x * RB + wave * LNB_RPW; r0 < rows; r0 += gridDim.x * RB) {
-    float xv[LNB_RPW][NE], gv[LNB_RPW][NE], m[LNB_RPW], rs[LNB_RPW];
+    float xv[LNB_RPW][NE], gv[LNB_RPW][NE], bv[LNB_RPW][NE], m[LNB_RPW], rs[LNB_RPW];
 #pragma unroll
     for (int q = 0; q < LNB_RPW; q++) {
       const int r = min(r0 + q, rows - 1);
       const float *xr = ids ? x + (size_t)ids[r] * dim : x + (size_t)r * dim;
+      const float *br = (res ? res : dx) + (size_t)r * dim;  // dx = res + ... or dx += ...
 #pragma unroll
       for (int j = 0; j < NE; j++) {
         xv[q][j] = xr[lane + 64 * j];
         gv[q][j] = dy[(size_t)r * dim + lane + 64 * j];
+        bv[q][j] = br[lane + 64 * j];
       }
       if (mean) {
         m[q] = mean[r];
@@ -245,11 +247,10 @@ __global__ __launch_bounds__(256) void ln_bwd_kernel(float *dx, const float *res
       const float a = (float)(wave_sum_d(s1) / (double)dim), b = (float)(wave_sum_d(s2) / (double)dim);
       if (r >= rows) continue;
       float *o = dx + (size_t)r * dim;
-      const float *base = res ? res + (size_t)r * dim : o;  // dx = res + ... (res given) or dx += ...
 #pragma unroll
       for (int j = 0; j < NE; j++) {
 #pragma clang fp contract(off)
-        o[lane + 64 * j] = base[lane + 64 * j] + rs[q] * (gv[q][j] * wv[j] - a - xv[q][j] * b);
+        o[lane + 64 * j] = bv[q][j] + rs[q] * (gv[q][j] * wv[j] - a - xv[q][j] * b);
       }
     }
   }

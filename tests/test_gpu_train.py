@@ -172,6 +172,22 @@ def test_backward_frozen_layers_fp32():
         check_grads(eng, want, "fp32", train_from=2, train_emb=False, label="frozen")
 
 
+def test_backward_head_only_fp32():
+    """trainFrom = Layers: only the final norm and the scorer head get
+    gradients; no layer keeps activations (forward.go:226-236)."""
+    from decide_amd.train import TrainEngine
+
+    cfg = small_cfg(layers=2)
+    w = weights_for(cfg)
+    batch = train_batch(cfg.vocab, cfg.vocab - 1, seed=6)
+    print("case: head only fp32", flush=True)
+    _, dl, want = oracle_grads(cfg, w, batch, train_from=cfg.layers, train_emb=False)
+    with TrainEngine(cfg, w, precision="fp32", train_from=cfg.layers, train_emb=False) as eng:
+        eng.forward(batch)
+        eng.backward(dl)
+        check_grads(eng, want, "fp32", train_from=cfg.layers, train_emb=False, label="head-only")
+
+
 def test_backward_accumulates_and_zero_grad():
     """Two backward passes add (the kernels are deterministic, so exactly
     2x); dn_zero_grad clears every gradient."""
