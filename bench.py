@@ -182,8 +182,8 @@ def systemone(args) -> int:
     return 0
 
 
-TRAIN_METRIC = ("training tokens/sec: one AdamW step over 32 examples (micro-batches within the trainer's 4000-token "
-                "GPU budget), ModernBERT-base, 1 MI355X")
+TRAIN_METRIC = ("training tokens/sec: one AdamW step over 32 examples (micro-batches within the trainer's TokenBudget, "
+                "%d tokens), ModernBERT-base, 1 MI355X")
 
 
 def train_batches(cfg, n_examples=32, token_budget=4000, seed=0):
@@ -251,14 +251,25 @@ def train_bench(args) -> int:
     for _ in range(args.warmup):
         step()
     log(f"timing {args.steps} steps")
+    eng.set_probe(1)
     losses, per_step = [], []
     for _ in range(args.steps):
         t0 = time.perf_counter()
         losses.append(step(timed=True))
         per_step.append(time.perf_counter() - t0)
     wall = sum(per_step)
+    probe, nprobe = eng.read_probe_backward()
+    eng.set_probe(-1)
+    # Roofline kernel: layer 1's QKV weight-gradient GEMM (dWqkv += dqkv^T . n1,
+    # 2 * 2304 * 768 flop per token, split over the tokens, with its split-K
+    # reduce), timed with HIP events on the weight-gradient stream; it shares
+    # the GPU with the main stream's kernels while it runs.
+    qkv_flop = 2.0 * (3 * H) * H * sum(len(s.ids) for s in ex) * args.steps
+    wg_s = probe["wgrad_qkv"] * 1e-3
+    dg_s = probe["dgrad_qkv"] * 1e-3
+    log("backward probe ms per launch (layer 1): %s" % {k: round(v / max(nprobe, 1), 4) for k, v in probe.items()})
     result = {
-        "metric": TRAIN_METRIC,
+        "metric": TRAIN_METRIC % args.token_budget,
         "value": round(T * args.steps / wall, 1),
         "unit": "tokens/s",
         "n_gpus": 1,
@@ -278,6 +289,14 @@ def train_bench(args) -> int:
                    "token_budget": args.token_budget, "precision": args.precision},
         "phase_ms_per_step": {k: round(v * 1e3 / args.steps, 3) for k, v in phases.items()},
         "loss_first_last": [round(losses[0], 5), round(losses[-1], 5)],
+        "backward_probe_ms_per_launch": {k: round(v / max(nprobe, 1), 5) for k, v in probe.items()},
+        "dgrad_qkv_tflops": round(qkv_flop / dg_s / 1e12, 2) if dg_s > 0 else None,
+        "roofline": {"kernel": "gemm_nt_kernel<bf16,128,128,...,EPI_F32> split-K + splitk_reduce_kernel: layer 1 "
+                               "dWqkv (weight-gradient stream, concurrent with the main stream)",
+                     "bound": "mfma", "achieved": round(qkv_flop / wg_s / 1e12, 2) if wg_s > 0 else None,
+                     "peak": PEAK[args.precision] / 1e12, "unit": "TFLOP/s",
+                     "frac": round(qkv_flop / wg_s / PEAK[args.precision], 4) if wg_s > 0 else None,
+                     "traffic": None, "flop_per_step": qkv_flop / args.steps},
     }
     if not args.no_cpu_baseline:
         import oracle

@@ -76,16 +76,17 @@ void release_train(TrainState &tr) {
     for (DevBuf *b : bufs) release(*b);
   }
   tr.layers.clear();
-  DevBuf *bufs[] = {&tr.dcur, &tr.dprev, &tr.dh1, &tr.dact, &tr.dwi, &tr.dn2, &tr.dctx, &tr.dqkv, &tr.dn1,
-                    &tr.dyop, &tr.dsum, &tr.part, &tr.lnpart, &tr.dE, &tr.dl, &tr.contrib, &tr.emb_order,
-                    &tr.emb_seg, &tr.emb_id, &tr.sq_part, &tr.sq_out, &tr.opT[0], &tr.opT[1],
-                    &tr.emb_mean, &tr.emb_rstd};
+  DevBuf *bufs[] = {&tr.dcur, &tr.dprev, &tr.dh1[0], &tr.dh1[1], &tr.dact, &tr.dwi[0], &tr.dwi[1], &tr.dn2,
+                    &tr.dctx, &tr.dqkv[0], &tr.dqkv[1], &tr.dn1, &tr.dop_out, &tr.dop_h1, &tr.dsum, &tr.part,
+                    &tr.lnpart, &tr.dE, &tr.dl, &tr.contrib, &tr.emb_order, &tr.emb_seg, &tr.emb_id, &tr.sq_part,
+                    &tr.sq_out, &tr.opT[0], &tr.opT[1], &tr.emb_mean, &tr.emb_rstd};
   if (tr.side) (void)hipStreamSynchronize(tr.side);
   for (DevBuf *b : bufs) release(*b);
   for (int i = 0; i < 2; i++) {
     if (tr.ev_ready[i]) (void)hipEventDestroy(tr.ev_ready[i]);
     if (tr.ev_done[i]) (void)hipEventDestroy(tr.ev_done[i]);
-    tr.ev_ready[i] = tr.ev_done[i] = nullptr;
+    if (tr.ev_trans[i]) (void)hipEventDestroy(tr.ev_trans[i]);
+    tr.ev_ready[i] = tr.ev_done[i] = tr.ev_trans[i] = nullptr;
   }
   if (tr.side) (void)hipStreamDestroy(tr.side);
   tr.side = nullptr;
@@ -625,6 +626,7 @@ void dn_close(dn_ctx *c) {
   for (auto &kv : c->w) release_slot(kv.second);
   release_train(c->tr);
   for (hipEvent_t e : c->probe_pool) (void)hipEventDestroy(e);
+  for (hipEvent_t e : c->probe_bwd_pool) (void)hipEventDestroy(e);
   DevBuf *bufs[] = {&c->inv_freq, &c->h,     &c->xn,       &c->qkv,         &c->ctxb,     &c->act,
                     &c->rope,     &c->kinfo, &c->ids,      &c->pos,         &c->opt,      &c->rowtok,
                     &c->logits,   &c->err_flag, &c->gA,    &c->gB,          &c->gC,       &c->d_seq_off, &c->head_s1, &c->head_d,
@@ -885,9 +887,27 @@ int dn_synchronize(dn_ctx *c) {
 int dn_set_probe(dn_ctx *c, int layer) {
   if (!c) return DN_INVALID_ARG;
   c->err.clear();
-  if (c->probe_used) HIPCHK(c, "hipStreamSynchronize", hipStreamSynchronize(c->stream));
+  if (c->probe_used || c->probe_bwd_used) HIPCHK(c, "hipStreamSynchronize", hipStreamSynchronize(c->stream));
   c->probe_layer = layer;
   c->probe_used = 0;
+  c->probe_bwd_used = 0;
+  return DN_OK;
+}
+
+int dn_read_probe_backward(dn_ctx *c, double *ms, int *count) {
+  if (!c || !ms || !count) return DN_INVALID_ARG;
+  c->err.clear();
+  HIPCHK(c, "hipStreamSynchronize", hipStreamSynchronize(c->stream));
+  if (c->tr.side) HIPCHK(c, "hipStreamSynchronize", hipStreamSynchronize(c->tr.side));
+  for (int f = 0; f < c->probe_bwd_used; f++)
+    for (int k = 0; k < 3; k++) {
+      float t = 0;
+      HIPCHK(c, "hipEventElapsedTime", hipEventElapsedTime(&t, c->probe_bwd_pool[(size_t)f * 6 + 2 * k],
+                                                           c->probe_bwd_pool[(size_t)f * 6 + 2 * k + 1]));
+      ms[k] += t;
+    }
+  *count += c->probe_bwd_used;
+  c->probe_bwd_used = 0;
   return DN_OK;
 }
 

@@ -184,7 +184,7 @@ constexpr int LNB_WAVES = 4, LNB_RPW = 4;
 template <int NE>
 __global__ __launch_bounds__(256) void ln_bwd_kernel(float *dx, const float *res, const float *dy, const float *x,
                                                      const int *ids, const float *mean, const float *rstd,
-                                                     const float *w, float eps, int rows, float *part) {
+                                                     const float *w, float eps, int rows, float *part, bf16 *dx_op) {
   constexpr int dim = 64 * NE;
   __shared__ float sw[LNB_WAVES][dim];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -250,7 +250,9 @@ __global__ __launch_bounds__(256) void ln_bwd_kernel(float *dx, const float *res
 #pragma unroll
       for (int j = 0; j < NE; j++) {
 #pragma clang fp contract(off)
-        o[lane + 64 * j] = bv[q][j] + rs[q] * (gv[q][j] * wv[j] - a - xv[q][j] * b);
+        const float v = bv[q][j] + rs[q] * (gv[q][j] * wv[j] - a - xv[q][j] * b);
+        o[lane + 64 * j] = v;
+        if (dx_op) dx_op[(size_t)r * dim + lane + 64 * j] = (bf16)v;  // the next GEMM's bf16 operand
       }
     }
   }
@@ -659,14 +661,14 @@ int ln_bwd_blocks(int rows) {
 
 hipError_t launch_ln_bwd(float *dx, const float *res, const float *dy, const float *x, const int *ids,
                          const float *mean, const float *rstd, const float *w, float eps, int rows, int dim,
-                         float *part, float *dw, hipStream_t s) {
+                         float *part, float *dw, hipStream_t s, void *dx_bf16) {
   if (rows <= 0) return hipSuccess;
   const int nb = ln_bwd_blocks(rows) - COLSUM_NG;
   switch (dim) {
 #define LNB_CASE(NE)                                                                                               \
   case 64 * NE:                                                                                                    \
     hipLaunchKernelGGL(ln_bwd_kernel<NE>, dim3(nb), dim3(256), 0, s, dx, res, dy, x, ids, mean, rstd, w, eps, rows, \
-                       part);                                                                                      \
+                       part, (bf16 *)dx_bf16);                                                                     \
     break;
     LNB_CASE(4)
     LNB_CASE(6)

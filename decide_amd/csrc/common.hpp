@@ -203,11 +203,12 @@ hipError_t launch_geglu_bwd(int precision, const float *dact, const void *wi, vo
                             hipStream_t s);
 // LayerNorm backward: dx = res + LNbwd(dy) when res is given, else dx += LNbwd(dy);
 // dw += the weight gradient (part holds ln_bwd_blocks(rows) x dim floats of scratch).
-// mean / rstd: the forward's row statistics (recomputed from x when null).
+// mean / rstd: the forward's row statistics (recomputed from x when null);
+// dx_bf16 (optional) receives dx rounded to bf16 (the next GEMM's operand).
 int ln_bwd_blocks(int rows);
 hipError_t launch_ln_bwd(float *dx, const float *res, const float *dy, const float *x, const int *ids,
                          const float *mean, const float *rstd, const float *w, float eps, int rows, int dim,
-                         float *part, float *dw, hipStream_t s);
+                         float *part, float *dw, hipStream_t s, void *dx_bf16 = nullptr);
 hipError_t launch_add(float *dst, const float *src, size_t n, hipStream_t s);
 hipError_t launch_embed_bwd(const float *dE, const int *order, const int *seg_start, const int *seg_id, int nseg,
                             int dim, float *gtok, hipStream_t s);

@@ -63,7 +63,11 @@ struct TrainState {
   int T = 0, R = 0;
   std::vector<int32_t> ids;   // token ids of the last training forward
   DevBuf emb_mean, emb_rstd;  // emb norm row statistics of the last training forward
-  DevBuf dcur, dprev, dh1, dact, dwi, dn2, dctx, dqkv, dn1, dyop, dsum, part, lnpart, dE, dl, contrib;
+  // dh1, dwi and dqkv alternate by layer parity: the weight-gradient stream
+  // transposes them while the main stream works on the next layer. dop_out /
+  // dop_h1: bf16 copies of dout and dh1 (the input-gradient GEMMs' operands).
+  DevBuf dcur, dprev, dh1[2], dact, dwi[2], dn2, dctx, dqkv[2], dn1, dop_out, dop_h1, dsum, part, lnpart, dE, dl,
+      contrib;
   DevBuf emb_order, emb_seg, emb_id, sq_part, sq_out;
   // Weight-gradient GEMMs run on a second stream: per layer parity, the
   // transposed operands of the layer's four GEMMs, and the events that order
@@ -71,6 +75,7 @@ struct TrainState {
   DevBuf opT[2];
   hipStream_t side = nullptr;
   hipEvent_t ev_ready[2] = {nullptr, nullptr}, ev_done[2] = {nullptr, nullptr};
+  hipEvent_t ev_trans[2] = {nullptr, nullptr};  // the layer's gradient transposes are done
 };
 
 struct dn_ctx {
@@ -100,6 +105,8 @@ struct dn_ctx {
   int probe_layer = -1;
   std::vector<hipEvent_t> probe_pool;  // 10 events per recorded forward
   int probe_used = 0;                  // forwards recorded
+  std::vector<hipEvent_t> probe_bwd_pool;  // 6 events per recorded backward
+  int probe_bwd_used = 0;
   TrainState tr;
 };
 

@@ -91,14 +91,16 @@ int refresh_wt(dn_ctx *c, const std::string &name, TensorSlot &t) {
   return DN_OK;
 }
 
-// Splits of the token (K) dimension for a weight-gradient GEMM: enough
-// workgroups for two per CU (about 512 tiles in all) while each split keeps
-// at least 512 tokens of K; the partial outputs cost splits x M x N floats
-// of extra traffic.
+// Splits of the token (K) dimension for a weight-gradient GEMM: about
+// WGRAD_TILES workgroups in all while each split keeps at least 512 tokens
+// of K; the partial outputs cost splits x M x N floats of extra traffic.
+#ifndef WGRAD_TILES
+#define WGRAD_TILES 512
+#endif
 int split_count(int M, int N, int Tp) {
   const int tiles = ((M + 127) / 128) * (N / 128);
   const int kb = Tp / 64;
-  int s = std::min({16, std::max(1, (512 + tiles - 1) / tiles), std::max(1, kb / 8)});
+  int s = std::min({16, std::max(1, (WGRAD_TILES + tiles - 1) / tiles), std::max(1, kb / 8)});
   while (s > 1 && kb % s) s--;
   return s;
 }
@@ -138,7 +140,14 @@ struct Bwd {
     a.N = N;
     a.K = Tp;
     a.accumulate = 1;
-    HIPCHK(c, "gemm(split-K)", launch_gemm_splitk(prec, a, split_count(M, N, Tp), (float *)c->tr.part.p, ws));
+    const int sp = split_count(M, N, Tp);
+    if (sp == 1) {  // one split: accumulate straight into the gradient
+      a.ldc = N;
+      a.n_store = N;
+      HIPCHK(c, "gemm", launch_gemm(prec, EPI_F32, a, ws));
+      return DN_OK;
+    }
+    HIPCHK(c, "gemm(split-K)", launch_gemm_splitk(prec, a, sp, (float *)c->tr.part.p, ws));
     return DN_OK;
   }
   // dst [cols x Tp] = src[T x cols]^T in the operand type (zero past T); with
@@ -154,6 +163,18 @@ struct Bwd {
     int rc_ = (expr);         \
     if (rc_) return rc_;      \
   } while (0)
+
+// Event pair slots for the backward probe of layer l (null when not probed).
+hipEvent_t *probe_bwd_slot(dn_ctx *c, int l) {
+  if (c->probe_layer != l) return nullptr;
+  const size_t need = (size_t)(c->probe_bwd_used + 1) * 6;
+  while (c->probe_bwd_pool.size() < need) {
+    hipEvent_t e;
+    if (hipEventCreate(&e) != hipSuccess) return nullptr;
+    c->probe_bwd_pool.push_back(e);
+  }
+  return &c->probe_bwd_pool[(size_t)c->probe_bwd_used * 6];
+}
 
 int backward_impl(dn_ctx *c, const float *dlogits) {
   const Config &g = c->cfg;
@@ -171,14 +192,17 @@ int backward_impl(dn_ctx *c, const float *dlogits) {
   const size_t TH = (size_t)T * H;
   HIPCHK(c, "hipMalloc", ensure(tr.dcur, 4 * TH));
   HIPCHK(c, "hipMalloc", ensure(tr.dprev, 4 * TH));
-  HIPCHK(c, "hipMalloc", ensure(tr.dh1, 4 * TH));
+  for (int q = 0; q < 2; q++) {
+    HIPCHK(c, "hipMalloc", ensure(tr.dh1[q], 4 * TH));
+    HIPCHK(c, "hipMalloc", ensure(tr.dwi[q], es * T * 2 * I));
+    HIPCHK(c, "hipMalloc", ensure(tr.dqkv[q], es * T * 3 * H));
+  }
   HIPCHK(c, "hipMalloc", ensure(tr.dn2, 4 * TH));
   HIPCHK(c, "hipMalloc", ensure(tr.dn1, 4 * TH));
   HIPCHK(c, "hipMalloc", ensure(tr.dact, 4 * (size_t)T * I));
-  HIPCHK(c, "hipMalloc", ensure(tr.dwi, es * T * 2 * I));
   HIPCHK(c, "hipMalloc", ensure(tr.dctx, es * TH));
-  HIPCHK(c, "hipMalloc", ensure(tr.dqkv, es * T * 3 * H));
-  HIPCHK(c, "hipMalloc", ensure(tr.dyop, es * TH));
+  HIPCHK(c, "hipMalloc", ensure(tr.dop_out, es * TH));
+  HIPCHK(c, "hipMalloc", ensure(tr.dop_h1, es * TH));
   // Transposed operands of one layer's weight-gradient GEMMs: dout, act, dwi,
   // n2, dh1, ctx, dqkv, n1 (rows of Tp tokens), one arena per layer parity.
   const size_t opT_rows = (size_t)8 * H + 3 * I;
@@ -188,11 +212,14 @@ int backward_impl(dn_ctx *c, const float *dlogits) {
     for (int q = 0; q < 2; q++) {
       HIPCHK(c, "hipEventCreate", hipEventCreateWithFlags(&tr.ev_ready[q], hipEventDisableTiming));
       HIPCHK(c, "hipEventCreate", hipEventCreateWithFlags(&tr.ev_done[q], hipEventDisableTiming));
+      HIPCHK(c, "hipEventCreate", hipEventCreateWithFlags(&tr.ev_trans[q], hipEventDisableTiming));
     }
   }
-  // Nothing of an earlier call may still use the arenas or the partials.
-  HIPCHK(c, "hipEventRecord", hipEventRecord(tr.ev_done[0], tr.side));
-  HIPCHK(c, "hipEventRecord", hipEventRecord(tr.ev_done[1], tr.side));
+  // Nothing of an earlier call may still use the arenas, buffers or partials.
+  for (int q = 0; q < 2; q++) {
+    HIPCHK(c, "hipEventRecord", hipEventRecord(tr.ev_done[q], tr.side));
+    HIPCHK(c, "hipEventRecord", hipEventRecord(tr.ev_trans[q], tr.side));
+  }
   HIPCHK(c, "hipMalloc", ensure(tr.dsum, 4 * (size_t)T * g.heads));
   // split-K partials: weight gradients (<= 16 splits) and input gradients (<= 4 splits of T x max(H, I))
   HIPCHK(c, "hipMalloc", ensure(tr.part, 4 * std::max((size_t)16 * std::max({(size_t)3 * H * H, (size_t)2 * I * H,
@@ -225,15 +252,23 @@ int backward_impl(dn_ctx *c, const float *dlogits) {
 
   const float *rope = (const float *)c->rope.p;
   const size_t nw = (size_t)c->lay_nwork;
-  float *dh1 = (float *)tr.dh1.p, *dn2 = (float *)tr.dn2.p, *dn1 = (float *)tr.dn1.p, *dact = (float *)tr.dact.p;
+  float *dn2 = (float *)tr.dn2.p, *dn1 = (float *)tr.dn1.p, *dact = (float *)tr.dact.p;
+  const bool bf = prec == DN_PRECISION_BF16;
   float *lnpart = (float *)tr.lnpart.p;
   for (int l = L - 1; l >= tr.train_from && l >= 0; l--) {
     const std::string p = layer_prefix(l);
     const LayerSave &S = tr.layers[l];
     const bool sliding = g.sliding[l] != 0;
     const int par = l & 1;
-    // This parity's arena is free once the weight-gradient GEMMs of layer l+2 are done.
-    HIPCHK(c, "hipStreamWaitEvent", hipStreamWaitEvent(s, tr.ev_done[par], 0));
+    hipEvent_t *ev = probe_bwd_slot(c, l);
+    auto mark = [&](int k, int end, hipStream_t st) -> int {
+      if (ev) HIPCHK(c, "hipEventRecord", hipEventRecord(ev[2 * k + end], st));
+      return DN_OK;
+    };
+    // This parity's gradient buffers are free once the weight-gradient stream
+    // has transposed layer l+2's; that stream alone writes the arenas after
+    // the top layer (whose arena write is ordered by the records at entry).
+    HIPCHK(c, "hipStreamWaitEvent", hipStreamWaitEvent(s, tr.ev_trans[par], 0));
     char *arena = (char *)tr.opT[par].p;
     size_t row0 = 0;
     auto slice = [&](int rows) {
@@ -243,23 +278,27 @@ int backward_impl(dn_ctx *c, const float *dlogits) {
     };
     void *doutT = slice(H), *actT = slice(I), *dwiT = slice(2 * I), *n2T = slice(H), *dh1T = slice(H),
          *ctxT = slice(H), *dqkvT = slice(3 * H), *n1T = slice(H);
-    // dout (fp32) as an operand: its transpose, and in bf16 its rounded copy.
-    RC(b.transpose(0, dcur, H, doutT, prec == DN_PRECISION_BF16 ? tr.dyop.p : nullptr));
-    const void *dout_op = prec == DN_PRECISION_BF16 ? tr.dyop.p : (const void *)dcur;
+    float *dh1 = (float *)tr.dh1[par].p;
+    void *dwi = tr.dwi[par].p, *dqkv = tr.dqkv[par].p;
+    const bool top = l == L - 1;
+    // dout (fp32) as an operand: in bf16 its rounded copy, written by the
+    // layer above's LN backward (for the top layer, by this transpose, which
+    // also gives its transposed copy; lower layers' transposes run on the
+    // weight-gradient stream).
+    if (top) RC(b.transpose(0, dcur, H, doutT, bf ? tr.dop_out.p : nullptr));
+    const void *dout_op = bf ? tr.dop_out.p : (const void *)dcur;
 
     // MLP: out = h1 + MlpWo(act)
     RC(b.gemm(EPI_F32, T, I, H, dout_op, H, wt(p + "mlp.Wo.weight"), H, dact, I));
-    HIPCHK(c, "geglu_bwd", launch_geglu_bwd(prec, dact, S.wi.p, tr.dwi.p, T, I, s));
-    RC(b.transpose(prec, tr.dwi.p, 2 * I, dwiT));
-    RC(b.gemm(EPI_F32, T, H, 2 * I, tr.dwi.p, 2 * I, wt(p + "mlp.Wi.weight"), 2 * I, dn2, H));
+    HIPCHK(c, "geglu_bwd", launch_geglu_bwd(prec, dact, S.wi.p, dwi, T, I, s));
+    RC(b.gemm(EPI_F32, T, H, 2 * I, dwi, 2 * I, wt(p + "mlp.Wi.weight"), 2 * I, dn2, H));
     HIPCHK(c, "ln_bwd(mlp_norm)", launch_ln_bwd(dh1, dcur, dn2, (const float *)S.h1.p, nullptr,
                                                 (const float *)S.mean2.p, (const float *)S.rstd2.p,
                                                 (const float *)W(c, p + "mlp_norm.weight"), g.eps, T, H, lnpart,
-                                                grad(p + "mlp_norm.weight"), s));
+                                                grad(p + "mlp_norm.weight"), s, bf ? tr.dop_h1.p : nullptr));
 
     // Attention: h1 = in + Wo(ctx)
-    RC(b.transpose(0, dh1, H, dh1T, prec == DN_PRECISION_BF16 ? tr.dyop.p : nullptr));
-    const void *dh1_op = prec == DN_PRECISION_BF16 ? tr.dyop.p : (const void *)dh1;
+    const void *dh1_op = bf ? tr.dop_h1.p : (const void *)dh1;
     RC(b.gemm(EPI_STORE, T, H, H, dh1_op, H, wt(p + "attn.Wo.weight"), H, tr.dctx.p, H));
 
     AttnBwdArgs at{};
@@ -268,7 +307,7 @@ int backward_impl(dn_ctx *c, const float *dlogits) {
     at.dctx = tr.dctx.p;
     at.lse = (const float *)S.lse.p;
     at.dsum = (float *)tr.dsum.p;
-    at.dqkv = tr.dqkv.p;
+    at.dqkv = dqkv;
     at.kinfo = (const int *)c->kinfo.p;
     at.cos_t = rope + (size_t)(sliding ? 2 : 0) * kPositions * 32;
     at.sin_t = rope + (size_t)(sliding ? 3 : 1) * kPositions * 32;
@@ -286,15 +325,20 @@ int backward_impl(dn_ctx *c, const float *dlogits) {
     at.half_window = g.half_window;
     at.scale = (float)(1.0 / std::sqrt(64.0));
     at.scale_log2 = at.scale * 1.44269504088896340736f;
+    RC(mark(DN_PROBE_BWD_ATTENTION, 0, s));
     HIPCHK(c, "attention_bwd", launch_attention_bwd(prec, at, s));
+    RC(mark(DN_PROBE_BWD_ATTENTION, 1, s));
 
-    RC(b.transpose(prec, tr.dqkv.p, 3 * H, dqkvT));
-    RC(b.gemm(EPI_F32, T, H, 3 * H, tr.dqkv.p, 3 * H, wt(p + "attn.Wqkv.weight"), 3 * H, dn1, H));
+    RC(mark(DN_PROBE_BWD_DGRAD_QKV, 0, s));
+    RC(b.gemm(EPI_F32, T, H, 3 * H, dqkv, 3 * H, wt(p + "attn.Wqkv.weight"), 3 * H, dn1, H));
+    RC(mark(DN_PROBE_BWD_DGRAD_QKV, 1, s));
+    // dprev held the layer above's dout: its transpose must be done.
+    HIPCHK(c, "hipStreamWaitEvent", hipStreamWaitEvent(s, tr.ev_trans[par ^ 1], 0));
     if (l > 0) {
       HIPCHK(c, "ln_bwd(attn_norm)", launch_ln_bwd(dprev, dh1, dn1, (const float *)S.hs.p, nullptr,
                                                    (const float *)S.mean1.p, (const float *)S.rstd1.p,
                                                    (const float *)W(c, p + "attn_norm.weight"), g.eps, T, H, lnpart,
-                                                   grad(p + "attn_norm.weight"), s));
+                                                   grad(p + "attn_norm.weight"), s, bf ? tr.dop_out.p : nullptr));
     } else {
       HIPCHK(c, "hipMemcpyAsync", hipMemcpyAsync(dprev, dh1, 4 * TH, hipMemcpyDeviceToDevice, s));
       HIPCHK(c, "add", launch_add(dprev, dn1, TH, s));
@@ -303,8 +347,13 @@ int backward_impl(dn_ctx *c, const float *dlogits) {
     // layer's input-gradient chain.
     HIPCHK(c, "hipEventRecord", hipEventRecord(tr.ev_ready[par], s));
     HIPCHK(c, "hipStreamWaitEvent", hipStreamWaitEvent(tr.side, tr.ev_ready[par], 0));
-    // The saved activations' transposes need nothing from this backward: they
-    // run on the side stream too.
+    // The gradients' transposes (their buffers alternate by layer parity;
+    // dout's is released by ev_trans), then the saved activations'.
+    if (!top) RC(b.transpose(0, dcur, H, doutT, nullptr, tr.side));
+    RC(b.transpose(prec, dwi, 2 * I, dwiT, nullptr, tr.side));
+    RC(b.transpose(0, dh1, H, dh1T, nullptr, tr.side));
+    RC(b.transpose(prec, dqkv, 3 * H, dqkvT, nullptr, tr.side));
+    HIPCHK(c, "hipEventRecord", hipEventRecord(tr.ev_trans[par], tr.side));
     RC(b.transpose(prec, S.act.p, I, actT, nullptr, tr.side));
     RC(b.transpose(prec, S.n2.p, H, n2T, nullptr, tr.side));
     RC(b.transpose(prec, S.ctx.p, H, ctxT, nullptr, tr.side));
@@ -312,7 +361,10 @@ int backward_impl(dn_ctx *c, const float *dlogits) {
     RC(b.wgrad(H, I, doutT, actT, grad(p + "mlp.Wo.weight"), tr.side));
     RC(b.wgrad(2 * I, H, dwiT, n2T, grad(p + "mlp.Wi.weight"), tr.side));
     RC(b.wgrad(H, H, dh1T, ctxT, grad(p + "attn.Wo.weight"), tr.side));
+    RC(mark(DN_PROBE_BWD_WGRAD_QKV, 0, tr.side));
     RC(b.wgrad(3 * H, H, dqkvT, n1T, grad(p + "attn.Wqkv.weight"), tr.side));
+    RC(mark(DN_PROBE_BWD_WGRAD_QKV, 1, tr.side));
+    if (ev) c->probe_bwd_used++;
     HIPCHK(c, "hipEventRecord", hipEventRecord(tr.ev_done[par], tr.side));
     std::swap(dcur, dprev);
   }

@@ -77,6 +77,15 @@ class TrainEngine(Engine):
         a = np.ascontiguousarray(data, np.float32).reshape(-1)
         check(lib.dn_upload_state(self._h, name.encode(), STATES[which], _ptr(a), a.size), self._h)
 
+    BWD_PROBE_NAMES = ("wgrad_qkv", "dgrad_qkv", "attention_bwd")
+
+    def read_probe_backward(self):
+        """(total ms per probed backward launch, number of backward passes recorded)."""
+        ms = np.zeros(3, np.float64)
+        cnt = ctypes.c_int(0)
+        check(lib.dn_read_probe_backward(self._h, _ptr(ms), ctypes.byref(cnt)), self._h)
+        return dict(zip(self.BWD_PROBE_NAMES, ms.tolist())), cnt.value
+
     def set_adam_step(self, step: int) -> None:
         check(lib.dn_set_adam_step(self._h, int(step)), self._h)
 

@@ -164,6 +164,15 @@ enum { DN_PROBE_QKV = 0, DN_PROBE_ATTENTION = 1, DN_PROBE_WO = 2, DN_PROBE_WI = 
 int dn_set_probe(dn_ctx *ctx, int layer);
 int dn_read_probe(dn_ctx *ctx, double *ms /* [5] */, int *count);
 
+/* The same probe in dn_backward: events around three launches of layer
+ * `layer`'s backward: the QKV weight-gradient GEMM (split-K GEMM + its
+ * reduce, on the weight-gradient stream), the input-gradient GEMM
+ * dqkv . Wqkv, and the attention backward (both kernels). dn_read_probe_backward
+ * adds their durations to ms[3] and the number of backward passes seen to
+ * *count, and resets it. No counterpart in the reference. */
+enum { DN_PROBE_BWD_WGRAD_QKV = 0, DN_PROBE_BWD_DGRAD_QKV = 1, DN_PROBE_BWD_ATTENTION = 2 };
+int dn_read_probe_backward(dn_ctx *ctx, double *ms /* [3] */, int *count);
+
 /* ---- host-side helpers mirroring the reference's scoring glue ---------- */
 
 /* nn.BuildSequence (internal/nn/forward.go:28-56). Writes pos[n] and, when
