@@ -295,6 +295,44 @@ def test_backward_matches_oracle_modernbert_base(prec):
         check_grads(eng, want, prec, label="base")
 
 
+def test_backward_full_size_deterministic_and_linear():
+    """At the trainer's micro-batch size (10 examples x 384 tokens under the
+    4000-token budget, ModernBERT-base, bf16, embeddings trained): a second
+    backward of the same forward gives bit-identical gradients (the weight
+    gradients run on a second stream, so an unsynchronised buffer would show
+    here), and the backward of 2 x dlogits after a fresh forward gives exactly
+    twice every gradient (the backward is linear in dlogits and scaling by 2
+    commutes with every rounding)."""
+    from decide_amd import modernbert_base
+    from decide_amd.nn import MASK_ID, build_sequence, tensor_shapes
+    from decide_amd.synth import pack_request, random_weights
+    from decide_amd.train import TrainEngine
+
+    cfg = modernbert_base()
+    w = random_weights(cfg, seed=11)
+    rng = np.random.default_rng(12)
+    batch = [build_sequence(pack_request(rng, 256, [16] * 8, cfg.vocab), MASK_ID, True) for _ in range(10)]
+    R = sum(len(s.mask_pos) for s in batch)
+    dl = (rng.standard_normal(R) * 0.1).astype(np.float32)
+    print(f"case: full-size backward determinism, T={sum(len(s.ids) for s in batch)}", flush=True)
+    names = list(tensor_shapes(cfg))
+    with TrainEngine(cfg, w, precision="bf16", train_from=0, train_emb=True) as eng:
+        eng.forward(batch)
+        eng.backward(dl)
+        once = {n: eng.download(n, "grad") for n in names}
+        for n, g in once.items():
+            assert np.all(np.isfinite(g)) and np.any(g), n
+        eng.zero_grad()
+        eng.backward(dl)
+        for n, g in once.items():
+            assert np.array_equal(eng.download(n, "grad"), g), n
+        eng.zero_grad()
+        eng.forward(batch)
+        eng.backward(2 * dl)
+        for n, g in once.items():
+            assert np.array_equal(eng.download(n, "grad"), 2 * g), n
+
+
 def test_training_errors():
     """Backward needs a training forward (an inference forward invalidates
     it) and the forward's row count; training must be enabled before bf16
