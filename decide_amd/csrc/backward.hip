@@ -27,24 +27,6 @@ __device__ __forceinline__ float ld_elem(const T *p) {
   return (float)*p;
 }
 
-// d gelu(x)/dx = Phi(x) + x phi(x) (geluGrad, ops.go:145-150): float64 in the
-// fp32 build; the bf16 build uses the same erf approximation as its forward.
-template <class T>
-__device__ __forceinline__ float gelu_grad(float x);
-template <>
-__device__ __forceinline__ float gelu_grad<float>(float x) {
-  const double xf = (double)x;
-  const double cdf = 0.5 * (1 + erf(xf * 1.41421356237309504880 / 2));
-  const double pdf = exp(-0.5 * xf * xf) / sqrt(2 * 3.14159265358979323846);
-  return (float)(cdf + xf * pdf);
-}
-template <>
-__device__ __forceinline__ float gelu_grad<bf16>(float x) {
-  const float cdf = 0.5f * (1.0f + erf_as(x * 0.70710678118654752440f));
-  const float pdf = exp2f(-0.5f * x * x * 1.44269504088896341f) * 0.39894228040143267794f;
-  return cdf + x * pdf;
-}
-
 // ---------------------------------------------------------------------------
 // 64 x 64 tiles through LDS: dstT[c][r] = src[r][c] for r < rows_pad (zero
 // for r >= rows), converted to TO; when copy is set also copy[r][c] = src[r][c]
@@ -75,38 +57,6 @@ __global__ __launch_bounds__(256) void transpose_kernel(const TI *src, int rows,
 
 // The same with 8-element vectors (16 bytes of bf16, 32 of fp32) on both
 // sides: needs cols, lds and ldt multiples of 8 and rows_pad a multiple of 64.
-template <class T>
-struct Vec8;
-template <>
-struct Vec8<bf16> {
-  static __device__ __forceinline__ void load(const bf16 *p, float (&v)[8]) {
-    const uint4 u = *(const uint4 *)p;
-    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-      v[2 * i] = __uint_as_float(w[i] << 16);
-      v[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
-    }
-  }
-  static __device__ __forceinline__ void store(bf16 *p, const float (&v)[8]) {
-    bf16x8 o;
-#pragma unroll
-    for (int i = 0; i < 8; i++) o[i] = (bf16)v[i];
-    *(bf16x8 *)p = o;
-  }
-};
-template <>
-struct Vec8<float> {
-  static __device__ __forceinline__ void load(const float *p, float (&v)[8]) {
-    const float4 a = *(const float4 *)p, b = *(const float4 *)(p + 4);
-    v[0] = a.x, v[1] = a.y, v[2] = a.z, v[3] = a.w, v[4] = b.x, v[5] = b.y, v[6] = b.z, v[7] = b.w;
-  }
-  static __device__ __forceinline__ void store(float *p, const float (&v)[8]) {
-    *(float4 *)p = make_float4(v[0], v[1], v[2], v[3]);
-    *(float4 *)(p + 4) = make_float4(v[4], v[5], v[6], v[7]);
-  }
-};
-
 template <class TI, class TO>
 __global__ __launch_bounds__(256) void transpose8_kernel(const TI *src, int rows, int cols, int lds, TO *dstT,
                                                          int ldt, int rows_pad, TO *copy) {

@@ -78,6 +78,57 @@ __device__ __forceinline__ float gelu_erf<bf16>(float x) {
   return 0.5f * x * (1.0f + erf_as(x * 0.70710678118654752440f));
 }
 
+// d gelu(x)/dx = Phi(x) + x phi(x) (geluGrad, ops.go:145-150): float64 in the
+// fp32 build; the bf16 build uses the same erf approximation as its forward.
+template <class T>
+__device__ __forceinline__ float gelu_grad(float x);
+template <>
+__device__ __forceinline__ float gelu_grad<float>(float x) {
+  const double xf = (double)x;
+  const double cdf = 0.5 * (1 + erf(xf * 1.41421356237309504880 / 2));
+  const double pdf = exp(-0.5 * xf * xf) / sqrt(2 * 3.14159265358979323846);
+  return (float)(cdf + xf * pdf);
+}
+template <>
+__device__ __forceinline__ float gelu_grad<bf16>(float x) {
+  const float cdf = 0.5f * (1.0f + erf_as(x * 0.70710678118654752440f));
+  const float pdf = exp2f(-0.5f * x * x * 1.44269504088896341f) * 0.39894228040143267794f;
+  return cdf + x * pdf;
+}
+
+// Eight consecutive elements as floats: 16 bytes of bf16 or 32 of fp32.
+template <class T>
+struct Vec8;
+template <>
+struct Vec8<bf16> {
+  static __device__ __forceinline__ void load(const bf16 *p, float (&v)[8]) {
+    const uint4 u = *(const uint4 *)p;
+    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      v[2 * i] = __uint_as_float(w[i] << 16);
+      v[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+    }
+  }
+  static __device__ __forceinline__ void store(bf16 *p, const float (&v)[8]) {
+    bf16x8 o;
+#pragma unroll
+    for (int i = 0; i < 8; i++) o[i] = (bf16)v[i];
+    *(bf16x8 *)p = o;
+  }
+};
+template <>
+struct Vec8<float> {
+  static __device__ __forceinline__ void load(const float *p, float (&v)[8]) {
+    const float4 a = *(const float4 *)p, b = *(const float4 *)(p + 4);
+    v[0] = a.x, v[1] = a.y, v[2] = a.z, v[3] = a.w, v[4] = b.x, v[5] = b.y, v[6] = b.z, v[7] = b.w;
+  }
+  static __device__ __forceinline__ void store(float *p, const float (&v)[8]) {
+    *(float4 *)p = make_float4(v[0], v[1], v[2], v[3]);
+    *(float4 *)(p + 4) = make_float4(v[4], v[5], v[6], v[7]);
+  }
+};
+
 // Summary of up to 32 consecutive tokens of one sequence, used by the
 // attention kernel to skip (or fast-path) whole key tiles.
 struct ChunkInfo {
@@ -103,13 +154,20 @@ struct GemmArgs {
   const float *res; // EPI_F32 with accumulate: C = res + result (res has C's layout); null: C += result
   void *C2;         // EPI_GEGLU_KEEP: the GeGLU output (ldc2), C receives the plain product
   int ldc2;
+  const void *gin;  // EPI_GEGLU_BWD: the GeGLU input (the Wi output, M x 2N, row stride ldc)
 };
 
 // GEMM epilogues: fp32 store / accumulate, store in the operand type, GeGLU of
-// value/gate column pairs, and (training) both the plain product and its GeGLU.
-enum { EPI_F32 = 0, EPI_STORE = 1, EPI_GEGLU = 2, EPI_GEGLU_KEEP = 3 };
+// value/gate column pairs, and (training) both the plain product and its
+// GeGLU, or the GeGLU backward: the product is the gradient of the GeGLU
+// output (M x N), and C (M x 2N, operand type, the interleaved Wi layout)
+// receives the gradients of its value and gate inputs, read from gin.
+enum { EPI_F32 = 0, EPI_STORE = 1, EPI_GEGLU = 2, EPI_GEGLU_KEEP = 3, EPI_GEGLU_BWD = 4 };
 
 hipError_t launch_gemm(int precision, int epi, const GemmArgs &a, hipStream_t s);
+// Whether launch_gemm takes this epilogue at M rows (EPI_GEGLU_BWD needs the
+// tiled kernel: M > 128 in bf16, M > 1024 in fp32).
+bool gemm_epi_ok(int precision, int epi, int M);
 // Split-K fp32-output GEMM: `splits` partial products, each over a.K / splits
 // of K (a.K % (splits * 64) == 0), written to partial + split * M * N
 // (row-major, ldc = N), then summed in split order into C (M x N, ldc = N;

@@ -88,10 +88,10 @@ __global__ __launch_bounds__(64 * WGM * WGN) __attribute__((amdgpu_waves_per_eu(
   constexpr int STAGE = (BM + BN) * RB;
   constexpr int LOADS = (BM + BN) * CPR / NT;  // 16-byte DMA loads per thread per stage
   static_assert(LOADS * NT == (BM + BN) * CPR, "tile rows must fill whole DMA instructions");
-  static_assert(EPI == EPI_F32 || TN % 2 == 0, "paired epilogues need 64-column wave tiles");
+  static_assert(EPI == EPI_F32 || EPI == EPI_GEGLU_BWD || TN % 2 == 0, "paired epilogues need 64-column wave tiles");
   static_assert(NSTAGE >= 2 && LOADS * (NSTAGE - 2) < 64, "pipeline depth");
   // fp32 epilogue staged in WGM passes of WM rows; the others in one pass.
-  constexpr int EPI_BYTES = (EPI == EPI_F32) ? WM * (BN + 4) * 4
+  constexpr int EPI_BYTES = (EPI == EPI_F32 || EPI == EPI_GEGLU_BWD) ? WM * (BN + 4) * 4
                                              : BM * ((EPI == EPI_GEGLU ? BN / 2 : BN) + 8) * (int)sizeof(T);
   constexpr int SMEM = NSTAGE * STAGE > EPI_BYTES ? NSTAGE * STAGE : EPI_BYTES;
   __shared__ __attribute__((aligned(1024))) char smem[SMEM];
@@ -222,7 +222,68 @@ __global__ __launch_bounds__(64 * WGM * WGN) __attribute__((amdgpu_waves_per_eu(
   // All waves done with the ring and every DMA landed: reuse it for the epilogue.
   wait_vmcnt<0>();
   __builtin_amdgcn_s_barrier();
-  if constexpr (EPI == EPI_F32) {
+  // fp32 staging of the rows of wave row `pass` (LD floats per row).
+  auto stage_f32 = [&](float *st, int LD, int pass) {
+    if (wm == pass) {
+#pragma unroll
+      for (int i = 0; i < TM; i++)
+#pragma unroll
+        for (int j = 0; j < TN; j++)
+#pragma unroll
+          for (int q = 0; q < 4; q++)
+            *(float4 *)(st + (i * 32 + lr) * LD + cw + j * 32 + mfma_row(4 * q, lane)) =
+                make_float4(acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]);
+    }
+  };
+  if constexpr (EPI == EPI_GEGLU_BWD) {
+    // The product is dact (the GeGLU output's gradient, fp32, as the
+    // reference's backward holds it); each thread takes 8 consecutive
+    // columns of one row (inside one 32-column group), reads the matching
+    // value and gate inputs and writes their gradients (backward.go:49-61).
+    // Output column n of the product is value column 64*(n/32) + n%32 of the
+    // interleaved layout, so the tile's outputs are 2*BN contiguous columns.
+    constexpr int LD = BN + 4, HM = WM, U = BN / 8;
+    constexpr int ITER = HM * U / NT;
+    constexpr int BATCH = ITER < 4 ? ITER : 4;
+    static_assert(ITER * NT == HM * U && ITER % BATCH == 0, "GeGLU backward epilogue shape");
+    float *st = (float *)smem;
+    const T *Wg = (const T *)g.gin;
+    T *D = (T *)gC;
+#pragma unroll
+    for (int pass = 0; pass < WGM; pass++) {
+      stage_f32(st, LD, pass);
+      __syncthreads();
+      for (int b0 = 0; b0 < ITER; b0 += BATCH) {
+        float a[BATCH][8], gt[BATCH][8];
+#pragma unroll
+        for (int u = 0; u < BATCH; u++) {
+          const int c = tid + (b0 + u) * NT, r = c / U, cu = (c % U) * 8;
+          const int row = min(m0 + pass * HM + r, g.M - 1);
+          const size_t o = (size_t)row * g.ldc + 2 * n0 + 64 * (cu >> 5) + (cu & 31);
+          Vec8<T>::load(Wg + o, a[u]);
+          Vec8<T>::load(Wg + o + 32, gt[u]);
+        }
+#pragma unroll
+        for (int u = 0; u < BATCH; u++) {
+          const int c = tid + (b0 + u) * NT, r = c / U, cu = (c % U) * 8;
+          const int row = m0 + pass * HM + r;
+          if (row >= g.M) continue;
+          const size_t o = (size_t)row * g.ldc + 2 * n0 + 64 * (cu >> 5) + (cu & 31);
+          const float4 d0 = *(const float4 *)(st + r * LD + cu), d1 = *(const float4 *)(st + r * LD + cu + 4);
+          const float da[8] = {d0.x, d0.y, d0.z, d0.w, d1.x, d1.y, d1.z, d1.w};
+          float dv[8], dg[8];
+#pragma unroll
+          for (int e = 0; e < 8; e++) {
+            dv[e] = da[e] * gt[u][e] * gelu_grad<T>(a[u][e]);
+            dg[e] = da[e] * gelu_erf<T>(a[u][e]);
+          }
+          Vec8<T>::store(D + o, dv);
+          Vec8<T>::store(D + o + 32, dg);
+        }
+      }
+      if (pass + 1 < WGM) __syncthreads();
+    }
+  } else if constexpr (EPI == EPI_F32) {
     constexpr int LD = BN + 4;  // floats per staged row
     constexpr int HM = WM;      // rows per pass: the waves with wm == pass stage theirs
     float *st = (float *)smem;
@@ -235,16 +296,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) __attribute__((amdgpu_waves_per_eu(
     const bool vec = (g.ldc & 3) == 0;
 #pragma unroll
     for (int pass = 0; pass < WGM; pass++) {
-      if (wm == pass) {
-#pragma unroll
-        for (int i = 0; i < TM; i++)
-#pragma unroll
-          for (int j = 0; j < TN; j++)
-#pragma unroll
-            for (int q = 0; q < 4; q++)
-              *(float4 *)(st + (i * 32 + lr) * LD + cw + j * 32 + mfma_row(4 * q, lane)) =
-                  make_float4(acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]);
-      }
+      stage_f32(st, LD, pass);
       __syncthreads();
       // All loads of a batch are issued before its stores (C is read and
       // written here, so the compiler would otherwise serialise each pair).
@@ -343,6 +395,9 @@ hipError_t launch_cfg(int epi, const GemmArgs &a, hipStream_t s, int splits = 1)
       break;
     case EPI_GEGLU:
       hipLaunchKernelGGL((gemm_nt_kernel<T, BM, BN, RB, NSTAGE, EPI_GEGLU, WPE, WGM, WGN>), grid, block, 0, s, a);
+      break;
+    case EPI_GEGLU_BWD:
+      hipLaunchKernelGGL((gemm_nt_kernel<T, BM, BN, RB, NSTAGE, EPI_GEGLU_BWD, WPE, WGM, WGN>), grid, block, 0, s, a);
       break;
     default:
       hipLaunchKernelGGL((gemm_nt_kernel<T, BM, BN, RB, NSTAGE, EPI_GEGLU_KEEP, WPE, WGM, WGN>), grid, block, 0, s, a);
@@ -630,8 +685,14 @@ bool gemm_shape_ok(int precision, int N, int K) {
   return N > 0 && K > 0 && N % 128 == 0 && K % kt == 0;
 }
 
+bool gemm_epi_ok(int precision, int epi, int M) {
+  if (epi != EPI_GEGLU_BWD) return true;
+  return precision == 1 ? M > 128 : M > 1024;
+}
+
 hipError_t launch_gemm(int precision, int epi, const GemmArgs &a0, hipStream_t s) {
   if (a0.M <= 0) return hipSuccess;
+  if (!gemm_epi_ok(precision, epi, a0.M) || (epi == EPI_GEGLU_BWD && (!a0.gin || a0.ldc % 8))) return hipErrorInvalidValue;
   // Small M goes to the whole-K kernel (grid: N/32 x M/64 workgroups). In
   // fp32 (the scorer's dense layer over all [MASK] rows, the fp32 validation
   // build) that pays up to M = 1024: the 64 x 128 tiles below would leave
@@ -655,12 +716,12 @@ hipError_t launch_gemm(int precision, int epi, const GemmArgs &a0, hipStream_t s
   //  * paired / store epilogues (N = 2304): 256 x 128, 64-byte stages x 3
   //    (72 KB LDS), two workgroups per CU so one tile's epilogue and DMA
   //    stalls overlap the other's MFMAs;
-  //  * fp32 residual epilogue (N = 768): 128 x 128, 64-byte stages x 3
-  //    (48 KB), three workgroups per CU.
+  //  * fp32 residual epilogue (N = 768) and the GeGLU backward (training):
+  //    128 x 128, 64-byte stages x 3 (48 KB), three workgroups per CU.
   const bool small = a.M <= 1024;
   if (precision == 1) {
     if (small) return launch_cfg<bf16, 64, 128, 128, 4, 1>(epi, a, s);
-    if (epi == EPI_F32) return launch_cfg<bf16, 128, 128, 64, 3, 3>(epi, a, s);
+    if (epi == EPI_F32 || epi == EPI_GEGLU_BWD) return launch_cfg<bf16, 128, 128, 64, 3, 3>(epi, a, s);
     return launch_cfg<bf16, 256, 128, 64, 3, 2>(epi, a, s);
   }
   if (small) return launch_cfg<float, 64, 128, 128, 4, 1>(epi, a, s);

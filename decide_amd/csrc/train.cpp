@@ -7,6 +7,7 @@
 // Per layer, from the top (dout = gradient of the layer output, fp32):
 //   dact = dout . MlpWo            gMlpWo += dout^T . act
 //   dwi  = GeGLU'(dact, wi)        gWi    += dwi^T . n2       dn2 = dwi . Wi
+//          (in the dact GEMM's epilogue, dact is never stored)
 //   dh1  = dout + LNbwd(dn2)       (mlp_norm)
 //   dctx = dh1 . Wo                gWo    += dh1^T . ctx
 //   dqkv = attention backward (RoPE inverse on dq, dk)
@@ -199,7 +200,8 @@ int backward_impl(dn_ctx *c, const float *dlogits) {
   }
   HIPCHK(c, "hipMalloc", ensure(tr.dn2, 4 * TH));
   HIPCHK(c, "hipMalloc", ensure(tr.dn1, 4 * TH));
-  HIPCHK(c, "hipMalloc", ensure(tr.dact, 4 * (size_t)T * I));
+  // dact only when the GeGLU backward cannot run in the GEMM's epilogue.
+  if (!gemm_epi_ok(prec, EPI_GEGLU_BWD, T)) HIPCHK(c, "hipMalloc", ensure(tr.dact, 4 * (size_t)T * I));
   HIPCHK(c, "hipMalloc", ensure(tr.dctx, es * TH));
   HIPCHK(c, "hipMalloc", ensure(tr.dop_out, es * TH));
   HIPCHK(c, "hipMalloc", ensure(tr.dop_h1, es * TH));
@@ -254,6 +256,7 @@ int backward_impl(dn_ctx *c, const float *dlogits) {
   const size_t nw = (size_t)c->lay_nwork;
   float *dn2 = (float *)tr.dn2.p, *dn1 = (float *)tr.dn1.p, *dact = (float *)tr.dact.p;
   const bool bf = prec == DN_PRECISION_BF16;
+  const bool fuse_geglu = gemm_epi_ok(prec, EPI_GEGLU_BWD, T);
   float *lnpart = (float *)tr.lnpart.p;
   for (int l = L - 1; l >= tr.train_from && l >= 0; l--) {
     const std::string p = layer_prefix(l);
@@ -289,8 +292,24 @@ int backward_impl(dn_ctx *c, const float *dlogits) {
     const void *dout_op = bf ? tr.dop_out.p : (const void *)dcur;
 
     // MLP: out = h1 + MlpWo(act)
-    RC(b.gemm(EPI_F32, T, I, H, dout_op, H, wt(p + "mlp.Wo.weight"), H, dact, I));
-    HIPCHK(c, "geglu_bwd", launch_geglu_bwd(prec, dact, S.wi.p, dwi, T, I, s));
+    if (fuse_geglu) {  // dwi straight from the GEMM's epilogue
+      GemmArgs ga{};
+      ga.A = dout_op;
+      ga.lda = H;
+      ga.B = wt(p + "mlp.Wo.weight");
+      ga.ldb = H;
+      ga.C = dwi;
+      ga.ldc = 2 * I;
+      ga.M = T;
+      ga.N = I;
+      ga.K = H;
+      ga.n_store = I;
+      ga.gin = S.wi.p;
+      HIPCHK(c, "gemm(geglu_bwd)", launch_gemm(prec, EPI_GEGLU_BWD, ga, s));
+    } else {
+      RC(b.gemm(EPI_F32, T, I, H, dout_op, H, wt(p + "mlp.Wo.weight"), H, dact, I));
+      HIPCHK(c, "geglu_bwd", launch_geglu_bwd(prec, dact, S.wi.p, dwi, T, I, s));
+    }
     RC(b.gemm(EPI_F32, T, H, 2 * I, dwi, 2 * I, wt(p + "mlp.Wi.weight"), 2 * I, dn2, H));
     HIPCHK(c, "ln_bwd(mlp_norm)", launch_ln_bwd(dh1, dcur, dn2, (const float *)S.h1.p, nullptr,
                                                 (const float *)S.mean2.p, (const float *)S.rstd2.p,
