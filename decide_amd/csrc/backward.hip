@@ -631,9 +631,15 @@ hipError_t launch_ln_bwd(float *dx, const float *res, const float *dy, const flo
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || !dw) return e;
+  return launch_ln_bwd_colsum(part, rows, dim, dw, s);
+}
+
+hipError_t launch_ln_bwd_colsum(float *part, int rows, int dim, float *dw, hipStream_t s) {
+  if (rows <= 0) return hipSuccess;
+  const int nb = ln_bwd_blocks(rows) - COLSUM_NG;
   float *part2 = part + (size_t)nb * dim;
   hipLaunchKernelGGL(colsum_kernel, dim3((dim + 63) / 64, COLSUM_NG), dim3(256), 0, s, part, nb, dim, part2);
-  e = hipGetLastError();
+  hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(colsum_final_kernel, dim3(blocks(dim)), dim3(256), 0, s, part2, dim, dw);
   return hipGetLastError();

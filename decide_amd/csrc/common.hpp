@@ -267,6 +267,9 @@ int ln_bwd_blocks(int rows);
 hipError_t launch_ln_bwd(float *dx, const float *res, const float *dy, const float *x, const int *ids,
                          const float *mean, const float *rstd, const float *w, float eps, int rows, int dim,
                          float *part, float *dw, hipStream_t s, void *dx_bf16 = nullptr);
+// The weight-gradient half alone (launch_ln_bwd with dw null leaves it out):
+// dw += the column sums of the per-block partials in part, in a fixed order.
+hipError_t launch_ln_bwd_colsum(float *part, int rows, int dim, float *dw, hipStream_t s);
 hipError_t launch_add(float *dst, const float *src, size_t n, hipStream_t s);
 hipError_t launch_embed_bwd(const float *dE, const int *order, const int *seg_start, const int *seg_id, int nseg,
                             int dim, float *gtok, hipStream_t s);

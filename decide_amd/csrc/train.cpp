@@ -227,7 +227,10 @@ int backward_impl(dn_ctx *c, const float *dlogits) {
   HIPCHK(c, "hipMalloc", ensure(tr.part, 4 * std::max((size_t)16 * std::max({(size_t)3 * H * H, (size_t)2 * I * H,
                                                                              (size_t)H * I}),
                                                         (size_t)4 * T * std::max(H, I))));
-  HIPCHK(c, "hipMalloc", ensure(tr.lnpart, 4 * (size_t)ln_bwd_blocks(std::max(T, R)) * H));
+  // LayerNorm weight-gradient partials: one slot per (layer parity, norm);
+  // their column sums run on the weight-gradient stream.
+  const size_t lnslot = (size_t)ln_bwd_blocks(std::max(T, R)) * H;
+  HIPCHK(c, "hipMalloc", ensure(tr.lnpart, 4 * 4 * lnslot));
   HIPCHK(c, "hipMalloc", ensure(tr.dl, 4 * (size_t)std::max(R, 1)));
   HIPCHK(c, "hipMalloc", ensure(tr.contrib, 4 * (size_t)std::max(R, 1) * 5 * H));
   for (int l = tr.train_from; l < L; l++) {
@@ -268,9 +271,10 @@ int backward_impl(dn_ctx *c, const float *dlogits) {
       if (ev) HIPCHK(c, "hipEventRecord", hipEventRecord(ev[2 * k + end], st));
       return DN_OK;
     };
-    // This parity's gradient buffers are free once the weight-gradient stream
-    // has transposed layer l+2's; that stream alone writes the arenas after
-    // the top layer (whose arena write is ordered by the records at entry).
+    // This parity's gradient buffers and LayerNorm partials are free once
+    // the weight-gradient stream has read layer l+2's; that stream alone
+    // writes the arenas after the top layer (whose arena write is ordered by
+    // the records at entry).
     HIPCHK(c, "hipStreamWaitEvent", hipStreamWaitEvent(s, tr.ev_trans[par], 0));
     char *arena = (char *)tr.opT[par].p;
     size_t row0 = 0;
@@ -311,10 +315,11 @@ int backward_impl(dn_ctx *c, const float *dlogits) {
       HIPCHK(c, "geglu_bwd", launch_geglu_bwd(prec, dact, S.wi.p, dwi, T, I, s));
     }
     RC(b.gemm(EPI_F32, T, H, 2 * I, dwi, 2 * I, wt(p + "mlp.Wi.weight"), 2 * I, dn2, H));
+    float *lnp_mlp = lnpart + (size_t)(2 * par) * lnslot, *lnp_attn = lnp_mlp + lnslot;
     HIPCHK(c, "ln_bwd(mlp_norm)", launch_ln_bwd(dh1, dcur, dn2, (const float *)S.h1.p, nullptr,
                                                 (const float *)S.mean2.p, (const float *)S.rstd2.p,
-                                                (const float *)W(c, p + "mlp_norm.weight"), g.eps, T, H, lnpart,
-                                                grad(p + "mlp_norm.weight"), s, bf ? tr.dop_h1.p : nullptr));
+                                                (const float *)W(c, p + "mlp_norm.weight"), g.eps, T, H, lnp_mlp,
+                                                nullptr, s, bf ? tr.dop_h1.p : nullptr));
 
     // Attention: h1 = in + Wo(ctx)
     const void *dh1_op = bf ? tr.dop_h1.p : (const void *)dh1;
@@ -356,8 +361,8 @@ int backward_impl(dn_ctx *c, const float *dlogits) {
     if (l > 0) {
       HIPCHK(c, "ln_bwd(attn_norm)", launch_ln_bwd(dprev, dh1, dn1, (const float *)S.hs.p, nullptr,
                                                    (const float *)S.mean1.p, (const float *)S.rstd1.p,
-                                                   (const float *)W(c, p + "attn_norm.weight"), g.eps, T, H, lnpart,
-                                                   grad(p + "attn_norm.weight"), s, bf ? tr.dop_out.p : nullptr));
+                                                   (const float *)W(c, p + "attn_norm.weight"), g.eps, T, H, lnp_attn,
+                                                   nullptr, s, bf ? tr.dop_out.p : nullptr));
     } else {
       HIPCHK(c, "hipMemcpyAsync", hipMemcpyAsync(dprev, dh1, 4 * TH, hipMemcpyDeviceToDevice, s));
       HIPCHK(c, "add", launch_add(dprev, dn1, TH, s));
@@ -366,12 +371,16 @@ int backward_impl(dn_ctx *c, const float *dlogits) {
     // layer's input-gradient chain.
     HIPCHK(c, "hipEventRecord", hipEventRecord(tr.ev_ready[par], s));
     HIPCHK(c, "hipStreamWaitEvent", hipStreamWaitEvent(tr.side, tr.ev_ready[par], 0));
-    // The gradients' transposes (their buffers alternate by layer parity;
-    // dout's is released by ev_trans), then the saved activations'.
+    // The gradients' transposes and the LayerNorm weight gradients (their
+    // buffers alternate by layer parity; ev_trans releases them and dout),
+    // then the saved activations' transposes.
     if (!top) RC(b.transpose(0, dcur, H, doutT, nullptr, tr.side));
     RC(b.transpose(prec, dwi, 2 * I, dwiT, nullptr, tr.side));
     RC(b.transpose(0, dh1, H, dh1T, nullptr, tr.side));
     RC(b.transpose(prec, dqkv, 3 * H, dqkvT, nullptr, tr.side));
+    HIPCHK(c, "colsum(mlp_norm)", launch_ln_bwd_colsum(lnp_mlp, T, H, grad(p + "mlp_norm.weight"), tr.side));
+    if (l > 0)
+      HIPCHK(c, "colsum(attn_norm)", launch_ln_bwd_colsum(lnp_attn, T, H, grad(p + "attn_norm.weight"), tr.side));
     HIPCHK(c, "hipEventRecord", hipEventRecord(tr.ev_trans[par], tr.side));
     RC(b.transpose(prec, S.act.p, I, actT, nullptr, tr.side));
     RC(b.transpose(prec, S.n2.p, H, n2T, nullptr, tr.side));
