@@ -168,7 +168,7 @@ hipError_t launch_gemm(int precision, int epi, const GemmArgs &a, hipStream_t s)
 // Whether launch_gemm takes this epilogue at M rows (EPI_GEGLU_BWD needs the
 // tiled kernel: M > 128 in bf16, M > 1024 in fp32).
 bool gemm_epi_ok(int precision, int epi, int M);
-// Split-K fp32-output GEMM: `splits` partial products, each over a.K / splits
+// Split-K fp32-output GEMM: `splits` (1..16) partial products, each over a.K / splits
 // of K (a.K % (splits * 64) == 0), written to partial + split * M * N
 // (row-major, ldc = N), then summed in split order into C (M x N, ldc = N;
 // added to C when a.accumulate, else stored). partial holds splits * M * N floats.

@@ -647,20 +647,33 @@ hipError_t launch_skinny(int epi, const GemmArgs &a, hipStream_t s) {
   return launch_skinny_cfg<T, 2, 1, 8>(epi, a, s);
 }
 
-// C (+)= sum over splits of part[s * n + i], in split order.
+// C (+)= sum over splits of part[s * n + i], in split order; four
+// consecutive elements per thread (n % 4 == 0), every split's load issued
+// before the sum.
 __global__ void splitk_reduce_kernel(const float *part, int splits, size_t n, float *C, int accumulate) {
-  const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const size_t i = ((size_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
   if (i >= n) return;
-  float acc = 0.0f;
-  for (int s = 0; s < splits; s++) acc += part[(size_t)s * n + i];
-  C[i] = accumulate ? C[i] + acc : acc;
+  constexpr int MAXS = 16;
+  float4 p[MAXS];
+#pragma unroll
+  for (int s = 0; s < MAXS; s++)
+    if (s < splits) p[s] = *(const float4 *)(part + (size_t)s * n + i);
+  float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+  for (int s = 0; s < MAXS; s++)
+    if (s < splits) acc = make_float4(acc.x + p[s].x, acc.y + p[s].y, acc.z + p[s].z, acc.w + p[s].w);
+  if (accumulate) {
+    const float4 c = *(const float4 *)(C + i);
+    acc = make_float4(c.x + acc.x, c.y + acc.y, c.z + acc.z, c.w + acc.w);
+  }
+  *(float4 *)(C + i) = acc;
 }
 
 }  // namespace
 
 hipError_t launch_gemm_splitk(int precision, const GemmArgs &a0, int splits, float *partial, hipStream_t s) {
   if (a0.M <= 0) return hipSuccess;
-  if (splits < 1 || a0.K % (splits * 64) != 0 || a0.N % 128 != 0) return hipErrorInvalidValue;
+  if (splits < 1 || splits > 16 || a0.K % (splits * 64) != 0 || a0.N % 128 != 0) return hipErrorInvalidValue;
   GemmArgs a = a0;
   a.K = a0.K / splits;
   a.C = partial;
@@ -674,8 +687,8 @@ hipError_t launch_gemm_splitk(int precision, const GemmArgs &a0, int splits, flo
                                 : launch_cfg<float, 128, 128, 128, 3, 1>(EPI_F32, a, s, splits);
   if (e != hipSuccess) return e;
   const size_t n = (size_t)a0.M * a0.N;
-  hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, partial, splits, n,
-                     (float *)a0.C, a0.accumulate);
+  hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)((n / 4 + 255) / 256)), dim3(256), 0, s, partial, splits,
+                     n, (float *)a0.C, a0.accumulate);
   return hipGetLastError();
 }
 
