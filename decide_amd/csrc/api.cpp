@@ -79,7 +79,7 @@ void release_train(TrainState &tr) {
   DevBuf *bufs[] = {&tr.dcur, &tr.dprev, &tr.dh1[0], &tr.dh1[1], &tr.dact, &tr.dwi[0], &tr.dwi[1], &tr.dn2,
                     &tr.dctx, &tr.dqkv[0], &tr.dqkv[1], &tr.dn1, &tr.dop_out, &tr.dop_h1, &tr.dsum, &tr.part,
                     &tr.lnpart, &tr.dE, &tr.dl, &tr.contrib, &tr.emb_order, &tr.emb_seg, &tr.emb_id, &tr.sq_part,
-                    &tr.sq_out, &tr.opT[0], &tr.opT[1], &tr.emb_mean, &tr.emb_rstd};
+                    &tr.sq_out, &tr.opT[0], &tr.opT[1], &tr.emb_mean, &tr.emb_rstd, &tr.mt};
   if (tr.side) (void)hipStreamSynchronize(tr.side);
   for (DevBuf *b : bufs) release(*b);
   for (int i = 0; i < 2; i++) {

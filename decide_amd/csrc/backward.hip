@@ -488,11 +488,29 @@ __global__ void head_param_kernel(HeadBwdArgs a, float *g_outw, float *g_normw, 
 // ---------------------------------------------------------------------------
 // Sum of squares in float64: block partials (fixed grid), then one sum in
 // partial order.
-__global__ __launch_bounds__(256) void sumsq_kernel(const float *x, size_t n, double *part) {
+// The table entry owning workgroup b: the last one whose first workgroup
+// (field FIRST) is <= b (binary search; the table is in ascending order).
+template <int MTensor::*FIRST>
+__device__ __forceinline__ int mt_find(const MTensor *t, int nt, int b) {
+  int lo = 0, hi = nt - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (t[mid].*FIRST <= b) lo = mid;
+    else hi = mid - 1;
+  }
+  return lo;
+}
+
+// Partial j of a tensor: the f64 sum of g^2 over i = 256*j + thread, strided
+// by 256*nparts, threads then waves in a fixed order.
+__global__ __launch_bounds__(256) void sumsq_multi_kernel(const MTensor *tab, int nt, double *part) {
   __shared__ double red[4];
+  const int ti = mt_find<&MTensor::first_part>(tab, nt, blockIdx.x);
+  const MTensor &t = tab[ti];
+  const int j = blockIdx.x - t.first_part;
   double s = 0;
-  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) {
-    const double v = (double)x[i];
+  for (size_t i = (size_t)j * 256 + threadIdx.x; i < t.n; i += (size_t)t.nparts * 256) {
+    const double v = (double)t.g[i];
     s += v * v;
   }
   s = wave_sum_d(s);
@@ -500,6 +518,12 @@ __global__ __launch_bounds__(256) void sumsq_kernel(const float *x, size_t n, do
   if (lane == 0) red[wave] = s;
   __syncthreads();
   if (threadIdx.x == 0) part[blockIdx.x] = red[0] + red[1] + red[2] + red[3];
+}
+
+__global__ __launch_bounds__(256) void zero_multi_kernel(const MTensor *tab, int nt) {
+  const MTensor &t = tab[mt_find<&MTensor::first_chunk>(tab, nt, blockIdx.x)];
+  const size_t k0 = (size_t)(blockIdx.x - t.first_chunk) * MT_CHUNK;
+  for (size_t k = k0 + threadIdx.x; k < t.n && k < k0 + MT_CHUNK; k += 256) t.g[k] = 0.0f;
 }
 
 // One block of 256 threads: strided per-thread sums, then the 256 sums in a
@@ -520,11 +544,15 @@ __global__ __launch_bounds__(256) void sum_doubles_kernel(const double *part, in
 // AdamW (Update, optim.go:118-141), written unfused as the reference
 // evaluates it. With wq (bf16 projections) the new weight is also stored in
 // the operand copy, rounded to nearest even.
-__global__ void adamw_kernel(float *p, const float *g, float *m, float *v, size_t n, float lr, float wd, float b1,
-                             float b2, float eps, float scale, float step_size, float inv_sqrt_b2c, bf16 *wq) {
-  const size_t k = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (k >= n) return;
-  {
+__global__ __launch_bounds__(256) void adamw_multi_kernel(const MTensor *tab, int nt, float b1, float b2, float eps,
+                                                          float scale, float step_size, float inv_sqrt_b2c) {
+  const MTensor &t = tab[mt_find<&MTensor::first_chunk>(tab, nt, blockIdx.x)];
+  const size_t k0 = (size_t)(blockIdx.x - t.first_chunk) * MT_CHUNK;
+  float *p = t.p, *m = t.m, *v = t.v;
+  const float *g = t.g;
+  bf16 *wq = t.wq;
+  const float lr = t.rate, wd = t.wd;
+  for (size_t k = k0 + threadIdx.x; k < t.n && k < k0 + MT_CHUNK; k += 256) {
 #pragma clang fp contract(off)
     const float gr = g[k] * scale;
     const float mk = b1 * m[k] + (1 - b1) * gr;
@@ -677,9 +705,15 @@ hipError_t launch_head_bwd(const float *h, const int *row_tok, const float *s1, 
 
 int sumsq_blocks(size_t n) { return (int)std::max<size_t>(1, std::min<size_t>(256, (n + 4095) / 4096)); }
 
-hipError_t launch_sumsq(const float *x, size_t n, double *part, hipStream_t s) {
-  if (n == 0) return hipSuccess;
-  hipLaunchKernelGGL(sumsq_kernel, dim3(sumsq_blocks(n)), dim3(256), 0, s, x, n, part);
+hipError_t launch_sumsq_multi(const MTensor *t, int nt, int total_parts, double *part, hipStream_t s) {
+  if (nt <= 0 || total_parts <= 0) return hipSuccess;
+  hipLaunchKernelGGL(sumsq_multi_kernel, dim3(total_parts), dim3(256), 0, s, t, nt, part);
+  return hipGetLastError();
+}
+
+hipError_t launch_zero_multi(const MTensor *t, int nt, int total_chunks, hipStream_t s) {
+  if (nt <= 0 || total_chunks <= 0) return hipSuccess;
+  hipLaunchKernelGGL(zero_multi_kernel, dim3(total_chunks), dim3(256), 0, s, t, nt);
   return hipGetLastError();
 }
 
@@ -688,11 +722,11 @@ hipError_t launch_sum_doubles(const double *part, int n, double *out, hipStream_
   return hipGetLastError();
 }
 
-hipError_t launch_adamw(float *p, const float *g, float *m, float *v, size_t n, float lr, float wd, float b1, float b2,
-                        float eps, float scale, float step_size, float inv_sqrt_b2c, void *wq_bf16, hipStream_t s) {
-  if (n == 0) return hipSuccess;
-  hipLaunchKernelGGL(adamw_kernel, dim3(blocks(n)), dim3(256), 0, s, p, g, m, v, n, lr, wd, b1, b2, eps, scale,
-                     step_size, inv_sqrt_b2c, (bf16 *)wq_bf16);
+hipError_t launch_adamw_multi(const MTensor *t, int nt, int total_chunks, float b1, float b2, float eps, float scale,
+                              float step_size, float inv_sqrt_b2c, hipStream_t s) {
+  if (nt <= 0 || total_chunks <= 0) return hipSuccess;
+  hipLaunchKernelGGL(adamw_multi_kernel, dim3(total_chunks), dim3(256), 0, s, t, nt, b1, b2, eps, scale, step_size,
+                     inv_sqrt_b2c);
   return hipGetLastError();
 }
 

@@ -279,9 +279,27 @@ hipError_t launch_embed_bwd(const float *dE, const int *order, const int *seg_st
 hipError_t launch_head_bwd(const float *h, const int *row_tok, const float *s1, const float *d, const float *dlogits,
                            int R, int H, float eps, const float *const *w, float *dcur, float *contrib,
                            float *const *g, hipStream_t s);
+// Optimizer work over many tensors in one launch: a device table of the
+// tensors, each owning a run of consecutive workgroups.
+struct MTensor {
+  float *p;        // fp32 parameters (the master copy of a bf16 projection)
+  float *g, *m, *v;
+  bf16 *wq;        // bf16 operand copy to refresh, or null
+  size_t n;
+  float rate, wd;  // learning rate; decoupled weight decay (times the rate), 0 if none
+  int first_chunk; // first workgroup of the elementwise kernels (MT_CHUNK elements each)
+  int first_part;  // first workgroup / partial of the sum of squares
+  int nparts;      // sumsq_blocks(n)
+};
+constexpr int MT_CHUNK = 4096;
 int sumsq_blocks(size_t n);
-hipError_t launch_sumsq(const float *x, size_t n, double *part, hipStream_t s);
+inline int mt_chunks(size_t n) { return (int)((n + MT_CHUNK - 1) / MT_CHUNK); }
+// part[first_part + j] = the j-th of nparts strided partial sums of g^2 (f64), per tensor.
+hipError_t launch_sumsq_multi(const MTensor *t, int nt, int total_parts, double *part, hipStream_t s);
 hipError_t launch_sum_doubles(const double *part, int n, double *out, hipStream_t s);
-hipError_t launch_adamw(float *p, const float *g, float *m, float *v, size_t n, float lr, float wd, float b1, float b2,
-                        float eps, float scale, float step_size, float inv_sqrt_b2c, void *wq_bf16, hipStream_t s);
+// g = 0 over every tensor of the table.
+hipError_t launch_zero_multi(const MTensor *t, int nt, int total_chunks, hipStream_t s);
+// AdamW (optim.go:118-141) over every tensor of the table.
+hipError_t launch_adamw_multi(const MTensor *t, int nt, int total_chunks, float b1, float b2, float eps, float scale,
+                              float step_size, float inv_sqrt_b2c, hipStream_t s);
 hipError_t launch_widen_bf16(const void *src, float *dst, size_t n, hipStream_t s);

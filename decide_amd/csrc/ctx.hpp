@@ -69,6 +69,8 @@ struct TrainState {
   DevBuf dcur, dprev, dh1[2], dact, dwi[2], dn2, dctx, dqkv[2], dn1, dop_out, dop_h1, dsum, part, lnpart, dE, dl,
       contrib;
   DevBuf emb_order, emb_seg, emb_id, sq_part, sq_out;
+  DevBuf mt;                        // optimizer tensor table (device copy of mt_host)
+  std::vector<MTensor> mt_host;
   // Weight-gradient GEMMs run on a second stream: per layer parity, the
   // transposed operands of the layer's four GEMMs, and the events that order
   // them against the main stream (operands ready / arena free again).

@@ -525,14 +525,53 @@ int dn_backward(dn_ctx *c, const float *dlogits, int nrows) {
   return backward_impl(c, dlogits);
 }
 
+// Uploads the optimizer table: every trainable tensor (or, with all, every
+// tensor that has a gradient), in the model's tensor order, with its workgroup
+// ranges; AdamW's rate and weight decay (optim.go:118-141) are filled in
+// when given. The host copy stays alive until the caller's synchronize.
+int mt_upload(dn_ctx *c, bool all, float lr, float head_lr, float weight_decay, int *nt, int *chunks, int *parts) {
+  TrainState &tr = c->tr;
+  tr.mt_host.clear();
+  int nc = 0, np = 0;
+  for (auto &kv : c->w) {
+    TensorSlot &t = kv.second;
+    if (all ? !t.train.grad.p : frozen(tr, kv.first)) continue;
+    MTensor e{};
+    e.p = param(c, t);
+    e.g = (float *)t.train.grad.p;
+    e.m = (float *)t.train.m.p;
+    e.v = (float *)t.train.v.p;
+    e.wq = bf16_slot(c, t) ? (bf16 *)t.buf.p : nullptr;
+    e.n = (size_t)t.n;
+    const bool head = kv.first.rfind("scorer.", 0) == 0;
+    e.rate = head ? head_lr : lr;
+    const bool decay = t.rank == 2 && kv.first != kTok;
+    e.wd = decay ? weight_decay * e.rate : 0.0f;
+    e.first_chunk = nc;
+    e.first_part = np;
+    e.nparts = sumsq_blocks(e.n);
+    nc += mt_chunks(e.n);
+    np += e.nparts;
+    tr.mt_host.push_back(e);
+  }
+  *nt = (int)tr.mt_host.size();
+  *chunks = nc;
+  *parts = np;
+  if (tr.mt_host.empty()) return DN_OK;
+  const size_t bytes = sizeof(MTensor) * tr.mt_host.size();
+  HIPCHK(c, "hipMalloc", ensure(tr.mt, bytes));
+  HIPCHK(c, "hipMemcpyAsync", hipMemcpyAsync(tr.mt.p, tr.mt_host.data(), bytes, hipMemcpyHostToDevice, c->stream));
+  return DN_OK;
+}
+
 int dn_zero_grad(dn_ctx *c) {
   if (!c) return DN_INVALID_ARG;
   c->err.clear();
   (void)hipSetDevice(c->device);
-  for (auto &kv : c->w)
-    if (kv.second.train.grad.p)
-      HIPCHK(c, "hipMemsetAsync",
-             hipMemsetAsync(kv.second.train.grad.p, 0, sizeof(float) * kv.second.n, c->stream));
+  int nt = 0, chunks = 0, parts = 0;
+  int rc = mt_upload(c, true, 0.0f, 0.0f, 0.0f, &nt, &chunks, &parts);
+  if (rc) return rc;
+  HIPCHK(c, "zero_grad", launch_zero_multi((const MTensor *)c->tr.mt.p, nt, chunks, c->stream));
   HIPCHK(c, "hipStreamSynchronize", hipStreamSynchronize(c->stream));
   return DN_OK;
 }
@@ -545,20 +584,15 @@ int dn_grad_sumsq(dn_ctx *c, double *out) {
   (void)hipSetDevice(c->device);
   rc = ensure_param_state(c);
   if (rc) return rc;
-  size_t nparts = 0;
-  for (auto &kv : c->w)
-    if (!frozen(c->tr, kv.first)) nparts += sumsq_blocks(kv.second.n);
   TrainState &tr = c->tr;
-  HIPCHK(c, "hipMalloc", ensure(tr.sq_part, sizeof(double) * std::max<size_t>(nparts, 1)));
+  int nt = 0, chunks = 0, nparts = 0;
+  rc = mt_upload(c, false, 0.0f, 0.0f, 0.0f, &nt, &chunks, &nparts);
+  if (rc) return rc;
+  HIPCHK(c, "hipMalloc", ensure(tr.sq_part, sizeof(double) * std::max(nparts, 1)));
   HIPCHK(c, "hipMalloc", ensure(tr.sq_out, sizeof(double)));
-  size_t off = 0;
-  for (auto &kv : c->w) {
-    if (frozen(tr, kv.first)) continue;
-    HIPCHK(c, "sumsq", launch_sumsq((const float *)kv.second.train.grad.p, kv.second.n,
-                                    (double *)tr.sq_part.p + off, c->stream));
-    off += sumsq_blocks(kv.second.n);
-  }
-  HIPCHK(c, "sum", launch_sum_doubles((const double *)tr.sq_part.p, (int)off, (double *)tr.sq_out.p, c->stream));
+  if (nparts == 0) HIPCHK(c, "hipMemsetAsync", hipMemsetAsync(tr.sq_part.p, 0, sizeof(double), c->stream));
+  HIPCHK(c, "sumsq", launch_sumsq_multi((const MTensor *)tr.mt.p, nt, nparts, (double *)tr.sq_part.p, c->stream));
+  HIPCHK(c, "sum", launch_sum_doubles((const double *)tr.sq_part.p, nparts, (double *)tr.sq_out.p, c->stream));
   HIPCHK(c, "hipMemcpyAsync", hipMemcpyAsync(out, tr.sq_out.p, sizeof(double), hipMemcpyDeviceToHost, c->stream));
   HIPCHK(c, "hipStreamSynchronize", hipStreamSynchronize(c->stream));
   return DN_OK;
@@ -578,18 +612,13 @@ int dn_adamw_step(dn_ctx *c, float lr, float head_lr, float weight_decay, float 
   const double b1c = 1 - std::pow((double)b1, (double)tr.adam_step);
   const double b2c = 1 - std::pow((double)b2, (double)tr.adam_step);
   const float step_size = (float)(1 / b1c), inv_sqrt_b2c = (float)(1 / std::sqrt(b2c));
-  for (auto &kv : c->w) {
-    if (frozen(tr, kv.first)) continue;
-    TensorSlot &t = kv.second;
-    const bool head = kv.first.rfind("scorer.", 0) == 0;
-    const float rate = head ? head_lr : lr;
-    const bool decay = t.rank == 2 && kv.first != kTok;
-    const float wd = decay ? weight_decay * rate : 0.0f;
-    HIPCHK(c, "adamw", launch_adamw(param(c, t), (const float *)t.train.grad.p, (float *)t.train.m.p,
-                                    (float *)t.train.v.p, t.n, rate, wd, b1, b2, eps, grad_scale, step_size,
-                                    inv_sqrt_b2c, bf16_slot(c, t) ? t.buf.p : nullptr, c->stream));
-    t.train.wt_valid = false;
-  }
+  int nt = 0, chunks = 0, parts = 0;
+  rc = mt_upload(c, false, lr, head_lr, weight_decay, &nt, &chunks, &parts);
+  if (rc) return rc;
+  HIPCHK(c, "adamw", launch_adamw_multi((const MTensor *)tr.mt.p, nt, chunks, b1, b2, eps, grad_scale, step_size,
+                                        inv_sqrt_b2c, c->stream));
+  for (auto &kv : c->w)
+    if (!frozen(tr, kv.first)) kv.second.train.wt_valid = false;
   HIPCHK(c, "hipStreamSynchronize", hipStreamSynchronize(c->stream));
   return DN_OK;
 }
