@@ -8,6 +8,7 @@
 #include <cstring>
 #include <map>
 #include <string>
+#include <utility>
 #include <vector>
 
 #include "ctx.hpp"
@@ -891,6 +892,15 @@ int dn_set_probe(dn_ctx *c, int layer) {
   c->probe_layer = layer;
   c->probe_used = 0;
   c->probe_bwd_used = 0;
+  // Events for the next kProbeForwards forwards and backwards are created
+  // here, so that the calls being timed create none (more grow on demand).
+  constexpr size_t kProbeForwards = 128;
+  for (auto pool : {std::make_pair(&c->probe_pool, (size_t)10), std::make_pair(&c->probe_bwd_pool, (size_t)6)})
+    while (layer >= 0 && pool.first->size() < kProbeForwards * pool.second) {
+      hipEvent_t e;
+      HIPCHK(c, "hipEventCreate", hipEventCreate(&e));
+      pool.first->push_back(e);
+    }
   return DN_OK;
 }
 

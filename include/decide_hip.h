@@ -157,7 +157,8 @@ int dn_synchronize(dn_ctx *ctx);
  * records HIP events on the context's stream around the five per-layer
  * launches of encoder layer `layer` (DN_PROBE_* order). dn_read_probe
  * synchronises, adds each launch's duration to ms[5] and the number of
- * forwards seen to *count, and resets the probe. layer < 0 disables it.
+ * forwards seen to *count, and resets the probe. layer < 0 disables it;
+ * layer >= 0 creates the events of the next 128 forwards and backwards at once.
  * No counterpart in the reference (its tests time whole calls,
  * internal/cuda/gemm_test.go:141-181). */
 enum { DN_PROBE_QKV = 0, DN_PROBE_ATTENTION = 1, DN_PROBE_WO = 2, DN_PROBE_WI = 3, DN_PROBE_MLPWO = 4 };
