@@ -731,10 +731,24 @@ hipError_t launch_gemm(int precision, int epi, const GemmArgs &a0, hipStream_t s
   //    stalls overlap the other's MFMAs;
   //  * fp32 residual epilogue (N = 768) and the GeGLU backward (training):
   //    128 x 128, 64-byte stages x 3 (48 KB), three workgroups per CU.
+  //  * medium M (the trainer's micro-batches: a few thousand rows) has too
+  //    few large tiles to fill 256 CUs: up to 4096 rows the fp32 and the
+  //    narrow (N <= 1024) store epilogues take 64 x 128 tiles and the wide
+  //    store 128 x 128; the GeGLU epilogues keep 128 x 128 up to 8192 rows
+  //    (isolated launches on the training shapes, 3840 rows: Wi + GeGLU 36.4
+  //    -> 31.3 us, dX GEMMs N = 768 K = 2304 32.3 -> 30.4 us, dctx 16.0 ->
+  //    12.6 us).
   const bool small = a.M <= 1024;
   if (precision == 1) {
     if (small) return launch_cfg<bf16, 64, 128, 128, 4, 1>(epi, a, s);
-    if (epi == EPI_F32 || epi == EPI_GEGLU_BWD) return launch_cfg<bf16, 128, 128, 64, 3, 3>(epi, a, s);
+    const bool medium = a.M <= 4096;
+    if (epi == EPI_F32 || (epi == EPI_STORE && a.N <= 1024 && a.M <= 16384)) {
+      if (medium) return launch_cfg<bf16, 64, 128, 128, 4, 1>(epi, a, s);
+      return launch_cfg<bf16, 128, 128, 64, 3, 3>(epi, a, s);
+    }
+    if (epi == EPI_GEGLU_BWD || (epi == EPI_STORE && medium) ||
+        ((epi == EPI_GEGLU || epi == EPI_GEGLU_KEEP) && a.M <= 8192))
+      return launch_cfg<bf16, 128, 128, 64, 3, 3>(epi, a, s);
     return launch_cfg<bf16, 256, 128, 64, 3, 2>(epi, a, s);
   }
   if (small) return launch_cfg<float, 64, 128, 128, 4, 1>(epi, a, s);
