@@ -683,7 +683,9 @@ hipError_t launch_gemm_splitk(int precision, const GemmArgs &a0, int splits, flo
   a.c_split = (size_t)a0.M * a0.N;
   a.ngroups = 1;
   a.order = 1;  // row-major tile order: the grid is (tiles, splits)
-  hipError_t e = precision == 1 ? launch_cfg<bf16, 128, 128, 64, 3, 3>(EPI_F32, a, s, splits)
+  // bf16: 64 x 128 tiles with 128-byte K stages (the long-K weight-gradient
+  // shapes run best on them, unsplit or lightly split).
+  hipError_t e = precision == 1 ? launch_cfg<bf16, 64, 128, 128, 4, 1>(EPI_F32, a, s, splits)
                                 : launch_cfg<float, 128, 128, 128, 3, 1>(EPI_F32, a, s, splits);
   if (e != hipSuccess) return e;
   const size_t n = (size_t)a0.M * a0.N;
