@@ -58,11 +58,9 @@ __global__ __launch_bounds__(256) void transpose_kernel(const TI *src, int rows,
 // The same with 8-element vectors (16 bytes of bf16, 32 of fp32) on both
 // sides: needs cols, lds and ldt multiples of 8 and rows_pad a multiple of 64.
 template <class TI, class TO>
-__global__ __launch_bounds__(256) void transpose8_kernel(const TI *src, int rows, int cols, int lds, TO *dstT,
-                                                         int ldt, int rows_pad, TO *copy) {
-  __shared__ float tile[64][65];
+__device__ __forceinline__ void transpose8_tile(float (&tile)[64][65], const TI *src, int rows, int cols, int lds,
+                                                TO *dstT, int ldt, int rows_pad, TO *copy, int c0, int r0) {
   const int tid = threadIdx.x;
-  const int c0 = blockIdx.x * 64, r0 = blockIdx.y * 64;
 #pragma unroll
   for (int j = 0; j < 2; j++) {
     const int it = tid + 256 * j, r = it >> 3, cg = (it & 7) * 8;
@@ -84,6 +82,33 @@ __global__ __launch_bounds__(256) void transpose8_kernel(const TI *src, int rows
     for (int u = 0; u < 8; u++) v[u] = tile[rg + u][c];
     Vec8<TO>::store(dstT + (size_t)(c0 + c) * ldt + r0 + rg, v);
   }
+}
+
+template <class TI, class TO>
+__global__ __launch_bounds__(256) void transpose8_kernel(const TI *src, int rows, int cols, int lds, TO *dstT,
+                                                         int ldt, int rows_pad, TO *copy) {
+  __shared__ float tile[64][65];
+  transpose8_tile<TI, TO>(tile, src, rows, cols, lds, dstT, ldt, rows_pad, copy, blockIdx.x * 64, blockIdx.y * 64);
+}
+
+// Several transposes in one launch (TransposeBatch): each job owns a run of
+// (cols/64) x (rows_pad/64) consecutive blocks; its input is fp32 or bf16.
+template <class TO>
+__global__ __launch_bounds__(256) void transpose8_batch_kernel(TransposeBatch b) {
+  __shared__ float tile[64][65];
+  int e = 0;
+#pragma unroll
+  for (int i = 1; i < TB_MAX; i++)
+    if (i < b.n && (int)blockIdx.x >= b.job[i].first_block) e = i;
+  const TransposeJob &J = b.job[e];
+  const int blk = blockIdx.x - J.first_block, nbx = J.cols / 64;
+  const int c0 = (blk % nbx) * 64, r0 = (blk / nbx) * 64;
+  if (J.f32_in)
+    transpose8_tile<float, TO>(tile, (const float *)J.src, b.rows, J.cols, J.cols, (TO *)J.dst, b.ldt, b.rows_pad,
+                               (TO *)nullptr, c0, r0);
+  else
+    transpose8_tile<bf16, TO>(tile, (const bf16 *)J.src, b.rows, J.cols, J.cols, (TO *)J.dst, b.ldt, b.rows_pad,
+                              (TO *)nullptr, c0, r0);
 }
 
 // GeGLU on the stored Wi output (rows interleaved in 64-column groups: 32
@@ -223,7 +248,10 @@ __global__ __launch_bounds__(256) void ln_bwd_kernel(float *dx, const float *res
 // lane, then the 4 waves in order) into part2[y][col]; colsum_final_kernel
 // adds the NG partial rows, in order, into out.
 constexpr int COLSUM_NG = 16;
-__global__ __launch_bounds__(256) void colsum_kernel(const float *part, int nparts, int n, float *part2) {
+__global__ __launch_bounds__(256) void colsum_kernel(const float *part_a, const float *part_b, int nparts, int n,
+                                                     float *part2_a, float *part2_b) {
+  const float *part = blockIdx.z ? part_b : part_a;
+  float *part2 = blockIdx.z ? part2_b : part2_a;
   __shared__ float red[4][64];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int c = blockIdx.x * 64 + lane;
@@ -243,7 +271,9 @@ __global__ __launch_bounds__(256) void colsum_kernel(const float *part, int npar
   if (wave == 0 && c < n) part2[(size_t)blockIdx.y * n + c] = ((red[0][lane] + red[1][lane]) + red[2][lane]) + red[3][lane];
 }
 
-__global__ void colsum_final_kernel(const float *part2, int n, float *out) {
+__global__ void colsum_final_kernel(const float *part2_a, const float *part2_b, int n, float *out_a, float *out_b) {
+  const float *part2 = blockIdx.y ? part2_b : part2_a;
+  float *out = blockIdx.y ? out_b : out_a;
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n) return;
   float acc = 0.0f;
@@ -575,6 +605,24 @@ inline unsigned blocks(size_t n, int per = 256) { return (unsigned)((n + per - 1
 
 }  // namespace
 
+hipError_t launch_transpose_batch(const TransposeBatch &b0, int precision_out, hipStream_t s) {
+  if (b0.n <= 0 || b0.rows_pad <= 0) return hipSuccess;
+  if (b0.n > TB_MAX || b0.rows_pad % 64 || b0.ldt % 8) return hipErrorInvalidValue;
+  TransposeBatch b = b0;
+  int blocks_total = 0;
+  for (int i = 0; i < b.n; i++) {
+    if (b.job[i].cols <= 0 || b.job[i].cols % 64) return hipErrorInvalidValue;
+    if (!b.job[i].f32_in && precision_out != 1) return hipErrorInvalidValue;
+    b.job[i].first_block = blocks_total;
+    blocks_total += (b.job[i].cols / 64) * (b.rows_pad / 64);
+  }
+  if (precision_out == 1)
+    hipLaunchKernelGGL(transpose8_batch_kernel<bf16>, dim3(blocks_total), dim3(256), 0, s, b);
+  else
+    hipLaunchKernelGGL(transpose8_batch_kernel<float>, dim3(blocks_total), dim3(256), 0, s, b);
+  return hipGetLastError();
+}
+
 hipError_t launch_transpose(int precision_in, int precision_out, const void *src, int rows, int cols, int lds,
                             void *dstT, int ldt, int rows_pad, void *copy, hipStream_t s) {
   if (rows_pad <= 0 || cols <= 0) return hipSuccess;
@@ -662,14 +710,18 @@ hipError_t launch_ln_bwd(float *dx, const float *res, const float *dy, const flo
   return launch_ln_bwd_colsum(part, rows, dim, dw, s);
 }
 
-hipError_t launch_ln_bwd_colsum(float *part, int rows, int dim, float *dw, hipStream_t s) {
+hipError_t launch_ln_bwd_colsum(float *part, int rows, int dim, float *dw, hipStream_t s, float *part_b,
+                                float *dw_b) {
   if (rows <= 0) return hipSuccess;
   const int nb = ln_bwd_blocks(rows) - COLSUM_NG;
-  float *part2 = part + (size_t)nb * dim;
-  hipLaunchKernelGGL(colsum_kernel, dim3((dim + 63) / 64, COLSUM_NG), dim3(256), 0, s, part, nb, dim, part2);
+  const int two = part_b && dw_b ? 2 : 1;
+  float *part2 = part + (size_t)nb * dim, *part2_b = two == 2 ? part_b + (size_t)nb * dim : part2;
+  hipLaunchKernelGGL(colsum_kernel, dim3((dim + 63) / 64, COLSUM_NG, two), dim3(256), 0, s, part,
+                     two == 2 ? part_b : part, nb, dim, part2, part2_b);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  hipLaunchKernelGGL(colsum_final_kernel, dim3(blocks(dim)), dim3(256), 0, s, part2, dim, dw);
+  hipLaunchKernelGGL(colsum_final_kernel, dim3(blocks(dim), two), dim3(256), 0, s, part2, part2_b, dim, dw,
+                     two == 2 ? dw_b : dw);
   return hipGetLastError();
 }
 

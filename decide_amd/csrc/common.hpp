@@ -256,6 +256,20 @@ hipError_t launch_pack(const float *src, int trans, int rows, int cols, int ld, 
 // Training kernels (backward.hip). Precision codes: 0 fp32, 1 bf16.
 hipError_t launch_transpose(int precision_in, int precision_out, const void *src, int rows, int cols, int lds,
                             void *dstT, int ldt, int rows_pad, void *copy, hipStream_t s);
+// Up to TB_MAX transposes dst[cols x ldt] = src[rows x cols]^T (zero for rows
+// .. rows_pad) in one launch; each src is fp32 or (bf16 output only) bf16,
+// cols a multiple of 64, rows_pad of 64. first_block is set by the launcher.
+constexpr int TB_MAX = 4;
+struct TransposeJob {
+  const void *src;
+  void *dst;
+  int cols, f32_in, first_block;
+};
+struct TransposeBatch {
+  TransposeJob job[TB_MAX];
+  int n, rows, rows_pad, ldt;
+};
+hipError_t launch_transpose_batch(const TransposeBatch &b, int precision_out, hipStream_t s);
 hipError_t launch_geglu_fwd(int precision, const void *wi, void *act, int rows, int I, hipStream_t s);
 hipError_t launch_geglu_bwd(int precision, const float *dact, const void *wi, void *dwi, int rows, int I,
                             hipStream_t s);
@@ -269,7 +283,9 @@ hipError_t launch_ln_bwd(float *dx, const float *res, const float *dy, const flo
                          float *part, float *dw, hipStream_t s, void *dx_bf16 = nullptr);
 // The weight-gradient half alone (launch_ln_bwd with dw null leaves it out):
 // dw += the column sums of the per-block partials in part, in a fixed order.
-hipError_t launch_ln_bwd_colsum(float *part, int rows, int dim, float *dw, hipStream_t s);
+// With part_b and dw_b, a second norm's partials and gradient in the same launches.
+hipError_t launch_ln_bwd_colsum(float *part, int rows, int dim, float *dw, hipStream_t s, float *part_b = nullptr,
+                                float *dw_b = nullptr);
 hipError_t launch_add(float *dst, const float *src, size_t n, hipStream_t s);
 hipError_t launch_embed_bwd(const float *dE, const int *order, const int *seg_start, const int *seg_id, int nseg,
                             int dim, float *gtok, hipStream_t s);

@@ -21,6 +21,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstring>
+#include <initializer_list>
 #include <numeric>
 #include <string>
 #include <vector>
@@ -107,6 +108,12 @@ int split_count(int prec, int M, int N, int Tp) {
   return s;
 }
 
+#define RCX(expr)         \
+  do {                    \
+    int rcx_ = (expr);    \
+    if (rcx_) return rcx_; \
+  } while (0)
+
 struct Bwd {
   dn_ctx *c;
   int prec, T, Tp, H, I, heads;
@@ -156,6 +163,29 @@ struct Bwd {
   // copy, also the operand-type copy of an fp32 src.
   int transpose(int prec_in, const void *src, int cols, void *dst, void *copy = nullptr, hipStream_t ts = nullptr) {
     HIPCHK(c, "transpose", launch_transpose(prec_in, prec, src, T, cols, cols, dst, Tp, Tp, copy, ts ? ts : s));
+    return DN_OK;
+  }
+  // Several such transposes {prec_in, src, cols, dst} in one launch when
+  // every width is a multiple of 64, else one launch each.
+  struct Job {
+    int prec_in;
+    const void *src;
+    int cols;
+    void *dst;
+  };
+  int transposes(std::initializer_list<Job> jobs, hipStream_t ts) {
+    bool batch = jobs.size() <= (size_t)TB_MAX;
+    for (const Job &j : jobs) batch = batch && j.cols % 64 == 0;
+    if (!batch) {
+      for (const Job &j : jobs) RCX(transpose(j.prec_in, j.src, j.cols, j.dst, nullptr, ts));
+      return DN_OK;
+    }
+    TransposeBatch tb{};
+    for (const Job &j : jobs) tb.job[tb.n++] = TransposeJob{j.src, j.dst, j.cols, j.prec_in == 0 ? 1 : 0, 0};
+    tb.rows = T;
+    tb.rows_pad = Tp;
+    tb.ldt = Tp;
+    HIPCHK(c, "transpose(batch)", launch_transpose_batch(tb, prec, ts));
     return DN_OK;
   }
 };
@@ -375,18 +405,17 @@ int backward_impl(dn_ctx *c, const float *dlogits) {
     // The gradients' transposes and the LayerNorm weight gradients (their
     // buffers alternate by layer parity; ev_trans releases them and dout),
     // then the saved activations' transposes.
-    if (!top) RC(b.transpose(0, dcur, H, doutT, nullptr, tr.side));
-    RC(b.transpose(prec, dwi, 2 * I, dwiT, nullptr, tr.side));
-    RC(b.transpose(0, dh1, H, dh1T, nullptr, tr.side));
-    RC(b.transpose(prec, dqkv, 3 * H, dqkvT, nullptr, tr.side));
-    HIPCHK(c, "colsum(mlp_norm)", launch_ln_bwd_colsum(lnp_mlp, T, H, grad(p + "mlp_norm.weight"), tr.side));
-    if (l > 0)
-      HIPCHK(c, "colsum(attn_norm)", launch_ln_bwd_colsum(lnp_attn, T, H, grad(p + "attn_norm.weight"), tr.side));
+    if (top)
+      RC(b.transposes({{prec, dwi, 2 * I, dwiT}, {0, dh1, H, dh1T}, {prec, dqkv, 3 * H, dqkvT}}, tr.side));
+    else
+      RC(b.transposes({{0, dcur, H, doutT}, {prec, dwi, 2 * I, dwiT}, {0, dh1, H, dh1T}, {prec, dqkv, 3 * H, dqkvT}},
+                      tr.side));
+    HIPCHK(c, "colsum(norms)", launch_ln_bwd_colsum(lnp_mlp, T, H, grad(p + "mlp_norm.weight"), tr.side,
+                                                    l > 0 ? lnp_attn : nullptr,
+                                                    l > 0 ? grad(p + "attn_norm.weight") : nullptr));
     HIPCHK(c, "hipEventRecord", hipEventRecord(tr.ev_trans[par], tr.side));
-    RC(b.transpose(prec, S.act.p, I, actT, nullptr, tr.side));
-    RC(b.transpose(prec, S.n2.p, H, n2T, nullptr, tr.side));
-    RC(b.transpose(prec, S.ctx.p, H, ctxT, nullptr, tr.side));
-    RC(b.transpose(prec, S.n1.p, H, n1T, nullptr, tr.side));
+    RC(b.transposes(
+        {{prec, S.act.p, I, actT}, {prec, S.n2.p, H, n2T}, {prec, S.ctx.p, H, ctxT}, {prec, S.n1.p, H, n1T}}, tr.side));
     RC(b.wgrad(H, I, doutT, actT, grad(p + "mlp.Wo.weight"), tr.side));
     RC(b.wgrad(2 * I, H, dwiT, n2T, grad(p + "mlp.Wi.weight"), tr.side));
     RC(b.wgrad(H, H, dh1T, ctxT, grad(p + "attn.Wo.weight"), tr.side));
