@@ -294,22 +294,29 @@ __global__ __launch_bounds__(64 * WGM * WGN) __attribute__((amdgpu_waves_per_eu(
     constexpr int BATCH = ITER < 8 ? ITER : 8;
     static_assert(ITER % BATCH == 0, "epilogue batching");
     const bool vec = (g.ldc & 3) == 0;
+    // Residual loads of a batch are issued before its stores (C is read and
+    // written here, so the compiler would otherwise serialise each pair); the
+    // first batch of each pass is loaded before that pass's staging barrier
+    // (the previous pass's stores cover other rows), so its latency overlaps
+    // the staging.
+    float4 old[BATCH];
+    auto load_old = [&](int pass, int b0) {
+#pragma unroll
+      for (int u = 0; u < BATCH; u++) {
+        const int c = tid + (b0 + u) * NT, r = c / V, c4 = (c % V) * 4;
+        const int row = m0 + pass * HM + r, col = n0 + c4;
+        old[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (g.accumulate && vec && row < g.M && col + 4 <= g.n_store)
+          old[u] = *(const float4 *)(R + (size_t)row * g.ldc + col);
+      }
+    };
+    load_old(0, 0);
 #pragma unroll
     for (int pass = 0; pass < WGM; pass++) {
       stage_f32(st, LD, pass);
       __syncthreads();
-      // All loads of a batch are issued before its stores (C is read and
-      // written here, so the compiler would otherwise serialise each pair).
       for (int b0 = 0; b0 < ITER; b0 += BATCH) {
-        float4 old[BATCH];
-#pragma unroll
-        for (int u = 0; u < BATCH; u++) {
-          const int c = tid + (b0 + u) * NT, r = c / V, c4 = (c % V) * 4;
-          const int row = m0 + pass * HM + r, col = n0 + c4;
-          old[u] = make_float4(0.f, 0.f, 0.f, 0.f);
-          if (g.accumulate && vec && row < g.M && col + 4 <= g.n_store)
-            old[u] = *(const float4 *)(R + (size_t)row * g.ldc + col);
-        }
+        if (b0 > 0) load_old(pass, b0);
 #pragma unroll
         for (int u = 0; u < BATCH; u++) {
           const int c = tid + (b0 + u) * NT, r = c / V, c4 = (c % V) * 4;
@@ -326,7 +333,10 @@ __global__ __launch_bounds__(64 * WGM * WGN) __attribute__((amdgpu_waves_per_eu(
           }
         }
       }
-      if (pass + 1 < WGM) __syncthreads();
+      if (pass + 1 < WGM) {
+        load_old(pass + 1, 0);
+        __syncthreads();
+      }
     }
   } else {
     // Operand-type epilogue: the plain product (gated false) or the GeGLU of
