@@ -291,7 +291,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) __attribute__((amdgpu_waves_per_eu(
     const float *R = g.res ? g.res : C;  // residual input of the accumulate
     constexpr int V = BN / 4;  // float4 per row
     constexpr int ITER = HM * V / NT;
-    constexpr int BATCH = ITER < 8 ? ITER : 8;
+    constexpr int BATCH = ITER <= 8 ? ITER : ITER % 8 == 0 ? 8 : ITER % 6 == 0 ? 6 : 4;
     static_assert(ITER % BATCH == 0, "epilogue batching");
     const bool vec = (g.ldc & 3) == 0;
     // Residual loads of a batch are issued before its stores (C is read and
@@ -413,6 +413,16 @@ hipError_t launch_cfg(int epi, const GemmArgs &a, hipStream_t s, int splits = 1)
       hipLaunchKernelGGL((gemm_nt_kernel<T, BM, BN, RB, NSTAGE, EPI_GEGLU_KEEP, WPE, WGM, WGN>), grid, block, 0, s, a);
       break;
   }
+  return hipGetLastError();
+}
+
+// The fp32 epilogue alone, for tiles whose wave columns (BN / 2 = 96) do not
+// pair up for the operand-type epilogues.
+template <class T, int BM, int BN, int RB, int NSTAGE, int WPE>
+hipError_t launch_cfg_f32(const GemmArgs &a, hipStream_t s, int splits = 1) {
+  const int tiles = ((a.M + BM - 1) / BM) * (a.N / BN);
+  hipLaunchKernelGGL((gemm_nt_kernel<T, BM, BN, RB, NSTAGE, EPI_F32, WPE, 2, 2>), dim3(tiles, splits), dim3(256), 0, s,
+                     a);
   return hipGetLastError();
 }
 
@@ -754,6 +764,14 @@ hipError_t launch_gemm(int precision, int epi, const GemmArgs &a0, hipStream_t s
   if (precision == 1) {
     if (small) return launch_cfg<bf16, 64, 128, 128, 4, 1>(epi, a, s);
     const bool medium = a.M <= 4096;
+    if (epi == EPI_F32 && a.N % 192 == 0 && a.M <= 16384) {
+      // 768-wide outputs in 192-column tiles: 3,840 rows make 240 tiles of
+      // 64 x 192 for 256 CUs where 64 x 128 made 360 (dX GEMM N = 768,
+      // K = 2304: 30.6 -> 24.2 us isolated; Wo 16.2 -> 12.7 us); up to
+      // 16384 rows 128 x 192 at two workgroups per CU.
+      if (medium) return launch_cfg_f32<bf16, 64, 192, 128, 4, 1>(a, s);
+      return launch_cfg_f32<bf16, 128, 192, 64, 3, 2>(a, s);
+    }
     if (epi == EPI_F32 || (epi == EPI_STORE && a.N <= 1024 && a.M <= 16384)) {
       if (medium) return launch_cfg<bf16, 64, 128, 128, 4, 1>(epi, a, s);
       return launch_cfg<bf16, 128, 128, 64, 3, 3>(epi, a, s);

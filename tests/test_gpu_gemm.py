@@ -98,12 +98,14 @@ def test_gemm_cfg1(eng):
     assert ratio <= 1.0 and rel <= 1e-5
 
 
-@pytest.mark.parametrize("M", [64, 112, 1000, 2048])
-def test_gemm_bf16_device(eng, M):
-    """bf16 operands, fp32 accumulate: against float64 of the same bf16 values."""
+@pytest.mark.parametrize("M,N,K", [(64, 2304, 768), (112, 2304, 768), (1000, 2304, 768), (2048, 2304, 768),
+                                   (3000, 768, 2304), (5000, 768, 1152)])
+def test_gemm_bf16_device(eng, M, N, K):
+    """bf16 operands, fp32 accumulate: against float64 of the same bf16 values.
+    Shapes cover every tile config of the fp32 epilogue: whole-K small-M,
+    64 x 128, 64 x 192 and 128 x 192 (ragged last row tiles)."""
     import torch
 
-    N, K = 2304, 768
     g = torch.Generator().manual_seed(M)
     A = torch.randn(M, K, generator=g).to(torch.bfloat16)
     B = (torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16)
