@@ -751,8 +751,10 @@ hipError_t launch_gemm(int precision, int epi, const GemmArgs &a0, hipStream_t s
   //  * paired / store epilogues (N = 2304): 256 x 128, 64-byte stages x 3
   //    (72 KB LDS), two workgroups per CU so one tile's epilogue and DMA
   //    stalls overlap the other's MFMAs;
-  //  * fp32 residual epilogue (N = 768) and the GeGLU backward (training):
-  //    128 x 128, 64-byte stages x 3 (48 KB), three workgroups per CU.
+  //  * fp32 epilogue with N a multiple of 192 (the 768-wide Wo / MlpWo and
+  //    dX GEMMs): 192-column tiles (below); other fp32 outputs and the GeGLU
+  //    backward (training): 128 x 128, 64-byte stages x 3 (48 KB), three
+  //    workgroups per CU.
   //  * medium M (the trainer's micro-batches: a few thousand rows) has too
   //    few large tiles to fill 256 CUs: up to 4096 rows the fp32 and the
   //    narrow (N <= 1024) store epilogues take 64 x 128 tiles and the wide
@@ -764,11 +766,12 @@ hipError_t launch_gemm(int precision, int epi, const GemmArgs &a0, hipStream_t s
   if (precision == 1) {
     if (small) return launch_cfg<bf16, 64, 128, 128, 4, 1>(epi, a, s);
     const bool medium = a.M <= 4096;
-    if (epi == EPI_F32 && a.N % 192 == 0 && a.M <= 16384) {
+    if (epi == EPI_F32 && a.N % 192 == 0) {
       // 768-wide outputs in 192-column tiles: 3,840 rows make 240 tiles of
       // 64 x 192 for 256 CUs where 64 x 128 made 360 (dX GEMM N = 768,
-      // K = 2304: 30.6 -> 24.2 us isolated; Wo 16.2 -> 12.7 us); up to
-      // 16384 rows 128 x 192 at two workgroups per CU.
+      // K = 2304: 30.6 -> 24.2 us isolated; Wo 16.2 -> 12.7 us); above 4096
+      // rows 128 x 192 at two workgroups per CU (cfg3's 32768 rows: 1024
+      // tiles, two full rounds of 512; forward 2.52 -> 2.56M tokens/s).
       if (medium) return launch_cfg_f32<bf16, 64, 192, 128, 4, 1>(a, s);
       return launch_cfg_f32<bf16, 128, 192, 64, 3, 2>(a, s);
     }
