@@ -244,7 +244,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) __attribute__((amdgpu_waves_per_eu(
     // interleaved layout, so the tile's outputs are 2*BN contiguous columns.
     constexpr int LD = BN + 4, HM = WM, U = BN / 8;
     constexpr int ITER = HM * U / NT;
-    constexpr int BATCH = ITER < 4 ? ITER : 4;
+    constexpr int BATCH = ITER <= 4 ? ITER : ITER % 4 == 0 ? 4 : ITER % 3 == 0 ? 3 : 2;
     static_assert(ITER * NT == HM * U && ITER % BATCH == 0, "GeGLU backward epilogue shape");
     float *st = (float *)smem;
     const T *Wg = (const T *)g.gin;
@@ -416,13 +416,13 @@ hipError_t launch_cfg(int epi, const GemmArgs &a, hipStream_t s, int splits = 1)
   return hipGetLastError();
 }
 
-// The fp32 epilogue alone, for tiles whose wave columns (BN / 2 = 96) do not
-// pair up for the operand-type epilogues.
-template <class T, int BM, int BN, int RB, int NSTAGE, int WPE>
-hipError_t launch_cfg_f32(const GemmArgs &a, hipStream_t s, int splits = 1) {
+// One epilogue alone (the fp32 one or the GeGLU backward), for tiles whose
+// wave columns (BN / 2 = 96) do not pair up for the operand-type epilogues.
+template <class T, int BM, int BN, int RB, int NSTAGE, int WPE, int EPI = EPI_F32>
+hipError_t launch_cfg_one(const GemmArgs &a, hipStream_t s, int splits = 1) {
+  static_assert(EPI == EPI_F32 || EPI == EPI_GEGLU_BWD, "epilogues that take 96-column wave tiles");
   const int tiles = ((a.M + BM - 1) / BM) * (a.N / BN);
-  hipLaunchKernelGGL((gemm_nt_kernel<T, BM, BN, RB, NSTAGE, EPI_F32, WPE, 2, 2>), dim3(tiles, splits), dim3(256), 0, s,
-                     a);
+  hipLaunchKernelGGL((gemm_nt_kernel<T, BM, BN, RB, NSTAGE, EPI, WPE, 2, 2>), dim3(tiles, splits), dim3(256), 0, s, a);
   return hipGetLastError();
 }
 
@@ -772,9 +772,13 @@ hipError_t launch_gemm(int precision, int epi, const GemmArgs &a0, hipStream_t s
       // K = 2304: 30.6 -> 24.2 us isolated; Wo 16.2 -> 12.7 us); above 4096
       // rows 128 x 192 at two workgroups per CU (cfg3's 32768 rows: 1024
       // tiles, two full rounds of 512; forward 2.52 -> 2.56M tokens/s).
-      if (medium) return launch_cfg_f32<bf16, 64, 192, 128, 4, 1>(a, s);
-      return launch_cfg_f32<bf16, 128, 192, 64, 3, 2>(a, s);
+      if (medium) return launch_cfg_one<bf16, 64, 192, 128, 4, 1>(a, s);
+      return launch_cfg_one<bf16, 128, 192, 64, 3, 2>(a, s);
     }
+    // GeGLU backward (N = 1152) at medium M: 64 x 192 at two workgroups per
+    // CU (3840 rows: 30.2 -> 25.8 us isolated).
+    if (epi == EPI_GEGLU_BWD && medium && a.N % 192 == 0)
+      return launch_cfg_one<bf16, 64, 192, 64, 4, 2, EPI_GEGLU_BWD>(a, s);
     if (epi == EPI_F32 || (epi == EPI_STORE && a.N <= 1024 && a.M <= 16384)) {
       if (medium) return launch_cfg<bf16, 64, 128, 128, 4, 1>(epi, a, s);
       return launch_cfg<bf16, 128, 128, 64, 3, 3>(epi, a, s);

@@ -295,6 +295,29 @@ def test_backward_matches_oracle_modernbert_base(prec):
         check_grads(eng, want, prec, label="base")
 
 
+@pytest.mark.parametrize("prec", ["fp32", "bf16"])
+def test_backward_matches_oracle_medium_rows(prec):
+    """ModernBERT-base at a trainer-like micro-batch of 4 examples x 384
+    tokens (1,536 rows): the medium-M GEMM tiles (64 x 192 for the 768-wide
+    fp32 outputs and the GeGLU backward, 128 x 128 stores) against the
+    oracle."""
+    from decide_amd import modernbert_base
+    from decide_amd.nn import MASK_ID, build_sequence
+    from decide_amd.synth import pack_request
+    from decide_amd.train import TrainEngine
+
+    cfg = modernbert_base()
+    w = weights_for(cfg, seed=13, std=0.02)
+    rng = np.random.default_rng(14)
+    batch = [build_sequence(pack_request(rng, 256, [16] * 8, cfg.vocab), MASK_ID, True) for _ in range(4)]
+    print(f"case: modernbert-base backward {prec}, T={sum(len(s.ids) for s in batch)}", flush=True)
+    _, dl, want = oracle_grads(cfg, effective_weights(w, prec), batch)
+    with TrainEngine(cfg, w, precision=prec) as eng:
+        eng.forward(batch)
+        eng.backward(dl)
+        check_grads(eng, want, prec, label="medium")
+
+
 def test_backward_full_size_deterministic_and_linear():
     """At the trainer's micro-batch size (10 examples x 384 tokens under the
     4000-token budget, ModernBERT-base, bf16, embeddings trained): a second
