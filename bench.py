@@ -273,8 +273,8 @@ def train_bench(args) -> int:
     probe, nprobe = eng.read_probe_backward()
     eng.set_probe(-1)
     # Roofline kernel: layer 1's QKV weight-gradient GEMM (dWqkv += dqkv^T . n1,
-    # 2 * 2304 * 768 flop per token; 2304 x 768 output in 64 x 128 tiles, which
-    # is enough tiles to run unsplit over the tokens), timed with HIP events on
+    # 2 * 2304 * 768 flop per token; 2304 x 768 output in 64 x 192 tiles, run
+    # unsplit over the tokens), timed with HIP events on
     # the weight-gradient stream; it shares the GPU with the main stream's
     # kernels while it runs.
     qkv_flop = 2.0 * (3 * H) * H * sum(len(s.ids) for s in ex) * args.steps
@@ -304,8 +304,8 @@ def train_bench(args) -> int:
         "loss_first_last": [round(losses[0], 5), round(losses[-1], 5)],
         "backward_probe_ms_per_launch": {k: round(v / max(nprobe, 1), 5) for k, v in probe.items()},
         "dgrad_qkv_tflops": round(qkv_flop / dg_s / 1e12, 2) if dg_s > 0 else None,
-        "roofline": {"kernel": "gemm_nt_kernel<bf16,64,128,128,4,EPI_F32> accumulating into the gradient (one "
-                               "split: 216 tiles): layer 1 dWqkv (weight-gradient stream, concurrent with the main "
+        "roofline": {"kernel": "gemm_nt_kernel<bf16,64,192,128,4,EPI_F32> accumulating into the gradient (one "
+                               "split: 144 tiles): layer 1 dWqkv (weight-gradient stream, concurrent with the main "
                                "stream)",
                      "bound": "mfma", "achieved": round(qkv_flop / wg_s / 1e12, 2) if wg_s > 0 else None,
                      "peak": PEAK[args.precision] / 1e12, "unit": "TFLOP/s",
