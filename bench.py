@@ -563,6 +563,21 @@ def main() -> int:
                 "unit": "TFLOP/s", "frac": round(wi_flop / wi_s / PEAK[prec], 4)}
     gemm_ms = avg["gemm_qkv"] + avg["gemm_wo"] + avg["gemm_wi"] + avg["gemm_mlpwo"]
     gemm_tflops = PROJ_FLOP_PER_TOKEN_LAYER * T / (gemm_ms * 1e-3) / 1e12
+    # The kernel with the largest share of GPU time at cfg3 is the fp32
+    # residual GEMM (Wo and MlpWo share its symbol): reported beside the Wi
+    # line against both roofs. Algorithmic bytes per launch: A, the weights,
+    # and the fp32 residual read and written (T x H each way).
+    res_view = None
+    if not hbm_bound and avg["gemm_wo"] > 0 and avg["gemm_mlpwo"] > 0:
+        res_s = (avg["gemm_wo"] + avg["gemm_mlpwo"]) * 1e-3
+        res_bytes = esz * (T * H + H * H) + esz * (T * I + H * I) + 2 * 2 * 4 * T * H
+        res_flop = 2.0 * T * H * (H + I)
+        res_view = {"kernel": "gemm_nt_kernel, EPI_F32 (Wo and MlpWo + fp32 residual), layer %d" % args.probe_layer,
+                    "hbm_achieved_GBps": round(res_bytes / res_s / 1e9, 1),
+                    "hbm_frac": round(res_bytes / res_s / 8e12, 4),
+                    "mfma_achieved_TFLOPs": round(res_flop / res_s / 1e12, 2),
+                    "mfma_frac": round(res_flop / res_s / PEAK[prec], 4),
+                    "algorithmic_bytes_per_pair": res_bytes, "flop_per_pair": res_flop}
     result = {
         "metric": METRIC,
         "value": round(value, 1),
@@ -589,6 +604,8 @@ def main() -> int:
                                     % ("gemm_skinny_kernel" if hbm_bound else "gemm_nt_kernel", args.probe_layer)},
                          **roof, traffic=traffic, flop_per_launch=wi_flop, algorithmic_bytes_per_launch=wi_bytes),
     }
+    if res_view:
+        result["roofline_residual_gemms"] = res_view
     if not args.no_cpu_baseline:
         log("cpu baseline")
         result["cpu_baseline"] = cpu_baseline(cfg, weights, args.config, args.cpu_budget)
