@@ -155,9 +155,7 @@ struct GemmArgs {
   void *C2;         // EPI_GEGLU_KEEP: the GeGLU output (ldc2), C receives the plain product
   int ldc2;
   const void *gin;  // EPI_GEGLU_BWD: the GeGLU input (the Wi output, M x 2N, row stride ldc)
-  int kvalid;
 };
-hipError_t launch_gemm_mn(const GemmArgs &a, int splits, float *partial, hipStream_t s);
 
 // GEMM epilogues: fp32 store / accumulate, store in the operand type, GeGLU of
 // value/gate column pairs, and (training) both the plain product and its

@@ -75,8 +75,7 @@ struct TileOrder {
 };
 
 // WGM x WGN waves tile the BM x BN block; each wave owns a WM x WN sub-tile.
-__device__ __forceinline__ int mn_swz(int row) { return ((row >> 1) & 1) << 2; }
-template <class T, int BM, int BN, int RB, int NSTAGE, int EPI, int WPE, int WGM, int WGN, bool MN = false>
+template <class T, int BM, int BN, int RB, int NSTAGE, int EPI, int WPE, int WGM, int WGN>
 __global__ __launch_bounds__(64 * WGM * WGN) __attribute__((amdgpu_waves_per_eu(WPE))) void gemm_nt_kernel(GemmArgs g) {
   using MF = Mfma<T>;
   typedef typename MF::frag frag;
@@ -115,43 +114,21 @@ __global__ __launch_bounds__(64 * WGM * WGN) __attribute__((amdgpu_waves_per_eu(
   // lane l writes row RPI*(wave+NW*i) + l/CPR, LDS chunk slot l%CPR, which
   // holds the row's logical 16-byte chunk (l%CPR) ^ swz(row).
   const char *src[LOADS];
-  int krow[MN ? LOADS : 1], kld[MN ? LOADS : 1];
 #pragma unroll
   for (int i = 0; i < LOADS; i++) {
     const int r = RPI * (wave + NW * i) + lane / CPR;
-    if constexpr (MN) {
-      const int rr = r < BM ? r : r - BM;
-      const int c = (lane % CPR) ^ mn_swz(rr);
-      if (r < BM) {
-        src[i] = (const char *)g.A + (size_t)(m0 + 8 * c) * sizeof(T);
-        krow[i] = r;
-        kld[i] = g.lda;
-      } else {
-        src[i] = (const char *)g.B + (size_t)(n0 + 64 * (rr >> 6) + 8 * c) * sizeof(T);
-        krow[i] = rr & 63;
-        kld[i] = g.ldb;
-      }
-    } else {
-      const int c = (lane % CPR) ^ swz<RB>(r);
-      if (r < BM)
-        src[i] = (const char *)gA + (size_t)min(m0 + r, g.M - 1) * g.lda * sizeof(T) + c * 16;
-      else
-        src[i] = (const char *)gB + (size_t)(n0 + r - BM) * g.ldb * sizeof(T) + c * 16;
-    }
+    const int c = (lane % CPR) ^ swz<RB>(r);
+    if (r < BM)
+      src[i] = (const char *)gA + (size_t)min(m0 + r, g.M - 1) * g.lda * sizeof(T) + c * 16;
+    else
+      src[i] = (const char *)gB + (size_t)(n0 + r - BM) * g.ldb * sizeof(T) + c * 16;
   }
   auto issue_part = [&](int stage, int k0, int i0, int i1) {
     char *dst = smem + stage * STAGE + wave * 1024;
     const size_t kb = (size_t)k0 * sizeof(T);
 #pragma unroll
-    for (int i = i0; i < i1; i++) {
-      if constexpr (MN) {
-        const size_t k = (size_t)min((int)koff + k0 + krow[i], g.kvalid - 1);
-        __builtin_amdgcn_global_load_lds((gbl_void *)(src[i] + k * kld[i] * sizeof(T)),
-                                         (lds_void *)(dst + i * NW * 1024), 16, 0, 0);
-      } else {
-        __builtin_amdgcn_global_load_lds((gbl_void *)(src[i] + kb), (lds_void *)(dst + i * NW * 1024), 16, 0, 0);
-      }
-    }
+    for (int i = i0; i < i1; i++)
+      __builtin_amdgcn_global_load_lds((gbl_void *)(src[i] + kb), (lds_void *)(dst + i * NW * 1024), 16, 0, 0);
   };
   auto issue = [&](int stage, int k0) { issue_part(stage, k0, 0, LOADS); };
 
@@ -184,36 +161,6 @@ __global__ __launch_bounds__(64 * WGM * WGN) __attribute__((amdgpu_waves_per_eu(
   auto load_frags = [&](int buf, int stage, int ks) {
     const char *sa = smem + stage * STAGE;
     const char *sb = sa + BM * RB;
-    if constexpr (MN) {
-      typedef short s4 __attribute__((ext_vector_type(4)));
-      typedef short s8 __attribute__((ext_vector_type(8)));
-      const int g16 = lane >> 4, q = lane & 15;
-      const int kk = ks * 16 + 8 * (g16 >> 1);
-      auto tr = [&](const char *p) {
-        s4 r;
-        asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(r) : "v"((unsigned)(size_t)(__attribute__((address_space(3))) const char *)p));
-        return r;
-      };
-
-      auto at = [](const char *part, int row, int col) {
-        const int b = col * 2;
-        return part + row * 128 + (((b >> 4) ^ mn_swz(row)) << 4) + (b & 15);
-      };
-      const int kr = kk + (q >> 2);
-#pragma unroll
-      for (int i = 0; i < TM; i++) {
-        const int col = wm * WM + i * 32 + 16 * (g16 & 1) + 4 * (q & 3);
-        const s8 v = __builtin_shufflevector(tr(at(sa, kr, col)), tr(at(sa, kr + 4, col)), 0, 1, 2, 3, 4, 5, 6, 7);
-        fa[buf][i] = __builtin_bit_cast(frag, v);
-      }
-#pragma unroll
-      for (int j = 0; j < TN; j++) {
-        const int nb = wn * WN + j * 32 + 16 * (g16 & 1), col = nb % 64 + 4 * (q & 3), hb = 64 * (nb / 64);
-        const s8 v = __builtin_shufflevector(tr(at(sb, hb + kr, col)), tr(at(sb, hb + kr + 4, col)), 0, 1, 2, 3, 4, 5, 6, 7);
-        fb[buf][j] = __builtin_bit_cast(frag, v);
-      }
-      return;
-    }
     const int ke = ks * MF::KSTEP + lh * MF::SLOTS;  // first k element of this lane's operand
     const int chunk = ke * (int)sizeof(T) / 16, within = ke * (int)sizeof(T) % 16;
 #pragma unroll
@@ -229,21 +176,12 @@ __global__ __launch_bounds__(64 * WGM * WGN) __attribute__((amdgpu_waves_per_eu(
   };
   // Waits until stage kt has landed for every wave: NSTAGE-2 later stages'
   // loads may still be in flight.
-  auto stage_ready = [&](int kt_l) {
+  auto stage_ready = [&]() {
     wait_vmcnt<LOADS * (NSTAGE - 2)>();
     __builtin_amdgcn_s_barrier();
-    if constexpr (MN) {
-      const int first_bad = g.kvalid - (int)koff - kt_l * KT;
-      if (first_bad < KT) {
-        char *sa = smem + (kt_l % NSTAGE) * STAGE;
-        for (int ch = tid; ch < KT * CPR; ch += NT)
-          if (ch / CPR >= first_bad) *(uint4 *)(sa + ch * 16) = make_uint4(0u, 0u, 0u, 0u);
-        __syncthreads();
-      }
-    }
   };
 
-  stage_ready(0);
+  stage_ready();
   load_frags(0, 0, 0);
   for (int kt = 0; kt < nk; kt++) {
     // Refill the buffer of stage kt-1 (every wave finished reading it before
@@ -264,13 +202,6 @@ __global__ __launch_bounds__(64 * WGM * WGN) __attribute__((amdgpu_waves_per_eu(
       // B is the MFMA's first operand: acc[i][j] holds the transposed
       // 32x32 block, so lane l owns token row l%32 and four runs of four
       // consecutive output columns (vector stores in the epilogue).
-      if constexpr (MN) {
-        static_assert(TM == 1 && TN == 2, "MN waits are written for 1x2 wave tiles");
-        if (ks + 1 < NKS)
-          asm volatile("s_waitcnt lgkmcnt(6)" : "+v"(fa[cur][0]), "+v"(fb[cur][0]), "+v"(fb[cur][1]));
-        else
-          asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(fa[cur][0]), "+v"(fb[cur][0]), "+v"(fb[cur][1]));
-      }
 #pragma unroll
       for (int i = 0; i < TM; i++)
 #pragma unroll
@@ -278,12 +209,12 @@ __global__ __launch_bounds__(64 * WGM * WGN) __attribute__((amdgpu_waves_per_eu(
       // One MFMA, then all of the next step's operand reads (they get the
       // rest of the step to land), then the DMA issues, then the MFMAs.
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      if (ks + 1 < NKS) __builtin_amdgcn_sched_group_barrier(0x100, (MN ? 2 : 1) * (TM + TN), 0);
+      if (ks + 1 < NKS) __builtin_amdgcn_sched_group_barrier(0x100, TM + TN, 0);
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
       __builtin_amdgcn_sched_group_barrier(0x020, PER_KS, 0);
       __builtin_amdgcn_sched_group_barrier(0x008, TM * TN - 2, 0);
       if (ks + 1 == NKS && kt + 1 < nk) {
-        stage_ready(kt + 1);
+        stage_ready();
         load_frags(cur ^ 1, (kt + 1) % NSTAGE, 0);
       }
     }
@@ -780,22 +711,6 @@ hipError_t launch_gemm_splitk(int precision, const GemmArgs &a0, int splits, flo
   const size_t n = (size_t)a0.M * a0.N;
   hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)((n / 4 + 255) / 256)), dim3(256), 0, s, partial, splits,
                      n, (float *)a0.C, a0.accumulate);
-  return hipGetLastError();
-}
-
-hipError_t launch_gemm_mn(const GemmArgs &a0, int splits, float *partial, hipStream_t s) {
-  GemmArgs a = a0;
-  a.K = a0.K / splits;
-  a.n_store = a0.N;
-  a.ngroups = 1;
-  a.order = 1;
-  if (splits > 1) { a.C = partial; a.accumulate = 0; a.c_split = (size_t)a0.M * a0.N; }
-  const int tiles = (a.M / 64) * (a.N / 128);
-  hipLaunchKernelGGL((gemm_nt_kernel<bf16, 64, 128, 128, 4, EPI_F32, 1, 2, 2, true>), dim3(tiles, splits), dim3(256), 0, s, a);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess || splits == 1) return e;
-  const size_t n = (size_t)a0.M * a0.N;
-  hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)((n / 4 + 255) / 256)), dim3(256), 0, s, partial, splits, n, (float *)a0.C, a0.accumulate);
   return hipGetLastError();
 }
 
