@@ -165,13 +165,6 @@ struct GemmArgs {
 enum { EPI_F32 = 0, EPI_STORE = 1, EPI_GEGLU = 2, EPI_GEGLU_KEEP = 3, EPI_GEGLU_BWD = 4 };
 
 hipError_t launch_gemm(int precision, int epi, const GemmArgs &a, hipStream_t s);
-// The tiled kernels alone (launch_gemm takes the ping-pong kernel where
-// gemm_pp_ok holds, these otherwise).
-hipError_t launch_gemm_tiled(int precision, int epi, const GemmArgs &a, hipStream_t s);
-// Persistent ping-pong kernel (gemm_pp.hip): bf16, M >= 8192, the qkv store
-// and the Wi + GeGLU epilogues, N % 192 == 0.
-bool gemm_pp_ok(int precision, int epi, const GemmArgs &a);
-hipError_t launch_gemm_pp(int epi, const GemmArgs &a, hipStream_t s);
 // Whether launch_gemm takes this epilogue at M rows (EPI_GEGLU_BWD needs the
 // tiled kernel: M > 128 in bf16, M > 1024 in fp32).
 bool gemm_epi_ok(int precision, int epi, int M);

@@ -727,12 +727,6 @@ bool gemm_epi_ok(int precision, int epi, int M) {
 
 hipError_t launch_gemm(int precision, int epi, const GemmArgs &a0, hipStream_t s) {
   if (a0.M <= 0) return hipSuccess;
-  if (gemm_pp_ok(precision, epi, a0)) return launch_gemm_pp(epi, a0, s);
-  return launch_gemm_tiled(precision, epi, a0, s);
-}
-
-hipError_t launch_gemm_tiled(int precision, int epi, const GemmArgs &a0, hipStream_t s) {
-  if (a0.M <= 0) return hipSuccess;
   if (!gemm_epi_ok(precision, epi, a0.M) || (epi == EPI_GEGLU_BWD && (!a0.gin || a0.ldc % 8))) return hipErrorInvalidValue;
   // Small M goes to the whole-K kernel (grid: N/32 x M/64 workgroups). In
   // fp32 (the scorer's dense layer over all [MASK] rows, the fp32 validation
