@@ -43,6 +43,7 @@ def log(msg: str) -> None:
 
 
 def cpu_threads() -> int:
+    """Host threads of this process's CPU share (the GPU box gives each GPU 16)."""
     try:
         n = len(os.sched_getaffinity(0))
     except AttributeError:
@@ -50,14 +51,36 @@ def cpu_threads() -> int:
     return max(1, min(16, n))
 
 
-def cpu_baseline(cfg, weights, name: str, budget_s: float = 12.0):
+def host_cpu_info() -> dict:
+    """nproc, sockets and model of the host CPU (from /proc/cpuinfo)."""
+    model, sockets = "unknown", set()
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
+                k, _, v = line.partition(":")
+                k, v = k.strip(), v.strip()
+                if k == "model name" and model == "unknown":
+                    model = v
+                elif k == "physical id":
+                    sockets.add(v)
+    except OSError:
+        pass
+    try:
+        affinity = len(os.sched_getaffinity(0))
+    except AttributeError:
+        affinity = None
+    return {"model": model, "nproc": os.cpu_count(), "sockets": max(1, len(sockets)), "affinity": affinity,
+            "threads_used": cpu_threads()}
+
+
+def cpu_baseline(cfg, weights, name: str, budget_s: float = 12.0, threads: int = None):
     """The oracle (C++ restatement of the reference's Go AVX2 forward) on a
     bounded sample of the same workload: whole sequences of the workload until
     about budget_s seconds of CPU work."""
     import oracle
     from decide_amd.synth import config_batch
 
-    threads = cpu_threads()
+    threads = threads or cpu_threads()
     oracle.set_workers(threads)
     model = oracle.OracleModel(cfg, weights)
     full = config_batch(name, vocab=cfg.vocab)
@@ -69,9 +92,28 @@ def cpu_baseline(cfg, weights, name: str, budget_s: float = 12.0):
         secs += time.perf_counter() - t0
         toks += len(s.ids)
         nseq += 1
-    return {"value": toks / secs, "unit": "tokens/s", "cores": threads, "kind": "port",
+    return {"value": round(toks / secs, 2), "unit": "tokens/s", "cores": threads, "kind": "port",
             "sample": f"{nseq} sequence(s) of {name} ({toks} tokens) one forward per sequence, "
                       f"{secs:.1f} s; C++ restatement of the reference Go AVX2 path (oracle/)"}
+
+
+def cpu_gemm_cfg1(threads: int, budget_s: float = 3.0) -> dict:
+    """cfg1 on the oracle's Go-order sgemm (blas.Sgemm's blocking and job
+    queue): GFLOP/s of X[512x768] . W^T, W[2304x768] over about budget_s."""
+    import oracle
+
+    rng = np.random.default_rng(0)
+    M, N, K = 512, 2304, 768
+    X = rng.standard_normal(M * K, dtype=np.float32)
+    W = (rng.standard_normal(N * K, dtype=np.float32) * np.float32(0.02)).astype(np.float32)
+    C = np.zeros(M * N, np.float32)
+    secs, n = 0.0, 0
+    while secs < budget_s:
+        t0 = time.perf_counter()
+        oracle.sgemm(False, True, M, N, K, X, K, W, K, C, N, False, workers=threads)
+        secs += time.perf_counter() - t0
+        n += 1
+    return {"gflops": round(2.0 * M * N * K * n / secs / 1e9, 2), "threads": threads, "calls": n}
 
 
 SYSTEMONE_METRIC = ("SystemOne call: 24 questions (cfg4 mix) over a 2048-token state, answered with one "
@@ -454,14 +496,20 @@ def main() -> int:
                     help="time one SystemOne call (24 questions) batched into one forward vs one forward each")
     ap.add_argument("--train", action="store_true",
                     help="time one training step (forward, backward, AdamW) at the trainer's GPU shape")
+    ap.add_argument("--no-extra-configs", action="store_true",
+                    help="default run: skip the cfg1 / cfg2 / cfg4 / cfg5 measurements after the headline")
+    ap.add_argument("--summarize-traffic", nargs=3, metavar=("FETCH_DIR", "WRITE_DIR", "OUT_JSON"),
+                    help="write the HBM traffic summary of two rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE)")
     ap.add_argument("--token-budget", type=int, default=4000,
                     help="--train: tokens per micro-batch (the trainer's TokenBudget; 4000 is its GPU default)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
-              "(the forward shards by sequence with no collective; see DESIGN.md)", file=sys.stderr)
+              "(the forward shards by sequence with no collective on the hot path)", file=sys.stderr)
         return 2
 
+    if args.summarize_traffic:
+        return summarize_traffic(*args.summarize_traffic)
     if args.tokenizer:
         return tokenizer_bench(args)
     if args.systemone:
@@ -472,32 +520,16 @@ def main() -> int:
     import torch
 
     from decide_amd import Engine, modernbert_base
-    from decide_amd.nn import flatten, row_tokens
-    from decide_amd.synth import config_batch, random_weights
+    from decide_amd.synth import random_weights
 
     cfg = modernbert_base()
     log("generating weights")
     weights = random_weights(cfg, seed=0)
-    batch = config_batch(args.config, vocab=cfg.vocab)
-    seq_len, ids, pos, opt, nmask, _ = flatten(batch)
-    T, R = int(seq_len.sum()), int(nmask.sum())
-    log(f"workload {args.config}: {len(batch)} sequences, T={T}, R={R}")
-
     torch.cuda.init()
     dev = torch.device("cuda:0")
     eng = Engine(cfg, weights, precision=args.precision)
     stream = torch.cuda.current_stream()
     eng.set_stream(stream.cuda_stream)
-    d_ids = torch.from_numpy(ids).to(dev)
-    d_pos = torch.from_numpy(pos).to(dev)
-    d_opt = torch.from_numpy(opt).to(dev)
-    d_rt = torch.from_numpy(row_tokens(batch)).to(dev)
-    d_out = torch.zeros(R, dtype=torch.float32, device=dev)
-    torch.cuda.synchronize()
-
-    def step():
-        eng.forward_device(seq_len, d_ids.data_ptr(), d_pos.data_ptr(), d_opt.data_ptr(), R, d_rt.data_ptr(),
-                           d_out.data_ptr())
 
     if args.copy_calibration:
         nbytes = args.copy_calibration << 20
@@ -509,14 +541,15 @@ def main() -> int:
         log(f"copy calibration: {nbytes} bytes read + {nbytes} bytes written")
         del src, dst
 
+    wl = Workload(eng, cfg, args.config, dev)
+    log(f"workload {args.config}: {wl.nseq} sequences, T={wl.T}, R={wl.R}")
     log(f"warmup {args.warmup}")
     for _ in range(args.warmup):
-        step()
+        wl.step()
     torch.cuda.synchronize()
     eng.check_device_errors()
 
     eng.set_probe(args.probe_layer)
-    per_step = []
     ev = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
     log(f"timing {args.steps} steps")
     quiesce_host()
@@ -524,7 +557,7 @@ def main() -> int:
     t0 = time.perf_counter()
     ev[0].record(stream)
     for k in range(args.steps):
-        step()
+        wl.step()
         ev[k + 1].record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
@@ -533,51 +566,51 @@ def main() -> int:
     eng.check_device_errors()
     per_step = [ev[k].elapsed_time(ev[k + 1]) for k in range(args.steps)]
     gpu_ms = sum(per_step)
-    ms_per_step = wall * 1e3 / args.steps
+    T = wl.T
     value = T * args.steps / wall
     avg = {k: v / max(nprobe, 1) for k, v in probe.items()}
     log("per-launch ms (layer %d): %s" % (args.probe_layer, {k: round(v, 4) for k, v in avg.items()}))
 
     prec = args.precision
-    # Roofline kernel: the Wi projection with the fused GeGLU epilogue, the
-    # largest projection GEMM (N = 2I = 2304, K = H = 768); every launch of its
-    # kernel symbol has this shape, so rocprof's per-symbol average is the
-    # per-launch duration measured here. With few tokens (cfg2, cfg5: the
-    # small-M kernel) the launch streams the weights and is bounded by HBM:
-    # achieved = algorithmic bytes (weights + activations in + out) / time.
-    wi_flop = 2.0 * T * (2 * I) * H
     esz = 2 if prec == "bf16" else 4
+    hbm_bound = T <= 128
+    attain = None
+    if prec == "bf16":
+        attain = {"changing_operands_tflops": round(eng.mfma_calibrate(0), 1),
+                  "constant_operands_tflops": round(eng.mfma_calibrate(1), 1),
+                  "method": "dn_mfma_calibrate: register-only v_mfma_f32_32x32x16_bf16 loop in the GEMMs' wave "
+                            "pattern on every CU, 2 waves per SIMD, no memory traffic; operands N(0,1) x "
+                            "N(0,0.02), rotated one lane per iteration (changing) or fixed (constant)"}
+    # Per-launch roofline views. The kernel with the largest share of GPU
+    # time at cfg3 is the fp32-residual GEMM (Wo and MlpWo share its symbol):
+    # algorithmic bytes per launch are A, the weights, and the fp32 residual
+    # read and written (T x H each way); by the roofline model it is bound by
+    # HBM (its bytes take longer at 8 TB/s than its flops at the MFMA peak).
+    res_s = (avg["gemm_wo"] + avg["gemm_mlpwo"]) * 1e-3
+    res_bytes = esz * (T * H + H * H) + esz * (T * I + H * I) + 2 * 2 * 4 * T * H
+    res_flop = 2.0 * T * H * (H + I)
+    wi_flop = 2.0 * T * (2 * I) * H
     wi_bytes = esz * (T * H + 2 * I * H + T * I)
     wi_s = avg["gemm_wi"] * 1e-3
-    hbm_bound = T <= 128
-    traffic = None
-    tpath = os.path.join(HERE, "profiles", "gemm_wi_geglu_cfg3_traffic.json")
-    if args.config == "cfg3" and prec == "bf16" and os.path.exists(tpath):
-        with open(tpath) as fh:
-            traffic = json.load(fh).get("hbm_bytes_per_launch")
+    traffic = read_traffic(args.config, prec)
     if hbm_bound:
-        roof = {"bound": "hbm", "achieved": round(wi_bytes / wi_s / 1e9, 1), "peak": 8000.0, "unit": "GB/s",
-                "frac": round(wi_bytes / wi_s / 8e12, 4)}
+        # small M (cfg2, cfg5): the skinny kernel streams the weights; the Wi
+        # launch (the largest weight matrix) is the line
+        roof = {"kernel": "gemm_skinny_kernel, EPI_GEGLU (Wi projection + fused GeGLU), layer %d" % args.probe_layer,
+                "bound": "hbm", "achieved": round(wi_bytes / wi_s / 1e9, 1), "peak": 8000.0, "unit": "GB/s",
+                "frac": round(wi_bytes / wi_s / 8e12, 4), "traffic": None,
+                "algorithmic_bytes_per_launch": wi_bytes}
     else:
-        roof = {"bound": "mfma", "achieved": round(wi_flop / wi_s / 1e12, 2), "peak": PEAK[prec] / 1e12,
-                "unit": "TFLOP/s", "frac": round(wi_flop / wi_s / PEAK[prec], 4)}
+        roof = {"kernel": "gemm_nt_kernel<bf16,128,192,64,3,EPI_F32,2,2,2> (Wo and MlpWo + fp32 residual), "
+                          "layer %d, average of its two launches" % args.probe_layer,
+                "bound": "hbm", "achieved": round(res_bytes / res_s / 1e9, 1), "peak": 8000.0, "unit": "GB/s",
+                "frac": round(res_bytes / res_s / 8e12, 4), "traffic": traffic.get("residual"),
+                "algorithmic_bytes_per_launch": res_bytes / 2,
+                "mfma_view": {"achieved_tflops": round(res_flop / res_s / 1e12, 2),
+                              "frac_of_2500": round(res_flop / res_s / PEAK[prec], 4),
+                              "flop_per_launch": res_flop / 2}}
     gemm_ms = avg["gemm_qkv"] + avg["gemm_wo"] + avg["gemm_wi"] + avg["gemm_mlpwo"]
     gemm_tflops = PROJ_FLOP_PER_TOKEN_LAYER * T / (gemm_ms * 1e-3) / 1e12
-    # The kernel with the largest share of GPU time at cfg3 is the fp32
-    # residual GEMM (Wo and MlpWo share its symbol): reported beside the Wi
-    # line against both roofs. Algorithmic bytes per launch: A, the weights,
-    # and the fp32 residual read and written (T x H each way).
-    res_view = None
-    if not hbm_bound and avg["gemm_wo"] > 0 and avg["gemm_mlpwo"] > 0:
-        res_s = (avg["gemm_wo"] + avg["gemm_mlpwo"]) * 1e-3
-        res_bytes = esz * (T * H + H * H) + esz * (T * I + H * I) + 2 * 2 * 4 * T * H
-        res_flop = 2.0 * T * H * (H + I)
-        res_view = {"kernel": "gemm_nt_kernel, EPI_F32 (Wo and MlpWo + fp32 residual), layer %d" % args.probe_layer,
-                    "hbm_achieved_GBps": round(res_bytes / res_s / 1e9, 1),
-                    "hbm_frac": round(res_bytes / res_s / 8e12, 4),
-                    "mfma_achieved_TFLOPs": round(res_flop / res_s / 1e12, 2),
-                    "mfma_frac": round(res_flop / res_s / PEAK[prec], 4),
-                    "algorithmic_bytes_per_pair": res_bytes, "flop_per_pair": res_flop}
     result = {
         "metric": METRIC,
         "value": round(value, 1),
@@ -585,32 +618,216 @@ def main() -> int:
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(ms_per_step, 4),
+        "ms_per_step": round(wall * 1e3 / args.steps, 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": prec,
         "data": "synthetic: random-init weights N(0,0.02) (InitRandom semantics, numpy PCG64 seed 0), "
                 "token ids uniform in [5,50368) minus specials, packed [CLS] premise [SEP] ([MASK] option)xK",
-        "config": {"workload": WORKLOADS[args.config], "batch": len(batch), "seq_len": int(seq_len.max()),
-                   "tokens_per_step": T, "rows_per_step": R, "layers": cfg.layers, "precision": prec},
+        "config": {"workload": WORKLOADS[args.config], "batch": wl.nseq, "seq_len": wl.max_len,
+                   "tokens_per_step": T, "rows_per_step": wl.R, "layers": cfg.layers, "precision": prec,
+                   "timed_call": "dn_forward_device (token arrays resident on the device)"},
         "gpu_ms_per_step_events": round(gpu_ms / args.steps, 4),
         "step_ms_p50": round(float(np.percentile(per_step, 50)), 4),
         "step_ms_p99": round(float(np.percentile(per_step, 99)), 4),
         "projection_gemm_tflops": round(gemm_tflops, 2),
         "projection_gemm_frac_peak": round(gemm_tflops * 1e12 / PEAK[prec], 4),
         "per_launch_ms": {k: round(v, 5) for k, v in avg.items()},
-        "roofline": dict({"kernel": "%s, EPI_GEGLU (Wi projection + fused GeGLU), layer %d"
-                                    % ("gemm_skinny_kernel" if hbm_bound else "gemm_nt_kernel", args.probe_layer)},
-                         **roof, traffic=traffic, flop_per_launch=wi_flop, algorithmic_bytes_per_launch=wi_bytes),
+        "roofline": roof,
     }
-    if res_view:
-        result["roofline_residual_gemms"] = res_view
+    if attain:
+        result["mfma_attainable"] = attain
+        result["projection_gemm_frac_attainable"] = round(gemm_tflops / attain["changing_operands_tflops"], 4)
+    if not hbm_bound:
+        result["roofline_wi_gemm"] = {
+            "kernel": "gemm_nt_kernel<bf16,256,128,64,3,EPI_GEGLU,2,2,2> (Wi projection + fused GeGLU), layer %d"
+                      % args.probe_layer,
+            "bound": "mfma", "achieved": round(wi_flop / wi_s / 1e12, 2), "peak": PEAK[prec] / 1e12,
+            "unit": "TFLOP/s", "frac": round(wi_flop / wi_s / PEAK[prec], 4), "traffic": traffic.get("wi"),
+            "flop_per_launch": wi_flop, "algorithmic_bytes_per_launch": wi_bytes}
+    # The same workload through the host-array entry point (ids/pos/opt in,
+    # logits out; PCIe copies included): never the headline value.
+    hio = []
+    for _ in range(max(3, args.steps // 4)):
+        t1 = time.perf_counter()
+        wl.host_forward()
+        hio.append(time.perf_counter() - t1)
+    result["host_io_tokens_per_s"] = round(T / float(np.median(hio)), 1)
+    if not args.no_extra_configs and args.config == "cfg3" and prec == "bf16":
+        result["configs"] = extra_configs(eng, cfg, dev, stream, args)
     if not args.no_cpu_baseline:
         log("cpu baseline")
         result["cpu_baseline"] = cpu_baseline(cfg, weights, args.config, args.cpu_budget)
+        result["cpu_baseline_1thread"] = cpu_baseline(cfg, weights, args.config, args.cpu_budget, threads=1)
+        result["host_cpu"] = host_cpu_info()
+        if "configs" in result:
+            result["configs"]["cfg1"]["oracle_sgemm"] = [cpu_gemm_cfg1(cpu_threads()), cpu_gemm_cfg1(1)]
     eng.close()
     print(json.dumps(result), flush=True)
+    return 0
+
+
+class Workload:
+    """One configuration's batch, staged on the device for dn_forward_device."""
+
+    def __init__(self, eng, cfg, name, dev):
+        import torch
+
+        from decide_amd.nn import flatten, row_tokens
+        from decide_amd.synth import config_batch
+
+        self.eng, self.batch = eng, config_batch(name, vocab=cfg.vocab)
+        self.seq_len, ids, pos, opt, nmask, _ = flatten(self.batch)
+        self.T, self.R, self.nseq = int(self.seq_len.sum()), int(nmask.sum()), len(self.batch)
+        self.max_len = int(self.seq_len.max())
+        self.d_ids = torch.from_numpy(ids).to(dev)
+        self.d_pos = torch.from_numpy(pos).to(dev)
+        self.d_opt = torch.from_numpy(opt).to(dev)
+        self.d_rt = torch.from_numpy(row_tokens(self.batch)).to(dev)
+        self.d_out = torch.zeros(self.R, dtype=torch.float32, device=dev)
+        torch.cuda.synchronize()
+
+    def step(self):
+        self.eng.forward_device(self.seq_len, self.d_ids.data_ptr(), self.d_pos.data_ptr(), self.d_opt.data_ptr(),
+                                self.R, self.d_rt.data_ptr(), self.d_out.data_ptr())
+
+    def host_forward(self):
+        return self.eng.forward(self.batch)
+
+
+def extra_configs(eng, cfg, dev, stream, args) -> dict:
+    """The other BASELINE configurations on the same engine and weights:
+    cfg1 (the fp32 projection GEMM on fp32 MFMA), cfg2 and cfg5 (one request:
+    latency of the host-array dn_forward call, and achieved weight-streaming
+    GB/s), cfg4 (8 x 2816-token SystemOne sequences: tokens/s)."""
+    import torch
+
+    out = {}
+    # cfg1: X[512x768] . W^T, W[2304x768], fp32 operands resident on the device
+    M, N, K = 512, 2304, 768
+    g = torch.Generator().manual_seed(0)
+    dA = torch.randn(M, K, generator=g).to(dev)
+    dB = (torch.randn(N, K, generator=g) * 0.02).to(dev)
+    dC = torch.zeros(M, N, device=dev)
+    for _ in range(5):
+        eng.gemm_device("fp32", M, N, K, dA.data_ptr(), dB.data_ptr(), dC.data_ptr())
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    reps = 200
+    e0.record(stream)
+    for _ in range(reps):
+        eng.gemm_device("fp32", M, N, K, dA.data_ptr(), dB.data_ptr(), dC.data_ptr())
+    e1.record(stream)
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / reps
+    flop = 2.0 * M * N * K
+    out["cfg1"] = {"workload": "fp32 X[512x768] . W^T, W[2304x768] on fp32 MFMA (dn_gemm_device, operands resident)",
+                   "us_per_call": round(us, 2), "tflops": round(flop / us / 1e6, 2),
+                   "frac_of_fp32_peak": round(flop / us / 1e6 / 157.3, 4)}
+    # cfg2 and cfg5: latency of one request through the host-array entry point
+    for name, reps in (("cfg2", 1000), ("cfg5", 10000)):
+        wl = Workload(eng, cfg, name, dev)
+        for _ in range(20):
+            wl.host_forward()
+        lat = np.empty(reps)
+        for r in range(reps):
+            t1 = time.perf_counter()
+            wl.host_forward()
+            lat[r] = time.perf_counter() - t1
+        # device time per forward (events around back-to-back device forwards)
+        e0.record(stream)
+        for _ in range(200):
+            wl.step()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        dev_ms = e0.elapsed_time(e1) / 200
+        wbytes = 2 * cfg.layers * H * (3 * H + H + 2 * I + I)  # bf16 projection weights streamed per forward
+        out[name] = {"workload": WORKLOADS[name], "repetitions": reps,
+                     "latency_ms_p50": round(float(np.percentile(lat, 50)) * 1e3, 4),
+                     "latency_ms_p99": round(float(np.percentile(lat, 99)) * 1e3, 4),
+                     "latency_call": "dn_forward (host ids in, logits out), wall clock per call",
+                     "device_ms_per_forward": round(dev_ms, 4),
+                     "tokens_per_s": round(wl.T / (dev_ms * 1e-3), 1),
+                     "weight_bytes_per_forward": wbytes,
+                     "achieved_GBps": round(wbytes / (dev_ms * 1e-3) / 1e9, 1),
+                     "frac_of_8TBps": round(wbytes / (dev_ms * 1e-3) / 8e12, 4)}
+    # cfg4: 8 sequences of 2816 tokens
+    wl = Workload(eng, cfg, "cfg4", dev)
+    for _ in range(3):
+        wl.step()
+    e0.record(stream)
+    steps = 10
+    for _ in range(steps):
+        wl.step()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    eng.check_device_errors()
+    out["cfg4"] = {"workload": WORKLOADS["cfg4"], "ms_per_forward": round(ms, 4),
+                   "tokens_per_s": round(wl.T / (ms * 1e-3), 1)}
+    return out
+
+
+def read_traffic(config: str, prec: str) -> dict:
+    """HBM bytes per launch of the roofline kernels, from the committed
+    rocprofv3 FETCH_SIZE / WRITE_SIZE summary (profiles/), when it covers
+    this workload."""
+    path = os.path.join(HERE, "profiles", "gemm_traffic_cfg3.json")
+    if config != "cfg3" or prec != "bf16" or not os.path.exists(path):
+        return {}
+    with open(path) as fh:
+        d = json.load(fh)
+    return {k: v.get("hbm_bytes_per_launch") for k, v in d.get("kernels", {}).items()}
+
+
+def summarize_traffic(fetch_dir: str, write_dir: str, out_path: str) -> int:
+    """Turns two rocprofv3 --pmc runs of `bench.py --steps 2 --warmup 1
+    --no-cpu-baseline --no-extra-configs --copy-calibration 512` (FETCH_SIZE,
+    then WRITE_SIZE) into bytes per launch for the roofline kernels, each
+    counter scaled by what it reads for the 512 MiB device copy."""
+    import csv
+    import glob
+
+    def per_kernel(d, counter):
+        rows = []
+        for f in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
+            rows += [r for r in csv.DictReader(open(f)) if r["Counter_Name"] == counter]
+        acc = {}
+        for r in rows:  # one row per dispatch and XCD: sum the XCDs of a dispatch
+            key = (r["Kernel_Name"], r["Dispatch_Id"])
+            acc[key] = acc.get(key, 0.0) + float(r["Counter_Value"])
+        byk = {}
+        for (k, _), v in acc.items():
+            byk.setdefault(k, []).append(v * 1024.0)
+        return {k: float(np.mean(v)) for k, v in byk.items()}
+
+    fetch, write = per_kernel(fetch_dir, "FETCH_SIZE"), per_kernel(write_dir, "WRITE_SIZE")
+    copy_bytes = 512 << 20
+    ck = [k for k in fetch if "copyBuffer" in k or "elementwise" in k]
+    fetch_scale = copy_bytes / max(fetch[k] for k in ck)
+    write_scale = copy_bytes / max(write[k] for k in ck)
+    T = 32768
+    pick = {"residual": ("EPI_F32", "128, 192"), "wi": ("EPI_GEGLU", "256, 128"), "qkv": ("EPI_STORE", "256, 128")}
+    alg = {"residual": (2 * (T * H + H * H) + 2 * (T * I + H * I) + 16 * T * H) / 2,
+           "wi": 2 * (T * H + 2 * I * H + T * I), "qkv": 2 * (T * H + 3 * H * H + 3 * T * H)}
+    kernels = {}
+    for name, (epi_tag, tile_tag) in pick.items():
+        epi_num = {"EPI_F32": "0", "EPI_GEGLU": "2", "EPI_STORE": "1"}[epi_tag]
+        cands = [k for k in fetch if "gemm_nt_kernel" in k and tile_tag in k and f", {epi_num}, " in k]
+        if not cands:
+            continue
+        k = cands[0]
+        fb, wb = fetch[k] * fetch_scale, write.get(k, 0.0) * write_scale
+        kernels[name] = {"symbol": k, "fetch_bytes_per_launch": round(fb), "write_bytes_per_launch": round(wb),
+                         "hbm_bytes_per_launch": round(fb + wb), "algorithmic_bytes_per_launch": alg[name]}
+    res = {"workload": "cfg3 (T=32768), bf16", "fetch_scale": fetch_scale, "write_scale": write_scale,
+           "method": "rocprofv3 --pmc FETCH_SIZE and --pmc WRITE_SIZE (separate runs of bench.py --steps 2 "
+                     "--warmup 1 --no-cpu-baseline --no-extra-configs --copy-calibration 512), KiB per dispatch "
+                     "summed over XCDs and averaged over the dispatches of each symbol, scaled by the counter's "
+                     "reading for the 512 MiB device copy", "kernels": kernels}
+    with open(out_path, "w") as fh:
+        json.dump(res, fh, indent=1)
+    print(json.dumps(res, indent=1))
     return 0
 
 

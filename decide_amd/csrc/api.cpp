@@ -632,7 +632,7 @@ void dn_close(dn_ctx *c) {
                     &c->rope,     &c->kinfo, &c->ids,      &c->pos,         &c->opt,      &c->rowtok,
                     &c->logits,   &c->err_flag, &c->gA,    &c->gB,          &c->gC,       &c->d_seq_off, &c->head_s1, &c->head_d,
                     &c->d_seq_len, &c->d_chunk_off, &c->d_chunk_desc, &c->d_work, &c->d_chunks,
-                    &c->d_codes,   &c->d_first};
+                    &c->d_codes,   &c->d_first, &c->calib};
   for (DevBuf *b : bufs) release(*b);
   if (c->own_stream) (void)hipStreamDestroy(c->own_stream);
   delete c;
@@ -934,6 +934,37 @@ int dn_read_probe(dn_ctx *c, double *ms, int *count) {
     }
   *count += c->probe_used;
   c->probe_used = 0;
+  return DN_OK;
+}
+
+int dn_mfma_calibrate(dn_ctx *c, int mode, double *tflops) {
+  if (!c || !tflops || (mode != 0 && mode != 1)) return DN_INVALID_ARG;
+  c->err.clear();
+  (void)hipSetDevice(c->device);
+  int cus = 0;
+  HIPCHK(c, "hipDeviceGetAttribute", hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, c->device));
+  HIPCHK(c, "hipMalloc", ensure(c->calib, 256 * sizeof(float)));
+  hipEvent_t e0, e1;
+  HIPCHK(c, "hipEventCreate", hipEventCreate(&e0));
+  hipError_t err = hipEventCreate(&e1);
+  if (err != hipSuccess) {
+    (void)hipEventDestroy(e0);
+    return hip_fail(c, "hipEventCreate", err);
+  }
+  // Two 4-wave blocks per CU (two waves per SIMD, as the GEMMs run); a short
+  // launch first so the timed one starts at the loaded clock.
+  const int blocks = 2 * cus, iters = 6000;
+  float ms = 0;
+  err = launch_mfma_calibrate(mode, blocks, iters / 4, (float *)c->calib.p, c->stream);
+  if (err == hipSuccess) err = hipEventRecord(e0, c->stream);
+  if (err == hipSuccess) err = launch_mfma_calibrate(mode, blocks, iters, (float *)c->calib.p, c->stream);
+  if (err == hipSuccess) err = hipEventRecord(e1, c->stream);
+  if (err == hipSuccess) err = hipEventSynchronize(e1);
+  if (err == hipSuccess) err = hipEventElapsedTime(&ms, e0, e1);
+  (void)hipEventDestroy(e0);
+  (void)hipEventDestroy(e1);
+  if (err != hipSuccess) return hip_fail(c, "mfma_calibrate", err);
+  *tflops = ms > 0 ? mfma_calibrate_flop(blocks, iters) / (ms * 1e-3) / 1e12 : 0.0;
   return DN_OK;
 }
 

@@ -319,3 +319,7 @@ hipError_t launch_zero_multi(const MTensor *t, int nt, int total_chunks, hipStre
 hipError_t launch_adamw_multi(const MTensor *t, int nt, int total_chunks, float b1, float b2, float eps, float scale,
                               float step_size, float inv_sqrt_b2c, hipStream_t s);
 hipError_t launch_widen_bf16(const void *src, float *dst, size_t n, hipStream_t s);
+// Register-only bf16 MFMA loop (calibrate.hip): mode 0 operands rotated every
+// iteration, mode 1 constant; mfma_calibrate_flop gives the work of a launch.
+hipError_t launch_mfma_calibrate(int mode, int blocks, int iters, float *sink, hipStream_t s);
+double mfma_calibrate_flop(int blocks, int iters);

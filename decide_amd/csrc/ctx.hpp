@@ -96,6 +96,7 @@ struct dn_ctx {
   DevBuf rope;
   bool rope_ready = false;
   DevBuf gA, gB, gC;  // dn_gemm_f32 staging
+  DevBuf calib;       // dn_mfma_calibrate's result sink
   // batch layout cache
   std::vector<int> lay_len;
   std::vector<int> h_seq_off, h_chunk_off;

@@ -67,6 +67,7 @@ _SIGS = {
     "dn_set_probe": ([_vp, _i], _i),
     "dn_read_probe": ([_vp, _f64p, _c.POINTER(_i)], _i),
     "dn_read_probe_backward": ([_vp, _f64p, _c.POINTER(_i)], _i),
+    "dn_mfma_calibrate": ([_vp, _i, _c.POINTER(_c.c_double)], _i),
     "dn_build_sequence": ([_i32p, _i, _c.c_int32, _i, _i32p, _i32p, _i32p, _c.POINTER(_i)], _i),
     "dn_answer": ([_f64p, _i, _c.c_double, _f64p, _c.POINTER(_i), _c.POINTER(_c.c_double)], _i),
     "dn_round": ([_c.c_double, _i], _c.c_double),

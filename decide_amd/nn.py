@@ -254,6 +254,12 @@ class Engine:
         check(lib.dn_read_probe(self._h, _ptr(ms), ctypes.byref(cnt)), self._h)
         return dict(zip(self.PROBE_NAMES, ms.tolist())), cnt.value
 
+    def mfma_calibrate(self, mode: int = 0) -> float:
+        """dn_mfma_calibrate: attainable bf16 MFMA TFLOP/s (mode 0 changing operands, 1 constant)."""
+        out = ctypes.c_double(0.0)
+        check(lib.dn_mfma_calibrate(self._h, int(mode), ctypes.byref(out)), self._h)
+        return out.value
+
     def gemm_f32(self, transA, transB, M, N, K, A, lda, B, ldb, C, ldc, accumulate) -> np.ndarray:
         """blas.Sgemm semantics on the GPU; C (float32, C-contiguous) is updated in place."""
         assert C.dtype == np.float32 and C.flags.c_contiguous

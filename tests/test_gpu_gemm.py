@@ -124,10 +124,10 @@ def test_gemm_bf16_device(eng, M, N, K):
 @pytest.mark.parametrize("M,N,K", [(1, 2304, 768), (31, 768, 1152), (33, 384, 768), (64, 2304, 768),
                                    (65, 768, 768), (112, 768, 1152), (128, 2304, 64), (100, 128, 4096)])
 def test_gemm_small_m(eng, prec, M, N, K):
-    """M <= 128 runs the split-K small-M kernel (K slices reduced by the last
-    workgroup of each tile). Same bar as above, C += accumulate checked, and
-    two calls in a row must agree bit for bit (the arrival counters reset
-    themselves and the slice sum order is fixed)."""
+    """M <= 128 runs the small-M kernel (each workgroup owns all of K; its
+    waves' partial tiles are summed through LDS in a fixed order). Same bar as
+    above, C += accumulate checked, and two calls in a row must agree bit for
+    bit (the reduction order does not depend on timing)."""
     import torch
 
     dt = torch.bfloat16 if prec == "bf16" else torch.float32
@@ -148,3 +148,11 @@ def test_gemm_small_m(eng, prec, M, N, K):
     err = (outs[0].double() - exact).abs()
     assert float((err / (1e-5 * bound + 1e-30)).max()) <= 1.0
     assert torch.equal(outs[0], outs[1])
+
+
+def test_mfma_calibrate(eng):
+    """dn_mfma_calibrate returns a plausible rate for both operand modes (the
+    register-only loop of the bench's attainable-peak line)."""
+    changing, constant = eng.mfma_calibrate(0), eng.mfma_calibrate(1)
+    print(f"attainable bf16 MFMA: changing operands {changing:.0f}, constant {constant:.0f} TFLOP/s")
+    assert 100.0 < changing < 2600.0 and 100.0 < constant < 2600.0
