@@ -146,18 +146,14 @@ const void *W(dn_ctx *c, const std::string &name) {
 }
 
 // Batch layout: sequence offsets, 32-token chunks and ATTN_QUERIES-query work items.
-int prepare_layout(dn_ctx *c, int nseq, const int32_t *seq_len) {
-  std::vector<int> len(seq_len, seq_len + nseq);
-  if (len == c->lay_len && c->d_seq_off.p) return DN_OK;
-  HIPCHK(c, "hipStreamSynchronize", hipStreamSynchronize(c->stream));  // old host staging may be in flight
-  c->lay_len.clear();
+void host_layout(dn_ctx *c, int nseq, const int32_t *seq_len, int *T_out, int *nch_out) {
   c->h_seq_off.assign(nseq + 1, 0);
   c->h_chunk_off.assign(nseq + 1, 0);
   c->h_chunk_desc.clear();
   c->h_work.clear();
   int T = 0, nch = 0;
   for (int s = 0; s < nseq; s++) {
-    const int n = len[s];
+    const int n = seq_len[s];
     c->h_seq_off[s] = T;
     c->h_chunk_off[s] = nch;
     for (int i = 0; i < n; i += 32) c->h_chunk_desc.push_back(make_int4(T + i, std::min(32, n - i), 0, 0));
@@ -167,30 +163,96 @@ int prepare_layout(dn_ctx *c, int nseq, const int32_t *seq_len) {
   }
   c->h_seq_off[nseq] = T;
   c->h_chunk_off[nseq] = nch;
-  HIPCHK(c, "hipMalloc", ensure(c->d_seq_off, sizeof(int) * (nseq + 1)));
-  HIPCHK(c, "hipMalloc", ensure(c->d_seq_len, sizeof(int) * (nseq + 1)));
-  HIPCHK(c, "hipMalloc", ensure(c->d_chunk_off, sizeof(int) * (nseq + 1)));
-  HIPCHK(c, "hipMalloc", ensure(c->d_chunk_desc, sizeof(int4) * (nch + 1)));
-  HIPCHK(c, "hipMalloc", ensure(c->d_chunks, sizeof(ChunkInfo) * (nch + 1)));
-  HIPCHK(c, "hipMalloc", ensure(c->d_work, sizeof(int4) * (c->h_work.size() + 1)));
-  HIPCHK(c, "hipMalloc", ensure(c->d_codes, sizeof(uint32_t) * 2 * ATTN_MAXKT * (c->h_work.size() + 1)));
-  HIPCHK(c, "hipMalloc", ensure(c->d_first, sizeof(int) * 2 * (c->h_work.size() + 1)));
-  c->lay_len = len;
-  HIPCHK(c, "hipMemcpyAsync", hipMemcpyAsync(c->d_seq_off.p, c->h_seq_off.data(), sizeof(int) * (nseq + 1),
-                                             hipMemcpyHostToDevice, c->stream));
-  HIPCHK(c, "hipMemcpyAsync",
-         hipMemcpyAsync(c->d_seq_len.p, c->lay_len.data(), sizeof(int) * nseq, hipMemcpyHostToDevice, c->stream));
-  HIPCHK(c, "hipMemcpyAsync", hipMemcpyAsync(c->d_chunk_off.p, c->h_chunk_off.data(), sizeof(int) * (nseq + 1),
-                                             hipMemcpyHostToDevice, c->stream));
-  if (nch)
-    HIPCHK(c, "hipMemcpyAsync", hipMemcpyAsync(c->d_chunk_desc.p, c->h_chunk_desc.data(), sizeof(int4) * nch,
-                                               hipMemcpyHostToDevice, c->stream));
+  *T_out = T;
+  *nch_out = nch;
+}
+
+int upload_layout(dn_ctx *c, const Workspace &w, int nseq, const int32_t *seq_len) {
+  hipStream_t s = c->stream;
+  HIPCHK(c, "hipMemcpyAsync", hipMemcpyAsync(w.seq_off, c->h_seq_off.data(), sizeof(int) * (nseq + 1),
+                                             hipMemcpyHostToDevice, s));
+  HIPCHK(c, "hipMemcpyAsync", hipMemcpyAsync(w.seq_len, seq_len, sizeof(int) * nseq, hipMemcpyHostToDevice, s));
+  HIPCHK(c, "hipMemcpyAsync", hipMemcpyAsync(w.chunk_off, c->h_chunk_off.data(), sizeof(int) * (nseq + 1),
+                                             hipMemcpyHostToDevice, s));
+  if (!c->h_chunk_desc.empty())
+    HIPCHK(c, "hipMemcpyAsync", hipMemcpyAsync(w.chunk_desc, c->h_chunk_desc.data(),
+                                               sizeof(int4) * c->h_chunk_desc.size(), hipMemcpyHostToDevice, s));
   if (!c->h_work.empty())
-    HIPCHK(c, "hipMemcpyAsync", hipMemcpyAsync(c->d_work.p, c->h_work.data(), sizeof(int4) * c->h_work.size(),
-                                               hipMemcpyHostToDevice, c->stream));
-  c->lay_T = T;
-  c->lay_nchunks = nch;
-  c->lay_nwork = (int)c->h_work.size();
+    HIPCHK(c, "hipMemcpyAsync", hipMemcpyAsync(w.work, c->h_work.data(), sizeof(int4) * c->h_work.size(),
+                                               hipMemcpyHostToDevice, s));
+  return DN_OK;
+}
+
+// The context's own workspace: layout arrays (re-uploaded only when the batch
+// layout changes) and activation buffers for T tokens and R rows.
+int ctx_workspace(dn_ctx *c, int nseq, const int32_t *seq_len, int R, Workspace *w) {
+  std::vector<int> len(seq_len, seq_len + nseq);
+  const bool same = len == c->lay_len && c->d_seq_off.p;
+  if (!same) {
+    HIPCHK(c, "hipStreamSynchronize", hipStreamSynchronize(c->stream));  // old host staging may be in flight
+    c->lay_len.clear();
+    int T = 0, nch = 0;
+    host_layout(c, nseq, seq_len, &T, &nch);
+    const size_t nw = c->h_work.size();
+    HIPCHK(c, "hipMalloc", ensure(c->d_seq_off, sizeof(int) * (nseq + 1)));
+    HIPCHK(c, "hipMalloc", ensure(c->d_seq_len, sizeof(int) * (nseq + 1)));
+    HIPCHK(c, "hipMalloc", ensure(c->d_chunk_off, sizeof(int) * (nseq + 1)));
+    HIPCHK(c, "hipMalloc", ensure(c->d_chunk_desc, sizeof(int4) * (nch + 1)));
+    HIPCHK(c, "hipMalloc", ensure(c->d_chunks, sizeof(ChunkInfo) * (nch + 1)));
+    HIPCHK(c, "hipMalloc", ensure(c->d_work, sizeof(int4) * (nw + 1)));
+    HIPCHK(c, "hipMalloc", ensure(c->d_codes, sizeof(uint32_t) * 2 * ATTN_MAXKT * (nw + 1)));
+    HIPCHK(c, "hipMalloc", ensure(c->d_first, sizeof(int) * 2 * (nw + 1)));
+    c->lay_len = len;
+    c->lay_T = T;
+    c->lay_nchunks = nch;
+    c->lay_nwork = (int)nw;
+  }
+  Workspace &o = *w;
+  o.seq_off = (int *)c->d_seq_off.p;
+  o.seq_len = (int *)c->d_seq_len.p;
+  o.chunk_off = (int *)c->d_chunk_off.p;
+  o.chunk_desc = (int4 *)c->d_chunk_desc.p;
+  o.chunks = (ChunkInfo *)c->d_chunks.p;
+  o.work = (int4 *)c->d_work.p;
+  o.codes = (uint32_t *)c->d_codes.p;
+  o.first = (int *)c->d_first.p;
+  o.T = c->lay_T;
+  o.nchunks = c->lay_nchunks;
+  o.nwork = c->lay_nwork;
+  if (!same) {
+    int rc = upload_layout(c, o, nseq, c->lay_len.data());
+    if (rc) return rc;
+  }
+  const Config &g = c->cfg;
+  const size_t es = g.precision == DN_PRECISION_BF16 ? 2 : 4, T = (size_t)o.T, H = g.hidden;
+  HIPCHK(c, "hipMalloc", ensure(c->h, sizeof(float) * T * H));
+  HIPCHK(c, "hipMalloc", ensure(c->xn, es * T * H));
+  HIPCHK(c, "hipMalloc", ensure(c->qkv, es * T * 3 * H));
+  HIPCHK(c, "hipMalloc", ensure(c->ctxb, es * T * H));
+  HIPCHK(c, "hipMalloc", ensure(c->act, es * T * g.inter));
+  HIPCHK(c, "hipMalloc", ensure(c->kinfo, sizeof(int) * T));
+  HIPCHK(c, "hipMalloc", ensure(c->head_s1, sizeof(float) * (size_t)std::max(R, 1) * H));
+  HIPCHK(c, "hipMalloc", ensure(c->head_d, sizeof(float) * (size_t)std::max(R, 1) * (H / 2)));
+  o.h = (float *)c->h.p;
+  o.xn = c->xn.p;
+  o.qkv = c->qkv.p;
+  o.ctx = c->ctxb.p;
+  o.act = c->act.p;
+  o.kinfo = (int *)c->kinfo.p;
+  o.head_s1 = (float *)c->head_s1.p;
+  o.head_d = (float *)c->head_d.p;
+  return DN_OK;
+}
+
+int ensure_rope(dn_ctx *c) {
+  if (c->rope_ready) return DN_OK;
+  HIPCHK(c, "hipMalloc", ensure(c->rope, sizeof(float) * kPositions * 32 * 4));
+  float *r = (float *)c->rope.p;
+  const double *inv = (const double *)c->inv_freq.p;
+  HIPCHK(c, "rope_tables", launch_rope_tables(nullptr, kPositions, inv, inv + 32, r, r + (size_t)kPositions * 32,
+                                              r + (size_t)2 * kPositions * 32, r + (size_t)3 * kPositions * 32,
+                                              c->stream));
+  c->rope_ready = true;
   return DN_OK;
 }
 
@@ -232,16 +294,23 @@ hipEvent_t *probe_slot(dn_ctx *c, int l) {
   } while (0)
 
 int forward_core(dn_ctx *c, int nseq, const int32_t *seq_len, const int32_t *d_ids, const int32_t *d_pos,
-                 const int32_t *d_opt, int R, const int32_t *d_row_tok, float *d_logits, bool train) {
+                 const int32_t *d_opt, int R, const int32_t *d_row_tok, float *d_logits, bool train,
+                 const Workspace *ws) {
   const Config &g = c->cfg;
   const int H = g.hidden, I = g.inter, L = g.layers;
   const int prec = g.precision;
   const size_t es = prec == DN_PRECISION_BF16 ? 2 : 4;
   TrainState &tr = c->tr;
   tr.have_forward = false;  // any forward replaces the layout and the encoder output
-  int rc = prepare_layout(c, nseq, seq_len);
-  if (rc) return rc;
-  const int T = c->lay_T;
+  Workspace w;
+  int rc = DN_OK;
+  if (ws) {
+    w = *ws;
+  } else {
+    rc = ctx_workspace(c, nseq, seq_len, R, &w);
+    if (rc) return rc;
+  }
+  const int T = w.T;
   hipStream_t s = c->stream;
   if (train) {
     tr.layers.resize(L);
@@ -261,48 +330,35 @@ int forward_core(dn_ctx *c, int nseq, const int32_t *seq_len, const int32_t *d_i
     HIPCHK(c, "hipMalloc", ensure(tr.emb_mean, sizeof(float) * T));
     HIPCHK(c, "hipMalloc", ensure(tr.emb_rstd, sizeof(float) * T));
   }
-  HIPCHK(c, "hipMalloc", ensure(c->h, sizeof(float) * T * H));
-  HIPCHK(c, "hipMalloc", ensure(c->xn, es * T * H));
-  HIPCHK(c, "hipMalloc", ensure(c->qkv, es * T * 3 * H));
-  HIPCHK(c, "hipMalloc", ensure(c->ctxb, es * T * H));
-  HIPCHK(c, "hipMalloc", ensure(c->act, es * T * I));
-  HIPCHK(c, "hipMalloc", ensure(c->kinfo, sizeof(int) * T));
+  if (ws && (!c->rope_ready || !c->err_flag.p))
+    return fail(c, DN_INVALID_ARG, "decide_hip: set-up incomplete (dn_set_config builds the RoPE tables)");
   rc = ensure_err_flag(c);
   if (rc) return rc;
+  rc = ensure_rope(c);
+  if (rc) return rc;
 
-  float *h = (float *)c->h.p;
-  const double *inv = (const double *)c->inv_freq.p;
-  if (!c->rope_ready) {
-    HIPCHK(c, "hipMalloc", ensure(c->rope, sizeof(float) * kPositions * 32 * 4));
-    float *r = (float *)c->rope.p;
-    HIPCHK(c, "rope_tables", launch_rope_tables(nullptr, kPositions, inv, inv + 32, r, r + (size_t)kPositions * 32,
-                                                r + (size_t)2 * kPositions * 32, r + (size_t)3 * kPositions * 32, s));
-    c->rope_ready = true;
-  }
+  float *h = w.h;
   const float *rope = (const float *)c->rope.p;
   const float *cos_g = rope, *sin_g = rope + (size_t)kPositions * 32, *cos_l = rope + (size_t)2 * kPositions * 32,
               *sin_l = rope + (size_t)3 * kPositions * 32;
-  int *kinfo = (int *)c->kinfo.p;
+  int *kinfo = w.kinfo;
 
   HIPCHK(c, "token_info", launch_token_info(d_pos, d_opt, kinfo, T, (int *)c->err_flag.p, s));
-  HIPCHK(c, "chunk_summary", launch_chunk_summary(kinfo, (const int4 *)c->d_chunk_desc.p,
-                                                  (ChunkInfo *)c->d_chunks.p, c->lay_nchunks, s));
+  HIPCHK(c, "chunk_summary", launch_chunk_summary(kinfo, w.chunk_desc, w.chunks, w.nchunks, s));
   // Attention tile classes for the two layer types (global, then local).
-  uint32_t *codes = (uint32_t *)c->d_codes.p;
-  int *first = (int *)c->d_first.p;
-  const size_t nw = (size_t)c->lay_nwork;
+  uint32_t *codes = w.codes;
+  int *first = w.first;
+  const size_t nw = (size_t)w.nwork;
   for (int sl = 0; sl < 2; sl++)
-    HIPCHK(c, "tile_codes", launch_tile_codes((const ChunkInfo *)c->d_chunks.p, (const int4 *)c->d_work.p,
-                                              (const int *)c->d_seq_len.p, (const int *)c->d_chunk_off.p,
-                                              c->lay_nwork, sl, g.half_window, codes + sl * nw * ATTN_MAXKT,
-                                              first + sl * nw, s));
+    HIPCHK(c, "tile_codes", launch_tile_codes(w.chunks, w.work, w.seq_len, w.chunk_off, w.nwork, sl, g.half_window,
+                                              codes + sl * nw * ATTN_MAXKT, first + sl * nw, s));
   // Training keeps each saved layer's input in its own buffer (LayerSave::hs)
   // and its post-attention residual in LayerSave::h1: the residual GEMMs read
   // one and write the next, so the residual stream moves through the saved
   // buffers without copies; unsaved layers update c->h in place.
   auto saved = [&](int l) -> LayerSave * { return train && l >= tr.train_from && l < L ? &tr.layers[l] : nullptr; };
   float *cur = saved(0) ? (float *)saved(0)->hs.p : h;  // the residual stream entering layer 0
-  void *xn0 = saved(0) ? saved(0)->n1.p : c->xn.p;      // layer 0's QKV input (no attn_norm)
+  void *xn0 = saved(0) ? saved(0)->n1.p : w.xn;         // layer 0's QKV input (no attn_norm)
   HIPCHK(c, "embed_ln",
          launch_embed_ln(prec, d_ids, T, (const float *)W(c, "model.embeddings.tok_embeddings.weight"), g.vocab,
                          (const float *)W(c, "model.embeddings.norm.weight"), g.eps, H, cur, xn0,
@@ -311,10 +367,10 @@ int forward_core(dn_ctx *c, int nseq, const int32_t *seq_len, const int32_t *d_i
 
   AttnArgs at{};
   at.kinfo = kinfo;
-  at.work = (const int4 *)c->d_work.p;
-  at.seq_off = (const int *)c->d_seq_off.p;
-  at.seq_len = (const int *)c->d_seq_len.p;
-  at.nwork = c->lay_nwork;
+  at.work = w.work;
+  at.seq_off = w.seq_off;
+  at.seq_len = w.seq_len;
+  at.nwork = w.nwork;
   at.H = H;
   at.heads = g.heads;
   at.half_window = g.half_window;
@@ -324,7 +380,7 @@ int forward_core(dn_ctx *c, int nseq, const int32_t *seq_len, const int32_t *d_i
   for (int l = 0; l < L; l++) {
     const std::string p = layer_prefix(l);
     const bool sliding = g.sliding[l] != 0;
-    hipEvent_t *ev = probe_slot(c, l);
+    hipEvent_t *ev = ws ? nullptr : probe_slot(c, l);  // the probe creates events: not in a caller's workspace
     probed |= ev != nullptr;
     // Training keeps this layer's activations (layers >= train_from).
     LayerSave *S = saved(l);
@@ -333,7 +389,7 @@ int forward_core(dn_ctx *c, int nseq, const int32_t *seq_len, const int32_t *d_i
     float *out = saved(l + 1) ? (float *)saved(l + 1)->hs.p : h;  // the layer's output
     void *x1 = xn0;  // QKV input: attn_norm(in), or for layer 0 the embedding output
     if (l > 0) {
-      x1 = S ? S->n1.p : c->xn.p;
+      x1 = S ? S->n1.p : w.xn;
       HIPCHK(c, "ln(attn_norm)",
              launch_ln(prec, in, T, H, (const float *)W(c, p + "attn_norm.weight"), g.eps, x1, s,
                        S ? (float *)S->mean1.p : nullptr, S ? (float *)S->rstd1.p : nullptr));
@@ -343,7 +399,7 @@ int forward_core(dn_ctx *c, int nseq, const int32_t *seq_len, const int32_t *d_i
     q.lda = H;
     q.B = W(c, p + "attn.Wqkv.weight");
     q.ldb = H;
-    q.C = S ? S->qkv.p : c->qkv.p;
+    q.C = S ? S->qkv.p : w.qkv;
     q.ldc = 3 * H;
     q.M = T;
     q.N = 3 * H;
@@ -352,7 +408,7 @@ int forward_core(dn_ctx *c, int nseq, const int32_t *seq_len, const int32_t *d_i
     PROBED(ev, DN_PROBE_QKV, "gemm(Wqkv)", launch_gemm(prec, EPI_STORE, q, s));
 
     at.qkv = q.C;
-    at.ctx = S ? S->ctx.p : c->ctxb.p;
+    at.ctx = S ? S->ctx.p : w.ctx;
     at.lse = S ? (float *)S->lse.p : nullptr;
     at.sliding = sliding ? 1 : 0;
     at.codes = codes + (sliding ? nw * ATTN_MAXKT : 0);
@@ -376,7 +432,7 @@ int forward_core(dn_ctx *c, int nseq, const int32_t *seq_len, const int32_t *d_i
     o.accumulate = 1;
     PROBED(ev, DN_PROBE_WO, "gemm(Wo)", launch_gemm(prec, EPI_F32, o, s));
 
-    void *x2 = S ? S->n2.p : c->xn.p;
+    void *x2 = S ? S->n2.p : w.xn;
     HIPCHK(c, "ln(mlp_norm)", launch_ln(prec, h1, T, H, (const float *)W(c, p + "mlp_norm.weight"), g.eps, x2, s,
                                         S ? (float *)S->mean2.p : nullptr, S ? (float *)S->rstd2.p : nullptr));
 
@@ -396,13 +452,13 @@ int forward_core(dn_ctx *c, int nseq, const int32_t *seq_len, const int32_t *d_i
       wi.ldc2 = I;
       PROBED(ev, DN_PROBE_WI, "gemm(Wi)", launch_gemm(prec, EPI_GEGLU_KEEP, wi, s));
     } else {
-      wi.C = c->act.p;
+      wi.C = w.act;
       wi.ldc = I;
       PROBED(ev, DN_PROBE_WI, "gemm(Wi)", launch_gemm(prec, EPI_GEGLU, wi, s));
     }
 
     GemmArgs mo{};
-    mo.A = S ? S->act.p : c->act.p;
+    mo.A = S ? S->act.p : w.act;
     mo.lda = I;
     mo.B = W(c, p + "mlp.Wo.weight");
     mo.ldb = I;
@@ -437,9 +493,7 @@ int forward_core(dn_ctx *c, int nseq, const int32_t *seq_len, const int32_t *d_i
   ha.out_b = (const float *)W(c, "scorer.out_proj.bias");
   ha.logits = d_logits;
   ha.err_flag = (int *)c->err_flag.p;
-  HIPCHK(c, "hipMalloc", ensure(c->head_s1, sizeof(float) * (size_t)std::max(R, 1) * H));
-  HIPCHK(c, "hipMalloc", ensure(c->head_d, sizeof(float) * (size_t)std::max(R, 1) * (H / 2)));
-  HIPCHK(c, "head", launch_head(ha, (float *)c->head_s1.p, (float *)c->head_d.p, s));
+  HIPCHK(c, "head", launch_head(ha, w.head_s1, w.head_d, s));
   if (train) {
     tr.have_forward = true;
     tr.T = T;
@@ -616,6 +670,12 @@ int dn_open(int device, dn_ctx **out) {
     return hip_fail(nullptr, "hipStreamCreate", e);
   }
   c->stream = c->own_stream;
+  int rc = noalloc_init(c);
+  if (rc) {
+    (void)hipStreamDestroy(c->own_stream);
+    delete c;
+    return rc;
+  }
   *out = c;
   return DN_OK;
 }
@@ -684,8 +744,15 @@ int dn_set_config(dn_ctx *c, int hidden, int inter, int heads, int layers, int v
   }
   HIPCHK(c, "hipMalloc", ensure(c->inv_freq, sizeof(inv)));
   HIPCHK(c, "hipMemcpy", hipMemcpy(c->inv_freq.p, inv, sizeof(inv), hipMemcpyHostToDevice));
-  c->rope_ready = false;  // tables follow the new thetas at the next forward
+  c->rope_ready = false;
   c->configured = true;
+  // Set-up work that forwards would otherwise do on first use: the RoPE
+  // tables of these thetas and the device error flag.
+  int rc = ensure_rope(c);
+  if (rc) return rc;
+  rc = ensure_err_flag(c);
+  if (rc) return rc;
+  HIPCHK(c, "hipStreamSynchronize", hipStreamSynchronize(c->stream));
   return DN_OK;
 }
 

@@ -80,6 +80,22 @@ struct TrainState {
   hipEvent_t ev_trans[2] = {nullptr, nullptr};  // the layer's gradient transposes are done
 };
 
+// Device memory one forward works in beyond the weights: the activations,
+// the batch layout and the head's scratch. forward_core takes it from the
+// context's own buffers unless a caller hands one in
+// (dn_forward_device_noalloc points it into the library's static scratch array).
+struct Workspace {
+  float *h = nullptr;                                   // fp32 [T x H] residual stream
+  void *xn = nullptr, *qkv = nullptr, *ctx = nullptr, *act = nullptr;  // operand type
+  int *kinfo = nullptr;                                 // [T]
+  float *head_s1 = nullptr, *head_d = nullptr;          // [R x H], [R x H/2]
+  int *seq_off = nullptr, *seq_len = nullptr, *chunk_off = nullptr, *first = nullptr;
+  int4 *chunk_desc = nullptr, *work = nullptr;
+  ChunkInfo *chunks = nullptr;
+  uint32_t *codes = nullptr;
+  int T = 0, nchunks = 0, nwork = 0;
+};
+
 struct dn_ctx {
   int device = 0;
   hipStream_t stream = nullptr;
@@ -97,6 +113,7 @@ struct dn_ctx {
   bool rope_ready = false;
   DevBuf gA, gB, gC;  // dn_gemm_f32 staging
   DevBuf calib;       // dn_mfma_calibrate's result sink
+  void *scratch = nullptr;  // this device's static scratch array (noalloc.cpp), from hipGetSymbolAddress
   // batch layout cache
   std::vector<int> lay_len;
   std::vector<int> h_seq_off, h_chunk_off;
@@ -135,8 +152,22 @@ int stage_batch(dn_ctx *c, int nseq, const int32_t *seq_len, const int32_t *ids,
                 int64_t *T);
 // The forward on device-resident token arrays; with train, the activations of
 // layers >= c->tr.train_from are kept in c->tr.layers.
+// ws: the workspace to run in (inference only); null = the context's buffers.
 int forward_core(dn_ctx *c, int nseq, const int32_t *seq_len, const int32_t *d_ids, const int32_t *d_pos,
-                 const int32_t *d_opt, int R, const int32_t *d_row_tok, float *d_logits, bool train);
+                 const int32_t *d_opt, int R, const int32_t *d_row_tok, float *d_logits, bool train,
+                 const Workspace *ws = nullptr);
+// The batch layout on the host (c->h_seq_off, h_chunk_off, h_chunk_desc,
+// h_work); *T and *nchunks receive the token and 32-token chunk counts.
+void host_layout(dn_ctx *c, int nseq, const int32_t *seq_len, int *T, int *nchunks);
+// Copies the host layout of the last host_layout call into w's device arrays.
+int upload_layout(dn_ctx *c, const Workspace &w, int nseq, const int32_t *seq_len);
+// RoPE tables of the configured thetas and the device error flag: built at
+// set-up (dn_set_config), so forwards allocate neither.
+int ensure_rope(dn_ctx *c);
+int ensure_err_flag(dn_ctx *c);
+// Fills in the context's own scratch pointer for its device (noalloc.cpp;
+// called by dn_open with the device current).
+int noalloc_init(dn_ctx *c);
 // Finishes a host-array forward: logits to the host and the device error flag.
 int finish_forward(dn_ctx *c, int R, float *logits);
 

@@ -60,6 +60,7 @@ _SIGS = {
     "dn_weights_ready": ([_vp], _i),
     "dn_forward": ([_vp, _i, _i32p, _i32p, _i32p, _i32p, _i32p, _i32p, _f32p, _i], _i),
     "dn_forward_device": ([_vp, _i, _i32p, _vp, _vp, _vp, _i, _vp, _vp], _i),
+    "dn_forward_device_noalloc": ([_vp, _i, _i32p, _vp, _vp, _vp, _i, _vp, _vp], _i),
     "dn_check_device_errors": ([_vp], _i),
     "dn_gemm_f32": ([_vp, _i, _i, _i, _i, _i, _f32p, _i, _f32p, _i, _f32p, _i, _i], _i),
     "dn_gemm_device": ([_vp, _i, _i, _i, _i, _vp, _vp, _vp, _i], _i),

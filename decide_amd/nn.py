@@ -236,6 +236,15 @@ class Engine:
                                     ctypes.c_void_p(d_pos), ctypes.c_void_p(d_opt) if d_opt else None, nrows,
                                     ctypes.c_void_p(d_row_tok), ctypes.c_void_p(d_logits)), self._h)
 
+    def forward_device_noalloc(self, seq_len: np.ndarray, d_ids: int, d_pos: int, d_opt: Optional[int], nrows: int,
+                               d_row_tok: int, d_logits: int) -> None:
+        """dn_forward_device_noalloc: the same forward in the library's static
+        scratch array (no device allocation)."""
+        sl = np.ascontiguousarray(seq_len, np.int32)
+        check(lib.dn_forward_device_noalloc(self._h, len(sl), _ptr(sl), ctypes.c_void_p(d_ids), ctypes.c_void_p(d_pos),
+                                            ctypes.c_void_p(d_opt) if d_opt else None, int(nrows),
+                                            ctypes.c_void_p(d_row_tok), ctypes.c_void_p(d_logits)), self._h)
+
     def check_device_errors(self) -> None:
         check(lib.dn_check_device_errors(self._h), self._h)
 

@@ -130,6 +130,21 @@ int dn_forward_device(dn_ctx *ctx, int nseq, const int32_t *seq_len, const int32
                       const int32_t *d_pos, const int32_t *d_opt_id, int nrows, const int32_t *d_row_tok,
                       float *d_logits);
 
+/* dn_forward_device without allocating: every buffer the forward works in
+ * beyond the weights and the caller's inputs and outputs (activations, batch
+ * layout, head scratch) comes from one static 64 MiB device array per GPU, so
+ * the call makes no hipMalloc / hipFree. About 5,100 tokens per call fit at
+ * ModernBERT-base in bf16 (about 2,900 in fp32); a larger batch gets
+ * DN_INVALID_ARG naming the bytes it needs. All calls on one GPU share the
+ * array: calls that overlap on one GPU (two contexts or streams) race. The
+ * context's stream is synchronised before the batch layout is uploaded.
+ * Arguments and results as dn_forward_device. No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc). */
+int dn_forward_device_noalloc(dn_ctx *ctx, int nseq, const int32_t *seq_len, const int32_t *d_ids,
+                              const int32_t *d_pos, const int32_t *d_opt_id, int nrows,
+                              const int32_t *d_row_tok, float *d_logits);
+
 /* Synchronises the stream and reports (DN_INVALID_ARG) any out-of-range token
  * id or row index seen by dn_forward_device since the last check. */
 int dn_check_device_errors(dn_ctx *ctx);
