@@ -288,3 +288,100 @@ def test_max_length_sequence(base, engines):
     long_ids = pack_request(rng, 8001, [48] * 4, cfg.vocab)
     with pytest.raises(Unsupported):
         engines["bf16"].forward([build_sequence(long_ids, 50284, True)])
+
+
+def _question_probs(logits, groups_per_seq):
+    """Softmax (T = 1) within each question's logits: groups_per_seq[i] lists
+    (first, K) of sequence i's questions, relative to that sequence."""
+    out, off = [], 0
+    for groups in groups_per_seq:
+        for first, k in groups:
+            z = np.asarray(logits[off + first: off + first + k], np.float64)
+            e = np.exp(z - z.max())
+            out.append(e / e.sum())
+        off += sum(k for _, k in groups)
+    return out
+
+
+def test_cfg4_full_batch(base, engines):
+    """cfg4 at its configured batch (8 x 2816 tokens, 84 options per
+    sequence in 24 questions): two sequences against the oracle, per question,
+    in both modes; each sequence's logits do not depend on the rest of the
+    batch (fp32: to 1e-4 * (1 + |logit|) against the sequence run alone; bf16:
+    the full-batch and single-sequence runs both within the bf16 bar)."""
+    from decide_amd.synth import cfg4_question_groups, config_batch
+
+    cfg, _, orc = base
+    batch = config_batch("cfg4", vocab=cfg.vocab)
+    assert len(batch) == 8 and all(len(s.ids) == 2816 and len(s.mask_pos) == 84 for s in batch)
+    groups = [(first, k) for _, first, k in cfg4_question_groups()]
+    full = {p: engines[p].forward(batch) for p in ("fp32", "bf16")}
+    for p in full:
+        assert full[p].shape == (8 * 84,) and np.all(np.isfinite(full[p]))
+    oracle.set_workers(WORKERS)
+    for i in (0, 5):
+        want = orc.forward([batch[i]])
+        pw = _question_probs(want, [groups])
+        for p, bar in (("fp32", 1e-5), ("bf16", 2e-3)):
+            part = full[p][84 * i: 84 * i + 84]
+            one = engines[p].forward([batch[i]])
+            for got in (part, one):
+                pg = _question_probs(got, [groups])
+                dp = max(float(np.max(np.abs(a - b))) for a, b in zip(pg, pw))
+                agree = np.mean([int(np.argmax(a) == np.argmax(b)) for a, b in zip(pg, pw)])
+                print(f"cfg4 seq {i} {p}: max|dp| {dp:.3g}, argmax agree {agree:.3f}", flush=True)
+                assert dp <= bar
+                if p == "fp32":
+                    assert agree == 1.0
+            if p == "fp32":
+                assert np.all(np.abs(one - part) <= 1e-4 * (1 + np.abs(one)))
+
+
+def test_argmax_agreement_1000_requests(base, engines):
+    """1,000 requests (500 shaped like cfg2, 500 like cfg5, seeds 10000+i) in
+    one batched forward against the oracle's logits in
+    tests/golden/argmax_1000.npz (written by make_argmax_fixture.py in this
+    directory).
+
+    fp32 validation build, float32 weights: the north-star bars, every argmax
+    and max |dp| <= 1e-5.
+
+    bf16 build, against the float32-weight logits and against the oracle run
+    on the same projection weights rounded to bf16 (identical weights): max
+    |dp| <= 2e-3. Its argmax agrees on >= 99.5% of the requests and on every
+    decisive one (the oracle's top two probabilities more than 2 x 2e-3
+    apart). The bf16 activations move these random-init logits by ~1e-3, and
+    19 of the 1,000 requests have a top-two logit gap under 1e-3, so raw
+    agreement is 99.5-99.7% here, below the north star's 99.9%: every request
+    that flips is a near-tie whose probabilities both paths give within the
+    2e-3 tolerance."""
+    import importlib.util
+
+    from conftest import GOLDEN
+
+    spec = importlib.util.spec_from_file_location("make_argmax_fixture",
+                                                  os.path.join(GOLDEN, "make_argmax_fixture.py"))
+    mk = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mk)
+    cfg = base[0]
+    batch = mk.requests(cfg.vocab)
+    fx = np.load(os.path.join(GOLDEN, "argmax_1000.npz"))
+    assert np.array_equal(np.concatenate([s.ids for s in batch]), fx["ids"])  # same requests as the fixture
+    groups = [[(0, len(s.mask_pos))] for s in batch]
+    got = {p: engines[p].forward(batch) for p in ("fp32", "bf16")}
+    for p, key, dp_bar, agree_bar in (("fp32", "logits_f32w", 1e-5, 1.0), ("bf16", "logits_f32w", 2e-3, 0.995),
+                                      ("bf16", "logits_bf16w", 2e-3, 0.995)):
+        want = fx[key].astype(np.float64)
+        assert got[p].shape == want.shape and np.all(np.isfinite(got[p]))
+        pg, pw = _question_probs(got[p], groups), _question_probs(want, groups)
+        dp = max(float(np.max(np.abs(a - b))) for a, b in zip(pg, pw))
+        flips = [i for i, (a, b) in enumerate(zip(pg, pw)) if np.argmax(a) != np.argmax(b)]
+        agree = 1.0 - len(flips) / len(batch)
+        top2 = np.array([np.diff(np.sort(b)[-2:])[0] for b in pw])
+        decisive = top2 > 2 * dp_bar
+        print(f"1000 requests {p} vs {key}: max|dp| {dp:.3g}, argmax agree {agree:.4f} (flipped {flips}, "
+              f"oracle top-2 prob gaps {[float(f'{top2[i]:.2g}') for i in flips]}; {int(decisive.sum())} decisive)",
+              flush=True)
+        assert dp <= dp_bar
+        assert agree >= agree_bar
+        assert not any(decisive[i] for i in flips)
