@@ -488,6 +488,10 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=12.0)
     ap.add_argument("--probe-layer", type=int, default=1)
+    ap.add_argument("--probe-steps", type=int, default=5,
+                    help="forwards run with the per-launch probe after the timed ones (one stream)")
+    ap.add_argument("--stream-split", type=int, default=8192, metavar="TOKENS",
+                    help="dn_set_stream_split: batches of at least TOKENS run in two parts on two streams (0: off)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="run one device copy of MIB MiB first (reference kernel for HBM counters)")
     ap.add_argument("--tokenizer", action="store_true",
@@ -541,6 +545,7 @@ def main() -> int:
         log(f"copy calibration: {nbytes} bytes read + {nbytes} bytes written")
         del src, dst
 
+    eng.set_stream_split(args.stream_split)
     wl = Workload(eng, cfg, args.config, dev)
     log(f"workload {args.config}: {wl.nseq} sequences, T={wl.T}, R={wl.R}")
     log(f"warmup {args.warmup}")
@@ -549,7 +554,6 @@ def main() -> int:
     torch.cuda.synchronize()
     eng.check_device_errors()
 
-    eng.set_probe(args.probe_layer)
     ev = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
     log(f"timing {args.steps} steps")
     quiesce_host()
@@ -561,9 +565,15 @@ def main() -> int:
         ev[k + 1].record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
+    eng.check_device_errors()
+    # Per-launch kernel durations: a separate run with the probe on (HIP
+    # events around layer probe_layer's five launches), where forwards run on
+    # one stream so that each interval times one kernel alone.
+    eng.set_probe(args.probe_layer)
+    for _ in range(args.probe_steps):
+        wl.step()
     probe, nprobe = eng.read_probe()
     eng.set_probe(-1)
-    eng.check_device_errors()
     per_step = [ev[k].elapsed_time(ev[k + 1]) for k in range(args.steps)]
     gpu_ms = sum(per_step)
     T = wl.T
@@ -634,6 +644,9 @@ def main() -> int:
         "projection_gemm_tflops": round(gemm_tflops, 2),
         "projection_gemm_frac_peak": round(gemm_tflops * 1e12 / PEAK[prec], 4),
         "per_launch_ms": {k: round(v, 5) for k, v in avg.items()},
+        "per_launch_method": f"HIP events on the launch stream around layer {args.probe_layer}'s launches, "
+                             f"{nprobe} forwards run after the timed ones on one stream",
+        "stream_split_min_tokens": args.stream_split,
         "roofline": roof,
     }
     if attain:

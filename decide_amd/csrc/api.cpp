@@ -146,40 +146,40 @@ const void *W(dn_ctx *c, const std::string &name) {
 }
 
 // Batch layout: sequence offsets, 32-token chunks and ATTN_QUERIES-query work items.
-void host_layout(dn_ctx *c, int nseq, const int32_t *seq_len, int *T_out, int *nch_out) {
-  c->h_seq_off.assign(nseq + 1, 0);
-  c->h_chunk_off.assign(nseq + 1, 0);
-  c->h_chunk_desc.clear();
-  c->h_work.clear();
+void host_layout(HostLayout &hl, int nseq, const int32_t *seq_len, int *T_out, int *nch_out) {
+  hl.seq_off.assign(nseq + 1, 0);
+  hl.chunk_off.assign(nseq + 1, 0);
+  hl.chunk_desc.clear();
+  hl.work.clear();
   int T = 0, nch = 0;
   for (int s = 0; s < nseq; s++) {
     const int n = seq_len[s];
-    c->h_seq_off[s] = T;
-    c->h_chunk_off[s] = nch;
-    for (int i = 0; i < n; i += 32) c->h_chunk_desc.push_back(make_int4(T + i, std::min(32, n - i), 0, 0));
-    for (int q = 0; q < n; q += ATTN_QUERIES) c->h_work.push_back(make_int4(s, q, 0, 0));
+    hl.seq_off[s] = T;
+    hl.chunk_off[s] = nch;
+    for (int i = 0; i < n; i += 32) hl.chunk_desc.push_back(make_int4(T + i, std::min(32, n - i), 0, 0));
+    for (int q = 0; q < n; q += ATTN_QUERIES) hl.work.push_back(make_int4(s, q, 0, 0));
     nch += (n + 31) / 32;
     T += n;
   }
-  c->h_seq_off[nseq] = T;
-  c->h_chunk_off[nseq] = nch;
+  hl.seq_off[nseq] = T;
+  hl.chunk_off[nseq] = nch;
   *T_out = T;
   *nch_out = nch;
 }
 
-int upload_layout(dn_ctx *c, const Workspace &w, int nseq, const int32_t *seq_len) {
-  hipStream_t s = c->stream;
-  HIPCHK(c, "hipMemcpyAsync", hipMemcpyAsync(w.seq_off, c->h_seq_off.data(), sizeof(int) * (nseq + 1),
-                                             hipMemcpyHostToDevice, s));
+int upload_layout(dn_ctx *c, const HostLayout &hl, const Workspace &w, int nseq, const int32_t *seq_len,
+                  hipStream_t s) {
+  HIPCHK(c, "hipMemcpyAsync",
+         hipMemcpyAsync(w.seq_off, hl.seq_off.data(), sizeof(int) * (nseq + 1), hipMemcpyHostToDevice, s));
   HIPCHK(c, "hipMemcpyAsync", hipMemcpyAsync(w.seq_len, seq_len, sizeof(int) * nseq, hipMemcpyHostToDevice, s));
-  HIPCHK(c, "hipMemcpyAsync", hipMemcpyAsync(w.chunk_off, c->h_chunk_off.data(), sizeof(int) * (nseq + 1),
-                                             hipMemcpyHostToDevice, s));
-  if (!c->h_chunk_desc.empty())
-    HIPCHK(c, "hipMemcpyAsync", hipMemcpyAsync(w.chunk_desc, c->h_chunk_desc.data(),
-                                               sizeof(int4) * c->h_chunk_desc.size(), hipMemcpyHostToDevice, s));
-  if (!c->h_work.empty())
-    HIPCHK(c, "hipMemcpyAsync", hipMemcpyAsync(w.work, c->h_work.data(), sizeof(int4) * c->h_work.size(),
+  HIPCHK(c, "hipMemcpyAsync",
+         hipMemcpyAsync(w.chunk_off, hl.chunk_off.data(), sizeof(int) * (nseq + 1), hipMemcpyHostToDevice, s));
+  if (!hl.chunk_desc.empty())
+    HIPCHK(c, "hipMemcpyAsync", hipMemcpyAsync(w.chunk_desc, hl.chunk_desc.data(), sizeof(int4) * hl.chunk_desc.size(),
                                                hipMemcpyHostToDevice, s));
+  if (!hl.work.empty())
+    HIPCHK(c, "hipMemcpyAsync",
+           hipMemcpyAsync(w.work, hl.work.data(), sizeof(int4) * hl.work.size(), hipMemcpyHostToDevice, s));
   return DN_OK;
 }
 
@@ -192,8 +192,8 @@ int ctx_workspace(dn_ctx *c, int nseq, const int32_t *seq_len, int R, Workspace 
     HIPCHK(c, "hipStreamSynchronize", hipStreamSynchronize(c->stream));  // old host staging may be in flight
     c->lay_len.clear();
     int T = 0, nch = 0;
-    host_layout(c, nseq, seq_len, &T, &nch);
-    const size_t nw = c->h_work.size();
+    host_layout(c->hlay, nseq, seq_len, &T, &nch);
+    const size_t nw = c->hlay.work.size();
     HIPCHK(c, "hipMalloc", ensure(c->d_seq_off, sizeof(int) * (nseq + 1)));
     HIPCHK(c, "hipMalloc", ensure(c->d_seq_len, sizeof(int) * (nseq + 1)));
     HIPCHK(c, "hipMalloc", ensure(c->d_chunk_off, sizeof(int) * (nseq + 1)));
@@ -220,7 +220,7 @@ int ctx_workspace(dn_ctx *c, int nseq, const int32_t *seq_len, int R, Workspace 
   o.nchunks = c->lay_nchunks;
   o.nwork = c->lay_nwork;
   if (!same) {
-    int rc = upload_layout(c, o, nseq, c->lay_len.data());
+    int rc = upload_layout(c, c->hlay, o, nseq, c->lay_len.data(), c->stream);
     if (rc) return rc;
   }
   const Config &g = c->cfg;
@@ -293,15 +293,319 @@ hipEvent_t *probe_slot(dn_ctx *c, int l) {
     if (slot) HIPCHK(c, "hipEventRecord", hipEventRecord((slot)[2 * (k) + 1], s)); \
   } while (0)
 
+// The tokens one stream works on: a workspace (for one part of a split
+// forward, a view at the part's token offset into the context's buffers),
+// those tokens' ids / positions / option ids, and the stream.
+struct Pass {
+  Workspace w;
+  const int32_t *ids, *pos, *opt;
+  hipStream_t s;
+};
+
+// Token info, 32-token chunk summaries, attention tile classes of both layer
+// types, and the embedding gather + emb norm into cur (fp32) and xn0.
+int enqueue_prologue(dn_ctx *c, const Pass &p, float *cur, void *xn0, float *emb_mean, float *emb_rstd) {
+  const Config &g = c->cfg;
+  const Workspace &w = p.w;
+  hipStream_t s = p.s;
+  HIPCHK(c, "token_info", launch_token_info(p.pos, p.opt, w.kinfo, w.T, (int *)c->err_flag.p, s));
+  HIPCHK(c, "chunk_summary", launch_chunk_summary(w.kinfo, w.chunk_desc, w.chunks, w.nchunks, s));
+  const size_t nw = (size_t)w.nwork;
+  for (int sl = 0; sl < 2; sl++)  // global, then local
+    HIPCHK(c, "tile_codes", launch_tile_codes(w.chunks, w.work, w.seq_len, w.chunk_off, w.nwork, sl, g.half_window,
+                                              w.codes + sl * nw * ATTN_MAXKT, w.first + sl * nw, s));
+  HIPCHK(c, "embed_ln",
+         launch_embed_ln(g.precision, p.ids, w.T, (const float *)W(c, "model.embeddings.tok_embeddings.weight"),
+                         g.vocab, (const float *)W(c, "model.embeddings.norm.weight"), g.eps, g.hidden, cur, xn0,
+                         (int *)c->err_flag.p, s, emb_mean, emb_rstd));
+  return DN_OK;
+}
+
+// The launches of encoder layer l over the pass's tokens: the residual stream
+// enters in `in`, leaves the attention half in h1 and the layer in out (the
+// same buffer unless training keeps them apart); x1 is the QKV input of layer
+// 0 (the embedding output; later layers normalise `in` into the workspace).
+// S (training) receives the layer's activations; ev brackets the five probed
+// launches.
+int enqueue_layer(dn_ctx *c, const Pass &p, int l, float *in, float *h1, float *out, void *x1, LayerSave *S,
+                  hipEvent_t *ev) {
+  const Config &g = c->cfg;
+  const int H = g.hidden, I = g.inter, prec = g.precision;
+  const Workspace &w = p.w;
+  const int T = w.T;
+  hipStream_t s = p.s;
+  const std::string pf = layer_prefix(l);
+  const bool sliding = g.sliding[l] != 0;
+  if (l > 0) {
+    x1 = S ? S->n1.p : w.xn;
+    HIPCHK(c, "ln(attn_norm)",
+           launch_ln(prec, in, T, H, (const float *)W(c, pf + "attn_norm.weight"), g.eps, x1, s,
+                     S ? (float *)S->mean1.p : nullptr, S ? (float *)S->rstd1.p : nullptr));
+  }
+  GemmArgs q{};
+  q.A = x1;
+  q.lda = H;
+  q.B = W(c, pf + "attn.Wqkv.weight");
+  q.ldb = H;
+  q.C = S ? S->qkv.p : w.qkv;
+  q.ldc = 3 * H;
+  q.M = T;
+  q.N = 3 * H;
+  q.K = H;
+  q.n_store = 3 * H;
+  PROBED(ev, DN_PROBE_QKV, "gemm(Wqkv)", launch_gemm(prec, EPI_STORE, q, s));
+
+  const float *rope = (const float *)c->rope.p;
+  const size_t tab = (size_t)kPositions * 32;
+  AttnArgs at{};
+  at.kinfo = w.kinfo;
+  at.work = w.work;
+  at.seq_off = w.seq_off;
+  at.seq_len = w.seq_len;
+  at.nwork = w.nwork;
+  at.H = H;
+  at.heads = g.heads;
+  at.half_window = g.half_window;
+  at.scale_log2 = (float)(1.0 / std::sqrt(64.0)) * 1.44269504088896340736f;
+  at.qkv = q.C;
+  at.ctx = S ? S->ctx.p : w.ctx;
+  at.lse = S ? (float *)S->lse.p : nullptr;
+  at.sliding = sliding ? 1 : 0;
+  at.codes = w.codes + (sliding ? (size_t)w.nwork * ATTN_MAXKT : 0);
+  at.first = w.first + (sliding ? w.nwork : 0);
+  at.cos_t = rope + (sliding ? 2 : 0) * tab;  // the layer type picks the table (forward.go:297-301)
+  at.sin_t = rope + (sliding ? 3 : 1) * tab;
+  PROBED(ev, DN_PROBE_ATTENTION, "attention", launch_attention(prec, at, s));
+
+  GemmArgs o{};
+  o.A = at.ctx;
+  o.lda = H;
+  o.B = W(c, pf + "attn.Wo.weight");
+  o.ldb = H;
+  o.C = h1;
+  o.res = h1 == in ? nullptr : in;
+  o.ldc = H;
+  o.M = T;
+  o.N = H;
+  o.K = H;
+  o.n_store = H;
+  o.accumulate = 1;
+  PROBED(ev, DN_PROBE_WO, "gemm(Wo)", launch_gemm(prec, EPI_F32, o, s));
+
+  void *x2 = S ? S->n2.p : w.xn;
+  HIPCHK(c, "ln(mlp_norm)", launch_ln(prec, h1, T, H, (const float *)W(c, pf + "mlp_norm.weight"), g.eps, x2, s,
+                                      S ? (float *)S->mean2.p : nullptr, S ? (float *)S->rstd2.p : nullptr));
+
+  GemmArgs wi{};
+  wi.A = x2;
+  wi.lda = H;
+  wi.B = W(c, pf + "mlp.Wi.weight");
+  wi.ldb = H;
+  wi.M = T;
+  wi.N = 2 * I;
+  wi.K = H;
+  wi.n_store = 2 * I;
+  if (S) {  // training keeps the pre-activation as well as the GeGLU output
+    wi.C = S->wi.p;
+    wi.ldc = 2 * I;
+    wi.C2 = S->act.p;
+    wi.ldc2 = I;
+    PROBED(ev, DN_PROBE_WI, "gemm(Wi)", launch_gemm(prec, EPI_GEGLU_KEEP, wi, s));
+  } else {
+    wi.C = w.act;
+    wi.ldc = I;
+    PROBED(ev, DN_PROBE_WI, "gemm(Wi)", launch_gemm(prec, EPI_GEGLU, wi, s));
+  }
+
+  GemmArgs mo{};
+  mo.A = S ? S->act.p : w.act;
+  mo.lda = I;
+  mo.B = W(c, pf + "mlp.Wo.weight");
+  mo.ldb = I;
+  mo.C = out;
+  mo.res = out == h1 ? nullptr : h1;
+  mo.ldc = H;
+  mo.M = T;
+  mo.N = H;
+  mo.K = I;
+  mo.n_store = H;
+  mo.accumulate = 1;
+  PROBED(ev, DN_PROBE_MLPWO, "gemm(MlpWo)", launch_gemm(prec, EPI_F32, mo, s));
+  return DN_OK;
+}
+
+// The scorer head over the R option rows (row_tok: indices into the T_total
+// tokens of h).
+int enqueue_head(dn_ctx *c, const float *h, int T_total, const int32_t *row_tok, int R, float *logits, float *s1,
+                 float *d, hipStream_t s) {
+  const Config &g = c->cfg;
+  HeadArgs ha{};
+  ha.h = h;
+  ha.row_tok = row_tok;
+  ha.R = R;
+  ha.T = T_total;
+  ha.H = g.hidden;
+  ha.eps = g.eps;
+  ha.final_norm = (const float *)W(c, "model.final_norm.weight");
+  ha.in_w = (const float *)W(c, "scorer.input_norm.weight");
+  ha.in_b = (const float *)W(c, "scorer.input_norm.bias");
+  ha.dense_w = (const float *)W(c, "scorer.dense.weight");
+  ha.dense_b = (const float *)W(c, "scorer.dense.bias");
+  ha.norm_w = (const float *)W(c, "scorer.norm.weight");
+  ha.norm_b = (const float *)W(c, "scorer.norm.bias");
+  ha.out_w = (const float *)W(c, "scorer.out_proj.weight");
+  ha.out_b = (const float *)W(c, "scorer.out_proj.bias");
+  ha.logits = logits;
+  ha.err_flag = (int *)c->err_flag.p;
+  HIPCHK(c, "head", launch_head(ha, s1, d, s));
+  return DN_OK;
+}
+
+// The layout arrays of part k (sequences seq_len[0..nseq)), rebuilt and
+// uploaded on stream s only when its sequence lengths change; fills the
+// layout fields of w.
+int part_layout(dn_ctx *c, int k, int nseq, const int32_t *seq_len, hipStream_t s, Workspace *w) {
+  PartLayout &P = c->parts[k];
+  std::vector<int> len(seq_len, seq_len + nseq);
+  const bool same = len == P.len && P.d_seq_off.p;
+  if (!same) {
+    int T = 0, nch = 0;
+    host_layout(P.hl, nseq, seq_len, &T, &nch);
+    const size_t nw = P.hl.work.size();
+    HIPCHK(c, "hipMalloc", ensure(P.d_seq_off, sizeof(int) * (nseq + 1)));
+    HIPCHK(c, "hipMalloc", ensure(P.d_seq_len, sizeof(int) * (nseq + 1)));
+    HIPCHK(c, "hipMalloc", ensure(P.d_chunk_off, sizeof(int) * (nseq + 1)));
+    HIPCHK(c, "hipMalloc", ensure(P.d_chunk_desc, sizeof(int4) * (nch + 1)));
+    HIPCHK(c, "hipMalloc", ensure(P.d_chunks, sizeof(ChunkInfo) * (nch + 1)));
+    HIPCHK(c, "hipMalloc", ensure(P.d_work, sizeof(int4) * (nw + 1)));
+    HIPCHK(c, "hipMalloc", ensure(P.d_codes, sizeof(uint32_t) * 2 * ATTN_MAXKT * (nw + 1)));
+    HIPCHK(c, "hipMalloc", ensure(P.d_first, sizeof(int) * 2 * (nw + 1)));
+    P.len = len;
+    P.T = T;
+    P.nchunks = nch;
+    P.nwork = (int)nw;
+  }
+  w->seq_off = (int *)P.d_seq_off.p;
+  w->seq_len = (int *)P.d_seq_len.p;
+  w->chunk_off = (int *)P.d_chunk_off.p;
+  w->chunk_desc = (int4 *)P.d_chunk_desc.p;
+  w->chunks = (ChunkInfo *)P.d_chunks.p;
+  w->work = (int4 *)P.d_work.p;
+  w->codes = (uint32_t *)P.d_codes.p;
+  w->first = (int *)P.d_first.p;
+  w->T = P.T;
+  w->nchunks = P.nchunks;
+  w->nwork = P.nwork;
+  if (!same) return upload_layout(c, P.hl, *w, nseq, P.len.data(), s);
+  return DN_OK;
+}
+
+// Inference forward of a large batch in two parts of whole sequences (about
+// half the tokens each), the first on the context's stream and the second on
+// aux_stream, layer by layer in alternation, so that one part's kernels fill
+// the GPU around the other's (a residual GEMM's HBM-bound epilogue beside a
+// projection GEMM's MFMA-bound main loop). Every kernel sees exactly the
+// tokens it would see in the single-stream forward, so the logits are the
+// same; the head runs once over all rows after the join.
+// The sequence index that cuts a batch nearest half of its tokens (both
+// parts non-empty); *first_tokens receives the first part's token count.
+int split_point(int nseq, const int32_t *seq_len, int T_total, int *first_tokens) {
+  int cut = 1, acc = seq_len[0];
+  while (cut < nseq - 1 && 2 * (acc + seq_len[cut]) <= T_total) acc += seq_len[cut++];
+  if (cut < nseq - 1 && std::abs(2 * (acc + seq_len[cut]) - T_total) < std::abs(2 * acc - T_total))
+    acc += seq_len[cut++];
+  *first_tokens = acc;
+  return cut;
+}
+
+// Smallest part of a split forward: above it every GEMM of a part runs the
+// tiled kernels of the single-stream forward (small M runs the small-M
+// kernels, whose summation order differs), so the logits are identical.
+constexpr int kMinPartTokens = 1025;
+
+int forward_split(dn_ctx *c, int nseq, const int32_t *seq_len, const int32_t *d_ids, const int32_t *d_pos,
+                  const int32_t *d_opt, int R, const int32_t *d_row_tok, float *d_logits, int T_total, int cut,
+                  int acc) {
+  const Config &g = c->cfg;
+  const int H = g.hidden, I = g.inter, L = g.layers;
+  const size_t es = g.precision == DN_PRECISION_BF16 ? 2 : 4;
+  const int cnt[2] = {cut, nseq - cut}, tok0[2] = {0, acc};
+  if (!c->aux_stream) {
+    HIPCHK(c, "hipStreamCreate", hipStreamCreateWithFlags(&c->aux_stream, hipStreamNonBlocking));
+    HIPCHK(c, "hipEventCreate", hipEventCreateWithFlags(&c->ev_fork, hipEventDisableTiming));
+    HIPCHK(c, "hipEventCreate", hipEventCreateWithFlags(&c->ev_join, hipEventDisableTiming));
+  }
+  const hipStream_t st[2] = {c->stream, c->aux_stream};
+  // Shared activation buffers for all tokens; each part works at its offset.
+  const size_t T = (size_t)T_total;
+  HIPCHK(c, "hipMalloc", ensure(c->h, sizeof(float) * T * H));
+  HIPCHK(c, "hipMalloc", ensure(c->xn, es * T * H));
+  HIPCHK(c, "hipMalloc", ensure(c->qkv, es * T * 3 * H));
+  HIPCHK(c, "hipMalloc", ensure(c->ctxb, es * T * H));
+  HIPCHK(c, "hipMalloc", ensure(c->act, es * T * I));
+  HIPCHK(c, "hipMalloc", ensure(c->kinfo, sizeof(int) * T));
+  HIPCHK(c, "hipMalloc", ensure(c->head_s1, sizeof(float) * (size_t)std::max(R, 1) * H));
+  HIPCHK(c, "hipMalloc", ensure(c->head_d, sizeof(float) * (size_t)std::max(R, 1) * (H / 2)));
+  int rc = ensure_err_flag(c);
+  if (rc) return rc;
+  rc = ensure_rope(c);
+  if (rc) return rc;
+  // The aux stream starts after everything already queued on the context's
+  // stream (the caller's uploads of the token arrays among it).
+  HIPCHK(c, "hipEventRecord", hipEventRecord(c->ev_fork, st[0]));
+  HIPCHK(c, "hipStreamWaitEvent", hipStreamWaitEvent(st[1], c->ev_fork, 0));
+  Pass ps[2];
+  for (int k = 0; k < 2; k++) {
+    const int32_t *sl = seq_len + (k ? cut : 0);
+    const bool changed = c->parts[k].len != std::vector<int>(sl, sl + cnt[k]);
+    if (changed) HIPCHK(c, "hipStreamSynchronize", hipStreamSynchronize(st[k]));  // host staging may be in flight
+    rc = part_layout(c, k, cnt[k], sl, st[k], &ps[k].w);
+    if (rc) return rc;
+    const size_t t0 = (size_t)tok0[k];
+    Workspace &w = ps[k].w;
+    w.h = (float *)c->h.p + t0 * H;
+    w.xn = (char *)c->xn.p + es * t0 * H;
+    w.qkv = (char *)c->qkv.p + es * t0 * 3 * H;
+    w.ctx = (char *)c->ctxb.p + es * t0 * H;
+    w.act = (char *)c->act.p + es * t0 * I;
+    w.kinfo = (int *)c->kinfo.p + t0;
+    ps[k].ids = d_ids + t0;
+    ps[k].pos = d_pos + t0;
+    ps[k].opt = d_opt ? d_opt + t0 : nullptr;
+    ps[k].s = st[k];
+    rc = enqueue_prologue(c, ps[k], w.h, w.xn, nullptr, nullptr);
+    if (rc) return rc;
+  }
+  for (int l = 0; l < L; l++)
+    for (int k = 0; k < 2; k++) {
+      rc = enqueue_layer(c, ps[k], l, ps[k].w.h, ps[k].w.h, ps[k].w.h, ps[k].w.xn, nullptr, nullptr);
+      if (rc) return rc;
+    }
+  HIPCHK(c, "hipEventRecord", hipEventRecord(c->ev_join, st[1]));
+  HIPCHK(c, "hipStreamWaitEvent", hipStreamWaitEvent(st[0], c->ev_join, 0));
+  return enqueue_head(c, (const float *)c->h.p, T_total, d_row_tok, R, d_logits, (float *)c->head_s1.p,
+                      (float *)c->head_d.p, st[0]);
+}
+
 int forward_core(dn_ctx *c, int nseq, const int32_t *seq_len, const int32_t *d_ids, const int32_t *d_pos,
                  const int32_t *d_opt, int R, const int32_t *d_row_tok, float *d_logits, bool train,
                  const Workspace *ws) {
   const Config &g = c->cfg;
   const int H = g.hidden, I = g.inter, L = g.layers;
-  const int prec = g.precision;
-  const size_t es = prec == DN_PRECISION_BF16 ? 2 : 4;
+  const size_t es = g.precision == DN_PRECISION_BF16 ? 2 : 4;
   TrainState &tr = c->tr;
   tr.have_forward = false;  // any forward replaces the layout and the encoder output
+  if (!ws && !train && c->probe_layer < 0 && nseq >= 2 && c->split_min_tokens > 0) {
+    long long T_total = 0;
+    for (int i = 0; i < nseq; i++) T_total += seq_len[i];
+    if (T_total >= c->split_min_tokens) {
+      int first = 0;
+      const int cut = split_point(nseq, seq_len, (int)T_total, &first);
+      if (first >= kMinPartTokens && T_total - first >= kMinPartTokens)
+        return forward_split(c, nseq, seq_len, d_ids, d_pos, d_opt, R, d_row_tok, d_logits, (int)T_total, cut,
+                             first);
+    }
+  }
   Workspace w;
   int rc = DN_OK;
   if (ws) {
@@ -311,7 +615,6 @@ int forward_core(dn_ctx *c, int nseq, const int32_t *seq_len, const int32_t *d_i
     if (rc) return rc;
   }
   const int T = w.T;
-  hipStream_t s = c->stream;
   if (train) {
     tr.layers.resize(L);
     for (int l = tr.train_from; l < L; l++) {
@@ -337,163 +640,39 @@ int forward_core(dn_ctx *c, int nseq, const int32_t *seq_len, const int32_t *d_i
   rc = ensure_rope(c);
   if (rc) return rc;
 
-  float *h = w.h;
-  const float *rope = (const float *)c->rope.p;
-  const float *cos_g = rope, *sin_g = rope + (size_t)kPositions * 32, *cos_l = rope + (size_t)2 * kPositions * 32,
-              *sin_l = rope + (size_t)3 * kPositions * 32;
-  int *kinfo = w.kinfo;
-
-  HIPCHK(c, "token_info", launch_token_info(d_pos, d_opt, kinfo, T, (int *)c->err_flag.p, s));
-  HIPCHK(c, "chunk_summary", launch_chunk_summary(kinfo, w.chunk_desc, w.chunks, w.nchunks, s));
-  // Attention tile classes for the two layer types (global, then local).
-  uint32_t *codes = w.codes;
-  int *first = w.first;
-  const size_t nw = (size_t)w.nwork;
-  for (int sl = 0; sl < 2; sl++)
-    HIPCHK(c, "tile_codes", launch_tile_codes(w.chunks, w.work, w.seq_len, w.chunk_off, w.nwork, sl, g.half_window,
-                                              codes + sl * nw * ATTN_MAXKT, first + sl * nw, s));
+  Pass ps;
+  ps.w = w;
+  ps.ids = d_ids;
+  ps.pos = d_pos;
+  ps.opt = d_opt;
+  ps.s = c->stream;
   // Training keeps each saved layer's input in its own buffer (LayerSave::hs)
   // and its post-attention residual in LayerSave::h1: the residual GEMMs read
   // one and write the next, so the residual stream moves through the saved
-  // buffers without copies; unsaved layers update c->h in place.
+  // buffers without copies; unsaved layers update the workspace's h in place.
   auto saved = [&](int l) -> LayerSave * { return train && l >= tr.train_from && l < L ? &tr.layers[l] : nullptr; };
+  float *h = w.h;
   float *cur = saved(0) ? (float *)saved(0)->hs.p : h;  // the residual stream entering layer 0
   void *xn0 = saved(0) ? saved(0)->n1.p : w.xn;         // layer 0's QKV input (no attn_norm)
-  HIPCHK(c, "embed_ln",
-         launch_embed_ln(prec, d_ids, T, (const float *)W(c, "model.embeddings.tok_embeddings.weight"), g.vocab,
-                         (const float *)W(c, "model.embeddings.norm.weight"), g.eps, H, cur, xn0,
-                         (int *)c->err_flag.p, s, train ? (float *)tr.emb_mean.p : nullptr,
-                         train ? (float *)tr.emb_rstd.p : nullptr));
-
-  AttnArgs at{};
-  at.kinfo = kinfo;
-  at.work = w.work;
-  at.seq_off = w.seq_off;
-  at.seq_len = w.seq_len;
-  at.nwork = w.nwork;
-  at.H = H;
-  at.heads = g.heads;
-  at.half_window = g.half_window;
-  at.scale_log2 = (float)(1.0 / std::sqrt(64.0)) * 1.44269504088896340736f;
-
+  rc = enqueue_prologue(c, ps, cur, xn0, train ? (float *)tr.emb_mean.p : nullptr,
+                        train ? (float *)tr.emb_rstd.p : nullptr);
+  if (rc) return rc;
   bool probed = false;
   for (int l = 0; l < L; l++) {
-    const std::string p = layer_prefix(l);
-    const bool sliding = g.sliding[l] != 0;
     hipEvent_t *ev = ws ? nullptr : probe_slot(c, l);  // the probe creates events: not in a caller's workspace
     probed |= ev != nullptr;
     // Training keeps this layer's activations (layers >= train_from).
     LayerSave *S = saved(l);
-    float *in = cur;                                // this layer's input (S->hs when saved)
-    float *h1 = S ? (float *)S->h1.p : in;          // residual after attention
+    float *in = cur;                                              // this layer's input (S->hs when saved)
+    float *h1 = S ? (float *)S->h1.p : in;                        // residual after attention
     float *out = saved(l + 1) ? (float *)saved(l + 1)->hs.p : h;  // the layer's output
-    void *x1 = xn0;  // QKV input: attn_norm(in), or for layer 0 the embedding output
-    if (l > 0) {
-      x1 = S ? S->n1.p : w.xn;
-      HIPCHK(c, "ln(attn_norm)",
-             launch_ln(prec, in, T, H, (const float *)W(c, p + "attn_norm.weight"), g.eps, x1, s,
-                       S ? (float *)S->mean1.p : nullptr, S ? (float *)S->rstd1.p : nullptr));
-    }
-    GemmArgs q{};
-    q.A = x1;
-    q.lda = H;
-    q.B = W(c, p + "attn.Wqkv.weight");
-    q.ldb = H;
-    q.C = S ? S->qkv.p : w.qkv;
-    q.ldc = 3 * H;
-    q.M = T;
-    q.N = 3 * H;
-    q.K = H;
-    q.n_store = 3 * H;
-    PROBED(ev, DN_PROBE_QKV, "gemm(Wqkv)", launch_gemm(prec, EPI_STORE, q, s));
-
-    at.qkv = q.C;
-    at.ctx = S ? S->ctx.p : w.ctx;
-    at.lse = S ? (float *)S->lse.p : nullptr;
-    at.sliding = sliding ? 1 : 0;
-    at.codes = codes + (sliding ? nw * ATTN_MAXKT : 0);
-    at.first = first + (sliding ? nw : 0);
-    at.cos_t = sliding ? cos_l : cos_g;  // the layer type picks the table (forward.go:297-301)
-    at.sin_t = sliding ? sin_l : sin_g;
-    PROBED(ev, DN_PROBE_ATTENTION, "attention", launch_attention(prec, at, s));
-
-    GemmArgs o{};
-    o.A = at.ctx;
-    o.lda = H;
-    o.B = W(c, p + "attn.Wo.weight");
-    o.ldb = H;
-    o.C = h1;
-    o.res = h1 == in ? nullptr : in;
-    o.ldc = H;
-    o.M = T;
-    o.N = H;
-    o.K = H;
-    o.n_store = H;
-    o.accumulate = 1;
-    PROBED(ev, DN_PROBE_WO, "gemm(Wo)", launch_gemm(prec, EPI_F32, o, s));
-
-    void *x2 = S ? S->n2.p : w.xn;
-    HIPCHK(c, "ln(mlp_norm)", launch_ln(prec, h1, T, H, (const float *)W(c, p + "mlp_norm.weight"), g.eps, x2, s,
-                                        S ? (float *)S->mean2.p : nullptr, S ? (float *)S->rstd2.p : nullptr));
-
-    GemmArgs wi{};
-    wi.A = x2;
-    wi.lda = H;
-    wi.B = W(c, p + "mlp.Wi.weight");
-    wi.ldb = H;
-    wi.M = T;
-    wi.N = 2 * I;
-    wi.K = H;
-    wi.n_store = 2 * I;
-    if (S) {  // training keeps the pre-activation as well as the GeGLU output
-      wi.C = S->wi.p;
-      wi.ldc = 2 * I;
-      wi.C2 = S->act.p;
-      wi.ldc2 = I;
-      PROBED(ev, DN_PROBE_WI, "gemm(Wi)", launch_gemm(prec, EPI_GEGLU_KEEP, wi, s));
-    } else {
-      wi.C = w.act;
-      wi.ldc = I;
-      PROBED(ev, DN_PROBE_WI, "gemm(Wi)", launch_gemm(prec, EPI_GEGLU, wi, s));
-    }
-
-    GemmArgs mo{};
-    mo.A = S ? S->act.p : w.act;
-    mo.lda = I;
-    mo.B = W(c, p + "mlp.Wo.weight");
-    mo.ldb = I;
-    mo.C = out;
-    mo.res = out == h1 ? nullptr : h1;
-    mo.ldc = H;
-    mo.M = T;
-    mo.N = H;
-    mo.K = I;
-    mo.n_store = H;
-    mo.accumulate = 1;
-    PROBED(ev, DN_PROBE_MLPWO, "gemm(MlpWo)", launch_gemm(prec, EPI_F32, mo, s));
+    rc = enqueue_layer(c, ps, l, in, h1, out, xn0, S, ev);
+    if (rc) return rc;
     cur = out;
   }
   if (probed) c->probe_used++;
-
-  HeadArgs ha{};
-  ha.h = h;
-  ha.row_tok = d_row_tok;
-  ha.R = R;
-  ha.T = T;
-  ha.H = H;
-  ha.eps = g.eps;
-  ha.final_norm = (const float *)W(c, "model.final_norm.weight");
-  ha.in_w = (const float *)W(c, "scorer.input_norm.weight");
-  ha.in_b = (const float *)W(c, "scorer.input_norm.bias");
-  ha.dense_w = (const float *)W(c, "scorer.dense.weight");
-  ha.dense_b = (const float *)W(c, "scorer.dense.bias");
-  ha.norm_w = (const float *)W(c, "scorer.norm.weight");
-  ha.norm_b = (const float *)W(c, "scorer.norm.bias");
-  ha.out_w = (const float *)W(c, "scorer.out_proj.weight");
-  ha.out_b = (const float *)W(c, "scorer.out_proj.bias");
-  ha.logits = d_logits;
-  ha.err_flag = (int *)c->err_flag.p;
-  HIPCHK(c, "head", launch_head(ha, w.head_s1, w.head_d, s));
+  rc = enqueue_head(c, h, T, d_row_tok, R, d_logits, w.head_s1, w.head_d, ps.s);
+  if (rc) return rc;
   if (train) {
     tr.have_forward = true;
     tr.T = T;
@@ -694,6 +873,14 @@ void dn_close(dn_ctx *c) {
                     &c->d_seq_len, &c->d_chunk_off, &c->d_chunk_desc, &c->d_work, &c->d_chunks,
                     &c->d_codes,   &c->d_first, &c->calib};
   for (DevBuf *b : bufs) release(*b);
+  for (PartLayout &P : c->parts)
+    for (DevBuf *b : {&P.d_seq_off, &P.d_seq_len, &P.d_chunk_off, &P.d_chunk_desc, &P.d_chunks, &P.d_work,
+                      &P.d_codes, &P.d_first})
+      release(*b);
+  if (c->aux_stream) (void)hipStreamSynchronize(c->aux_stream);
+  if (c->aux_stream) (void)hipStreamDestroy(c->aux_stream);
+  if (c->ev_fork) (void)hipEventDestroy(c->ev_fork);
+  if (c->ev_join) (void)hipEventDestroy(c->ev_join);
   if (c->own_stream) (void)hipStreamDestroy(c->own_stream);
   delete c;
 }
@@ -943,6 +1130,13 @@ int dn_gemm_device(dn_ctx *c, int precision, int M, int N, int K, const void *d_
   a.n_store = N;
   a.accumulate = accumulate ? 1 : 0;
   HIPCHK(c, "gemm", launch_gemm(precision, EPI_F32, a, c->stream));
+  return DN_OK;
+}
+
+int dn_set_stream_split(dn_ctx *c, int min_tokens) {
+  if (!c || min_tokens < 0) return DN_INVALID_ARG;
+  c->err.clear();
+  c->split_min_tokens = min_tokens;
   return DN_OK;
 }
 

@@ -96,6 +96,25 @@ struct Workspace {
   int T = 0, nchunks = 0, nwork = 0;
 };
 
+// The batch layout on the host: token offset and 32-token chunk offset of
+// each sequence, the chunks (first token, length) and the attention work
+// items (sequence, first query).
+struct HostLayout {
+  std::vector<int> seq_off, chunk_off;
+  std::vector<int4> chunk_desc, work;
+};
+
+// One part of a forward split over two streams: its sequences' layout and
+// device layout arrays (the activation buffers are the context's, at the
+// part's token offset).
+struct PartLayout {
+  std::vector<int> len;
+  HostLayout hl;
+  DevBuf d_seq_off, d_seq_len, d_chunk_off, d_chunk_desc, d_chunks, d_work, d_codes, d_first;
+  int T = 0, nchunks = 0, nwork = 0;
+};
+constexpr int kMaxParts = 2;
+
 struct dn_ctx {
   int device = 0;
   hipStream_t stream = nullptr;
@@ -114,10 +133,16 @@ struct dn_ctx {
   DevBuf gA, gB, gC;  // dn_gemm_f32 staging
   DevBuf calib;       // dn_mfma_calibrate's result sink
   void *scratch = nullptr;  // this device's static scratch array (noalloc.cpp), from hipGetSymbolAddress
+  // Forwards of large batches run in two parts of whole sequences, one per
+  // stream (the context's and aux_stream, created on first use at the
+  // default priority), so the kernels of one part overlap the other's.
+  PartLayout parts[kMaxParts];
+  hipStream_t aux_stream = nullptr;
+  hipEvent_t ev_fork = nullptr, ev_join = nullptr;
+  int split_min_tokens = 8192;  // batches from this many tokens (and >= 2 sequences) are split
   // batch layout cache
   std::vector<int> lay_len;
-  std::vector<int> h_seq_off, h_chunk_off;
-  std::vector<int4> h_chunk_desc, h_work;
+  HostLayout hlay;
   DevBuf d_seq_off, d_seq_len, d_chunk_off, d_chunk_desc, d_work, d_chunks;
   DevBuf d_codes, d_first;  // attention tile classes per work item: [global | local]
   int lay_T = 0, lay_nchunks = 0, lay_nwork = 0;
@@ -156,11 +181,12 @@ int stage_batch(dn_ctx *c, int nseq, const int32_t *seq_len, const int32_t *ids,
 int forward_core(dn_ctx *c, int nseq, const int32_t *seq_len, const int32_t *d_ids, const int32_t *d_pos,
                  const int32_t *d_opt, int R, const int32_t *d_row_tok, float *d_logits, bool train,
                  const Workspace *ws = nullptr);
-// The batch layout on the host (c->h_seq_off, h_chunk_off, h_chunk_desc,
-// h_work); *T and *nchunks receive the token and 32-token chunk counts.
-void host_layout(dn_ctx *c, int nseq, const int32_t *seq_len, int *T, int *nchunks);
-// Copies the host layout of the last host_layout call into w's device arrays.
-int upload_layout(dn_ctx *c, const Workspace &w, int nseq, const int32_t *seq_len);
+// The batch layout of nseq sequences on the host; *T and *nchunks receive
+// the token and 32-token chunk counts.
+void host_layout(HostLayout &hl, int nseq, const int32_t *seq_len, int *T, int *nchunks);
+// Copies a host layout into w's device arrays on stream s.
+int upload_layout(dn_ctx *c, const HostLayout &hl, const Workspace &w, int nseq, const int32_t *seq_len,
+                  hipStream_t s);
 // RoPE tables of the configured thetas and the device error flag: built at
 // set-up (dn_set_config), so forwards allocate neither.
 int ensure_rope(dn_ctx *c);

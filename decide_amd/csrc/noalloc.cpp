@@ -70,8 +70,8 @@ extern "C" int dn_forward_device_noalloc(dn_ctx *c, int nseq, const int32_t *seq
   // out of them must have finished.
   HIPCHK(c, "hipStreamSynchronize", hipStreamSynchronize(c->stream));
   int T = 0, nch = 0;
-  host_layout(c, nseq, seq_len, &T, &nch);
-  const int nwork = (int)c->h_work.size();
+  host_layout(c->hlay, nseq, seq_len, &T, &nch);
+  const int nwork = (int)c->hlay.work.size();
   const Config &g = c->cfg;
   const size_t es = g.precision == DN_PRECISION_BF16 ? 2 : 4, H = g.hidden, I = g.inter, Tz = T;
   const size_t R1 = (size_t)(nrows > 0 ? nrows : 1);
@@ -111,7 +111,7 @@ extern "C" int dn_forward_device_noalloc(dn_ctx *c, int nseq, const int32_t *seq
   w.T = T;
   w.nchunks = nch;
   w.nwork = nwork;
-  rc = upload_layout(c, w, nseq, seq_len);
+  rc = upload_layout(c, c->hlay, w, nseq, seq_len, c->stream);
   if (rc) return rc;
   return forward_core(c, nseq, seq_len, d_ids, d_pos, d_opt_id, nrows, d_row_tok, d_logits, false, &w);
 }

@@ -263,6 +263,10 @@ class Engine:
         check(lib.dn_read_probe(self._h, _ptr(ms), ctypes.byref(cnt)), self._h)
         return dict(zip(self.PROBE_NAMES, ms.tolist())), cnt.value
 
+    def set_stream_split(self, min_tokens: int) -> None:
+        """dn_set_stream_split: batches of >= min_tokens tokens run in two parts on two streams (0: off)."""
+        check(lib.dn_set_stream_split(self._h, int(min_tokens)), self._h)
+
     def mfma_calibrate(self, mode: int = 0) -> float:
         """dn_mfma_calibrate: attainable bf16 MFMA TFLOP/s (mode 0 changing operands, 1 constant)."""
         out = ctypes.c_double(0.0)

@@ -165,6 +165,17 @@ int dn_gemm_f32(dn_ctx *ctx, int transA, int transB, int M, int N, int K, const 
 int dn_gemm_device(dn_ctx *ctx, int precision, int M, int N, int K, const void *d_A, const void *d_B,
                    float *d_C, int accumulate);
 
+/* Inference forwards (dn_forward, dn_forward_device, dn_evaluate) of batches
+ * with at least min_tokens tokens and two or more sequences run in two parts
+ * of whole sequences (cut nearest half the tokens; both parts must exceed
+ * 1024 tokens), one on the context's stream and one on a second stream
+ * of the context (default priority), layer by layer in alternation, joined
+ * before the scorer head: one part's kernels fill the GPU around the other's.
+ * The logits are the same as the single-stream forward's. 0 turns it off; the
+ * default is 8192. While a kernel probe is enabled (dn_set_probe) forwards
+ * run on one stream. No counterpart in the reference. */
+int dn_set_stream_split(dn_ctx *ctx, int min_tokens);
+
 /* Waits for the context's stream. */
 int dn_synchronize(dn_ctx *ctx);
 

@@ -385,3 +385,40 @@ def test_argmax_agreement_1000_requests(base, engines):
         assert dp <= dp_bar
         assert agree >= agree_bar
         assert not any(decisive[i] for i in flips)
+
+
+def test_stream_split_matches_single_stream(base, engines):
+    """dn_set_stream_split: a batch run in two parts on two streams gives the
+    single-stream forward's logits bit for bit (each kernel sees the same
+    tokens; parts above 1024 tokens run the same GEMM kernels), for the cfg3
+    batch, an odd, ragged batch and one whose cut falls after a long
+    sequence (2816 tokens, then 20 x 64); through dn_forward and
+    dn_forward_device."""
+    import torch
+
+    from decide_amd.nn import build_sequence, flatten, row_tokens
+    from decide_amd.synth import config_batch, pack_request
+
+    cfg = base[0]
+    rng = np.random.default_rng(77)
+    ragged = [build_sequence(pack_request(rng, int(p), [int(k)] * int(m), cfg.vocab), 50284, True)
+              for p, k, m in zip(rng.integers(40, 900, 9), rng.integers(3, 20, 9), rng.integers(1, 9, 9))]
+    lopsided = config_batch("cfg4", vocab=cfg.vocab, nseq=1) + config_batch("cfg5", vocab=cfg.vocab) * 20
+    for p in ("bf16", "fp32"):
+        eng = engines[p]
+        for batch in (config_batch("cfg3", vocab=cfg.vocab), ragged, lopsided):
+            eng.set_stream_split(0)
+            one = eng.forward(batch)
+            eng.set_stream_split(1)
+            two = eng.forward(batch)
+            assert np.array_equal(one, two), (p, len(batch), float(np.max(np.abs(one - two))))
+            seq_len, ids, pos, opt, nmask, _ = flatten(batch)
+            d = {k: torch.from_numpy(v).cuda() for k, v in dict(ids=ids, pos=pos, opt=opt,
+                                                                 rt=row_tokens(batch)).items()}
+            out = torch.zeros(len(one), dtype=torch.float32, device="cuda")
+            torch.cuda.synchronize()
+            eng.forward_device(seq_len, d["ids"].data_ptr(), d["pos"].data_ptr(), d["opt"].data_ptr(), len(one),
+                               d["rt"].data_ptr(), out.data_ptr())
+            eng.check_device_errors()
+            assert np.array_equal(out.cpu().numpy(), one)
+        eng.set_stream_split(8192)
