@@ -57,6 +57,7 @@ template <int R>
 struct Staging<bf16, R> {
   uint4 k_lo[R], k_hi[R], v0[R], v1[R];
   float4 c_lo[R], c_hi[R], s_lo[R], s_hi[R];
+  uint32_t valid;  // bit j: K item j's key, 8+j / 16+j: V item j's two keys exist (zeroed at the store)
   int info;
 };
 
@@ -66,6 +67,7 @@ template <int R>
 struct Staging<float, R> {
   uint4 k_lo[2 * R], k_hi[2 * R], v[4 * R];
   float4 c[2 * R], s[2 * R];
+  uint32_t valid;  // bit j: K item j's key, 8+j: V item j's key exists (zeroed at the store)
   int info;
 };
 
@@ -75,26 +77,51 @@ __device__ __forceinline__ uint4 keep_if(bool ok, uint4 v) {
   return make_uint4(ok ? v.x : 0u, ok ? v.y : 0u, ok ? v.z : 0u, ok ? v.w : 0u);
 }
 
+// The per-token info (((opt+1) << 16) | pos) a thread needs to stage a key
+// tile: the positions of its K items' keys (they index the RoPE tables) and,
+// for the first 64 threads, key k0 + tid (the tile's mask info). Loaded one
+// tile ahead of the K / V / RoPE loads, so that the position-dependent table
+// loads issue at once instead of waiting for a dependent load every tile.
+template <class T, int R>
+struct KeyInfo {
+  static constexpr int KI = sizeof(T) == 2 ? R : 2 * R;  // K items per thread
+  int pk[KI];
+  int pi;
+};
+
+template <class T, int R>
+__device__ __forceinline__ void key_info_load(KeyInfo<T, R> &f, const int *kinfo, int base, int n, int k0, int tid) {
+  constexpr int NT = 256 / R, SH = sizeof(T) == 2 ? 2 : 3;  // K item it -> key it >> SH
+#pragma unroll
+  for (int j = 0; j < KeyInfo<T, R>::KI; j++) {
+    const int key = (tid + NT * j) >> SH;
+    f.pk[j] = kinfo[base + min(k0 + key, n - 1)];
+  }
+  f.pi = (tid < KTILE && k0 + tid < n) ? kinfo[base + k0 + tid] : 0;
+}
+
 // Loads one key tile (keys k0 .. k0+63) into registers; NT threads, R = 256/NT.
 template <class T, int R>
 __device__ __forceinline__ void stage_load(Staging<T, R> &st, const T *qkv, int ld, int H, int head, int base, int n,
-                                           int k0, const float *cos_t, const float *sin_t, const int *kinfo,
-                                           int tid) {
+                                           int k0, const float *cos_t, const float *sin_t,
+                                           const KeyInfo<T, R> &ki, int tid) {
   constexpr int NT = 256 / R;
   // Keys past the sequence end read the last key's row (in bounds) and are
   // zeroed; their RoPE factors are whatever that row has (results unused).
   // The RoPE tables are indexed by position (low 16 bits of the key's info).
+  // The loaded values are not touched here (a select on them would wait for
+  // the loads): keys past the sequence end are zeroed by stage_store.
+  st.valid = 0;
   if constexpr (sizeof(T) == 2) {
 #pragma unroll
     for (int j = 0; j < R; j++) {  // K: key = it / 4, chunk c = it % 4 (elements 8c..8c+7 and 32+8c..)
       const int it = tid + NT * j, key = it >> 2, c = it & 3;
-      const bool ok = k0 + key < n;
+      st.valid |= (k0 + key < n ? 1u : 0u) << j;
       const size_t tok = (size_t)(base + min(k0 + key, n - 1));
       const T *row = qkv + tok * ld + H + head * D;
-      const uint4 lo = *(const uint4 *)(row + 8 * c), hi = *(const uint4 *)(row + 32 + 8 * c);
-      st.k_lo[j] = keep_if(ok, lo);
-      st.k_hi[j] = keep_if(ok, hi);
-      const size_t p = (size_t)(kinfo[tok] & 0xffff);
+      st.k_lo[j] = *(const uint4 *)(row + 8 * c);
+      st.k_hi[j] = *(const uint4 *)(row + 32 + 8 * c);
+      const size_t p = (size_t)(ki.pk[j] & 0xffff);
       st.c_lo[j] = *(const float4 *)(cos_t + p * 32 + 8 * c);
       st.c_hi[j] = *(const float4 *)(cos_t + p * 32 + 8 * c + 4);
       st.s_lo[j] = *(const float4 *)(sin_t + p * 32 + 8 * c);
@@ -104,33 +131,31 @@ __device__ __forceinline__ void stage_load(Staging<T, R> &st, const T *qkv, int 
     for (int j = 0; j < R; j++) {  // V: key pair p = it % 32, d group g = it / 32
       const int it = tid + NT * j, p = it & 31, g = it >> 5;
       const int k = k0 + 2 * p;
-      const uint4 a = *(const uint4 *)(qkv + (size_t)(base + min(k, n - 1)) * ld + 2 * H + head * D + 8 * g);
-      const uint4 b = *(const uint4 *)(qkv + (size_t)(base + min(k + 1, n - 1)) * ld + 2 * H + head * D + 8 * g);
-      st.v0[j] = keep_if(k < n, a);
-      st.v1[j] = keep_if(k + 1 < n, b);
+      st.v0[j] = *(const uint4 *)(qkv + (size_t)(base + min(k, n - 1)) * ld + 2 * H + head * D + 8 * g);
+      st.v1[j] = *(const uint4 *)(qkv + (size_t)(base + min(k + 1, n - 1)) * ld + 2 * H + head * D + 8 * g);
+      st.valid |= ((k < n ? 1u : 0u) << (8 + j)) | ((k + 1 < n ? 1u : 0u) << (16 + j));
     }
   } else {
 #pragma unroll
     for (int j = 0; j < 2 * R; j++) {  // K: (key, chunk c in 0..7) = item tid + NT j
       const int it = tid + NT * j, key = it >> 3, c = it & 7;
-      const bool ok = k0 + key < n;
+      st.valid |= (k0 + key < n ? 1u : 0u) << j;
       const size_t tok = (size_t)(base + min(k0 + key, n - 1));
       const T *row = qkv + tok * ld + H + head * D;
-      const uint4 lo = *(const uint4 *)(row + 4 * c), hi = *(const uint4 *)(row + 32 + 4 * c);
-      st.k_lo[j] = keep_if(ok, lo);
-      st.k_hi[j] = keep_if(ok, hi);
-      const size_t p = (size_t)(kinfo[tok] & 0xffff);
+      st.k_lo[j] = *(const uint4 *)(row + 4 * c);
+      st.k_hi[j] = *(const uint4 *)(row + 32 + 4 * c);
+      const size_t p = (size_t)(ki.pk[j] & 0xffff);
       st.c[j] = *(const float4 *)(cos_t + p * 32 + 4 * c);
       st.s[j] = *(const float4 *)(sin_t + p * 32 + 4 * c);
     }
 #pragma unroll
     for (int j = 0; j < 4 * R; j++) {  // V: key = it % 64, d group g = it / 64
       const int it = tid + NT * j, key = it & 63, g = it >> 6;
-      const uint4 v = *(const uint4 *)(qkv + (size_t)(base + min(k0 + key, n - 1)) * ld + 2 * H + head * D + 4 * g);
-      st.v[j] = keep_if(k0 + key < n, v);
+      st.v[j] = *(const uint4 *)(qkv + (size_t)(base + min(k0 + key, n - 1)) * ld + 2 * H + head * D + 4 * g);
+      st.valid |= (k0 + key < n ? 1u : 0u) << (8 + j);
     }
   }
-  st.info = (tid < KTILE && k0 + tid < n) ? kinfo[base + k0 + tid] : 0;
+  st.info = ki.pi;
 }
 
 __device__ __forceinline__ float bf_lo(uint32_t w) { return __uint_as_float(w << 16); }
@@ -159,8 +184,10 @@ __device__ __forceinline__ void stage_store(const Staging<T, R> &st, char *sK, c
 #pragma unroll
     for (int j = 0; j < R; j++) {
       const int it = tid + NT * j, key = it >> 2, c = it & 3;
-      const uint32_t klo[4] = {st.k_lo[j].x, st.k_lo[j].y, st.k_lo[j].z, st.k_lo[j].w};
-      const uint32_t khi[4] = {st.k_hi[j].x, st.k_hi[j].y, st.k_hi[j].z, st.k_hi[j].w};
+      const bool ok = (st.valid >> j) & 1;
+      const uint4 kl = keep_if(ok, st.k_lo[j]), kh = keep_if(ok, st.k_hi[j]);
+      const uint32_t klo[4] = {kl.x, kl.y, kl.z, kl.w};
+      const uint32_t khi[4] = {kh.x, kh.y, kh.z, kh.w};
       const float cs[8] = {st.c_lo[j].x, st.c_lo[j].y, st.c_lo[j].z, st.c_lo[j].w,
                            st.c_hi[j].x, st.c_hi[j].y, st.c_hi[j].z, st.c_hi[j].w};
       const float sn[8] = {st.s_lo[j].x, st.s_lo[j].y, st.s_lo[j].z, st.s_lo[j].w,
@@ -187,8 +214,9 @@ __device__ __forceinline__ void stage_store(const Staging<T, R> &st, char *sK, c
       const int it = tid + NT * j, p = it & 31, g = it >> 5;
       const int lp = p & 7, q4 = lp >> 1;
       const int pw = (p & ~7) + ((((q4 & 1) << 1) | (q4 >> 1)) << 1) + (lp & 1);
-      const uint32_t va[4] = {st.v0[j].x, st.v0[j].y, st.v0[j].z, st.v0[j].w};
-      const uint32_t vb[4] = {st.v1[j].x, st.v1[j].y, st.v1[j].z, st.v1[j].w};
+      const uint4 v0 = keep_if((st.valid >> (8 + j)) & 1, st.v0[j]), v1 = keep_if((st.valid >> (16 + j)) & 1, st.v1[j]);
+      const uint32_t va[4] = {v0.x, v0.y, v0.z, v0.w};
+      const uint32_t vb[4] = {v1.x, v1.y, v1.z, v1.w};
 #pragma unroll
       for (int w = 0; w < 4; w++) {
         *(uint32_t *)(sV + (8 * g + 2 * w) * ROWV + 4 * pw) = (va[w] & 0xffffu) | (vb[w] << 16);
@@ -199,7 +227,9 @@ __device__ __forceinline__ void stage_store(const Staging<T, R> &st, char *sK, c
 #pragma unroll
     for (int j = 0; j < 2 * R; j++) {
       const int it = tid + NT * j, key = it >> 3, c = it & 7;
-      float4 lo = *(const float4 *)&st.k_lo[j], hi = *(const float4 *)&st.k_hi[j];
+      const bool ok = (st.valid >> j) & 1;
+      const uint4 kl = keep_if(ok, st.k_lo[j]), kh = keep_if(ok, st.k_hi[j]);
+      float4 lo = *(const float4 *)&kl, hi = *(const float4 *)&kh;
       const float4 cs = st.c[j], sn = st.s[j];
       rope1(lo.x, hi.x, cs.x, sn.x);
       rope1(lo.y, hi.y, cs.y, sn.y);
@@ -211,7 +241,7 @@ __device__ __forceinline__ void stage_store(const Staging<T, R> &st, char *sK, c
 #pragma unroll
     for (int j = 0; j < 4 * R; j++) {
       const int it = tid + NT * j, key = it & 63, g = it >> 6;
-      const uint4 v = st.v[j];
+      const uint4 v = keep_if((st.valid >> (8 + j)) & 1, st.v[j]);
       *(uint32_t *)(sV + (4 * g + 0) * ROWV + 4 * key) = v.x;
       *(uint32_t *)(sV + (4 * g + 1) * ROWV + 4 * key) = v.y;
       *(uint32_t *)(sV + (4 * g + 2) * ROWV + 4 * key) = v.z;
@@ -270,8 +300,12 @@ __global__ __launch_bounds__(64 * QW) __attribute__((amdgpu_waves_per_eu(QT == 1
   for (int kt = tid; kt < nkt; kt += NT) sCode[kt] = codes[kt];
   int kt = a.first[wi];
   Staging<T, R> st;
+  KeyInfo<T, R> ki;
   const bool stager = tid < 256;
-  if (kt < nkt && stager) stage_load<T, R>(st, qkv, ld, H, head, base, n, kt * KTILE, a.cos_t, a.sin_t, a.kinfo, tid);
+  if (kt < nkt && stager) {
+    key_info_load<T, R>(ki, a.kinfo, base, n, kt * KTILE, tid);
+    stage_load<T, R>(st, qkv, ld, H, head, base, n, kt * KTILE, a.cos_t, a.sin_t, ki, tid);
+  }
 
   // This lane's queries (one per query tile), their RoPE factors and the
   // rotated Q^T operands (B operand: column = query, k = head dim).
@@ -337,15 +371,23 @@ __global__ __launch_bounds__(64 * QW) __attribute__((amdgpu_waves_per_eu(QT == 1
     return kt;
   };
 
-  // Pipeline: the first tile is stored, the second one's loads are issued;
-  // then per tile: compute it from buffer b, store the next tile (loaded
-  // during the compute) into buffer b^1, issue the loads of the one after,
-  // one barrier.
-  int kn = nkt, b = 0;
+  // Pipeline: the first tile is stored, the second one's loads are issued
+  // and the third one's key info; then per tile: compute it from buffer b,
+  // store the next tile (loaded during the compute) into buffer b^1, issue
+  // the loads of the one after (its key info arrived during the compute) and
+  // the key info of the one after that, one barrier.
+  int kn = nkt, kn_next = nkt, b = 0;
   if (kt < nkt) {
     if (stager) stage_store<T, R>(st, sK[0], sV[0], sInfo[0], tid, ROWK, ROWV);
     kn = next_tile(kt + 1);
-    if (kn < nkt && stager) stage_load<T, R>(st, qkv, ld, H, head, base, n, kn * KTILE, a.cos_t, a.sin_t, a.kinfo, tid);
+    if (kn < nkt) {
+      if (stager) {
+        key_info_load<T, R>(ki, a.kinfo, base, n, kn * KTILE, tid);
+        stage_load<T, R>(st, qkv, ld, H, head, base, n, kn * KTILE, a.cos_t, a.sin_t, ki, tid);
+      }
+      kn_next = next_tile(kn + 1);
+      if (kn_next < nkt && stager) key_info_load<T, R>(ki, a.kinfo, base, n, kn_next * KTILE, tid);
+    }
     __syncthreads();
   }
   const unsigned win2 = a.sliding ? (unsigned)(2 * a.half_window) : 0xffffffffu;
@@ -493,9 +535,12 @@ __global__ __launch_bounds__(64 * QW) __attribute__((amdgpu_waves_per_eu(QT == 1
       const int nb = NBUF == 2 ? b ^ 1 : 0;
       if constexpr (NBUF == 1) __syncthreads();  // every wave is done with the one buffer
       if (stager) stage_store<T, R>(st, sK[nb], sV[nb], sInfo[nb], tid, ROWK, ROWV);
-      kn2 = next_tile(kn + 1);
-      if (kn2 < nkt && stager)
-        stage_load<T, R>(st, qkv, ld, H, head, base, n, kn2 * KTILE, a.cos_t, a.sin_t, a.kinfo, tid);
+      kn2 = kn_next;  // == next_tile(kn + 1); ki holds its key info
+      if (kn2 < nkt) {
+        if (stager) stage_load<T, R>(st, qkv, ld, H, head, base, n, kn2 * KTILE, a.cos_t, a.sin_t, ki, tid);
+        kn_next = next_tile(kn2 + 1);
+        if (kn_next < nkt && stager) key_info_load<T, R>(ki, a.kinfo, base, n, kn_next * KTILE, tid);
+      }
     }
     __syncthreads();  // the next tile's buffer is complete; buffer b is free
     kt = kn;
