@@ -773,8 +773,8 @@ int stage_batch(dn_ctx *c, int nseq, const int32_t *seq_len, const int32_t *ids,
   for (int64_t t = 0; t < T; t++) {
     if (pos[t] < 0 || pos[t] > 0xffff)
       return fail(c, DN_UNSUPPORTED, "decide_hip: position id " + std::to_string(pos[t]) + " outside [0, 65535]");
-    if (opt_id && (opt_id[t] < -1 || opt_id[t] > 32765))
-      return fail(c, DN_UNSUPPORTED, "decide_hip: option id " + std::to_string(opt_id[t]) + " outside [-1, 32765]");
+    if (opt_id && (opt_id[t] < -1 || opt_id[t] > 32766))
+      return fail(c, DN_UNSUPPORTED, "decide_hip: option id " + std::to_string(opt_id[t]) + " outside [-1, 32766]");
   }
   const int R = (int)row_tok.size();
   *R_out = R;

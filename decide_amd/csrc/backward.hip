@@ -401,13 +401,15 @@ __global__ __launch_bounds__(256) void head_bwd_row_kernel(HeadBwdArgs a) {
 #pragma unroll
   for (int j = 0; j < EF; j++) {
     const int i = tid + 256 * j;
+    float s2;
     {
 #pragma clang fp contract(off)
       xh2[j] = (ge[j] - m2) * r2;
+      s2 = xh2[j] * nw[j] + (okf[j] ? a.norm_b[i] : 0.0f);  // the forward's s2, unfused (ops.go:83)
     }
     ds2[j] = okf[j] ? dl * a.out_w[i] : 0.0f;
     if (okf[j]) {
-      ct[i] = dl * (xh2[j] * nw[j] + a.norm_b[i]);  // OutW: dl * s2
+      ct[i] = dl * s2;  // OutW: dl * s2
       ct[half + i] = ds2[j] * xh2[j];               // norm weight
       ct[2 * half + i] = ds2[j];                    // norm bias
     }
@@ -466,12 +468,17 @@ __global__ __launch_bounds__(256) void head_bwd_row_kernel(HeadBwdArgs a) {
   float dfN[EH], dRow[EH];
   row_ln_bwd(ds1, xh1, wI, ok, r1, H, red, dfN);
   row_ln_bwd(dfN, xhF, wF, ok, rF, H, red, dRow);
+  // Rows that share a token: the reference copies dRows into dcur in row
+  // order, so the last such row's gradient stands (backward.go:30-33). This
+  // block writes dcur only if no later row names the same token.
+  bool last = true;
+  for (int r2 = r + 1; r2 < a.R; r2++) last = last && a.row_tok[r2] != t;
 #pragma unroll
   for (int j = 0; j < EH; j++) {
     const int i = tid + 256 * j;
     if (ok[j]) {
       ct[4 * half + 2 * H + i] = dfN[j] * xhF[j];  // final_norm weight
-      a.dcur[(size_t)t * H + i] = dRow[j];
+      if (last) a.dcur[(size_t)t * H + i] = dRow[j];
     }
   }
 }

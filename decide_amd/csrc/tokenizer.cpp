@@ -192,8 +192,35 @@ uint32_t compose(uint32_t a, uint32_t b) {  // 0: none
   return 0;
 }
 
+// Leading / trailing non-starters of r's NFKD decomposition ({0, 0} for the
+// code points that have none).
+NonStarters non_starters(uint32_t r) {
+  size_t lo = 0, hi = sizeof(kNonStarters) / sizeof(kNonStarters[0]);
+  while (lo < hi) {
+    const size_t m = (lo + hi) / 2;
+    if (r < kNonStarters[m].cp)
+      hi = m;
+    else if (r > kNonStarters[m].cp)
+      lo = m + 1;
+    else
+      return kNonStarters[m];
+  }
+  return NonStarters{r, 0, 0};
+}
+
+constexpr uint32_t kCgj = 0x034F;  // COMBINING GRAPHEME JOINER, a starter of class 0
+constexpr int kMaxNonStarters = 30;
+
 // NFC of UTF-8 text. Invalid bytes pass through unchanged (as x/text/norm
 // leaves them) and split the text into independently normalised runs.
+// Before normalising, runs of more than 30 non-starters are broken with CGJ
+// (UAX #15's Stream-Safe Text Process, which x/text's NFC applies): a code
+// point whose decomposition's leading non-starters would take the count of
+// consecutive non-starters past 30 gets a CGJ in front of it. A code point
+// whose decomposition holds no starter adds its length to the count, any
+// other sets the count to its trailing non-starters; an invalid byte is a
+// starter. Text below U+0300 holds no non-starter, so the fast path needs
+// no count.
 std::string nfc(const std::string &s) {
   bool fast = true;
   for (size_t i = 0; i < s.size() && fast;) {
@@ -241,15 +268,22 @@ std::string nfc(const std::string &s) {
     for (uint32_t r : buf) append_utf8(out, r);
     buf.clear();
   };
+  int run = 0;  // consecutive non-starters so far
   for (size_t i = 0; i < s.size();) {
     size_t l;
     const uint32_t r = decode_rune(s, i, &l);
-    (void)r;
     if (l == 1 && (unsigned char)s[i] >= 0x80) {  // an invalid byte
       flush();
       out += s[i];
+      run = 0;
     } else {
+      const NonStarters ns = non_starters(r);
+      if (run + ns.lead > kMaxNonStarters) {
+        buf.push_back(kCgj);
+        run = 0;
+      }
       decompose(r, buf);
+      run = ns.lead ? run + ns.lead : ns.trail;
     }
     i += l;
   }

@@ -11,7 +11,9 @@ import ctypes
 import os
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "libdecide_hip.so")
+# DECIDE_HIP_LIBRARY names another build of the same library (the host-code
+# sanitizer build the CPU tests load); the default is the in-tree build.
+LIB_PATH = os.environ.get("DECIDE_HIP_LIBRARY") or os.path.join(HERE, "libdecide_hip.so")
 
 DN_OK, DN_NO_GPU, DN_INVALID_ARG, DN_OUT_OF_MEMORY, DN_DEVICE_ERROR, DN_UNSUPPORTED = range(6)
 DN_PRECISION_FP32, DN_PRECISION_BF16 = 0, 1

@@ -10,11 +10,14 @@ TEST INFRASTRUCTURE ONLY: the checker of the library's host tokenizer
   pre_tokenize    tokenizer.go:214-272 (+ contraction :274-283)
   byte_to_rune    tokenizer.go:286-309
   bpe             tokenizer.go:320-365
-NFC is Python's unicodedata.normalize (the reference uses
-golang.org/x/text/unicode/norm v0.x: both implement UAX #15; Python 3.10
-carries Unicode 13.0, x/text Unicode 15.0, which differ only for code points
-assigned after 13.0). Text is bytes; invalid UTF-8 follows Go: []rune makes
-each invalid byte one U+FFFD, NFC passes it through.
+NFC is Python's unicodedata.normalize after UAX #15's Stream-Safe Text
+Process (the reference uses golang.org/x/text/unicode/norm v0.x, whose
+NFC.String inserts U+034F COMBINING GRAPHEME JOINER into runs of more than
+30 non-starters before normalising; unicodedata does not, so stream_safe
+restates it from UAX #15 D5). Python 3.10 carries Unicode 13.0, x/text
+Unicode 15.0, which differ only for code points assigned after 13.0. Text is
+bytes; invalid UTF-8 follows Go: []rune makes each invalid byte one U+FFFD,
+NFC passes it through.
 """
 from __future__ import annotations
 
@@ -65,19 +68,56 @@ def runes_to_bytes(rs) -> bytes:
     return "".join(chr(r) for r in rs).encode("utf-8")
 
 
+CGJ = "\u034f"
+MAX_NON_STARTERS = 30
+
+
+def nfkd_non_starters(ch: str):
+    """(leading, trailing, total) counts of non-starters (canonical combining
+    class != 0) in the NFKD decomposition of one character."""
+    d = unicodedata.normalize("NFKD", ch)
+    ns = [unicodedata.combining(c) != 0 for c in d]
+    lead = next((i for i, v in enumerate(ns) if not v), len(ns))
+    trail = next((i for i, v in enumerate(reversed(ns)) if not v), len(ns))
+    return lead, trail, len(ns)
+
+
+def stream_safe(s: str) -> str:
+    """UAX #15 D5, the Stream-Safe Text Process: walking the text, keep the
+    number of consecutive non-starters; before a character whose
+    decomposition's leading non-starters would take it past 30, emit CGJ and
+    restart the count. A character whose decomposition holds no starter adds
+    all its code points to the count; any other sets it to its trailing
+    non-starters."""
+    out, count = [], 0
+    for ch in s:
+        lead, trail, total = nfkd_non_starters(ch)
+        if count + lead > MAX_NON_STARTERS:
+            out.append(CGJ)
+            count = 0
+        out.append(ch)
+        count = count + total if lead == total else trail
+    return "".join(out)
+
+
+def nfc_run(rs) -> bytes:
+    return unicodedata.normalize("NFC", stream_safe("".join(rs))).encode("utf-8")
+
+
 def nfc(b: bytes) -> bytes:
-    """norm.NFC.String: valid runs normalised, invalid bytes kept."""
+    """norm.NFC.String: valid runs made stream-safe and normalised, invalid
+    bytes kept (each one ends a run: x/text treats it as a starter)."""
     out, run, i = [], [], 0
     while i < len(b):
         r, n = go_decode(b, i)
         if n == 1 and b[i] >= 0x80:
-            out.append(unicodedata.normalize("NFC", "".join(run)).encode("utf-8"))
+            out.append(nfc_run(run))
             run = []
             out.append(b[i:i + 1])
         else:
             run.append(chr(r))
         i += n
-    out.append(unicodedata.normalize("NFC", "".join(run)).encode("utf-8"))
+    out.append(nfc_run(run))
     return b"".join(out)
 
 

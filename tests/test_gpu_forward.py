@@ -268,6 +268,39 @@ def test_forward_device_position_range_flagged(base, engines):
             assert np.array_equal(out.cpu().numpy(), want)
 
 
+def test_option_id_limit(base, engines):
+    """Option ids are packed as ((opt + 1) << 16) | pos in a signed 32-bit
+    word, so 32766 is the largest id either entry point takes. dn_forward and
+    dn_forward_device both accept it (and agree bit for bit); 32767 is refused
+    by dn_forward's host check and flagged by dn_forward_device's kernels."""
+    import torch
+    from decide_amd import Unsupported
+    from decide_amd.nn import Sequence, flatten, row_tokens
+
+    eng = engines["bf16"]
+    ids = np.array([50281, 7, 50284, 9, 50282], np.int32)
+    for oid in (32766, 32767):
+        opt = np.array([-1, oid, -1, oid, -1], np.int32)
+        seq = Sequence(ids=ids, pos=np.arange(5, dtype=np.int32), opt=opt, mask_pos=np.array([2], np.int32))
+        seq_len, fids, fpos, fopt, _, _ = flatten([seq])
+        d = {k: torch.from_numpy(v).cuda() for k, v in dict(ids=fids, pos=fpos, opt=fopt,
+                                                              rt=row_tokens([seq])).items()}
+        out = torch.zeros(1, dtype=torch.float32, device="cuda")
+        torch.cuda.synchronize()
+        eng.forward_device(seq_len, d["ids"].data_ptr(), d["pos"].data_ptr(), d["opt"].data_ptr(), 1,
+                           d["rt"].data_ptr(), out.data_ptr())
+        if oid == 32766:
+            host = eng.forward([seq])
+            eng.check_device_errors()
+            assert np.isfinite(host).all() and np.array_equal(out.cpu().numpy(), host)
+        else:
+            with pytest.raises(Unsupported) as ei:
+                eng.forward([seq])
+            assert "option id 32767 outside [-1, 32766]" in ei.value.message
+            with pytest.raises(Unsupported):
+                eng.check_device_errors()
+
+
 def test_max_length_sequence(base, engines):
     """The longest sequence this build accepts (8192 tokens, the reference's
     Local limit: 8000-token premise + 4 options x 48) against the oracle in

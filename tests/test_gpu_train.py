@@ -155,6 +155,42 @@ def test_backward_matches_oracle_small(prec):
         check_grads(eng, want, prec, label="small")
 
 
+def test_backward_duplicate_mask_positions_fp32():
+    """Two [MASK] rows naming the same token (stage_batch accepts repeated
+    mask positions): their scores and head gradients both count, and the
+    reference copies the rows' gradients into dcur in row order, so the last
+    such row's gradient is the one that flows into the encoder
+    (backward.go:30-33). The target sits on the first duplicate, so the two
+    rows' dlogits differ (p - 1 against p) and a wrong winner shows up in every
+    encoder gradient."""
+    from decide_amd.nn import Sequence
+    from decide_amd.train import TrainEngine
+
+    cfg = small_cfg(2)
+    w = weights_for(cfg)
+    batch = train_batch(cfg.vocab, cfg.vocab - 1, specs=[(20, [5, 6, 7], True), (30, [4, 4], False)])
+    s0 = batch[0]
+    mp = np.array([s0.mask_pos[0], s0.mask_pos[1], s0.mask_pos[2], s0.mask_pos[0]], np.int32)
+    batch[0] = Sequence(ids=s0.ids, pos=s0.pos, opt=s0.opt, mask_pos=mp)
+    print(f"case: duplicate mask positions fp32, T={sum(len(s.ids) for s in batch)}", flush=True)
+    oracle.set_workers(WORKERS)
+    m = oracle.OracleModel(cfg, w)
+    want_logits = m.forward_train(batch, 0)
+    _, dl = oracle.loss_and_grad(want_logits, batch, [0, 1])
+    assert dl[0] != dl[3]
+    g = m.zeros_like()
+    m.backward(dl, g, train_emb=True)
+    from decide_amd.nn import tensor_shapes
+
+    want = {n: g.get(n, int(np.prod(sh))).reshape(sh) for n, sh in tensor_shapes(cfg).items()}
+    with TrainEngine(cfg, w, precision="fp32") as eng:
+        logits = eng.forward(batch)
+        assert logits[0] == logits[3]
+        assert np.all(np.abs(logits.astype(np.float64) - want_logits) <= 1e-4 * (1 + np.abs(want_logits)))
+        eng.backward(dl)
+        check_grads(eng, want, "fp32", label="duplicate mask positions")
+
+
 def test_backward_frozen_layers_fp32():
     """trainFrom = 2 without embeddings: layers 0-1 and the embeddings get
     exactly zero, the rest match (TestForwardBackwardMatchesPyTorch's frozen

@@ -171,6 +171,62 @@ def test_nfc_matches_unicodedata():
         assert nfc(nfd) == want, hex(c)
 
 
+# Hand-derived answers of UAX #15's Stream-Safe Text Process followed by NFC
+# (U+0301 acute and U+0316 grave-below are non-starters of class 230 / 220;
+# U+00E9's decomposition ends in one non-starter; U+0344 decomposes to two).
+A, G, CGJ = "\u0301", "\u0316", "\u034f"
+STREAM_SAFE_CASES = [
+    ("a" + A * 30, "\u00e1" + A * 29),                       # 30 non-starters: untouched
+    ("a" + A * 31, "\u00e1" + A * 29 + CGJ + A),             # the 31st gets a CGJ in front
+    ("\u00e9" + A * 30, "\u00e9" + A * 29 + CGJ + A),        # e-acute's own mark counts
+    (G * 70, G * 30 + CGJ + G * 30 + CGJ + G * 10),         # no starter at all
+    ("a" + A * 29 + "\u0344", "\u00e1" + A * 28 + CGJ + "\u0308\u0301"),  # two at once
+    ("a" + A * 30 + G, "\u00e1" + A * 29 + CGJ + G),         # no reordering across the CGJ
+    ("a" + G + A * 30, "\u00e1" + G + A * 28 + CGJ + A),     # G + 29 A, then the CGJ
+]
+
+
+def test_stream_safe_known_answers():
+    """NFC with x/text's stream-safe step: the oracle and dn_nfc against
+    answers worked by hand from UAX #15 D5; an invalid byte restarts the
+    count (20 + 20 marks around it stay untouched)."""
+    from decide_amd.tokenizer import nfc
+
+    for text, want in STREAM_SAFE_CASES:
+        assert ot.nfc(text.encode()) == want.encode(), [hex(ord(c)) for c in text]
+        assert nfc(text) == want.encode(), [hex(ord(c)) for c in text]
+    b = ("a" + A * 20).encode() + b"\xff" + (A * 20).encode()
+    want = ("\u00e1" + A * 19).encode() + b"\xff" + (A * 20).encode()
+    assert ot.nfc(b) == want and nfc(b) == want
+
+
+def test_stream_safe_matches_oracle():
+    """Long runs of combining marks (classes 202-240, marks with several
+    non-starters in their decompositions, precomposed letters whose
+    decompositions end in marks, invalid bytes) through dn_nfc and the
+    oracle's stream-safe NFC."""
+    from decide_amd.tokenizer import nfc
+
+    rng = random.Random(15)
+    marks = [0x301, 0x300, 0x316, 0x323, 0x327, 0x302, 0x308, 0x345, 0x344, 0xF73, 0xF75, 0x93C, 0x3099, 0x5B0]
+    starters = ["a", "e", "\u00e9", "\u1e09", "\u00a8", "\uff9e", "\u1100", "\u1161", "\uac00", "x"]
+    hits = 0
+    for i in range(400):
+        parts = []
+        for _ in range(rng.randint(1, 4)):
+            if rng.random() < 0.7:
+                parts.append(rng.choice(starters))
+            parts.append("".join(chr(rng.choice(marks)) for _ in range(rng.randint(0, 75))))
+        b = "".join(parts).encode()
+        if i % 7 == 0:
+            cut = rng.randint(0, len(b))
+            b = b[:cut] + b"\xc3" + b[cut:]
+        want = ot.nfc(b)
+        hits += want.count(CGJ.encode())
+        assert nfc(b) == want, b
+    assert hits > 100  # the cases do exercise the CGJ insertion
+
+
 def test_merges_outside_the_vocabulary():
     """A merge whose parts or result are not vocabulary entries: the string
     form of bpe (tokenizer.go:320-365) applies it, and a final part that is
