@@ -18,6 +18,7 @@ import argparse
 import gc
 import json
 import os
+import re
 import sys
 import time
 
@@ -795,49 +796,74 @@ def read_traffic(config: str, prec: str) -> dict:
 
 def summarize_traffic(fetch_dir: str, write_dir: str, out_path: str) -> int:
     """Turns two rocprofv3 --pmc runs of `bench.py --steps 2 --warmup 1
-    --no-cpu-baseline --no-extra-configs --copy-calibration 512` (FETCH_SIZE,
-    then WRITE_SIZE) into bytes per launch for the roofline kernels, each
-    counter scaled by what it reads for the 512 MiB device copy."""
+    --probe-steps 1 --no-cpu-baseline --no-extra-configs --copy-calibration 512
+    --stream-split 0` (FETCH_SIZE, then WRITE_SIZE; one stream, so every GEMM
+    launch covers the whole batch) into bytes per launch for the roofline
+    kernels, each counter scaled by what it reads for the 512 MiB device
+    copy."""
     import csv
     import glob
 
-    def per_kernel(d, counter):
-        rows = []
+    def per_dispatch(d, counter):
+        acc, names = {}, {}
         for f in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
-            rows += [r for r in csv.DictReader(open(f)) if r["Counter_Name"] == counter]
-        acc = {}
-        for r in rows:  # one row per dispatch and XCD: sum the XCDs of a dispatch
-            key = (r["Kernel_Name"], r["Dispatch_Id"])
-            acc[key] = acc.get(key, 0.0) + float(r["Counter_Value"])
+            for r in csv.DictReader(open(f)):
+                if r["Counter_Name"] != counter:
+                    continue
+                key = (f, r["Dispatch_Id"])  # rows of one dispatch (per XCD where split) are summed
+                acc[key] = acc.get(key, 0.0) + float(r["Counter_Value"]) * 1024.0
+                names[key] = r["Kernel_Name"]
         byk = {}
-        for (k, _), v in acc.items():
-            byk.setdefault(k, []).append(v * 1024.0)
-        return {k: float(np.mean(v)) for k, v in byk.items()}
+        for key, v in acc.items():
+            byk.setdefault(names[key], []).append(v)
+        return byk
 
-    fetch, write = per_kernel(fetch_dir, "FETCH_SIZE"), per_kernel(write_dir, "WRITE_SIZE")
+    def gemm_params(name):
+        """Template arguments of gemm_nt_kernel<bf16, BM, BN, BK, STAGES, EPI, ...>
+        from a mangled (..Li128ELi192E..) or demangled (<.., 128, 192, ..>) name."""
+        if "gemm_nt_kernel" not in name:
+            return None
+        tail = name.split("gemm_nt_kernel", 1)[1]
+        m = re.findall(r"Li(\d+)E", tail)
+        if not m:
+            m = re.findall(r"(?<=[<,\s])(\d+)(?=[,>])", tail.split(">")[0] + ">")
+        return tuple(int(x) for x in m)
+
+    fetch, write = per_dispatch(fetch_dir, "FETCH_SIZE"), per_dispatch(write_dir, "WRITE_SIZE")
     copy_bytes = 512 << 20
-    ck = [k for k in fetch if "copyBuffer" in k or "elementwise" in k]
-    fetch_scale = copy_bytes / max(fetch[k] for k in ck)
-    write_scale = copy_bytes / max(write[k] for k in ck)
+    # The calibration copy is the largest copy dispatch of each run.
+    fetch_scale = copy_bytes / max(max(v) for k, v in fetch.items() if "copyBuffer" in k)
+    write_scale = copy_bytes / max(max(v) for k, v in write.items() if "copyBuffer" in k)
     T = 32768
-    pick = {"residual": ("EPI_F32", "128, 192"), "wi": ("EPI_GEGLU", "256, 128"), "qkv": ("EPI_STORE", "256, 128")}
+    pick = {"residual": (128, 192, 0), "wi": (256, 128, 2), "qkv": (256, 128, 1)}  # BM, BN, epilogue
     alg = {"residual": (2 * (T * H + H * H) + 2 * (T * I + H * I) + 16 * T * H) / 2,
            "wi": 2 * (T * H + 2 * I * H + T * I), "qkv": 2 * (T * H + 3 * H * H + 3 * T * H)}
     kernels = {}
-    for name, (epi_tag, tile_tag) in pick.items():
-        epi_num = {"EPI_F32": "0", "EPI_GEGLU": "2", "EPI_STORE": "1"}[epi_tag]
-        cands = [k for k in fetch if "gemm_nt_kernel" in k and tile_tag in k and f", {epi_num}, " in k]
+    for name, (bm, bn, epi) in pick.items():
+        cands = [k for k in fetch if (gemm_params(k) or (0,) * 5)[:5] in
+                 [(bm, bn, 64, st, epi) for st in (2, 3, 4)]]
         if not cands:
             continue
         k = cands[0]
-        fb, wb = fetch[k] * fetch_scale, write.get(k, 0.0) * write_scale
-        kernels[name] = {"symbol": k, "fetch_bytes_per_launch": round(fb), "write_bytes_per_launch": round(wb),
-                         "hbm_bytes_per_launch": round(fb + wb), "algorithmic_bytes_per_launch": alg[name]}
+        fb = float(np.mean(fetch[k])) * fetch_scale
+        wb = float(np.mean(write.get(k, [0.0]))) * write_scale
+        kernels[name] = {"symbol": k, "template_args": list(gemm_params(k)), "dispatches": len(fetch[k]),
+                         "fetch_bytes_per_launch": round(fb), "write_bytes_per_launch": round(wb),
+                         "hbm_bytes_per_launch": round(fb + wb), "algorithmic_bytes_per_launch": alg[name],
+                         "traffic_over_algorithmic": round((fb + wb) / alg[name], 3)}
+    others = {}
+    for k, v in fetch.items():
+        if "attention_kernel" in k or "ln_kernel" in k:
+            tag = "attention" if "attention_kernel" in k else "layernorm"
+            others[tag] = {"symbol": k, "fetch_bytes_per_launch": round(float(np.mean(v)) * fetch_scale),
+                           "write_bytes_per_launch": round(float(np.mean(write.get(k, [0.0]))) * write_scale)}
     res = {"workload": "cfg3 (T=32768), bf16", "fetch_scale": fetch_scale, "write_scale": write_scale,
            "method": "rocprofv3 --pmc FETCH_SIZE and --pmc WRITE_SIZE (separate runs of bench.py --steps 2 "
-                     "--warmup 1 --no-cpu-baseline --no-extra-configs --copy-calibration 512), KiB per dispatch "
+                     "--warmup 1 --probe-steps 1 --no-cpu-baseline --no-extra-configs --copy-calibration 512 "
+                     "--stream-split 0), KiB per dispatch "
                      "summed over XCDs and averaged over the dispatches of each symbol, scaled by the counter's "
-                     "reading for the 512 MiB device copy", "kernels": kernels}
+                     "reading for the 512 MiB device copy (the largest copy dispatch of each run)", "kernels": kernels,
+           "other_kernels": others}
     with open(out_path, "w") as fh:
         json.dump(res, fh, indent=1)
     print(json.dumps(res, indent=1))
