@@ -291,50 +291,46 @@ __global__ __launch_bounds__(64 * WGM * WGN) __attribute__((amdgpu_waves_per_eu(
     const float *R = g.res ? g.res : C;  // residual input of the accumulate
     constexpr int V = BN / 4;  // float4 per row
     constexpr int ITER = HM * V / NT;
-    constexpr int BATCH = ITER <= 8 ? ITER : ITER % 8 == 0 ? 8 : ITER % 6 == 0 ? 6 : 4;
-    static_assert(ITER % BATCH == 0, "epilogue batching");
+    static_assert(ITER * NT == HM * V, "epilogue shape");
     const bool vec = (g.ldc & 3) == 0;
-    // Residual loads of a batch are issued before its stores (C is read and
-    // written here, so the compiler would otherwise serialise each pair); the
-    // first batch of each pass is loaded before that pass's staging barrier
-    // (the previous pass's stores cover other rows), so its latency overlaps
-    // the staging.
-    float4 old[BATCH];
-    auto load_old = [&](int pass, int b0) {
+    // The residual loads of a pass are issued together (one HBM round trip
+    // per pass): pass 0's before its staging, so that their latency overlaps
+    // it; each later pass's right after the previous pass's stores, before
+    // its staging barrier. Loads and stores of an element are made by the
+    // same thread; the rows of different passes are disjoint.
+    float4 old[ITER];
+    auto load_old = [&](int pass) {
 #pragma unroll
-      for (int u = 0; u < BATCH; u++) {
-        const int c = tid + (b0 + u) * NT, r = c / V, c4 = (c % V) * 4;
+      for (int u = 0; u < ITER; u++) {
+        const int c = tid + u * NT, r = c / V, c4 = (c % V) * 4;
         const int row = m0 + pass * HM + r, col = n0 + c4;
         old[u] = make_float4(0.f, 0.f, 0.f, 0.f);
         if (g.accumulate && vec && row < g.M && col + 4 <= g.n_store)
           old[u] = *(const float4 *)(R + (size_t)row * g.ldc + col);
       }
     };
-    load_old(0, 0);
+    load_old(0);
 #pragma unroll
     for (int pass = 0; pass < WGM; pass++) {
       stage_f32(st, LD, pass);
       __syncthreads();
-      for (int b0 = 0; b0 < ITER; b0 += BATCH) {
-        if (b0 > 0) load_old(pass, b0);
 #pragma unroll
-        for (int u = 0; u < BATCH; u++) {
-          const int c = tid + (b0 + u) * NT, r = c / V, c4 = (c % V) * 4;
-          const int row = m0 + pass * HM + r, col = n0 + c4;
-          if (row >= g.M || col >= g.n_store) continue;
-          const float4 v = *(const float4 *)(st + r * LD + c4);
-          float *p = C + (size_t)row * g.ldc + col;
-          if (vec && col + 4 <= g.n_store) {
-            *(float4 *)p = make_float4(v.x + old[u].x, v.y + old[u].y, v.z + old[u].z, v.w + old[u].w);
-          } else {
-            const float vv[4] = {v.x, v.y, v.z, v.w};
-            const float *pr = R + (size_t)row * g.ldc + col;
-            for (int q = 0; q < 4 && col + q < g.n_store; q++) p[q] = g.accumulate ? pr[q] + vv[q] : vv[q];
-          }
+      for (int u = 0; u < ITER; u++) {
+        const int c = tid + u * NT, r = c / V, c4 = (c % V) * 4;
+        const int row = m0 + pass * HM + r, col = n0 + c4;
+        if (row >= g.M || col >= g.n_store) continue;
+        const float4 v = *(const float4 *)(st + r * LD + c4);
+        float *p = C + (size_t)row * g.ldc + col;
+        if (vec && col + 4 <= g.n_store) {
+          *(float4 *)p = make_float4(v.x + old[u].x, v.y + old[u].y, v.z + old[u].z, v.w + old[u].w);
+        } else {
+          const float vv[4] = {v.x, v.y, v.z, v.w};
+          const float *pr = R + (size_t)row * g.ldc + col;
+          for (int q = 0; q < 4 && col + q < g.n_store; q++) p[q] = g.accumulate ? pr[q] + vv[q] : vv[q];
         }
       }
       if (pass + 1 < WGM) {
-        load_old(pass + 1, 0);
+        load_old(pass + 1);
         __syncthreads();
       }
     }
@@ -396,9 +392,15 @@ template <class T, int BM, int BN, int RB, int NSTAGE, int WPE, int WGM = 2, int
 hipError_t launch_cfg(int epi, const GemmArgs &a, hipStream_t s, int splits = 1) {
   const int tiles = ((a.M + BM - 1) / BM) * (a.N / BN);
   dim3 grid(tiles, splits), block(64 * WGM * WGN);
+  // bf16 256-row tiles serve only the operand-type epilogues (the fp32 ones
+  // take 128 x 192 or 128 x 128 tiles): the fp32 epilogue is not built there.
+  constexpr bool f32_epi = !(sizeof(T) == 2 && BM == 256);
   switch (epi) {
     case EPI_F32:
-      hipLaunchKernelGGL((gemm_nt_kernel<T, BM, BN, RB, NSTAGE, EPI_F32, WPE, WGM, WGN>), grid, block, 0, s, a);
+      if constexpr (f32_epi)
+        hipLaunchKernelGGL((gemm_nt_kernel<T, BM, BN, RB, NSTAGE, EPI_F32, WPE, WGM, WGN>), grid, block, 0, s, a);
+      else
+        return hipErrorInvalidValue;
       break;
     case EPI_STORE:
       hipLaunchKernelGGL((gemm_nt_kernel<T, BM, BN, RB, NSTAGE, EPI_STORE, WPE, WGM, WGN>), grid, block, 0, s, a);
