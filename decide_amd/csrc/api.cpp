@@ -784,29 +784,62 @@ int stage_batch(dn_ctx *c, int nseq, const int32_t *seq_len, const int32_t *ids,
   if (T == 0) return DN_OK;
   (void)hipSetDevice(c->device);
   hipStream_t s = c->stream;
-  HIPCHK(c, "hipMalloc", ensure(c->ids, sizeof(int) * T));
-  HIPCHK(c, "hipMalloc", ensure(c->pos, sizeof(int) * T));
-  HIPCHK(c, "hipMalloc", ensure(c->opt, sizeof(int) * T));
-  HIPCHK(c, "hipMalloc", ensure(c->rowtok, sizeof(int) * R));
-  HIPCHK(c, "hipMalloc", ensure(c->logits, sizeof(float) * R));
+  // One pinned staging buffer and one copy for the whole batch: [ids | pos |
+  // opt | rowtok] (opt only when given). A call that staged ends by
+  // synchronizing its stream (finish_forward); one that failed before that
+  // leaves pin_pending set, and the buffer is not rewritten before its copy
+  // has finished.
+  if (c->pin_pending) {
+    HIPCHK(c, "hipStreamSynchronize", hipStreamSynchronize(s));
+    c->pin_pending = false;
+  }
+  const size_t nin = (size_t)(opt_id ? 3 : 2) * T + R, in_bytes = sizeof(int32_t) * nin;
+  const size_t pin_bytes = std::max(in_bytes, sizeof(float) * R + sizeof(int));
+  if (c->pin_cap < pin_bytes) {
+    if (c->pin) (void)hipHostFree(c->pin);
+    c->pin = nullptr;
+    c->pin_cap = 0;
+    const size_t cap = std::max<size_t>(pin_bytes + pin_bytes / 2, 64 << 10);
+    HIPCHK(c, "hipHostMalloc", hipHostMalloc(&c->pin, cap, hipHostMallocDefault));
+    c->pin_cap = cap;
+  }
+  HIPCHK(c, "hipMalloc", ensure(c->io, in_bytes));
+  HIPCHK(c, "hipMalloc", ensure(c->logits, sizeof(float) * std::max(R, 1)));
   int rc = ensure_err_flag(c);
   if (rc) return rc;
+  int32_t *hp = (int32_t *)c->pin, *dp = (int32_t *)c->io.p;
+  std::memcpy(hp, ids, sizeof(int32_t) * T);
+  std::memcpy(hp + T, pos, sizeof(int32_t) * T);
+  c->d_ids = dp;
+  c->d_pos = dp + T;
+  size_t off = 2 * (size_t)T;
+  c->d_opt = nullptr;
+  if (opt_id) {
+    std::memcpy(hp + off, opt_id, sizeof(int32_t) * T);
+    c->d_opt = dp + off;
+    off += T;
+  }
+  std::memcpy(hp + off, row_tok.data(), sizeof(int32_t) * R);
+  c->d_rowtok = dp + off;
   HIPCHK(c, "hipMemsetAsync", hipMemsetAsync(c->err_flag.p, 0, sizeof(int), s));
-  HIPCHK(c, "hipMemcpyAsync", hipMemcpyAsync(c->ids.p, ids, sizeof(int) * T, hipMemcpyHostToDevice, s));
-  HIPCHK(c, "hipMemcpyAsync", hipMemcpyAsync(c->pos.p, pos, sizeof(int) * T, hipMemcpyHostToDevice, s));
-  if (opt_id)
-    HIPCHK(c, "hipMemcpyAsync", hipMemcpyAsync(c->opt.p, opt_id, sizeof(int) * T, hipMemcpyHostToDevice, s));
-  HIPCHK(c, "hipMemcpyAsync",
-         hipMemcpyAsync(c->rowtok.p, row_tok.data(), sizeof(int) * R, hipMemcpyHostToDevice, s));
+  c->pin_pending = true;
+  HIPCHK(c, "hipMemcpyAsync", hipMemcpyAsync(c->io.p, c->pin, in_bytes, hipMemcpyHostToDevice, s));
   return DN_OK;
 }
 
 int finish_forward(dn_ctx *c, int R, float *logits) {
   hipStream_t s = c->stream;
-  HIPCHK(c, "hipMemcpyAsync", hipMemcpyAsync(logits, c->logits.p, sizeof(float) * R, hipMemcpyDeviceToHost, s));
-  int flag = 0;
-  HIPCHK(c, "hipMemcpyAsync", hipMemcpyAsync(&flag, c->err_flag.p, sizeof(int), hipMemcpyDeviceToHost, s));
+  // Logits and the error flag come back through the pinned staging buffer
+  // (the batch's copy out of it precedes these on the stream).
+  char *hp = (char *)c->pin;
+  HIPCHK(c, "hipMemcpyAsync", hipMemcpyAsync(hp, c->logits.p, sizeof(float) * R, hipMemcpyDeviceToHost, s));
+  HIPCHK(c, "hipMemcpyAsync",
+         hipMemcpyAsync(hp + sizeof(float) * R, c->err_flag.p, sizeof(int), hipMemcpyDeviceToHost, s));
   HIPCHK(c, "hipStreamSynchronize", hipStreamSynchronize(s));
+  c->pin_pending = false;
+  int flag = 0;
+  std::memcpy(&flag, hp + sizeof(float) * R, sizeof(int));
+  if (R > 0) std::memcpy(logits, hp, sizeof(float) * R);
   if (flag) return fail(c, DN_DEVICE_ERROR, "decide_hip: device saw an out-of-range index after validation");
   return DN_OK;
 }
@@ -868,11 +901,12 @@ void dn_close(dn_ctx *c) {
   for (hipEvent_t e : c->probe_pool) (void)hipEventDestroy(e);
   for (hipEvent_t e : c->probe_bwd_pool) (void)hipEventDestroy(e);
   DevBuf *bufs[] = {&c->inv_freq, &c->h,     &c->xn,       &c->qkv,         &c->ctxb,     &c->act,
-                    &c->rope,     &c->kinfo, &c->ids,      &c->pos,         &c->opt,      &c->rowtok,
+                    &c->rope,     &c->kinfo, &c->io,
                     &c->logits,   &c->err_flag, &c->gA,    &c->gB,          &c->gC,       &c->d_seq_off, &c->head_s1, &c->head_d,
                     &c->d_seq_len, &c->d_chunk_off, &c->d_chunk_desc, &c->d_work, &c->d_chunks,
                     &c->d_codes,   &c->d_first, &c->calib};
   for (DevBuf *b : bufs) release(*b);
+  if (c->pin) (void)hipHostFree(c->pin);
   for (PartLayout &P : c->parts)
     for (DevBuf *b : {&P.d_seq_off, &P.d_seq_len, &P.d_chunk_off, &P.d_chunk_desc, &P.d_chunks, &P.d_work,
                       &P.d_codes, &P.d_first})
@@ -1008,9 +1042,7 @@ int dn_forward(dn_ctx *c, int nseq, const int32_t *seq_len, const int32_t *ids, 
   int64_t T = 0;
   rc = stage_batch(c, nseq, seq_len, ids, pos, opt_id, nmask, mask_pos, logits_cap, &R, &T);
   if (rc || T == 0) return rc;
-  rc = forward_core(c, nseq, seq_len, (const int32_t *)c->ids.p, (const int32_t *)c->pos.p,
-                    opt_id ? (const int32_t *)c->opt.p : nullptr, R, (const int32_t *)c->rowtok.p,
-                    (float *)c->logits.p, false);
+  rc = forward_core(c, nseq, seq_len, c->d_ids, c->d_pos, c->d_opt, R, c->d_rowtok, (float *)c->logits.p, false);
   if (rc) return rc;
   return finish_forward(c, R, logits);
 }

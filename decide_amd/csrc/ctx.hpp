@@ -125,7 +125,16 @@ struct dn_ctx {
   std::map<std::string, TensorSlot> w;
   DevBuf inv_freq;  // 32 doubles global theta, 32 local
   // workspace
-  DevBuf h, xn, qkv, ctxb, act, kinfo, ids, pos, opt, rowtok, logits, err_flag, head_s1, head_d;
+  DevBuf h, xn, qkv, ctxb, act, kinfo, logits, err_flag, head_s1, head_d;
+  // A host batch (dn_forward, dn_forward_train) arrives as one copy: the
+  // token ids, positions, option ids and mask-row tokens packed in `io`, with
+  // these views into it (valid until the next staged batch), from a pinned
+  // host buffer that also receives the logits and the error flag.
+  DevBuf io;
+  const int32_t *d_ids = nullptr, *d_pos = nullptr, *d_opt = nullptr, *d_rowtok = nullptr;
+  void *pin = nullptr;
+  size_t pin_cap = 0;
+  bool pin_pending = false;  // a copy out of `pin` may be in flight (a call failed before its final sync)
   // RoPE cos/sin per position 0..65535 (global theta, then local), built once
   // per configuration at the first forward.
   DevBuf rope;

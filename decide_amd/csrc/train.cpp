@@ -282,7 +282,7 @@ int backward_impl(dn_ctx *c, const float *dlogits) {
   float *hg[9] = {grad("scorer.out_proj.weight"), grad("scorer.norm.weight"),  grad("scorer.norm.bias"),
                   grad("scorer.dense.bias"),      grad("scorer.dense.weight"), grad("scorer.input_norm.weight"),
                   grad("scorer.input_norm.bias"), grad("model.final_norm.weight"), grad("scorer.out_proj.bias")};
-  HIPCHK(c, "head_bwd", launch_head_bwd((const float *)c->h.p, (const int *)c->rowtok.p, (const float *)c->head_s1.p,
+  HIPCHK(c, "head_bwd", launch_head_bwd((const float *)c->h.p, c->d_rowtok, (const float *)c->head_s1.p,
                                         (const float *)c->head_d.p, (const float *)tr.dl.p, R, H, g.eps, hw, dcur,
                                         (float *)tr.contrib.p, hg, s));
 
@@ -436,7 +436,7 @@ int backward_impl(dn_ctx *c, const float *dlogits) {
     HIPCHK(c, "hipMalloc", ensure(tr.dE, 4 * TH));
     HIPCHK(c, "hipMemsetAsync", hipMemsetAsync(tr.dE.p, 0, 4 * TH, s));
     HIPCHK(c, "ln_bwd(emb)", launch_ln_bwd((float *)tr.dE.p, nullptr, dcur, (const float *)W(c, kTok),
-                                           (const int *)c->ids.p, (const float *)tr.emb_mean.p,
+                                           c->d_ids, (const float *)tr.emb_mean.p,
                                            (const float *)tr.emb_rstd.p, (const float *)W(c, kEmbNorm), g.eps, T, H,
                                            lnpart,
                                            grad(kEmbNorm), s));
@@ -534,9 +534,7 @@ int dn_forward_train(dn_ctx *c, int nseq, const int32_t *seq_len, const int32_t 
   if (rc) return rc;
   c->tr.have_forward = false;
   if (T == 0) return DN_OK;
-  rc = forward_core(c, nseq, seq_len, (const int32_t *)c->ids.p, (const int32_t *)c->pos.p,
-                    opt_id ? (const int32_t *)c->opt.p : nullptr, R, (const int32_t *)c->rowtok.p,
-                    (float *)c->logits.p, true);
+  rc = forward_core(c, nseq, seq_len, c->d_ids, c->d_pos, c->d_opt, R, c->d_rowtok, (float *)c->logits.p, true);
   if (rc) return rc;
   c->tr.ids.assign(ids, ids + T);
   return finish_forward(c, R, logits);
