@@ -97,7 +97,9 @@ __device__ __forceinline__ void key_info_load(KeyInfo<T, R> &f, const int *kinfo
     const int key = (tid + NT * j) >> SH;
     f.pk[j] = kinfo[base + min(k0 + key, n - 1)];
   }
-  f.pi = (tid < KTILE && k0 + tid < n) ? kinfo[base + k0 + tid] : 0;
+  // Keys past the sequence end get option field 0xffff (option id -2, which
+  // neither the prefix (-1) nor any query's own option matches).
+  f.pi = (tid < KTILE && k0 + tid < n) ? kinfo[base + k0 + tid] : (int)0xffff0000u;
 }
 
 // Loads one key tile (keys k0 .. k0+63) into registers; NT threads, R = 256/NT.
@@ -177,8 +179,8 @@ __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
 }
 
 template <class T, int R>
-__device__ __forceinline__ void stage_store(const Staging<T, R> &st, char *sK, char *sV, int *sInfo, int tid,
-                                            int ROWK, int ROWV) {
+__device__ __forceinline__ void stage_store(const Staging<T, R> &st, char *sK, char *sV, int *sKo, int *sKw,
+                                            int half_window, int tid, int ROWK, int ROWV) {
   constexpr int NT = 256 / R;
   if constexpr (sizeof(T) == 2) {
 #pragma unroll
@@ -248,10 +250,16 @@ __device__ __forceinline__ void stage_store(const Staging<T, R> &st, char *sK, c
       *(uint32_t *)(sV + (4 * g + 3) * ROWV + 4 * key) = v.w;
     }
   }
-  if (tid < KTILE) sInfo[tid] = st.info;
+  // Each key's mask fields, decoded once: option id (-1 prefix, -2 past the
+  // sequence end) and position + half window.
+  if (tid < KTILE) {
+    sKo[tid] = (st.info >> 16) - 1;
+    sKw[tid] = (st.info & 0xffff) + half_window;
+  }
 }
 
-template <class T, int QW, int QT>
+// LOCAL: a sliding-window layer (the window test is compiled in).
+template <class T, int QW, int QT, bool LOCAL>
 __global__ __launch_bounds__(64 * QW) __attribute__((amdgpu_waves_per_eu(QT == 1 ? 3 : 2))) void attention_kernel(
     AttnArgs a) {
   // R staging items per thread; with more than 4 waves only the first 256
@@ -269,7 +277,10 @@ __global__ __launch_bounds__(64 * QW) __attribute__((amdgpu_waves_per_eu(QT == 1
   constexpr int NBUF = sizeof(T) == 2 ? 2 : 1;
   __shared__ __attribute__((aligned(16))) char sK[NBUF][KTILE * ROWK];
   __shared__ __attribute__((aligned(16))) char sV[NBUF][D * ROWV];
-  __shared__ __attribute__((aligned(16))) int sInfo[NBUF][KTILE];
+  // Per staged key: option id (-1 prefix, -2 past the sequence end) and
+  // position + half window, the fields the per-element mask tests.
+  __shared__ __attribute__((aligned(16))) int sKo[NBUF][KTILE];
+  __shared__ __attribute__((aligned(16))) int sKw[NBUF][KTILE];
   // Per key tile: for each 32-query chunk c of the work item, the 2-bit class
   // of each 32-key half (bits 4c..4c+1 keys 0-31, 4c+2..4c+3 keys 32-63).
   __shared__ uint32_t sCode[ATTN_MAXKT];
@@ -378,7 +389,7 @@ __global__ __launch_bounds__(64 * QW) __attribute__((amdgpu_waves_per_eu(QT == 1
   // the key info of the one after that, one barrier.
   int kn = nkt, kn_next = nkt, b = 0;
   if (kt < nkt) {
-    if (stager) stage_store<T, R>(st, sK[0], sV[0], sInfo[0], tid, ROWK, ROWV);
+    if (stager) stage_store<T, R>(st, sK[0], sV[0], sKo[0], sKw[0], a.half_window, tid, ROWK, ROWV);
     kn = next_tile(kt + 1);
     if (kn < nkt) {
       if (stager) {
@@ -390,11 +401,11 @@ __global__ __launch_bounds__(64 * QW) __attribute__((amdgpu_waves_per_eu(QT == 1
     }
     __syncthreads();
   }
-  const unsigned win2 = a.sliding ? (unsigned)(2 * a.half_window) : 0xffffffffu;
+  const unsigned win2 = (unsigned)(2 * a.half_window);
   while (kt < nkt) {
     const int k0 = kt * KTILE;
     const char *sKb = sK[b], *sVb = sV[b];
-    const int *sInfob = sInfo[b];
+    const int *sKob = sKo[b], *sKwb = sKw[b];
     // This wave's classes: per query tile t and 32-key half i (uniform
     // across the wave).
     const int mycode =
@@ -445,16 +456,16 @@ __global__ __launch_bounds__(64 * QW) __attribute__((amdgpu_waves_per_eu(QT == 1
 #pragma unroll
           for (int g = 0; g < 4; g++) {
             const int kl = i * 32 + 8 * g + 4 * lh;  // 4 consecutive keys kl..kl+3
-            const int4 inf4 = *(const int4 *)(sInfob + kl);
-            const int inf[4] = {inf4.x, inf4.y, inf4.z, inf4.w};
+            const int4 ko4 = *(const int4 *)(sKob + kl), kw4 = *(const int4 *)(sKwb + kl);
+            const int kos[4] = {ko4.x, ko4.y, ko4.z, ko4.w}, kws[4] = {kw4.x, kw4.y, kw4.z, kw4.w};
 #pragma unroll
             for (int u = 0; u < 4; u++) {
               // Block mask: a prefix query sees prefix keys; an option query
-              // sees prefix keys and its own option, i.e. ko in {-1, qopt}.
+              // sees prefix keys and its own option, i.e. ko in {-1, qopt}
+              // (keys past the sequence end carry -2 and match neither).
               // Window: |kpos - qpos| <= W on local layers.
-              const int ko = (inf[u] >> 16) - 1, kp = inf[u] & 0xffff;
-              const bool ok = (k0 + kl + u < n) & ((ko == -1) | (ko == qopt[t])) &
-                              ((unsigned)(kp - qpos[t] + a.half_window) <= win2);
+              bool ok = (kos[u] == -1) | (kos[u] == qopt[t]);
+              if constexpr (LOCAL) ok = ok & ((unsigned)(kws[u] - qpos[t]) <= win2);
               sT[t][i][4 * g + u] = ok ? sT[t][i][4 * g + u] : -INFINITY;
             }
           }
@@ -534,7 +545,7 @@ __global__ __launch_bounds__(64 * QW) __attribute__((amdgpu_waves_per_eu(QT == 1
     if (kn < nkt) {
       const int nb = NBUF == 2 ? b ^ 1 : 0;
       if constexpr (NBUF == 1) __syncthreads();  // every wave is done with the one buffer
-      if (stager) stage_store<T, R>(st, sK[nb], sV[nb], sInfo[nb], tid, ROWK, ROWV);
+      if (stager) stage_store<T, R>(st, sK[nb], sV[nb], sKo[nb], sKw[nb], a.half_window, tid, ROWK, ROWV);
       kn2 = kn_next;  // == next_tile(kn + 1); ki holds its key info
       if (kn2 < nkt) {
         if (stager) stage_load<T, R>(st, qkv, ld, H, head, base, n, kn2 * KTILE, a.cos_t, a.sin_t, ki, tid);
@@ -1201,10 +1212,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void a
 hipError_t launch_attention(int precision, const AttnArgs &a, hipStream_t s) {
   if (a.nwork <= 0) return hipSuccess;
   dim3 grid(a.nwork * a.heads), block(64 * ATTN_WAVES);
-  if (precision == 1)
-    hipLaunchKernelGGL((attention_kernel<bf16, ATTN_WAVES, ATTN_QT>), grid, block, 0, s, a);
-  else
-    hipLaunchKernelGGL((attention_kernel<float, ATTN_WAVES, ATTN_QT>), grid, block, 0, s, a);
+  if (precision == 1) {
+    if (a.sliding)
+      hipLaunchKernelGGL((attention_kernel<bf16, ATTN_WAVES, ATTN_QT, true>), grid, block, 0, s, a);
+    else
+      hipLaunchKernelGGL((attention_kernel<bf16, ATTN_WAVES, ATTN_QT, false>), grid, block, 0, s, a);
+  } else {
+    if (a.sliding)
+      hipLaunchKernelGGL((attention_kernel<float, ATTN_WAVES, ATTN_QT, true>), grid, block, 0, s, a);
+    else
+      hipLaunchKernelGGL((attention_kernel<float, ATTN_WAVES, ATTN_QT, false>), grid, block, 0, s, a);
+  }
   return hipGetLastError();
 }
 
