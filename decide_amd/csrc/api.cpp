@@ -3,6 +3,7 @@
 // replaces are in include/decide_hip.h.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdio>
 #include <cstring>
@@ -123,7 +124,7 @@ void define_tensors(dn_ctx *c) {
     add(p + "attn.Wqkv.weight", 3 * H * H, 2, true);
     add(p + "attn.Wo.weight", H * H, 2, true);
     add(p + "mlp_norm.weight", H, 1);
-    add(p + "mlp.Wi.weight", 2 * I * H, 2, true, true);
+    add(p + "mlp.Wi.weight", 2 * I * H, 2, true, !g.generic);  // interleaved for the MFMA GeGLU epilogue
     add(p + "mlp.Wo.weight", H * I, 2, true);
   }
   add("model.final_norm.weight", H, 1);
@@ -219,6 +220,8 @@ int ctx_workspace(dn_ctx *c, int nseq, const int32_t *seq_len, int R, Workspace 
   o.T = c->lay_T;
   o.nchunks = c->lay_nchunks;
   o.nwork = c->lay_nwork;
+  o.nseq = (int)c->lay_len.size();
+  o.max_len = c->lay_len.empty() ? 0 : *std::max_element(c->lay_len.begin(), c->lay_len.end());
   if (!same) {
     int rc = upload_layout(c, c->hlay, o, nseq, c->lay_len.data(), c->stream);
     if (rc) return rc;
@@ -321,6 +324,12 @@ int enqueue_prologue(dn_ctx *c, const Pass &p, float *cur, void *xn0, float *emb
   return DN_OK;
 }
 
+// A projection GEMM of the model: the MFMA kernels, or the any-shape kernel
+// for geometries they do not tile.
+hipError_t layer_gemm(const Config &g, int epi, const GemmArgs &a, hipStream_t s) {
+  return g.generic ? launch_gemm_generic(g.precision, epi, a, s) : launch_gemm(g.precision, epi, a, s);
+}
+
 // The launches of encoder layer l over the pass's tokens: the residual stream
 // enters in `in`, leaves the attention half in h1 and the layer in out (the
 // same buffer unless training keeps them apart); x1 is the QKV input of layer
@@ -353,7 +362,7 @@ int enqueue_layer(dn_ctx *c, const Pass &p, int l, float *in, float *h1, float *
   q.N = 3 * H;
   q.K = H;
   q.n_store = 3 * H;
-  PROBED(ev, DN_PROBE_QKV, "gemm(Wqkv)", launch_gemm(prec, EPI_STORE, q, s));
+  PROBED(ev, DN_PROBE_QKV, "gemm(Wqkv)", layer_gemm(g, EPI_STORE, q, s));
 
   const float *rope = (const float *)c->rope.p;
   const size_t tab = (size_t)kPositions * 32;
@@ -375,7 +384,12 @@ int enqueue_layer(dn_ctx *c, const Pass &p, int l, float *in, float *h1, float *
   at.first = w.first + (sliding ? w.nwork : 0);
   at.cos_t = rope + (sliding ? 2 : 0) * tab;  // the layer type picks the table (forward.go:297-301)
   at.sin_t = rope + (sliding ? 3 : 1) * tab;
-  PROBED(ev, DN_PROBE_ATTENTION, "attention", launch_attention(prec, at, s));
+  at.nseq = w.nseq;
+  at.max_len = w.max_len;
+  at.head_dim = H / g.heads;
+  at.scale = (float)(1.0 / std::sqrt((double)at.head_dim));  // forward.go:351
+  PROBED(ev, DN_PROBE_ATTENTION, "attention",
+         g.generic ? launch_attention_generic(prec, at, s) : launch_attention(prec, at, s));
 
   GemmArgs o{};
   o.A = at.ctx;
@@ -390,7 +404,7 @@ int enqueue_layer(dn_ctx *c, const Pass &p, int l, float *in, float *h1, float *
   o.K = H;
   o.n_store = H;
   o.accumulate = 1;
-  PROBED(ev, DN_PROBE_WO, "gemm(Wo)", launch_gemm(prec, EPI_F32, o, s));
+  PROBED(ev, DN_PROBE_WO, "gemm(Wo)", layer_gemm(g, EPI_F32, o, s));
 
   void *x2 = S ? S->n2.p : w.xn;
   HIPCHK(c, "ln(mlp_norm)", launch_ln(prec, h1, T, H, (const float *)W(c, pf + "mlp_norm.weight"), g.eps, x2, s,
@@ -410,11 +424,11 @@ int enqueue_layer(dn_ctx *c, const Pass &p, int l, float *in, float *h1, float *
     wi.ldc = 2 * I;
     wi.C2 = S->act.p;
     wi.ldc2 = I;
-    PROBED(ev, DN_PROBE_WI, "gemm(Wi)", launch_gemm(prec, EPI_GEGLU_KEEP, wi, s));
+    PROBED(ev, DN_PROBE_WI, "gemm(Wi)", layer_gemm(g, EPI_GEGLU_KEEP, wi, s));
   } else {
     wi.C = w.act;
     wi.ldc = I;
-    PROBED(ev, DN_PROBE_WI, "gemm(Wi)", launch_gemm(prec, EPI_GEGLU, wi, s));
+    PROBED(ev, DN_PROBE_WI, "gemm(Wi)", layer_gemm(g, EPI_GEGLU, wi, s));
   }
 
   GemmArgs mo{};
@@ -430,7 +444,7 @@ int enqueue_layer(dn_ctx *c, const Pass &p, int l, float *in, float *h1, float *
   mo.K = I;
   mo.n_store = H;
   mo.accumulate = 1;
-  PROBED(ev, DN_PROBE_MLPWO, "gemm(MlpWo)", launch_gemm(prec, EPI_F32, mo, s));
+  PROBED(ev, DN_PROBE_MLPWO, "gemm(MlpWo)", layer_gemm(g, EPI_F32, mo, s));
   return DN_OK;
 }
 
@@ -457,7 +471,7 @@ int enqueue_head(dn_ctx *c, const float *h, int T_total, const int32_t *row_tok,
   ha.out_b = (const float *)W(c, "scorer.out_proj.bias");
   ha.logits = logits;
   ha.err_flag = (int *)c->err_flag.p;
-  HIPCHK(c, "head", launch_head(ha, s1, d, s));
+  HIPCHK(c, "head", launch_head(ha, s1, d, s, g.generic));
   return DN_OK;
 }
 
@@ -496,6 +510,8 @@ int part_layout(dn_ctx *c, int k, int nseq, const int32_t *seq_len, hipStream_t 
   w->T = P.T;
   w->nchunks = P.nchunks;
   w->nwork = P.nwork;
+  w->nseq = nseq;
+  w->max_len = len.empty() ? 0 : *std::max_element(len.begin(), len.end());
   if (!same) return upload_layout(c, P.hl, *w, nseq, P.len.data(), s);
   return DN_OK;
 }
@@ -936,9 +952,16 @@ int dn_set_config(dn_ctx *c, int hidden, int inter, int heads, int layers, int v
     return fail(c, DN_INVALID_ARG, "nn: incomplete or inconsistent config");
   if (precision != DN_PRECISION_FP32 && precision != DN_PRECISION_BF16)
     return fail(c, DN_INVALID_ARG, "decide_hip: unknown precision " + std::to_string(precision));
-  if (hidden / heads != 64 || hidden % 256 != 0 || inter % 64 != 0 || hidden > 1024)
-    return fail(c, DN_UNSUPPORTED, "decide_hip: this build implements head_dim 64, hidden % 256 == 0 (<= 1024) "
-                                   "and intermediate % 64 == 0");
+  // The MFMA kernels take head_dim 64 with hidden % 256 == 0 and intermediate
+  // % 64 == 0 (ModernBERT-base); other geometries up to hidden 1024 with head
+  // widths 8, 16, 32 or 64 (the reference's own test models among them) run
+  // the any-shape GEMM and attention kernels.
+  const int hd = hidden / heads;
+  const bool fast = hd == 64 && hidden % 256 == 0 && inter % 64 == 0 && hidden <= 1024;
+  const bool generic_ok = (hd == 8 || hd == 16 || hd == 32 || hd == 64) && hidden % 8 == 0 && hidden <= 1024;
+  if (!fast && !generic_ok)
+    return fail(c, DN_UNSUPPORTED, "decide_hip: this build implements hidden <= 1024 with hidden % 8 == 0 and "
+                                   "head_dim 8, 16, 32 or 64");
   (void)hipSetDevice(c->device);
   for (auto &kv : c->w) release_slot(kv.second);
   c->w.clear();
@@ -956,12 +979,14 @@ int dn_set_config(dn_ctx *c, int hidden, int inter, int heads, int layers, int v
   g.theta_l = theta_local;
   g.sliding.assign(layer_is_sliding, layer_is_sliding + layers);
   g.precision = precision;
+  g.generic = !fast;
   define_tensors(c);
-  // inv_freq_i = 1 / theta^(2i/64), model.go:244-247.
+  // inv_freq_i = 1 / theta^(2i/D), model.go:244-247, for the D/2 rotation
+  // pairs (tables keep 32 columns; narrower heads use the first D/2).
   double inv[64];
   for (int i = 0; i < 32; i++) {
-    inv[i] = 1.0 / std::pow(theta_global, (double)(2 * i) / 64.0);
-    inv[32 + i] = 1.0 / std::pow(theta_local, (double)(2 * i) / 64.0);
+    inv[i] = i < hd / 2 ? 1.0 / std::pow(theta_global, (double)(2 * i) / (double)hd) : 0.0;
+    inv[32 + i] = i < hd / 2 ? 1.0 / std::pow(theta_local, (double)(2 * i) / (double)hd) : 0.0;
   }
   HIPCHK(c, "hipMalloc", ensure(c->inv_freq, sizeof(inv)));
   HIPCHK(c, "hipMemcpy", hipMemcpy(c->inv_freq.p, inv, sizeof(inv), hipMemcpyHostToDevice));

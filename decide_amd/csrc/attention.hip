@@ -1209,6 +1209,97 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void a
 
 }  // namespace
 
+// Attention for head widths other than 64 (the reference's small test
+// models): thread = one query of one (sequence, head). The reference's attnFwd
+// + softmaxMasked (forward.go:347-409, ops.go) in three passes over the
+// sequence's allowed keys, scores recomputed each time: the maximum of the
+// scaled scores; the f64 sum of e_j = float32(exp(s_j * scale - max)); ctx =
+// sum_j p_j v_j with p_j = e_j * float32(1 / sum). q and k are rotated as
+// applyRope does, in fp32, from the un-rotated qkv.
+template <class T, int D>
+__global__ __launch_bounds__(64) void attention_generic_kernel(AttnArgs a) {
+  constexpr int HALF = D / 2;
+  const int sq = blockIdx.y, head = blockIdx.z;
+  const int n = a.seq_len[sq], base = a.seq_off[sq];
+  const int qi = blockIdx.x * 64 + threadIdx.x;
+  if (qi >= n) return;
+  const int H = a.H, ld = 3 * H;
+  const T *qkv = (const T *)a.qkv;
+  const int qinf = a.kinfo[base + qi];
+  const int qopt = (qinf >> 16) - 1, qpos = qinf & 0xffff;
+  auto rotate = [&](float (&x)[D], int pos) {
+#pragma unroll
+    for (int i = 0; i < HALF; i++) rope1(x[i], x[i + HALF], a.cos_t[(size_t)pos * 32 + i], a.sin_t[(size_t)pos * 32 + i]);
+  };
+  float q[D];
+  {
+    const T *src = qkv + (size_t)(base + qi) * ld + head * D;
+#pragma unroll
+    for (int d = 0; d < D; d++) q[d] = (float)src[d];
+    rotate(q, qpos);
+  }
+  const float scale = a.scale;
+  // Score of key j (raw, unscaled) if the mask allows it.
+  auto score = [&](int j, float &sc) -> bool {
+    const int inf = a.kinfo[base + j], ko = (inf >> 16) - 1, kp = inf & 0xffff;
+    if (ko != -1 && ko != qopt) return false;
+    if (a.sliding && abs(kp - qpos) > a.half_window) return false;
+    float k[D];
+    const T *src = qkv + (size_t)(base + j) * ld + H + head * D;
+#pragma unroll
+    for (int d = 0; d < D; d++) k[d] = (float)src[d];
+    rotate(k, kp);
+    float acc = 0.0f;
+#pragma unroll
+    for (int d = 0; d < D; d++) acc = fmaf(q[d], k[d], acc);
+    sc = acc;
+    return true;
+  };
+  float maxv = -INFINITY;
+  for (int j = 0; j < n; j++) {
+    float sc;
+    if (score(j, sc)) maxv = fmaxf(maxv, sc * scale);
+  }
+  double sum = 0.0;
+  for (int j = 0; j < n; j++) {
+    float sc;
+    if (score(j, sc)) sum += (double)(float)exp((double)(sc * scale - maxv));
+  }
+  const float inv = (float)(1.0 / sum);
+  float o[D];
+#pragma unroll
+  for (int d = 0; d < D; d++) o[d] = 0.0f;
+  for (int j = 0; j < n; j++) {
+    float sc;
+    if (!score(j, sc)) continue;
+    const float p = (float)exp((double)(sc * scale - maxv)) * inv;
+    const T *v = qkv + (size_t)(base + j) * ld + 2 * H + head * D;
+#pragma unroll
+    for (int d = 0; d < D; d++) o[d] = fmaf(p, (float)v[d], o[d]);
+  }
+  T *out = (T *)a.ctx + (size_t)(base + qi) * H + head * D;
+#pragma unroll
+  for (int d = 0; d < D; d++) out[d] = (T)o[d];
+}
+
+template <class T>
+hipError_t launch_attention_generic_t(const AttnArgs &a, hipStream_t s) {
+  const dim3 grid((a.max_len + 63) / 64, a.nseq, a.heads), block(64);
+  switch (a.head_dim) {
+    case 8: hipLaunchKernelGGL((attention_generic_kernel<T, 8>), grid, block, 0, s, a); break;
+    case 16: hipLaunchKernelGGL((attention_generic_kernel<T, 16>), grid, block, 0, s, a); break;
+    case 32: hipLaunchKernelGGL((attention_generic_kernel<T, 32>), grid, block, 0, s, a); break;
+    case 64: hipLaunchKernelGGL((attention_generic_kernel<T, 64>), grid, block, 0, s, a); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_attention_generic(int precision, const AttnArgs &a, hipStream_t s) {
+  if (a.nseq <= 0 || a.max_len <= 0) return hipSuccess;
+  return precision == 1 ? launch_attention_generic_t<bf16>(a, s) : launch_attention_generic_t<float>(a, s);
+}
+
 hipError_t launch_attention(int precision, const AttnArgs &a, hipStream_t s) {
   if (a.nwork <= 0) return hipSuccess;
   dim3 grid(a.nwork * a.heads), block(64 * ATTN_WAVES);

@@ -165,6 +165,11 @@ struct GemmArgs {
 enum { EPI_F32 = 0, EPI_STORE = 1, EPI_GEGLU = 2, EPI_GEGLU_KEEP = 3, EPI_GEGLU_BWD = 4 };
 
 hipError_t launch_gemm(int precision, int epi, const GemmArgs &a, hipStream_t s);
+// Any-shape GEMM for model geometries the MFMA kernels do not tile: one thread
+// per output element, an fp32 dot product over K in order. EPI_F32,
+// EPI_STORE and EPI_GEGLU, the last over the natural Wi layout (value rows
+// [0, N/2), gate rows [N/2, N); output N/2 columns).
+hipError_t launch_gemm_generic(int precision, int epi, const GemmArgs &a, hipStream_t s);
 // Whether launch_gemm takes this epilogue at M rows (EPI_GEGLU_BWD needs the
 // tiled kernel: M > 128 in bf16, M > 1024 in fp32).
 bool gemm_epi_ok(int precision, int epi, int M);
@@ -201,8 +206,15 @@ struct AttnArgs {
   float scale_log2;   // softmax scale * log2(e)
   float *lse;         // training: per (token, head) log2 of the softmax denominator of the
                       // scaled scores, lse[t*heads + head] = max*scale_log2 + log2(sum); null otherwise
+  int nseq, max_len, head_dim;  // the any-geometry kernel: sequences, longest one, head width,
+  float scale;                  // and the softmax scale float32(1 / sqrt(head_dim))
 };
 hipError_t launch_attention(int precision, const AttnArgs &a, hipStream_t s);
+// Attention for model geometries the MFMA kernel does not take (head width 8,
+// 16 or 32; the reference's own small test models): one thread per query,
+// the reference's two-pass masked softmax (attnFwd + softmaxMasked,
+// forward.go:347-409, ops.go), fp32 arithmetic. Same inputs and output.
+hipError_t launch_attention_generic(int precision, const AttnArgs &a, hipStream_t s);
 
 // Attention backward (the reference's attnBwd + the RoPE inverse,
 // backward.go:117-159 and :77-81): dqkv from dctx, the un-rotated qkv, ctx and
@@ -249,7 +261,9 @@ struct HeadArgs {
   float *logits;
   int *err_flag;
 };
-hipError_t launch_head(const HeadArgs &a, float *s1, float *d, hipStream_t s);
+// generic: the dense layer's GEMM on the any-shape kernel (geometries the
+// MFMA GEMMs do not tile).
+hipError_t launch_head(const HeadArgs &a, float *s1, float *d, hipStream_t s, bool generic = false);
 hipError_t launch_pack(const float *src, int trans, int rows, int cols, int ld, float *dst, int dst_rows,
                        int dst_cols, hipStream_t s);
 

@@ -41,6 +41,10 @@ struct Config {
   double theta_g = 160000, theta_l = 10000;
   std::vector<uint8_t> sliding;
   int precision = DN_PRECISION_BF16;
+  // Geometry outside the MFMA kernels' shapes (head_dim != 64, hidden % 256,
+  // intermediate % 64): any-shape GEMM and attention kernels, Wi stored in its
+  // natural layout, no training.
+  bool generic = false;
 };
 
 // Activations of one layer kept by a training forward (the reference's
@@ -94,6 +98,7 @@ struct Workspace {
   ChunkInfo *chunks = nullptr;
   uint32_t *codes = nullptr;
   int T = 0, nchunks = 0, nwork = 0;
+  int nseq = 0, max_len = 0;
 };
 
 // The batch layout on the host: token offset and 32-token chunk offset of

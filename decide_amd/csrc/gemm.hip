@@ -727,6 +727,54 @@ bool gemm_epi_ok(int precision, int epi, int M) {
   return precision == 1 ? M > 128 : M > 1024;
 }
 
+// Any-shape GEMM (model geometries the MFMA kernels do not tile): thread n of
+// block (x, m) computes output element (m, 256 x + n) as an fp32 dot product
+// over K in order, then the epilogue. Performance is not its purpose.
+template <class T, int EPI>
+__global__ __launch_bounds__(256) void gemm_generic_kernel(GemmArgs g) {
+  const int m = blockIdx.y, n = blockIdx.x * 256 + threadIdx.x;
+  const int ncols = EPI == EPI_GEGLU ? g.N / 2 : g.N;
+  if (m >= g.M || n >= ncols) return;
+  const T *a = (const T *)g.A + (size_t)m * g.lda;
+  auto dot = [&](int row) {
+    const T *b = (const T *)g.B + (size_t)row * g.ldb;
+    float acc = 0.0f;
+    for (int k = 0; k < g.K; k++) acc = fmaf((float)a[k], (float)b[k], acc);
+    return acc;
+  };
+  if constexpr (EPI == EPI_F32) {
+    if (n >= g.n_store) return;
+    const float v = dot(n);
+    float *C = (float *)g.C + (size_t)m * g.ldc + n;
+    const float *R = g.res ? g.res + (size_t)m * g.ldc + n : C;
+    *C = g.accumulate ? *R + v : v;
+  } else if constexpr (EPI == EPI_STORE) {
+    ((T *)g.C)[(size_t)m * g.ldc + n] = (T)dot(n);
+  } else {
+    const float v = dot(n), gate = dot(ncols + n);
+    ((T *)g.C)[(size_t)m * g.ldc + n] = (T)(gelu_erf<T>(v) * gate);
+  }
+}
+
+template <class T>
+hipError_t launch_gemm_generic_t(int epi, const GemmArgs &a, hipStream_t s) {
+  const int ncols = epi == EPI_GEGLU ? a.N / 2 : a.N;
+  const dim3 grid((ncols + 255) / 256, a.M), block(256);
+  switch (epi) {
+    case EPI_F32: hipLaunchKernelGGL((gemm_generic_kernel<T, EPI_F32>), grid, block, 0, s, a); break;
+    case EPI_STORE: hipLaunchKernelGGL((gemm_generic_kernel<T, EPI_STORE>), grid, block, 0, s, a); break;
+    case EPI_GEGLU: hipLaunchKernelGGL((gemm_generic_kernel<T, EPI_GEGLU>), grid, block, 0, s, a); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_gemm_generic(int precision, int epi, const GemmArgs &a, hipStream_t s) {
+  if (a.M <= 0) return hipSuccess;
+  if (a.N <= 0 || a.K <= 0 || (epi == EPI_GEGLU && a.N % 2)) return hipErrorInvalidValue;
+  return precision == 1 ? launch_gemm_generic_t<bf16>(epi, a, s) : launch_gemm_generic_t<float>(epi, a, s);
+}
+
 hipError_t launch_gemm(int precision, int epi, const GemmArgs &a0, hipStream_t s) {
   if (a0.M <= 0) return hipSuccess;
   if (!gemm_epi_ok(precision, epi, a0.M) || (epi == EPI_GEGLU_BWD && (!a0.gin || a0.ldc % 8))) return hipErrorInvalidValue;

@@ -12,6 +12,7 @@
 // Nothing in it needs to start at zero: each forward writes every element it
 // reads (embedding + LayerNorm write the residual stream before the residual
 // GEMMs accumulate into it; the layout is uploaded by every call).
+#include <algorithm>
 #include <mutex>
 
 #include "ctx.hpp"
@@ -111,6 +112,8 @@ extern "C" int dn_forward_device_noalloc(dn_ctx *c, int nseq, const int32_t *seq
   w.T = T;
   w.nchunks = nch;
   w.nwork = nwork;
+  w.nseq = nseq;
+  w.max_len = *std::max_element(seq_len, seq_len + nseq);
   rc = upload_layout(c, c->hlay, w, nseq, seq_len, c->stream);
   if (rc) return rc;
   return forward_core(c, nseq, seq_len, d_ids, d_pos, d_opt_id, nrows, d_row_tok, d_logits, false, &w);

@@ -294,9 +294,9 @@ hipError_t launch_rope_tables(const int *pos, int Tn, const double *inv_g, const
   return hipGetLastError();
 }
 
-hipError_t launch_head(const HeadArgs &a, float *s1, float *d, hipStream_t s) {
+hipError_t launch_head(const HeadArgs &a, float *s1, float *d, hipStream_t s, bool generic) {
   if (a.R <= 0) return hipSuccess;
-  if (a.H > 1024 || a.H % 256 != 0) return hipErrorInvalidValue;
+  if (a.H > 1024 || a.H % 8 != 0) return hipErrorInvalidValue;
   const dim3 grid((a.R + 3) / 4), block(256);
   hipLaunchKernelGGL(head_pre_kernel, grid, block, 0, s, a, s1);
   hipError_t e = hipGetLastError();
@@ -312,7 +312,7 @@ hipError_t launch_head(const HeadArgs &a, float *s1, float *d, hipStream_t s) {
   g.N = a.H / 2;
   g.K = a.H;
   g.n_store = a.H / 2;
-  e = launch_gemm(0, EPI_F32, g, s);
+  e = generic ? launch_gemm_generic(0, EPI_F32, g, s) : launch_gemm(0, EPI_F32, g, s);
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(head_post_kernel, grid, block, 0, s, a, d);
   return hipGetLastError();

@@ -501,6 +501,9 @@ int dn_enable_training(dn_ctx *c) {
   c->err.clear();
   if (!c->configured) return fail(c, DN_INVALID_ARG, "decide_hip: dn_set_config has not been called");
   if (c->tr.enabled) return DN_OK;
+  if (c->cfg.generic)
+    return fail(c, DN_UNSUPPORTED, "decide_hip: training needs head_dim 64, hidden % 256 == 0 and "
+                                   "intermediate % 64 == 0");
   for (auto &kv : c->w)
     if (kv.second.set && bf16_slot(c, kv.second))
       return fail(c, DN_INVALID_ARG, "decide_hip: dn_enable_training must precede the weight uploads");

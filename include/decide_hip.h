@@ -76,9 +76,12 @@ int dn_set_stream(dn_ctx *ctx, void *stream);
  * residual stream, statistics and head; DN_PRECISION_FP32 = fp32 MFMA
  * everywhere (the validation build). Must precede dn_upload_tensor.
  * Replaces the config capture of gpunn.New (internal/gpunn/model.go:80-122).
- * This build implements head_dim 64 with hidden % 256 == 0 (<= 1024) and
- * inter % 64 == 0 (ModernBERT-base: 768/1152/12 heads); others give
- * DN_UNSUPPORTED. */
+ * head_dim 64 with hidden % 256 == 0 (<= 1024) and inter % 64 == 0
+ * (ModernBERT-base: 768/1152/12 heads) runs the MFMA kernels; other
+ * geometries with hidden <= 1024, hidden % 8 == 0 and head_dim 8, 16, 32 or
+ * 64 (the reference's own test models, e.g. tiny_ref's 32/48/4 heads) run
+ * any-shape GEMM and attention kernels (inference only: dn_enable_training
+ * reports DN_UNSUPPORTED for them); anything else gives DN_UNSUPPORTED. */
 int dn_set_config(dn_ctx *ctx, int hidden, int inter, int heads, int layers, int vocab, float eps,
                   int half_window, double theta_global, double theta_local,
                   const uint8_t *layer_is_sliding /* [layers] */, int precision);
