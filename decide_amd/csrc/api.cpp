@@ -146,12 +146,23 @@ const void *W(dn_ctx *c, const std::string &name) {
   return it == c->w.end() ? nullptr : it->second.buf.p;
 }
 
+// The global-layer work items (ATTN_QUERIES_GLOBAL queries) follow the
+// ATTN_QUERIES ones in the work array; their tile codes and first tiles
+// follow the two sections (global, local) of the ATTN_QUERIES items.
+void set_work2(Workspace &w, int nwork2) {
+  w.nwork2 = nwork2;
+  w.work2 = w.work + w.nwork;
+  w.codes2 = w.codes + (size_t)2 * w.nwork * ATTN_MAXKT;
+  w.first2 = w.first + 2 * w.nwork;
+}
+
 // Batch layout: sequence offsets, 32-token chunks and ATTN_QUERIES-query work items.
 void host_layout(HostLayout &hl, int nseq, const int32_t *seq_len, int *T_out, int *nch_out) {
   hl.seq_off.assign(nseq + 1, 0);
   hl.chunk_off.assign(nseq + 1, 0);
   hl.chunk_desc.clear();
   hl.work.clear();
+  hl.work2.clear();
   int T = 0, nch = 0;
   for (int s = 0; s < nseq; s++) {
     const int n = seq_len[s];
@@ -159,6 +170,7 @@ void host_layout(HostLayout &hl, int nseq, const int32_t *seq_len, int *T_out, i
     hl.chunk_off[s] = nch;
     for (int i = 0; i < n; i += 32) hl.chunk_desc.push_back(make_int4(T + i, std::min(32, n - i), 0, 0));
     for (int q = 0; q < n; q += ATTN_QUERIES) hl.work.push_back(make_int4(s, q, 0, 0));
+    for (int q = 0; q < n; q += ATTN_QUERIES_GLOBAL) hl.work2.push_back(make_int4(s, q, 0, 0));
     nch += (n + 31) / 32;
     T += n;
   }
@@ -181,6 +193,9 @@ int upload_layout(dn_ctx *c, const HostLayout &hl, const Workspace &w, int nseq,
   if (!hl.work.empty())
     HIPCHK(c, "hipMemcpyAsync",
            hipMemcpyAsync(w.work, hl.work.data(), sizeof(int4) * hl.work.size(), hipMemcpyHostToDevice, s));
+  if (!hl.work2.empty())
+    HIPCHK(c, "hipMemcpyAsync",
+           hipMemcpyAsync(w.work2, hl.work2.data(), sizeof(int4) * hl.work2.size(), hipMemcpyHostToDevice, s));
   return DN_OK;
 }
 
@@ -194,19 +209,20 @@ int ctx_workspace(dn_ctx *c, int nseq, const int32_t *seq_len, int R, Workspace 
     c->lay_len.clear();
     int T = 0, nch = 0;
     host_layout(c->hlay, nseq, seq_len, &T, &nch);
-    const size_t nw = c->hlay.work.size();
+    const size_t nw = c->hlay.work.size(), nw2 = c->hlay.work2.size();
     HIPCHK(c, "hipMalloc", ensure(c->d_seq_off, sizeof(int) * (nseq + 1)));
     HIPCHK(c, "hipMalloc", ensure(c->d_seq_len, sizeof(int) * (nseq + 1)));
     HIPCHK(c, "hipMalloc", ensure(c->d_chunk_off, sizeof(int) * (nseq + 1)));
     HIPCHK(c, "hipMalloc", ensure(c->d_chunk_desc, sizeof(int4) * (nch + 1)));
     HIPCHK(c, "hipMalloc", ensure(c->d_chunks, sizeof(ChunkInfo) * (nch + 1)));
-    HIPCHK(c, "hipMalloc", ensure(c->d_work, sizeof(int4) * (nw + 1)));
-    HIPCHK(c, "hipMalloc", ensure(c->d_codes, sizeof(uint32_t) * 2 * ATTN_MAXKT * (nw + 1)));
-    HIPCHK(c, "hipMalloc", ensure(c->d_first, sizeof(int) * 2 * (nw + 1)));
+    HIPCHK(c, "hipMalloc", ensure(c->d_work, sizeof(int4) * (nw + nw2 + 1)));
+    HIPCHK(c, "hipMalloc", ensure(c->d_codes, sizeof(uint32_t) * ATTN_MAXKT * (2 * nw + nw2 + 1)));
+    HIPCHK(c, "hipMalloc", ensure(c->d_first, sizeof(int) * (2 * nw + nw2 + 1)));
     c->lay_len = len;
     c->lay_T = T;
     c->lay_nchunks = nch;
     c->lay_nwork = (int)nw;
+    c->lay_nwork2 = (int)nw2;
   }
   Workspace &o = *w;
   o.seq_off = (int *)c->d_seq_off.p;
@@ -220,6 +236,7 @@ int ctx_workspace(dn_ctx *c, int nseq, const int32_t *seq_len, int R, Workspace 
   o.T = c->lay_T;
   o.nchunks = c->lay_nchunks;
   o.nwork = c->lay_nwork;
+  set_work2(o, c->lay_nwork2);
   o.nseq = (int)c->lay_len.size();
   o.max_len = c->lay_len.empty() ? 0 : *std::max_element(c->lay_len.begin(), c->lay_len.end());
   if (!same) {
@@ -300,6 +317,7 @@ hipEvent_t *probe_slot(dn_ctx *c, int l) {
 // forward, a view at the part's token offset into the context's buffers),
 // those tokens' ids / positions / option ids, and the stream.
 struct Pass {
+  bool train = false;  // a training forward: every layer on the ATTN_QUERIES work items
   Workspace w;
   const int32_t *ids, *pos, *opt;
   hipStream_t s;
@@ -314,9 +332,14 @@ int enqueue_prologue(dn_ctx *c, const Pass &p, float *cur, void *xn0, float *emb
   HIPCHK(c, "token_info", launch_token_info(p.pos, p.opt, w.kinfo, w.T, (int *)c->err_flag.p, s));
   HIPCHK(c, "chunk_summary", launch_chunk_summary(w.kinfo, w.chunk_desc, w.chunks, w.nchunks, s));
   const size_t nw = (size_t)w.nwork;
-  for (int sl = 0; sl < 2; sl++)  // global, then local
+  // Local layers always use the ATTN_QUERIES items; global layers those in
+  // training (the backward's layout) and the ATTN_QUERIES_GLOBAL ones else.
+  for (int sl = p.train ? 0 : 1; sl < 2; sl++)
     HIPCHK(c, "tile_codes", launch_tile_codes(w.chunks, w.work, w.seq_len, w.chunk_off, w.nwork, sl, g.half_window,
                                               w.codes + sl * nw * ATTN_MAXKT, w.first + sl * nw, s));
+  if (!p.train)
+    HIPCHK(c, "tile_codes", launch_tile_codes(w.chunks, w.work2, w.seq_len, w.chunk_off, w.nwork2, 0, g.half_window,
+                                              w.codes2, w.first2, s, ATTN_WAVES * ATTN_QT_GLOBAL));
   HIPCHK(c, "embed_ln",
          launch_embed_ln(g.precision, p.ids, w.T, (const float *)W(c, "model.embeddings.tok_embeddings.weight"),
                          g.vocab, (const float *)W(c, "model.embeddings.norm.weight"), g.eps, g.hidden, cur, xn0,
@@ -382,6 +405,14 @@ int enqueue_layer(dn_ctx *c, const Pass &p, int l, float *in, float *h1, float *
   at.sliding = sliding ? 1 : 0;
   at.codes = w.codes + (sliding ? (size_t)w.nwork * ATTN_MAXKT : 0);
   at.first = w.first + (sliding ? w.nwork : 0);
+  at.qt = ATTN_QT;
+  if (!sliding && !p.train && w.nwork2 > 0) {  // global layer of an inference forward: 256-query items
+    at.work = w.work2;
+    at.nwork = w.nwork2;
+    at.codes = w.codes2;
+    at.first = w.first2;
+    at.qt = ATTN_QT_GLOBAL;
+  }
   at.cos_t = rope + (sliding ? 2 : 0) * tab;  // the layer type picks the table (forward.go:297-301)
   at.sin_t = rope + (sliding ? 3 : 1) * tab;
   at.nseq = w.nseq;
@@ -485,19 +516,20 @@ int part_layout(dn_ctx *c, int k, int nseq, const int32_t *seq_len, hipStream_t 
   if (!same) {
     int T = 0, nch = 0;
     host_layout(P.hl, nseq, seq_len, &T, &nch);
-    const size_t nw = P.hl.work.size();
+    const size_t nw = P.hl.work.size(), nw2 = P.hl.work2.size();
     HIPCHK(c, "hipMalloc", ensure(P.d_seq_off, sizeof(int) * (nseq + 1)));
     HIPCHK(c, "hipMalloc", ensure(P.d_seq_len, sizeof(int) * (nseq + 1)));
     HIPCHK(c, "hipMalloc", ensure(P.d_chunk_off, sizeof(int) * (nseq + 1)));
     HIPCHK(c, "hipMalloc", ensure(P.d_chunk_desc, sizeof(int4) * (nch + 1)));
     HIPCHK(c, "hipMalloc", ensure(P.d_chunks, sizeof(ChunkInfo) * (nch + 1)));
-    HIPCHK(c, "hipMalloc", ensure(P.d_work, sizeof(int4) * (nw + 1)));
-    HIPCHK(c, "hipMalloc", ensure(P.d_codes, sizeof(uint32_t) * 2 * ATTN_MAXKT * (nw + 1)));
-    HIPCHK(c, "hipMalloc", ensure(P.d_first, sizeof(int) * 2 * (nw + 1)));
+    HIPCHK(c, "hipMalloc", ensure(P.d_work, sizeof(int4) * (nw + nw2 + 1)));
+    HIPCHK(c, "hipMalloc", ensure(P.d_codes, sizeof(uint32_t) * ATTN_MAXKT * (2 * nw + nw2 + 1)));
+    HIPCHK(c, "hipMalloc", ensure(P.d_first, sizeof(int) * (2 * nw + nw2 + 1)));
     P.len = len;
     P.T = T;
     P.nchunks = nch;
     P.nwork = (int)nw;
+    P.nwork2 = (int)nw2;
   }
   w->seq_off = (int *)P.d_seq_off.p;
   w->seq_len = (int *)P.d_seq_len.p;
@@ -510,6 +542,7 @@ int part_layout(dn_ctx *c, int k, int nseq, const int32_t *seq_len, hipStream_t 
   w->T = P.T;
   w->nchunks = P.nchunks;
   w->nwork = P.nwork;
+  set_work2(*w, P.nwork2);
   w->nseq = nseq;
   w->max_len = len.empty() ? 0 : *std::max_element(len.begin(), len.end());
   if (!same) return upload_layout(c, P.hl, *w, nseq, P.len.data(), s);
@@ -657,6 +690,7 @@ int forward_core(dn_ctx *c, int nseq, const int32_t *seq_len, const int32_t *d_i
   if (rc) return rc;
 
   Pass ps;
+  ps.train = train;
   ps.w = w;
   ps.ids = d_ids;
   ps.pos = d_pos;

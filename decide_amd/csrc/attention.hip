@@ -1303,14 +1303,21 @@ hipError_t launch_attention_generic(int precision, const AttnArgs &a, hipStream_
 hipError_t launch_attention(int precision, const AttnArgs &a, hipStream_t s) {
   if (a.nwork <= 0) return hipSuccess;
   dim3 grid(a.nwork * a.heads), block(64 * ATTN_WAVES);
+  // Sliding-window layers take ATTN_QT; global layers ATTN_QT or (their
+  // inference layout) ATTN_QT_GLOBAL.
+  if (a.qt != ATTN_QT && (a.sliding || a.qt != ATTN_QT_GLOBAL)) return hipErrorInvalidValue;
   if (precision == 1) {
     if (a.sliding)
       hipLaunchKernelGGL((attention_kernel<bf16, ATTN_WAVES, ATTN_QT, true>), grid, block, 0, s, a);
+    else if (a.qt == ATTN_QT_GLOBAL)
+      hipLaunchKernelGGL((attention_kernel<bf16, ATTN_WAVES, ATTN_QT_GLOBAL, false>), grid, block, 0, s, a);
     else
       hipLaunchKernelGGL((attention_kernel<bf16, ATTN_WAVES, ATTN_QT, false>), grid, block, 0, s, a);
   } else {
     if (a.sliding)
       hipLaunchKernelGGL((attention_kernel<float, ATTN_WAVES, ATTN_QT, true>), grid, block, 0, s, a);
+    else if (a.qt == ATTN_QT_GLOBAL)
+      hipLaunchKernelGGL((attention_kernel<float, ATTN_WAVES, ATTN_QT_GLOBAL, false>), grid, block, 0, s, a);
     else
       hipLaunchKernelGGL((attention_kernel<float, ATTN_WAVES, ATTN_QT, false>), grid, block, 0, s, a);
   }
@@ -1318,10 +1325,17 @@ hipError_t launch_attention(int precision, const AttnArgs &a, hipStream_t s) {
 }
 
 hipError_t launch_tile_codes(const ChunkInfo *chunks, const int4 *work, const int *seq_len, const int *chunk_off,
-                             int nwork, int sliding, int half_window, uint32_t *codes, int *first, hipStream_t s) {
+                             int nwork, int sliding, int half_window, uint32_t *codes, int *first, hipStream_t s,
+                             int nc) {
   if (nwork <= 0) return hipSuccess;
-  hipLaunchKernelGGL(tile_codes_kernel<ATTN_WAVES * ATTN_QT>, dim3(nwork), dim3(64), 0, s, chunks, work, seq_len, chunk_off,
-                     sliding, half_window, codes, first);
+  if (nc == ATTN_WAVES * ATTN_QT)
+    hipLaunchKernelGGL(tile_codes_kernel<ATTN_WAVES * ATTN_QT>, dim3(nwork), dim3(64), 0, s, chunks, work, seq_len,
+                       chunk_off, sliding, half_window, codes, first);
+  else if (nc == ATTN_WAVES * ATTN_QT_GLOBAL)
+    hipLaunchKernelGGL(tile_codes_kernel<ATTN_WAVES * ATTN_QT_GLOBAL>, dim3(nwork), dim3(64), 0, s, chunks, work,
+                       seq_len, chunk_off, sliding, half_window, codes, first);
+  else
+    return hipErrorInvalidValue;
   return hipGetLastError();
 }
 

@@ -180,16 +180,18 @@ bool gemm_epi_ok(int precision, int epi, int M);
 hipError_t launch_gemm_splitk(int precision, const GemmArgs &a, int splits, float *partial, hipStream_t s);
 bool gemm_shape_ok(int precision, int N, int K);
 
-// Attention work item: 32 * ATTN_QT * ATTN_WAVES queries of one sequence
-// (each wave owns ATTN_QT tiles of 32 queries), for every head. ATTN_QT = 2
-// halves the LDS fragment reads per MFMA but needs 250 VGPRs (2 waves per
-// SIMD instead of 3); measured slower (cfg3 local layers 90 -> 111 us), so 1.
+// Attention work item: 32 * QT * ATTN_WAVES queries of one sequence (each
+// wave owns QT tiles of 32 queries), for every head. The kernel waits mostly
+// on its staged key tiles (one tile of prefetch), so more queries per staged
+// tile pays where a work item walks many tiles: global layers of an
+// inference forward take QT = 2 (256 queries, 2 waves per SIMD; cfg3 global
+// layers ~125 -> ~63 us), sliding-window layers and training QT = 1 (128
+// queries, 3 waves per SIMD; local layers with QT = 2: 86 -> 104 us).
 constexpr int ATTN_WAVES = 4;
-#ifndef ATTN_QT_SETTING
-#define ATTN_QT_SETTING 1
-#endif
-constexpr int ATTN_QT = ATTN_QT_SETTING;
+constexpr int ATTN_QT = 1;
 constexpr int ATTN_QUERIES = 32 * ATTN_QT * ATTN_WAVES;
+constexpr int ATTN_QT_GLOBAL = 2;
+constexpr int ATTN_QUERIES_GLOBAL = 32 * ATTN_QT_GLOBAL * ATTN_WAVES;
 // Key tiles (64 keys) per sequence: sequences up to 8192 tokens.
 constexpr int ATTN_MAXKT = 128;
 
@@ -206,6 +208,7 @@ struct AttnArgs {
   float scale_log2;   // softmax scale * log2(e)
   float *lse;         // training: per (token, head) log2 of the softmax denominator of the
                       // scaled scores, lse[t*heads + head] = max*scale_log2 + log2(sum); null otherwise
+  int qt;                       // query tiles per wave of the work items (ATTN_QT or ATTN_QT_GLOBAL)
   int nseq, max_len, head_dim;  // the any-geometry kernel: sequences, longest one, head width,
   float scale;                  // and the softmax scale float32(1 / sqrt(head_dim))
 };
@@ -240,8 +243,10 @@ struct AttnBwdArgs {
 };
 hipError_t launch_attention_bwd(int precision, const AttnBwdArgs &a, hipStream_t s);
 
+// Tile classes of work items of 32 * nc queries (nc = ATTN_WAVES * QT).
 hipError_t launch_tile_codes(const ChunkInfo *chunks, const int4 *work, const int *seq_len, const int *chunk_off,
-                             int nwork, int sliding, int half_window, uint32_t *codes, int *first, hipStream_t s);
+                             int nwork, int sliding, int half_window, uint32_t *codes, int *first, hipStream_t s,
+                             int nc = ATTN_WAVES * ATTN_QT);
 hipError_t launch_chunk_summary(const int *kinfo, const int4 *chunk_desc, ChunkInfo *out, int nchunks, hipStream_t s);
 hipError_t launch_token_info(const int *pos, const int *opt, int *kinfo, int T, int *err_flag, hipStream_t s);
 hipError_t launch_rope_tables(const int *pos, int T, const double *inv_g, const double *inv_l, float *cos_g,

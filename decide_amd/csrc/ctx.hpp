@@ -97,6 +97,13 @@ struct Workspace {
   int4 *chunk_desc = nullptr, *work = nullptr;
   ChunkInfo *chunks = nullptr;
   uint32_t *codes = nullptr;
+  // Global-layer work items of ATTN_QUERIES_GLOBAL queries (inference), their
+  // tile codes and first tiles (inside the arrays above, after the
+  // ATTN_QUERIES items' sections).
+  int4 *work2 = nullptr;
+  uint32_t *codes2 = nullptr;
+  int *first2 = nullptr;
+  int nwork2 = 0;
   int T = 0, nchunks = 0, nwork = 0;
   int nseq = 0, max_len = 0;
 };
@@ -106,7 +113,7 @@ struct Workspace {
 // items (sequence, first query).
 struct HostLayout {
   std::vector<int> seq_off, chunk_off;
-  std::vector<int4> chunk_desc, work;
+  std::vector<int4> chunk_desc, work, work2;  // work2: ATTN_QUERIES_GLOBAL-query items
 };
 
 // One part of a forward split over two streams: its sequences' layout and
@@ -116,7 +123,7 @@ struct PartLayout {
   std::vector<int> len;
   HostLayout hl;
   DevBuf d_seq_off, d_seq_len, d_chunk_off, d_chunk_desc, d_chunks, d_work, d_codes, d_first;
-  int T = 0, nchunks = 0, nwork = 0;
+  int T = 0, nchunks = 0, nwork = 0, nwork2 = 0;
 };
 constexpr int kMaxParts = 2;
 
@@ -159,7 +166,7 @@ struct dn_ctx {
   HostLayout hlay;
   DevBuf d_seq_off, d_seq_len, d_chunk_off, d_chunk_desc, d_work, d_chunks;
   DevBuf d_codes, d_first;  // attention tile classes per work item: [global | local]
-  int lay_T = 0, lay_nchunks = 0, lay_nwork = 0;
+  int lay_T = 0, lay_nchunks = 0, lay_nwork = 0, lay_nwork2 = 0;
   // kernel probe: events[2*k], events[2*k+1] bracket launch k of one forward
   int probe_layer = -1;
   std::vector<hipEvent_t> probe_pool;  // 10 events per recorded forward
@@ -204,6 +211,9 @@ int upload_layout(dn_ctx *c, const HostLayout &hl, const Workspace &w, int nseq,
 // RoPE tables of the configured thetas and the device error flag: built at
 // set-up (dn_set_config), so forwards allocate neither.
 int ensure_rope(dn_ctx *c);
+// Points the global-layer (ATTN_QUERIES_GLOBAL) work-item fields of w into
+// its work / codes / first arrays, after the ATTN_QUERIES items' sections.
+void set_work2(Workspace &w, int nwork2);
 int ensure_err_flag(dn_ctx *c);
 // Fills in the context's own scratch pointer for its device (noalloc.cpp;
 // called by dn_open with the device current).

@@ -72,7 +72,7 @@ extern "C" int dn_forward_device_noalloc(dn_ctx *c, int nseq, const int32_t *seq
   HIPCHK(c, "hipStreamSynchronize", hipStreamSynchronize(c->stream));
   int T = 0, nch = 0;
   host_layout(c->hlay, nseq, seq_len, &T, &nch);
-  const int nwork = (int)c->hlay.work.size();
+  const int nwork = (int)c->hlay.work.size(), nwork2 = (int)c->hlay.work2.size();
   const Config &g = c->cfg;
   const size_t es = g.precision == DN_PRECISION_BF16 ? 2 : 4, H = g.hidden, I = g.inter, Tz = T;
   const size_t R1 = (size_t)(nrows > 0 ? nrows : 1);
@@ -98,9 +98,9 @@ extern "C" int dn_forward_device_noalloc(dn_ctx *c, int nseq, const int32_t *seq
   w.chunk_off = (int *)take(sizeof(int) * (nseq + 1));
   w.chunk_desc = (int4 *)take(sizeof(int4) * (nch + 1));
   w.chunks = (ChunkInfo *)take(sizeof(ChunkInfo) * (nch + 1));
-  w.work = (int4 *)take(sizeof(int4) * (nwork + 1));
-  w.codes = (uint32_t *)take(sizeof(uint32_t) * 2 * ATTN_MAXKT * (nwork + 1));
-  w.first = (int *)take(sizeof(int) * 2 * (nwork + 1));
+  w.work = (int4 *)take(sizeof(int4) * (nwork + nwork2 + 1));
+  w.codes = (uint32_t *)take(sizeof(uint32_t) * ATTN_MAXKT * (2 * nwork + nwork2 + 1));
+  w.first = (int *)take(sizeof(int) * (2 * nwork + nwork2 + 1));
   if (off > kScratchBytes) {
     const size_t per_token = sizeof(float) * H + es * (5 * H + I) + sizeof(int);
     return fail(c, DN_INVALID_ARG, "decide_hip: dn_forward_device_noalloc: this batch (" + std::to_string(T) +
@@ -112,6 +112,7 @@ extern "C" int dn_forward_device_noalloc(dn_ctx *c, int nseq, const int32_t *seq
   w.T = T;
   w.nchunks = nch;
   w.nwork = nwork;
+  set_work2(w, nwork2);
   w.nseq = nseq;
   w.max_len = *std::max_element(seq_len, seq_len + nseq);
   rc = upload_layout(c, c->hlay, w, nseq, seq_len, c->stream);
