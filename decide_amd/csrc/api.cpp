@@ -317,7 +317,10 @@ hipEvent_t *probe_slot(dn_ctx *c, int l) {
 // forward, a view at the part's token offset into the context's buffers),
 // those tokens' ids / positions / option ids, and the stream.
 struct Pass {
-  bool train = false;  // a training forward: every layer on the ATTN_QUERIES work items
+  // Global layers on ATTN_QUERIES_GLOBAL work items (the two-stream forward of
+  // a large batch); every other forward, training included, uses ATTN_QUERIES
+  // items for all layers.
+  bool wide_global = false;
   Workspace w;
   const int32_t *ids, *pos, *opt;
   hipStream_t s;
@@ -332,12 +335,12 @@ int enqueue_prologue(dn_ctx *c, const Pass &p, float *cur, void *xn0, float *emb
   HIPCHK(c, "token_info", launch_token_info(p.pos, p.opt, w.kinfo, w.T, (int *)c->err_flag.p, s));
   HIPCHK(c, "chunk_summary", launch_chunk_summary(w.kinfo, w.chunk_desc, w.chunks, w.nchunks, s));
   const size_t nw = (size_t)w.nwork;
-  // Local layers always use the ATTN_QUERIES items; global layers those in
-  // training (the backward's layout) and the ATTN_QUERIES_GLOBAL ones else.
-  for (int sl = p.train ? 0 : 1; sl < 2; sl++)
+  // Local layers use the ATTN_QUERIES items; global layers too, or the
+  // ATTN_QUERIES_GLOBAL ones in the two-stream forward.
+  for (int sl = p.wide_global ? 1 : 0; sl < 2; sl++)
     HIPCHK(c, "tile_codes", launch_tile_codes(w.chunks, w.work, w.seq_len, w.chunk_off, w.nwork, sl, g.half_window,
                                               w.codes + sl * nw * ATTN_MAXKT, w.first + sl * nw, s));
-  if (!p.train)
+  if (p.wide_global)
     HIPCHK(c, "tile_codes", launch_tile_codes(w.chunks, w.work2, w.seq_len, w.chunk_off, w.nwork2, 0, g.half_window,
                                               w.codes2, w.first2, s, ATTN_WAVES * ATTN_QT_GLOBAL));
   HIPCHK(c, "embed_ln",
@@ -406,7 +409,7 @@ int enqueue_layer(dn_ctx *c, const Pass &p, int l, float *in, float *h1, float *
   at.codes = w.codes + (sliding ? (size_t)w.nwork * ATTN_MAXKT : 0);
   at.first = w.first + (sliding ? w.nwork : 0);
   at.qt = ATTN_QT;
-  if (!sliding && !p.train && w.nwork2 > 0) {  // global layer of an inference forward: 256-query items
+  if (!sliding && p.wide_global && w.nwork2 > 0) {  // global layer of the two-stream forward: 256-query items
     at.work = w.work2;
     at.nwork = w.nwork2;
     at.codes = w.codes2;
@@ -622,6 +625,7 @@ int forward_split(dn_ctx *c, int nseq, const int32_t *seq_len, const int32_t *d_
     ps[k].pos = d_pos + t0;
     ps[k].opt = d_opt ? d_opt + t0 : nullptr;
     ps[k].s = st[k];
+    ps[k].wide_global = true;
     rc = enqueue_prologue(c, ps[k], w.h, w.xn, nullptr, nullptr);
     if (rc) return rc;
   }
@@ -690,7 +694,6 @@ int forward_core(dn_ctx *c, int nseq, const int32_t *seq_len, const int32_t *d_i
   if (rc) return rc;
 
   Pass ps;
-  ps.train = train;
   ps.w = w;
   ps.ids = d_ids;
   ps.pos = d_pos;

@@ -181,12 +181,12 @@ hipError_t launch_gemm_splitk(int precision, const GemmArgs &a, int splits, floa
 bool gemm_shape_ok(int precision, int N, int K);
 
 // Attention work item: 32 * QT * ATTN_WAVES queries of one sequence (each
-// wave owns QT tiles of 32 queries), for every head. The kernel waits mostly
-// on its staged key tiles (one tile of prefetch), so more queries per staged
-// tile pays where a work item walks many tiles: global layers of an
-// inference forward take QT = 2 (256 queries, 2 waves per SIMD; cfg3 global
-// layers ~125 -> ~63 us), sliding-window layers and training QT = 1 (128
-// queries, 3 waves per SIMD; local layers with QT = 2: 86 -> 104 us).
+// wave owns QT tiles of 32 queries), for every head. QT = 1 (128 queries, 3
+// waves per SIMD) everywhere except the global layers of the two-stream
+// forward of a large batch, which take QT = 2 (256 queries, 2 waves per SIMD:
+// alone it is no faster, cfg3 125 -> 123 us and cfg4 317 -> 360 us per global
+// layer, but beside the other stream's kernels the whole forward gains, cfg3
+// +1%, cfg4 +2%). Local layers with QT = 2: 86 -> 104 us.
 constexpr int ATTN_WAVES = 4;
 constexpr int ATTN_QT = 1;
 constexpr int ATTN_QUERIES = 32 * ATTN_QT * ATTN_WAVES;
