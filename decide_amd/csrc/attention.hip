@@ -97,9 +97,11 @@ __device__ __forceinline__ void key_info_load(KeyInfo<T, R> &f, const int *kinfo
     const int key = (tid + NT * j) >> SH;
     f.pk[j] = kinfo[base + min(k0 + key, n - 1)];
   }
-  // Keys past the sequence end get option field 0xffff (option id -2, which
-  // neither the prefix (-1) nor any query's own option matches).
-  f.pi = (tid < KTILE && k0 + tid < n) ? kinfo[base + k0 + tid] : (int)0xffff0000u;
+  // Key k0 + (tid % 64)'s info, clamped to the last key; stage_load replaces
+  // it for keys past the end. No select here: a register write after this
+  // load would have to wait for every load still in flight to that register,
+  // and in the tile loop that wait also covered the tile just issued.
+  f.pi = kinfo[base + min(k0 + (tid & (KTILE - 1)), n - 1)];
 }
 
 // Loads one key tile (keys k0 .. k0+63) into registers; NT threads, R = 256/NT.
@@ -157,7 +159,9 @@ __device__ __forceinline__ void stage_load(Staging<T, R> &st, const T *qkv, int 
       st.valid |= (k0 + key < n ? 1u : 0u) << (8 + j);
     }
   }
-  st.info = ki.pi;
+  // Keys past the sequence end get option field 0xffff (option id -2, which
+  // neither the prefix (-1) nor any query's own option matches).
+  st.info = k0 + tid < n ? ki.pi : (int)0xffff0000u;
 }
 
 __device__ __forceinline__ float bf_lo(uint32_t w) { return __uint_as_float(w << 16); }
