@@ -493,6 +493,8 @@ def main() -> int:
                     help="forwards run with the per-launch probe after the timed ones (one stream)")
     ap.add_argument("--stream-split", type=int, default=8192, metavar="TOKENS",
                     help="dn_set_stream_split: batches of at least TOKENS run in two parts on two streams (0: off)")
+    ap.add_argument("--row-tail", type=int, default=2048, metavar="TOKENS",
+                    help="dn_set_row_tail: batches of at least TOKENS finish the last layer on the option rows (0: off)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="run one device copy of MIB MiB first (reference kernel for HBM counters)")
     ap.add_argument("--tokenizer", action="store_true",
@@ -547,6 +549,7 @@ def main() -> int:
         del src, dst
 
     eng.set_stream_split(args.stream_split)
+    eng.set_row_tail(args.row_tail)
     wl = Workload(eng, cfg, args.config, dev)
     log(f"workload {args.config}: {wl.nseq} sequences, T={wl.T}, R={wl.R}")
     log(f"warmup {args.warmup}")
@@ -648,6 +651,7 @@ def main() -> int:
         "per_launch_method": f"HIP events on the launch stream around layer {args.probe_layer}'s launches, "
                              f"{nprobe} forwards run after the timed ones on one stream",
         "stream_split_min_tokens": args.stream_split,
+        "row_tail_min_tokens": args.row_tail,
         "roofline": roof,
     }
     if attain:

@@ -361,9 +361,10 @@ hipError_t layer_gemm(const Config &g, int epi, const GemmArgs &a, hipStream_t s
 // same buffer unless training keeps them apart); x1 is the QKV input of layer
 // 0 (the embedding output; later layers normalise `in` into the workspace).
 // S (training) receives the layer's activations; ev brackets the five probed
-// launches.
+// launches. attn_only: stop after attention (enqueue_rows_tail finishes the
+// layer for the head's rows).
 int enqueue_layer(dn_ctx *c, const Pass &p, int l, float *in, float *h1, float *out, void *x1, LayerSave *S,
-                  hipEvent_t *ev) {
+                  hipEvent_t *ev, bool attn_only = false) {
   const Config &g = c->cfg;
   const int H = g.hidden, I = g.inter, prec = g.precision;
   const Workspace &w = p.w;
@@ -424,6 +425,7 @@ int enqueue_layer(dn_ctx *c, const Pass &p, int l, float *in, float *h1, float *
   at.scale = (float)(1.0 / std::sqrt((double)at.head_dim));  // forward.go:351
   PROBED(ev, DN_PROBE_ATTENTION, "attention",
          g.generic ? launch_attention_generic(prec, at, s) : launch_attention(prec, at, s));
+  if (attn_only) return DN_OK;
 
   GemmArgs o{};
   o.A = at.ctx;
@@ -482,8 +484,78 @@ int enqueue_layer(dn_ctx *c, const Pass &p, int l, float *in, float *h1, float *
   return DN_OK;
 }
 
+// Whether the last layer carries only the head's R rows past attention
+// (dn_set_row_tail): an inference forward of at least tail_min_tokens tokens
+// with at most a quarter of them head rows, unless the probe times the last
+// layer's launches. Everything after attention in a layer is row-wise, and
+// the head reads only its rows of the last layer's output.
+bool tail_on_rows(const dn_ctx *c, int T, int R, bool train) {
+  return !train && R > 0 && c->tail_min_tokens > 0 && T >= c->tail_min_tokens && 4LL * R <= T &&
+         c->probe_layer != c->cfg.layers - 1;
+}
+
+// Layer l after its attention, for the R rows row_tok (indices into the
+// T_total tokens) only: their attention output (ctx) and residual (h) rows
+// are gathered, then Wo + residual, mlp_norm, Wi + GeGLU and MlpWo +
+// residual run on R rows. The buffers are those the layer no longer reads
+// once its attention has run: h_r (fp32 [R x H]) and the mlp_norm output at
+// the start of qkv_buf, the gathered ctx rows in xn_buf, the GeGLU output in
+// act_buf. *h_out receives h_r, whose row r is token row_tok[r]'s output.
+int enqueue_rows_tail(dn_ctx *c, int l, const void *ctx, const float *h, int T_total, const int32_t *row_tok, int R,
+                      void *qkv_buf, void *xn_buf, void *act_buf, float **h_out, hipStream_t s) {
+  const Config &g = c->cfg;
+  const int H = g.hidden, I = g.inter, prec = g.precision;
+  const std::string pf = layer_prefix(l);
+  float *h_r = (float *)qkv_buf;
+  void *xn_r = (char *)qkv_buf + sizeof(float) * (size_t)R * H;
+  void *ctx_r = xn_buf, *act_r = act_buf;
+  HIPCHK(c, "gather_rows",
+         launch_gather_rows(prec, ctx, h, row_tok, R, T_total, H, ctx_r, h_r, (int *)c->err_flag.p, s));
+  GemmArgs o{};
+  o.A = ctx_r;
+  o.lda = H;
+  o.B = W(c, pf + "attn.Wo.weight");
+  o.ldb = H;
+  o.C = h_r;
+  o.ldc = H;
+  o.M = R;
+  o.N = H;
+  o.K = H;
+  o.n_store = H;
+  o.accumulate = 1;
+  HIPCHK(c, "gemm(Wo)", layer_gemm(g, EPI_F32, o, s));
+  HIPCHK(c, "ln(mlp_norm)", launch_ln(prec, h_r, R, H, (const float *)W(c, pf + "mlp_norm.weight"), g.eps, xn_r, s));
+  GemmArgs wi{};
+  wi.A = xn_r;
+  wi.lda = H;
+  wi.B = W(c, pf + "mlp.Wi.weight");
+  wi.ldb = H;
+  wi.C = act_r;
+  wi.ldc = I;
+  wi.M = R;
+  wi.N = 2 * I;
+  wi.K = H;
+  wi.n_store = 2 * I;
+  HIPCHK(c, "gemm(Wi)", layer_gemm(g, EPI_GEGLU, wi, s));
+  GemmArgs mo{};
+  mo.A = act_r;
+  mo.lda = I;
+  mo.B = W(c, pf + "mlp.Wo.weight");
+  mo.ldb = I;
+  mo.C = h_r;
+  mo.ldc = H;
+  mo.M = R;
+  mo.N = H;
+  mo.K = I;
+  mo.n_store = H;
+  mo.accumulate = 1;
+  HIPCHK(c, "gemm(MlpWo)", layer_gemm(g, EPI_F32, mo, s));
+  *h_out = h_r;
+  return DN_OK;
+}
+
 // The scorer head over the R option rows (row_tok: indices into the T_total
-// tokens of h).
+// tokens of h; null: rows 0 .. R-1 of h, T_total = R).
 int enqueue_head(dn_ctx *c, const float *h, int T_total, const int32_t *row_tok, int R, float *logits, float *s1,
                  float *d, hipStream_t s) {
   const Config &g = c->cfg;
@@ -629,13 +701,22 @@ int forward_split(dn_ctx *c, int nseq, const int32_t *seq_len, const int32_t *d_
     rc = enqueue_prologue(c, ps[k], w.h, w.xn, nullptr, nullptr);
     if (rc) return rc;
   }
+  const bool rows_tail = tail_on_rows(c, T_total, R, false);
   for (int l = 0; l < L; l++)
     for (int k = 0; k < 2; k++) {
-      rc = enqueue_layer(c, ps[k], l, ps[k].w.h, ps[k].w.h, ps[k].w.h, ps[k].w.xn, nullptr, nullptr);
+      rc = enqueue_layer(c, ps[k], l, ps[k].w.h, ps[k].w.h, ps[k].w.h, ps[k].w.xn, nullptr, nullptr,
+                         rows_tail && l == L - 1);
       if (rc) return rc;
     }
   HIPCHK(c, "hipEventRecord", hipEventRecord(c->ev_join, st[1]));
   HIPCHK(c, "hipStreamWaitEvent", hipStreamWaitEvent(st[0], c->ev_join, 0));
+  if (rows_tail) {  // the parts' buffers are views into the shared ones: row_tok indexes them directly
+    float *h_r = nullptr;
+    rc = enqueue_rows_tail(c, L - 1, c->ctxb.p, (const float *)c->h.p, T_total, d_row_tok, R, c->qkv.p, c->xn.p,
+                           c->act.p, &h_r, st[0]);
+    if (rc) return rc;
+    return enqueue_head(c, h_r, R, nullptr, R, d_logits, (float *)c->head_s1.p, (float *)c->head_d.p, st[0]);
+  }
   return enqueue_head(c, (const float *)c->h.p, T_total, d_row_tok, R, d_logits, (float *)c->head_s1.p,
                       (float *)c->head_d.p, st[0]);
 }
@@ -711,6 +792,7 @@ int forward_core(dn_ctx *c, int nseq, const int32_t *seq_len, const int32_t *d_i
                         train ? (float *)tr.emb_rstd.p : nullptr);
   if (rc) return rc;
   bool probed = false;
+  const bool rows_tail = tail_on_rows(c, T, R, train);
   for (int l = 0; l < L; l++) {
     hipEvent_t *ev = ws ? nullptr : probe_slot(c, l);  // the probe creates events: not in a caller's workspace
     probed |= ev != nullptr;
@@ -719,12 +801,19 @@ int forward_core(dn_ctx *c, int nseq, const int32_t *seq_len, const int32_t *d_i
     float *in = cur;                                              // this layer's input (S->hs when saved)
     float *h1 = S ? (float *)S->h1.p : in;                        // residual after attention
     float *out = saved(l + 1) ? (float *)saved(l + 1)->hs.p : h;  // the layer's output
-    rc = enqueue_layer(c, ps, l, in, h1, out, xn0, S, ev);
+    rc = enqueue_layer(c, ps, l, in, h1, out, xn0, S, ev, rows_tail && l == L - 1);
     if (rc) return rc;
     cur = out;
   }
   if (probed) c->probe_used++;
-  rc = enqueue_head(c, h, T, d_row_tok, R, d_logits, w.head_s1, w.head_d, ps.s);
+  if (rows_tail) {
+    float *h_r = nullptr;
+    rc = enqueue_rows_tail(c, L - 1, w.ctx, h, T, d_row_tok, R, w.qkv, w.xn, w.act, &h_r, ps.s);
+    if (rc) return rc;
+    rc = enqueue_head(c, h_r, R, nullptr, R, d_logits, w.head_s1, w.head_d, ps.s);
+  } else {
+    rc = enqueue_head(c, h, T, d_row_tok, R, d_logits, w.head_s1, w.head_d, ps.s);
+  }
   if (rc) return rc;
   if (train) {
     tr.have_forward = true;
@@ -1231,6 +1320,13 @@ int dn_set_stream_split(dn_ctx *c, int min_tokens) {
   if (!c || min_tokens < 0) return DN_INVALID_ARG;
   c->err.clear();
   c->split_min_tokens = min_tokens;
+  return DN_OK;
+}
+
+int dn_set_row_tail(dn_ctx *c, int min_tokens) {
+  if (!c || min_tokens < 0) return DN_INVALID_ARG;
+  c->err.clear();
+  c->tail_min_tokens = min_tokens;
   return DN_OK;
 }
 

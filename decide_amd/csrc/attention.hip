@@ -407,7 +407,6 @@ __global__ __launch_bounds__(64 * QW) __attribute__((amdgpu_waves_per_eu(QT == 1
   }
   const unsigned win2 = (unsigned)(2 * a.half_window);
   while (kt < nkt) {
-    const int k0 = kt * KTILE;
     const char *sKb = sK[b], *sVb = sV[b];
     const int *sKob = sKo[b], *sKwb = sKw[b];
     // This wave's classes: per query tile t and 32-key half i (uniform

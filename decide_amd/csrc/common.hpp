@@ -259,7 +259,7 @@ hipError_t launch_ln(int precision, const float *x, int rows, int H, const float
                      float *mean = nullptr, float *rstd = nullptr);
 struct HeadArgs {
   const float *h;
-  const int *row_tok;
+  const int *row_tok;  // the rows of h the head reads; null: rows 0 .. R-1
   int R, T, H;
   float eps;
   const float *final_norm, *in_w, *in_b, *dense_w, *dense_b, *norm_w, *norm_b, *out_w, *out_b;
@@ -271,6 +271,10 @@ struct HeadArgs {
 hipError_t launch_head(const HeadArgs &a, float *s1, float *d, hipStream_t s, bool generic = false);
 hipError_t launch_pack(const float *src, int trans, int rows, int cols, int ld, float *dst, int dst_rows,
                        int dst_cols, hipStream_t s);
+// ctx_r[r] = ctx[row_tok[r]] (operand type), h_r[r] = h[row_tok[r]] (fp32), H
+// columns, r < R; an index outside [0, T) sets bit 2 of *err_flag.
+hipError_t launch_gather_rows(int precision, const void *ctx, const float *h, const int *row_tok, int R, int T,
+                              int H, void *ctx_r, float *h_r, int *err_flag, hipStream_t s);
 
 // Training kernels (backward.hip). Precision codes: 0 fp32, 1 bf16.
 hipError_t launch_transpose(int precision_in, int precision_out, const void *src, int rows, int cols, int lds,

@@ -161,6 +161,7 @@ struct dn_ctx {
   hipStream_t aux_stream = nullptr;
   hipEvent_t ev_fork = nullptr, ev_join = nullptr;
   int split_min_tokens = 8192;  // batches from this many tokens (and >= 2 sequences) are split
+  int tail_min_tokens = 2048;   // from this many tokens the last layer's tail runs on the head's rows
   // batch layout cache
   std::vector<int> lay_len;
   HostLayout hlay;

@@ -169,7 +169,7 @@ __global__ __launch_bounds__(256) void head_pre_kernel(HeadArgs a, float *s1) {
   const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (r >= a.R) return;
   const int dim = a.H, nvec = dim / 4;
-  int t = a.row_tok[r];
+  int t = a.row_tok ? a.row_tok[r] : r;
   if (t < 0 || t >= a.T) {
     if (lane == 0) atomicOr(a.err_flag, 2);
     t = 0;
@@ -244,6 +244,31 @@ __global__ __launch_bounds__(256) void head_post_kernel(HeadArgs a, const float 
   if (lane == 0) a.logits[r] = dot + a.out_b[0];
 }
 
+// Rows row_tok[r] of the attention output ctx (operand type) and of the
+// residual stream h (fp32) copied to row r of ctx_r / h_r: the inputs of the
+// last layer's row-wise tail when only the head's rows are carried past
+// attention. One wave per row; a row index outside [0, T) raises error flag 2
+// (as head_pre does) and copies row 0.
+template <class T>
+__global__ __launch_bounds__(256) void gather_rows_kernel(const T *ctx, const float *h, const int *row_tok, int R,
+                                                          int Tn, int H, T *ctx_r, float *h_r, int *err_flag) {
+  const int lane = threadIdx.x & 63;
+  const int r = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= R) return;
+  int t = row_tok[r];
+  if (t < 0 || t >= Tn) {
+    if (lane == 0) atomicOr(err_flag, 2);
+    t = 0;
+  }
+  const float4 *hs = (const float4 *)(h + (size_t)t * H);
+  float4 *hd = (float4 *)(h_r + (size_t)r * H);
+  for (int j = lane; j < H / 4; j += 64) hd[j] = hs[j];
+  // 16-byte chunks of the operand row (H * sizeof(T) is a multiple of 16)
+  const uint4 *cs = (const uint4 *)(ctx + (size_t)t * H);
+  uint4 *cd = (uint4 *)(ctx_r + (size_t)r * H);
+  for (int j = lane; j < (int)(H * sizeof(T) / 16); j += 64) cd[j] = cs[j];
+}
+
 // dst[dst_rows x dst_cols] (row-major, zero padded) = op(src) where op(src)
 // is rows x cols; src is row-major with leading dimension ld, stored
 // transposed (cols x rows) when trans is set.
@@ -315,6 +340,20 @@ hipError_t launch_head(const HeadArgs &a, float *s1, float *d, hipStream_t s, bo
   e = generic ? launch_gemm_generic(0, EPI_F32, g, s) : launch_gemm(0, EPI_F32, g, s);
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(head_post_kernel, grid, block, 0, s, a, d);
+  return hipGetLastError();
+}
+
+hipError_t launch_gather_rows(int precision, const void *ctx, const float *h, const int *row_tok, int R, int T,
+                              int H, void *ctx_r, float *h_r, int *err_flag, hipStream_t s) {
+  if (R <= 0) return hipSuccess;
+  if (H % 8 != 0) return hipErrorInvalidValue;
+  const dim3 grid((R + 3) / 4), block(256);
+  if (precision == 1)
+    hipLaunchKernelGGL(gather_rows_kernel<bf16>, grid, block, 0, s, (const bf16 *)ctx, h, row_tok, R, T, H,
+                       (bf16 *)ctx_r, h_r, err_flag);
+  else
+    hipLaunchKernelGGL(gather_rows_kernel<float>, grid, block, 0, s, (const float *)ctx, h, row_tok, R, T, H,
+                       (float *)ctx_r, h_r, err_flag);
   return hipGetLastError();
 }
 

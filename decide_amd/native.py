@@ -68,6 +68,7 @@ _SIGS = {
     "dn_gemm_device": ([_vp, _i, _i, _i, _i, _vp, _vp, _vp, _i], _i),
     "dn_synchronize": ([_vp], _i),
     "dn_set_stream_split": ([_vp, _i], _i),
+    "dn_set_row_tail": ([_vp, _i], _i),
     "dn_set_probe": ([_vp, _i], _i),
     "dn_read_probe": ([_vp, _f64p, _c.POINTER(_i)], _i),
     "dn_read_probe_backward": ([_vp, _f64p, _c.POINTER(_i)], _i),

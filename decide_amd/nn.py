@@ -267,6 +267,11 @@ class Engine:
         """dn_set_stream_split: batches of >= min_tokens tokens run in two parts on two streams (0: off)."""
         check(lib.dn_set_stream_split(self._h, int(min_tokens)), self._h)
 
+    def set_row_tail(self, min_tokens: int) -> None:
+        """dn_set_row_tail: batches of >= min_tokens tokens (option rows at most a
+        quarter of them) finish the last layer on the option rows only (0: off)."""
+        check(lib.dn_set_row_tail(self._h, int(min_tokens)), self._h)
+
     def mfma_calibrate(self, mode: int = 0) -> float:
         """dn_mfma_calibrate: attainable bf16 MFMA TFLOP/s (mode 0 changing operands, 1 constant)."""
         out = ctypes.c_double(0.0)

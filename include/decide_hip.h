@@ -179,6 +179,18 @@ int dn_gemm_device(dn_ctx *ctx, int precision, int M, int N, int K, const void *
  * run on one stream. No counterpart in the reference. */
 int dn_set_stream_split(dn_ctx *ctx, int min_tokens);
 
+/* Inference forwards (dn_forward, dn_forward_device, dn_evaluate) of batches
+ * with at least min_tokens tokens, at most a quarter of them option rows, run
+ * the last encoder layer past its attention on the option rows only: their
+ * attention output and residual rows are gathered, and Wo, mlp_norm, Wi and
+ * MlpWo run on R rows instead of T. Every step after attention is row-wise and
+ * the scorer head reads only those rows, so the logits are those of the full
+ * layer up to the summation order of the smaller GEMMs' kernels. 0 turns it
+ * off; the default is 2048. While the kernel probe times the last layer
+ * (dn_set_probe) forwards run the full layer. No counterpart in the reference
+ * (forward.go:212-243 runs every layer over all tokens, then gathers). */
+int dn_set_row_tail(dn_ctx *ctx, int min_tokens);
+
 /* Waits for the context's stream. */
 int dn_synchronize(dn_ctx *ctx);
 

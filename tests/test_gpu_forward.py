@@ -455,3 +455,84 @@ def test_stream_split_matches_single_stream(base, engines):
             eng.check_device_errors()
             assert np.array_equal(out.cpu().numpy(), one)
         eng.set_stream_split(8192)
+
+
+def test_row_tail_matches_full_last_layer(base, engines):
+    """dn_set_row_tail: finishing the last layer on the option rows only (their
+    attention output and residual rows gathered; Wo, mlp_norm, Wi and MlpWo
+    on R rows) gives the logits of the full layer, whose other rows the head
+    never reads: the cfg3 batch on one and two streams, the cfg4 batch and a
+    ragged batch; through dn_forward and dn_forward_device. The smaller GEMMs
+    may sum in another order (fp32: the small-M kernel), so the bar is the
+    fp32 rounding bar (|d| <= 1e-5 * (1 + |logit|)) in fp32 and the bf16 bar
+    in bf16; the figures are printed."""
+    import torch
+
+    from decide_amd.nn import build_sequence, flatten, row_tokens
+    from decide_amd.synth import config_batch, pack_request
+
+    cfg = base[0]
+    rng = np.random.default_rng(78)
+    ragged = [build_sequence(pack_request(rng, int(p), [int(k)] * int(m), cfg.vocab), 50284, True)
+              for p, k, m in zip(rng.integers(200, 900, 7), rng.integers(3, 20, 7), rng.integers(1, 9, 7))]
+    for p in ("bf16", "fp32"):
+        eng = engines[p]
+        for name, batch, split in (("cfg3", config_batch("cfg3", vocab=cfg.vocab), 1),
+                                   ("cfg3", config_batch("cfg3", vocab=cfg.vocab), 0),
+                                   ("cfg4", config_batch("cfg4", vocab=cfg.vocab), 8192), ("ragged", ragged, 0)):
+            assert sum(len(s.ids) for s in batch) >= 2048
+            eng.set_stream_split(split)
+            eng.set_row_tail(0)
+            full = eng.forward(batch)
+            eng.set_row_tail(2048)
+            tail = eng.forward(batch)
+            d = np.abs(tail.astype(np.float64) - full)
+            print(f"row tail {p} {name} split {split}: {len(tail)} rows, bit-identical {np.array_equal(tail, full)}, "
+                  f"max |dlogit| {float(d.max()):.3g}", flush=True)
+            if p == "fp32":
+                assert np.all(d <= 1e-5 * (1 + np.abs(full)))
+            else:
+                compare(tail, full.astype(np.float64), batch, p)
+            seq_len, ids, pos, opt, nmask, _ = flatten(batch)
+            dv = {k: torch.from_numpy(v).cuda() for k, v in dict(ids=ids, pos=pos, opt=opt,
+                                                                  rt=row_tokens(batch)).items()}
+            out = torch.zeros(len(tail), dtype=torch.float32, device="cuda")
+            torch.cuda.synchronize()
+            eng.forward_device(seq_len, dv["ids"].data_ptr(), dv["pos"].data_ptr(), dv["opt"].data_ptr(), len(tail),
+                               dv["rt"].data_ptr(), out.data_ptr())
+            eng.check_device_errors()
+            assert np.array_equal(out.cpu().numpy(), tail)
+        eng.set_stream_split(8192)
+
+
+def test_row_tail_flags_bad_row_index(base, engines):
+    """With the last layer finished on the option rows, dn_forward_device's
+    row indices are checked by the row gather: one outside [0, T) is reported
+    by dn_check_device_errors as forward.go's mask-position error, and the
+    context stays usable."""
+    import torch
+
+    from decide_amd import InvalidArgument
+    from decide_amd.nn import flatten, row_tokens
+    from decide_amd.synth import config_batch
+
+    eng = engines["bf16"]
+    batch = config_batch("cfg4", vocab=base[0].vocab, nseq=1)
+    want = eng.forward(batch)
+    seq_len, ids, pos, opt, nmask, _ = flatten(batch)
+    good = row_tokens(batch)
+    bad = good.copy()
+    bad[3] = len(ids)
+    for rt in (bad, good):
+        dv = {k: torch.from_numpy(v).cuda() for k, v in dict(ids=ids, pos=pos, opt=opt, rt=rt).items()}
+        out = torch.zeros(len(want), dtype=torch.float32, device="cuda")
+        torch.cuda.synchronize()
+        eng.forward_device(seq_len, dv["ids"].data_ptr(), dv["pos"].data_ptr(), dv["opt"].data_ptr(), len(want),
+                           dv["rt"].data_ptr(), out.data_ptr())
+        if rt is bad:
+            with pytest.raises(InvalidArgument) as ei:
+                eng.check_device_errors()
+            assert ei.value.message == "nn: mask position out of range"
+        else:
+            eng.check_device_errors()
+            assert np.array_equal(out.cpu().numpy(), want)
