@@ -554,6 +554,138 @@ int enqueue_rows_tail(dn_ctx *c, int l, const void *ctx, const float *h, int T_t
   return DN_OK;
 }
 
+// Whether the last layer of a row-tail forward also runs its attention and
+// its Q projection on the option rows (enqueue_rows_layer): the MFMA
+// geometry, at most ROW_ITEMS_MAXSEQ sequences, and room for the row buffers
+// in the buffers that layer leaves free (h_r in ctx; the gathered QKV input,
+// Q and attention rows in act; the GeGLU rows in xn).
+bool rows_layer_fits(const dn_ctx *c, int T, int R, int nseq) {
+  const Config &g = c->cfg;
+  if (g.generic || nseq > ROW_ITEMS_MAXSEQ) return false;
+  const size_t es = g.precision == DN_PRECISION_BF16 ? 2 : 4, H = g.hidden, I = g.inter, t = T, r = R;
+  return 4 * r * H <= es * t * H && 3 * es * r * H <= es * t * I && es * r * I <= es * t * H;
+}
+
+// Layer l (the last) for the R option rows row_tok only, over the batch
+// layout and buffers of w: attn_norm of every token (l > 0; x1 is layer 0's
+// input otherwise), K and V of every token (rows H..3H of Wqkv into qkv's k
+// and v columns), the rows' QKV input and residual gathered, their Q, the
+// option-row attention (launch_row_items groups the rows by sequence), then
+// Wo + residual, mlp_norm, Wi + GeGLU and MlpWo + residual on R rows. Every
+// row's result is what the full layer gives that token: attention rows are
+// independent queries over the same keys, and the rest is row-wise.
+// *h_out receives h_r (row r: token row_tok[r]).
+int enqueue_rows_layer(dn_ctx *c, const Workspace &w, int l, const float *h, const void *x1,
+                       const int32_t *row_tok, int R, float **h_out, hipStream_t s) {
+  const Config &g = c->cfg;
+  const int H = g.hidden, I = g.inter, prec = g.precision, T = w.T;
+  const size_t es = prec == DN_PRECISION_BF16 ? 2 : 4;
+  const std::string pf = layer_prefix(l);
+  if (l > 0) {
+    HIPCHK(c, "ln(attn_norm)", launch_ln(prec, h, T, H, (const float *)W(c, pf + "attn_norm.weight"), g.eps, w.xn, s));
+    x1 = w.xn;
+  }
+  float *h_r = (float *)w.ctx;
+  char *A = (char *)w.act;
+  void *xn_r = A, *q_r = A + es * R * H, *ctx_r = A + 2 * es * R * H, *act_r = w.xn;
+  HIPCHK(c, "gather_rows", launch_gather_rows(prec, x1, h, row_tok, R, T, H, xn_r, h_r, (int *)c->err_flag.p, s));
+  const char *wqkv = (const char *)W(c, pf + "attn.Wqkv.weight");
+  GemmArgs kv{};
+  kv.A = x1;
+  kv.lda = H;
+  kv.B = wqkv + es * H * H;
+  kv.ldb = H;
+  kv.C = (char *)w.qkv + es * H;
+  kv.ldc = 3 * H;
+  kv.M = T;
+  kv.N = 2 * H;
+  kv.K = H;
+  kv.n_store = 2 * H;
+  HIPCHK(c, "gemm(Wqkv k, v)", layer_gemm(g, EPI_STORE, kv, s));
+  GemmArgs q{};
+  q.A = xn_r;
+  q.lda = H;
+  q.B = wqkv;
+  q.ldb = H;
+  q.C = q_r;
+  q.ldc = H;
+  q.M = R;
+  q.N = H;
+  q.K = H;
+  q.n_store = H;
+  HIPCHK(c, "gemm(Wqkv q)", layer_gemm(g, EPI_STORE, q, s));
+  // Work items in head_s1 (free until the head): items, then slots, then the count.
+  const int nit = w.nseq + (R + ATTN_QUERIES - 1) / ATTN_QUERIES;
+  int4 *items = (int4 *)w.head_s1;
+  int *rows = (int *)(items + nit), *nitems = rows + R;
+  HIPCHK(c, "row_items", launch_row_items(row_tok, R, w.seq_off, w.nseq, T, items, rows, nitems, s));
+  const bool sliding = g.sliding[l] != 0;
+  const float *rope = (const float *)c->rope.p;
+  const size_t tab = (size_t)kPositions * 32;
+  AttnArgs at{};
+  at.qkv = w.qkv;
+  at.ctx = ctx_r;
+  at.kinfo = w.kinfo;
+  at.cos_t = rope + (sliding ? 2 : 0) * tab;
+  at.sin_t = rope + (sliding ? 3 : 1) * tab;
+  at.seq_off = w.seq_off;
+  at.seq_len = w.seq_len;
+  at.nwork = nit;
+  at.H = H;
+  at.heads = g.heads;
+  at.sliding = sliding ? 1 : 0;
+  at.half_window = g.half_window;
+  at.scale_log2 = (float)(1.0 / std::sqrt(64.0)) * 1.44269504088896340736f;
+  at.qt = ATTN_QT;
+  at.items = items;
+  at.nitems = nitems;
+  at.rows = rows;
+  at.row_tok = row_tok;
+  at.q_rows = q_r;
+  HIPCHK(c, "attention(rows)", launch_attention_rows(prec, at, s));
+  GemmArgs o{};
+  o.A = ctx_r;
+  o.lda = H;
+  o.B = W(c, pf + "attn.Wo.weight");
+  o.ldb = H;
+  o.C = h_r;
+  o.ldc = H;
+  o.M = R;
+  o.N = H;
+  o.K = H;
+  o.n_store = H;
+  o.accumulate = 1;
+  HIPCHK(c, "gemm(Wo)", layer_gemm(g, EPI_F32, o, s));
+  HIPCHK(c, "ln(mlp_norm)", launch_ln(prec, h_r, R, H, (const float *)W(c, pf + "mlp_norm.weight"), g.eps, xn_r, s));
+  GemmArgs wi{};
+  wi.A = xn_r;
+  wi.lda = H;
+  wi.B = W(c, pf + "mlp.Wi.weight");
+  wi.ldb = H;
+  wi.C = act_r;
+  wi.ldc = I;
+  wi.M = R;
+  wi.N = 2 * I;
+  wi.K = H;
+  wi.n_store = 2 * I;
+  HIPCHK(c, "gemm(Wi)", layer_gemm(g, EPI_GEGLU, wi, s));
+  GemmArgs mo{};
+  mo.A = act_r;
+  mo.lda = I;
+  mo.B = W(c, pf + "mlp.Wo.weight");
+  mo.ldb = I;
+  mo.C = h_r;
+  mo.ldc = H;
+  mo.M = R;
+  mo.N = H;
+  mo.K = I;
+  mo.n_store = H;
+  mo.accumulate = 1;
+  HIPCHK(c, "gemm(MlpWo)", layer_gemm(g, EPI_F32, mo, s));
+  *h_out = h_r;
+  return DN_OK;
+}
+
 // The scorer head over the R option rows (row_tok: indices into the T_total
 // tokens of h; null: rows 0 .. R-1 of h, T_total = R).
 int enqueue_head(dn_ctx *c, const float *h, int T_total, const int32_t *row_tok, int R, float *logits, float *s1,
@@ -649,7 +781,7 @@ constexpr int kMinPartTokens = 1025;
 
 int forward_split(dn_ctx *c, int nseq, const int32_t *seq_len, const int32_t *d_ids, const int32_t *d_pos,
                   const int32_t *d_opt, int R, const int32_t *d_row_tok, float *d_logits, int T_total, int cut,
-                  int acc) {
+                  int acc, const Workspace *wfull) {
   const Config &g = c->cfg;
   const int H = g.hidden, I = g.inter, L = g.layers;
   const size_t es = g.precision == DN_PRECISION_BF16 ? 2 : 4;
@@ -702,7 +834,8 @@ int forward_split(dn_ctx *c, int nseq, const int32_t *seq_len, const int32_t *d_
     if (rc) return rc;
   }
   const bool rows_tail = tail_on_rows(c, T_total, R, false);
-  for (int l = 0; l < L; l++)
+  const bool rows_layer = rows_tail && rows_layer_fits(c, T_total, R, nseq);
+  for (int l = 0; l < (rows_layer ? L - 1 : L); l++)
     for (int k = 0; k < 2; k++) {
       rc = enqueue_layer(c, ps[k], l, ps[k].w.h, ps[k].w.h, ps[k].w.h, ps[k].w.xn, nullptr, nullptr,
                          rows_tail && l == L - 1);
@@ -710,6 +843,13 @@ int forward_split(dn_ctx *c, int nseq, const int32_t *seq_len, const int32_t *d_
     }
   HIPCHK(c, "hipEventRecord", hipEventRecord(c->ev_join, st[1]));
   HIPCHK(c, "hipStreamWaitEvent", hipStreamWaitEvent(st[0], c->ev_join, 0));
+  if (rows_layer) {  // the last layer over the whole batch: its layout from ctx_workspace (taken before the fork)
+    float *h_r = nullptr;
+    rc = enqueue_rows_layer(c, *wfull, L - 1, (const float *)c->h.p, L == 1 ? c->xn.p : nullptr, d_row_tok, R, &h_r,
+                            st[0]);
+    if (rc) return rc;
+    return enqueue_head(c, h_r, R, nullptr, R, d_logits, (float *)c->head_s1.p, (float *)c->head_d.p, st[0]);
+  }
   if (rows_tail) {  // the parts' buffers are views into the shared ones: row_tok indexes them directly
     float *h_r = nullptr;
     rc = enqueue_rows_tail(c, L - 1, c->ctxb.p, (const float *)c->h.p, T_total, d_row_tok, R, c->qkv.p, c->xn.p,
@@ -735,9 +875,18 @@ int forward_core(dn_ctx *c, int nseq, const int32_t *seq_len, const int32_t *d_i
     if (T_total >= c->split_min_tokens) {
       int first = 0;
       const int cut = split_point(nseq, seq_len, (int)T_total, &first);
-      if (first >= kMinPartTokens && T_total - first >= kMinPartTokens)
+      if (first >= kMinPartTokens && T_total - first >= kMinPartTokens) {
+        // The option-row last layer runs over the whole batch: its layout comes
+        // from the context's workspace (uploaded here, before the fork, when it
+        // changes).
+        Workspace wf;
+        if (tail_on_rows(c, (int)T_total, R, false) && rows_layer_fits(c, (int)T_total, R, nseq)) {
+          const int rc = ctx_workspace(c, nseq, seq_len, R, &wf);
+          if (rc) return rc;
+        }
         return forward_split(c, nseq, seq_len, d_ids, d_pos, d_opt, R, d_row_tok, d_logits, (int)T_total, cut,
-                             first);
+                             first, &wf);
+      }
     }
   }
   Workspace w;
@@ -793,7 +942,8 @@ int forward_core(dn_ctx *c, int nseq, const int32_t *seq_len, const int32_t *d_i
   if (rc) return rc;
   bool probed = false;
   const bool rows_tail = tail_on_rows(c, T, R, train);
-  for (int l = 0; l < L; l++) {
+  const bool rows_layer = rows_tail && rows_layer_fits(c, T, R, w.nseq);
+  for (int l = 0; l < (rows_layer ? L - 1 : L); l++) {
     hipEvent_t *ev = ws ? nullptr : probe_slot(c, l);  // the probe creates events: not in a caller's workspace
     probed |= ev != nullptr;
     // Training keeps this layer's activations (layers >= train_from).
@@ -806,7 +956,12 @@ int forward_core(dn_ctx *c, int nseq, const int32_t *seq_len, const int32_t *d_i
     cur = out;
   }
   if (probed) c->probe_used++;
-  if (rows_tail) {
+  if (rows_layer) {
+    float *h_r = nullptr;
+    rc = enqueue_rows_layer(c, w, L - 1, cur, L == 1 ? xn0 : nullptr, d_row_tok, R, &h_r, ps.s);
+    if (rc) return rc;
+    rc = enqueue_head(c, h_r, R, nullptr, R, d_logits, w.head_s1, w.head_d, ps.s);
+  } else if (rows_tail) {
     float *h_r = nullptr;
     rc = enqueue_rows_tail(c, L - 1, w.ctx, h, T, d_row_tok, R, w.qkv, w.xn, w.act, &h_r, ps.s);
     if (rc) return rc;

@@ -263,7 +263,10 @@ __device__ __forceinline__ void stage_store(const Staging<T, R> &st, char *sK, c
 }
 
 // LOCAL: a sliding-window layer (the window test is compiled in).
-template <class T, int QW, int QT, bool LOCAL>
+// LIST: the queries are the option rows of a.items (row_items_kernel): Q
+// read from a.q_rows and the output written at row r, every key tile tested
+// per element.
+template <class T, int QW, int QT, bool LOCAL, bool LIST = false>
 __global__ __launch_bounds__(64 * QW) __attribute__((amdgpu_waves_per_eu(QT == 1 ? 3 : 2))) void attention_kernel(
     AttnArgs a) {
   // R staging items per thread; with more than 4 waves only the first 256
@@ -300,8 +303,16 @@ __global__ __launch_bounds__(64 * QW) __attribute__((amdgpu_waves_per_eu(QT == 1
   const int bid = blockIdx.x;
   int logical = bid;
   if (total % 8 == 0) logical = (bid % 8) * (total / 8) + bid / 8;
-  const int4 wk = a.work[logical / a.heads];
-  const int s = wk.x, q0 = wk.y, head = logical % a.heads;
+  const int wi = logical / a.heads, head = logical % a.heads;
+  int s, q0 = 0, slot0 = 0, cnt = 0;
+  if constexpr (LIST) {
+    if (wi >= *a.nitems) return;  // the grid is sized by an upper bound on the items
+    const int4 it = a.items[wi];
+    s = it.x, slot0 = it.y, cnt = it.z;
+  } else {
+    const int4 wk = a.work[wi];
+    s = wk.x, q0 = wk.y;
+  }
   const int n = a.seq_len[s], base = a.seq_off[s];
   const int H = a.H, ld = 3 * H;
   const T *qkv = (const T *)a.qkv;
@@ -310,10 +321,20 @@ __global__ __launch_bounds__(64 * QW) __attribute__((amdgpu_waves_per_eu(QT == 1
   // This work item's tile classes (computed once per forward and layer type
   // by tile_codes_kernel) and its first needed tile: the first tile's loads
   // are issued before the classes reach LDS.
-  const int wi = logical / a.heads;
-  const uint32_t *codes = a.codes + (size_t)wi * ATTN_MAXKT;
-  for (int kt = tid; kt < nkt; kt += NT) sCode[kt] = codes[kt];
-  int kt = a.first[wi];
+  int kt;
+  if constexpr (LIST) {
+    // Class 2 (per element) for both halves of every tile, for the waves
+    // that hold rows.
+    uint32_t all = 0;
+    for (int w = 0; w < QW * QT; w++)
+      if (32 * w < cnt) all |= 0xAu << (4 * w);
+    for (int k = tid; k < nkt; k += NT) sCode[k] = all;
+    kt = 0;
+  } else {
+    const uint32_t *codes = a.codes + (size_t)wi * ATTN_MAXKT;
+    for (int k = tid; k < nkt; k += NT) sCode[k] = codes[k];
+    kt = a.first[wi];
+  }
   Staging<T, R> st;
   KeyInfo<T, R> ki;
   const bool stager = tid < 256;
@@ -326,17 +347,29 @@ __global__ __launch_bounds__(64 * QW) __attribute__((amdgpu_waves_per_eu(QT == 1
   // rotated Q^T operands (B operand: column = query, k = head dim).
   constexpr int NKS = D / MF::KSTEP;
   frag qf[QT][NKS];
-  int qopt[QT], qpos[QT];
+  int qopt[QT], qpos[QT], qrow_r[QT];
   bool qvalid[QT];
 #pragma unroll
   for (int t = 0; t < QT; t++) {
-    const int q = q0 + (wave * QT + t) * 32 + lr;
-    qvalid[t] = q < n;
-    const int qq = qvalid[t] ? q : n - 1;
+    int qq;
+    const T *qrow;
+    if constexpr (LIST) {
+      const int idx = (wave * QT + t) * 32 + lr;
+      qvalid[t] = idx < cnt;
+      const int r = a.rows[slot0 + (qvalid[t] ? idx : 0)];
+      qrow_r[t] = r;
+      // a row token outside the sequence (flagged by the row gather) reads an in-bounds query
+      qq = min(max(a.row_tok[r] - base, 0), n - 1);
+      qrow = (const T *)a.q_rows + (size_t)r * H + head * D;
+    } else {
+      const int q = q0 + (wave * QT + t) * 32 + lr;
+      qvalid[t] = q < n;
+      qq = qvalid[t] ? q : n - 1;
+      qrow = qkv + (size_t)(base + qq) * ld + head * D;
+    }
     const int qinfo = a.kinfo[base + qq];
     qopt[t] = (qinfo >> 16) - 1;
     qpos[t] = qinfo & 0xffff;
-    const T *qrow = qkv + (size_t)(base + qq) * ld + head * D;
     const float *cq = a.cos_t + (size_t)qpos[t] * 32, *sq = a.sin_t + (size_t)qpos[t] * 32;
 #pragma unroll
     for (int ks = 0; ks < NKS; ks++) qf[t][ks] = *(const frag *)(qrow + ks * MF::KSTEP + lh * MF::SLOTS);
@@ -568,13 +601,13 @@ __global__ __launch_bounds__(64 * QW) __attribute__((amdgpu_waves_per_eu(QT == 1
   for (int t = 0; t < QT; t++) {
     const float l_tot = l_run[t] + __shfl_xor(l_run[t], 32);
     const float inv = 1.0f / l_tot;
-    if (a.lse && qvalid[t] && lh == 0) {
+    if (!LIST && a.lse && qvalid[t] && lh == 0) {
       const int q = q0 + (wave * QT + t) * 32 + lr;
       a.lse[(size_t)(base + q) * a.heads + head] = m_run[t] * a.scale_log2 + log2f(l_tot);
     }
     if (qvalid[t]) {
       const int q = q0 + (wave * QT + t) * 32 + lr;
-      T *out = (T *)a.ctx + (size_t)(base + q) * H + head * D;
+      T *out = (T *)a.ctx + (size_t)(LIST ? qrow_r[t] : base + q) * H + head * D;
 #pragma unroll
       for (int i = 0; i < 2; i++)
 #pragma unroll
@@ -590,6 +623,73 @@ __global__ __launch_bounds__(64 * QW) __attribute__((amdgpu_waves_per_eu(QT == 1
           }
         }
     }
+  }
+}
+
+// Work items of the option-row attention (attention_kernel<..., LIST>): the
+// rows r < R (row_tok[r] a token of the batch) grouped by sequence, each
+// sequence's rows in chunks of up to ATTN_QUERIES, item = (sequence, first
+// slot in rows[], row count). One workgroup of 1024 threads, thread j owning
+// sequence j (nseq <= ROW_ITEMS_MAXSEQ):
+//   1. every row's sequence (binary search of seq_off), counted per sequence;
+//   2. exclusive scans of the counts (first slot) and of the chunk counts
+//      (first item);
+//   3. every row placed in a slot of its sequence (in atomic order: a row's
+//      result does not depend on its slot) and the items written.
+// A row token outside [0, T) counts as sequence 0 (the row gather flags it).
+__device__ __forceinline__ int block_excl_scan(int v, int *wsum) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  int x = v;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(x, o);
+    if (lane >= o) x += y;
+  }
+  if (lane == 63) wsum[wave] = x;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int acc = 0;
+    for (int w = 0; w < 16; w++) {
+      const int t = wsum[w];
+      wsum[w] = acc;
+      acc += t;
+    }
+    wsum[16] = acc;
+  }
+  __syncthreads();
+  return x - v + wsum[wave];
+}
+
+__global__ __launch_bounds__(1024) void row_items_kernel(const int *row_tok, int R, const int *seq_off, int nseq,
+                                                         int T, int4 *items, int *rows, int *nitems) {
+  __shared__ int cnt[ROW_ITEMS_MAXSEQ], fill[ROW_ITEMS_MAXSEQ], wsum[17];
+  const int j = threadIdx.x;
+  cnt[j] = 0;
+  fill[j] = 0;
+  __syncthreads();
+  auto seq_of = [&](int r) {
+    const int t = row_tok[r];
+    if (t < 0 || t >= T) return 0;
+    int lo = 0, hi = nseq - 1;  // last sequence whose offset is <= t
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (seq_off[mid] <= t) lo = mid;
+      else hi = mid - 1;
+    }
+    return lo;
+  };
+  for (int r = j; r < R; r += 1024) atomicAdd(&cnt[seq_of(r)], 1);
+  __syncthreads();
+  const int c = j < nseq ? cnt[j] : 0, nch = (c + ATTN_QUERIES - 1) / ATTN_QUERIES;
+  const int slot0 = block_excl_scan(c, wsum);
+  const int item0 = block_excl_scan(nch, wsum);
+  if (j == 0) *nitems = wsum[16];
+  for (int k = 0; k < nch; k++) items[item0 + k] = make_int4(j, slot0 + k * ATTN_QUERIES, min(ATTN_QUERIES, c - k * ATTN_QUERIES), 0);
+  cnt[j] = slot0;  // reused: first slot of sequence j
+  __syncthreads();
+  for (int r = j; r < R; r += 1024) {
+    const int sq = seq_of(r);
+    rows[cnt[sq] + atomicAdd(&fill[sq], 1)] = r;
   }
 }
 
@@ -1324,6 +1424,31 @@ hipError_t launch_attention(int precision, const AttnArgs &a, hipStream_t s) {
     else
       hipLaunchKernelGGL((attention_kernel<float, ATTN_WAVES, ATTN_QT, false>), grid, block, 0, s, a);
   }
+  return hipGetLastError();
+}
+
+hipError_t launch_attention_rows(int precision, const AttnArgs &a, hipStream_t s) {
+  if (a.nwork <= 0) return hipSuccess;
+  if (a.qt != ATTN_QT) return hipErrorInvalidValue;
+  dim3 grid(a.nwork * a.heads), block(64 * ATTN_WAVES);
+  if (precision == 1) {
+    if (a.sliding)
+      hipLaunchKernelGGL((attention_kernel<bf16, ATTN_WAVES, ATTN_QT, true, true>), grid, block, 0, s, a);
+    else
+      hipLaunchKernelGGL((attention_kernel<bf16, ATTN_WAVES, ATTN_QT, false, true>), grid, block, 0, s, a);
+  } else {
+    if (a.sliding)
+      hipLaunchKernelGGL((attention_kernel<float, ATTN_WAVES, ATTN_QT, true, true>), grid, block, 0, s, a);
+    else
+      hipLaunchKernelGGL((attention_kernel<float, ATTN_WAVES, ATTN_QT, false, true>), grid, block, 0, s, a);
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_row_items(const int *row_tok, int R, const int *seq_off, int nseq, int T, int4 *items, int *rows,
+                            int *nitems, hipStream_t s) {
+  if (nseq <= 0 || nseq > ROW_ITEMS_MAXSEQ || R <= 0) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(row_items_kernel, dim3(1), dim3(1024), 0, s, row_tok, R, seq_off, nseq, T, items, rows, nitems);
   return hipGetLastError();
 }
 

@@ -211,8 +211,24 @@ struct AttnArgs {
   int qt;                       // query tiles per wave of the work items (ATTN_QT or ATTN_QT_GLOBAL)
   int nseq, max_len, head_dim;  // the any-geometry kernel: sequences, longest one, head width,
   float scale;                  // and the softmax scale float32(1 / sqrt(head_dim))
+  // Option-row attention (launch_attention_rows): work items and slots from
+  // launch_row_items (nwork: an upper bound on the items, nseq + ceil(R /
+  // ATTN_QUERIES)); Q of row r at q_rows + r * H (rotated by the kernel);
+  // ctx row r receives row r's output.
+  const int4 *items;
+  const int *nitems, *rows, *row_tok;
+  const void *q_rows;
 };
 hipError_t launch_attention(int precision, const AttnArgs &a, hipStream_t s);
+// Attention of the option rows only (the last layer past which only they are
+// used): the queries are rows r of row_tok grouped into a.items.
+hipError_t launch_attention_rows(int precision, const AttnArgs &a, hipStream_t s);
+// items / rows / nitems for launch_attention_rows from row_tok[R] and the
+// batch's seq_off (nseq + 1 entries); nseq <= ROW_ITEMS_MAXSEQ. items needs
+// nseq + ceil(R / ATTN_QUERIES) entries, rows R.
+constexpr int ROW_ITEMS_MAXSEQ = 1024;
+hipError_t launch_row_items(const int *row_tok, int R, const int *seq_off, int nseq, int T, int4 *items, int *rows,
+                            int *nitems, hipStream_t s);
 // Attention for model geometries the MFMA kernel does not take (head width 8,
 // 16 or 32; the reference's own small test models): one thread per query,
 // the reference's two-pass masked softmax (attnFwd + softmaxMasked,
