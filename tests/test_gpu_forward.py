@@ -536,3 +536,51 @@ def test_row_tail_flags_bad_row_index(base, engines):
         else:
             eng.check_device_errors()
             assert np.array_equal(out.cpu().numpy(), want)
+
+
+def test_row_tail_gather_fallbacks(base, engines):
+    """The row tail's other form (attention over every token, then the
+    option rows' attention output gathered), taken for batches of more than
+    1,024 sequences and for geometries the MFMA kernels do not tile: logits
+    of the full last layer, in both modes (fp32: |d| <= 1e-5 * (1 + |logit|);
+    bf16: the bf16 bar)."""
+    from decide_amd import Engine, NoGPUError
+    from decide_amd.nn import Config, build_sequence
+    from decide_amd.synth import config_batch, random_weights
+
+    cfg = base[0]
+    many = config_batch("cfg5", vocab=cfg.vocab) * 1100  # 1,100 sequences, 70,400 tokens, 2,200 rows
+    small_cfg = Config(hidden=96, intermediate=80, heads=6, layers=3, vocab=300, half_window=8,
+                       layer_types=["full_attention", "sliding_attention", "full_attention"])
+    rng = np.random.default_rng(11)
+    generic = []
+    for _ in range(8):  # 8 x ~300 tokens
+        ids = [1] + list(rng.integers(3, 299, size=280)) + [2]
+        for ln in (4, 5, 6):
+            ids += [299] + list(rng.integers(3, 299, size=ln - 1))
+        generic.append(build_sequence(np.array(ids + [2], np.int32), 299, independent=True))
+    try:
+        small = {p: Engine(small_cfg, random_weights(small_cfg, seed=9, std=0.05), precision=p)
+                 for p in ("fp32", "bf16")}
+    except NoGPUError:
+        pytest.skip("no GPU")
+    try:
+        cases = [("1100 sequences", engines["bf16"], many, "bf16"), ("1100 sequences", engines["fp32"], many, "fp32"),
+                 ("generic geometry", small["fp32"], generic, "fp32"),
+                 ("generic geometry", small["bf16"], generic, "bf16")]
+        for name, eng, batch, p in cases:
+            assert sum(len(s.ids) for s in batch) >= 2048
+            eng.set_row_tail(0)
+            full = eng.forward(batch)
+            eng.set_row_tail(2048)
+            tail = eng.forward(batch)
+            d = np.abs(tail.astype(np.float64) - full)
+            print(f"row tail fallback, {name} {p}: {len(tail)} rows, bit-identical {np.array_equal(tail, full)}, "
+                  f"max |dlogit| {float(d.max()):.3g}", flush=True)
+            if p == "fp32":
+                assert np.all(d <= 1e-5 * (1 + np.abs(full)))
+            else:
+                compare(tail, full.astype(np.float64), batch, p)
+    finally:
+        for e in small.values():
+            e.close()
