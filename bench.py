@@ -742,6 +742,10 @@ def extra_configs(eng, cfg, dev, stream, args) -> dict:
     out["cfg1"] = {"workload": "fp32 X[512x768] . W^T, W[2304x768] on fp32 MFMA (dn_gemm_device, operands resident)",
                    "us_per_call": round(us, 2), "tflops": round(flop / us / 1e6, 2),
                    "frac_of_fp32_peak": round(flop / us / 1e6 / 157.3, 4)}
+    # the fp32 matrix cores' attainable rate on such operands (register-only loop)
+    att32 = eng.mfma_calibrate(2)
+    out["cfg1"]["fp32_mfma_attainable_tflops"] = round(att32, 1)
+    out["cfg1"]["frac_of_fp32_attainable"] = round(flop / us / 1e6 / att32, 4) if att32 > 0 else None
     # cfg2 and cfg5: latency of one request through the host-array entry point
     for name, reps in (("cfg2", 1000), ("cfg5", 10000)):
         wl = Workload(eng, cfg, name, dev)

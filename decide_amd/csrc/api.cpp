@@ -1544,7 +1544,7 @@ int dn_read_probe(dn_ctx *c, double *ms, int *count) {
 }
 
 int dn_mfma_calibrate(dn_ctx *c, int mode, double *tflops) {
-  if (!c || !tflops || (mode != 0 && mode != 1)) return DN_INVALID_ARG;
+  if (!c || !tflops || mode < 0 || mode > 3) return DN_INVALID_ARG;
   c->err.clear();
   (void)hipSetDevice(c->device);
   int cus = 0;
@@ -1570,7 +1570,7 @@ int dn_mfma_calibrate(dn_ctx *c, int mode, double *tflops) {
   (void)hipEventDestroy(e0);
   (void)hipEventDestroy(e1);
   if (err != hipSuccess) return hip_fail(c, "mfma_calibrate", err);
-  *tflops = ms > 0 ? mfma_calibrate_flop(blocks, iters) / (ms * 1e-3) / 1e12 : 0.0;
+  *tflops = ms > 0 ? mfma_calibrate_flop(mode, blocks, iters) / (ms * 1e-3) / 1e12 : 0.0;
   return DN_OK;
 }
 

@@ -361,4 +361,4 @@ hipError_t launch_widen_bf16(const void *src, float *dst, size_t n, hipStream_t 
 // Register-only bf16 MFMA loop (calibrate.hip): mode 0 operands rotated every
 // iteration, mode 1 constant; mfma_calibrate_flop gives the work of a launch.
 hipError_t launch_mfma_calibrate(int mode, int blocks, int iters, float *sink, hipStream_t s);
-double mfma_calibrate_flop(int blocks, int iters);
+double mfma_calibrate_flop(int mode, int blocks, int iters);

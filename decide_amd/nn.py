@@ -273,7 +273,8 @@ class Engine:
         check(lib.dn_set_row_tail(self._h, int(min_tokens)), self._h)
 
     def mfma_calibrate(self, mode: int = 0) -> float:
-        """dn_mfma_calibrate: attainable bf16 MFMA TFLOP/s (mode 0 changing operands, 1 constant)."""
+        """dn_mfma_calibrate: attainable MFMA TFLOP/s (bf16: mode 0 changing operands, 1 constant;
+        fp32: 2 changing, 3 constant)."""
         out = ctypes.c_double(0.0)
         check(lib.dn_mfma_calibrate(self._h, int(mode), ctypes.byref(out)), self._h)
         return out.value

@@ -215,13 +215,15 @@ int dn_read_probe(dn_ctx *ctx, double *ms /* [5] */, int *count);
 enum { DN_PROBE_BWD_WGRAD_QKV = 0, DN_PROBE_BWD_DGRAD_QKV = 1, DN_PROBE_BWD_ATTENTION = 2 };
 int dn_read_probe_backward(dn_ctx *ctx, double *ms /* [3] */, int *count);
 
-/* Attainable bf16 MFMA rate of this GPU (TFLOP/s), for the roofline: a
- * register-only loop of v_mfma_f32_32x32x16_bf16 in the projection GEMMs' wave
- * pattern on every CU, no memory traffic. mode 0: operands with the forward's
- * statistics (activations ~ N(0,1), weights ~ N(0,0.02)) that change every
- * iteration, as a real GEMM's do; mode 1: constant operands. The matrix core
- * runs slower the more its inputs toggle, so mode 0 is the ceiling a GEMM on
- * real data can approach. Synchronous (~10 ms). No counterpart in the
+/* Attainable MFMA rate of this GPU (TFLOP/s), for the roofline: a
+ * register-only loop of v_mfma_f32_32x32x16_bf16 (modes 0, 1) or
+ * v_mfma_f32_32x32x2_f32 (modes 2, 3: the fp32 validation mode and
+ * dn_gemm_f32) in the projection GEMMs' wave pattern on every CU, no memory
+ * traffic. Modes 0 and 2: operands with the forward's statistics
+ * (activations ~ N(0,1), weights ~ N(0,0.02)) that change every iteration, as
+ * a real GEMM's do; modes 1 and 3: constant operands. The matrix core runs
+ * slower the more its inputs toggle, so modes 0 and 2 are the ceilings a GEMM
+ * on real data can approach. Synchronous (~10 ms). No counterpart in the
  * reference. */
 int dn_mfma_calibrate(dn_ctx *ctx, int mode, double *tflops);
 
