@@ -584,3 +584,62 @@ def test_row_tail_gather_fallbacks(base, engines):
     finally:
         for e in small.values():
             e.close()
+
+
+@pytest.mark.parametrize("layer_types", [["full_attention"], ["full_attention", "sliding_attention"]],
+                         ids=["one_layer", "sliding_last"])
+def test_row_tail_other_last_layers(layer_types):
+    """The option-row last layer when that layer is layer 0 (its QKV input is
+    the embedding norm) and when it is a sliding-window layer (the list-mode
+    attention with the window test), on a small MFMA geometry (hidden 256, 4
+    heads of 64) over 2,600 tokens: the logits of the full last layer up to
+    the small-M GEMM kernel's summation order (36 rows; |d| <= 1e-5 * (1 +
+    |logit|)), and of the oracle within the bars."""
+    from decide_amd import Engine, NoGPUError
+    from decide_amd.nn import Config, build_sequence
+    from decide_amd.synth import random_weights
+
+    cfg = Config(hidden=256, intermediate=384, heads=4, layers=len(layer_types), vocab=400, half_window=16,
+                 layer_types=layer_types)
+    w = random_weights(cfg, seed=13, std=0.05)
+    rng = np.random.default_rng(14)
+    batch = []
+    for prem in (900, 700, 500, 300):  # 4 sequences, ~2,600 tokens, 36 option rows
+        ids = [1] + list(rng.integers(3, 399, size=prem)) + [2]
+        for ln in (5, 9, 17, 3, 12, 7, 20, 4, 6):
+            ids += [399] + list(rng.integers(3, 399, size=ln - 1))
+        batch.append(build_sequence(np.array(ids + [2], np.int32), 399, independent=True))
+    assert sum(len(s.ids) for s in batch) >= 2048
+    oracle.set_workers(WORKERS)
+    want = oracle.OracleModel(cfg, w).forward(batch)
+    for p in ("bf16", "fp32"):
+        try:
+            eng = Engine(cfg, w, precision=p)
+        except NoGPUError:
+            pytest.skip("no GPU")
+        with eng:
+            eng.set_row_tail(0)
+            full = eng.forward(batch)
+            eng.set_row_tail(2048)
+            tail = eng.forward(batch)
+        d = np.abs(tail.astype(np.float64) - full)
+        print(f"{layer_types} {p}: bit-identical {np.array_equal(tail, full)}, max |dlogit| {float(d.max()):.3g}",
+              flush=True)
+        assert np.all(d <= 1e-5 * (1 + np.abs(full)))
+        if p == "bf16":
+            # probabilities only: this random one- or two-layer model's options are near ties
+            # (logits within ~0.04), so argmax is not a meaningful bf16 check here
+            wb = {n: (a if not n.endswith(("attn.Wqkv.weight", "attn.Wo.weight", "mlp.Wi.weight", "mlp.Wo.weight"))
+                      else _bf16_round(a)) for n, a in w.items()}
+            ref = oracle.OracleModel(cfg, wb).forward(batch)
+            dp = max(float(np.max(np.abs(a - b))) for a, b in zip(probs_per_seq(tail, batch), probs_per_seq(ref, batch)))
+            print(f"bf16 against the oracle (bf16 weights): max |dp| {dp:.3g}", flush=True)
+            assert dp <= 2e-3
+        else:
+            compare(tail, want, batch, p)
+
+
+def _bf16_round(a):
+    u = np.ascontiguousarray(a, np.float32).view(np.uint32).astype(np.uint64)
+    u = (u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000
+    return u.astype(np.uint32).view(np.float32).reshape(np.shape(a))
