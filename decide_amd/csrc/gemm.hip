@@ -457,7 +457,11 @@ __global__ __launch_bounds__(64 * W) void gemm_skinny_kernel(GemmArgs g) {
   constexpr int TR = 32 * MB, TC = 32 * NB, TE = TR * TC;
   static_assert((EPI != EPI_GEGLU && EPI != EPI_GEGLU_KEEP) || NB == 2, "GeGLU tiles pair 32 value and 32 gate columns");
   static_assert(W == 4 || W == 8, "wave count");
-  __shared__ __attribute__((aligned(16))) float red[4 * TE];
+  // Partial tiles held in LDS at once: all W when they fit in 64 KB.
+  constexpr bool FOLD = W == 8 && 8 * TE * 4 > 65536;
+  constexpr int NP = FOLD ? 4 : W;
+  constexpr int TE4 = TE / 4, NQ = (TE4 + NT - 1) / NT;  // fp32 epilogue float4s per thread
+  __shared__ __attribute__((aligned(16))) float red[NP * TE];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, lr = lane & 31, lh = lane >> 5;
   const int n0 = blockIdx.x * TC, m0 = blockIdx.y * TR;
@@ -489,6 +493,22 @@ __global__ __launch_bounds__(64 * W) void gemm_skinny_kernel(GemmArgs g) {
   uint4 la[MB][4], lb[NB][4];
   int grp = wave;
   if (grp < ngrp) SKINNY_LOAD(la, lb, grp);
+  // The fp32 epilogue's residual input, loaded now (behind the first operand
+  // group) so its latency overlaps the main loop instead of following the
+  // reduction; each element is read and then written by this thread only.
+  float4 pre[NQ];
+  const bool vec = (g.ldc & 3) == 0;
+  if constexpr (EPI == EPI_F32) {
+    const float *R = g.res ? g.res : (const float *)g.C;
+#pragma unroll
+    for (int k = 0; k < NQ; k++) {
+      pre[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+      const int q = tid + NT * k;
+      const int r = q / (TC / 4), col = n0 + (q % (TC / 4)) * 4;
+      if (g.accumulate && vec && q < TE4 && m0 + r < g.M && col + 4 <= g.n_store)
+        pre[k] = *(const float4 *)(R + (size_t)(m0 + r) * g.ldc + col);
+    }
+  }
   for (; grp < ngrp; grp += W) {
     uint4 na[MB][4], nb[NB][4];
     const bool more = grp + W < ngrp;
@@ -528,9 +548,12 @@ __global__ __launch_bounds__(64 * W) void gemm_skinny_kernel(GemmArgs g) {
   }
 #undef SKINNY_LOAD
 
-  // Reduce the W partial tiles (row-major TR x TC): with 8 waves, waves 4..7
-  // hand theirs to waves 0..3 first; then the four are summed in wave order.
-  if constexpr (W == 8) {
+  // Reduce the W partial tiles (row-major TR x TC) in a fixed order:
+  // (p0 + p4) + (p1 + p5) + (p2 + p6) + (p3 + p7) with 8 waves, p0 + p1 + p2 +
+  // p3 with 4. When the eight partials fit in LDS every wave stores its own
+  // and one barrier follows; otherwise waves 4..7 fold theirs into waves 0..3
+  // first. Each epilogue thread then sums only the elements it stores.
+  if constexpr (FOLD) {
     if (wave >= 4) {
       float *mine = red + (wave - 4) * TE;
 #pragma unroll
@@ -552,7 +575,7 @@ __global__ __launch_bounds__(64 * W) void gemm_skinny_kernel(GemmArgs g) {
     }
     __syncthreads();
   }
-  if (wave < 4) {
+  if (wave < NP) {
     float *mine = red + wave * TE;
 #pragma unroll
     for (int i = 0; i < MB; i++)
@@ -562,35 +585,38 @@ __global__ __launch_bounds__(64 * W) void gemm_skinny_kernel(GemmArgs g) {
         for (int e = 0; e < 16; e++) mine[(32 * i + mfma_row(e, lane)) * TC + 32 * j + lr] = acc[i][j][e];
   }
   __syncthreads();
-  float4 *red4 = (float4 *)red;
-  constexpr int TE4 = TE / 4;
-  for (int q = tid; q < TE4; q += NT) {
-    float4 v = red4[q];
+  const float4 *red4 = (const float4 *)red;
+  // The reduced tile's float4 at index q4 (row-major TR x TC / 4).
+  auto rsum4 = [&](int q4) {
+    auto add = [](float4 x, float4 y) { return make_float4(x.x + y.x, x.y + y.y, x.z + y.z, x.w + y.w); };
+    float4 v;
+    if constexpr (NP == 8) {
+      v = add(red4[q4], red4[4 * TE4 + q4]);
 #pragma unroll
-    for (int w = 1; w < 4; w++) {
-      const float4 u = red4[w * TE4 + q];
-      v.x += u.x;
-      v.y += u.y;
-      v.z += u.z;
-      v.w += u.w;
+      for (int w = 1; w < 4; w++) v = add(v, add(red4[w * TE4 + q4], red4[(w + 4) * TE4 + q4]));
+    } else {
+      v = red4[q4];
+#pragma unroll
+      for (int w = 1; w < 4; w++) v = add(v, red4[w * TE4 + q4]);
     }
-    red4[q] = v;  // each index is read and written by one thread only
-  }
-  __syncthreads();
+    return v;
+  };
 
   if constexpr (EPI == EPI_F32) {
     float *C = (float *)g.C;
-    const bool vec = (g.ldc & 3) == 0;
-    for (int q = tid; q < TE4; q += NT) {
+#pragma unroll
+    for (int k = 0; k < NQ; k++) {
+      const int q = tid + NT * k;
+      if (q >= TE4) break;
       const int r = q / (TC / 4), c4 = (q % (TC / 4)) * 4, col = n0 + c4;
       if (m0 + r >= g.M || col >= g.n_store) continue;
-      const float4 v = red4[q];
+      const float4 v = rsum4(q);
       float *p = C + (size_t)(m0 + r) * g.ldc + col;
-      const float *pr = (g.res ? g.res : C) + (size_t)(m0 + r) * g.ldc + col;  // residual input
       if (vec && col + 4 <= g.n_store) {
-        float4 o = g.accumulate ? *(const float4 *)pr : make_float4(0.f, 0.f, 0.f, 0.f);
+        const float4 o = pre[k];
         *(float4 *)p = make_float4(o.x + v.x, o.y + v.y, o.z + v.z, o.w + v.w);
       } else {
+        const float *pr = (g.res ? g.res : C) + (size_t)(m0 + r) * g.ldc + col;  // residual input
         const float vv[4] = {v.x, v.y, v.z, v.w};
         for (int u = 0; u < 4 && col + u < g.n_store; u++) p[u] = g.accumulate ? pr[u] + vv[u] : vv[u];
       }
@@ -604,14 +630,24 @@ __global__ __launch_bounds__(64 * W) void gemm_skinny_kernel(GemmArgs g) {
       for (int q = tid; q < TR * (OC / EPV); q += NT) {
         const int r = q / (OC / EPV), c = (q % (OC / EPV)) * EPV;
         if (m0 + r >= g.M) continue;
+        float val[EPV], gate[EPV];
+#pragma unroll
+        for (int h = 0; h < EPV / 4; h++) {
+          const float4 v = rsum4((r * TC + c) / 4 + h);
+          val[4 * h] = v.x, val[4 * h + 1] = v.y, val[4 * h + 2] = v.z, val[4 * h + 3] = v.w;
+          if constexpr (G) {
+            const float4 u = rsum4((r * TC + 32 + c) / 4 + h);
+            gate[4 * h] = u.x, gate[4 * h + 1] = u.y, gate[4 * h + 2] = u.z, gate[4 * h + 3] = u.w;
+          }
+        }
         unsigned w[4];
 #pragma unroll
         for (int u = 0; u < EPV; u++) {
           float v;
           if constexpr (!G) {
-            v = red[r * TC + c + u];
+            v = val[u];
           } else {
-            v = gelu_erf<T>(red[r * TC + c + u]) * red[r * TC + 32 + c + u];
+            v = gelu_erf<T>(val[u]) * gate[u];
           }
           if constexpr (sizeof(T) == 2) {
             const unsigned b = __builtin_bit_cast(unsigned short, (bf16)v);
