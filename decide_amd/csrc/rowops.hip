@@ -9,9 +9,45 @@
 
 namespace {
 
+// Butterfly sums over the 64 lanes, v + v[lane ^ o] for o = 32, 16, ..., 1,
+// without LDS round trips: the lane-32 and lane-16 exchanges are
+// v_permlane32_swap / v_permlane16_swap (swapping a copy of v with itself
+// leaves v[l] in one result and v[l ^ o] in the other, so their sum is the
+// exchange sum), the others DPP moves: row_ror:8 is lane ^ 8 within a row of
+// 16; row_ror:4 reads lane (l +- 4) mod 16, which after the three steps
+// above holds the same value as lane l ^ 4 (each lane's value depends on
+// l % 8 only); quad_perm [2,3,0,1] and [1,0,3,2] are lane ^ 2 and lane ^ 1.
+// Floating-point addition is commutative, so every lane ends with the same
+// bits as the shuffle butterfly v += __shfl_xor(v, o).
+template <int CTRL>
+__device__ __forceinline__ unsigned dpp_u32(unsigned x) {
+  return (unsigned)__builtin_amdgcn_update_dpp(0, (int)x, CTRL, 0xF, 0xF, false);
+}
+template <int CTRL>
+__device__ __forceinline__ double dpp_f64(double v) {
+  const unsigned long long u = __double_as_longlong(v);
+  const unsigned lo = dpp_u32<CTRL>((unsigned)u), hi = dpp_u32<CTRL>((unsigned)(u >> 32));
+  return __longlong_as_double((long long)(((unsigned long long)hi << 32) | lo));
+}
 __device__ __forceinline__ double wave_sum(double v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  {
+    const unsigned long long u = __double_as_longlong(v);
+    const auto lo = __builtin_amdgcn_permlane32_swap((unsigned)u, (unsigned)u, false, false);
+    const auto hi = __builtin_amdgcn_permlane32_swap((unsigned)(u >> 32), (unsigned)(u >> 32), false, false);
+    v = __longlong_as_double((long long)(((unsigned long long)hi[0] << 32) | lo[0])) +
+        __longlong_as_double((long long)(((unsigned long long)hi[1] << 32) | lo[1]));
+  }
+  {
+    const unsigned long long u = __double_as_longlong(v);
+    const auto lo = __builtin_amdgcn_permlane16_swap((unsigned)u, (unsigned)u, false, false);
+    const auto hi = __builtin_amdgcn_permlane16_swap((unsigned)(u >> 32), (unsigned)(u >> 32), false, false);
+    v = __longlong_as_double((long long)(((unsigned long long)hi[0] << 32) | lo[0])) +
+        __longlong_as_double((long long)(((unsigned long long)hi[1] << 32) | lo[1]));
+  }
+  v += dpp_f64<0x128>(v);  // row_ror:8
+  v += dpp_f64<0x124>(v);  // row_ror:4
+  v += dpp_f64<0x4E>(v);   // quad_perm [2,3,0,1]
+  v += dpp_f64<0xB1>(v);   // quad_perm [1,0,3,2]
   return v;
 }
 __device__ __forceinline__ float wave_sumf(float v) {
@@ -73,21 +109,24 @@ __global__ __launch_bounds__(256) void embed_ln_kernel(const int *ids, int Tn, c
   }
   const int nvec = dim / 4;
   const float4 *src = (const float4 *)(tok + (size_t)id * dim);
-  float4 x[MAXV];
+  float4 x[MAXV], wv[MAXV];
+  const float4 *w4 = (const float4 *)w;
 #pragma unroll
   for (int j = 0; j < MAXV; j++)
     if (lane + 64 * j < nvec) x[j] = src[lane + 64 * j];
+#pragma unroll
+  for (int j = 0; j < MAXV; j++)  // the weights with the row, not after its statistics
+    if (lane + 64 * j < nvec) wv[j] = w4[lane + 64 * j];
   float mean, rs;
   row_stats(x, nvec, lane, dim, eps, mean, rs);
   if (mean_out && lane == 0) {  // training keeps the statistics (forward.go:220, layerNormFwd's mean/rstd)
     mean_out[t] = mean;
     rstd_out[t] = rs;
   }
-  const float4 *w4 = (const float4 *)w;
 #pragma unroll
   for (int j = 0; j < MAXV; j++)
     if (lane + 64 * j < nvec) {
-      const float4 ww = w4[lane + 64 * j];
+      const float4 ww = wv[j];
       float4 y;
       y.x = (x[j].x - mean) * rs * ww.x;
       y.y = (x[j].y - mean) * rs * ww.y;
@@ -115,7 +154,12 @@ __global__ __launch_bounds__(256) void ln_kernel(const float *xin, int rows, int
     for (int j = 0; j < MAXV; j++)
       if (lane + 64 * j < nvec) x[rr][j] = src[lane + 64 * j];
   }
+  // The weights are loaded with the row, not after its statistics.
   const float4 *w4 = (const float4 *)w;
+  float4 wv[MAXV];
+#pragma unroll
+  for (int j = 0; j < MAXV; j++)
+    if (lane + 64 * j < nvec) wv[j] = w4[lane + 64 * j];
 #pragma unroll
   for (int rr = 0; rr < RPW; rr++) {
     const int r = r0 + rr;
@@ -129,7 +173,7 @@ __global__ __launch_bounds__(256) void ln_kernel(const float *xin, int rows, int
 #pragma unroll
     for (int j = 0; j < MAXV; j++)
       if (lane + 64 * j < nvec) {
-        const float4 ww = w4[lane + 64 * j];
+        const float4 ww = wv[j];
         float4 o;
         o.x = (x[rr][j].x - mean) * rs * ww.x;
         o.y = (x[rr][j].y - mean) * rs * ww.y;
@@ -175,28 +219,35 @@ __global__ __launch_bounds__(256) void head_pre_kernel(HeadArgs a, float *s1) {
     t = 0;
   }
   const float4 *src = (const float4 *)(a.h + (size_t)t * dim);
-  float4 x[MAXV];
+  float4 x[MAXV], fwv[MAXV], iwv[MAXV], ibv[MAXV];
 #pragma unroll
   for (int j = 0; j < MAXV; j++)
     if (lane + 64 * j < nvec) x[j] = src[lane + 64 * j];
-  float mean, rs;
-  row_stats(x, nvec, lane, dim, a.eps, mean, rs);
-  const float4 *fw = (const float4 *)a.final_norm;
+  // Both norms' weights with the row, not after its statistics.
+  const float4 *fw = (const float4 *)a.final_norm, *iw = (const float4 *)a.in_w, *ib = (const float4 *)a.in_b;
 #pragma unroll
   for (int j = 0; j < MAXV; j++)
     if (lane + 64 * j < nvec) {
-      const float4 ww = fw[lane + 64 * j];
+      fwv[j] = fw[lane + 64 * j];
+      iwv[j] = iw[lane + 64 * j];
+      ibv[j] = ib[lane + 64 * j];
+    }
+  float mean, rs;
+  row_stats(x, nvec, lane, dim, a.eps, mean, rs);
+#pragma unroll
+  for (int j = 0; j < MAXV; j++)
+    if (lane + 64 * j < nvec) {
+      const float4 ww = fwv[j];
       x[j].x = (x[j].x - mean) * rs * ww.x;
       x[j].y = (x[j].y - mean) * rs * ww.y;
       x[j].z = (x[j].z - mean) * rs * ww.z;
       x[j].w = (x[j].w - mean) * rs * ww.w;
     }
   row_stats(x, nvec, lane, dim, 1e-5f, mean, rs);
-  const float4 *iw = (const float4 *)a.in_w, *ib = (const float4 *)a.in_b;
 #pragma unroll
   for (int j = 0; j < MAXV; j++)
     if (lane + 64 * j < nvec) {
-      const float4 ww = iw[lane + 64 * j], bb = ib[lane + 64 * j];
+      const float4 ww = iwv[j], bb = ibv[j];
       float4 y;
       y.x = (x[j].x - mean) * rs * ww.x + bb.x;
       y.y = (x[j].y - mean) * rs * ww.y + bb.y;
@@ -212,15 +263,26 @@ __global__ __launch_bounds__(256) void head_post_kernel(HeadArgs a, const float 
   if (r >= a.R) return;
   const int half = a.H / 2;
   constexpr int MAXE = 8;  // half <= 512
-  float g[MAXE];
+  float g[MAXE], nw[MAXE], nb[MAXE], ow[MAXE];
+#pragma unroll
+  for (int j = 0; j < MAXE; j++) {  // the norm and output weights with the row, not after its statistics
+    const int i = lane + 64 * j;
+    if (i < half) {
+      g[j] = d[(size_t)r * half + i] + a.dense_b[i];
+      nw[j] = a.norm_w[i];
+      nb[j] = a.norm_b[i];
+      ow[j] = a.out_w[i];
+    }
+  }
   double s = 0;
 #pragma unroll
   for (int j = 0; j < MAXE; j++) {
     const int i = lane + 64 * j;
-    g[j] = 0.0f;
     if (i < half) {
-      g[j] = gelu_erf<float>(d[(size_t)r * half + i] + a.dense_b[i]);
+      g[j] = gelu_erf<float>(g[j]);
       s += (double)g[j];
+    } else {
+      g[j] = 0.0f;
     }
   }
   const double mu = wave_sum(s) / (double)half;
@@ -238,7 +300,7 @@ __global__ __launch_bounds__(256) void head_post_kernel(HeadArgs a, const float 
 #pragma unroll
   for (int j = 0; j < MAXE; j++) {
     const int i = lane + 64 * j;
-    if (i < half) dot += ((g[j] - m) * rs * a.norm_w[i] + a.norm_b[i]) * a.out_w[i];
+    if (i < half) dot += ((g[j] - m) * rs * nw[j] + nb[j]) * ow[j];
   }
   dot = wave_sumf(dot);
   if (lane == 0) a.logits[r] = dot + a.out_b[0];
