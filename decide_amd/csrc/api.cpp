@@ -169,8 +169,9 @@ void host_layout(HostLayout &hl, int nseq, const int32_t *seq_len, int *T_out, i
     hl.seq_off[s] = T;
     hl.chunk_off[s] = nch;
     for (int i = 0; i < n; i += 32) hl.chunk_desc.push_back(make_int4(T + i, std::min(32, n - i), 0, 0));
-    for (int q = 0; q < n; q += ATTN_QUERIES) hl.work.push_back(make_int4(s, q, 0, 0));
-    for (int q = 0; q < n; q += ATTN_QUERIES_GLOBAL) hl.work2.push_back(make_int4(s, q, 0, 0));
+    // Work item: (sequence, first query, sequence offset, sequence length).
+    for (int q = 0; q < n; q += ATTN_QUERIES) hl.work.push_back(make_int4(s, q, T, n));
+    for (int q = 0; q < n; q += ATTN_QUERIES_GLOBAL) hl.work2.push_back(make_int4(s, q, T, n));
     nch += (n + 31) / 32;
     T += n;
   }

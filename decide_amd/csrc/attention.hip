@@ -304,16 +304,18 @@ __global__ __launch_bounds__(64 * QW) __attribute__((amdgpu_waves_per_eu(QT == 1
   int logical = bid;
   if (total % 8 == 0) logical = (bid % 8) * (total / 8) + bid / 8;
   const int wi = logical / a.heads, head = logical % a.heads;
-  int s, q0 = 0, slot0 = 0, cnt = 0;
+  int s, q0 = 0, slot0 = 0, cnt = 0, n, base;
   if constexpr (LIST) {
     if (wi >= *a.nitems) return;  // the grid is sized by an upper bound on the items
     const int4 it = a.items[wi];
     s = it.x, slot0 = it.y, cnt = it.z;
+    n = a.seq_len[s], base = a.seq_off[s];
   } else {
+    // (sequence, first query, offset, length): no dependent load for the
+    // sequence's extent before the key info and staging loads.
     const int4 wk = a.work[wi];
-    s = wk.x, q0 = wk.y;
+    s = wk.x, q0 = wk.y, base = wk.z, n = wk.w;
   }
-  const int n = a.seq_len[s], base = a.seq_off[s];
   const int H = a.H, ld = 3 * H;
   const T *qkv = (const T *)a.qkv;
   const int nkt = (n + KTILE - 1) / KTILE;
@@ -751,8 +753,13 @@ __global__ void chunk_summary_kernel(const int *kinfo, const int4 *desc, ChunkIn
   if (c >= nchunks) return;
   const int4 d = desc[c];  // (first token, length)
   ChunkInfo ci = {0x7fffffff, -0x7fffffff, 0x7fffffff, -1, 0, 0, d.y, 0};
-  for (int i = 0; i < d.y; i++) {
-    const int v = kinfo[d.x + i];
+  int kv[32];  // the chunk's (<= 32) token infos, all loads issued before the first use
+#pragma unroll
+  for (int i = 0; i < 32; i++) kv[i] = i < d.y ? kinfo[d.x + i] : 0;
+#pragma unroll
+  for (int i = 0; i < 32; i++) {
+    if (i >= d.y) break;
+    const int v = kv[i];
     const int o = (v >> 16) - 1, p = v & 0xffff;
     ci.pmin = min(ci.pmin, p);
     ci.pmax = max(ci.pmax, p);

@@ -200,7 +200,7 @@ struct AttnArgs {
   void *ctx;
   const int *kinfo;   // per token: ((opt+1) << 16) | pos
   const float *cos_t, *sin_t;  // RoPE tables [65536 x 32] of this layer's theta, row = position
-  const int4 *work;   // (seq, q0, 0, 0) per workgroup
+  const int4 *work;   // (seq, q0, seq offset, seq length) per workgroup
   const uint32_t *codes;  // [nwork][ATTN_MAXKT] tile classes of this layer type (tile_codes_kernel)
   const int *first;       // [nwork] first tile with an allowed pair
   const int *seq_off, *seq_len;
