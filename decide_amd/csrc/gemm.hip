@@ -53,6 +53,12 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
 }
 
+// Round-to-nearest-even fp32 pair -> two bf16 in one word (lo first).
+__device__ __forceinline__ unsigned pack_bf16_pair(float lo, float hi) {
+  return (unsigned)__builtin_bit_cast(unsigned short, (bf16)lo) |
+         ((unsigned)__builtin_bit_cast(unsigned short, (bf16)hi) << 16);
+}
+
 template <int BM, int BN>
 struct TileOrder {
   int m0, n0;
@@ -447,6 +453,29 @@ hipError_t launch_cfg_one(const GemmArgs &a, hipStream_t s, int splits = 1) {
 // l%32 at group offset 2*VPL*j + VPL*(l/32); for bf16 that is exactly the
 // k step j operand of v_mfma_f32_32x32x16_bf16, for fp32 the four values
 // feed four v_mfma_f32_32x32x2f32 (A and B use the same k order).
+template <int V>
+using fvec = float __attribute__((ext_vector_type(V)));
+
+// Sum of the NP partial tiles (TE floats apart) at float index idx (a
+// multiple of V): (p0 + p4) + (p1 + p5) + (p2 + p6) + (p3 + p7) for eight,
+// p0 + p1 + p2 + p3 for four.
+template <int V, int NP, int TE>
+__device__ __forceinline__ fvec<V> partial_sum(const float *red, int idx) {
+  const fvec<V> *p = (const fvec<V> *)(red + idx);
+  constexpr int S = TE / V;
+  fvec<V> v;
+  if constexpr (NP == 8) {
+    v = p[0] + p[4 * S];
+#pragma unroll
+    for (int w = 1; w < 4; w++) v = v + (p[w * S] + p[(w + 4) * S]);
+  } else {
+    v = p[0];
+#pragma unroll
+    for (int w = 1; w < 4; w++) v = v + p[w * S];
+  }
+  return v;
+}
+
 template <class T, int MB, int NB, int EPI, int W>
 __global__ __launch_bounds__(64 * W) void gemm_skinny_kernel(GemmArgs g) {
   using MF = Mfma<T>;
@@ -460,7 +489,9 @@ __global__ __launch_bounds__(64 * W) void gemm_skinny_kernel(GemmArgs g) {
   // Partial tiles held in LDS at once: all W when they fit in 64 KB.
   constexpr bool FOLD = W == 8 && 8 * TE * 4 > 65536;
   constexpr int NP = FOLD ? 4 : W;
-  constexpr int TE4 = TE / 4, NQ = (TE4 + NT - 1) / NT;  // fp32 epilogue float4s per thread
+  // The fp32 epilogue works on items of FV floats, two when that gives every
+  // thread one item; NQ items per thread.
+  constexpr int FV = TE <= 2 * NT ? 2 : 4, TEV = TE / FV, NQ = (TEV + NT - 1) / NT;
   __shared__ __attribute__((aligned(16))) float red[NP * TE];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, lr = lane & 31, lh = lane >> 5;
@@ -496,17 +527,17 @@ __global__ __launch_bounds__(64 * W) void gemm_skinny_kernel(GemmArgs g) {
   // The fp32 epilogue's residual input, loaded now (behind the first operand
   // group) so its latency overlaps the main loop instead of following the
   // reduction; each element is read and then written by this thread only.
-  float4 pre[NQ];
-  const bool vec = (g.ldc & 3) == 0;
+  fvec<FV> pre[NQ];
+  const bool vec = (g.ldc & (FV - 1)) == 0;
   if constexpr (EPI == EPI_F32) {
     const float *R = g.res ? g.res : (const float *)g.C;
 #pragma unroll
     for (int k = 0; k < NQ; k++) {
-      pre[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+      pre[k] = 0.0f;
       const int q = tid + NT * k;
-      const int r = q / (TC / 4), col = n0 + (q % (TC / 4)) * 4;
-      if (g.accumulate && vec && q < TE4 && m0 + r < g.M && col + 4 <= g.n_store)
-        pre[k] = *(const float4 *)(R + (size_t)(m0 + r) * g.ldc + col);
+      const int r = q / (TC / FV), col = n0 + (q % (TC / FV)) * FV;
+      if (g.accumulate && vec && q < TEV && m0 + r < g.M && col + FV <= g.n_store)
+        pre[k] = *(const fvec<FV> *)(R + (size_t)(m0 + r) * g.ldc + col);
     }
   }
   for (; grp < ngrp; grp += W) {
@@ -585,78 +616,67 @@ __global__ __launch_bounds__(64 * W) void gemm_skinny_kernel(GemmArgs g) {
         for (int e = 0; e < 16; e++) mine[(32 * i + mfma_row(e, lane)) * TC + 32 * j + lr] = acc[i][j][e];
   }
   __syncthreads();
-  const float4 *red4 = (const float4 *)red;
-  // The reduced tile's float4 at index q4 (row-major TR x TC / 4).
-  auto rsum4 = [&](int q4) {
-    auto add = [](float4 x, float4 y) { return make_float4(x.x + y.x, x.y + y.y, x.z + y.z, x.w + y.w); };
-    float4 v;
-    if constexpr (NP == 8) {
-      v = add(red4[q4], red4[4 * TE4 + q4]);
-#pragma unroll
-      for (int w = 1; w < 4; w++) v = add(v, add(red4[w * TE4 + q4], red4[(w + 4) * TE4 + q4]));
-    } else {
-      v = red4[q4];
-#pragma unroll
-      for (int w = 1; w < 4; w++) v = add(v, red4[w * TE4 + q4]);
-    }
-    return v;
-  };
-
   if constexpr (EPI == EPI_F32) {
     float *C = (float *)g.C;
 #pragma unroll
     for (int k = 0; k < NQ; k++) {
       const int q = tid + NT * k;
-      if (q >= TE4) break;
-      const int r = q / (TC / 4), c4 = (q % (TC / 4)) * 4, col = n0 + c4;
+      if (q >= TEV) break;
+      const int r = q / (TC / FV), c = (q % (TC / FV)) * FV, col = n0 + c;
       if (m0 + r >= g.M || col >= g.n_store) continue;
-      const float4 v = rsum4(q);
+      const fvec<FV> v = partial_sum<FV, NP, TE>(red, r * TC + c);
       float *p = C + (size_t)(m0 + r) * g.ldc + col;
-      if (vec && col + 4 <= g.n_store) {
-        const float4 o = pre[k];
-        *(float4 *)p = make_float4(o.x + v.x, o.y + v.y, o.z + v.z, o.w + v.w);
+      if (vec && col + FV <= g.n_store) {
+        *(fvec<FV> *)p = pre[k] + v;
       } else {
         const float *pr = (g.res ? g.res : C) + (size_t)(m0 + r) * g.ldc + col;  // residual input
-        const float vv[4] = {v.x, v.y, v.z, v.w};
-        for (int u = 0; u < 4 && col + u < g.n_store; u++) p[u] = g.accumulate ? pr[u] + vv[u] : vv[u];
+        for (int u = 0; u < FV && col + u < g.n_store; u++) p[u] = g.accumulate ? pr[u] + v[u] : v[u];
       }
     }
   } else {
     auto emit = [&](auto gated, T *C, int ldo) {
       constexpr bool G = decltype(gated)::value;
-      constexpr int EPV = 16 / (int)sizeof(T);  // elements per 16-byte store
-      constexpr int OC = G ? TC / 2 : TC;       // output columns of the tile
+      constexpr int OC = G ? TC / 2 : TC;  // output columns of the tile
+      // Elements per thread item: bf16 down to 2 (a 4-byte store) so that
+      // every thread has an item; fp32 4 (16 bytes).
+      constexpr int EPV = sizeof(T) == 4 ? 4 : TR * OC >= 8 * NT ? 8 : TR * OC >= 4 * NT ? 4 : 2;
+      constexpr int RV = EPV > 4 ? 4 : EPV;  // partial-sum vector width
       const int oc0 = G ? n0 / 2 : n0;
       for (int q = tid; q < TR * (OC / EPV); q += NT) {
         const int r = q / (OC / EPV), c = (q % (OC / EPV)) * EPV;
         if (m0 + r >= g.M) continue;
         float val[EPV], gate[EPV];
 #pragma unroll
-        for (int h = 0; h < EPV / 4; h++) {
-          const float4 v = rsum4((r * TC + c) / 4 + h);
-          val[4 * h] = v.x, val[4 * h + 1] = v.y, val[4 * h + 2] = v.z, val[4 * h + 3] = v.w;
+        for (int h = 0; h < EPV / RV; h++) {
+          const fvec<RV> v = partial_sum<RV, NP, TE>(red, r * TC + c + RV * h);
+#pragma unroll
+          for (int u = 0; u < RV; u++) val[RV * h + u] = v[u];
           if constexpr (G) {
-            const float4 u = rsum4((r * TC + 32 + c) / 4 + h);
-            gate[4 * h] = u.x, gate[4 * h + 1] = u.y, gate[4 * h + 2] = u.z, gate[4 * h + 3] = u.w;
+            const fvec<RV> x = partial_sum<RV, NP, TE>(red, r * TC + 32 + c + RV * h);
+#pragma unroll
+            for (int u = 0; u < RV; u++) gate[RV * h + u] = x[u];
           }
         }
-        unsigned w[4];
+        float o[EPV];
 #pragma unroll
         for (int u = 0; u < EPV; u++) {
-          float v;
           if constexpr (!G) {
-            v = val[u];
+            o[u] = val[u];
           } else {
-            v = gelu_erf<T>(val[u]) * gate[u];
-          }
-          if constexpr (sizeof(T) == 2) {
-            const unsigned b = __builtin_bit_cast(unsigned short, (bf16)v);
-            w[u / 2] = (u & 1) ? (w[u / 2] | (b << 16)) : b;
-          } else {
-            w[u] = __float_as_uint(v);
+            o[u] = gelu_erf<T>(val[u]) * gate[u];
           }
         }
-        *(uint4 *)(C + (size_t)(m0 + r) * ldo + oc0 + c) = make_uint4(w[0], w[1], w[2], w[3]);
+        T *dst = C + (size_t)(m0 + r) * ldo + oc0 + c;
+        if constexpr (sizeof(T) == 2) {
+          unsigned w[EPV / 2];
+#pragma unroll
+          for (int u = 0; u < EPV / 2; u++) w[u] = pack_bf16_pair(o[2 * u], o[2 * u + 1]);
+          if constexpr (EPV == 8) *(uint4 *)dst = make_uint4(w[0], w[1], w[2], w[3]);
+          else if constexpr (EPV == 4) *(uint2 *)dst = make_uint2(w[0], w[1]);
+          else *(unsigned *)dst = w[0];
+        } else {
+          *(float4 *)dst = make_float4(o[0], o[1], o[2], o[3]);
+        }
       }
     };
     if constexpr (EPI == EPI_STORE) {
