@@ -484,7 +484,8 @@ __global__ __launch_bounds__(64 * W) void gemm_skinny_kernel(GemmArgs g) {
   constexpr int VPL = 16 / (int)sizeof(T);  // elements per 16-byte load
   constexpr int GK = 8 * VPL;               // k elements per group
   constexpr int TR = 32 * MB, TC = 32 * NB, TE = TR * TC;
-  static_assert((EPI != EPI_GEGLU && EPI != EPI_GEGLU_KEEP) || NB == 2, "GeGLU tiles pair 32 value and 32 gate columns");
+  static_assert(EPI != EPI_GEGLU_KEEP || NB == 2, "the kept pre-activation tile is 32 value + 32 gate columns");
+  static_assert(EPI != EPI_GEGLU || NB <= 2, "GeGLU tiles");
   static_assert(W == 4 || W == 8, "wave count");
   // Partial tiles held in LDS at once: all W when they fit in 64 KB.
   constexpr bool FOLD = W == 8 && 8 * TE * 4 > 65536;
@@ -501,7 +502,17 @@ __global__ __launch_bounds__(64 * W) void gemm_skinny_kernel(GemmArgs g) {
 #pragma unroll
   for (int i = 0; i < MB; i++) ap[i] = (const T *)g.A + (size_t)min(m0 + 32 * i + lr, g.M - 1) * g.lda + lh * VPL;
 #pragma unroll
-  for (int j = 0; j < NB; j++) bp[j] = (const T *)g.B + (size_t)(n0 + 32 * j + lr) * g.ldb + lh * VPL;
+  for (int j = 0; j < NB; j++) {
+    // GeGLU on 32-column tiles: the 64-row group n0 / 64 of the interleaved
+    // weights holds 32 value rows then their 32 gate rows; tile half
+    // (n0 / 32) % 2 takes value rows 16h .. 16h+15 as columns 0..15 and the
+    // matching gate rows as columns 16..31, so the tile's outputs are the 16
+    // columns n0 / 2 .. n0 / 2 + 15.
+    const int row = (EPI == EPI_GEGLU && NB == 1)
+                        ? (n0 & ~63) + (lr < 16 ? 0 : 32) + ((n0 >> 5) & 1) * 16 + (lr & 15)
+                        : n0 + 32 * j + lr;
+    bp[j] = (const T *)g.B + (size_t)row * g.ldb + lh * VPL;
+  }
 
   f32x16 acc[MB][NB];
 #pragma unroll
@@ -652,7 +663,7 @@ __global__ __launch_bounds__(64 * W) void gemm_skinny_kernel(GemmArgs g) {
 #pragma unroll
           for (int u = 0; u < RV; u++) val[RV * h + u] = v[u];
           if constexpr (G) {
-            const fvec<RV> x = partial_sum<RV, NP, TE>(red, r * TC + 32 + c + RV * h);
+            const fvec<RV> x = partial_sum<RV, NP, TE>(red, r * TC + TC / 2 + c + RV * h);
 #pragma unroll
             for (int u = 0; u < RV; u++) gate[RV * h + u] = x[u];
           }
@@ -701,8 +712,7 @@ hipError_t launch_skinny_cfg(int epi, const GemmArgs &a, hipStream_t s) {
       hipLaunchKernelGGL((gemm_skinny_kernel<T, MB, NB, EPI_STORE, W>), grid, block, 0, s, a);
       break;
     case EPI_GEGLU:
-      if constexpr (NB == 2) hipLaunchKernelGGL((gemm_skinny_kernel<T, MB, 2, EPI_GEGLU, W>), grid, block, 0, s, a);
-      else return hipErrorInvalidValue;
+      hipLaunchKernelGGL((gemm_skinny_kernel<T, MB, NB, EPI_GEGLU, W>), grid, block, 0, s, a);
       break;
     default:
       if constexpr (NB == 2) hipLaunchKernelGGL((gemm_skinny_kernel<T, MB, 2, EPI_GEGLU_KEEP, W>), grid, block, 0, s, a);
@@ -718,6 +728,12 @@ hipError_t launch_skinny_cfg(int epi, const GemmArgs &a, hipStream_t s) {
 template <class T>
 hipError_t launch_skinny(int epi, const GemmArgs &a, hipStream_t s) {
   if (epi == EPI_GEGLU || epi == EPI_GEGLU_KEEP) {
+    // Inference GeGLU on 32-column tiles (16 outputs each) while their grid
+    // fits one workgroup per CU (MI355X: 256): twice the workgroups of the
+    // 64-column tiles, a third less operand traffic per workgroup (cfg5
+    // 0.809 -> 0.789 ms; at 112 rows, 288 workgroups, 0.932 -> 0.951 ms).
+    if (a.M <= 128 && epi == EPI_GEGLU && (a.N / 32) * ((a.M + 31) / 32) <= 256)
+      return launch_skinny_cfg<T, 1, 1, 8>(epi, a, s);
     if (a.M <= 128) return launch_skinny_cfg<T, 1, 2, 8>(epi, a, s);
     return launch_skinny_cfg<T, 2, 2, 8>(epi, a, s);
   }
