@@ -446,7 +446,8 @@ hipError_t launch_cfg_one(const GemmArgs &a, hipStream_t s, int splits = 1) {
 //     operand is used by one wave only, so LDS staging buys nothing),
 //     prefetching the next group while the current one is multiplied.
 //   * The waves' partial tiles are summed through LDS in a fixed order, so
-//     results do not depend on timing. (Splitting K across workgroups would
+//     results do not depend on timing, by the threads that store the
+//     result (one barrier). (Splitting K across workgroups would
 //     need a device-scope release/acquire per workgroup, which on gfx950 is
 //     an L2 writeback + invalidate and costs more than it saves.)
 // Operand layout: in load j of a group, lane l reads the 16 bytes of row
@@ -722,9 +723,11 @@ hipError_t launch_skinny_cfg(int epi, const GemmArgs &a, hipStream_t s) {
   return hipGetLastError();
 }
 
-// 32-row tiles up to 128 rows (more workgroups for the few rows: cfg5
-// 1.10 -> 0.92 ms, cfg2 1.18 -> 1.06 ms against 64-row tiles), 64-row tiles
-// above; 32 columns (64 for GeGLU's value/gate pairs), 8 waves.
+// Tile choice, 8 waves: 32-row tiles up to 128 rows while the grid fits one
+// workgroup per CU (more workgroups for the few rows: cfg5 1.10 -> 0.92 ms,
+// cfg2 1.18 -> 1.06 ms against 64-row tiles everywhere), 64-row tiles
+// otherwise; 32 columns, or for GeGLU 32 (16 value + 16 gate rows) or 64
+// (32 + 32; training's kept pre-activation always).
 template <class T>
 hipError_t launch_skinny(int epi, const GemmArgs &a, hipStream_t s) {
   if (epi == EPI_GEGLU || epi == EPI_GEGLU_KEEP) {
