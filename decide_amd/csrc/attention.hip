@@ -225,8 +225,9 @@ __device__ __forceinline__ void stage_store(const Staging<T, R> &st, char *sK, c
       const uint32_t vb[4] = {v1.x, v1.y, v1.z, v1.w};
 #pragma unroll
       for (int w = 0; w < 4; w++) {
-        *(uint32_t *)(sV + (8 * g + 2 * w) * ROWV + 4 * pw) = (va[w] & 0xffffu) | (vb[w] << 16);
-        *(uint32_t *)(sV + (8 * g + 2 * w + 1) * ROWV + 4 * pw) = (va[w] >> 16) | (vb[w] & 0xffff0000u);
+        // Byte permutes: (va & 0xffff) | (vb << 16) and (va >> 16) | (vb & 0xffff0000).
+        *(uint32_t *)(sV + (8 * g + 2 * w) * ROWV + 4 * pw) = __builtin_amdgcn_perm(vb[w], va[w], 0x05040100u);
+        *(uint32_t *)(sV + (8 * g + 2 * w + 1) * ROWV + 4 * pw) = __builtin_amdgcn_perm(vb[w], va[w], 0x07060302u);
       }
     }
   } else {
