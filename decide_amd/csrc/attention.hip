@@ -459,13 +459,11 @@ __global__ __launch_bounds__(64 * QW) __attribute__((amdgpu_waves_per_eu(QT == 1
     if (mycode != 0) {
       // S^T = K . Q^T per query tile for 64 keys (two 32x32 tiles); a K
       // fragment read from LDS feeds every query tile that needs its half.
+      // A half with no allowed pair (class 0) is neither computed nor read
+      // below; the others start from a zero accumulator operand (no
+      // per-tile register initialisation).
       f32x16 sT[QT][2];
-#pragma unroll
-      for (int t = 0; t < QT; t++)
-#pragma unroll
-        for (int i = 0; i < 2; i++)
-#pragma unroll
-          for (int e = 0; e < 16; e++) sT[t][i][e] = hcls[t][i] ? 0.0f : -INFINITY;
+      const f32x16 zero = {};
 #pragma unroll
       for (int i = 0; i < 2; i++) {
         int any = 0;
@@ -478,7 +476,7 @@ __global__ __launch_bounds__(64 * QW) __attribute__((amdgpu_waves_per_eu(QT == 1
           frag kf = *(const frag *)(sKb + (i * 32 + lr) * ROWK + kof);
 #pragma unroll
           for (int t = 0; t < QT; t++)
-            if (hcls[t][i]) sT[t][i] = MF::mma(kf, qf[t][ks], sT[t][i]);
+            if (hcls[t][i]) sT[t][i] = MF::mma(kf, qf[t][ks], ks == 0 ? zero : sT[t][i]);
         }
       }
 
@@ -511,9 +509,11 @@ __global__ __launch_bounds__(64 * QW) __attribute__((amdgpu_waves_per_eu(QT == 1
         }
         float mx = -INFINITY;
 #pragma unroll
-        for (int i = 0; i < 2; i++)
+        for (int i = 0; i < 2; i++) {
+          if (hcls[t][i] == 0) continue;
 #pragma unroll
           for (int e = 0; e < 16; e++) mx = fmaxf(mx, sT[t][i][e]);
+        }
         mx = fmaxf(mx, __shfl_xor(mx, 32));
         const float m_new = fmaxf(m_run[t], mx);
         const float m_use = m_new == -INFINITY ? 0.0f : m_new;
