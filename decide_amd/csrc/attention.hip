@@ -121,8 +121,10 @@ __device__ __forceinline__ void stage_load(Staging<T, R> &st, const T *qkv, int 
     for (int j = 0; j < R; j++) {  // K: key = it / 4, chunk c = it % 4 (elements 8c..8c+7 and 32+8c..)
       const int it = tid + NT * j, key = it >> 2, c = it & 3;
       st.valid |= (k0 + key < n ? 1u : 0u) << j;
-      const size_t tok = (size_t)(base + min(k0 + key, n - 1));
-      const T *row = qkv + tok * ld + H + head * D;
+      // Token indices are non-negative: zero-extended, the row offset is one
+      // 32 x 32 -> 64-bit multiply-add.
+      const size_t tok = (unsigned)(base + min(k0 + key, n - 1));
+      const T *row = qkv + tok * (unsigned)ld + H + head * D;
       st.k_lo[j] = *(const uint4 *)(row + 8 * c);
       st.k_hi[j] = *(const uint4 *)(row + 32 + 8 * c);
       const size_t p = (size_t)(ki.pk[j] & 0xffff);
@@ -135,8 +137,9 @@ __device__ __forceinline__ void stage_load(Staging<T, R> &st, const T *qkv, int 
     for (int j = 0; j < R; j++) {  // V: key pair p = it % 32, d group g = it / 32
       const int it = tid + NT * j, p = it & 31, g = it >> 5;
       const int k = k0 + 2 * p;
-      st.v0[j] = *(const uint4 *)(qkv + (size_t)(base + min(k, n - 1)) * ld + 2 * H + head * D + 8 * g);
-      st.v1[j] = *(const uint4 *)(qkv + (size_t)(base + min(k + 1, n - 1)) * ld + 2 * H + head * D + 8 * g);
+      st.v0[j] = *(const uint4 *)(qkv + (size_t)(unsigned)(base + min(k, n - 1)) * (unsigned)ld + 2 * H + head * D + 8 * g);
+      st.v1[j] = *(const uint4 *)(qkv + (size_t)(unsigned)(base + min(k + 1, n - 1)) * (unsigned)ld + 2 * H + head * D +
+                                  8 * g);
       st.valid |= ((k < n ? 1u : 0u) << (8 + j)) | ((k + 1 < n ? 1u : 0u) << (16 + j));
     }
   } else {
