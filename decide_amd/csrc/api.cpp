@@ -333,14 +333,17 @@ int enqueue_prologue(dn_ctx *c, const Pass &p, float *cur, void *xn0, float *emb
   const Config &g = c->cfg;
   const Workspace &w = p.w;
   hipStream_t s = p.s;
-  HIPCHK(c, "token_info", launch_token_info(p.pos, p.opt, w.kinfo, w.T, (int *)c->err_flag.p, s));
-  HIPCHK(c, "chunk_summary", launch_chunk_summary(w.kinfo, w.chunk_desc, w.chunks, w.nchunks, s));
+  HIPCHK(c, "token_chunk", launch_token_chunk(p.pos, p.opt, w.chunk_desc, w.nchunks, w.kinfo, w.chunks,
+                                              (int *)c->err_flag.p, s));
   const size_t nw = (size_t)w.nwork;
-  // Local layers use the ATTN_QUERIES items; global layers too, or the
-  // ATTN_QUERIES_GLOBAL ones in the two-stream forward.
-  for (int sl = p.wide_global ? 1 : 0; sl < 2; sl++)
-    HIPCHK(c, "tile_codes", launch_tile_codes(w.chunks, w.work, w.seq_len, w.chunk_off, w.nwork, sl, g.half_window,
-                                              w.codes + sl * nw * ATTN_MAXKT, w.first + sl * nw, s));
+  // Local layers use the ATTN_QUERIES items; global layers too (both types
+  // in one launch), or the ATTN_QUERIES_GLOBAL ones in the two-stream forward.
+  if (p.wide_global)
+    HIPCHK(c, "tile_codes", launch_tile_codes(w.chunks, w.work, w.seq_len, w.chunk_off, w.nwork, 1, g.half_window,
+                                              w.codes + nw * ATTN_MAXKT, w.first + nw, s));
+  else
+    HIPCHK(c, "tile_codes", launch_tile_codes(w.chunks, w.work, w.seq_len, w.chunk_off, w.nwork, -1, g.half_window,
+                                              w.codes, w.first, s));
   if (p.wide_global)
     HIPCHK(c, "tile_codes", launch_tile_codes(w.chunks, w.work2, w.seq_len, w.chunk_off, w.nwork2, 0, g.half_window,
                                               w.codes2, w.first2, s, ATTN_WAVES * ATTN_QT_GLOBAL));

@@ -712,6 +712,14 @@ __global__ __launch_bounds__(64) void tile_codes_kernel(const ChunkInfo *chunks,
   static_assert(NC <= 8, "32-bit codes");
   __shared__ int s_first;
   const int wi = blockIdx.x, tid = threadIdx.x;
+  // sliding < 0: both layer types in one launch, blockIdx.y = 1 for the
+  // sliding-window one, its codes and first tiles one section (gridDim.x
+  // items) after the global ones.
+  if (sliding < 0) {
+    sliding = blockIdx.y;
+    codes += (size_t)sliding * gridDim.x * ATTN_MAXKT;
+    first += sliding * gridDim.x;
+  }
   const int4 wk = work[wi];
   const int s = wk.x, q0 = wk.y;
   const int n = seq_len[s], cbase = chunk_off[s];
@@ -741,42 +749,48 @@ __global__ __launch_bounds__(64) void tile_codes_kernel(const ChunkInfo *chunks,
   if (tid == 0) first[wi] = s_first;
 }
 
-// Packs (option id + 1, position) per token; positions outside [0, 65535] or
-// option ids outside [-1, 32766] set bit 4 of the error flag (the packed
-// form and the per-position RoPE tables cover that range only).
-__global__ void token_info_kernel(const int *pos, const int *opt, int *kinfo, int T, int *err_flag) {
-  const int t = blockIdx.x * blockDim.x + threadIdx.x;
-  if (t >= T) return;
-  const int o = opt ? opt[t] : -1, p = pos[t];
-  if (p < 0 || p > 65535 || o < -1 || o > 32766) atomicOr(err_flag, 4);
-  kinfo[t] = ((o + 1) << 16) | (p & 0xffff);
-}
 
-__global__ void chunk_summary_kernel(const int *kinfo, const int4 *desc, ChunkInfo *out, int nchunks) {
-  const int c = blockIdx.x * blockDim.x + threadIdx.x;
-  if (c >= nchunks) return;
-  const int4 d = desc[c];  // (first token, length)
-  ChunkInfo ci = {0x7fffffff, -0x7fffffff, 0x7fffffff, -1, 0, 0, d.y, 0};
-  int kv[32];  // the chunk's (<= 32) token infos, all loads issued before the first use
-#pragma unroll
-  for (int i = 0; i < 32; i++) kv[i] = i < d.y ? kinfo[d.x + i] : 0;
-#pragma unroll
-  for (int i = 0; i < 32; i++) {
-    if (i >= d.y) break;
-    const int v = kv[i];
-    const int o = (v >> 16) - 1, p = v & 0xffff;
-    ci.pmin = min(ci.pmin, p);
-    ci.pmax = max(ci.pmax, p);
-    if (o < 0) {
-      ci.nprefix++;
+// Token info and 32-token chunk summaries in one launch: 32 lanes per chunk
+// (desc = (first token, length)), lane i packing token i's info
+// (((opt+1) << 16) | pos; a position outside [0, 65535] or an option id
+// outside [-1, 32766] sets bit 4 of the error flag, the packed form and the
+// per-position RoPE tables covering that range only) and the chunk's summary
+// reduced over the lanes (integer min / max / counts, exact in any order).
+__global__ __launch_bounds__(256) void token_chunk_kernel(const int *pos, const int *opt, const int4 *desc,
+                                                          int nchunks, int *kinfo, ChunkInfo *out, int *err_flag) {
+  const int c = (blockIdx.x * blockDim.x + threadIdx.x) >> 5, i = threadIdx.x & 31;
+  if (c >= nchunks) return;  // whole 32-lane groups leave together
+  const int4 d = desc[c];
+  int pmin = 0x7fffffff, pmax = -0x7fffffff, omin = 0x7fffffff, omax = -1, npre = 0, nopt = 0;
+  if (i < d.y) {
+    const int t = d.x + i;
+    const int o = opt ? opt[t] : -1, p = pos[t];
+    if (p < 0 || p > 65535 || o < -1 || o > 32766) atomicOr(err_flag, 4);
+    const int v = ((o + 1) << 16) | (p & 0xffff);
+    kinfo[t] = v;
+    const int ov = (v >> 16) - 1, pv = v & 0xffff;
+    pmin = pv;
+    pmax = pv;
+    if (ov < 0) {
+      npre = 1;
     } else {
-      ci.nopt++;
-      ci.omin = min(ci.omin, o);
-      ci.omax = max(ci.omax, o);
+      nopt = 1;
+      omin = ov;
+      omax = ov;
     }
   }
-  out[c] = ci;
+#pragma unroll
+  for (int m = 16; m > 0; m >>= 1) {
+    pmin = min(pmin, __shfl_xor(pmin, m, 32));
+    pmax = max(pmax, __shfl_xor(pmax, m, 32));
+    omin = min(omin, __shfl_xor(omin, m, 32));
+    omax = max(omax, __shfl_xor(omax, m, 32));
+    npre += __shfl_xor(npre, m, 32);
+    nopt += __shfl_xor(nopt, m, 32);
+  }
+  if (i == 0) out[c] = ChunkInfo{pmin, pmax, omin, omax, npre, nopt, d.y, 0};
 }
+
 
 // ---------------------------------------------------------------------------
 // Attention backward: the reference's attnBwd (backward.go:117-159) with the
@@ -1467,28 +1481,27 @@ hipError_t launch_tile_codes(const ChunkInfo *chunks, const int4 *work, const in
                              int nwork, int sliding, int half_window, uint32_t *codes, int *first, hipStream_t s,
                              int nc) {
   if (nwork <= 0) return hipSuccess;
+  const dim3 grid(nwork, sliding < 0 ? 2 : 1);
   if (nc == ATTN_WAVES * ATTN_QT)
-    hipLaunchKernelGGL(tile_codes_kernel<ATTN_WAVES * ATTN_QT>, dim3(nwork), dim3(64), 0, s, chunks, work, seq_len,
+    hipLaunchKernelGGL(tile_codes_kernel<ATTN_WAVES * ATTN_QT>, grid, dim3(64), 0, s, chunks, work, seq_len,
                        chunk_off, sliding, half_window, codes, first);
   else if (nc == ATTN_WAVES * ATTN_QT_GLOBAL)
-    hipLaunchKernelGGL(tile_codes_kernel<ATTN_WAVES * ATTN_QT_GLOBAL>, dim3(nwork), dim3(64), 0, s, chunks, work,
+    hipLaunchKernelGGL(tile_codes_kernel<ATTN_WAVES * ATTN_QT_GLOBAL>, grid, dim3(64), 0, s, chunks, work,
                        seq_len, chunk_off, sliding, half_window, codes, first);
   else
     return hipErrorInvalidValue;
   return hipGetLastError();
 }
 
-hipError_t launch_token_info(const int *pos, const int *opt, int *kinfo, int T, int *err_flag, hipStream_t s) {
-  if (T <= 0) return hipSuccess;
-  hipLaunchKernelGGL(token_info_kernel, dim3((T + 255) / 256), dim3(256), 0, s, pos, opt, kinfo, T, err_flag);
+
+hipError_t launch_token_chunk(const int *pos, const int *opt, const int4 *desc, int nchunks, int *kinfo,
+                              ChunkInfo *out, int *err_flag, hipStream_t s) {
+  if (nchunks <= 0) return hipSuccess;
+  hipLaunchKernelGGL(token_chunk_kernel, dim3((nchunks + 7) / 8), dim3(256), 0, s, pos, opt, desc, nchunks, kinfo,
+                     out, err_flag);
   return hipGetLastError();
 }
 
-hipError_t launch_chunk_summary(const int *kinfo, const int4 *desc, ChunkInfo *out, int nchunks, hipStream_t s) {
-  if (nchunks <= 0) return hipSuccess;
-  hipLaunchKernelGGL(chunk_summary_kernel, dim3((nchunks + 127) / 128), dim3(128), 0, s, kinfo, desc, out, nchunks);
-  return hipGetLastError();
-}
 
 hipError_t launch_attention_bwd(int precision, const AttnBwdArgs &a, hipStream_t s) {
   if (a.nwork <= 0) return hipSuccess;

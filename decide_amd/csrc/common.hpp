@@ -259,12 +259,20 @@ struct AttnBwdArgs {
 };
 hipError_t launch_attention_bwd(int precision, const AttnBwdArgs &a, hipStream_t s);
 
-// Tile classes of work items of 32 * nc queries (nc = ATTN_WAVES * QT).
+// Tile classes of work items of 32 * nc queries (nc = ATTN_WAVES * QT);
+// sliding 0: global layers, 1: sliding-window layers, -1: both in one launch
+// (the sliding-window codes and first tiles one section of nwork items after
+// the global ones).
 hipError_t launch_tile_codes(const ChunkInfo *chunks, const int4 *work, const int *seq_len, const int *chunk_off,
                              int nwork, int sliding, int half_window, uint32_t *codes, int *first, hipStream_t s,
                              int nc = ATTN_WAVES * ATTN_QT);
-hipError_t launch_chunk_summary(const int *kinfo, const int4 *chunk_desc, ChunkInfo *out, int nchunks, hipStream_t s);
-hipError_t launch_token_info(const int *pos, const int *opt, int *kinfo, int T, int *err_flag, hipStream_t s);
+// Per token: kinfo = ((opt+1) << 16) | pos (positions outside [0, 65535] or
+// option ids outside [-1, 32766] set bit 4 of err_flag: the packed form and
+// the per-position RoPE tables cover that range only); per 32-token chunk
+// (chunk_desc = (first token, length); the chunks cover every token): its
+// ChunkInfo summary.
+hipError_t launch_token_chunk(const int *pos, const int *opt, const int4 *chunk_desc, int nchunks, int *kinfo,
+                              ChunkInfo *out, int *err_flag, hipStream_t s);
 hipError_t launch_rope_tables(const int *pos, int T, const double *inv_g, const double *inv_l, float *cos_g,
                               float *sin_g, float *cos_l, float *sin_l, hipStream_t s);
 // LayerNorm launchers; mean / rstd (optional, [rows]) receive the row statistics.
