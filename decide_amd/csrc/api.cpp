@@ -333,8 +333,13 @@ int enqueue_prologue(dn_ctx *c, const Pass &p, float *cur, void *xn0, float *emb
   const Config &g = c->cfg;
   const Workspace &w = p.w;
   hipStream_t s = p.s;
-  HIPCHK(c, "token_chunk", launch_token_chunk(p.pos, p.opt, w.chunk_desc, w.nchunks, w.kinfo, w.chunks,
-                                              (int *)c->err_flag.p, s));
+  // Token info, chunk summaries and the embedding gather + emb norm in one
+  // launch, then the tile classes (which need the chunk summaries).
+  HIPCHK(c, "prologue",
+         launch_prologue(g.precision, p.pos, p.opt, w.chunk_desc, w.nchunks, w.kinfo, w.chunks, p.ids, w.T,
+                         (const float *)W(c, "model.embeddings.tok_embeddings.weight"), g.vocab,
+                         (const float *)W(c, "model.embeddings.norm.weight"), g.eps, g.hidden, cur, xn0,
+                         (int *)c->err_flag.p, s, emb_mean, emb_rstd));
   const size_t nw = (size_t)w.nwork;
   // Local layers use the ATTN_QUERIES items; global layers too (both types
   // in one launch), or the ATTN_QUERIES_GLOBAL ones in the two-stream forward.
@@ -347,10 +352,6 @@ int enqueue_prologue(dn_ctx *c, const Pass &p, float *cur, void *xn0, float *emb
   if (p.wide_global)
     HIPCHK(c, "tile_codes", launch_tile_codes(w.chunks, w.work2, w.seq_len, w.chunk_off, w.nwork2, 0, g.half_window,
                                               w.codes2, w.first2, s, ATTN_WAVES * ATTN_QT_GLOBAL));
-  HIPCHK(c, "embed_ln",
-         launch_embed_ln(g.precision, p.ids, w.T, (const float *)W(c, "model.embeddings.tok_embeddings.weight"),
-                         g.vocab, (const float *)W(c, "model.embeddings.norm.weight"), g.eps, g.hidden, cur, xn0,
-                         (int *)c->err_flag.p, s, emb_mean, emb_rstd));
   return DN_OK;
 }
 

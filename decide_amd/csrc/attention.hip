@@ -750,46 +750,6 @@ __global__ __launch_bounds__(64) void tile_codes_kernel(const ChunkInfo *chunks,
 }
 
 
-// Token info and 32-token chunk summaries in one launch: 32 lanes per chunk
-// (desc = (first token, length)), lane i packing token i's info
-// (((opt+1) << 16) | pos; a position outside [0, 65535] or an option id
-// outside [-1, 32766] sets bit 4 of the error flag, the packed form and the
-// per-position RoPE tables covering that range only) and the chunk's summary
-// reduced over the lanes (integer min / max / counts, exact in any order).
-__global__ __launch_bounds__(256) void token_chunk_kernel(const int *pos, const int *opt, const int4 *desc,
-                                                          int nchunks, int *kinfo, ChunkInfo *out, int *err_flag) {
-  const int c = (blockIdx.x * blockDim.x + threadIdx.x) >> 5, i = threadIdx.x & 31;
-  if (c >= nchunks) return;  // whole 32-lane groups leave together
-  const int4 d = desc[c];
-  int pmin = 0x7fffffff, pmax = -0x7fffffff, omin = 0x7fffffff, omax = -1, npre = 0, nopt = 0;
-  if (i < d.y) {
-    const int t = d.x + i;
-    const int o = opt ? opt[t] : -1, p = pos[t];
-    if (p < 0 || p > 65535 || o < -1 || o > 32766) atomicOr(err_flag, 4);
-    const int v = ((o + 1) << 16) | (p & 0xffff);
-    kinfo[t] = v;
-    const int ov = (v >> 16) - 1, pv = v & 0xffff;
-    pmin = pv;
-    pmax = pv;
-    if (ov < 0) {
-      npre = 1;
-    } else {
-      nopt = 1;
-      omin = ov;
-      omax = ov;
-    }
-  }
-#pragma unroll
-  for (int m = 16; m > 0; m >>= 1) {
-    pmin = min(pmin, __shfl_xor(pmin, m, 32));
-    pmax = max(pmax, __shfl_xor(pmax, m, 32));
-    omin = min(omin, __shfl_xor(omin, m, 32));
-    omax = max(omax, __shfl_xor(omax, m, 32));
-    npre += __shfl_xor(npre, m, 32);
-    nopt += __shfl_xor(nopt, m, 32);
-  }
-  if (i == 0) out[c] = ChunkInfo{pmin, pmax, omin, omax, npre, nopt, d.y, 0};
-}
 
 
 // ---------------------------------------------------------------------------
@@ -1494,13 +1454,6 @@ hipError_t launch_tile_codes(const ChunkInfo *chunks, const int4 *work, const in
 }
 
 
-hipError_t launch_token_chunk(const int *pos, const int *opt, const int4 *desc, int nchunks, int *kinfo,
-                              ChunkInfo *out, int *err_flag, hipStream_t s) {
-  if (nchunks <= 0) return hipSuccess;
-  hipLaunchKernelGGL(token_chunk_kernel, dim3((nchunks + 7) / 8), dim3(256), 0, s, pos, opt, desc, nchunks, kinfo,
-                     out, err_flag);
-  return hipGetLastError();
-}
 
 
 hipError_t launch_attention_bwd(int precision, const AttnBwdArgs &a, hipStream_t s) {

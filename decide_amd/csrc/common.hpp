@@ -266,19 +266,21 @@ hipError_t launch_attention_bwd(int precision, const AttnBwdArgs &a, hipStream_t
 hipError_t launch_tile_codes(const ChunkInfo *chunks, const int4 *work, const int *seq_len, const int *chunk_off,
                              int nwork, int sliding, int half_window, uint32_t *codes, int *first, hipStream_t s,
                              int nc = ATTN_WAVES * ATTN_QT);
-// Per token: kinfo = ((opt+1) << 16) | pos (positions outside [0, 65535] or
-// option ids outside [-1, 32766] set bit 4 of err_flag: the packed form and
-// the per-position RoPE tables cover that range only); per 32-token chunk
-// (chunk_desc = (first token, length); the chunks cover every token): its
-// ChunkInfo summary.
-hipError_t launch_token_chunk(const int *pos, const int *opt, const int4 *chunk_desc, int nchunks, int *kinfo,
-                              ChunkInfo *out, int *err_flag, hipStream_t s);
 hipError_t launch_rope_tables(const int *pos, int T, const double *inv_g, const double *inv_l, float *cos_g,
                               float *sin_g, float *cos_l, float *sin_l, hipStream_t s);
+// The forward's prologue in one launch: per token kinfo = ((opt+1) << 16) |
+// pos (a position outside [0, 65535] or an option id outside [-1, 32766]
+// sets bit 4 of err: the packed form and the per-position RoPE tables cover
+// that range only); per 32-token chunk (chunk_desc = (first token, length),
+// the chunks covering every token) its ChunkInfo summary; and the embedding
+// gather (an id outside [0, vocab) sets bit 1 of err and reads row 0) + emb
+// norm into h (fp32) and xn (operand type), with the row statistics in
+// mean / rstd when given (training).
+hipError_t launch_prologue(int precision, const int *pos, const int *opt, const int4 *chunk_desc, int nchunks,
+                           int *kinfo, ChunkInfo *chunks, const int *ids, int Tn, const float *tok, int vocab,
+                           const float *w, float eps, int H, float *h, void *xn, int *err, hipStream_t s,
+                           float *mean = nullptr, float *rstd = nullptr);
 // LayerNorm launchers; mean / rstd (optional, [rows]) receive the row statistics.
-hipError_t launch_embed_ln(int precision, const int *ids, int T, const float *tok, int vocab, const float *w, float eps,
-                           int H, float *h, void *xn, int *err_flag, hipStream_t s, float *mean = nullptr,
-                           float *rstd = nullptr);
 hipError_t launch_ln(int precision, const float *x, int rows, int H, const float *w, float eps, void *y, hipStream_t s,
                      float *mean = nullptr, float *rstd = nullptr);
 struct HeadArgs {

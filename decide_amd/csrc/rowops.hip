@@ -92,15 +92,58 @@ __device__ __forceinline__ void store4<bf16>(bf16 *p, float4 v) {
   *(bf16x4 *)p = o;
 }
 
+// Token info and 32-token chunk summaries in one launch: 32 lanes per chunk
+// (desc = (first token, length)), lane i packing token i's info
+// (((opt+1) << 16) | pos; a position outside [0, 65535] or an option id
+// outside [-1, 32766] sets bit 4 of the error flag, the packed form and the
+// per-position RoPE tables covering that range only) and the chunk's summary
+// reduced over the lanes (integer min / max / counts, exact in any order).
+// Chunk c = (256-thread block b) * 8 + threadIdx.x / 32.
+__device__ __forceinline__ void token_chunk(int b, const int *pos, const int *opt, const int4 *desc, int nchunks,
+                                            int *kinfo, ChunkInfo *out, int *err_flag) {
+  const int c = (b * 256 + (int)threadIdx.x) >> 5, i = threadIdx.x & 31;
+  if (c >= nchunks) return;  // whole 32-lane groups leave together
+  const int4 d = desc[c];
+  int pmin = 0x7fffffff, pmax = -0x7fffffff, omin = 0x7fffffff, omax = -1, npre = 0, nopt = 0;
+  if (i < d.y) {
+    const int t = d.x + i;
+    const int o = opt ? opt[t] : -1, p = pos[t];
+    if (p < 0 || p > 65535 || o < -1 || o > 32766) atomicOr(err_flag, 4);
+    const int v = ((o + 1) << 16) | (p & 0xffff);
+    kinfo[t] = v;
+    const int ov = (v >> 16) - 1, pv = v & 0xffff;
+    pmin = pv;
+    pmax = pv;
+    if (ov < 0) {
+      npre = 1;
+    } else {
+      nopt = 1;
+      omin = ov;
+      omax = ov;
+    }
+  }
+#pragma unroll
+  for (int m = 16; m > 0; m >>= 1) {
+    pmin = min(pmin, __shfl_xor(pmin, m, 32));
+    pmax = max(pmax, __shfl_xor(pmax, m, 32));
+    omin = min(omin, __shfl_xor(omin, m, 32));
+    omax = max(omax, __shfl_xor(omax, m, 32));
+    npre += __shfl_xor(npre, m, 32);
+    nopt += __shfl_xor(nopt, m, 32);
+  }
+  if (i == 0) out[c] = ChunkInfo{pmin, pmax, omin, omax, npre, nopt, d.y, 0};
+}
+
 // Embedding gather (forward.go:204-209) + emb norm (forward.go:220). Writes the
 // fp32 residual stream h and its GEMM-operand copy xn (layer 0 has no
 // attn_norm, so its QKV input is h itself).
+// Rows 4b .. 4b+3 (256-thread block b), one wave per row.
 template <class T>
-__global__ __launch_bounds__(256) void embed_ln_kernel(const int *ids, int Tn, const float *tok, int vocab,
-                                                       const float *w, float eps, int dim, float *h, T *xn,
-                                                       int *err, float *mean_out, float *rstd_out) {
+__device__ __forceinline__ void embed_ln(int b, const int *ids, int Tn, const float *tok, int vocab, const float *w,
+                                         float eps, int dim, float *h, T *xn, int *err, float *mean_out,
+                                         float *rstd_out) {
   const int lane = threadIdx.x & 63;
-  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int t = b * 4 + (threadIdx.x >> 6);
   if (t >= Tn) return;
   int id = ids[t];
   if (id < 0 || id >= vocab) {
@@ -136,6 +179,23 @@ __global__ __launch_bounds__(256) void embed_ln_kernel(const int *ids, int Tn, c
       store4<T>(xn + (size_t)t * dim + 4 * (lane + 64 * j), y);
     }
 }
+
+// The forward's prologue in one launch: blocks [0, nb_tc) pack the token info
+// and summarise the 32-token chunks, the rest gather the embeddings and
+// apply the embedding norm (independent work, one launch boundary fewer).
+template <class T>
+__global__ __launch_bounds__(256) void prologue_kernel(const int *pos, const int *opt, const int4 *desc, int nchunks,
+                                                       int *kinfo, ChunkInfo *chunks, int nb_tc, const int *ids,
+                                                       int Tn, const float *tok, int vocab, const float *w,
+                                                       float eps, int dim, float *h, T *xn, int *err,
+                                                       float *mean_out, float *rstd_out) {
+  const int b = blockIdx.x;
+  if (b < nb_tc)
+    token_chunk(b, pos, opt, desc, nchunks, kinfo, chunks, err);
+  else
+    embed_ln<T>(b - nb_tc, ids, Tn, tok, vocab, w, eps, dim, h, xn, err, mean_out, rstd_out);
+}
+
 
 // Bias-free LayerNorm of the fp32 residual stream into the GEMM operand type
 // (attn_norm forward.go:289-294, mlp_norm forward.go:324).
@@ -346,17 +406,20 @@ __global__ void pack_kernel(const float *src, int trans, int rows, int cols, int
 
 }  // namespace
 
-hipError_t launch_embed_ln(int precision, const int *ids, int Tn, const float *tok, int vocab, const float *w,
-                           float eps, int H, float *h, void *xn, int *err, hipStream_t s, float *mean,
-                           float *rstd) {
+
+hipError_t launch_prologue(int precision, const int *pos, const int *opt, const int4 *chunk_desc, int nchunks,
+                           int *kinfo, ChunkInfo *chunks, const int *ids, int Tn, const float *tok, int vocab,
+                           const float *w, float eps, int H, float *h, void *xn, int *err, hipStream_t s,
+                           float *mean, float *rstd) {
   if (Tn <= 0) return hipSuccess;
-  dim3 grid((Tn + 3) / 4), block(256);
+  const int nb_tc = (nchunks + 7) / 8, nb_emb = (Tn + 3) / 4;
+  dim3 grid(nb_tc + nb_emb), block(256);
   if (precision == 1)
-    hipLaunchKernelGGL(embed_ln_kernel<bf16>, grid, block, 0, s, ids, Tn, tok, vocab, w, eps, H, h, (bf16 *)xn, err,
-                       mean, rstd);
+    hipLaunchKernelGGL(prologue_kernel<bf16>, grid, block, 0, s, pos, opt, chunk_desc, nchunks, kinfo, chunks, nb_tc,
+                       ids, Tn, tok, vocab, w, eps, H, h, (bf16 *)xn, err, mean, rstd);
   else
-    hipLaunchKernelGGL(embed_ln_kernel<float>, grid, block, 0, s, ids, Tn, tok, vocab, w, eps, H, h, (float *)xn,
-                       err, mean, rstd);
+    hipLaunchKernelGGL(prologue_kernel<float>, grid, block, 0, s, pos, opt, chunk_desc, nchunks, kinfo, chunks,
+                       nb_tc, ids, Tn, tok, vocab, w, eps, H, h, (float *)xn, err, mean, rstd);
   return hipGetLastError();
 }
 
