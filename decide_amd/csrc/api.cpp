@@ -254,6 +254,9 @@ int ctx_workspace(dn_ctx *c, int nseq, const int32_t *seq_len, int R, Workspace 
   HIPCHK(c, "hipMalloc", ensure(c->kinfo, sizeof(int) * T));
   HIPCHK(c, "hipMalloc", ensure(c->head_s1, sizeof(float) * (size_t)std::max(R, 1) * H));
   HIPCHK(c, "hipMalloc", ensure(c->head_d, sizeof(float) * (size_t)std::max(R, 1) * (H / 2)));
+  if (T <= (size_t)kSmallSplitMaxTokens)
+    HIPCHK(c, "hipMalloc", ensure(c->smallpart, sizeof(float) * kSmallSplitParts * T * H));
+  o.part = T <= (size_t)kSmallSplitMaxTokens ? (float *)c->smallpart.p : nullptr;
   o.h = (float *)c->h.p;
   o.xn = c->xn.p;
   o.qkv = c->qkv.p;
@@ -355,6 +358,17 @@ int enqueue_prologue(dn_ctx *c, const Pass &p, float *cur, void *xn0, float *emb
   return DN_OK;
 }
 
+// Split-K parts of a small batch's residual GEMM (32 x 32 tiles): the most,
+// among the counts launch_ln_parts sums, that keep tiles x parts within
+// kSplitMaxWorkgroups and give every part a whole number of K groups (1: no
+// split).
+int small_split_parts(int precision, int T, int N, int K) {
+  const int tiles = (N / 32) * ((T + 31) / 32), kt = precision == DN_PRECISION_BF16 ? 64 : 32;
+  for (int p : {6, 4, 3, 2})
+    if (p <= kSmallSplitParts && tiles * p <= kSplitMaxWorkgroups && K % (p * kt) == 0) return p;
+  return 1;
+}
+
 // A projection GEMM of the model: the MFMA kernels, or the any-shape kernel
 // for geometries they do not tile.
 hipError_t layer_gemm(const Config &g, int epi, const GemmArgs &a, hipStream_t s) {
@@ -367,9 +381,14 @@ hipError_t layer_gemm(const Config &g, int epi, const GemmArgs &a, hipStream_t s
 // 0 (the embedding output; later layers normalise `in` into the workspace).
 // S (training) receives the layer's activations; ev brackets the five probed
 // launches. attn_only: stop after attention (enqueue_rows_tail finishes the
-// layer for the head's rows).
+// layer for the head's rows). Small inference batches (w.part set, the
+// residual stream updated in place): Wo runs split over K and mlp_norm sums
+// its parts into the residual; in_parts > 0: `in` still lacks the previous
+// layer's MlpWo parts, which attn_norm adds; mo_parts non-null: this layer's
+// MlpWo may leave its parts for the next layer's attn_norm the same way and
+// stores their count (0: the residual stream is complete).
 int enqueue_layer(dn_ctx *c, const Pass &p, int l, float *in, float *h1, float *out, void *x1, LayerSave *S,
-                  hipEvent_t *ev, bool attn_only = false) {
+                  hipEvent_t *ev, bool attn_only = false, int in_parts = 0, int *mo_parts = nullptr) {
   const Config &g = c->cfg;
   const int H = g.hidden, I = g.inter, prec = g.precision;
   const Workspace &w = p.w;
@@ -377,11 +396,16 @@ int enqueue_layer(dn_ctx *c, const Pass &p, int l, float *in, float *h1, float *
   hipStream_t s = p.s;
   const std::string pf = layer_prefix(l);
   const bool sliding = g.sliding[l] != 0;
+  const bool split = w.part && !S && !g.generic && h1 == in && out == in;
   if (l > 0) {
     x1 = S ? S->n1.p : w.xn;
-    HIPCHK(c, "ln(attn_norm)",
-           launch_ln(prec, in, T, H, (const float *)W(c, pf + "attn_norm.weight"), g.eps, x1, s,
-                     S ? (float *)S->mean1.p : nullptr, S ? (float *)S->rstd1.p : nullptr));
+    if (in_parts > 0 && split)
+      HIPCHK(c, "ln(attn_norm)", launch_ln_parts(prec, in, w.part, in_parts, T, H,
+                                                 (const float *)W(c, pf + "attn_norm.weight"), g.eps, x1, s));
+    else
+      HIPCHK(c, "ln(attn_norm)",
+             launch_ln(prec, in, T, H, (const float *)W(c, pf + "attn_norm.weight"), g.eps, x1, s,
+                       S ? (float *)S->mean1.p : nullptr, S ? (float *)S->rstd1.p : nullptr));
   }
   GemmArgs q{};
   q.A = x1;
@@ -445,11 +469,17 @@ int enqueue_layer(dn_ctx *c, const Pass &p, int l, float *in, float *h1, float *
   o.K = H;
   o.n_store = H;
   o.accumulate = 1;
-  PROBED(ev, DN_PROBE_WO, "gemm(Wo)", layer_gemm(g, EPI_F32, o, s));
-
   void *x2 = S ? S->n2.p : w.xn;
-  HIPCHK(c, "ln(mlp_norm)", launch_ln(prec, h1, T, H, (const float *)W(c, pf + "mlp_norm.weight"), g.eps, x2, s,
-                                      S ? (float *)S->mean2.p : nullptr, S ? (float *)S->rstd2.p : nullptr));
+  const int wo_parts = split ? small_split_parts(prec, T, H, H) : 1;
+  if (wo_parts > 1) {
+    PROBED(ev, DN_PROBE_WO, "gemm(Wo)", launch_gemm_small_split(prec, o, wo_parts, w.part, s));
+    HIPCHK(c, "ln(mlp_norm)", launch_ln_parts(prec, h1, w.part, wo_parts, T, H,
+                                              (const float *)W(c, pf + "mlp_norm.weight"), g.eps, x2, s));
+  } else {
+    PROBED(ev, DN_PROBE_WO, "gemm(Wo)", layer_gemm(g, EPI_F32, o, s));
+    HIPCHK(c, "ln(mlp_norm)", launch_ln(prec, h1, T, H, (const float *)W(c, pf + "mlp_norm.weight"), g.eps, x2, s,
+                                        S ? (float *)S->mean2.p : nullptr, S ? (float *)S->rstd2.p : nullptr));
+  }
 
   GemmArgs wi{};
   wi.A = x2;
@@ -485,7 +515,12 @@ int enqueue_layer(dn_ctx *c, const Pass &p, int l, float *in, float *h1, float *
   mo.K = I;
   mo.n_store = H;
   mo.accumulate = 1;
-  PROBED(ev, DN_PROBE_MLPWO, "gemm(MlpWo)", layer_gemm(g, EPI_F32, mo, s));
+  const int parts = split && mo_parts ? small_split_parts(prec, T, H, I) : 1;
+  if (mo_parts) *mo_parts = parts > 1 ? parts : 0;
+  if (parts > 1)
+    PROBED(ev, DN_PROBE_MLPWO, "gemm(MlpWo)", launch_gemm_small_split(prec, mo, parts, w.part, s));
+  else
+    PROBED(ev, DN_PROBE_MLPWO, "gemm(MlpWo)", layer_gemm(g, EPI_F32, mo, s));
   return DN_OK;
 }
 
@@ -948,7 +983,9 @@ int forward_core(dn_ctx *c, int nseq, const int32_t *seq_len, const int32_t *d_i
   bool probed = false;
   const bool rows_tail = tail_on_rows(c, T, R, train);
   const bool rows_layer = rows_tail && rows_layer_fits(c, T, R, w.nseq);
-  for (int l = 0; l < (rows_layer ? L - 1 : L); l++) {
+  const int nfull = rows_layer ? L - 1 : L;  // layers enqueue_layer runs
+  int pending = 0;                           // MlpWo parts not yet in the residual stream
+  for (int l = 0; l < nfull; l++) {
     hipEvent_t *ev = ws ? nullptr : probe_slot(c, l);  // the probe creates events: not in a caller's workspace
     probed |= ev != nullptr;
     // Training keeps this layer's activations (layers >= train_from).
@@ -956,8 +993,13 @@ int forward_core(dn_ctx *c, int nseq, const int32_t *seq_len, const int32_t *d_i
     float *in = cur;                                              // this layer's input (S->hs when saved)
     float *h1 = S ? (float *)S->h1.p : in;                        // residual after attention
     float *out = saved(l + 1) ? (float *)saved(l + 1)->hs.p : h;  // the layer's output
-    rc = enqueue_layer(c, ps, l, in, h1, out, xn0, S, ev, rows_tail && l == L - 1);
+    // The last layer's MlpWo completes the residual stream itself (the head
+    // or the option-row layer reads it).
+    int parts = 0;
+    rc = enqueue_layer(c, ps, l, in, h1, out, xn0, S, ev, rows_tail && l == L - 1, pending,
+                       !train && l + 1 < nfull ? &parts : nullptr);
     if (rc) return rc;
+    pending = parts;
     cur = out;
   }
   if (probed) c->probe_used++;

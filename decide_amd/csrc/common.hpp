@@ -178,6 +178,12 @@ bool gemm_epi_ok(int precision, int epi, int M);
 // (row-major, ldc = N), then summed in split order into C (M x N, ldc = N;
 // added to C when a.accumulate, else stored). partial holds splits * M * N floats.
 hipError_t launch_gemm_splitk(int precision, const GemmArgs &a, int splits, float *partial, hipStream_t s);
+// Small M (<= 128) split-K on the whole-K kernel, no reduction: workgroup z of
+// a tile multiplies K elements [z*K/splits, (z+1)*K/splits) and stores its
+// fp32 partial product at partial + z * M * N (row-major, ldc = N); a.C,
+// a.res and a.accumulate are ignored. The consumer sums the splits
+// (launch_ln's partial inputs). a.K % (splits * 64) == 0 (bf16) / 32 (fp32).
+hipError_t launch_gemm_small_split(int precision, const GemmArgs &a, int splits, float *partial, hipStream_t s);
 bool gemm_shape_ok(int precision, int N, int K);
 
 // Attention work item: 32 * QT * ATTN_WAVES queries of one sequence (each
@@ -283,6 +289,13 @@ hipError_t launch_prologue(int precision, const int *pos, const int *opt, const 
 // LayerNorm launchers; mean / rstd (optional, [rows]) receive the row statistics.
 hipError_t launch_ln(int precision, const float *x, int rows, int H, const float *w, float eps, void *y, hipStream_t s,
                      float *mean = nullptr, float *rstd = nullptr);
+// LayerNorm of x + (p0 + p1 + ... + p{nparts-1}) (the split-K partial
+// products of the residual GEMM before it, summed left to right, then added
+// to x), the sum stored back into x first: the residual update
+// C = res + A.B^T and the norm that reads it in one launch. part holds
+// nparts slices of rows x H floats; nparts 4 or 6.
+hipError_t launch_ln_parts(int precision, float *x, const float *part, int nparts, int rows, int H, const float *w,
+                           float eps, void *y, hipStream_t s);
 struct HeadArgs {
   const float *h;
   const int *row_tok;  // the rows of h the head reads; null: rows 0 .. R-1

@@ -84,6 +84,12 @@ struct TrainState {
   hipEvent_t ev_trans[2] = {nullptr, nullptr};  // the layer's gradient transposes are done
 };
 
+// Inference batches of at most kSmallSplitMaxTokens tokens split the residual
+// GEMMs (Wo, MlpWo) over K across workgroups, into at most kSmallSplitParts
+// parts and kSplitMaxWorkgroups workgroups; the LayerNorm after each sums
+// the parts into the residual stream.
+constexpr int kSmallSplitMaxTokens = 128, kSmallSplitParts = 6, kSplitMaxWorkgroups = 256;
+
 // Device memory one forward works in beyond the weights: the activations,
 // the batch layout and the head's scratch. forward_core takes it from the
 // context's own buffers unless a caller hands one in
@@ -93,6 +99,9 @@ struct Workspace {
   void *xn = nullptr, *qkv = nullptr, *ctx = nullptr, *act = nullptr;  // operand type
   int *kinfo = nullptr;                                 // [T]
   float *head_s1 = nullptr, *head_d = nullptr;          // [R x H], [R x H/2]
+  // [kSmallSplitParts x T x H] split-K partial products of the residual
+  // GEMMs for batches of at most kSmallSplitMaxTokens tokens; null otherwise.
+  float *part = nullptr;
   int *seq_off = nullptr, *seq_len = nullptr, *chunk_off = nullptr, *first = nullptr;
   int4 *chunk_desc = nullptr, *work = nullptr;
   ChunkInfo *chunks = nullptr;
@@ -137,7 +146,7 @@ struct dn_ctx {
   std::map<std::string, TensorSlot> w;
   DevBuf inv_freq;  // 32 doubles global theta, 32 local
   // workspace
-  DevBuf h, xn, qkv, ctxb, act, kinfo, logits, err_flag, head_s1, head_d;
+  DevBuf h, xn, qkv, ctxb, act, kinfo, logits, err_flag, head_s1, head_d, smallpart;
   // A host batch (dn_forward, dn_forward_train) arrives as one copy: the
   // token ids, positions, option ids and mask-row tokens packed in `io`, with
   // these views into it (valid until the next staged batch), from a pinned

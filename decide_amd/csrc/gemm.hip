@@ -477,10 +477,20 @@ __device__ __forceinline__ fvec<V> partial_sum(const float *red, int idx) {
   return v;
 }
 
-template <class T, int MB, int NB, int EPI, int W>
+template <class T, int MB, int NB, int EPI, int W, bool F16 = false>
 __global__ __launch_bounds__(64 * W) void gemm_skinny_kernel(GemmArgs g) {
   using MF = Mfma<T>;
   typedef typename MF::frag frag;
+  static_assert(!F16 || sizeof(T) == 2, "16 x 16 blocks: bf16");
+  // F16: the tile as 16 x 16 blocks of v_mfma_f32_16x16x32_bf16, whose
+  // operand lanes read 64 contiguous bytes of a row (four lanes x 16 bytes)
+  // where the 32 x 32 x 16 form reads 32 (two lanes): half the cache-line
+  // sectors per load instruction.
+  constexpr int BW = F16 ? 16 : 32;                  // block width
+  constexpr int RB = 32 * MB / BW, CB = 32 * NB / BW;  // row / column blocks
+  constexpr int NS = F16 ? 2 : 4;                    // MFMA k steps per 64-element group
+  constexpr int NE = F16 ? 4 : 16;                   // accumulator elements per lane
+  typedef float accv __attribute__((__vector_size__(NE * sizeof(float))));
   constexpr int NT = 64 * W;
   constexpr int VPL = 16 / (int)sizeof(T);  // elements per 16-byte load
   constexpr int GK = 8 * VPL;               // k elements per group
@@ -498,42 +508,53 @@ __global__ __launch_bounds__(64 * W) void gemm_skinny_kernel(GemmArgs g) {
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, lr = lane & 31, lh = lane >> 5;
   const int n0 = blockIdx.x * TC, m0 = blockIdx.y * TR;
+  // Split-K (fp32 epilogue): blockIdx.z takes K elements [z*K, (z+1)*K) of A
+  // and B and writes its own partial output, c_split elements further on.
+  const int kz = blockIdx.z * g.K;
 
-  const T *ap[MB], *bp[NB];
+  // This lane's row (column) within a block and its first k element.
+  const int brow = F16 ? (lane & 15) : lr, bk = F16 ? (lane >> 4) * VPL : lh * VPL;
+  const T *ap[RB], *bp[CB];
 #pragma unroll
-  for (int i = 0; i < MB; i++) ap[i] = (const T *)g.A + (size_t)min(m0 + 32 * i + lr, g.M - 1) * g.lda + lh * VPL;
+  for (int i = 0; i < RB; i++) ap[i] = (const T *)g.A + (size_t)min(m0 + BW * i + brow, g.M - 1) * g.lda + kz + bk;
 #pragma unroll
-  for (int j = 0; j < NB; j++) {
+  for (int j = 0; j < CB; j++) {
+    const int cc = BW * j + brow;  // tile column
     // GeGLU on 32-column tiles: the 64-row group n0 / 64 of the interleaved
     // weights holds 32 value rows then their 32 gate rows; tile half
     // (n0 / 32) % 2 takes value rows 16h .. 16h+15 as columns 0..15 and the
     // matching gate rows as columns 16..31, so the tile's outputs are the 16
     // columns n0 / 2 .. n0 / 2 + 15.
     const int row = (EPI == EPI_GEGLU && NB == 1)
-                        ? (n0 & ~63) + (lr < 16 ? 0 : 32) + ((n0 >> 5) & 1) * 16 + (lr & 15)
-                        : n0 + 32 * j + lr;
-    bp[j] = (const T *)g.B + (size_t)row * g.ldb + lh * VPL;
+                        ? (n0 & ~63) + (cc < 16 ? 0 : 32) + ((n0 >> 5) & 1) * 16 + (cc & 15)
+                        : n0 + cc;
+    bp[j] = (const T *)g.B + (size_t)row * g.ldb + kz + bk;
   }
 
-  f32x16 acc[MB][NB];
+  accv acc[RB][CB];
 #pragma unroll
-  for (int i = 0; i < MB; i++)
+  for (int i = 0; i < RB; i++)
 #pragma unroll
-    for (int j = 0; j < NB; j++)
+    for (int j = 0; j < CB; j++)
 #pragma unroll
-      for (int e = 0; e < 16; e++) acc[i][j][e] = 0.0f;
+      for (int e = 0; e < NE; e++) acc[i][j][e] = 0.0f;
+  // Tile element (row-major TR x TC) of accumulator element e of block (i, j).
+  auto tile_at = [&](int i, int j, int e) {
+    if constexpr (F16) return (BW * i + 4 * (lane >> 4) + e) * TC + BW * j + (lane & 15);
+    else return (32 * i + mfma_row(e, lane)) * TC + 32 * j + lr;
+  };
 
-#define SKINNY_LOAD(XA, XB, GRP)                                                                  \
-  do {                                                                                            \
-    const int k_ = (GRP) * GK;                                                                    \
-    _Pragma("unroll") for (int i = 0; i < MB; i++) _Pragma("unroll") for (int q = 0; q < 4; q++) \
-        XA[i][q] = *(const uint4 *)(ap[i] + k_ + 2 * VPL * q);                                    \
-    _Pragma("unroll") for (int j = 0; j < NB; j++) _Pragma("unroll") for (int q = 0; q < 4; q++) \
-        XB[j][q] = *(const uint4 *)(bp[j] + k_ + 2 * VPL * q);                                    \
+#define SKINNY_LOAD(XA, XB, GRP)                                                                   \
+  do {                                                                                             \
+    const int k_ = (GRP) * GK;                                                                     \
+    _Pragma("unroll") for (int i = 0; i < RB; i++) _Pragma("unroll") for (int q = 0; q < NS; q++) \
+        XA[i][q] = *(const uint4 *)(ap[i] + k_ + (GK / NS) * q);                                   \
+    _Pragma("unroll") for (int j = 0; j < CB; j++) _Pragma("unroll") for (int q = 0; q < NS; q++) \
+        XB[j][q] = *(const uint4 *)(bp[j] + k_ + (GK / NS) * q);                                   \
   } while (0)
 
   const int ngrp = g.K / GK;
-  uint4 la[MB][4], lb[NB][4];
+  uint4 la[RB][NS], lb[CB][NS];
   int grp = wave;
   if (grp < ngrp) SKINNY_LOAD(la, lb, grp);
   // The fp32 epilogue's residual input, loaded now (behind the first operand
@@ -553,12 +574,19 @@ __global__ __launch_bounds__(64 * W) void gemm_skinny_kernel(GemmArgs g) {
     }
   }
   for (; grp < ngrp; grp += W) {
-    uint4 na[MB][4], nb[NB][4];
+    uint4 na[RB][NS], nb[CB][NS];
     const bool more = grp + W < ngrp;
     if (more) SKINNY_LOAD(na, nb, grp + W);
 #pragma unroll
-    for (int q = 0; q < 4; q++) {
-      if constexpr (sizeof(T) == 2) {
+    for (int q = 0; q < NS; q++) {
+      if constexpr (F16) {
+#pragma unroll
+        for (int i = 0; i < RB; i++)
+#pragma unroll
+          for (int j = 0; j < CB; j++)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(frag, la[i][q]),
+                                                                __builtin_bit_cast(frag, lb[j][q]), acc[i][j], 0, 0, 0);
+      } else if constexpr (sizeof(T) == 2) {
 #pragma unroll
         for (int i = 0; i < MB; i++)
 #pragma unroll
@@ -580,13 +608,13 @@ __global__ __launch_bounds__(64 * W) void gemm_skinny_kernel(GemmArgs g) {
     }
     if (more) {
 #pragma unroll
-      for (int i = 0; i < MB; i++)
+      for (int i = 0; i < RB; i++)
 #pragma unroll
-        for (int q = 0; q < 4; q++) la[i][q] = na[i][q];
+        for (int q = 0; q < NS; q++) la[i][q] = na[i][q];
 #pragma unroll
-      for (int j = 0; j < NB; j++)
+      for (int j = 0; j < CB; j++)
 #pragma unroll
-        for (int q = 0; q < 4; q++) lb[j][q] = nb[j][q];
+        for (int q = 0; q < NS; q++) lb[j][q] = nb[j][q];
     }
   }
 #undef SKINNY_LOAD
@@ -600,36 +628,36 @@ __global__ __launch_bounds__(64 * W) void gemm_skinny_kernel(GemmArgs g) {
     if (wave >= 4) {
       float *mine = red + (wave - 4) * TE;
 #pragma unroll
-      for (int i = 0; i < MB; i++)
+      for (int i = 0; i < RB; i++)
 #pragma unroll
-        for (int j = 0; j < NB; j++)
+        for (int j = 0; j < CB; j++)
 #pragma unroll
-          for (int e = 0; e < 16; e++) mine[(32 * i + mfma_row(e, lane)) * TC + 32 * j + lr] = acc[i][j][e];
+          for (int e = 0; e < NE; e++) mine[tile_at(i, j, e)] = acc[i][j][e];
     }
     __syncthreads();
     if (wave < 4) {
       const float *theirs = red + wave * TE;
 #pragma unroll
-      for (int i = 0; i < MB; i++)
+      for (int i = 0; i < RB; i++)
 #pragma unroll
-        for (int j = 0; j < NB; j++)
+        for (int j = 0; j < CB; j++)
 #pragma unroll
-          for (int e = 0; e < 16; e++) acc[i][j][e] += theirs[(32 * i + mfma_row(e, lane)) * TC + 32 * j + lr];
+          for (int e = 0; e < NE; e++) acc[i][j][e] += theirs[tile_at(i, j, e)];
     }
     __syncthreads();
   }
   if (wave < NP) {
     float *mine = red + wave * TE;
 #pragma unroll
-    for (int i = 0; i < MB; i++)
+    for (int i = 0; i < RB; i++)
 #pragma unroll
-      for (int j = 0; j < NB; j++)
+      for (int j = 0; j < CB; j++)
 #pragma unroll
-        for (int e = 0; e < 16; e++) mine[(32 * i + mfma_row(e, lane)) * TC + 32 * j + lr] = acc[i][j][e];
+        for (int e = 0; e < NE; e++) mine[tile_at(i, j, e)] = acc[i][j][e];
   }
   __syncthreads();
   if constexpr (EPI == EPI_F32) {
-    float *C = (float *)g.C;
+    float *C = (float *)g.C + blockIdx.z * g.c_split;
 #pragma unroll
     for (int k = 0; k < NQ; k++) {
       const int q = tid + NT * k;
@@ -702,21 +730,26 @@ __global__ __launch_bounds__(64 * W) void gemm_skinny_kernel(GemmArgs g) {
   }
 }
 
+// bf16 32 x 32 tiles run as 16 x 16 x 32 MFMA blocks (cfg5 0.7165 -> 0.7055
+// ms); the 64-row and 64-column tiles of 112-row batches were slower that
+// way (0.860 -> 0.868 ms) and keep 32 x 32 x 16.
 template <class T, int MB, int NB, int W>
-hipError_t launch_skinny_cfg(int epi, const GemmArgs &a, hipStream_t s) {
-  dim3 grid(a.N / (32 * NB), (a.M + 32 * MB - 1) / (32 * MB)), block(64 * W);
+hipError_t launch_skinny_cfg(int epi, const GemmArgs &a, hipStream_t s, int splits = 1) {
+  constexpr bool F = sizeof(T) == 2 && MB == 1 && NB == 1;
+  dim3 grid(a.N / (32 * NB), (a.M + 32 * MB - 1) / (32 * MB), splits), block(64 * W);
   switch (epi) {
     case EPI_F32:
-      hipLaunchKernelGGL((gemm_skinny_kernel<T, MB, NB, EPI_F32, W>), grid, block, 0, s, a);
+      hipLaunchKernelGGL((gemm_skinny_kernel<T, MB, NB, EPI_F32, W, F>), grid, block, 0, s, a);
       break;
     case EPI_STORE:
-      hipLaunchKernelGGL((gemm_skinny_kernel<T, MB, NB, EPI_STORE, W>), grid, block, 0, s, a);
+      hipLaunchKernelGGL((gemm_skinny_kernel<T, MB, NB, EPI_STORE, W, F>), grid, block, 0, s, a);
       break;
     case EPI_GEGLU:
-      hipLaunchKernelGGL((gemm_skinny_kernel<T, MB, NB, EPI_GEGLU, W>), grid, block, 0, s, a);
+      hipLaunchKernelGGL((gemm_skinny_kernel<T, MB, NB, EPI_GEGLU, W, F>), grid, block, 0, s, a);
       break;
     default:
-      if constexpr (NB == 2) hipLaunchKernelGGL((gemm_skinny_kernel<T, MB, 2, EPI_GEGLU_KEEP, W>), grid, block, 0, s, a);
+      if constexpr (NB == 2)
+        hipLaunchKernelGGL((gemm_skinny_kernel<T, MB, 2, EPI_GEGLU_KEEP, W, F>), grid, block, 0, s, a);
       else return hipErrorInvalidValue;
       break;
   }
@@ -744,6 +777,23 @@ hipError_t launch_skinny(int epi, const GemmArgs &a, hipStream_t s) {
   // tiles (QKV at 112 rows: 288 -> 144 workgroups, cfg2 0.917 -> 0.901 ms).
   if (a.M <= 128 && (a.N / 32) * ((a.M + 31) / 32) <= 256) return launch_skinny_cfg<T, 1, 1, 8>(epi, a, s);
   return launch_skinny_cfg<T, 2, 1, 8>(epi, a, s);
+}
+
+// Small-M split-K: a workgroup's time grows with the K it streams (~3.4 ns
+// per K element at M = 64 on top of ~2.1 us, whatever the grid), so K is
+// split over `splits` workgroups per tile, each writing an fp32 partial tile
+// into partial[z][M x N]; the consumer sums them.
+template <class T>
+hipError_t launch_skinny_split(const GemmArgs &a0, int splits, float *partial, hipStream_t s) {
+  GemmArgs a = a0;
+  a.K = a0.K / splits;
+  a.C = partial;
+  a.res = nullptr;
+  a.ldc = a0.N;
+  a.n_store = a0.N;
+  a.accumulate = 0;
+  a.c_split = (size_t)a0.M * a0.N;
+  return launch_skinny_cfg<T, 1, 1, 8>(EPI_F32, a, s, splits);
 }
 
 // C (+)= sum over splits of part[s * n + i], in split order; four
@@ -791,6 +841,14 @@ hipError_t launch_gemm_splitk(int precision, const GemmArgs &a0, int splits, flo
   hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)((n / 4 + 255) / 256)), dim3(256), 0, s, partial, splits,
                      n, (float *)a0.C, a0.accumulate);
   return hipGetLastError();
+}
+
+hipError_t launch_gemm_small_split(int precision, const GemmArgs &a, int splits, float *partial, hipStream_t s) {
+  if (a.M <= 0) return hipSuccess;
+  const int kt = precision == 1 ? 64 : 32;
+  if (a.M > 128 || splits < 1 || a.K % (splits * kt) != 0 || a.N % 128 != 0) return hipErrorInvalidValue;
+  return precision == 1 ? launch_skinny_split<bf16>(a, splits, partial, s)
+                        : launch_skinny_split<float>(a, splits, partial, s);
 }
 
 // All tile configs use BN = 128; K is staged 64 or 128 bytes per step.

@@ -93,6 +93,7 @@ extern "C" int dn_forward_device_noalloc(dn_ctx *c, int nseq, const int32_t *seq
   w.kinfo = (int *)take(sizeof(int) * Tz);
   w.head_s1 = (float *)take(sizeof(float) * R1 * H);
   w.head_d = (float *)take(sizeof(float) * R1 * (H / 2));
+  if (T <= kSmallSplitMaxTokens) w.part = (float *)take(sizeof(float) * kSmallSplitParts * Tz * H);
   w.seq_off = (int *)take(sizeof(int) * (nseq + 1));
   w.seq_len = (int *)take(sizeof(int) * (nseq + 1));
   w.chunk_off = (int *)take(sizeof(int) * (nseq + 1));

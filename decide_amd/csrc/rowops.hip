@@ -199,12 +199,18 @@ __global__ __launch_bounds__(256) void prologue_kernel(const int *pos, const int
 
 // Bias-free LayerNorm of the fp32 residual stream into the GEMM operand type
 // (attn_norm forward.go:289-294, mlp_norm forward.go:324).
-// RPW rows per wave (their loads and reductions interleave).
-template <class T, int RPW>
-__global__ __launch_bounds__(256) void ln_kernel(const float *xin, int rows, int dim, const float *w, float eps,
-                                                 T *y, float *mean_out, float *rstd_out) {
+// RPW rows per wave (their loads and reductions interleave). NPART > 0: the
+// row is xin + (p0 + p1 + ... ) over the NPART split-K partial products at
+// part + k * pstride (the residual GEMM's C = res + A.B^T), stored to xout
+// before it is normalised.
+// WPB waves per workgroup.
+template <class T, int RPW, int NPART = 0, int WPB = 4>
+__global__ __launch_bounds__(64 * WPB) void ln_kernel(const float *xin, int rows, int dim, const float *w, float eps,
+                                                      T *y, float *mean_out, float *rstd_out,
+                                                      const float *part = nullptr, size_t pstride = 0,
+                                                      float *xout = nullptr) {
   const int lane = threadIdx.x & 63;
-  const int r0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * RPW;
+  const int r0 = (blockIdx.x * WPB + (threadIdx.x >> 6)) * RPW;
   const int nvec = dim / 4;
   float4 x[RPW][MAXV];
 #pragma unroll
@@ -213,6 +219,30 @@ __global__ __launch_bounds__(256) void ln_kernel(const float *xin, int rows, int
 #pragma unroll
     for (int j = 0; j < MAXV; j++)
       if (lane + 64 * j < nvec) x[rr][j] = src[lane + 64 * j];
+  }
+  if constexpr (NPART > 0) {
+    float4 p[RPW][NPART][MAXV];
+#pragma unroll
+    for (int rr = 0; rr < RPW; rr++)
+#pragma unroll
+      for (int k = 0; k < NPART; k++) {
+        const float4 *src = (const float4 *)(part + k * pstride + (size_t)min(r0 + rr, rows - 1) * dim);
+#pragma unroll
+        for (int j = 0; j < MAXV; j++)
+          if (lane + 64 * j < nvec) p[rr][k][j] = src[lane + 64 * j];
+      }
+#pragma unroll
+    for (int rr = 0; rr < RPW; rr++)
+#pragma unroll
+      for (int j = 0; j < MAXV; j++)
+        if (lane + 64 * j < nvec) {
+          float4 a = p[rr][0][j];
+#pragma unroll
+          for (int k = 1; k < NPART; k++)
+            a = make_float4(a.x + p[rr][k][j].x, a.y + p[rr][k][j].y, a.z + p[rr][k][j].z, a.w + p[rr][k][j].w);
+          x[rr][j] = make_float4(x[rr][j].x + a.x, x[rr][j].y + a.y, x[rr][j].z + a.z, x[rr][j].w + a.w);
+          if (r0 + rr < rows) *(float4 *)(xout + (size_t)(r0 + rr) * dim + 4 * (lane + 64 * j)) = x[rr][j];
+        }
   }
   // The weights are loaded with the row, not after its statistics.
   const float4 *w4 = (const float4 *)w;
@@ -433,6 +463,31 @@ hipError_t launch_ln(int precision, const float *x, int rows, int H, const float
   else
     hipLaunchKernelGGL((ln_kernel<float, RPW>), grid, block, 0, s, x, rows, H, w, eps, (float *)y, mean, rstd);
   return hipGetLastError();
+}
+
+hipError_t launch_ln_parts(int precision, float *x, const float *part, int nparts, int rows, int H, const float *w,
+                           float eps, void *y, hipStream_t s) {
+  if (rows <= 0) return hipSuccess;
+  // One row per workgroup: a CU streams a burst of loads at only ~50 GB/s,
+  // so the row's (1 + nparts) x H floats are spread over as many CUs as rows.
+  dim3 grid(rows), block(64);
+  const size_t ps = (size_t)rows * H;
+#define LN_PARTS(N)                                                                                               \
+  if (nparts == N) {                                                                                              \
+    if (precision == 1)                                                                                           \
+      hipLaunchKernelGGL((ln_kernel<bf16, 1, N, 1>), grid, block, 0, s, x, rows, H, w, eps, (bf16 *)y, nullptr,   \
+                         nullptr, part, ps, x);                                                                   \
+    else                                                                                                          \
+      hipLaunchKernelGGL((ln_kernel<float, 1, N, 1>), grid, block, 0, s, x, rows, H, w, eps, (float *)y, nullptr, \
+                         nullptr, part, ps, x);                                                                   \
+    return hipGetLastError();                                                                                     \
+  }
+  LN_PARTS(2)
+  LN_PARTS(3)
+  LN_PARTS(4)
+  LN_PARTS(6)
+#undef LN_PARTS
+  return hipErrorInvalidValue;
 }
 
 hipError_t launch_rope_tables(const int *pos, int Tn, const double *inv_g, const double *inv_l, float *cos_g,
