@@ -220,6 +220,13 @@ __global__ __launch_bounds__(64 * WPB) void ln_kernel(const float *xin, int rows
     for (int j = 0; j < MAXV; j++)
       if (lane + 64 * j < nvec) x[rr][j] = src[lane + 64 * j];
   }
+  // The weights are loaded with the row (and before the partial
+  // products), not after its statistics.
+  const float4 *w4 = (const float4 *)w;
+  float4 wv[MAXV];
+#pragma unroll
+  for (int j = 0; j < MAXV; j++)
+    if (lane + 64 * j < nvec) wv[j] = w4[lane + 64 * j];
   if constexpr (NPART > 0) {
     float4 p[RPW][NPART][MAXV];
 #pragma unroll
@@ -241,15 +248,16 @@ __global__ __launch_bounds__(64 * WPB) void ln_kernel(const float *xin, int rows
           for (int k = 1; k < NPART; k++)
             a = make_float4(a.x + p[rr][k][j].x, a.y + p[rr][k][j].y, a.z + p[rr][k][j].z, a.w + p[rr][k][j].w);
           x[rr][j] = make_float4(x[rr][j].x + a.x, x[rr][j].y + a.y, x[rr][j].z + a.z, x[rr][j].w + a.w);
-          if (r0 + rr < rows) *(float4 *)(xout + (size_t)(r0 + rr) * dim + 4 * (lane + 64 * j)) = x[rr][j];
         }
-  }
-  // The weights are loaded with the row, not after its statistics.
-  const float4 *w4 = (const float4 *)w;
-  float4 wv[MAXV];
+    // Stored after every sum: a store between them makes the next sum wait
+    // for it (the wait counter counts stores too).
 #pragma unroll
-  for (int j = 0; j < MAXV; j++)
-    if (lane + 64 * j < nvec) wv[j] = w4[lane + 64 * j];
+    for (int rr = 0; rr < RPW; rr++)
+#pragma unroll
+      for (int j = 0; j < MAXV; j++)
+        if (lane + 64 * j < nvec && r0 + rr < rows)
+          *(float4 *)(xout + (size_t)(r0 + rr) * dim + 4 * (lane + 64 * j)) = x[rr][j];
+  }
 #pragma unroll
   for (int rr = 0; rr < RPW; rr++) {
     const int r = r0 + rr;
