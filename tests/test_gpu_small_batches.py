@@ -2,8 +2,10 @@
 total token count T swept across the small-M GEMM's tile rules (every
 projection runs the whole-K kernel up to 128 rows: 32-row tiles while the
 grid fits one workgroup per CU, 64-row tiles past it; Wi + GeGLU on 32- or
-64-column tiles by the same rule) and the forward prologue's 32-token chunks
-(ragged sequences, one to three per batch, independent and plain).
+64-column tiles by the same rule), the split counts of the residual GEMMs
+(Wo / MlpWo split over K into 2 to 6 parts that the next LayerNorm sums,
+fewer parts as T grows) and the forward prologue's 32-token chunks (ragged
+sequences, one to three per batch, independent and plain).
 
 Bars as in test_gpu_forward: fp32 max |dp| <= 1e-5 and logits within
 1e-4 * (1 + |logit|); bf16 max |dp| <= 2e-3; argmax agreement."""
