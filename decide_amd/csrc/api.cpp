@@ -606,6 +606,10 @@ bool rows_layer_fits(const dn_ctx *c, int T, int R, int nseq) {
   return 4 * r * H <= es * t * H && 3 * es * r * H <= es * t * I && es * r * I <= es * t * H;
 }
 
+// Bytes the option-row attention's work list takes in head_s1: nit int4
+// items, R row slots and the item count.
+size_t row_items_bytes(int nit, int R) { return sizeof(int4) * (size_t)nit + sizeof(int) * ((size_t)R + 1); }
+
 // Layer l (the last) for the R option rows row_tok only, over the batch
 // layout and buffers of w: attn_norm of every token (l > 0; x1 is layer 0's
 // input otherwise), K and V of every token (rows H..3H of Wqkv into qkv's k
@@ -654,8 +658,13 @@ int enqueue_rows_layer(dn_ctx *c, const Workspace &w, int l, const float *h, con
   q.K = H;
   q.n_store = H;
   HIPCHK(c, "gemm(Wqkv q)", layer_gemm(g, EPI_STORE, q, s));
-  // Work items in head_s1 (free until the head): items, then slots, then the count.
-  const int nit = w.nseq + (R + ATTN_QUERIES - 1) / ATTN_QUERIES;
+  // Work items in head_s1 (free until the head): items, then slots, then the
+  // count. Only sequences that hold rows make items, at most one per row, and
+  // a sequence's rows split into ceil(r/128) items, so min(nseq, R) +
+  // ceil(R/128) bounds the count whatever the rows' distribution.
+  const int nit = std::min(w.nseq, R) + (R + ATTN_QUERIES - 1) / ATTN_QUERIES;
+  if (row_items_bytes(nit, R) > sizeof(float) * (size_t)R * H)
+    return fail(c, DN_DEVICE_ERROR, "decide_hip: row work items exceed the head scratch");
   int4 *items = (int4 *)w.head_s1;
   int *rows = (int *)(items + nit), *nitems = rows + R;
   HIPCHK(c, "row_items", launch_row_items(row_tok, R, w.seq_off, w.nseq, T, items, rows, nitems, s));

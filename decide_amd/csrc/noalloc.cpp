@@ -1,6 +1,7 @@
 // dn_forward_device_noalloc: the forward of dn_forward_device for callers
-// that cannot allocate device memory (code under HIP graph capture, tight
-// serving loops, harnesses that forbid hipMalloc). Every buffer the forward
+// that cannot allocate device memory (tight serving loops, harnesses that
+// forbid hipMalloc). It synchronises the context's stream before uploading
+// the batch layout, so it refuses a capturing stream (DN_UNSUPPORTED). Every buffer the forward
 // works in beyond the weights and the caller's inputs and outputs (the
 // activations, the batch layout, the head's scratch) is carved out of one
 // static device array per GPU, `scratch`, of kScratchBytes. The call makes no
@@ -68,7 +69,13 @@ extern "C" int dn_forward_device_noalloc(dn_ctx *c, int nseq, const int32_t *seq
   if (!c->scratch) return fail(c, DN_DEVICE_ERROR, "decide_hip: no scratch array on this device");
   (void)hipSetDevice(c->device);
   // The host layout vectors are rewritten below: an earlier call's copies
-  // out of them must have finished.
+  // out of them must have finished. A capturing stream cannot be waited for
+  // (and a captured copy would read those vectors at replay), so capture is
+  // refused before anything is enqueued.
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  HIPCHK(c, "hipStreamIsCapturing", hipStreamIsCapturing(c->stream, &cap));
+  if (cap != hipStreamCaptureStatusNone)
+    return fail(c, DN_UNSUPPORTED, "decide_hip: dn_forward_device_noalloc cannot run under stream capture");
   HIPCHK(c, "hipStreamSynchronize", hipStreamSynchronize(c->stream));
   int T = 0, nch = 0;
   host_layout(c->hlay, nseq, seq_len, &T, &nch);

@@ -5,9 +5,9 @@
  * The library replaces the reference's GPU stack for inference
  * (internal/cuda: purego driver FFI + NVRTC-built PTX, internal/gpunn:
  * orchestration, cmd/ptxgen: codegen) and gives a device engine for the CPU
- * forward in internal/nn. A host binding (the Go/purego stub is in
- * INTEGRATION.md, the Python ctypes veneer is decide_amd/) dlopens it with
- * RTLD_NOW|RTLD_GLOBAL as internal/cuda/lib_unix.go:7-9 does for libcuda.
+ * forward in internal/nn. A host binding (the Go/purego package go/hipnn,
+ * the Python ctypes veneer decide_amd/) dlopens it with RTLD_NOW|RTLD_GLOBAL
+ * as internal/cuda/lib_unix.go:7-9 does for libcuda.
  *
  * Conventions (mirroring internal/cuda/driver.go):
  *   - every call returns an int status; 0 is success (driver.go:123-142);
@@ -140,10 +140,12 @@ int dn_forward_device(dn_ctx *ctx, int nseq, const int32_t *seq_len, const int32
  * ModernBERT-base in bf16 (about 2,900 in fp32); a larger batch gets
  * DN_INVALID_ARG naming the bytes it needs. All calls on one GPU share the
  * array: calls that overlap on one GPU (two contexts or streams) race. The
- * context's stream is synchronised before the batch layout is uploaded.
- * Arguments and results as dn_forward_device. No counterpart in the
- * reference: it is for callers that cannot allocate device memory (code under
- * graph capture, tight serving loops, harnesses that forbid hipMalloc). */
+ * context's stream is synchronised before the batch layout is uploaded, so
+ * the call cannot be captured into a graph: on a capturing stream it returns
+ * DN_UNSUPPORTED before enqueuing anything. Arguments and results as
+ * dn_forward_device. No counterpart in the reference: it is for callers that
+ * cannot allocate device memory (tight serving loops, harnesses that forbid
+ * hipMalloc). */
 int dn_forward_device_noalloc(dn_ctx *ctx, int nseq, const int32_t *seq_len, const int32_t *d_ids,
                               const int32_t *d_pos, const int32_t *d_opt_id, int nrows,
                               const int32_t *d_row_tok, float *d_logits);

@@ -39,6 +39,7 @@ def lib():
             build()
         L = ctypes.CDLL(_LIB_PATH)
         L.orc_set_workers.argtypes = [ctypes.c_int]
+        L.orc_set_rounding.argtypes = [ctypes.c_int]
         L.orc_get_workers.restype = ctypes.c_int
         gemm_args = [ctypes.c_int] * 5 + [ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_int,
                                           ctypes.c_void_p, ctypes.c_int, ctypes.c_int]
@@ -96,6 +97,17 @@ def lib():
 
 def set_workers(n: int) -> None:
     lib().orc_set_workers(int(n))
+
+
+# Stage rounding switches (bit values of RND_* in oracle.cpp). Each rounds one
+# stage's values to bfloat16 where a bf16 device path stores or multiplies
+# them; they exist to attribute the bf16 path's logit error to its stages and
+# are not part of the reference's arithmetic.
+ROUND_XN, ROUND_QKV, ROUND_QK, ROUND_P, ROUND_CTX, ROUND_ACT = 1, 2, 4, 8, 16, 32
+
+
+def set_rounding(mask: int) -> None:
+    lib().orc_set_rounding(int(mask))
 
 
 def _ptr(a: np.ndarray) -> int:

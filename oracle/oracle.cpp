@@ -128,6 +128,47 @@ Pool &pool() {
 
 int g_workers = 1;  // runtime.GOMAXPROCS(0) / blas.Workers
 
+// Emulated operand rounding (not part of the reference's arithmetic): each bit
+// rounds one stage's values to bfloat16 (nearest even) where a bf16 device
+// path stores or multiplies them, so that the effect of each stage on the
+// logits can be measured on the CPU. 0 (the default) is the reference.
+int g_round = 0;
+enum : int {
+  RND_XN = 1,     // LayerNorm outputs feeding QKV and Wi (and layer 0's emb-norm output)
+  RND_QKV = 2,    // the QKV GEMM's stored output, before RoPE
+  RND_QK = 4,     // q and k after RoPE (score MFMA operands)
+  RND_P = 8,      // attention probabilities before P.V
+  RND_CTX = 16,   // attention output (Wo's operand)
+  RND_ACT = 32,   // GeGLU output (MlpWo's operand)
+  RND_FP16 = 128, // round the stages above to IEEE binary16 instead of bfloat16
+};
+inline float bf16_round(float x) {
+  uint32_t u;
+  std::memcpy(&u, &x, 4);
+  if ((u & 0x7F800000u) == 0x7F800000u) return x;
+  u = (u + 0x7FFFu + ((u >> 16) & 1u)) & 0xFFFF0000u;
+  std::memcpy(&x, &u, 4);
+  return x;
+}
+// Nearest-even binary16 value of x (subnormals kept, overflow to infinity).
+inline float fp16_round(float x) {
+  float a = std::fabs(x);
+  if (!(a < 65520.0f)) return a != a ? x : std::copysign(INFINITY, x);
+  if (a < 6.103515625e-05f) return std::nearbyint(x * 16777216.0f) / 16777216.0f;  // quantum 2^-24
+  uint32_t u;
+  std::memcpy(&u, &x, 4);
+  u = (u + 0xFFFu + ((u >> 13) & 1u)) & 0xFFFFE000u;
+  std::memcpy(&x, &u, 4);
+  return x;
+}
+void round_if(int bit, float *x, size_t n) {
+  if (!(g_round & bit)) return;
+  if (g_round & RND_FP16)
+    for (size_t i = 0; i < n; i++) x[i] = fp16_round(x[i]);
+  else
+    for (size_t i = 0; i < n; i++) x[i] = bf16_round(x[i]);
+}
+
 // parallelFor, internal/nn/ops.go:13-44.
 void parallel_for(int n, const std::function<void(int, int)> &fn) {
   int workers = g_workers;
@@ -483,6 +524,7 @@ void attn_fwd(const Config &cfg, const std::vector<SeqInfo> &seqs, float *ctx, c
       sgemm(1, false, true, n, n, D, q, stride, k, stride, Pp, n, false);
       const uint8_t *mask = sliding ? s.slide.data() : (s.full.empty() ? nullptr : s.full.data());
       softmax_masked(Pp, n, scale, mask);
+      round_if(RND_P, Pp, (size_t)n * n);
       sgemm(1, false, false, n, D, n, Pp, n, v, stride, ctx + (size_t)s.off * H + hd * D, H, false);
     }
   });
@@ -495,6 +537,9 @@ void attn_fwd(const Config &cfg, const std::vector<SeqInfo> &seqs, float *ctx, c
 extern "C" {
 
 void orc_set_workers(int n) { g_workers = n < 1 ? 1 : n; }
+
+// Stage rounding switches (RND_* bits above); 0 restores the reference.
+void orc_set_rounding(int mask) { g_round = mask; }
 int orc_get_workers(void) { return g_workers; }
 
 // blas.Sgemm (gemm.go:61) with an explicit worker count (Sgemm1 == workers 1).
@@ -678,6 +723,7 @@ int forward_impl(const Model &m, int nseq, const int32_t *seq_len, const int32_t
   std::vector<float> ping((size_t)T * H), pong((size_t)T * H);
   float *cur = trainFrom == 0 ? c.hs[0].data() : ping.data();
   layer_norm(cur, c.embX.data(), T, H, embNorm, nullptr, cfg.eps, c.embMean.data(), c.embRstd.data());
+  std::vector<float> x0r;  // layer 0's QKV operand when rounded (the residual stays exact)
   if (dbg_hs) std::memcpy(dbg_hs, cur, sizeof(float) * T * H);
 
   LayerCache frozen;
@@ -706,15 +752,24 @@ int forward_impl(const Model &m, int nseq, const int32_t *seq_len, const int32_t
       lc.rstd1.resize(T);
       layer_norm(lc.n1.data(), in, T, H, attnNorm, nullptr, cfg.eps, lc.mean1.data(), lc.rstd1.data());
       x1 = lc.n1.data();
+      round_if(RND_XN, lc.n1.data(), (size_t)T * H);
+    } else if (g_round & RND_XN) {
+      x0r.assign(in, in + (size_t)T * H);
+      round_if(RND_XN, x0r.data(), x0r.size());
+      x1 = x0r.data();
     }
     if (dbg_n1) std::memcpy(dbg_n1 + (size_t)l * T * H, x1, sizeof(float) * T * H);
     lc.qkv.resize((size_t)T * 3 * H);
     linear(lc.qkv.data(), x1, T, H, Wqkv, 3 * H);
+    round_if(RND_QKV, lc.qkv.data(), (size_t)T * 3 * H);
     apply_rope(lc.qkv.data(), T, H, cfg.heads, D, sliding ? c.cosL.data() : c.cosG.data(),
                sliding ? c.sinL.data() : c.sinG.data());
+    if (g_round & RND_QK)
+      for (int t = 0; t < T; t++) round_if(RND_QK, &lc.qkv[(size_t)t * 3 * H], (size_t)2 * H);
     lc.ctx.resize((size_t)T * H);
     if (keep) lc.P.assign(pTotal, 0);
     attn_fwd(cfg, seqs, lc.ctx.data(), lc.qkv.data(), sliding, keep ? lc.P.data() : nullptr);
+    round_if(RND_CTX, lc.ctx.data(), (size_t)T * H);
     linear(tmp.data(), lc.ctx.data(), T, H, Wo, H);
     if (dbg_attn) std::memcpy(dbg_attn + (size_t)l * T * H, tmp.data(), sizeof(float) * T * H);
     lc.h1.resize((size_t)T * H);
@@ -725,6 +780,7 @@ int forward_impl(const Model &m, int nseq, const int32_t *seq_len, const int32_t
     lc.mean2.resize(T);
     lc.rstd2.resize(T);
     layer_norm(lc.n2.data(), lc.h1.data(), T, H, mlpNorm, nullptr, cfg.eps, lc.mean2.data(), lc.rstd2.data());
+    round_if(RND_XN, lc.n2.data(), (size_t)T * H);
     lc.wi.resize((size_t)T * 2 * I);
     linear(lc.wi.data(), lc.n2.data(), T, H, Wi, 2 * I);
     lc.act.resize((size_t)T * I);
@@ -735,6 +791,7 @@ int forward_impl(const Model &m, int nseq, const int32_t *seq_len, const int32_t
         for (int i = 0; i < I; i++) a[i] = gelu(row[i]) * row[I + i];
       }
     });
+    round_if(RND_ACT, lc.act.data(), (size_t)T * I);
     linear(tmp.data(), lc.act.data(), T, I, MlpWo, H);
     parallel_for(T * H, [&](int lo, int hi) {
       for (int i = lo; i < hi; i++) out[i] = lc.h1[i] + tmp[i];

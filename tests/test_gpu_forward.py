@@ -538,6 +538,44 @@ def test_row_tail_flags_bad_row_index(base, engines):
             assert np.array_equal(out.cpu().numpy(), want)
 
 
+def test_row_tail_few_rows_many_sequences(base, engines):
+    """dn_forward_device and its no-alloc form accept fewer head rows than
+    sequences. With 200 sequences of 12 tokens (2,400 tokens, so the last
+    layer runs on the rows) and one or three rows, the option-row attention's
+    work list (one item per sequence that holds rows, plus one per 128 rows)
+    fits the head scratch whatever the sequence count; each row's logit is
+    the full forward's for that token (fp32: |d| <= 1e-5 * (1 + |logit|))."""
+    import torch
+
+    from decide_amd.nn import build_sequence, flatten, row_tokens
+    from decide_amd.synth import pack_request
+
+    cfg = base[0]
+    rng = np.random.default_rng(91)
+    batch = [build_sequence(pack_request(rng, 7, [5], cfg.vocab), 50284, True) for _ in range(200)]
+    assert sum(len(s.ids) for s in batch) >= 2048
+    eng = engines["fp32"]
+    eng.set_row_tail(2048)
+    full = eng.forward(batch)
+    seq_len, ids, pos, opt, nmask, _ = flatten(batch)
+    rt_all = row_tokens(batch)
+    for pick in ([0], [17, 120, 199]):
+        rt = rt_all[pick].astype(np.int32)
+        dv = {k: torch.from_numpy(v).cuda() for k, v in dict(ids=ids, pos=pos, opt=opt, rt=rt).items()}
+        for fn in (eng.forward_device, eng.forward_device_noalloc):
+            out = torch.full((len(rt),), float("nan"), dtype=torch.float32, device="cuda")
+            torch.cuda.synchronize()
+            fn(seq_len, dv["ids"].data_ptr(), dv["pos"].data_ptr(), dv["opt"].data_ptr(), len(rt),
+               dv["rt"].data_ptr(), out.data_ptr())
+            eng.synchronize()
+            eng.check_device_errors()
+            got = out.cpu().numpy().astype(np.float64)
+            want = full[pick].astype(np.float64)
+            print(f"{fn.__name__} rows {pick}: max |dlogit| {float(np.max(np.abs(got - want))):.3g}", flush=True)
+            assert np.all(np.abs(got - want) <= 1e-5 * (1 + np.abs(want)))
+    assert np.array_equal(eng.forward(batch), full)
+
+
 def test_row_tail_gather_fallbacks(base, engines):
     """The row tail's other form (attention over every token, then the
     option rows' attention output gathered), taken for batches of more than
