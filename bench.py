@@ -28,7 +28,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, HERE)
 
 METRIC = "encoder tokens/sec + GEMM TFLOP/s (% bf16 MFMA peak), ModernBERT-base, 1 MI355X"
-PEAK = {"bf16": 2.5e15, "fp32": 157.3e12}  # dense MFMA peaks, FLOP/s
+PEAK = {"bf16": 2.5e15, "fp16": 2.5e15, "fp32": 157.3e12}  # dense MFMA peaks, FLOP/s
 H, I = 768, 1152
 PROJ_FLOP_PER_TOKEN_LAYER = 2 * H * (3 * H + H + 2 * I + I)  # 10,027,008
 WORKLOADS = {
@@ -485,7 +485,11 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", default="cfg3", choices=sorted(WORKLOADS))
-    ap.add_argument("--precision", default="bf16", choices=["bf16", "fp32"])
+    ap.add_argument("--precision", default="bf16", choices=["bf16", "fp16", "fp32"])
+    ap.add_argument("--certify", type=float, default=0.0, metavar="MARGIN",
+                    help="dn_set_certify margin (16-bit precisions; 0: off)")
+    ap.add_argument("--nseq", type=int, default=None,
+                    help="sequences of the configuration's shape (default: the configuration's batch)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=12.0)
     ap.add_argument("--probe-layer", type=int, default=1)
@@ -534,7 +538,7 @@ def main() -> int:
     weights = random_weights(cfg, seed=0)
     torch.cuda.init()
     dev = torch.device("cuda:0")
-    eng = Engine(cfg, weights, precision=args.precision)
+    eng = Engine(cfg, weights, precision=args.precision, certify=args.certify)
     stream = torch.cuda.current_stream()
     eng.set_stream(stream.cuda_stream)
 
@@ -550,13 +554,14 @@ def main() -> int:
 
     eng.set_stream_split(args.stream_split)
     eng.set_row_tail(args.row_tail)
-    wl = Workload(eng, cfg, args.config, dev)
+    wl = Workload(eng, cfg, args.config, dev, nseq=args.nseq)
     log(f"workload {args.config}: {wl.nseq} sequences, T={wl.T}, R={wl.R}")
     log(f"warmup {args.warmup}")
     for _ in range(args.warmup):
         wl.step()
     torch.cuda.synchronize()
     eng.check_device_errors()
+    eng.read_certify()  # counters cover the timed steps only
 
     ev = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
     log(f"timing {args.steps} steps")
@@ -570,6 +575,7 @@ def main() -> int:
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     eng.check_device_errors()
+    cert_counts = eng.read_certify()
     # Per-launch kernel durations: a separate run with the probe on (HIP
     # events around layer probe_layer's five launches), where forwards run on
     # one stream so that each interval times one kernel alone.
@@ -586,15 +592,19 @@ def main() -> int:
     log("per-launch ms (layer %d): %s" % (args.probe_layer, {k: round(v, 4) for k, v in avg.items()}))
 
     prec = args.precision
-    esz = 2 if prec == "bf16" else 4
+    esz = 4 if prec == "fp32" else 2
+    tname = {"bf16": "bf16", "fp16": "f16", "fp32": "float"}[prec]
     hbm_bound = T <= 128
     attain = None
-    if prec == "bf16":
-        attain = {"changing_operands_tflops": round(eng.mfma_calibrate(0), 1),
-                  "constant_operands_tflops": round(eng.mfma_calibrate(1), 1),
-                  "method": "dn_mfma_calibrate: register-only v_mfma_f32_32x32x16_bf16 loop in the GEMMs' wave "
+    if prec != "fp32":
+        m0 = 0 if prec == "bf16" else 4
+        attain = {"changing_operands_tflops": round(eng.mfma_calibrate(m0), 1),
+                  "constant_operands_tflops": round(eng.mfma_calibrate(m0 + 1), 1),
+                  "method": f"dn_mfma_calibrate: register-only v_mfma_f32_32x32x16_{tname} loop in the GEMMs' wave "
                             "pattern on every CU, 2 waves per SIMD, no memory traffic; operands N(0,1) x "
                             "N(0,0.02), rotated one lane per iteration (changing) or fixed (constant)"}
+        if prec == "fp16":
+            attain["bf16_changing_operands_tflops"] = round(eng.mfma_calibrate(0), 1)
     # Per-launch roofline views. The kernel with the largest share of GPU
     # time at cfg3 is the fp32-residual GEMM (Wo and MlpWo share its symbol):
     # algorithmic bytes per launch are A, the weights, and the fp32 residual
@@ -615,7 +625,7 @@ def main() -> int:
                 "frac": round(wi_bytes / wi_s / 8e12, 4), "traffic": None,
                 "algorithmic_bytes_per_launch": wi_bytes}
     else:
-        roof = {"kernel": "gemm_nt_kernel<bf16,128,192,64,3,EPI_F32,2,2,2> (Wo and MlpWo + fp32 residual), "
+        roof = {"kernel": f"gemm_nt_kernel<{tname},128,192,64,3,EPI_F32,2,2,2> (Wo and MlpWo + fp32 residual), "
                           "layer %d, average of its two launches" % args.probe_layer,
                 "bound": "hbm", "achieved": round(res_bytes / res_s / 1e9, 1), "peak": 8000.0, "unit": "GB/s",
                 "frac": round(res_bytes / res_s / 8e12, 4), "traffic": traffic.get("residual"),
@@ -654,12 +664,17 @@ def main() -> int:
         "row_tail_min_tokens": args.row_tail,
         "roofline": roof,
     }
+    if args.certify:
+        result["certify"] = {"margin": args.certify,
+                             "sequences_checked": cert_counts[0], "sequences_recomputed_fp32": cert_counts[1],
+                             "method": "dn_set_certify: sequences whose two best logits are closer than the margin "
+                                       "are recomputed on the fp32 twin inside each timed step"}
     if attain:
         result["mfma_attainable"] = attain
         result["projection_gemm_frac_attainable"] = round(gemm_tflops / attain["changing_operands_tflops"], 4)
     if not hbm_bound:
         result["roofline_wi_gemm"] = {
-            "kernel": "gemm_nt_kernel<bf16,256,128,64,3,EPI_GEGLU,2,2,2> (Wi projection + fused GeGLU), layer %d"
+            "kernel": f"gemm_nt_kernel<{tname},256,128,64,3,EPI_GEGLU,2,2,2> (Wi projection + fused GeGLU), layer %d"
                       % args.probe_layer,
             "bound": "mfma", "achieved": round(wi_flop / wi_s / 1e12, 2), "peak": PEAK[prec] / 1e12,
             "unit": "TFLOP/s", "frac": round(wi_flop / wi_s / PEAK[prec], 4), "traffic": traffic.get("wi"),
@@ -672,7 +687,7 @@ def main() -> int:
         wl.host_forward()
         hio.append(time.perf_counter() - t1)
     result["host_io_tokens_per_s"] = round(T / float(np.median(hio)), 1)
-    if not args.no_extra_configs and args.config == "cfg3" and prec == "bf16":
+    if not args.no_extra_configs and args.config == "cfg3" and prec != "fp32":
         result["configs"] = extra_configs(eng, cfg, dev, stream, args)
     if not args.no_cpu_baseline:
         log("cpu baseline")
@@ -689,13 +704,13 @@ def main() -> int:
 class Workload:
     """One configuration's batch, staged on the device for dn_forward_device."""
 
-    def __init__(self, eng, cfg, name, dev):
+    def __init__(self, eng, cfg, name, dev, nseq=None):
         import torch
 
         from decide_amd.nn import flatten, row_tokens
         from decide_amd.synth import config_batch
 
-        self.eng, self.batch = eng, config_batch(name, vocab=cfg.vocab)
+        self.eng, self.batch = eng, config_batch(name, vocab=cfg.vocab, nseq=nseq)
         self.seq_len, ids, pos, opt, nmask, _ = flatten(self.batch)
         self.T, self.R, self.nseq = int(self.seq_len.sum()), int(nmask.sum()), len(self.batch)
         self.max_len = int(self.seq_len.max())

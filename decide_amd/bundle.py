@@ -129,13 +129,14 @@ def bundle_encoder(tokenizer_json: str) -> Tuple[Callable[[str], Sequence[int]],
 
 
 def load_bundle(bundle_dir: str, precision: str = "bf16", device: int = 0,
-                encoder: Optional[Tuple[Callable[[str], Sequence[int]], int]] = None) -> Local:
+                encoder: Optional[Tuple[Callable[[str], Sequence[int]], int]] = None, certify: float = 0.0) -> Local:
     """bundle.Load (bundle.go:95-125) onto the device: a Local whose weights are
     resident and whose tokenizer is the bundle's tokenizer.json.
-    ``encoder`` = (encode, mask_id) replaces that tokenizer."""
+    ``encoder`` = (encode, mask_id) replaces that tokenizer; ``certify`` > 0
+    turns on dn_set_certify with that margin (16-bit precisions)."""
     meta = read_meta(bundle_dir)
     cfg = nn.load_config(os.path.join(bundle_dir, "config.json"))
-    engine = nn.Engine(cfg, precision=precision, device=device)
+    engine = nn.Engine(cfg, precision=precision, device=device, certify=certify)
     upload_weights(engine, os.path.join(bundle_dir, "model.safetensors"))
     encode, mask_id = encoder if encoder is not None else bundle_encoder(os.path.join(bundle_dir, "tokenizer.json"))
     cal = meta.get("calibration") or {}

@@ -103,6 +103,19 @@ uint16_t f32_to_bf16_rne(float f) {
   return (uint16_t)(u >> 16);
 }
 
+// Nearest-even binary16 bits of f (the compiler's conversion: subnormals
+// kept, |f| >= 65520 to infinity). bf16 values with 2^-17 <= |f| <= 65504
+// convert exactly.
+uint16_t f32_to_f16_rne(float f) {
+  const _Float16 h = (_Float16)f;
+  uint16_t b;
+  std::memcpy(&b, &h, 2);
+  return b;
+}
+
+// Whether a finite f lies outside binary16's range (it would become infinite).
+bool f16_overflows(float f) { return std::isfinite(f) && std::fabs(f) >= 65520.0f; }
+
 std::string layer_prefix(int l) { return "model.layers." + std::to_string(l) + "."; }
 
 void define_tensors(dn_ctx *c) {
@@ -245,7 +258,7 @@ int ctx_workspace(dn_ctx *c, int nseq, const int32_t *seq_len, int R, Workspace 
     if (rc) return rc;
   }
   const Config &g = c->cfg;
-  const size_t es = g.precision == DN_PRECISION_BF16 ? 2 : 4, T = (size_t)o.T, H = g.hidden;
+  const size_t es = prec16(g.precision) ? 2 : 4, T = (size_t)o.T, H = g.hidden;
   HIPCHK(c, "hipMalloc", ensure(c->h, sizeof(float) * T * H));
   HIPCHK(c, "hipMalloc", ensure(c->xn, es * T * H));
   HIPCHK(c, "hipMalloc", ensure(c->qkv, es * T * 3 * H));
@@ -363,7 +376,7 @@ int enqueue_prologue(dn_ctx *c, const Pass &p, float *cur, void *xn0, float *emb
 // kSplitMaxWorkgroups and give every part a whole number of K groups (1: no
 // split).
 int small_split_parts(int precision, int T, int N, int K) {
-  const int tiles = (N / 32) * ((T + 31) / 32), kt = precision == DN_PRECISION_BF16 ? 64 : 32;
+  const int tiles = (N / 32) * ((T + 31) / 32), kt = prec16(precision) ? 64 : 32;
   for (int p : {6, 4, 3, 2})
     if (p <= kSmallSplitParts && tiles * p <= kSplitMaxWorkgroups && K % (p * kt) == 0) return p;
   return 1;
@@ -602,7 +615,7 @@ int enqueue_rows_tail(dn_ctx *c, int l, const void *ctx, const float *h, int T_t
 bool rows_layer_fits(const dn_ctx *c, int T, int R, int nseq) {
   const Config &g = c->cfg;
   if (g.generic || nseq > ROW_ITEMS_MAXSEQ) return false;
-  const size_t es = g.precision == DN_PRECISION_BF16 ? 2 : 4, H = g.hidden, I = g.inter, t = T, r = R;
+  const size_t es = prec16(g.precision) ? 2 : 4, H = g.hidden, I = g.inter, t = T, r = R;
   return 4 * r * H <= es * t * H && 3 * es * r * H <= es * t * I && es * r * I <= es * t * H;
 }
 
@@ -623,7 +636,7 @@ int enqueue_rows_layer(dn_ctx *c, const Workspace &w, int l, const float *h, con
                        const int32_t *row_tok, int R, float **h_out, hipStream_t s) {
   const Config &g = c->cfg;
   const int H = g.hidden, I = g.inter, prec = g.precision, T = w.T;
-  const size_t es = prec == DN_PRECISION_BF16 ? 2 : 4;
+  const size_t es = prec16(prec) ? 2 : 4;
   const std::string pf = layer_prefix(l);
   if (l > 0) {
     HIPCHK(c, "ln(attn_norm)", launch_ln(prec, h, T, H, (const float *)W(c, pf + "attn_norm.weight"), g.eps, w.xn, s));
@@ -833,7 +846,7 @@ int forward_split(dn_ctx *c, int nseq, const int32_t *seq_len, const int32_t *d_
                   int acc, const Workspace *wfull) {
   const Config &g = c->cfg;
   const int H = g.hidden, I = g.inter, L = g.layers;
-  const size_t es = g.precision == DN_PRECISION_BF16 ? 2 : 4;
+  const size_t es = prec16(g.precision) ? 2 : 4;
   const int cnt[2] = {cut, nseq - cut}, tok0[2] = {0, acc};
   if (!c->aux_stream) {
     HIPCHK(c, "hipStreamCreate", hipStreamCreateWithFlags(&c->aux_stream, hipStreamNonBlocking));
@@ -915,7 +928,7 @@ int forward_core(dn_ctx *c, int nseq, const int32_t *seq_len, const int32_t *d_i
                  const Workspace *ws) {
   const Config &g = c->cfg;
   const int H = g.hidden, I = g.inter, L = g.layers;
-  const size_t es = g.precision == DN_PRECISION_BF16 ? 2 : 4;
+  const size_t es = prec16(g.precision) ? 2 : 4;
   TrainState &tr = c->tr;
   tr.have_forward = false;  // any forward replaces the layout and the encoder output
   if (!ws && !train && c->probe_layer < 0 && nseq >= 2 && c->split_min_tokens > 0) {
@@ -1058,7 +1071,13 @@ int64_t wi_src_row(int64_t r, int64_t I) {
 
 int upload_f32(dn_ctx *c, TensorSlot &t, const float *data, int64_t n) {
   (void)hipSetDevice(c->device);
-  const bool bf = t.proj && c->cfg.precision == DN_PRECISION_BF16;
+  const bool bf = t.proj && prec16(c->cfg.precision);
+  const bool half = c->cfg.precision == DN_PRECISION_FP16;
+  if (bf && half)
+    for (int64_t i = 0; i < n; i++)
+      if (f16_overflows(data[i]))
+        return fail(c, DN_UNSUPPORTED, "decide_hip: a projection weight is outside the fp16 range (|w| >= 65520)");
+  uint16_t (*to16)(float) = half ? f32_to_f16_rne : f32_to_bf16_rne;
   const size_t bytes = (size_t)n * (bf ? 2 : 4);
   HIPCHK(c, "hipMalloc", ensure(t.buf, bytes));
   const int64_t H = c->cfg.hidden, I = c->cfg.inter;
@@ -1071,11 +1090,11 @@ int upload_f32(dn_ctx *c, TensorSlot &t, const float *data, int64_t n) {
     if (t.wi) {
       for (int64_t r = 0; r < rows; r++) {
         const float *s = data + src_row(r) * H;
-        for (int64_t k = 0; k < H; k++) tmp[r * H + k] = f32_to_bf16_rne(s[k]);
+        for (int64_t k = 0; k < H; k++) tmp[r * H + k] = to16(s[k]);
         if (!master.empty()) std::memcpy(&master[r * H], s, sizeof(float) * H);
       }
     } else {
-      for (int64_t i = 0; i < n; i++) tmp[i] = f32_to_bf16_rne(data[i]);
+      for (int64_t i = 0; i < n; i++) tmp[i] = to16(data[i]);
       if (!master.empty()) std::memcpy(master.data(), data, sizeof(float) * n);
     }
     HIPCHK(c, "hipMemcpy", hipMemcpy(t.buf.p, tmp.data(), bytes, hipMemcpyHostToDevice));
@@ -1249,6 +1268,7 @@ void dn_close(dn_ctx *c) {
   if (!c) return;
   (void)hipSetDevice(c->device);
   if (c->stream) (void)hipStreamSynchronize(c->stream);
+  close_certify(c);
   for (auto &kv : c->w) release_slot(kv.second);
   release_train(c->tr);
   for (hipEvent_t e : c->probe_pool) (void)hipEventDestroy(e);
@@ -1257,7 +1277,7 @@ void dn_close(dn_ctx *c) {
                     &c->rope,     &c->kinfo, &c->io,
                     &c->logits,   &c->err_flag, &c->gA,    &c->gB,          &c->gC,       &c->d_seq_off, &c->head_s1, &c->head_d,
                     &c->d_seq_len, &c->d_chunk_off, &c->d_chunk_desc, &c->d_work, &c->d_chunks,
-                    &c->d_codes,   &c->d_first, &c->calib};
+                    &c->d_codes,   &c->d_first, &c->calib, &c->smallpart};
   for (DevBuf *b : bufs) release(*b);
   if (c->pin) (void)hipHostFree(c->pin);
   for (PartLayout &P : c->parts)
@@ -1287,8 +1307,9 @@ int dn_set_config(dn_ctx *c, int hidden, int inter, int heads, int layers, int v
   if (hidden <= 0 || inter <= 0 || heads <= 0 || layers <= 0 || vocab <= 0 || !layer_is_sliding ||
       hidden % heads != 0 || hidden % 2 != 0)
     return fail(c, DN_INVALID_ARG, "nn: incomplete or inconsistent config");
-  if (precision != DN_PRECISION_FP32 && precision != DN_PRECISION_BF16)
+  if (precision != DN_PRECISION_FP32 && precision != DN_PRECISION_BF16 && precision != DN_PRECISION_FP16)
     return fail(c, DN_INVALID_ARG, "decide_hip: unknown precision " + std::to_string(precision));
+  close_certify(c);  // a new configuration starts without certification (and its twin)
   // The MFMA kernels take head_dim 64 with hidden % 256 == 0 and intermediate
   // % 64 == 0 (ModernBERT-base); other geometries up to hidden 1024 with head
   // widths 8, 16, 32 or 64 (the reference's own test models among them) run
@@ -1339,14 +1360,14 @@ int dn_set_config(dn_ctx *c, int hidden, int inter, int heads, int layers, int v
   return DN_OK;
 }
 
-int dn_upload_tensor_bf16(dn_ctx *c, const char *name, const uint16_t *bits, int64_t n) {
-  if (!c) return DN_INVALID_ARG;
-  c->err.clear();
+static int upload_bf16_impl(dn_ctx *c, const char *name, const uint16_t *bits, int64_t n) {
   TensorSlot *t = nullptr;
   int rc = find_slot(c, name, bits, n, &t);
   if (rc) return rc;
   if (!(t->proj && c->cfg.precision == DN_PRECISION_BF16)) {
-    // Stored as float32: widen exactly (safetensors.go:113-124).
+    // Stored as float32 (widened exactly, safetensors.go:113-124) or, in
+    // fp16 mode, as binary16 from the widened values: exact for bf16 values
+    // of magnitude 2^-17 .. 65504, nearest-even below that.
     std::vector<float> f((size_t)n);
     for (int64_t i = 0; i < n; i++) {
       const uint32_t u = (uint32_t)bits[i] << 16;
@@ -1378,20 +1399,32 @@ int dn_upload_tensor_bf16(dn_ctx *c, const char *name, const uint16_t *bits, int
   return DN_OK;
 }
 
+int dn_upload_tensor_bf16(dn_ctx *c, const char *name, const uint16_t *bits, int64_t n) {
+  if (!c) return DN_INVALID_ARG;
+  c->err.clear();
+  int rc = upload_bf16_impl(c, name, bits, n);
+  if (rc || !c->exact) return rc;
+  rc = dn_upload_tensor_bf16(c->exact, name, bits, n);  // the certification twin widens to float32
+  return rc ? fail(c, rc, c->exact->err) : DN_OK;
+}
+
 int dn_upload_tensor(dn_ctx *c, const char *name, const float *data, int64_t n) {
   if (!c) return DN_INVALID_ARG;
   c->err.clear();
   TensorSlot *t = nullptr;
   int rc = find_slot(c, name, data, n, &t);
   if (rc) return rc;
-  return upload_f32(c, *t, data, n);
+  rc = upload_f32(c, *t, data, n);
+  if (rc || !c->exact) return rc;
+  rc = dn_upload_tensor(c->exact, name, data, n);  // the certification twin keeps float32
+  return rc ? fail(c, rc, c->exact->err) : DN_OK;
 }
 
 int dn_weights_ready(const dn_ctx *c) {
   if (!c || !c->configured) return 0;
   for (auto &kv : c->w)
     if (!kv.second.set) return 0;
-  return 1;
+  return !c->exact || dn_weights_ready(c->exact);
 }
 
 int dn_forward(dn_ctx *c, int nseq, const int32_t *seq_len, const int32_t *ids, const int32_t *pos,
@@ -1406,7 +1439,9 @@ int dn_forward(dn_ctx *c, int nseq, const int32_t *seq_len, const int32_t *ids, 
   if (rc || T == 0) return rc;
   rc = forward_core(c, nseq, seq_len, c->d_ids, c->d_pos, c->d_opt, R, c->d_rowtok, (float *)c->logits.p, false);
   if (rc) return rc;
-  return finish_forward(c, R, logits);
+  rc = finish_forward(c, R, logits);
+  if (rc) return rc;
+  return certify_host(c, nseq, seq_len, ids, pos, opt_id, nmask, mask_pos, logits);
 }
 
 int dn_forward_device(dn_ctx *c, int nseq, const int32_t *seq_len, const int32_t *d_ids, const int32_t *d_pos,
@@ -1423,7 +1458,9 @@ int dn_forward_device(dn_ctx *c, int nseq, const int32_t *seq_len, const int32_t
       return fail(c, DN_UNSUPPORTED, "decide_hip: sequence " + std::to_string(s) + " is longer than 8192 tokens");
   }
   (void)hipSetDevice(c->device);
-  return forward_core(c, nseq, seq_len, d_ids, d_pos, d_opt_id, nrows, d_row_tok, d_logits, false);
+  int rc2 = forward_core(c, nseq, seq_len, d_ids, d_pos, d_opt_id, nrows, d_row_tok, d_logits, false);
+  if (rc2) return rc2;
+  return certify_device(c, nseq, seq_len, d_ids, d_pos, d_opt_id, nrows, d_row_tok, d_logits);
 }
 
 int dn_check_device_errors(dn_ctx *c) {
@@ -1505,11 +1542,11 @@ int dn_gemm_device(dn_ctx *c, int precision, int M, int N, int K, const void *d_
                    int accumulate) {
   if (!c) return DN_INVALID_ARG;
   c->err.clear();
-  if (precision != DN_PRECISION_FP32 && precision != DN_PRECISION_BF16)
+  if (precision != DN_PRECISION_FP32 && precision != DN_PRECISION_BF16 && precision != DN_PRECISION_FP16)
     return fail(c, DN_INVALID_ARG, "decide_hip: unknown precision");
   if (M < 0 || !d_A || !d_B || !d_C) return fail(c, DN_INVALID_ARG, "decide_hip: dn_gemm_device: bad argument");
   if (!gemm_shape_ok(precision, N, K))
-    return fail(c, DN_UNSUPPORTED, "decide_hip: dn_gemm_device needs N % 128 == 0 and K % 64 (bf16) / 32 (fp32)");
+    return fail(c, DN_UNSUPPORTED, "decide_hip: dn_gemm_device needs N % 128 == 0 and K % 64 (bf16, fp16) / 32 (fp32)");
   (void)hipSetDevice(c->device);
   GemmArgs a{};
   a.A = d_A;
@@ -1600,7 +1637,7 @@ int dn_read_probe(dn_ctx *c, double *ms, int *count) {
 }
 
 int dn_mfma_calibrate(dn_ctx *c, int mode, double *tflops) {
-  if (!c || !tflops || mode < 0 || mode > 3) return DN_INVALID_ARG;
+  if (!c || !tflops || mode < 0 || mode > 5) return DN_INVALID_ARG;
   c->err.clear();
   (void)hipSetDevice(c->device);
   int cus = 0;

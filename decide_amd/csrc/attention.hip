@@ -47,14 +47,12 @@ __device__ __forceinline__ int tile_class(const ChunkInfo &q, const ChunkInfo &k
   return (block_full && win_full && k.len == 32) ? 1 : 2;
 }
 
+// 16-bit types (bf16, fp16): each of a thread's R items is one (key, 16-byte
+// chunk pair (c, c+4)) of K with its RoPE factors and one (key pair, 8-d
+// group) of V; the workgroup's threads cover the tile's 256 K items and 256
+// V items.
 template <class T, int R>
-struct Staging;
-
-// bf16: each of a thread's R items is one (key, 16-byte chunk pair (c, c+4))
-// of K with its RoPE factors and one (key pair, 8-d group) of V; the
-// workgroup's threads cover the tile's 256 K items and 256 V items.
-template <int R>
-struct Staging<bf16, R> {
+struct Staging {
   uint4 k_lo[R], k_hi[R], v0[R], v1[R];
   float4 c_lo[R], c_hi[R], s_lo[R], s_hi[R];
   uint32_t valid;  // bit j: K item j's key, 8+j / 16+j: V item j's two keys exist (zeroed at the store)
@@ -167,9 +165,6 @@ __device__ __forceinline__ void stage_load(Staging<T, R> &st, const T *qkv, int 
   st.info = k0 + tid < n ? ki.pi : (int)0xffff0000u;
 }
 
-__device__ __forceinline__ float bf_lo(uint32_t w) { return __uint_as_float(w << 16); }
-__device__ __forceinline__ float bf_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
-
 // RoPE of one (a, b) pair, unfused like applyRope (ops.go:169-170).
 __device__ __forceinline__ void rope1(float &a, float &b, float c, float s) {
 #pragma clang fp contract(off)
@@ -177,12 +172,6 @@ __device__ __forceinline__ void rope1(float &a, float &b, float c, float s) {
   const float y = b * c + a * s;
   a = x;
   b = y;
-}
-
-// Round-to-nearest-even fp32 -> bf16 pair packed in one word (lo in bits 0..15).
-__device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
-  bf16x2_t v = {(bf16)lo, (bf16)hi};
-  return __builtin_bit_cast(uint32_t, v);
 }
 
 template <class T, int R>
@@ -204,11 +193,11 @@ __device__ __forceinline__ void stage_store(const Staging<T, R> &st, char *sK, c
       uint32_t po[4], ph[4];
 #pragma unroll
       for (int w = 0; w < 4; w++) {
-        float a0 = bf_lo(klo[w]), a1 = bf_hi(klo[w]), b0 = bf_lo(khi[w]), b1 = bf_hi(khi[w]);
+        float a0 = lo16<T>(klo[w]), a1 = hi16<T>(klo[w]), b0 = lo16<T>(khi[w]), b1 = hi16<T>(khi[w]);
         rope1(a0, b0, cs[2 * w], sn[2 * w]);
         rope1(a1, b1, cs[2 * w + 1], sn[2 * w + 1]);
-        po[w] = pack_bf16(a0, a1);
-        ph[w] = pack_bf16(b0, b1);
+        po[w] = pack16<T>(a0, a1);
+        ph[w] = pack16<T>(b0, b1);
       }
       *(uint4 *)(sK + key * ROWK + 16 * c) = make_uint4(po[0], po[1], po[2], po[3]);
       *(uint4 *)(sK + key * ROWK + 64 + 16 * c) = make_uint4(ph[0], ph[1], ph[2], ph[3]);
@@ -282,7 +271,7 @@ __global__ __launch_bounds__(64 * QW) __attribute__((amdgpu_waves_per_eu(QT == 1
   typedef typename MF::frag frag;
   constexpr int ROWK = D * sizeof(T) + 16;       // K tile row bytes (key-major)
   constexpr int ROWV = KTILE * sizeof(T) + 16;   // V^T tile row bytes (d-major)
-  // bf16: two buffers, tile t is computed from one while tile t+1 is stored
+  // 16-bit: two buffers, tile t is computed from one while tile t+1 is stored
   // into the other, with one barrier per tile. fp32 (the validation mode,
   // twice the bytes) keeps one buffer and a second barrier.
   constexpr int NBUF = sizeof(T) == 2 ? 2 : 1;
@@ -398,8 +387,8 @@ __global__ __launch_bounds__(64 * QW) __attribute__((amdgpu_waves_per_eu(QT == 1
         }
         const float x2 = x * c - y * sn, y2 = y * c + x * sn;
         if constexpr (sizeof(T) == 2) {
-          qf[t][ks][u] = (bf16)x2;
-          qf[t][ks + NKS / 2][u] = (bf16)y2;
+          qf[t][ks][u] = to_elem<T>(x2);
+          qf[t][ks + NKS / 2][u] = to_elem<T>(y2);
         } else {
           qf[t][ks] = x2;
           qf[t][ks + NKS / 2] = y2;
@@ -561,7 +550,7 @@ __global__ __launch_bounds__(64 * QW) __attribute__((amdgpu_waves_per_eu(QT == 1
           if constexpr (sizeof(T) == 2) {
             const int ti = ks >> 1, r0 = (ks & 1) * 8;
 #pragma unroll
-            for (int u = 0; u < 8; u++) pf[t][u] = (bf16)sT[t][ti][r0 + u];
+            for (int u = 0; u < 8; u++) pf[t][u] = to_elem<T>(sT[t][ti][r0 + u]);
           } else {
             pf[t] = sT[t][ks >> 4][ks & 15];
           }
@@ -620,9 +609,8 @@ __global__ __launch_bounds__(64 * QW) __attribute__((amdgpu_waves_per_eu(QT == 1
         for (int g = 0; g < 4; g++) {
           const int d0 = i * 32 + 8 * g + 4 * lh;
           if constexpr (sizeof(T) == 2) {
-            bf16x4 o = {(bf16)(ot[t][i][4 * g] * inv), (bf16)(ot[t][i][4 * g + 1] * inv),
-                        (bf16)(ot[t][i][4 * g + 2] * inv), (bf16)(ot[t][i][4 * g + 3] * inv)};
-            *(bf16x4 *)(out + d0) = o;
+            *(uint2 *)(out + d0) = make_uint2(pack16<T>(ot[t][i][4 * g] * inv, ot[t][i][4 * g + 1] * inv),
+                                              pack16<T>(ot[t][i][4 * g + 2] * inv, ot[t][i][4 * g + 3] * inv));
           } else {
             *(float4 *)(out + d0) = make_float4(ot[t][i][4 * g] * inv, ot[t][i][4 * g + 1] * inv,
                                                 ot[t][i][4 * g + 2] * inv, ot[t][i][4 * g + 3] * inv);
@@ -826,11 +814,11 @@ __device__ __forceinline__ void rows_store(const RowStage<T> &st, char *dst, int
         uint32_t po[4], ph[4];
 #pragma unroll
         for (int w = 0; w < 4; w++) {
-          float a0 = bf_lo(l[w]), a1 = bf_hi(l[w]), b0 = bf_lo(h[w]), b1 = bf_hi(h[w]);
+          float a0 = lo16<T>(l[w]), a1 = hi16<T>(l[w]), b0 = lo16<T>(h[w]), b1 = hi16<T>(h[w]);
           rope1(a0, b0, cs[2 * w], sn[2 * w]);
           rope1(a1, b1, cs[2 * w + 1], sn[2 * w + 1]);
-          po[w] = pack_bf16(a0, a1);
-          ph[w] = pack_bf16(b0, b1);
+          po[w] = pack16<T>(a0, a1);
+          ph[w] = pack16<T>(b0, b1);
         }
         lo = make_uint4(po[0], po[1], po[2], po[3]);
         hi = make_uint4(ph[0], ph[1], ph[2], ph[3]);
@@ -907,7 +895,7 @@ __device__ __forceinline__ typename Mfma<T>::frag acc_frag(const f32x16 (&x)[2],
   if constexpr (sizeof(T) == 2) {
     const int ti = ks >> 1, r0 = (ks & 1) * 8;
 #pragma unroll
-    for (int u = 0; u < 8; u++) f[u] = (bf16)x[ti][r0 + u];
+    for (int u = 0; u < 8; u++) f[u] = to_elem<T>(x[ti][r0 + u]);
   } else {
     f = x[ks >> 4][ks & 15];
   }
@@ -936,8 +924,7 @@ __device__ __forceinline__ void store_row64(f32x16 (&x)[2], T *dst, const float 
     for (int g = 0; g < 4; g++) {
       const int d0 = b * 32 + 8 * g + 4 * lh;
       if constexpr (sizeof(T) == 2) {
-        bf16x4 o = {(bf16)x[b][4 * g], (bf16)x[b][4 * g + 1], (bf16)x[b][4 * g + 2], (bf16)x[b][4 * g + 3]};
-        *(bf16x4 *)(dst + d0) = o;
+        *(uint2 *)(dst + d0) = make_uint2(pack16<T>(x[b][4 * g], x[b][4 * g + 1]), pack16<T>(x[b][4 * g + 2], x[b][4 * g + 3]));
       } else {
         *(float4 *)(dst + d0) = make_float4(x[b][4 * g], x[b][4 * g + 1], x[b][4 * g + 2], x[b][4 * g + 3]);
       }
@@ -1009,8 +996,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void a
         }
         rope1(x, y, cq[i], sq[i]);
         if constexpr (sizeof(T) == 2) {
-          qf[ks][u] = (bf16)x;
-          qf[ks + NKS / 2][u] = (bf16)y;
+          qf[ks][u] = to_elem<T>(x);
+          qf[ks + NKS / 2][u] = to_elem<T>(y);
         } else {
           qf[ks] = x;
           qf[ks + NKS / 2] = y;
@@ -1154,8 +1141,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void a
         }
         rope1(x, y, ck[i], sk[i]);
         if constexpr (sizeof(T) == 2) {
-          kf[ks][u] = (bf16)x;
-          kf[ks + NKS / 2][u] = (bf16)y;
+          kf[ks][u] = to_elem<T>(x);
+          kf[ks + NKS / 2][u] = to_elem<T>(y);
         } else {
           kf[ks] = x;
           kf[ks + NKS / 2] = y;
@@ -1273,8 +1260,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void a
         if constexpr (sizeof(T) == 2) {
 #pragma unroll
           for (int u = 0; u < 8; u++) {
-            pf[u] = (bf16)sc[kl * 8 + u];
-            df[u] = (bf16)dp[kl * 8 + u];
+            pf[u] = to_elem<T>(sc[kl * 8 + u]);
+            df[u] = to_elem<T>(dp[kl * 8 + u]);
           }
         } else {
           pf = sc[kl];
@@ -1367,7 +1354,7 @@ __global__ __launch_bounds__(64) void attention_generic_kernel(AttnArgs a) {
   }
   T *out = (T *)a.ctx + (size_t)(base + qi) * H + head * D;
 #pragma unroll
-  for (int d = 0; d < D; d++) out[d] = (T)o[d];
+  for (int d = 0; d < D; d++) out[d] = to_elem<T>(o[d]);
 }
 
 template <class T>
@@ -1385,48 +1372,48 @@ hipError_t launch_attention_generic_t(const AttnArgs &a, hipStream_t s) {
 
 hipError_t launch_attention_generic(int precision, const AttnArgs &a, hipStream_t s) {
   if (a.nseq <= 0 || a.max_len <= 0) return hipSuccess;
-  return precision == 1 ? launch_attention_generic_t<bf16>(a, s) : launch_attention_generic_t<float>(a, s);
+  return precision == PREC_BF16  ? launch_attention_generic_t<bf16>(a, s)
+         : precision == PREC_F16 ? launch_attention_generic_t<f16>(a, s)
+                                 : launch_attention_generic_t<float>(a, s);
+}
+
+template <class T>
+void launch_attention_t(const AttnArgs &a, hipStream_t s) {
+  dim3 grid(a.nwork * a.heads), block(64 * ATTN_WAVES);
+  if (a.sliding)
+    hipLaunchKernelGGL((attention_kernel<T, ATTN_WAVES, ATTN_QT, true>), grid, block, 0, s, a);
+  else if (a.qt == ATTN_QT_GLOBAL)
+    hipLaunchKernelGGL((attention_kernel<T, ATTN_WAVES, ATTN_QT_GLOBAL, false>), grid, block, 0, s, a);
+  else
+    hipLaunchKernelGGL((attention_kernel<T, ATTN_WAVES, ATTN_QT, false>), grid, block, 0, s, a);
+}
+
+template <class T>
+void launch_attention_rows_t(const AttnArgs &a, hipStream_t s) {
+  dim3 grid(a.nwork * a.heads), block(64 * ATTN_WAVES);
+  if (a.sliding)
+    hipLaunchKernelGGL((attention_kernel<T, ATTN_WAVES, ATTN_QT, true, true>), grid, block, 0, s, a);
+  else
+    hipLaunchKernelGGL((attention_kernel<T, ATTN_WAVES, ATTN_QT, false, true>), grid, block, 0, s, a);
 }
 
 hipError_t launch_attention(int precision, const AttnArgs &a, hipStream_t s) {
   if (a.nwork <= 0) return hipSuccess;
-  dim3 grid(a.nwork * a.heads), block(64 * ATTN_WAVES);
   // Sliding-window layers take ATTN_QT; global layers ATTN_QT or (their
   // inference layout) ATTN_QT_GLOBAL.
   if (a.qt != ATTN_QT && (a.sliding || a.qt != ATTN_QT_GLOBAL)) return hipErrorInvalidValue;
-  if (precision == 1) {
-    if (a.sliding)
-      hipLaunchKernelGGL((attention_kernel<bf16, ATTN_WAVES, ATTN_QT, true>), grid, block, 0, s, a);
-    else if (a.qt == ATTN_QT_GLOBAL)
-      hipLaunchKernelGGL((attention_kernel<bf16, ATTN_WAVES, ATTN_QT_GLOBAL, false>), grid, block, 0, s, a);
-    else
-      hipLaunchKernelGGL((attention_kernel<bf16, ATTN_WAVES, ATTN_QT, false>), grid, block, 0, s, a);
-  } else {
-    if (a.sliding)
-      hipLaunchKernelGGL((attention_kernel<float, ATTN_WAVES, ATTN_QT, true>), grid, block, 0, s, a);
-    else if (a.qt == ATTN_QT_GLOBAL)
-      hipLaunchKernelGGL((attention_kernel<float, ATTN_WAVES, ATTN_QT_GLOBAL, false>), grid, block, 0, s, a);
-    else
-      hipLaunchKernelGGL((attention_kernel<float, ATTN_WAVES, ATTN_QT, false>), grid, block, 0, s, a);
-  }
+  if (precision == PREC_BF16) launch_attention_t<bf16>(a, s);
+  else if (precision == PREC_F16) launch_attention_t<f16>(a, s);
+  else launch_attention_t<float>(a, s);
   return hipGetLastError();
 }
 
 hipError_t launch_attention_rows(int precision, const AttnArgs &a, hipStream_t s) {
   if (a.nwork <= 0) return hipSuccess;
   if (a.qt != ATTN_QT) return hipErrorInvalidValue;
-  dim3 grid(a.nwork * a.heads), block(64 * ATTN_WAVES);
-  if (precision == 1) {
-    if (a.sliding)
-      hipLaunchKernelGGL((attention_kernel<bf16, ATTN_WAVES, ATTN_QT, true, true>), grid, block, 0, s, a);
-    else
-      hipLaunchKernelGGL((attention_kernel<bf16, ATTN_WAVES, ATTN_QT, false, true>), grid, block, 0, s, a);
-  } else {
-    if (a.sliding)
-      hipLaunchKernelGGL((attention_kernel<float, ATTN_WAVES, ATTN_QT, true, true>), grid, block, 0, s, a);
-    else
-      hipLaunchKernelGGL((attention_kernel<float, ATTN_WAVES, ATTN_QT, false, true>), grid, block, 0, s, a);
-  }
+  if (precision == PREC_BF16) launch_attention_rows_t<bf16>(a, s);
+  else if (precision == PREC_F16) launch_attention_rows_t<f16>(a, s);
+  else launch_attention_rows_t<float>(a, s);
   return hipGetLastError();
 }
 
@@ -1460,7 +1447,8 @@ hipError_t launch_attention_bwd(int precision, const AttnBwdArgs &a, hipStream_t
   if (a.nwork <= 0) return hipSuccess;
   static_assert(ATTN_QUERIES == 128 && ATTN_WAVES == 4, "backward kernels use 4-wave, 128-token work items");
   dim3 grid(a.nwork * a.heads), block(256);
-  if (precision == 1) {
+  if (precision == PREC_F16) return hipErrorInvalidValue;  // training: fp32 and bf16
+  if (precision == PREC_BF16) {
     hipLaunchKernelGGL(attn_bwd_dq_kernel<bf16>, grid, block, 0, s, a);
     hipLaunchKernelGGL(attn_bwd_dkdv_kernel<bf16>, grid, block, 0, s, a);
   } else {

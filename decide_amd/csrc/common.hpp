@@ -14,6 +14,16 @@ typedef __bf16 bf16;
 typedef bf16 bf16x8 __attribute__((__vector_size__(8 * sizeof(bf16))));
 typedef bf16 bf16x4 __attribute__((__vector_size__(4 * sizeof(bf16))));
 typedef bf16 bf16x2_t __attribute__((__vector_size__(2 * sizeof(bf16))));
+// IEEE binary16: the operand type of the fp16 mode (11-bit significand where
+// bf16 has 8, the same MFMA rate and bytes).
+typedef _Float16 f16;
+typedef f16 f16x8 __attribute__((__vector_size__(8 * sizeof(f16))));
+typedef f16 f16x2_t __attribute__((__vector_size__(2 * sizeof(f16))));
+
+// Precision codes of the launchers: 0 fp32, 1 bf16, 2 fp16 (operand type of
+// the GEMM / attention operands and the activations stored between kernels).
+enum { PREC_F32 = 0, PREC_BF16 = 1, PREC_F16 = 2 };
+inline bool prec16(int precision) { return precision != PREC_F32; }
 typedef float f32x16 __attribute__((__vector_size__(16 * sizeof(float))));
 typedef float f32x4 __attribute__((__vector_size__(4 * sizeof(float))));
 
@@ -36,6 +46,30 @@ struct Mfma<bf16> {
 };
 
 template <>
+struct Mfma<f16> {
+  static constexpr int KSTEP = 16;  // v_mfma_f32_32x32x16_f16
+  static constexpr int SLOTS = 8;
+  typedef f16x8 frag;
+  static __device__ __forceinline__ f32x16 mma(frag a, frag b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  }
+};
+
+// The 16 x 16 x 32 form of the 16-bit MFMAs (4 accumulators per lane: lane l
+// owns column l%16 and rows 4*(l/16) .. +3; operand lane l feeds row l%16
+// with 8 consecutive k values from 8*(l/16)).
+template <class T>
+__device__ __forceinline__ f32x4 mma16x16(typename Mfma<T>::frag a, typename Mfma<T>::frag b, f32x4 c);
+template <>
+__device__ __forceinline__ f32x4 mma16x16<bf16>(bf16x8 a, bf16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+template <>
+__device__ __forceinline__ f32x4 mma16x16<f16>(f16x8 a, f16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+template <>
 struct Mfma<float> {
   static constexpr int KSTEP = 2;  // v_mfma_f32_32x32x2_f32
   static constexpr int SLOTS = 1;
@@ -54,6 +88,35 @@ template <>
 __device__ __forceinline__ float to_elem<float>(float x) { return x; }
 template <>
 __device__ __forceinline__ bf16 to_elem<bf16>(float x) { return (bf16)x; }
+template <>
+__device__ __forceinline__ f16 to_elem<f16>(float x) { return (f16)x; }
+
+// Two 16-bit elements in one 32-bit word (element 0 in bits 0..15): widen
+// one of them, or round a pair to nearest even and pack it.
+template <class T>
+__device__ __forceinline__ float lo16(uint32_t w);
+template <class T>
+__device__ __forceinline__ float hi16(uint32_t w);
+template <class T>
+__device__ __forceinline__ uint32_t pack16(float lo, float hi);
+template <>
+__device__ __forceinline__ float lo16<bf16>(uint32_t w) { return __uint_as_float(w << 16); }
+template <>
+__device__ __forceinline__ float hi16<bf16>(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+template <>
+__device__ __forceinline__ uint32_t pack16<bf16>(float lo, float hi) {
+  bf16x2_t v = {(bf16)lo, (bf16)hi};
+  return __builtin_bit_cast(uint32_t, v);
+}
+template <>
+__device__ __forceinline__ float lo16<f16>(uint32_t w) { return (float)__builtin_bit_cast(f16, (uint16_t)w); }
+template <>
+__device__ __forceinline__ float hi16<f16>(uint32_t w) { return (float)__builtin_bit_cast(f16, (uint16_t)(w >> 16)); }
+template <>
+__device__ __forceinline__ uint32_t pack16<f16>(float lo, float hi) {
+  f16x2_t v = {(f16)lo, (f16)hi};
+  return __builtin_bit_cast(uint32_t, v);
+}
 
 // GELU, exact erf form: 0.5*x*(1 + erf(x/sqrt2)) (internal/nn/ops.go:140-142).
 // The fp32 validation build evaluates erf in double as the reference does.
@@ -75,6 +138,11 @@ __device__ __forceinline__ float erf_as(float x) {
 }
 template <>
 __device__ __forceinline__ float gelu_erf<bf16>(float x) {
+  return 0.5f * x * (1.0f + erf_as(x * 0.70710678118654752440f));
+}
+// fp16 results are rounded to 2^-11 relative: the same approximation.
+template <>
+__device__ __forceinline__ float gelu_erf<f16>(float x) {
   return 0.5f * x * (1.0f + erf_as(x * 0.70710678118654752440f));
 }
 
@@ -115,6 +183,22 @@ struct Vec8<bf16> {
 #pragma unroll
     for (int i = 0; i < 8; i++) o[i] = (bf16)v[i];
     *(bf16x8 *)p = o;
+  }
+};
+template <>
+struct Vec8<f16> {
+  static __device__ __forceinline__ void load(const f16 *p, float (&v)[8]) {
+    const uint4 u = *(const uint4 *)p;
+    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      v[2 * i] = lo16<f16>(w[i]);
+      v[2 * i + 1] = hi16<f16>(w[i]);
+    }
+  }
+  static __device__ __forceinline__ void store(f16 *p, const float (&v)[8]) {
+    *(uint4 *)p = make_uint4(pack16<f16>(v[0], v[1]), pack16<f16>(v[2], v[3]), pack16<f16>(v[4], v[5]),
+                             pack16<f16>(v[6], v[7]));
   }
 };
 template <>

@@ -184,6 +184,14 @@ struct dn_ctx {
   std::vector<hipEvent_t> probe_bwd_pool;  // 6 events per recorded backward
   int probe_bwd_used = 0;
   TrainState tr;
+  // Certified argmax (dn_set_certify, certify.cpp): an fp32 twin holding the
+  // same weights recomputes the sequences whose two best logits are closer
+  // than the margin; counters of sequences checked / recomputed; the twin's
+  // compact batch and logits for dn_forward_device.
+  dn_ctx *exact = nullptr;
+  float certify_margin = 0.0f;
+  int64_t cert_checked = 0, cert_recomputed = 0;
+  DevBuf cert_in, cert_out;
 };
 
 namespace dnh {
@@ -230,6 +238,13 @@ int ensure_err_flag(dn_ctx *c);
 int noalloc_init(dn_ctx *c);
 // Finishes a host-array forward: logits to the host and the device error flag.
 int finish_forward(dn_ctx *c, int R, float *logits);
+// Certified argmax (certify.cpp): near-tie sequences of a finished forward
+// recomputed on the fp32 twin (no-ops without dn_set_certify).
+int certify_host(dn_ctx *c, int nseq, const int32_t *seq_len, const int32_t *ids, const int32_t *pos,
+                 const int32_t *opt_id, const int32_t *nmask, const int32_t *mask_pos, float *logits);
+int certify_device(dn_ctx *c, int nseq, const int32_t *seq_len, const int32_t *d_ids, const int32_t *d_pos,
+                   const int32_t *d_opt, int R, const int32_t *d_row_tok, float *d_logits);
+void close_certify(dn_ctx *c);
 
 }  // namespace dnh
 

@@ -53,12 +53,6 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
 }
 
-// Round-to-nearest-even fp32 pair -> two bf16 in one word (lo first).
-__device__ __forceinline__ unsigned pack_bf16_pair(float lo, float hi) {
-  return (unsigned)__builtin_bit_cast(unsigned short, (bf16)lo) |
-         ((unsigned)__builtin_bit_cast(unsigned short, (bf16)hi) << 16);
-}
-
 template <int BM, int BN>
 struct TileOrder {
   int m0, n0;
@@ -401,6 +395,9 @@ hipError_t launch_cfg(int epi, const GemmArgs &a, hipStream_t s, int splits = 1)
   // bf16 256-row tiles serve only the operand-type epilogues (the fp32 ones
   // take 128 x 192 or 128 x 128 tiles): the fp32 epilogue is not built there.
   constexpr bool f32_epi = !(sizeof(T) == 2 && BM == 256);
+  // The fp16 mode is inference only: no training epilogues.
+  constexpr bool train_epi = !std::is_same<T, f16>::value;
+  if (!train_epi && (epi == EPI_GEGLU_BWD || epi == EPI_GEGLU_KEEP)) return hipErrorInvalidValue;
   switch (epi) {
     case EPI_F32:
       if constexpr (f32_epi)
@@ -415,10 +412,12 @@ hipError_t launch_cfg(int epi, const GemmArgs &a, hipStream_t s, int splits = 1)
       hipLaunchKernelGGL((gemm_nt_kernel<T, BM, BN, RB, NSTAGE, EPI_GEGLU, WPE, WGM, WGN>), grid, block, 0, s, a);
       break;
     case EPI_GEGLU_BWD:
-      hipLaunchKernelGGL((gemm_nt_kernel<T, BM, BN, RB, NSTAGE, EPI_GEGLU_BWD, WPE, WGM, WGN>), grid, block, 0, s, a);
+      if constexpr (train_epi)
+        hipLaunchKernelGGL((gemm_nt_kernel<T, BM, BN, RB, NSTAGE, EPI_GEGLU_BWD, WPE, WGM, WGN>), grid, block, 0, s, a);
       break;
     default:
-      hipLaunchKernelGGL((gemm_nt_kernel<T, BM, BN, RB, NSTAGE, EPI_GEGLU_KEEP, WPE, WGM, WGN>), grid, block, 0, s, a);
+      if constexpr (train_epi)
+        hipLaunchKernelGGL((gemm_nt_kernel<T, BM, BN, RB, NSTAGE, EPI_GEGLU_KEEP, WPE, WGM, WGN>), grid, block, 0, s, a);
       break;
   }
   return hipGetLastError();
@@ -481,11 +480,11 @@ template <class T, int MB, int NB, int EPI, int W, bool F16 = false>
 __global__ __launch_bounds__(64 * W) void gemm_skinny_kernel(GemmArgs g) {
   using MF = Mfma<T>;
   typedef typename MF::frag frag;
-  static_assert(!F16 || sizeof(T) == 2, "16 x 16 blocks: bf16");
-  // F16: the tile as 16 x 16 blocks of v_mfma_f32_16x16x32_bf16, whose
-  // operand lanes read 64 contiguous bytes of a row (four lanes x 16 bytes)
-  // where the 32 x 32 x 16 form reads 32 (two lanes): half the cache-line
-  // sectors per load instruction.
+  static_assert(!F16 || sizeof(T) == 2, "16 x 16 blocks: 16-bit operands");
+  // F16: the tile as 16 x 16 blocks of the 16 x 16 x 32 MFMA, whose operand
+  // lanes read 64 contiguous bytes of a row (four lanes x 16 bytes) where the
+  // 32 x 32 x 16 form reads 32 (two lanes): half the cache-line sectors per
+  // load instruction.
   constexpr int BW = F16 ? 16 : 32;                  // block width
   constexpr int RB = 32 * MB / BW, CB = 32 * NB / BW;  // row / column blocks
   constexpr int NS = F16 ? 2 : 4;                    // MFMA k steps per 64-element group
@@ -584,8 +583,7 @@ __global__ __launch_bounds__(64 * W) void gemm_skinny_kernel(GemmArgs g) {
         for (int i = 0; i < RB; i++)
 #pragma unroll
           for (int j = 0; j < CB; j++)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(frag, la[i][q]),
-                                                                __builtin_bit_cast(frag, lb[j][q]), acc[i][j], 0, 0, 0);
+            acc[i][j] = mma16x16<T>(__builtin_bit_cast(frag, la[i][q]), __builtin_bit_cast(frag, lb[j][q]), acc[i][j]);
       } else if constexpr (sizeof(T) == 2) {
 #pragma unroll
         for (int i = 0; i < MB; i++)
@@ -677,8 +675,8 @@ __global__ __launch_bounds__(64 * W) void gemm_skinny_kernel(GemmArgs g) {
     auto emit = [&](auto gated, T *C, int ldo) {
       constexpr bool G = decltype(gated)::value;
       constexpr int OC = G ? TC / 2 : TC;  // output columns of the tile
-      // Elements per thread item: bf16 down to 2 (a 4-byte store) so that
-      // every thread has an item; fp32 4 (16 bytes).
+      // Elements per thread item: 16-bit types down to 2 (a 4-byte store) so
+      // that every thread has an item; fp32 4 (16 bytes).
       constexpr int EPV = sizeof(T) == 4 ? 4 : TR * OC >= 8 * NT ? 8 : TR * OC >= 4 * NT ? 4 : 2;
       constexpr int RV = EPV > 4 ? 4 : EPV;  // partial-sum vector width
       const int oc0 = G ? n0 / 2 : n0;
@@ -710,7 +708,7 @@ __global__ __launch_bounds__(64 * W) void gemm_skinny_kernel(GemmArgs g) {
         if constexpr (sizeof(T) == 2) {
           unsigned w[EPV / 2];
 #pragma unroll
-          for (int u = 0; u < EPV / 2; u++) w[u] = pack_bf16_pair(o[2 * u], o[2 * u + 1]);
+          for (int u = 0; u < EPV / 2; u++) w[u] = pack16<T>(o[2 * u], o[2 * u + 1]);
           if constexpr (EPV == 8) *(uint4 *)dst = make_uint4(w[0], w[1], w[2], w[3]);
           else if constexpr (EPV == 4) *(uint2 *)dst = make_uint2(w[0], w[1]);
           else *(unsigned *)dst = w[0];
@@ -748,7 +746,7 @@ hipError_t launch_skinny_cfg(int epi, const GemmArgs &a, hipStream_t s, int spli
       hipLaunchKernelGGL((gemm_skinny_kernel<T, MB, NB, EPI_GEGLU, W, F>), grid, block, 0, s, a);
       break;
     default:
-      if constexpr (NB == 2)
+      if constexpr (NB == 2 && !std::is_same<T, f16>::value)
         hipLaunchKernelGGL((gemm_skinny_kernel<T, MB, 2, EPI_GEGLU_KEEP, W, F>), grid, block, 0, s, a);
       else return hipErrorInvalidValue;
       break;
@@ -822,6 +820,7 @@ __global__ void splitk_reduce_kernel(const float *part, int splits, size_t n, fl
 
 hipError_t launch_gemm_splitk(int precision, const GemmArgs &a0, int splits, float *partial, hipStream_t s) {
   if (a0.M <= 0) return hipSuccess;
+  if (precision == PREC_F16) return hipErrorInvalidValue;  // training only
   if (splits < 1 || splits > 16 || a0.K % (splits * 64) != 0 || a0.N % 128 != 0) return hipErrorInvalidValue;
   GemmArgs a = a0;
   a.K = a0.K / splits;
@@ -845,21 +844,22 @@ hipError_t launch_gemm_splitk(int precision, const GemmArgs &a0, int splits, flo
 
 hipError_t launch_gemm_small_split(int precision, const GemmArgs &a, int splits, float *partial, hipStream_t s) {
   if (a.M <= 0) return hipSuccess;
-  const int kt = precision == 1 ? 64 : 32;
+  const int kt = prec16(precision) ? 64 : 32;
   if (a.M > 128 || splits < 1 || a.K % (splits * kt) != 0 || a.N % 128 != 0) return hipErrorInvalidValue;
-  return precision == 1 ? launch_skinny_split<bf16>(a, splits, partial, s)
-                        : launch_skinny_split<float>(a, splits, partial, s);
+  return precision == PREC_BF16  ? launch_skinny_split<bf16>(a, splits, partial, s)
+         : precision == PREC_F16 ? launch_skinny_split<f16>(a, splits, partial, s)
+                                 : launch_skinny_split<float>(a, splits, partial, s);
 }
 
 // All tile configs use BN = 128; K is staged 64 or 128 bytes per step.
 bool gemm_shape_ok(int precision, int N, int K) {
-  const int kt = precision == 1 ? 64 : 32;
+  const int kt = prec16(precision) ? 64 : 32;
   return N > 0 && K > 0 && N % 128 == 0 && K % kt == 0;
 }
 
 bool gemm_epi_ok(int precision, int epi, int M) {
   if (epi != EPI_GEGLU_BWD) return true;
-  return precision == 1 ? M > 128 : M > 1024;
+  return prec16(precision) ? M > 128 : M > 1024;
 }
 
 // Any-shape GEMM (model geometries the MFMA kernels do not tile): thread n of
@@ -884,10 +884,10 @@ __global__ __launch_bounds__(256) void gemm_generic_kernel(GemmArgs g) {
     const float *R = g.res ? g.res + (size_t)m * g.ldc + n : C;
     *C = g.accumulate ? *R + v : v;
   } else if constexpr (EPI == EPI_STORE) {
-    ((T *)g.C)[(size_t)m * g.ldc + n] = (T)dot(n);
+    ((T *)g.C)[(size_t)m * g.ldc + n] = to_elem<T>(dot(n));
   } else {
     const float v = dot(n), gate = dot(ncols + n);
-    ((T *)g.C)[(size_t)m * g.ldc + n] = (T)(gelu_erf<T>(v) * gate);
+    ((T *)g.C)[(size_t)m * g.ldc + n] = to_elem<T>(gelu_erf<T>(v) * gate);
   }
 }
 
@@ -907,8 +907,15 @@ hipError_t launch_gemm_generic_t(int epi, const GemmArgs &a, hipStream_t s) {
 hipError_t launch_gemm_generic(int precision, int epi, const GemmArgs &a, hipStream_t s) {
   if (a.M <= 0) return hipSuccess;
   if (a.N <= 0 || a.K <= 0 || (epi == EPI_GEGLU && a.N % 2)) return hipErrorInvalidValue;
-  return precision == 1 ? launch_gemm_generic_t<bf16>(epi, a, s) : launch_gemm_generic_t<float>(epi, a, s);
+  return precision == PREC_BF16  ? launch_gemm_generic_t<bf16>(epi, a, s)
+         : precision == PREC_F16 ? launch_gemm_generic_t<f16>(epi, a, s)
+                                 : launch_gemm_generic_t<float>(epi, a, s);
 }
+
+// The tiled kernel's configuration for 16-bit operands (bf16 or fp16; the
+// same tiles, measured on bf16).
+template <class T>
+hipError_t launch_gemm16(int epi, const GemmArgs &a, hipStream_t s);
 
 hipError_t launch_gemm(int precision, int epi, const GemmArgs &a0, hipStream_t s) {
   if (a0.M <= 0) return hipSuccess;
@@ -917,12 +924,15 @@ hipError_t launch_gemm(int precision, int epi, const GemmArgs &a0, hipStream_t s
   // fp32 (the scorer's dense layer over all [MASK] rows, the fp32 validation
   // build) that pays up to M = 1024: the 64 x 128 tiles below would leave
   // most CUs idle with a 24-step fp32 K loop each.
-  if (a0.M <= 128) return precision == 1 ? launch_skinny<bf16>(epi, a0, s) : launch_skinny<float>(epi, a0, s);
-  if (precision == 0 && a0.M <= 1024) return launch_skinny<float>(epi, a0, s);
+  if (a0.M <= 128)
+    return precision == PREC_BF16  ? launch_skinny<bf16>(epi, a0, s)
+           : precision == PREC_F16 ? launch_skinny<f16>(epi, a0, s)
+                                   : launch_skinny<float>(epi, a0, s);
+  if (precision == PREC_F32 && a0.M <= 1024) return launch_skinny<float>(epi, a0, s);
   GemmArgs a = a0;
   // N groups per XCD sweep: keep the group's slice of B (N/groups rows of
   // K elements) within about 2 MB of L2.
-  const size_t b_bytes = (size_t)a.N * a.K * (precision == 1 ? 2 : 4);
+  const size_t b_bytes = (size_t)a.N * a.K * (prec16(precision) ? 2 : 4);
   const int tiles_n = a.N / 128;
   int groups = 1;
   while (b_bytes / groups > (2u << 20) && groups < tiles_n) {
@@ -947,9 +957,17 @@ hipError_t launch_gemm(int precision, int epi, const GemmArgs &a0, hipStream_t s
   //    (isolated launches on the training shapes, 3840 rows: Wi + GeGLU 36.4
   //    -> 31.3 us, dX GEMMs N = 768 K = 2304 32.3 -> 30.4 us, dctx 16.0 ->
   //    12.6 us).
+  if (precision == PREC_BF16) return launch_gemm16<bf16>(epi, a, s);
+  if (precision == PREC_F16) return launch_gemm16<f16>(epi, a, s);
+  if (a.M <= 1024) return launch_cfg<float, 64, 128, 128, 4, 1>(epi, a, s);
+  return launch_cfg<float, 256, 128, 128, 3, 1>(epi, a, s);
+}
+
+template <class T>
+hipError_t launch_gemm16(int epi, const GemmArgs &a, hipStream_t s) {
   const bool small = a.M <= 1024;
-  if (precision == 1) {
-    if (small) return launch_cfg<bf16, 64, 128, 128, 4, 1>(epi, a, s);
+  {
+    if (small) return launch_cfg<T, 64, 128, 128, 4, 1>(epi, a, s);
     const bool medium = a.M <= 4096;
     if (epi == EPI_F32 && a.N % 192 == 0) {
       // 768-wide outputs in 192-column tiles: 3,840 rows make 240 tiles of
@@ -957,22 +975,21 @@ hipError_t launch_gemm(int precision, int epi, const GemmArgs &a0, hipStream_t s
       // K = 2304: 30.6 -> 24.2 us isolated; Wo 16.2 -> 12.7 us); above 4096
       // rows 128 x 192 at two workgroups per CU (cfg3's 32768 rows: 1024
       // tiles, two full rounds of 512; forward 2.52 -> 2.56M tokens/s).
-      if (medium) return launch_cfg_one<bf16, 64, 192, 128, 4, 1>(a, s);
-      return launch_cfg_one<bf16, 128, 192, 64, 3, 2>(a, s);
+      if (medium) return launch_cfg_one<T, 64, 192, 128, 4, 1>(a, s);
+      return launch_cfg_one<T, 128, 192, 64, 3, 2>(a, s);
     }
     // GeGLU backward (N = 1152) at medium M: 64 x 192 at two workgroups per
-    // CU (3840 rows: 30.2 -> 25.8 us isolated).
-    if (epi == EPI_GEGLU_BWD && medium && a.N % 192 == 0)
-      return launch_cfg_one<bf16, 64, 192, 64, 4, 2, EPI_GEGLU_BWD>(a, s);
+    // CU (3840 rows: 30.2 -> 25.8 us isolated). Training only (bf16).
+    if constexpr (!std::is_same<T, f16>::value)
+      if (epi == EPI_GEGLU_BWD && medium && a.N % 192 == 0)
+        return launch_cfg_one<T, 64, 192, 64, 4, 2, EPI_GEGLU_BWD>(a, s);
     if (epi == EPI_F32 || (epi == EPI_STORE && a.N <= 1024 && a.M <= 16384)) {
-      if (medium) return launch_cfg<bf16, 64, 128, 128, 4, 1>(epi, a, s);
-      return launch_cfg<bf16, 128, 128, 64, 3, 3>(epi, a, s);
+      if (medium) return launch_cfg<T, 64, 128, 128, 4, 1>(epi, a, s);
+      return launch_cfg<T, 128, 128, 64, 3, 3>(epi, a, s);
     }
     if (epi == EPI_GEGLU_BWD || (epi == EPI_STORE && medium) ||
         ((epi == EPI_GEGLU || epi == EPI_GEGLU_KEEP) && a.M <= 8192))
-      return launch_cfg<bf16, 128, 128, 64, 3, 3>(epi, a, s);
-    return launch_cfg<bf16, 256, 128, 64, 3, 2>(epi, a, s);
+      return launch_cfg<T, 128, 128, 64, 3, 3>(epi, a, s);
+    return launch_cfg<T, 256, 128, 64, 3, 2>(epi, a, s);
   }
-  if (small) return launch_cfg<float, 64, 128, 128, 4, 1>(epi, a, s);
-  return launch_cfg<float, 256, 128, 128, 3, 1>(epi, a, s);
 }

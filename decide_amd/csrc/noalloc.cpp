@@ -1,12 +1,13 @@
 // dn_forward_device_noalloc: the forward of dn_forward_device for callers
 // that cannot allocate device memory (tight serving loops, harnesses that
 // forbid hipMalloc). It synchronises the context's stream before uploading
-// the batch layout, so it refuses a capturing stream (DN_UNSUPPORTED). Every buffer the forward
-// works in beyond the weights and the caller's inputs and outputs (the
-// activations, the batch layout, the head's scratch) is carved out of one
-// static device array per GPU, `scratch`, of kScratchBytes. The call makes no
-// hipMalloc / hipFree and uses no allocating library routine; the RoPE tables
-// and the error flag come from set-up (dn_set_config).
+// the batch layout, so it refuses a capturing stream (DN_UNSUPPORTED).
+// Every buffer the forward works in beyond the weights and the caller's
+// inputs and outputs (the activations, the batch layout, the head's
+// scratch) is carved out of one static device array per GPU, `scratch`, of
+// kScratchBytes. The call makes no hipMalloc / hipFree and uses no
+// allocating library routine; the RoPE tables and the error flag come from
+// set-up (dn_set_config).
 //
 // Every call on a GPU shares that GPU's array and it keeps the last call's
 // contents: calls that overlap on one GPU (two contexts, two streams) race.
@@ -81,7 +82,7 @@ extern "C" int dn_forward_device_noalloc(dn_ctx *c, int nseq, const int32_t *seq
   host_layout(c->hlay, nseq, seq_len, &T, &nch);
   const int nwork = (int)c->hlay.work.size(), nwork2 = (int)c->hlay.work2.size();
   const Config &g = c->cfg;
-  const size_t es = g.precision == DN_PRECISION_BF16 ? 2 : 4, H = g.hidden, I = g.inter, Tz = T;
+  const size_t es = prec16(g.precision) ? 2 : 4, H = g.hidden, I = g.inter, Tz = T;
   const size_t R1 = (size_t)(nrows > 0 ? nrows : 1);
   // Carve the workspace (256-byte aligned pieces) before touching anything.
   size_t off = 0;

@@ -88,8 +88,11 @@ __device__ __forceinline__ void store4<float>(float *p, float4 v) {
 }
 template <>
 __device__ __forceinline__ void store4<bf16>(bf16 *p, float4 v) {
-  bf16x4 o = {(bf16)v.x, (bf16)v.y, (bf16)v.z, (bf16)v.w};
-  *(bf16x4 *)p = o;
+  *(uint2 *)p = make_uint2(pack16<bf16>(v.x, v.y), pack16<bf16>(v.z, v.w));
+}
+template <>
+__device__ __forceinline__ void store4<f16>(f16 *p, float4 v) {
+  *(uint2 *)p = make_uint2(pack16<f16>(v.x, v.y), pack16<f16>(v.z, v.w));
 }
 
 // Token info and 32-token chunk summaries in one launch: 32 lanes per chunk
@@ -452,9 +455,12 @@ hipError_t launch_prologue(int precision, const int *pos, const int *opt, const 
   if (Tn <= 0) return hipSuccess;
   const int nb_tc = (nchunks + 7) / 8, nb_emb = (Tn + 3) / 4;
   dim3 grid(nb_tc + nb_emb), block(256);
-  if (precision == 1)
+  if (precision == PREC_BF16)
     hipLaunchKernelGGL(prologue_kernel<bf16>, grid, block, 0, s, pos, opt, chunk_desc, nchunks, kinfo, chunks, nb_tc,
                        ids, Tn, tok, vocab, w, eps, H, h, (bf16 *)xn, err, mean, rstd);
+  else if (precision == PREC_F16)
+    hipLaunchKernelGGL(prologue_kernel<f16>, grid, block, 0, s, pos, opt, chunk_desc, nchunks, kinfo, chunks, nb_tc,
+                       ids, Tn, tok, vocab, w, eps, H, h, (f16 *)xn, err, mean, rstd);
   else
     hipLaunchKernelGGL(prologue_kernel<float>, grid, block, 0, s, pos, opt, chunk_desc, nchunks, kinfo, chunks,
                        nb_tc, ids, Tn, tok, vocab, w, eps, H, h, (float *)xn, err, mean, rstd);
@@ -466,8 +472,10 @@ hipError_t launch_ln(int precision, const float *x, int rows, int H, const float
   if (rows <= 0) return hipSuccess;
   constexpr int RPW = 1;
   dim3 grid((rows + 4 * RPW - 1) / (4 * RPW)), block(256);
-  if (precision == 1)
+  if (precision == PREC_BF16)
     hipLaunchKernelGGL((ln_kernel<bf16, RPW>), grid, block, 0, s, x, rows, H, w, eps, (bf16 *)y, mean, rstd);
+  else if (precision == PREC_F16)
+    hipLaunchKernelGGL((ln_kernel<f16, RPW>), grid, block, 0, s, x, rows, H, w, eps, (f16 *)y, mean, rstd);
   else
     hipLaunchKernelGGL((ln_kernel<float, RPW>), grid, block, 0, s, x, rows, H, w, eps, (float *)y, mean, rstd);
   return hipGetLastError();
@@ -482,8 +490,11 @@ hipError_t launch_ln_parts(int precision, float *x, const float *part, int npart
   const size_t ps = (size_t)rows * H;
 #define LN_PARTS(N)                                                                                               \
   if (nparts == N) {                                                                                              \
-    if (precision == 1)                                                                                           \
+    if (precision == PREC_BF16)                                                                                   \
       hipLaunchKernelGGL((ln_kernel<bf16, 1, N, 1>), grid, block, 0, s, x, rows, H, w, eps, (bf16 *)y, nullptr,   \
+                         nullptr, part, ps, x);                                                                   \
+    else if (precision == PREC_F16)                                                                               \
+      hipLaunchKernelGGL((ln_kernel<f16, 1, N, 1>), grid, block, 0, s, x, rows, H, w, eps, (f16 *)y, nullptr,     \
                          nullptr, part, ps, x);                                                                   \
     else                                                                                                          \
       hipLaunchKernelGGL((ln_kernel<float, 1, N, 1>), grid, block, 0, s, x, rows, H, w, eps, (float *)y, nullptr, \
@@ -536,9 +547,12 @@ hipError_t launch_gather_rows(int precision, const void *ctx, const float *h, co
   if (R <= 0) return hipSuccess;
   if (H % 8 != 0) return hipErrorInvalidValue;
   const dim3 grid((R + 3) / 4), block(256);
-  if (precision == 1)
+  if (precision == PREC_BF16)
     hipLaunchKernelGGL(gather_rows_kernel<bf16>, grid, block, 0, s, (const bf16 *)ctx, h, row_tok, R, T, H,
                        (bf16 *)ctx_r, h_r, err_flag);
+  else if (precision == PREC_F16)
+    hipLaunchKernelGGL(gather_rows_kernel<f16>, grid, block, 0, s, (const f16 *)ctx, h, row_tok, R, T, H,
+                       (f16 *)ctx_r, h_r, err_flag);
   else
     hipLaunchKernelGGL(gather_rows_kernel<float>, grid, block, 0, s, (const float *)ctx, h, row_tok, R, T, H,
                        (float *)ctx_r, h_r, err_flag);

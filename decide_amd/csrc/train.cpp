@@ -504,6 +504,8 @@ int dn_enable_training(dn_ctx *c) {
   if (c->cfg.generic)
     return fail(c, DN_UNSUPPORTED, "decide_hip: training needs head_dim 64, hidden % 256 == 0 and "
                                    "intermediate % 64 == 0");
+  if (c->cfg.precision == DN_PRECISION_FP16)
+    return fail(c, DN_UNSUPPORTED, "decide_hip: training runs in fp32 or bf16 (fp16 is inference only)");
   for (auto &kv : c->w)
     if (kv.second.set && bf16_slot(c, kv.second))
       return fail(c, DN_INVALID_ARG, "decide_hip: dn_enable_training must precede the weight uploads");

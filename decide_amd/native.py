@@ -16,7 +16,8 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.environ.get("DECIDE_HIP_LIBRARY") or os.path.join(HERE, "libdecide_hip.so")
 
 DN_OK, DN_NO_GPU, DN_INVALID_ARG, DN_OUT_OF_MEMORY, DN_DEVICE_ERROR, DN_UNSUPPORTED = range(6)
-DN_PRECISION_FP32, DN_PRECISION_BF16 = 0, 1
+DN_PRECISION_FP32, DN_PRECISION_BF16, DN_PRECISION_FP16 = 0, 1, 2
+PRECISIONS = {"fp32": DN_PRECISION_FP32, "bf16": DN_PRECISION_BF16, "fp16": DN_PRECISION_FP16}
 DN_STATE_WEIGHT, DN_STATE_GRAD, DN_STATE_M, DN_STATE_V = range(4)
 
 
@@ -69,6 +70,8 @@ _SIGS = {
     "dn_synchronize": ([_vp], _i),
     "dn_set_stream_split": ([_vp, _i], _i),
     "dn_set_row_tail": ([_vp, _i], _i),
+    "dn_set_certify": ([_vp, _c.c_float], _i),
+    "dn_read_certify": ([_vp, _c.POINTER(_c.c_int64), _c.POINTER(_c.c_int64)], _i),
     "dn_set_probe": ([_vp, _i], _i),
     "dn_read_probe": ([_vp, _f64p, _c.POINTER(_i)], _i),
     "dn_read_probe_backward": ([_vp, _f64p, _c.POINTER(_i)], _i),

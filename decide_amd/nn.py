@@ -168,9 +168,9 @@ class Engine:
     batch order."""
 
     def __init__(self, cfg: Config, weights: Optional[Dict[str, np.ndarray]] = None, precision: str = "bf16",
-                 device: int = 0):
+                 device: int = 0, certify: float = 0.0):
         self.cfg = cfg
-        self.precision = {"bf16": native.DN_PRECISION_BF16, "fp32": native.DN_PRECISION_FP32}[precision]
+        self.precision = native.PRECISIONS[precision]
         h = ctypes.c_void_p()
         check(lib.dn_open(device, ctypes.byref(h)))
         self._h = h
@@ -178,6 +178,8 @@ class Engine:
         check(lib.dn_set_config(h, cfg.hidden, cfg.intermediate, cfg.heads, cfg.layers, cfg.vocab,
                                 float(cfg.eps), cfg.half_window, float(cfg.global_theta), float(cfg.local_theta),
                                 sl.ctypes.data_as(ctypes.c_void_p), self.precision), h)
+        if certify:
+            self.set_certify(certify)
         if weights is not None:
             self.load(weights)
 
@@ -272,9 +274,21 @@ class Engine:
         quarter of them) finish the last layer on the option rows only (0: off)."""
         check(lib.dn_set_row_tail(self._h, int(min_tokens)), self._h)
 
+    def set_certify(self, margin: float) -> None:
+        """dn_set_certify: sequences whose two best logits are closer than margin
+        (or not finite) are recomputed on an fp32 twin (16-bit modes; before the
+        weight uploads; 0: off)."""
+        check(lib.dn_set_certify(self._h, ctypes.c_float(margin)), self._h)
+
+    def read_certify(self):
+        """dn_read_certify: (sequences checked, sequences recomputed) since the last read."""
+        a, b = ctypes.c_int64(0), ctypes.c_int64(0)
+        check(lib.dn_read_certify(self._h, ctypes.byref(a), ctypes.byref(b)), self._h)
+        return a.value, b.value
+
     def mfma_calibrate(self, mode: int = 0) -> float:
         """dn_mfma_calibrate: attainable MFMA TFLOP/s (bf16: mode 0 changing operands, 1 constant;
-        fp32: 2 changing, 3 constant)."""
+        fp32: 2 changing, 3 constant; fp16: 4 changing, 5 constant)."""
         out = ctypes.c_double(0.0)
         check(lib.dn_mfma_calibrate(self._h, int(mode), ctypes.byref(out)), self._h)
         return out.value
@@ -289,7 +303,7 @@ class Engine:
         return C
 
     def gemm_device(self, precision: str, M, N, K, d_A: int, d_B: int, d_C: int, accumulate=False) -> None:
-        p = {"bf16": native.DN_PRECISION_BF16, "fp32": native.DN_PRECISION_FP32}[precision]
+        p = native.PRECISIONS[precision]
         check(lib.dn_gemm_device(self._h, p, M, N, K, ctypes.c_void_p(d_A), ctypes.c_void_p(d_B),
                                  ctypes.c_void_p(d_C), int(accumulate)), self._h)
 

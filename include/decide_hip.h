@@ -42,7 +42,7 @@ enum {
   DN_UNSUPPORTED = 5    /* geometry or mode this build does not implement */
 };
 
-enum { DN_PRECISION_FP32 = 0, DN_PRECISION_BF16 = 1 };
+enum { DN_PRECISION_FP32 = 0, DN_PRECISION_BF16 = 1, DN_PRECISION_FP16 = 2 };
 
 typedef struct dn_ctx dn_ctx;
 
@@ -73,8 +73,12 @@ int dn_set_stream(dn_ctx *ctx, void *stream);
 /* Model geometry, the fields of nn.Config (internal/nn/config.go:12-27;
  * defaults from LoadConfig :33-95) plus the arithmetic mode:
  * DN_PRECISION_BF16 = bf16 GEMM/attention operands, fp32 accumulate,
- * residual stream, statistics and head; DN_PRECISION_FP32 = fp32 MFMA
- * everywhere (the validation build). Must precede dn_upload_tensor.
+ * residual stream, statistics and head; DN_PRECISION_FP16 = the same with
+ * IEEE binary16 operands (11-bit significand where bf16 has 8: projection
+ * weights rounded to nearest fp16, activations stored in fp16; same MFMA
+ * rate and bytes; inference only; a projection weight of magnitude >= 65520
+ * gives DN_UNSUPPORTED); DN_PRECISION_FP32 = fp32 MFMA everywhere (the
+ * validation build). Must precede dn_upload_tensor.
  * Replaces the config capture of gpunn.New (internal/gpunn/model.go:80-122).
  * head_dim 64 with hidden % 256 == 0 (<= 1024) and inter % 64 == 0
  * (ModernBERT-base: 768/1152/12 heads) runs the MFMA kernels; other
@@ -88,14 +92,16 @@ int dn_set_config(dn_ctx *ctx, int hidden, int inter, int heads, int layers, int
 
 /* Uploads one parameter by its nn.Model.Tensors() name
  * (internal/nn/model.go:51-84), as n float32 values in that tensor's layout.
- * bf16 mode converts the four projection matrices to bf16 (round to nearest
- * even) and interleaves the Wi rows for the fused GeGLU epilogue.
+ * bf16 (fp16) mode converts the four projection matrices to bf16 (fp16),
+ * rounding to nearest even, and interleaves the Wi rows for the fused GeGLU
+ * epilogue.
  * Replaces the per-tensor upload loop of gpunn.New (model.go:80-122). */
 int dn_upload_tensor(dn_ctx *ctx, const char *name, const float *data, int64_t n);
 
 /* The same upload from bfloat16 bits, as a BF16 entry of a safetensors
  * bundle holds them (n uint16 values, little-endian bit patterns). bf16 mode
  * stores the projection matrices' bits as given (no float32 round trip);
+ * fp16 mode converts them to binary16 (exact for magnitudes 2^-17 .. 65504);
  * every other tensor, and every tensor in fp32 mode, is widened exactly to
  * float32. Replaces the BF16 branch of safetensors.(*File).Float32
  * (internal/safetensors/safetensors.go:113-124) followed by the upload. */
@@ -193,6 +199,28 @@ int dn_set_stream_split(dn_ctx *ctx, int min_tokens);
  * (forward.go:212-243 runs every layer over all tokens, then gathers). */
 int dn_set_row_tail(dn_ctx *ctx, int min_tokens);
 
+/* Certified argmax for the 16-bit modes. The reference answers a question
+ * with the argmax of its options' float32 logits (local.go:254-262, :291);
+ * a bf16 / fp16 forward moves each logit by its rounding error, so options
+ * closer than that error may swap. With margin > 0, every dn_forward and
+ * dn_forward_device checks each sequence's logits (dn_evaluate lays out one
+ * question per sequence): a sequence whose two largest logits are less than
+ * `margin` apart, or with a non-finite logit, is run again on an fp32 twin of
+ * the context (same geometry and weights in float32, fp32 MFMA: the
+ * validation mode) and its logits are replaced. The margin should bound the
+ * 16-bit path's error of a logit difference; measured on ModernBERT-base
+ * random-init requests: fp16 1.2e-4 RMS (5e-4 max over 1,000 requests), bf16
+ * 1.0e-3 RMS. dn_forward_device becomes synchronous and expects each
+ * sequence's rows to be its mask positions (rows are assigned to sequences by
+ * token index). Must follow dn_set_config and precede the weight uploads
+ * (which then also go to the twin); 0 turns it off. Training contexts and
+ * the fp32 mode refuse it; dn_forward_device_noalloc returns the 16-bit
+ * logits unchecked. No counterpart in the reference (its GPU path is fp32). */
+int dn_set_certify(dn_ctx *ctx, float margin);
+/* Sequences checked and recomputed by certification since the last call
+ * (then reset to 0). */
+int dn_read_certify(dn_ctx *ctx, int64_t *checked, int64_t *recomputed);
+
 /* Waits for the context's stream. */
 int dn_synchronize(dn_ctx *ctx);
 
@@ -218,14 +246,15 @@ enum { DN_PROBE_BWD_WGRAD_QKV = 0, DN_PROBE_BWD_DGRAD_QKV = 1, DN_PROBE_BWD_ATTE
 int dn_read_probe_backward(dn_ctx *ctx, double *ms /* [3] */, int *count);
 
 /* Attainable MFMA rate of this GPU (TFLOP/s), for the roofline: a
- * register-only loop of v_mfma_f32_32x32x16_bf16 (modes 0, 1) or
+ * register-only loop of v_mfma_f32_32x32x16_bf16 (modes 0, 1),
  * v_mfma_f32_32x32x2_f32 (modes 2, 3: the fp32 validation mode and
- * dn_gemm_f32) in the projection GEMMs' wave pattern on every CU, no memory
- * traffic. Modes 0 and 2: operands with the forward's statistics
- * (activations ~ N(0,1), weights ~ N(0,0.02)) that change every iteration, as
- * a real GEMM's do; modes 1 and 3: constant operands. The matrix core runs
- * slower the more its inputs toggle, so modes 0 and 2 are the ceilings a GEMM
- * on real data can approach. Synchronous (~10 ms). No counterpart in the
+ * dn_gemm_f32) or v_mfma_f32_32x32x16_f16 (modes 4, 5) in the projection
+ * GEMMs' wave pattern on every CU, no memory traffic. Modes 0, 2 and 4:
+ * operands with the forward's statistics (activations ~ N(0,1), weights ~
+ * N(0,0.02)) that change every iteration, as a real GEMM's do; modes 1, 3
+ * and 5: constant operands. The matrix core runs slower the more its inputs
+ * toggle, so modes 0, 2 and 4 are the ceilings a GEMM on real data can
+ * approach. Synchronous (~10 ms). No counterpart in the
  * reference. */
 int dn_mfma_calibrate(dn_ctx *ctx, int mode, double *tflops);
 

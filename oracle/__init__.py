@@ -40,6 +40,7 @@ def lib():
         L = ctypes.CDLL(_LIB_PATH)
         L.orc_set_workers.argtypes = [ctypes.c_int]
         L.orc_set_rounding.argtypes = [ctypes.c_int]
+        L.orc_set_rounding_layers.argtypes = [ctypes.c_int, ctypes.c_int]
         L.orc_get_workers.restype = ctypes.c_int
         gemm_args = [ctypes.c_int] * 5 + [ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_int,
                                           ctypes.c_void_p, ctypes.c_int, ctypes.c_int]
@@ -106,8 +107,9 @@ def set_workers(n: int) -> None:
 ROUND_XN, ROUND_QKV, ROUND_QK, ROUND_P, ROUND_CTX, ROUND_ACT = 1, 2, 4, 8, 16, 32
 
 
-def set_rounding(mask: int) -> None:
+def set_rounding(mask: int, layers=(0, 1 << 30)) -> None:
     lib().orc_set_rounding(int(mask))
+    lib().orc_set_rounding_layers(int(layers[0]), int(layers[1]))
 
 
 def _ptr(a: np.ndarray) -> int:

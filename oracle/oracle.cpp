@@ -133,6 +133,8 @@ int g_workers = 1;  // runtime.GOMAXPROCS(0) / blas.Workers
 // path stores or multiplies them, so that the effect of each stage on the
 // logits can be measured on the CPU. 0 (the default) is the reference.
 int g_round = 0;
+int g_round_lo = 0, g_round_hi = 1 << 30;  // layers [lo, hi) round; the others are exact
+int g_round_now = 0;                         // the current layer's switches
 enum : int {
   RND_XN = 1,     // LayerNorm outputs feeding QKV and Wi (and layer 0's emb-norm output)
   RND_QKV = 2,    // the QKV GEMM's stored output, before RoPE
@@ -162,8 +164,8 @@ inline float fp16_round(float x) {
   return x;
 }
 void round_if(int bit, float *x, size_t n) {
-  if (!(g_round & bit)) return;
-  if (g_round & RND_FP16)
+  if (!(g_round_now & bit)) return;
+  if (g_round_now & RND_FP16)
     for (size_t i = 0; i < n; i++) x[i] = fp16_round(x[i]);
   else
     for (size_t i = 0; i < n; i++) x[i] = bf16_round(x[i]);
@@ -540,6 +542,11 @@ void orc_set_workers(int n) { g_workers = n < 1 ? 1 : n; }
 
 // Stage rounding switches (RND_* bits above); 0 restores the reference.
 void orc_set_rounding(int mask) { g_round = mask; }
+// Restricts the stage rounding to encoder layers [lo, hi).
+void orc_set_rounding_layers(int lo, int hi) {
+  g_round_lo = lo;
+  g_round_hi = hi;
+}
 int orc_get_workers(void) { return g_workers; }
 
 // blas.Sgemm (gemm.go:61) with an explicit worker count (Sgemm1 == workers 1).
@@ -744,6 +751,7 @@ int forward_impl(const Model &m, int nseq, const int32_t *seq_len, const int32_t
     LayerCache &lc = keep ? c.lc[l] : frozen;
     bool sliding = cfg.sliding[l] != 0;
     // layerFwd, forward.go:284-343.
+    g_round_now = l >= g_round_lo && l < g_round_hi ? g_round : 0;
     const float *in = cur;
     const float *x1 = in;
     if (l > 0) {  // layer 0 has no attn_norm (model.go:13-14, forward.go:289-294)
@@ -753,7 +761,7 @@ int forward_impl(const Model &m, int nseq, const int32_t *seq_len, const int32_t
       layer_norm(lc.n1.data(), in, T, H, attnNorm, nullptr, cfg.eps, lc.mean1.data(), lc.rstd1.data());
       x1 = lc.n1.data();
       round_if(RND_XN, lc.n1.data(), (size_t)T * H);
-    } else if (g_round & RND_XN) {
+    } else if (g_round_now & RND_XN) {
       x0r.assign(in, in + (size_t)T * H);
       round_if(RND_XN, x0r.data(), x0r.size());
       x1 = x0r.data();
@@ -764,7 +772,7 @@ int forward_impl(const Model &m, int nseq, const int32_t *seq_len, const int32_t
     round_if(RND_QKV, lc.qkv.data(), (size_t)T * 3 * H);
     apply_rope(lc.qkv.data(), T, H, cfg.heads, D, sliding ? c.cosL.data() : c.cosG.data(),
                sliding ? c.sinL.data() : c.sinG.data());
-    if (g_round & RND_QK)
+    if (g_round_now & RND_QK)
       for (int t = 0; t < T; t++) round_if(RND_QK, &lc.qkv[(size_t)t * 3 * H], (size_t)2 * H);
     lc.ctx.resize((size_t)T * H);
     if (keep) lc.P.assign(pTotal, 0);

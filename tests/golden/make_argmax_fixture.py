@@ -1,11 +1,13 @@
 """Writes tests/golden/argmax_1000.npz: the CPU oracle's logits for 1,000
 requests (500 shaped like cfg2: 64-token premise + 3 options x 16; 500 like
 cfg5: 40-token premise + 2 options x 12), each with its own seed, on
-ModernBERT-base geometry with random_weights(seed=0), twice: with those
-float32 weights (logits_f32w), and with the four projection matrices rounded
-to bfloat16 (round to nearest even; logits_bf16w), the values a BF16 bundle
-holds and the bf16 device path multiplies, so that both sides run identical
-weights. The oracle is the C++
+ModernBERT-base geometry with random_weights(seed=0), three times: with those
+float32 weights (logits_f32w); with the four projection matrices rounded to
+bfloat16 (round to nearest even; logits_bf16w), the values a BF16 bundle
+holds and the bf16 device path multiplies; and with them rounded to IEEE
+binary16 (nearest even; logits_f16w), the values the fp16 device path
+multiplies; so that each device mode can be checked against the oracle on
+identical weights. The oracle is the C++
 restatement of the reference's Go forward and is bit-identical for any worker
 count, so these logits are what the reference's CPU path gives for the same
 weights and ids. The GPU test regenerates the ids from the seeds and checks
@@ -53,6 +55,11 @@ def bf16_projection_weights(w):
     return out
 
 
+def f16_projection_weights(w):
+    """The projection matrices rounded to binary16 (nearest even), widened back."""
+    return {name: (a.astype(np.float16).astype(np.float32) if name.endswith(PROJ) else a) for name, a in w.items()}
+
+
 def main():
     import oracle
     from decide_amd import modernbert_base
@@ -64,7 +71,8 @@ def main():
     w = random_weights(cfg, seed=0)
     t0 = time.time()
     out = {}
-    for key, weights in (("logits_f32w", w), ("logits_bf16w", bf16_projection_weights(w))):
+    for key, weights in (("logits_f32w", w), ("logits_bf16w", bf16_projection_weights(w)),
+                         ("logits_f16w", f16_projection_weights(w))):
         model = oracle.OracleModel(cfg, weights)
         out[key] = np.concatenate([model.forward(batch[i:i + 50]) for i in range(0, len(batch), 50)]).astype(
             np.float32)

@@ -98,29 +98,32 @@ def test_gemm_cfg1(eng):
     assert ratio <= 1.0 and rel <= 1e-5
 
 
+@pytest.mark.parametrize("prec", ["bf16", "fp16"])
 @pytest.mark.parametrize("M,N,K", [(64, 2304, 768), (112, 2304, 768), (1000, 2304, 768), (2048, 2304, 768),
                                    (3000, 768, 2304), (5000, 768, 1152)])
-def test_gemm_bf16_device(eng, M, N, K):
-    """bf16 operands, fp32 accumulate: against float64 of the same bf16 values.
-    Shapes cover every tile config of the fp32 epilogue: whole-K small-M,
-    64 x 128, 64 x 192 and 128 x 192 (ragged last row tiles)."""
+def test_gemm_16bit_device(eng, prec, M, N, K):
+    """bf16 / fp16 operands, fp32 accumulate: against float64 of the same
+    16-bit values. Shapes cover every tile config of the fp32 epilogue:
+    whole-K small-M, 64 x 128, 64 x 192 and 128 x 192 (ragged last row
+    tiles)."""
     import torch
 
+    dt = torch.bfloat16 if prec == "bf16" else torch.float16
     g = torch.Generator().manual_seed(M)
-    A = torch.randn(M, K, generator=g).to(torch.bfloat16)
-    B = (torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16)
+    A = torch.randn(M, K, generator=g).to(dt)
+    B = (torch.randn(N, K, generator=g) * 0.02).to(dt)
     exact = A.double() @ B.double().T
     bound = A.double().abs() @ B.double().abs().T
     dA, dB = A.cuda(), B.cuda()
     dC = torch.zeros(M, N, dtype=torch.float32, device="cuda")
     torch.cuda.synchronize()
-    eng.gemm_device("bf16", M, N, K, dA.data_ptr(), dB.data_ptr(), dC.data_ptr())
+    eng.gemm_device(prec, M, N, K, dA.data_ptr(), dB.data_ptr(), dC.data_ptr())
     eng.synchronize()
     err = (dC.cpu().double() - exact).abs()
     assert float((err / (1e-5 * bound + 1e-30)).max()) <= 1.0
 
 
-@pytest.mark.parametrize("prec", ["bf16", "fp32"])
+@pytest.mark.parametrize("prec", ["bf16", "fp16", "fp32"])
 @pytest.mark.parametrize("M,N,K", [(1, 2304, 768), (31, 768, 1152), (33, 384, 768), (64, 2304, 768),
                                    (65, 768, 768), (112, 768, 1152), (128, 2304, 64), (100, 128, 4096)])
 def test_gemm_small_m(eng, prec, M, N, K):
@@ -130,7 +133,7 @@ def test_gemm_small_m(eng, prec, M, N, K):
     bit (the reduction order does not depend on timing)."""
     import torch
 
-    dt = torch.bfloat16 if prec == "bf16" else torch.float32
+    dt = {"bf16": torch.bfloat16, "fp16": torch.float16, "fp32": torch.float32}[prec]
     g = torch.Generator().manual_seed(M * 7 + N + K)
     A = torch.randn(M, K, generator=g).to(dt)
     B = (torch.randn(N, K, generator=g) * 0.02).to(dt)

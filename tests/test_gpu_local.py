@@ -6,8 +6,8 @@ Also: BF16 bundles (bf16 bits uploaded as stored) and the error paths.
 Bars: fp32 mode, rounded probabilities within 1e-4 (one unit of the
 4th place, since a 1e-6 difference can cross a rounding boundary), Score
 expectation within 0.01, confidence within 0.001, the same choice; bf16
-mode, probabilities within 2e-3 plus one rounding unit. The fp32 cases pin
-the batching itself."""
+and fp16 modes, probabilities within 2e-3 plus one rounding unit. The fp32
+cases pin the batching itself."""
 import json
 import os
 
@@ -105,16 +105,18 @@ def check_answers(resp, want, qs, prec):
     print(f"{prec}: worst |dp| (rounded) {worst:.3g}", flush=True)
 
 
-@pytest.mark.parametrize("prec,dt", [("fp32", "F32"), ("bf16", "BF16"), ("fp32", "BF16")])
-def test_system_one_matches_serial_oracle(bundles, prec, dt):
+@pytest.mark.parametrize("prec,dt,cert", [("fp32", "F32", 0), ("bf16", "BF16", 0), ("fp32", "BF16", 0),
+                                          ("fp16", "F32", 0), ("fp16", "BF16", 0), ("fp16", "BF16", 1e-3)])
+def test_system_one_matches_serial_oracle(bundles, prec, dt, cert):
     """The oracle runs the weights the bundle stores (BF16 widened exactly),
-    so in bf16 mode only the activation rounding differs."""
+    so in bf16 mode only the activation rounding differs. cert: the certified
+    argmax's margin (dn_set_certify)."""
     from decide_amd import bundle
     from decide_amd.local import format_state
 
     d, cfg, om = bundles[dt]
-    print(f"case: system_one {prec} {dt} bundle", flush=True)
-    loc = bundle.load_bundle(d, precision=prec, encoder=(byte_encode, MIN_MASK))
+    print(f"case: system_one {prec} {dt} bundle, certify {cert}", flush=True)
+    loc = bundle.load_bundle(d, precision=prec, encoder=(byte_encode, MIN_MASK), certify=cert)
     qs = questions()
     resp = loc.system_one(STATE, qs)
     assert resp["model"] == "decide-test-0" and resp["order"] == [q for q, _ in qs]
@@ -129,7 +131,7 @@ def test_system_one_matches_serial_oracle(bundles, prec, dt):
     loc.engine.close()
 
 
-@pytest.mark.parametrize("prec", ["fp32", "bf16"])
+@pytest.mark.parametrize("prec", ["fp32", "bf16", "fp16"])
 def test_many_questions_long_state(bundles, prec):
     """24 questions over a ~1500-token state: one forward of 24 sequences
     (the GEMMs take the large-M path) against 24 serial oracle forwards."""
@@ -156,7 +158,7 @@ def test_many_questions_long_state(bundles, prec):
     loc.engine.close()
 
 
-@pytest.mark.parametrize("prec", ["fp32", "bf16"])
+@pytest.mark.parametrize("prec", ["fp32", "bf16", "fp16"])
 def test_bf16_upload_equals_widened_f32(bundles, prec):
     """dn_upload_tensor_bf16(bits) gives the same device model as
     dn_upload_tensor(widen(bits)): identical logits, bit for bit."""

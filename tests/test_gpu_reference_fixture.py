@@ -100,7 +100,7 @@ def test_reference_fixture_bf16(tiny_ref):
     assert dp <= 2e-3
 
 
-@pytest.mark.parametrize("prec", ["fp32", "bf16"])
+@pytest.mark.parametrize("prec", ["fp32", "bf16", "fp16"])
 def test_generic_geometry_matches_oracle(prec):
     """hidden 96, 6 heads of 16, intermediate 80, half window 8, global and
     local layers; an independent-options sequence, a plain one and a short
@@ -122,7 +122,8 @@ def test_generic_geometry_matches_oracle(prec):
     with engine(cfg, w, prec) as eng:
         got = eng.forward(batch)
     oracle.set_workers(4)
-    wb = w if prec == "fp32" else {n: (bf16_round(a) if n.endswith(PROJ) else a) for n, a in w.items()}
+    rnd = {"fp32": None, "bf16": bf16_round, "fp16": lambda a: np.asarray(a, np.float16).astype(np.float32)}[prec]
+    wb = w if rnd is None else {n: (rnd(a) if n.endswith(PROJ) else a) for n, a in w.items()}
     want = oracle.OracleModel(cfg, wb).forward(batch)
     if prec == "fp32":
         assert np.all(np.abs(got.astype(np.float64) - want) <= 1e-5 * (1 + np.abs(want)))

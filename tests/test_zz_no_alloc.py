@@ -33,7 +33,7 @@ def _run(eng, batch, noalloc):
     return out.cpu().numpy()
 
 
-@pytest.mark.parametrize("precision", ["bf16", "fp32"])
+@pytest.mark.parametrize("precision", ["bf16", "fp16", "fp32"])
 def test_noalloc_matches_forward_device(precision):
     from decide_amd import Engine, NoGPUError, modernbert_base
     from decide_amd.synth import config_batch, random_weights
