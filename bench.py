@@ -689,6 +689,10 @@ def main() -> int:
     result["host_io_tokens_per_s"] = round(T / float(np.median(hio)), 1)
     if not args.no_extra_configs and args.config == "cfg3" and prec != "fp32":
         result["configs"] = extra_configs(eng, cfg, dev, stream, args)
+    if not args.no_extra_configs and prec == "bf16" and not args.certify:
+        eng.close()
+        eng = None
+        result["certified_fp16"] = certified_run(cfg, weights, dev, stream, args)
     if not args.no_cpu_baseline:
         log("cpu baseline")
         result["cpu_baseline"] = cpu_baseline(cfg, weights, args.config, args.cpu_budget)
@@ -696,9 +700,58 @@ def main() -> int:
         result["host_cpu"] = host_cpu_info()
         if "configs" in result:
             result["configs"]["cfg1"]["oracle_sgemm"] = [cpu_gemm_cfg1(cpu_threads()), cpu_gemm_cfg1(1)]
-    eng.close()
+    if eng is not None:
+        eng.close()
     print(json.dumps(result), flush=True)
     return 0
+
+
+def certified_run(cfg, weights, dev, stream, args, margin=1e-3) -> dict:
+    """The same workload with the answers certified against the reference
+    (fp16 operands + dn_set_certify: sequences whose two best logits are
+    closer than `margin`, ~8x the fp16 path's RMS error of a logit difference,
+    are recomputed on the fp32 twin inside the step), and the latency of one
+    cfg2 / cfg5 request through dn_forward in that mode."""
+    import torch
+
+    from decide_amd import Engine
+
+    eng = Engine(cfg, weights, precision="fp16", certify=margin)
+    eng.set_stream(stream.cuda_stream)
+    eng.set_stream_split(args.stream_split)
+    eng.set_row_tail(args.row_tail)
+    wl = Workload(eng, cfg, args.config, dev, nseq=args.nseq)
+    for _ in range(args.warmup):
+        wl.step()
+    torch.cuda.synchronize()
+    eng.read_certify()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        wl.step()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    checked, recomputed = eng.read_certify()
+    out = {"precision": "fp16", "certify_margin": margin, "tokens_per_s": round(wl.T * args.steps / wall, 1),
+           "ms_per_step": round(wall * 1e3 / args.steps, 4), "sequences_checked": checked,
+           "sequences_recomputed_fp32": recomputed,
+           "timed_call": "dn_forward_device with dn_set_certify (synchronous: logits read back, near-ties "
+                         "recomputed on the fp32 twin, logits written back)"}
+    for name, reps in (("cfg2", 500), ("cfg5", 2000)):
+        w2 = Workload(eng, cfg, name, dev)
+        for _ in range(20):
+            w2.host_forward()
+        eng.read_certify()
+        lat = np.empty(reps)
+        for r in range(reps):
+            t1 = time.perf_counter()
+            w2.host_forward()
+            lat[r] = time.perf_counter() - t1
+        _, rc = eng.read_certify()
+        out[name] = {"latency_ms_p50": round(float(np.percentile(lat, 50)) * 1e3, 4),
+                     "latency_ms_p99": round(float(np.percentile(lat, 99)) * 1e3, 4),
+                     "requests": reps, "recomputed": rc}
+    eng.close()
+    return out
 
 
 class Workload:

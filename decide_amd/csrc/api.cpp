@@ -960,6 +960,10 @@ int forward_core(dn_ctx *c, int nseq, const int32_t *seq_len, const int32_t *d_i
     if (rc) return rc;
   }
   const int T = w.T;
+  // The split-K residual GEMMs (partials summed by the next LayerNorm) are an
+  // inference path: a training forward's frozen layers keep the whole-K
+  // kernels, the summation order of its trainable ones.
+  if (train) w.part = nullptr;
   if (train) {
     tr.layers.resize(L);
     for (int l = tr.train_from; l < L; l++) {

@@ -446,9 +446,11 @@ hipError_t launch_cfg_one(const GemmArgs &a, hipStream_t s, int splits = 1) {
 //     prefetching the next group while the current one is multiplied.
 //   * The waves' partial tiles are summed through LDS in a fixed order, so
 //     results do not depend on timing, by the threads that store the
-//     result (one barrier). (Splitting K across workgroups would
-//     need a device-scope release/acquire per workgroup, which on gfx950 is
-//     an L2 writeback + invalidate and costs more than it saves.)
+//     result (one barrier). Splitting K across workgroups of one launch
+//     would need a device-scope release/acquire per workgroup (an L2
+//     writeback + invalidate on gfx950); instead launch_gemm_small_split
+//     gives each K slice its own fp32 partial tile and the kernel that
+//     follows (the next LayerNorm, launch_ln_parts) sums the slices.
 // Operand layout: in load j of a group, lane l reads the 16 bytes of row
 // l%32 at group offset 2*VPL*j + VPL*(l/32); for bf16 that is exactly the
 // k step j operand of v_mfma_f32_32x32x16_bf16, for fp32 the four values

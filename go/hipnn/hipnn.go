@@ -25,6 +25,8 @@ import (
 	"fmt"
 	"os"
 	"runtime"
+	"strconv"
+	"strings"
 	"sync"
 
 	"github.com/ebitengine/purego"
@@ -47,7 +49,14 @@ const (
 const (
 	PrecisionFP32 int32 = 0 // fp32 MFMA everywhere: the validation mode
 	PrecisionBF16 int32 = 1 // bf16 GEMM / attention operands, fp32 accumulation
+	PrecisionFP16 int32 = 2 // binary16 operands (11-bit significands), fp32 accumulation
 )
+
+// DefaultCertifyMargin is the dn_set_certify margin the decide.Local wiring
+// uses with PrecisionFP16: about 8x the fp16 forward's RMS error of a
+// difference of two logits on ModernBERT-base (1.2e-4), so a question whose
+// two best options are closer than that is answered from the fp32 path.
+const DefaultCertifyMargin float32 = 1e-3
 
 // Question kinds of dn_evaluate (DN_KIND_*), decide.Local's evalChoice /
 // evalScore / evalNoul (local.go:264-356).
@@ -65,6 +74,7 @@ type api struct {
 	setConfig    func(ctx uintptr, hidden, inter, heads, layers, vocab int32, eps float32, halfWindow int32, thetaG, thetaL float64, sliding *uint8, precision int32) int32
 	uploadTensor func(ctx uintptr, name string, data *float32, n int64) int32
 	weightsReady func(ctx uintptr) int32
+	setCertify   func(ctx uintptr, margin float32) int32
 	forward      func(ctx uintptr, nseq int32, seqLen, ids, pos, optID, nmask, maskPos *int32, logits *float32, capacity int32) int32
 	evaluate     func(ctx uintptr, nq int32, kind, nOpt, qLen, ids *int32, temperature *float64, maskID int32, independent int32, probs *float64, choice *int32, confidence, value *float64) int32
 }
@@ -108,6 +118,7 @@ func Load() error {
 		reg(&lib.setConfig, "dn_set_config")
 		reg(&lib.uploadTensor, "dn_upload_tensor")
 		reg(&lib.weightsReady, "dn_weights_ready")
+		reg(&lib.setCertify, "dn_set_certify")
 		reg(&lib.forward, "dn_forward")
 		reg(&lib.evaluate, "dn_evaluate")
 		if missing != "" {
@@ -128,6 +139,14 @@ type Model struct {
 // (internal/nn/model.go:51-84). It replaces cuda.Open + gpunn.New in
 // train.NewInferer (internal/train/engine.go:152-167).
 func New(m *nn.Model, precision int32) (*Model, error) {
+	return NewWith(m, precision, 0)
+}
+
+// NewWith is New with certified argmax (dn_set_certify): with certifyMargin >
+// 0 in a 16-bit precision, a sequence whose two largest logits are closer
+// than the margin is recomputed on the library's fp32 twin, so its Choice
+// comes out as the float32 reference's.
+func NewWith(m *nn.Model, precision int32, certifyMargin float32) (*Model, error) {
 	if err := Load(); err != nil {
 		return nil, err
 	}
@@ -165,6 +184,13 @@ func New(m *nn.Model, precision int32) (*Model, error) {
 		err := g.err(rc)
 		g.Free()
 		return nil, err
+	}
+	if certifyMargin > 0 {
+		if rc := lib.setCertify(ctx, certifyMargin); rc != dnOK {
+			err := g.err(rc)
+			g.Free()
+			return nil, err
+		}
 	}
 	for _, t := range m.Tensors() {
 		if len(t.Data) == 0 {
@@ -260,10 +286,38 @@ type Result struct {
 	Value      float64   // Score expectation (2 places) or Noul p(true) (4 places)
 }
 
+// QuestionError is a dn_evaluate failure of one question: Index is its
+// position in the Evaluate call, Err the reason ("input contains the reserved
+// [MASK] token", ...). decide.Local reports it under the question's id.
+type QuestionError struct {
+	Index int
+	Err   error
+}
+
+func (e *QuestionError) Error() string { return fmt.Sprintf("decide: question %d: %v", e.Index, e.Err) }
+func (e *QuestionError) Unwrap() error { return e.Err }
+
+// questionError turns dn_evaluate's "decide: question N: reason" into a
+// *QuestionError; other errors pass through.
+func questionError(err error) error {
+	const pre = "decide: question "
+	msg := err.Error()
+	if !strings.HasPrefix(msg, pre) {
+		return err
+	}
+	num, reason, ok := strings.Cut(msg[len(pre):], ": ")
+	idx, perr := strconv.Atoi(num)
+	if !ok || perr != nil {
+		return err
+	}
+	return &QuestionError{Index: idx, Err: errors.New(reason)}
+}
+
 // Evaluate answers every question of one call with a single forward: the
 // batched form of Local.Evaluate's loop (local.go:126-150) over evalChoice /
-// evalScore / evalNoul. An error names the first failing question by index
-// ("decide: question 3: ..."); the caller substitutes the question's id.
+// evalScore / evalNoul. Questions with at most one option (not Noul) carry
+// no IDs and are answered without the model, as evalChoice / evalScore do. A
+// failure of one question is a *QuestionError naming its index.
 func (g *Model) Evaluate(qs []Question, maskID int32, independent bool) ([]Result, error) {
 	n := len(qs)
 	if n == 0 {
@@ -287,7 +341,7 @@ func (g *Model) Evaluate(qs []Question, maskID int32, independent bool) ([]Resul
 	}
 	if rc := lib.evaluate(g.ctx, int32(n), &kind[0], &nOpt[0], &qLen[0], ptr32(ids), &temp[0], maskID, ind,
 		&probs[0], &choice[0], &conf[0], &value[0]); rc != dnOK {
-		return nil, g.err(rc)
+		return nil, questionError(g.err(rc))
 	}
 	out := make([]Result, n)
 	off := 0

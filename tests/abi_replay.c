@@ -9,16 +9,23 @@
  *   New      dn_open(0) -> DN_NO_GPU is ErrNoGPU; dn_set_config,
  *            dn_upload_tensor per Tensors() entry, dn_weights_ready.
  *   Forward  the flattened batch through dn_forward.
+ *   Evaluate the questions of one SystemOne call through dn_evaluate (one
+ *            forward for all of them, as the wired decide.Local does).
  *   Free     dn_close.
  *
  * Without argv[3] the replay stops after dn_open (and dn_close when a device
  * was opened). argv[3] is a manifest written by tests/test_go_binding.py:
  *   config H I heads layers vocab eps half_window theta_g theta_l precision s_0 .. s_{layers-1}
+ *   certify MARGIN         (dn_set_certify, before the tensors; NewWith's call)
  *   tensor NAME N          (N float32 values, in order, from argv[4])
  *   seq n has_opt nmask    then lines: ids, pos, [opt], mask positions
+ *   question kind nopt n temperature   then a line of n token ids
+ *   evaluate mask_id independent       (last: the questions through dn_evaluate)
  * Output lines: "ErrNoGPU (...)", "error <status> <message>", "ok <nlogits>"
- * followed by "logit <float32 bits in hex>" per logit. Exit status 0 unless
- * the replay itself is broken (bad manifest, unexpected status). */
+ * followed by "logit <float32 bits in hex>" per logit; with `evaluate`,
+ * "answers <nq>" followed by "answer <choice> <confidence> <value> <probs...>"
+ * per question (doubles in %.17g). Exit status 0 unless the replay itself is
+ * broken (bad manifest, unexpected status). */
 #include <dlfcn.h>
 #include <stdint.h>
 #include <stdio.h>
@@ -33,6 +40,9 @@ typedef int (*upload_fn)(void *, const char *, const float *, int64_t);
 typedef int (*ready_fn)(const void *);
 typedef int (*forward_fn)(void *, int, const int32_t *, const int32_t *, const int32_t *, const int32_t *,
                           const int32_t *, const int32_t *, float *, int);
+typedef int (*certify_fn)(void *, float);
+typedef int (*evaluate_fn)(void *, int, const int32_t *, const int32_t *, const int32_t *, const int32_t *,
+                           const double *, int32_t, int, double *, int32_t *, double *, double *);
 
 enum { DN_OK = 0, DN_NO_GPU = 1 };
 
@@ -79,6 +89,8 @@ int main(int argc, char **argv) {
   upload_fn dn_upload_tensor = (upload_fn)need(h, "dn_upload_tensor");
   ready_fn dn_weights_ready = (ready_fn)need(h, "dn_weights_ready");
   forward_fn dn_forward = (forward_fn)need(h, "dn_forward");
+  certify_fn dn_set_certify = (certify_fn)need(h, "dn_set_certify");
+  evaluate_fn dn_evaluate = (evaluate_fn)need(h, "dn_evaluate");
 
   /* New */
   void *ctx = NULL;
@@ -121,8 +133,36 @@ int main(int argc, char **argv) {
   int nseq = 0, T = 0, R = 0;
   int32_t *seq_len = NULL, *ids = NULL, *pos = NULL, *opt = NULL, *nmask = NULL, *mask = NULL;
   int any_opt = 0;
+  int nq = 0, qtok = 0, do_eval = 0, eval_mask = 0, eval_ind = 0;
+  int32_t *qkind = NULL, *qnopt = NULL, *qlen = NULL, *qids = NULL;
+  double *qtemp = NULL;
   while (fscanf(mf, "%255s", word) == 1) {
-    if (!strcmp(word, "tensor")) {
+    if (!strcmp(word, "certify")) {
+      float margin;
+      if (fscanf(mf, "%f", &margin) != 1) return 2;
+      rc = dn_set_certify(ctx, margin);
+      if (rc != DN_OK) {
+        printf("error %d %s\n", rc, dn_last_error(ctx));
+        dn_close(ctx);
+        return 0;
+      }
+    } else if (!strcmp(word, "question")) {
+      int kd, k, n;
+      double t;
+      if (fscanf(mf, "%d %d %d %lf", &kd, &k, &n, &t) != 4) return 2;
+      qkind = realloc(qkind, sizeof(int32_t) * (nq + 1));
+      qnopt = realloc(qnopt, sizeof(int32_t) * (nq + 1));
+      qlen = realloc(qlen, sizeof(int32_t) * (nq + 1));
+      qtemp = realloc(qtemp, sizeof(double) * (nq + 1));
+      qids = realloc(qids, sizeof(int32_t) * (qtok + n + 1));
+      if (read_ints(mf, qids + qtok, n)) return 2;
+      qkind[nq] = kd, qnopt[nq] = k, qlen[nq] = n, qtemp[nq] = t;
+      nq++;
+      qtok += n;
+    } else if (!strcmp(word, "evaluate")) {
+      if (fscanf(mf, "%d %d", &eval_mask, &eval_ind) != 2) return 2;
+      do_eval = 1;
+    } else if (!strcmp(word, "tensor")) {
       char name[256];
       long long n;
       if (fscanf(mf, "%255s %lld", name, &n) != 2) return 2;
@@ -165,6 +205,29 @@ int main(int argc, char **argv) {
     printf("error weights not ready\n");
     dn_close(ctx);
     return 1;
+  }
+  if (do_eval) {
+    /* Evaluate: Model.Evaluate's single dn_evaluate call. */
+    int nprob = 0;
+    for (int q = 0; q < nq; q++) nprob += qnopt[q];
+    double *probs = calloc((size_t)nprob + 1, sizeof(double)), *conf = calloc((size_t)nq + 1, sizeof(double));
+    double *value = calloc((size_t)nq + 1, sizeof(double));
+    int32_t *choice = calloc((size_t)nq + 1, sizeof(int32_t));
+    rc = dn_evaluate(ctx, nq, qkind, qnopt, qlen, qids, qtemp, eval_mask, eval_ind, probs, choice, conf, value);
+    if (rc != DN_OK) {
+      printf("error %d %s\n", rc, dn_last_error(ctx));
+    } else {
+      printf("answers %d\n", nq);
+      for (int q = 0, po = 0; q < nq; po += qnopt[q], q++) {
+        printf("answer %d %.17g %.17g", choice[q], conf[q], value[q]);
+        for (int i = 0; i < qnopt[q]; i++) printf(" %.17g", probs[po + i]);
+        printf("\n");
+      }
+    }
+    dn_close(ctx);
+    free(probs), free(conf), free(value), free(choice);
+    free(qkind), free(qnopt), free(qlen), free(qids), free(qtemp), free(sliding);
+    return 0;
   }
   /* Forward */
   float *logits = calloc((size_t)R + 1, sizeof(float));

@@ -97,13 +97,24 @@ def test_binding_types_match_the_c_prototypes():
 
 def test_wiring_patch_names_the_binding():
     """The patch hooks both inference entry points and keeps ErrNoGPU's
-    fall-through (engine.go:42-61's pattern)."""
+    fall-through (engine.go:42-61's pattern); it applies to the reference
+    sources (checked with `patch -p1 --dry-run` where they are present)."""
     patch = open(os.path.join(ROOT, "go", "hipnn", "wiring.patch")).read()
     assert "+++ b/internal/train/engine.go" in patch and "+++ b/local.go" in patch
     assert patch.count("errors.Is(") >= 2 and "hipnn.ErrNoGPU" in patch
     assert "lm.dev.Forward([]nn.Sequence{seq})" in patch
+    # Local.Evaluate answers a whole call with one batched hipnn.Evaluate,
+    # per-question failures reported under the question's id
+    assert "lm.dev.Evaluate(" in patch and "var qe *hipnn.QuestionError" in patch
+    assert 'fmt.Errorf("decide: question %q: %w", id, err)' in patch
+    assert "hipnn.NewWith(b.Model, hipnn.PrecisionFP16, hipnn.DefaultCertifyMargin)" in patch
     for name in re.findall(r"hipnn\.(\w+)\(", patch):
         assert re.search(rf"^func {name}\(", open(GO_SRC).read(), re.M), name
+    ref = "/root/reference"
+    if os.path.isdir(ref) and shutil.which("patch"):
+        r = subprocess.run(["patch", "-p1", "--dry-run", "-i", os.path.join(ROOT, "go", "hipnn", "wiring.patch")],
+                           cwd=ref, capture_output=True, text=True)
+        assert r.returncode == 0, r.stdout + r.stderr
 
 
 @pytest.fixture(scope="module")
@@ -209,3 +220,101 @@ def test_replay_forward_matches_engine(replay, prec):
     bad = [batch[0], Sequence(ids=batch[1].ids, pos=batch[1].pos, opt=None, mask_pos=np.zeros(0, np.int32))]
     write_manifest(m, wb, cfg, w, bad, p)
     assert replay(str(m), str(wb))[1] == "error 2 nn: sequence 1 has no options"
+
+
+def _logits(out):
+    return np.array([struct.unpack("<f", bytes.fromhex(l.split()[1])[::-1])[0] for l in out if l.startswith("logit ")],
+                    np.float32)
+
+
+@pytest.mark.gpu
+def test_replay_reference_fixture(replay, tiny_ref):
+    """internal/gpunn/gpunn_test.go:119-164's check, through the binding's
+    call sequence: the reference's own PyTorch fixture (tiny_ref.safetensors:
+    its weights and its two packed sequences) through New -> Forward -> Free
+    from C in the fp32 mode. The logits match the fixture's PyTorch logits at
+    relErr <= 1e-4 (the reference test's bar) and the oracle's at
+    1e-5 * (1 + |logit|)."""
+    from conftest import rel_err, tiny_config, tiny_weights
+    from decide_amd.nn import build_sequence
+
+    tensors, meta = tiny_ref
+    cfg = tiny_config(meta)
+    w = tiny_weights(tensors, cfg)
+    batch = [build_sequence(s["ids"], meta["mask_id"], s["independent"]) for s in meta["seqs"]]
+    m, wb = replay.dir / "m_tiny.txt", replay.dir / "w_tiny.bin"
+    write_manifest(m, wb, cfg, w, batch, 0)
+    print("case: replay tiny_ref fixture fp32", flush=True)
+    out = replay(str(m), str(wb))
+    assert out[1] == f"ok {len(tensors['logits'])}", out[:3]
+    got = _logits(out)
+    err = rel_err(got, tensors["logits"])
+    oracle_mod = __import__("oracle")
+    oracle_mod.set_workers(4)
+    want = oracle_mod.OracleModel(cfg, w).forward(batch)
+    print(f"relErr against the PyTorch logits {err:.3g}; max |d| against the oracle "
+          f"{float(np.max(np.abs(got.astype(np.float64) - want))):.3g}", flush=True)
+    assert err <= 1e-4
+    assert np.all(np.abs(got.astype(np.float64) - want) <= 1e-5 * (1 + np.abs(want)))
+
+
+def _evaluate_manifest(path_m, path_w, cfg, w, precision, certify, qspecs, mask_id):
+    write_manifest(path_m, path_w, cfg, w, [], precision)
+    lines = open(path_m).read().splitlines()
+    if certify:
+        lines.insert(1, f"certify {certify!r}")
+    for kind, nopt, ids, temp in qspecs:
+        lines.append(f"question {kind} {nopt} {len(ids)} {temp!r}")
+        lines.append(" ".join(map(str, ids)))
+    lines.append(f"evaluate {mask_id} 1")
+    open(path_m, "w").write("\n".join(lines) + "\n")
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("prec,certify", [("fp32", 0.0), ("fp16", 1e-3)])
+def test_replay_evaluate_matches_serial_oracle(replay, prec, certify):
+    """The wired decide.Local's call from C: every question of one SystemOne
+    call through ONE dn_evaluate (hipnn.Evaluate), in the fp32 validation
+    mode and in the mode the wiring uses (fp16 + certified argmax, margin
+    1e-3), against the serial oracle, which answers each question with its own
+    Forward as local.go:126-204 does. Choice and Score argmaxes agree exactly;
+    rounded probabilities within 1e-4 (fp32) / 2e-3 + 1e-4 (fp16)."""
+    import oracle as orc
+
+    from decide_amd import local as L
+    from decide_amd.nn import config_from_dict
+    from decide_amd.synth import random_weights
+    from test_gpu_local import CAL, STATE, TINY, questions
+    from test_local import MIN_MASK, byte_encode
+
+    cfg = config_from_dict(TINY)
+    w = random_weights(cfg, seed=7, std=0.05)
+    cal = L.Calibration(CAL["temperature"], CAL["default"])
+    state = L.format_state(STATE)
+    qs = questions()
+    specs = []
+    for _, q in qs:
+        kind, texts, ck = L._options(q)
+        need = kind == L.DN_KIND_NOUL or len(texts) > 1
+        ids = byte_encode(L.pack_text(state, q.instructions, texts)) if need else []
+        specs.append((kind, len(texts), list(map(int, ids)), cal.temperature_for(ck)))
+    m, wb = replay.dir / f"m_eval_{prec}.txt", replay.dir / f"w_eval_{prec}.bin"
+    _evaluate_manifest(m, wb, cfg, w, {"fp32": 0, "fp16": 2}[prec], certify, specs, MIN_MASK)
+    print(f"case: replay dn_evaluate {prec} certify {certify}", flush=True)
+    out = replay(str(m), str(wb))
+    assert out[1] == f"answers {len(qs)}", out[:3]
+    orc.set_workers(4)
+    om = orc.OracleModel(cfg, w)
+    tol = 1e-4 + 1e-9 if prec == "fp32" else 2e-3 + 1e-4
+    names = {L.DN_KIND_CHOICE: "choice", L.DN_KIND_SCORE: "score", L.DN_KIND_NOUL: "noul"}
+    for (kind, nopt, ids, temp), line in zip(specs, out[2:]):
+        f = line.split()
+        assert f[0] == "answer"
+        choice, conf, value = int(f[1]), float(f[2]), float(f[3])
+        probs = np.array([float(x) for x in f[4:]])
+        want = orc.evaluate_question(om, names[kind], nopt, ids, MIN_MASK, True, temp)
+        assert len(probs) == len(want["probs"]) and choice == want["choice"], (line, want)
+        if nopt:
+            assert np.all(np.abs(probs - want["probs"]) <= tol), (line, want)
+        assert abs(value - want["value"]) <= tol * max(1, nopt) ** 2, (line, want)
+        assert abs(conf - want["confidence"]) <= 1e-3 + tol * max(1, nopt), (line, want)

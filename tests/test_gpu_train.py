@@ -238,6 +238,33 @@ def test_backward_frozen_layers_fp32():
         check_grads(eng, want, "fp32", train_from=2, train_emb=False, label="frozen")
 
 
+@pytest.mark.parametrize("prec", ["fp32", "bf16"])
+def test_backward_frozen_layers_small_batch(prec):
+    """A training forward of at most 128 tokens (the size at which inference
+    splits the residual GEMMs over K): frozen layers 0-1 and trainable layer 2
+    give the oracle's gradients (fp32 bar; bf16 against the oracle on the same
+    bf16-rounded projection weights at the bf16 bar), and the logits match an
+    inference forward of the same batch to fp32 rounding in fp32."""
+    from decide_amd import Engine
+    from decide_amd.train import TrainEngine
+
+    cfg = small_cfg()
+    w = weights_for(cfg)
+    batch = train_batch(cfg.vocab, cfg.vocab - 1, seed=11, specs=[(30, [5, 6], True), (60, [10, 12], True)])
+    assert sum(len(s.ids) for s in batch) <= 128
+    print(f"case: frozen layers, small batch {prec}", flush=True)
+    wref = effective_weights(w, prec)
+    _, dl, want = oracle_grads(cfg, wref, batch, train_from=2, train_emb=False)
+    with TrainEngine(cfg, w, precision=prec, train_from=2, train_emb=False) as eng:
+        got = eng.forward(batch)
+        eng.backward(dl)
+        check_grads(eng, want, prec, train_from=2, train_emb=False, label="frozen small batch")
+    if prec == "fp32":
+        with Engine(cfg, w, precision="fp32") as inf:
+            ref = inf.forward(batch)
+        assert np.all(np.abs(got.astype(np.float64) - ref) <= 1e-5 * (1 + np.abs(ref)))
+
+
 def test_backward_head_only_fp32():
     """trainFrom = Layers: only the final norm and the scorer head get
     gradients; no layer keeps activations (forward.go:226-236)."""
