@@ -155,9 +155,9 @@ def test_gemm_small_m(eng, prec, M, N, K):
 
 def test_mfma_calibrate(eng):
     """dn_mfma_calibrate returns a plausible rate for both operand modes (the
-    register-only loop of the bench's attainable-peak line), in bf16 (below
-    the 2.5 PFLOP/s peak) and fp32 (below 157.3 TFLOP/s); other modes are
-    refused."""
+    register-only loop of the bench's attainable-peak line), in bf16 and fp16
+    (below the 2.5 PFLOP/s peak) and fp32 (below 157.3 TFLOP/s); other modes
+    are refused."""
     from decide_amd import InvalidArgument
 
     changing, constant = eng.mfma_calibrate(0), eng.mfma_calibrate(1)
@@ -166,5 +166,8 @@ def test_mfma_calibrate(eng):
     c32, k32 = eng.mfma_calibrate(2), eng.mfma_calibrate(3)
     print(f"attainable fp32 MFMA: changing operands {c32:.1f}, constant {k32:.1f} TFLOP/s")
     assert 10.0 < c32 < 160.0 and 10.0 < k32 < 160.0
+    c16, k16 = eng.mfma_calibrate(4), eng.mfma_calibrate(5)
+    print(f"attainable fp16 MFMA: changing operands {c16:.0f}, constant {k16:.0f} TFLOP/s")
+    assert 100.0 < c16 < 2600.0 and 100.0 < k16 < 2600.0
     with pytest.raises(InvalidArgument):
-        eng.mfma_calibrate(4)
+        eng.mfma_calibrate(6)
