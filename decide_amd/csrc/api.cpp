@@ -384,7 +384,9 @@ int small_split_parts(int precision, int T, int N, int K) {
 
 // A projection GEMM of the model: the MFMA kernels, or the any-shape kernel
 // for geometries they do not tile.
-hipError_t layer_gemm(const Config &g, int epi, const GemmArgs &a, hipStream_t s) {
+hipError_t layer_gemm(const Config &g, int epi, const GemmArgs &a0, hipStream_t s) {
+  GemmArgs a = a0;
+  a.skinny_regs = g.skinny_regs ? 1 : 0;
   return g.generic ? launch_gemm_generic(g.precision, epi, a, s) : launch_gemm(g.precision, epi, a, s);
 }
 
@@ -485,6 +487,7 @@ int enqueue_layer(dn_ctx *c, const Pass &p, int l, float *in, float *h1, float *
   void *x2 = S ? S->n2.p : w.xn;
   const int wo_parts = split ? small_split_parts(prec, T, H, H) : 1;
   if (wo_parts > 1) {
+    o.skinny_regs = g.skinny_regs ? 1 : 0;
     PROBED(ev, DN_PROBE_WO, "gemm(Wo)", launch_gemm_small_split(prec, o, wo_parts, w.part, s));
     HIPCHK(c, "ln(mlp_norm)", launch_ln_parts(prec, h1, w.part, wo_parts, T, H,
                                               (const float *)W(c, pf + "mlp_norm.weight"), g.eps, x2, s));
@@ -530,6 +533,7 @@ int enqueue_layer(dn_ctx *c, const Pass &p, int l, float *in, float *h1, float *
   mo.accumulate = 1;
   const int parts = split && mo_parts ? small_split_parts(prec, T, H, I) : 1;
   if (mo_parts) *mo_parts = parts > 1 ? parts : 0;
+  mo.skinny_regs = g.skinny_regs ? 1 : 0;
   if (parts > 1)
     PROBED(ev, DN_PROBE_MLPWO, "gemm(MlpWo)", launch_gemm_small_split(prec, mo, parts, w.part, s));
   else
@@ -1572,6 +1576,12 @@ int dn_set_stream_split(dn_ctx *c, int min_tokens) {
   if (!c || min_tokens < 0) return DN_INVALID_ARG;
   c->err.clear();
   c->split_min_tokens = min_tokens;
+  return DN_OK;
+}
+
+int dn_set_small_m_loads(dn_ctx *c, int mode) {
+  if (!c || (mode != 0 && mode != 1)) return DN_INVALID_ARG;
+  c->cfg.skinny_regs = mode == 0;
   return DN_OK;
 }
 

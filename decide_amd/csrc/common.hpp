@@ -239,6 +239,8 @@ struct GemmArgs {
   void *C2;         // EPI_GEGLU_KEEP: the GeGLU output (ldc2), C receives the plain product
   int ldc2;
   const void *gin;  // EPI_GEGLU_BWD: the GeGLU input (the Wi output, M x 2N, row stride ldc)
+  int skinny_regs;  // small-M kernel, 16-bit 32 x 32 tiles: operands loaded straight into registers
+                    // (0: whole 128-byte rows through LDS by global->LDS DMA)
 };
 
 // GEMM epilogues: fp32 store / accumulate, store in the operand type, GeGLU of

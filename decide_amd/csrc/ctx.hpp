@@ -45,6 +45,9 @@ struct Config {
   // intermediate % 64): any-shape GEMM and attention kernels, Wi stored in its
   // natural layout, no training.
   bool generic = false;
+  // Small-M GEMMs on 32 x 32 tiles (16-bit): operands straight into registers
+  // instead of through LDS (dn_set_small_m_loads; the same results).
+  bool skinny_regs = false;
 };
 
 // Activations of one layer kept by a training forward (the reference's

@@ -53,6 +53,17 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
 }
 
+// One 16-byte LDS read whose completion the caller waits for itself
+// (s_waitcnt lgkmcnt): the compiler does not see it as a read of memory that
+// global->LDS DMA writes, so it adds no vmcnt wait of its own before it.
+__device__ __forceinline__ uint4 lds_read16(const char *p) {
+  typedef int i32x4 __attribute__((ext_vector_type(4)));
+  const uint32_t a = (uint32_t)(size_t)(const __attribute__((address_space(3))) char *)p;
+  i32x4 v;
+  asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(a) : "memory");
+  return __builtin_bit_cast(uint4, v);
+}
+
 template <int BM, int BN>
 struct TileOrder {
   int m0, n0;
@@ -478,11 +489,20 @@ __device__ __forceinline__ fvec<V> partial_sum(const float *red, int idx) {
   return v;
 }
 
-template <class T, int MB, int NB, int EPI, int W, bool F16 = false>
+template <class T, int MB, int NB, int EPI, int W, bool F16 = false, bool DMA = false>
 __global__ __launch_bounds__(64 * W) void gemm_skinny_kernel(GemmArgs g) {
   using MF = Mfma<T>;
   typedef typename MF::frag frag;
   static_assert(!F16 || sizeof(T) == 2, "16 x 16 blocks: 16-bit operands");
+  static_assert(!DMA || (F16 && MB == 1 && NB == 1 && W == 8), "LDS operand path: 16-bit 32 x 32 tiles, 8 waves");
+  // DMA: each wave stages its K groups through a private two-slot LDS slab.
+  // A group's 32 A rows and 32 B rows (128 bytes each) arrive by eight
+  // wave-wide global->LDS loads, lane l carrying 16 bytes of row 8j + l/8, so
+  // every row is read as one whole 128-byte segment (the register path's
+  // lanes read 64-byte pieces of 16 rows per instruction); the fragments are
+  // then read from LDS in the same layout the register path loads them in,
+  // so both paths feed the MFMAs the same operands in the same order.
+  constexpr int SLAB = 64 * 128;  // bytes of one group (64 rows x 128 bytes)
   // F16: the tile as 16 x 16 blocks of the 16 x 16 x 32 MFMA, whose operand
   // lanes read 64 contiguous bytes of a row (four lanes x 16 bytes) where the
   // 32 x 32 x 16 form reads 32 (two lanes): half the cache-line sectors per
@@ -505,7 +525,10 @@ __global__ __launch_bounds__(64 * W) void gemm_skinny_kernel(GemmArgs g) {
   // The fp32 epilogue works on items of FV floats, two when that gives every
   // thread one item; NQ items per thread.
   constexpr int FV = TE <= 2 * NT ? 2 : 4, TEV = TE / FV, NQ = (TEV + NT - 1) / NT;
-  __shared__ __attribute__((aligned(16))) float red[NP * TE];
+  // The partial tiles; in DMA mode the same memory first holds the waves'
+  // slabs (W x 2 groups), and a barrier separates the two uses.
+  constexpr int RED = DMA && W * 2 * SLAB / 4 > NP * TE ? W * 2 * SLAB / 4 : NP * TE;
+  __shared__ __attribute__((aligned(1024))) float red[RED];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, lr = lane & 31, lh = lane >> 5;
   const int n0 = blockIdx.x * TC, m0 = blockIdx.y * TR;
@@ -557,7 +580,7 @@ __global__ __launch_bounds__(64 * W) void gemm_skinny_kernel(GemmArgs g) {
   const int ngrp = g.K / GK;
   uint4 la[RB][NS], lb[CB][NS];
   int grp = wave;
-  if (grp < ngrp) SKINNY_LOAD(la, lb, grp);
+  if (!DMA && grp < ngrp) SKINNY_LOAD(la, lb, grp);
   // The fp32 epilogue's residual input, loaded now (behind the first operand
   // group) so its latency overlaps the main loop instead of following the
   // reduction; each element is read and then written by this thread only.
@@ -573,6 +596,76 @@ __global__ __launch_bounds__(64 * W) void gemm_skinny_kernel(GemmArgs g) {
       if (g.accumulate && vec && q < TEV && m0 + r < g.M && col + FV <= g.n_store)
         pre[k] = *(const fvec<FV> *)(R + (size_t)(m0 + r) * g.ldc + col);
     }
+  }
+  if constexpr (DMA) {
+    // Slab row r < 32 is A row m0 + r, r >= 32 the B row of tile column
+    // r - 32 (the mapping of bp above). DMA load j of a group fills slab
+    // rows 8j .. 8j+7; lane l brings the 16-byte chunk (l % 8) ^ swz(row) of
+    // row 8j + l / 8 into LDS slot l % 8 of that row, so a row's logical
+    // chunk c sits in slot c ^ swz(row) (the XOR swizzle spreads the 16 rows
+    // a quarter-wave reads over distinct banks).
+    const int wv = __builtin_amdgcn_readfirstlane(wave);
+    const char *dsrc[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      const int r = 8 * j + (lane >> 3);
+      const int c = (lane & 7) ^ swz<128>(r);
+      const T *row;
+      if (r < 32) {
+        row = (const T *)g.A + (size_t)min(m0 + r, g.M - 1) * g.lda;
+      } else {
+        const int cc = r - 32;
+        const int br = EPI == EPI_GEGLU ? (n0 & ~63) + (cc < 16 ? 0 : 32) + ((n0 >> 5) & 1) * 16 + (cc & 15) : n0 + cc;
+        row = (const T *)g.B + (size_t)br * g.ldb;
+      }
+      dsrc[j] = (const char *)(row + kz) + c * 16;
+    }
+    // The LDS reads are opaque to the compiler (lds_read16), so it adds no
+    // waits of its own for the DMA: the vmcnt waits below are the only ones.
+    auto issue = [&](int gi, int slot) {
+      char *dst = (char *)red + (wv * 2 + slot) * SLAB;
+      const size_t kb = (size_t)gi * GK * sizeof(T);
+#pragma unroll
+      for (int j = 0; j < 8; j++)
+        __builtin_amdgcn_global_load_lds((gbl_void *)(dsrc[j] + kb), (lds_void *)(dst + j * 1024), 16, 0, 0);
+    };
+    // This wave's groups: wv, wv + W, ... (the register path's order).
+    const int myn = wv < ngrp ? (ngrp - 1 - wv) / W + 1 : 0;
+    if (myn > 0) issue(wv, 0);
+    if (myn > 1) issue(wv + W, 1);
+    for (int i = 0; i < myn; i++) {
+      // Group i has landed once at most the next group's eight loads are
+      // outstanding (the residual loads above are older and count as done).
+      if (i + 1 < myn) wait_vmcnt<8>();
+      else wait_vmcnt<0>();
+      const char *sl = (const char *)red + (wv * 2 + (i & 1)) * SLAB;
+#pragma unroll
+      for (int q = 0; q < NS; q++) {
+        const int c = (lane >> 4) + 4 * q;  // the register path's k chunk for this lane
+#pragma unroll
+        for (int b = 0; b < 2; b++) {
+          const int ra = 16 * b + (lane & 15), rb = 32 + ra;
+          la[b][q] = lds_read16(sl + ra * 128 + ((c ^ swz<128>(ra)) << 4));
+          lb[b][q] = lds_read16(sl + rb * 128 + ((c ^ swz<128>(rb)) << 4));
+        }
+      }
+      // The fragments are in registers (lgkmcnt(0)): the MFMAs may use them
+      // and the slot can be refilled with group i + 2.
+      __builtin_amdgcn_s_waitcnt(0xc07f);
+      if (i + 2 < myn) issue(wv + (i + 2) * W, i & 1);
+#pragma unroll
+      for (int q = 0; q < NS; q++)
+#pragma unroll
+        for (int a = 0; a < RB; a++)
+#pragma unroll
+          for (int b = 0; b < CB; b++)
+            acc[a][b] = mma16x16<T>(__builtin_bit_cast(frag, la[a][q]), __builtin_bit_cast(frag, lb[b][q]), acc[a][b]);
+    }
+    // Every load has landed and every wave is done with its slab before the
+    // partial tiles reuse the memory.
+    wait_vmcnt<0>();
+    __syncthreads();
+    grp = ngrp;  // the register loop below does nothing
   }
   for (; grp < ngrp; grp += W) {
     uint4 na[RB][NS], nb[CB][NS];
@@ -736,16 +829,25 @@ __global__ __launch_bounds__(64 * W) void gemm_skinny_kernel(GemmArgs g) {
 template <class T, int MB, int NB, int W>
 hipError_t launch_skinny_cfg(int epi, const GemmArgs &a, hipStream_t s, int splits = 1) {
   constexpr bool F = sizeof(T) == 2 && MB == 1 && NB == 1;
+  constexpr bool D = F && W == 8;  // the LDS operand path exists for these tiles
   dim3 grid(a.N / (32 * NB), (a.M + 32 * MB - 1) / (32 * MB), splits), block(64 * W);
+  const bool dma = D && !a.skinny_regs;
+#define SKINNY_LAUNCH(E)                                                                        \
+  do {                                                                                          \
+    if (dma)                                                                                    \
+      hipLaunchKernelGGL((gemm_skinny_kernel<T, MB, NB, E, W, F, D>), grid, block, 0, s, a);   \
+    else                                                                                        \
+      hipLaunchKernelGGL((gemm_skinny_kernel<T, MB, NB, E, W, F>), grid, block, 0, s, a);      \
+  } while (0)
   switch (epi) {
     case EPI_F32:
-      hipLaunchKernelGGL((gemm_skinny_kernel<T, MB, NB, EPI_F32, W, F>), grid, block, 0, s, a);
+      SKINNY_LAUNCH(EPI_F32);
       break;
     case EPI_STORE:
-      hipLaunchKernelGGL((gemm_skinny_kernel<T, MB, NB, EPI_STORE, W, F>), grid, block, 0, s, a);
+      SKINNY_LAUNCH(EPI_STORE);
       break;
     case EPI_GEGLU:
-      hipLaunchKernelGGL((gemm_skinny_kernel<T, MB, NB, EPI_GEGLU, W, F>), grid, block, 0, s, a);
+      SKINNY_LAUNCH(EPI_GEGLU);
       break;
     default:
       if constexpr (NB == 2 && !std::is_same<T, f16>::value)
@@ -753,6 +855,7 @@ hipError_t launch_skinny_cfg(int epi, const GemmArgs &a, hipStream_t s, int spli
       else return hipErrorInvalidValue;
       break;
   }
+#undef SKINNY_LAUNCH
   return hipGetLastError();
 }
 

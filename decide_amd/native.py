@@ -71,6 +71,7 @@ _SIGS = {
     "dn_set_stream_split": ([_vp, _i], _i),
     "dn_set_row_tail": ([_vp, _i], _i),
     "dn_set_certify": ([_vp, _c.c_float], _i),
+    "dn_set_small_m_loads": ([_vp, _i], _i),
     "dn_read_certify": ([_vp, _c.POINTER(_c.c_int64), _c.POINTER(_c.c_int64)], _i),
     "dn_set_probe": ([_vp, _i], _i),
     "dn_read_probe": ([_vp, _f64p, _c.POINTER(_i)], _i),

@@ -274,6 +274,10 @@ class Engine:
         quarter of them) finish the last layer on the option rows only (0: off)."""
         check(lib.dn_set_row_tail(self._h, int(min_tokens)), self._h)
 
+    def set_small_m_loads(self, mode: int) -> None:
+        """dn_set_small_m_loads: 1 operands of the small-M GEMMs through LDS (default), 0 into registers."""
+        check(lib.dn_set_small_m_loads(self._h, int(mode)), self._h)
+
     def set_certify(self, margin: float) -> None:
         """dn_set_certify: sequences whose two best logits are closer than margin
         (or not finite) are recomputed on an fp32 twin (16-bit modes; before the

@@ -199,6 +199,14 @@ int dn_set_stream_split(dn_ctx *ctx, int min_tokens);
  * (forward.go:212-243 runs every layer over all tokens, then gathers). */
 int dn_set_row_tail(dn_ctx *ctx, int min_tokens);
 
+/* How the small-M GEMM kernel (batches of at most 128 tokens, 16-bit modes,
+ * 32 x 32 output tiles) loads its operands: 1 (the default) whole 128-byte
+ * rows into LDS by global->LDS DMA, then the MFMA fragments from LDS; 0 each
+ * lane's fragment straight into registers. Both feed the same MFMAs the same
+ * operands in the same order: the logits are identical. No counterpart in
+ * the reference. */
+int dn_set_small_m_loads(dn_ctx *ctx, int mode);
+
 /* Certified argmax for the 16-bit modes. The reference answers a question
  * with the argmax of its options' float32 logits (local.go:254-262, :291);
  * a bf16 / fp16 forward moves each logit by its rounding error, so options

@@ -72,3 +72,24 @@ def test_small_batch_matches_oracle(base_small, total):
     want = orc.forward(batch)
     for prec in ("fp32", "bf16", "fp16"):
         compare(engs[prec].forward(batch), want, batch, prec)
+
+
+@pytest.mark.parametrize("prec", ["bf16", "fp16"])
+def test_small_m_operand_paths_agree(base_small, prec):
+    """dn_set_small_m_loads: the small-M GEMM's two operand paths (whole rows
+    through LDS by global->LDS DMA, the default; fragments straight into
+    registers) feed the MFMAs the same operands in the same order, so every
+    batch size gives bit-identical logits."""
+    cfg, _, engs = base_small
+    eng = engs[prec]
+    rng = np.random.default_rng(77)
+    try:
+        for total in TOTALS:
+            batch = batch_with_total(total, cfg.vocab, rng)
+            eng.set_small_m_loads(1)
+            lds = eng.forward(batch)
+            eng.set_small_m_loads(0)
+            regs = eng.forward(batch)
+            assert np.array_equal(lds, regs), (total, float(np.max(np.abs(lds - regs))))
+    finally:
+        eng.set_small_m_loads(1)
