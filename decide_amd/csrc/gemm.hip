@@ -53,15 +53,36 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
 }
 
-// One 16-byte LDS read whose completion the caller waits for itself
-// (s_waitcnt lgkmcnt): the compiler does not see it as a read of memory that
-// global->LDS DMA writes, so it adds no vmcnt wait of its own before it.
-__device__ __forceinline__ uint4 lds_read16(const char *p) {
+// Eight 16-byte LDS reads and the wait for them (s_waitcnt lgkmcnt(0)) in
+// one statement, so the outputs hold the data when the statement ends (an
+// asm output counts as written at the end of its statement; were the wait a
+// separate statement, a register copy the compiler placed in between would
+// read a value not yet landed). The compiler does not see these as reads of
+// memory that global->LDS DMA writes, so it adds no vmcnt wait of its own:
+// the caller waits for the DMA explicitly.
+__device__ __forceinline__ void lds_read8x16(const char *const (&p)[8], uint4 (&o)[8]) {
   typedef int i32x4 __attribute__((ext_vector_type(4)));
-  const uint32_t a = (uint32_t)(size_t)(const __attribute__((address_space(3))) char *)p;
-  i32x4 v;
-  asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(a) : "memory");
-  return __builtin_bit_cast(uint4, v);
+  uint32_t a[8];
+#pragma unroll
+  for (int i = 0; i < 8; i++) a[i] = (uint32_t)(size_t)(const __attribute__((address_space(3))) char *)p[i];
+  i32x4 v0, v1, v2, v3, v4, v5, v6, v7;
+  asm volatile(
+      "ds_read_b128 %0, %8\n\t"
+      "ds_read_b128 %1, %9\n\t"
+      "ds_read_b128 %2, %10\n\t"
+      "ds_read_b128 %3, %11\n\t"
+      "ds_read_b128 %4, %12\n\t"
+      "ds_read_b128 %5, %13\n\t"
+      "ds_read_b128 %6, %14\n\t"
+      "ds_read_b128 %7, %15\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(v0), "=&v"(v1), "=&v"(v2), "=&v"(v3), "=&v"(v4), "=&v"(v5), "=&v"(v6), "=&v"(v7)
+      : "v"(a[0]), "v"(a[1]), "v"(a[2]), "v"(a[3]), "v"(a[4]), "v"(a[5]), "v"(a[6]), "v"(a[7])
+      : "memory");
+  o[0] = __builtin_bit_cast(uint4, v0), o[1] = __builtin_bit_cast(uint4, v1);
+  o[2] = __builtin_bit_cast(uint4, v2), o[3] = __builtin_bit_cast(uint4, v3);
+  o[4] = __builtin_bit_cast(uint4, v4), o[5] = __builtin_bit_cast(uint4, v5);
+  o[6] = __builtin_bit_cast(uint4, v6), o[7] = __builtin_bit_cast(uint4, v7);
 }
 
 template <int BM, int BN>
@@ -620,7 +641,7 @@ __global__ __launch_bounds__(64 * W) void gemm_skinny_kernel(GemmArgs g) {
       }
       dsrc[j] = (const char *)(row + kz) + c * 16;
     }
-    // The LDS reads are opaque to the compiler (lds_read16), so it adds no
+    // The LDS reads are opaque to the compiler (lds_read8x16), so it adds no
     // waits of its own for the DMA: the vmcnt waits below are the only ones.
     auto issue = [&](int gi, int slot) {
       char *dst = (char *)red + (wv * 2 + slot) * SLAB;
@@ -639,19 +660,28 @@ __global__ __launch_bounds__(64 * W) void gemm_skinny_kernel(GemmArgs g) {
       if (i + 1 < myn) wait_vmcnt<8>();
       else wait_vmcnt<0>();
       const char *sl = (const char *)red + (wv * 2 + (i & 1)) * SLAB;
+      const char *fp[8];
+      uint4 fr[8];
 #pragma unroll
       for (int q = 0; q < NS; q++) {
         const int c = (lane >> 4) + 4 * q;  // the register path's k chunk for this lane
 #pragma unroll
         for (int b = 0; b < 2; b++) {
           const int ra = 16 * b + (lane & 15), rb = 32 + ra;
-          la[b][q] = lds_read16(sl + ra * 128 + ((c ^ swz<128>(ra)) << 4));
-          lb[b][q] = lds_read16(sl + rb * 128 + ((c ^ swz<128>(rb)) << 4));
+          fp[4 * q + b] = sl + ra * 128 + ((c ^ swz<128>(ra)) << 4);
+          fp[4 * q + 2 + b] = sl + rb * 128 + ((c ^ swz<128>(rb)) << 4);
         }
       }
-      // The fragments are in registers (lgkmcnt(0)): the MFMAs may use them
-      // and the slot can be refilled with group i + 2.
-      __builtin_amdgcn_s_waitcnt(0xc07f);
+      // The fragments are in registers when this returns: the MFMAs may use
+      // them and the slot can be refilled with group i + 2.
+      lds_read8x16(fp, fr);
+#pragma unroll
+      for (int q = 0; q < NS; q++)
+#pragma unroll
+        for (int b = 0; b < 2; b++) {
+          la[b][q] = fr[4 * q + b];
+          lb[b][q] = fr[4 * q + 2 + b];
+        }
       if (i + 2 < myn) issue(wv + (i + 2) * W, i & 1);
 #pragma unroll
       for (int q = 0; q < NS; q++)
