@@ -625,7 +625,7 @@ def main() -> int:
                 "frac": round(wi_bytes / wi_s / 8e12, 4), "traffic": None,
                 "algorithmic_bytes_per_launch": wi_bytes}
     else:
-        roof = {"kernel": f"gemm_nt_kernel<{tname},128,192,64,3,EPI_F32,2,2,2> (Wo and MlpWo + fp32 residual), "
+        roof = {"kernel": f"gemm_nt_kernel<{tname},128,384,64,3,EPI_F32,2,2,4> (Wo and MlpWo + fp32 residual), "
                           "layer %d, average of its two launches" % args.probe_layer,
                 "bound": "hbm", "achieved": round(res_bytes / res_s / 1e9, 1), "peak": 8000.0, "unit": "GB/s",
                 "frac": round(res_bytes / res_s / 8e12, 4), "traffic": traffic.get("residual"),
@@ -927,7 +927,7 @@ def summarize_traffic(fetch_dir: str, write_dir: str, out_path: str) -> int:
     fetch_scale = copy_bytes / max(max(v) for k, v in fetch.items() if "copyBuffer" in k)
     write_scale = copy_bytes / max(max(v) for k, v in write.items() if "copyBuffer" in k)
     T = 32768
-    pick = {"residual": (128, 192, 0), "wi": (256, 128, 2), "qkv": (256, 128, 1)}  # BM, BN, epilogue
+    pick = {"residual": (128, 384, 0), "wi": (256, 128, 2), "qkv": (256, 128, 1)}  # BM, BN, epilogue
     alg = {"residual": (2 * (T * H + H * H) + 2 * (T * I + H * I) + 16 * T * H) / 2,
            "wi": 2 * (T * H + 2 * I * H + T * I), "qkv": 2 * (T * H + 3 * H * H + 3 * T * H)}
     kernels = {}

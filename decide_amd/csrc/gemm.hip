@@ -460,8 +460,11 @@ hipError_t launch_cfg(int epi, const GemmArgs &a, hipStream_t s, int splits = 1)
 template <class T, int BM, int BN, int RB, int NSTAGE, int WPE, int EPI = EPI_F32>
 hipError_t launch_cfg_one(const GemmArgs &a, hipStream_t s, int splits = 1) {
   static_assert(EPI == EPI_F32 || EPI == EPI_GEGLU_BWD, "epilogues that take 96-column wave tiles");
+  constexpr int WGN = BN / 96;  // 96-column wave tiles: 2 x 2 waves for 192 columns, 2 x 4 for 384
+  static_assert(WGN * 96 == BN && (WGN == 2 || WGN == 4), "96-column wave tiles");
   const int tiles = ((a.M + BM - 1) / BM) * (a.N / BN);
-  hipLaunchKernelGGL((gemm_nt_kernel<T, BM, BN, RB, NSTAGE, EPI, WPE, 2, 2>), dim3(tiles, splits), dim3(256), 0, s, a);
+  hipLaunchKernelGGL((gemm_nt_kernel<T, BM, BN, RB, NSTAGE, EPI, WPE, 2, WGN>), dim3(tiles, splits), dim3(128 * WGN),
+                     0, s, a);
   return hipGetLastError();
 }
 
@@ -1107,10 +1110,15 @@ hipError_t launch_gemm16(int epi, const GemmArgs &a, hipStream_t s) {
     if (epi == EPI_F32 && a.N % 192 == 0) {
       // 768-wide outputs in 192-column tiles: 3,840 rows make 240 tiles of
       // 64 x 192 for 256 CUs where 64 x 128 made 360 (dX GEMM N = 768,
-      // K = 2304: 30.6 -> 24.2 us isolated; Wo 16.2 -> 12.7 us); above 4096
-      // rows 128 x 192 at two workgroups per CU (cfg3's 32768 rows: 1024
-      // tiles, two full rounds of 512; forward 2.52 -> 2.56M tokens/s).
+      // K = 2304: 30.6 -> 24.2 us isolated; Wo 16.2 -> 12.7 us). Above 4096
+      // rows, 384-column tiles of 8 waves at one workgroup per CU (99 KB of
+      // LDS): the A panel is read twice instead of four times, and in the
+      // two-stream forward the other stream's kernels fit beside them (cfg3
+      // 2.68 -> 2.72M tokens/s, alternating runs on one box; alone each launch
+      // is 2-4% slower than 128 x 192 at two workgroups per CU, which remains
+      // for N not a multiple of 384).
       if (medium) return launch_cfg_one<T, 64, 192, 128, 4, 1>(a, s);
+      if (a.N % 384 == 0) return launch_cfg_one<T, 128, 384, 64, 3, 2>(a, s);
       return launch_cfg_one<T, 128, 192, 64, 3, 2>(a, s);
     }
     // GeGLU backward (N = 1152) at medium M: 64 x 192 at two workgroups per

@@ -100,12 +100,12 @@ def test_gemm_cfg1(eng):
 
 @pytest.mark.parametrize("prec", ["bf16", "fp16"])
 @pytest.mark.parametrize("M,N,K", [(64, 2304, 768), (112, 2304, 768), (1000, 2304, 768), (2048, 2304, 768),
-                                   (3000, 768, 2304), (5000, 768, 1152)])
+                                   (3000, 768, 2304), (5000, 768, 1152), (9000, 768, 768)])
 def test_gemm_16bit_device(eng, prec, M, N, K):
     """bf16 / fp16 operands, fp32 accumulate: against float64 of the same
     16-bit values. Shapes cover every tile config of the fp32 epilogue:
-    whole-K small-M, 64 x 128, 64 x 192 and 128 x 192 (ragged last row
-    tiles)."""
+    whole-K small-M, 64 x 128, 64 x 192 and the large-M tiles of the
+    768-wide residual GEMMs (ragged last row tiles)."""
     import torch
 
     dt = torch.bfloat16 if prec == "bf16" else torch.float16
