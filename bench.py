@@ -874,6 +874,13 @@ def extra_configs(eng, cfg, dev, stream, args) -> dict:
     return out
 
 
+# Template arguments <BM, BN, BK, STAGES, EPI, WG/CU, wave rows, wave cols>
+# of the 16-bit roofline kernels at cfg3 (launch_gemm16's choice for T =
+# 32768): the residual GEMMs (N = 768) and the Wi GEMM (N = 2 x 1152).
+ROOF_TILES = {"residual": [128, 384, 64, 3, 0, 2, 2, 4], "wi": [256, 128, 64, 3, 2, 2, 2, 2],
+              "qkv": [256, 128, 64, 3, 1, 2, 2, 2]}
+
+
 def read_traffic(config: str, prec: str) -> dict:
     """HBM bytes per launch of the roofline kernels, from the committed
     rocprofv3 FETCH_SIZE / WRITE_SIZE summary (profiles/), when it covers
@@ -883,7 +890,10 @@ def read_traffic(config: str, prec: str) -> dict:
         return {}
     with open(path) as fh:
         d = json.load(fh)
-    return {k: v.get("hbm_bytes_per_launch") for k, v in d.get("kernels", {}).items()}
+    # A summary of other tile shapes than the ones launched now describes
+    # another kernel: its bytes are not reported.
+    return {k: v.get("hbm_bytes_per_launch") for k, v in d.get("kernels", {}).items()
+            if v.get("template_args") == ROOF_TILES.get(k)}
 
 
 def summarize_traffic(fetch_dir: str, write_dir: str, out_path: str) -> int:
@@ -946,8 +956,14 @@ def summarize_traffic(fetch_dir: str, write_dir: str, out_path: str) -> int:
     others = {}
     for k, v in fetch.items():
         if "attention_kernel" in k or "ln_kernel" in k:
+            # Per symbol; the summary keeps each family's most-dispatched
+            # variant (attention: the full-batch layers, not the last layer's
+            # row-tail variant).
             tag = "attention" if "attention_kernel" in k else "layernorm"
-            others[tag] = {"symbol": k, "fetch_bytes_per_launch": round(float(np.mean(v)) * fetch_scale),
+            if tag in others and others[tag]["dispatches"] >= len(v):
+                continue
+            others[tag] = {"symbol": k, "dispatches": len(v),
+                           "fetch_bytes_per_launch": round(float(np.mean(v)) * fetch_scale),
                            "write_bytes_per_launch": round(float(np.mean(write.get(k, [0.0]))) * write_scale)}
     res = {"workload": "cfg3 (T=32768), bf16", "fetch_scale": fetch_scale, "write_scale": write_scale,
            "method": "rocprofv3 --pmc FETCH_SIZE and --pmc WRITE_SIZE (separate runs of bench.py --steps 2 "
