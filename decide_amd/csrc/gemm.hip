@@ -106,6 +106,42 @@ struct TileOrder {
   }
 };
 
+// Copies a staged tile (BM rows of V 16-byte vectors, LD elements apart in
+// LDS) to rows m0.. of C (row stride ldc, from column c0), rows past M
+// skipped. The LDS reads go in batches of eight ahead of their stores, so a
+// thread waits for LDS once per batch rather than once per vector.
+template <class T, int BM, int V, int NT, int LD>
+__device__ __forceinline__ void store_staged(const T *st, T *C, int ldc, int m0, int c0, int M, int tid) {
+  constexpr int EPV = 16 / sizeof(T), ITER = BM * V / NT;
+  static_assert(ITER * NT == BM * V, "staged tile shape");
+  if constexpr (ITER % 8 == 0) {
+    // One asm statement reads the batch and waits for it (lds_read8x16), so
+    // the compiler cannot sink each read into its store's row guard.
+#pragma unroll
+    for (int b0 = 0; b0 < ITER; b0 += 8) {
+      const char *p[8];
+      uint4 v[8];
+#pragma unroll
+      for (int u = 0; u < 8; u++) {
+        const int c = tid + (b0 + u) * NT;
+        p[u] = (const char *)(st + (c / V) * LD + (c % V) * EPV);
+      }
+      lds_read8x16(p, v);
+#pragma unroll
+      for (int u = 0; u < 8; u++) {
+        const int c = tid + (b0 + u) * NT, row = m0 + c / V;
+        if (row < M) *(uint4 *)(C + (size_t)row * ldc + c0 + (c % V) * EPV) = v[u];
+      }
+    }
+  } else {
+#pragma unroll
+    for (int u = 0; u < ITER; u++) {
+      const int c = tid + u * NT, row = m0 + c / V;
+      if (row < M) *(uint4 *)(C + (size_t)row * ldc + c0 + (c % V) * EPV) = *(const uint4 *)(st + (c / V) * LD + (c % V) * EPV);
+    }
+  }
+}
+
 // WGM x WGN waves tile the BM x BN block; each wave owns a WM x WN sub-tile.
 template <class T, int BM, int BN, int RB, int NSTAGE, int EPI, int WPE, int WGM, int WGN>
 __global__ __launch_bounds__(64 * WGM * WGN) __attribute__((amdgpu_waves_per_eu(WPE))) void gemm_nt_kernel(GemmArgs g) {
@@ -401,12 +437,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) __attribute__((amdgpu_waves_per_eu(
       const int oc0 = G ? n0 / 2 : n0;
       constexpr int EPV = 16 / sizeof(T);  // elements per 16-byte vector
       constexpr int V = OC / EPV;
-      for (int c = tid; c < BM * V; c += NT) {
-        const int r = c / V, cc = (c % V) * EPV;
-        const int row = m0 + r;
-        if (row >= g.M) continue;
-        *(uint4 *)(Cout + (size_t)row * ldo + oc0 + cc) = *(const uint4 *)(st + r * LD + cc);
-      }
+      store_staged<T, BM, V, NT, LD>(st, Cout, ldo, m0, oc0, g.M, tid);
     };
     if constexpr (EPI == EPI_STORE) {
       emit(std::false_type{}, (T *)gC, g.ldc);
