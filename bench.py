@@ -117,6 +117,76 @@ def cpu_gemm_cfg1(threads: int, budget_s: float = 3.0) -> dict:
     return {"gflops": round(2.0 * M * N * K * n / secs / 1e9, 2), "threads": threads, "calls": n}
 
 
+LIBGEMM_METRIC = ("projection GEMMs alone, back to back: this library's kernels vs hipBLASLt (torch.mm), "
+                  "bf16, ModernBERT-base shapes, 1 MI355X")
+
+
+def library_gemm(args) -> int:
+    """Times the forward's four projection shapes in isolation at cfg3's and
+    cfg4's token counts: QKV and Wi through dn_gemm_device_store (the plain
+    product rounded to bf16: Wi without its GeGLU), Wo and MlpWo through
+    dn_gemm_device (fp32 output added to C: the residual read-modify-write),
+    against torch.mm (hipBLASLt, bf16 output, no residual) with the activation
+    row stride the forward uses (K) and with K + 64. Repetitions alternate the
+    three. Back-to-back launches of one kernel run at a lower shader clock than
+    the same launch inside a forward, so these figures are not the forward's
+    per-launch times. Prints one JSON line."""
+    import torch
+
+    from decide_amd import Engine, modernbert_base
+
+    torch.cuda.init()
+    eng = Engine(modernbert_base(), None, precision="bf16")  # no weights: the GEMM entry points only
+    eng.set_stream(torch.cuda.current_stream().cuda_stream)
+
+    def timed(f, it=20):
+        for _ in range(3):
+            f()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(it):
+            f()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / it * 1e3
+
+    rows = []
+    for T, wl in ((32768, "cfg3"), (22528, "cfg4")):
+        for name, N, K in (("qkv", 3 * H, H), ("wi", 2 * I, H), ("wo", H, H), ("mlpwo", H, I)):
+            g = torch.Generator(device="cuda").manual_seed(T + N + K)
+            A = torch.randn(T, K + 64, device="cuda", generator=g).to(torch.bfloat16)
+            Bw = (torch.randn(N, K + 64, device="cuda", generator=g) * 0.02).to(torch.bfloat16)
+            Ac, Bc = A[:, :K].contiguous(), Bw[:, :K].contiguous()
+            Ap, Bp = A[:, :K], Bw[:, :K]  # row stride K + 64
+            if name in ("qkv", "wi"):
+                C = torch.empty(T, N, device="cuda", dtype=torch.bfloat16)
+                ours = lambda: eng.gemm_device_store("bf16", T, N, K, Ac.data_ptr(), Bc.data_ptr(), C.data_ptr())  # noqa: E731
+            else:
+                C = torch.zeros(T, N, device="cuda", dtype=torch.float32)
+                ours = lambda: eng.gemm_device("bf16", T, N, K, Ac.data_ptr(), Bc.data_ptr(), C.data_ptr(), True)  # noqa: E731
+            lib = lambda: torch.mm(Ac, Bc.t())  # noqa: E731
+            libp = lambda: torch.mm(Ap, Bp.t())  # noqa: E731
+            t = {"ours": [], "lib": [], "libp": []}
+            for _ in range(3):
+                t["ours"].append(timed(ours))
+                t["lib"].append(timed(lib))
+                t["libp"].append(timed(libp))
+            eng.check_device_errors()
+            flop = 2.0 * T * N * K
+            med = {k: float(np.median(v)) for k, v in t.items()}
+            rows.append({"workload": wl, "gemm": name, "M": T, "N": N, "K": K,
+                         "ours_us": round(med["ours"], 1), "ours_tflops": round(flop / med["ours"] / 1e6, 1),
+                         "hipblaslt_us": round(med["lib"], 1), "hipblaslt_tflops": round(flop / med["lib"] / 1e6, 1),
+                         "hipblaslt_lda_k_plus_64_us": round(med["libp"], 1)})
+            log(f"{wl} {name}: ours {med['ours']:.1f} us, hipBLASLt {med['lib']:.1f} us (lda K+64: {med['libp']:.1f})")
+            del A, Bw, Ac, Bc, C
+    print(json.dumps({"metric": LIBGEMM_METRIC, "unit": "us", "higher_is_better": False, "n_gpus": 1,
+                      "data": "synthetic: A N(0,1), B N(0,0.02), bf16", "results": rows}))
+    eng.close()
+    return 0
+
+
 SYSTEMONE_METRIC = ("SystemOne call: 24 questions (cfg4 mix) over a 2048-token state, answered with one "
                     "batched forward vs one forward per question, ModernBERT-base, 1 MI355X")
 
@@ -503,6 +573,8 @@ def main() -> int:
                     help="run one device copy of MIB MiB first (reference kernel for HBM counters)")
     ap.add_argument("--tokenizer", action="store_true",
                     help="time the host tokenizer (dn_tokenize) against HuggingFace tokenizers; no GPU")
+    ap.add_argument("--library-gemm", action="store_true",
+                    help="time the projection GEMM shapes alone: this library's kernels vs hipBLASLt (torch.mm)")
     ap.add_argument("--systemone", action="store_true",
                     help="time one SystemOne call (24 questions) batched into one forward vs one forward each")
     ap.add_argument("--train", action="store_true",
@@ -525,6 +597,8 @@ def main() -> int:
         return tokenizer_bench(args)
     if args.systemone:
         return systemone(args)
+    if args.library_gemm:
+        return library_gemm(args)
     if args.train:
         return train_bench(args)
 

@@ -1572,6 +1572,32 @@ int dn_gemm_device(dn_ctx *c, int precision, int M, int N, int K, const void *d_
   return DN_OK;
 }
 
+int dn_gemm_device_store(dn_ctx *c, int precision, int M, int N, int K, const void *d_A, const void *d_B, void *d_C) {
+  if (!c) return DN_INVALID_ARG;
+  c->err.clear();
+  if (precision != DN_PRECISION_BF16 && precision != DN_PRECISION_FP16)
+    return fail(c, DN_INVALID_ARG, "decide_hip: dn_gemm_device_store takes 16-bit operands (bf16, fp16)");
+  if (M < 0 || !d_A || !d_B || !d_C)
+    return fail(c, DN_INVALID_ARG, "decide_hip: dn_gemm_device_store: bad argument");
+  if (!gemm_shape_ok(precision, N, K))
+    return fail(c, DN_UNSUPPORTED, "decide_hip: dn_gemm_device_store needs N % 128 == 0 and K % 64 == 0");
+  (void)hipSetDevice(c->device);
+  GemmArgs a{};
+  a.A = d_A;
+  a.lda = K;
+  a.B = d_B;
+  a.ldb = K;
+  a.C = d_C;
+  a.ldc = N;
+  a.M = M;
+  a.N = N;
+  a.K = K;
+  a.n_store = N;
+  a.skinny_regs = c->cfg.skinny_regs ? 1 : 0;
+  HIPCHK(c, "gemm", launch_gemm(precision, EPI_STORE, a, c->stream));
+  return DN_OK;
+}
+
 int dn_set_stream_split(dn_ctx *c, int min_tokens) {
   if (!c || min_tokens < 0) return DN_INVALID_ARG;
   c->err.clear();

@@ -67,6 +67,7 @@ _SIGS = {
     "dn_check_device_errors": ([_vp], _i),
     "dn_gemm_f32": ([_vp, _i, _i, _i, _i, _i, _f32p, _i, _f32p, _i, _f32p, _i, _i], _i),
     "dn_gemm_device": ([_vp, _i, _i, _i, _i, _vp, _vp, _vp, _i], _i),
+    "dn_gemm_device_store": ([_vp, _i, _i, _i, _i, _vp, _vp, _vp], _i),
     "dn_synchronize": ([_vp], _i),
     "dn_set_stream_split": ([_vp, _i], _i),
     "dn_set_row_tail": ([_vp, _i], _i),

@@ -311,6 +311,12 @@ class Engine:
         check(lib.dn_gemm_device(self._h, p, M, N, K, ctypes.c_void_p(d_A), ctypes.c_void_p(d_B),
                                  ctypes.c_void_p(d_C), int(accumulate)), self._h)
 
+    def gemm_device_store(self, precision: str, M, N, K, d_A: int, d_B: int, d_C: int) -> None:
+        """dn_gemm_device_store: C (operand type) = A . B^T, rounded to the operand type."""
+        p = native.PRECISIONS[precision]
+        check(lib.dn_gemm_device_store(self._h, p, M, N, K, ctypes.c_void_p(d_A), ctypes.c_void_p(d_B),
+                                       ctypes.c_void_p(d_C)), self._h)
+
 
 def open_engine(cfg: Config, weights, precision="bf16", device=0) -> Engine:
     return Engine(cfg, weights, precision=precision, device=device)

@@ -176,6 +176,14 @@ int dn_gemm_f32(dn_ctx *ctx, int transA, int transB, int M, int N, int K, const 
 int dn_gemm_device(dn_ctx *ctx, int precision, int M, int N, int K, const void *d_A, const void *d_B,
                    float *d_C, int accumulate);
 
+/* The same GEMM with the output rounded to the operand type, as the forward
+ * stores its QKV projection: d_C[M x N] (bf16 or fp16, row stride N) =
+ * d_A[M x K] . d_B[N x K]^T, fp32 accumulate, round to nearest even. 16-bit
+ * precisions only; N % 128 == 0, K % 64 == 0. Asynchronous. Same reference
+ * counterpart as dn_gemm_device (linearFwd, forward.go:122-124). */
+int dn_gemm_device_store(dn_ctx *ctx, int precision, int M, int N, int K, const void *d_A, const void *d_B,
+                         void *d_C);
+
 /* Inference forwards (dn_forward, dn_forward_device, dn_evaluate) of batches
  * with at least min_tokens tokens and two or more sequences run in two parts
  * of whole sequences (cut nearest half the tokens; both parts must exceed

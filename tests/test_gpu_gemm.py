@@ -123,6 +123,39 @@ def test_gemm_16bit_device(eng, prec, M, N, K):
     assert float((err / (1e-5 * bound + 1e-30)).max()) <= 1.0
 
 
+@pytest.mark.parametrize("prec", ["bf16", "fp16"])
+@pytest.mark.parametrize("M,N,K", [(100, 2304, 768), (3000, 2304, 768), (20000, 2304, 768), (12000, 1536, 768)])
+def test_gemm_16bit_device_store(eng, prec, M, N, K):
+    """dn_gemm_device_store (the QKV epilogue: output rounded to the operand
+    type) at every tile config of that epilogue: small M, medium, the
+    large-M 256 x 128 tiles and N = 1536 (the last layer's K and V). Each
+    output must be the 16-bit rounding of a value within the fp32 error
+    bound of the float64 product, i.e. within half an output ulp plus that
+    bound; and it must equal the fp32-output GEMM (dn_gemm_device) rounded to
+    the same type, bit for bit (the same MFMA sums, rounded once)."""
+    import torch
+
+    dt = torch.bfloat16 if prec == "bf16" else torch.float16
+    g = torch.Generator().manual_seed(M + N)
+    A = torch.randn(M, K, generator=g).to(dt)
+    B = (torch.randn(N, K, generator=g) * 0.02).to(dt)
+    dA, dB = A.cuda(), B.cuda()
+    dC = torch.zeros(M, N, dtype=dt, device="cuda")
+    dF = torch.zeros(M, N, dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+    eng.gemm_device_store(prec, M, N, K, dA.data_ptr(), dB.data_ptr(), dC.data_ptr())
+    eng.gemm_device(prec, M, N, K, dA.data_ptr(), dB.data_ptr(), dF.data_ptr())
+    eng.synchronize()
+    assert torch.equal(dC.cpu(), dF.cpu().to(dt))
+    exact = A.double() @ B.double().T
+    bound = A.double().abs() @ B.double().abs().T
+    # half an ulp: 2^-8 (bf16, 8-bit significand) or 2^-11 (fp16) relative,
+    # 2^-25 absolute below fp16's normal range
+    half_ulp = exact.abs() * (2.0 ** -8 if prec == "bf16" else 2.0 ** -11) + 2.0 ** -25
+    err = (dC.cpu().double() - exact).abs()
+    assert float((err / (1e-5 * bound + half_ulp * 1.0001)).max()) <= 1.0
+
+
 @pytest.mark.parametrize("prec", ["bf16", "fp16", "fp32"])
 @pytest.mark.parametrize("M,N,K", [(1, 2304, 768), (31, 768, 1152), (33, 384, 768), (64, 2304, 768),
                                    (65, 768, 768), (112, 768, 1152), (128, 2304, 64), (100, 128, 4096)])
