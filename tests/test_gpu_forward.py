@@ -125,6 +125,57 @@ def test_small_geometry_ragged(small, prec):
             off += k
 
 
+def random_layout_batch(vocab, mask_id, seed):
+    """A seeded random batch: 1-24 sequences of 1-250 premise tokens and 0-6
+    options of 1-40 tokens, plain or independent; a few thousand tokens."""
+    from decide_amd.nn import build_sequence
+
+    rng = np.random.default_rng(1000 + seed)
+    out = []
+    for _ in range(int(rng.integers(1, 25))):
+        ids = list(rng.integers(2, mask_id, size=int(rng.integers(1, 251))))
+        nopt = int(rng.integers(0, 7))
+        for _ in range(nopt):
+            ln = int(rng.integers(1, 41))
+            ids += [mask_id] + list(rng.integers(2, mask_id, size=ln - 1))
+        if nopt == 0:
+            ids.append(mask_id)  # every sequence scores at least one row
+        ids.append(1)
+        out.append(build_sequence(np.array(ids, np.int32), mask_id, independent=bool(rng.integers(0, 2))))
+    return out
+
+
+@pytest.mark.parametrize("prec", ["fp32", "bf16"])
+def test_random_layouts_match_oracle(small, prec):
+    """Seeded random batch layouts (ragged lengths, option counts and
+    independence mixed) against the oracle, through each orchestration path
+    of the forward: one stream, the two-stream split (threshold lowered so
+    that the larger batches take it) and the option-row last layer (forced
+    on). fp32 holds the 1e-5 bar on every run; bf16 the small geometry's
+    1e-2 bar (its std 0.05 weights, as test_small_geometry_ragged)."""
+    from decide_amd import Engine, NoGPUError
+
+    cfg, w, orc = small
+    oracle.set_workers(WORKERS)
+    try:
+        eng = Engine(cfg, w, precision=prec)
+    except NoGPUError:
+        pytest.skip("no GPU")
+    with eng:
+        for seed in range(6):
+            batch = random_layout_batch(cfg.vocab, cfg.vocab - 1, seed)
+            want = orc.forward(batch)
+            ntok = sum(len(s.ids) for s in batch)
+            for split, tail in ((0, 0), (2048, 0), (0, 1), (2048, 1)):
+                eng.set_stream_split(split)
+                eng.set_row_tail(tail)
+                got = eng.forward(batch)
+                print(f"seed {seed}: {len(batch)} sequences, {ntok} tokens, split {split} tail {tail}", flush=True)
+                compare(got, want, batch, prec, bf16_dp=1e-2)
+        eng.set_stream_split(8192)
+        eng.set_row_tail(2048)
+
+
 # ---------------------------------------------------------------- ModernBERT-base
 @pytest.fixture(scope="module")
 def base():
