@@ -128,10 +128,12 @@ __device__ __forceinline__ float gelu_erf<float>(float x) {
 }
 // erf(x) for the bf16 path, whose result is rounded to bf16 (2^-9 relative)
 // anyway: the rational approximation 7.1.26 of Abramowitz & Stegun,
-// |error| <= 1.5e-7, evaluated with one exp2 and one reciprocal.
+// |error| <= 1.5e-7, evaluated with one exp2 and one hardware reciprocal
+// (v_rcp_f32, 1 ulp: a correctly rounded one compiles to the ten-instruction
+// IEEE division sequence, for an error far below the formula's own).
 __device__ __forceinline__ float erf_as(float x) {
   const float ax = fabsf(x);
-  const float t = __frcp_rn(1.0f + 0.3275911f * ax);
+  const float t = __builtin_amdgcn_rcpf(1.0f + 0.3275911f * ax);
   const float p = t * (0.254829592f + t * (-0.284496736f + t * (1.421413741f + t * (-1.453152027f + t * 1.061405429f))));
   const float y = 1.0f - p * exp2f(-ax * ax * 1.44269504088896341f);
   return copysignf(y, x);
