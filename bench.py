@@ -699,7 +699,7 @@ def main() -> int:
                 "frac": round(wi_bytes / wi_s / 8e12, 4), "traffic": None,
                 "algorithmic_bytes_per_launch": wi_bytes}
     else:
-        roof = {"kernel": f"gemm_nt_kernel<{tname},128,384,64,3,EPI_F32,2,2,4> (Wo and MlpWo + fp32 residual), "
+        roof = {"kernel": f"gemm_nt_kernel<{tname},256,192,128,2,EPI_F32,2,4,2> (Wo and MlpWo + fp32 residual), "
                           "layer %d, average of its two launches" % args.probe_layer,
                 "bound": "hbm", "achieved": round(res_bytes / res_s / 1e9, 1), "peak": 8000.0, "unit": "GB/s",
                 "frac": round(res_bytes / res_s / 8e12, 4), "traffic": traffic.get("residual"),
@@ -951,7 +951,7 @@ def extra_configs(eng, cfg, dev, stream, args) -> dict:
 # Template arguments <BM, BN, BK, STAGES, EPI, WG/CU, wave rows, wave cols>
 # of the 16-bit roofline kernels at cfg3 (launch_gemm16's choice for T =
 # 32768): the residual GEMMs (N = 768) and the Wi GEMM (N = 2 x 1152).
-ROOF_TILES = {"residual": [128, 384, 64, 3, 0, 2, 2, 4], "wi": [256, 128, 64, 3, 2, 2, 2, 2],
+ROOF_TILES = {"residual": [256, 192, 128, 2, 0, 2, 4, 2], "wi": [256, 128, 64, 3, 2, 2, 2, 2],
               "qkv": [256, 128, 64, 3, 1, 2, 2, 2]}
 
 
@@ -1011,13 +1011,11 @@ def summarize_traffic(fetch_dir: str, write_dir: str, out_path: str) -> int:
     fetch_scale = copy_bytes / max(max(v) for k, v in fetch.items() if "copyBuffer" in k)
     write_scale = copy_bytes / max(max(v) for k, v in write.items() if "copyBuffer" in k)
     T = 32768
-    pick = {"residual": (128, 384, 0), "wi": (256, 128, 2), "qkv": (256, 128, 1)}  # BM, BN, epilogue
     alg = {"residual": (2 * (T * H + H * H) + 2 * (T * I + H * I) + 16 * T * H) / 2,
            "wi": 2 * (T * H + 2 * I * H + T * I), "qkv": 2 * (T * H + 3 * H * H + 3 * T * H)}
     kernels = {}
-    for name, (bm, bn, epi) in pick.items():
-        cands = [k for k in fetch if (gemm_params(k) or (0,) * 5)[:5] in
-                 [(bm, bn, 64, st, epi) for st in (2, 3, 4)]]
+    for name, tiles in ROOF_TILES.items():
+        cands = [k for k in fetch if list(gemm_params(k) or ())[:5] == tiles[:5]]
         if not cands:
             continue
         k = cands[0]

@@ -488,14 +488,16 @@ hipError_t launch_cfg(int epi, const GemmArgs &a, hipStream_t s, int splits = 1)
 
 // One epilogue alone (the fp32 one or the GeGLU backward), for tiles whose
 // wave columns (BN / 2 = 96) do not pair up for the operand-type epilogues.
-template <class T, int BM, int BN, int RB, int NSTAGE, int WPE, int EPI = EPI_F32>
+// WGM rows of waves (64-row wave tiles when BM = 256 and WGM = 4).
+template <class T, int BM, int BN, int RB, int NSTAGE, int WPE, int EPI = EPI_F32, int WGM = 2>
 hipError_t launch_cfg_one(const GemmArgs &a, hipStream_t s, int splits = 1) {
   static_assert(EPI == EPI_F32 || EPI == EPI_GEGLU_BWD, "epilogues that take 96-column wave tiles");
   constexpr int WGN = BN / 96;  // 96-column wave tiles: 2 x 2 waves for 192 columns, 2 x 4 for 384
   static_assert(WGN * 96 == BN && (WGN == 2 || WGN == 4), "96-column wave tiles");
+  static_assert(WGM * WGN <= 8, "at most 8 waves per workgroup");
   const int tiles = ((a.M + BM - 1) / BM) * (a.N / BN);
-  hipLaunchKernelGGL((gemm_nt_kernel<T, BM, BN, RB, NSTAGE, EPI, WPE, 2, WGN>), dim3(tiles, splits), dim3(128 * WGN),
-                     0, s, a);
+  hipLaunchKernelGGL((gemm_nt_kernel<T, BM, BN, RB, NSTAGE, EPI, WPE, WGM, WGN>), dim3(tiles, splits),
+                     dim3(64 * WGM * WGN), 0, s, a);
   return hipGetLastError();
 }
 
@@ -1142,15 +1144,20 @@ hipError_t launch_gemm16(int epi, const GemmArgs &a, hipStream_t s) {
       // 768-wide outputs in 192-column tiles: 3,840 rows make 240 tiles of
       // 64 x 192 for 256 CUs where 64 x 128 made 360 (dX GEMM N = 768,
       // K = 2304: 30.6 -> 24.2 us isolated; Wo 16.2 -> 12.7 us). Above 4096
-      // rows, 384-column tiles of 8 waves at one workgroup per CU (99 KB of
-      // LDS): the A panel is read twice instead of four times, and in the
-      // two-stream forward the other stream's kernels fit beside them (cfg3
-      // 2.68 -> 2.72M tokens/s, alternating runs on one box; alone each launch
-      // is 2-4% slower than 128 x 192 at two workgroups per CU, which remains
-      // for N not a multiple of 384).
+      // rows, 256 x 192 tiles of 8 waves (64 x 96 each) at one workgroup per
+      // CU (112 KB of LDS: 2 stages of 64 K elements). These GEMMs are bound
+      // by the vector memory path (TA/TD), not by HBM or the matrix cores:
+      // every byte staged into LDS and every fp32 residual byte passes it.
+      // Per output element the main loop stages (1/BN + 1/BM) K operand
+      // elements: 0.0091 K for 256 x 192 against 0.0104 K for 128 x 384
+      // (-12.5%), and the residual read + write is the same. Alternating
+      // runs on one box, cfg3: Wo 80.7 -> 75.7 us, MlpWo 90.5 -> 83.8 us per
+      // launch, forward 2.80 -> 2.82M tokens/s; TA busy 0.64 -> 0.38, TD
+      // 0.77 -> 0.71 (128 x 384 tiles of 8 waves with 3 stages of 32 K
+      // elements before; 128 x 192 at two workgroups per CU was 2-4% slower
+      // still).
       if (medium) return launch_cfg_one<T, 64, 192, 128, 4, 1>(a, s);
-      if (a.N % 384 == 0) return launch_cfg_one<T, 128, 384, 64, 3, 2>(a, s);
-      return launch_cfg_one<T, 128, 192, 64, 3, 2>(a, s);
+      return launch_cfg_one<T, 256, 192, 128, 2, 2, EPI_F32, 4>(a, s);
     }
     // GeGLU backward (N = 1152) at medium M: 64 x 192 at two workgroups per
     // CU (3840 rows: 30.2 -> 25.8 us isolated). Training only (bf16).
