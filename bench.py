@@ -569,6 +569,8 @@ def main() -> int:
                     help="dn_set_stream_split: batches of at least TOKENS run in two parts on two streams (0: off)")
     ap.add_argument("--row-tail", type=int, default=2048, metavar="TOKENS",
                     help="dn_set_row_tail: batches of at least TOKENS finish the last layer on the option rows (0: off)")
+    ap.add_argument("--ln-fold", type=int, default=1, choices=(0, 1),
+                    help="dn_set_ln_fold: bf16 batches of more than 1024 tokens run the LayerNorms inside the GEMMs")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="run one device copy of MIB MiB first (reference kernel for HBM counters)")
     ap.add_argument("--tokenizer", action="store_true",
@@ -628,6 +630,7 @@ def main() -> int:
 
     eng.set_stream_split(args.stream_split)
     eng.set_row_tail(args.row_tail)
+    eng.set_ln_fold(bool(args.ln_fold))
     wl = Workload(eng, cfg, args.config, dev, nseq=args.nseq)
     log(f"workload {args.config}: {wl.nseq} sequences, T={wl.T}, R={wl.R}")
     log(f"warmup {args.warmup}")
@@ -682,15 +685,24 @@ def main() -> int:
     # Per-launch roofline views. The kernel with the largest share of GPU
     # time at cfg3 is the fp32-residual GEMM (Wo and MlpWo share its symbol):
     # algorithmic bytes per launch are A, the weights, and the fp32 residual
-    # read and written (T x H each way); by the roofline model it is bound by
-    # HBM (its bytes take longer at 8 TB/s than its flops at the MFMA peak).
+    # read and written (T x H each way); with the folded LayerNorm (bf16,
+    # T > 1024) also the next norm's bf16 operand (T x H) and the row
+    # statistics (16 bytes per row and 192 columns) it writes. By the roofline
+    # model it is bound by HBM (its bytes take longer at 8 TB/s than its flops
+    # at the MFMA peak).
+    fold = bool(args.ln_fold) and prec == "bf16" and T > 1024
     res_s = (avg["gemm_wo"] + avg["gemm_mlpwo"]) * 1e-3
     res_bytes = esz * (T * H + H * H) + esz * (T * I + H * I) + 2 * 2 * 4 * T * H
+    if fold:
+        res_bytes += 2 * (esz * T * H + 16 * T * (H // 192))
     res_flop = 2.0 * T * H * (H + I)
     wi_flop = 2.0 * T * (2 * I) * H
     wi_bytes = esz * (T * H + 2 * I * H + T * I)
     wi_s = avg["gemm_wi"] * 1e-3
-    traffic = read_traffic(args.config, prec)
+    traffic = read_traffic(args.config, prec, fold)
+    res_name = (f"gemm_nt_kernel<{tname},256,192,128,2,EPI_F32_LN,2,4,2> (Wo and MlpWo + fp32 residual + the next "
+                "LayerNorm's operand and statistics)" if fold else
+                f"gemm_nt_kernel<{tname},256,192,128,2,EPI_F32,2,4,2> (Wo and MlpWo + fp32 residual)")
     if hbm_bound:
         # small M (cfg2, cfg5): the skinny kernel streams the weights; the Wi
         # launch (the largest weight matrix) is the line
@@ -699,8 +711,7 @@ def main() -> int:
                 "frac": round(wi_bytes / wi_s / 8e12, 4), "traffic": None,
                 "algorithmic_bytes_per_launch": wi_bytes}
     else:
-        roof = {"kernel": f"gemm_nt_kernel<{tname},256,192,128,2,EPI_F32,2,4,2> (Wo and MlpWo + fp32 residual), "
-                          "layer %d, average of its two launches" % args.probe_layer,
+        roof = {"kernel": res_name + ", layer %d, average of its two launches" % args.probe_layer,
                 "bound": "hbm", "achieved": round(res_bytes / res_s / 1e9, 1), "peak": 8000.0, "unit": "GB/s",
                 "frac": round(res_bytes / res_s / 8e12, 4), "traffic": traffic.get("residual"),
                 "algorithmic_bytes_per_launch": res_bytes / 2,
@@ -736,6 +747,7 @@ def main() -> int:
                              f"{nprobe} forwards run after the timed ones on one stream",
         "stream_split_min_tokens": args.stream_split,
         "row_tail_min_tokens": args.row_tail,
+        "ln_fold": bool(args.ln_fold),
         "roofline": roof,
     }
     if args.certify:
@@ -748,7 +760,8 @@ def main() -> int:
         result["projection_gemm_frac_attainable"] = round(gemm_tflops / attain["changing_operands_tflops"], 4)
     if not hbm_bound:
         result["roofline_wi_gemm"] = {
-            "kernel": f"gemm_nt_kernel<{tname},256,128,64,3,EPI_GEGLU,2,2,2> (Wi projection + fused GeGLU), layer %d"
+            "kernel": f"gemm_nt_kernel<{tname},256,128,64,3,{'EPI_GEGLU_LN' if fold else 'EPI_GEGLU'},2,2,2> "
+                      f"(Wi projection + fused GeGLU{' + folded mlp_norm' if fold else ''}), layer %d"
                       % args.probe_layer,
             "bound": "mfma", "achieved": round(wi_flop / wi_s / 1e12, 2), "peak": PEAK[prec] / 1e12,
             "unit": "TFLOP/s", "frac": round(wi_flop / wi_s / PEAK[prec], 4), "traffic": traffic.get("wi"),
@@ -953,9 +966,18 @@ def extra_configs(eng, cfg, dev, stream, args) -> dict:
 # 32768): the residual GEMMs (N = 768) and the Wi GEMM (N = 2 x 1152).
 ROOF_TILES = {"residual": [256, 192, 128, 2, 0, 2, 4, 2], "wi": [256, 128, 64, 3, 2, 2, 2, 2],
               "qkv": [256, 128, 64, 3, 1, 2, 2, 2]}
+# With the folded LayerNorm (the default bf16 forward above 1024 tokens) the
+# same tiles run the EPI_F32_LN / EPI_GEGLU_LN / EPI_STORE_LN epilogues.
+FOLD_EPI = {"residual": 5, "wi": 7, "qkv": 6}
 
 
-def read_traffic(config: str, prec: str) -> dict:
+def roof_tiles(fold: bool) -> dict:
+    if not fold:
+        return ROOF_TILES
+    return {k: v[:4] + [FOLD_EPI[k]] + v[5:] for k, v in ROOF_TILES.items()}
+
+
+def read_traffic(config: str, prec: str, fold: bool = False) -> dict:
     """HBM bytes per launch of the roofline kernels, from the committed
     rocprofv3 FETCH_SIZE / WRITE_SIZE summary (profiles/), when it covers
     this workload."""
@@ -966,8 +988,9 @@ def read_traffic(config: str, prec: str) -> dict:
         d = json.load(fh)
     # A summary of other tile shapes than the ones launched now describes
     # another kernel: its bytes are not reported.
+    tiles = roof_tiles(fold)
     return {k: v.get("hbm_bytes_per_launch") for k, v in d.get("kernels", {}).items()
-            if v.get("template_args") == ROOF_TILES.get(k)}
+            if v.get("template_args") == tiles.get(k)}
 
 
 def summarize_traffic(fetch_dir: str, write_dir: str, out_path: str) -> int:
@@ -1013,9 +1036,20 @@ def summarize_traffic(fetch_dir: str, write_dir: str, out_path: str) -> int:
     T = 32768
     alg = {"residual": (2 * (T * H + H * H) + 2 * (T * I + H * I) + 16 * T * H) / 2,
            "wi": 2 * (T * H + 2 * I * H + T * I), "qkv": 2 * (T * H + 3 * H * H + 3 * T * H)}
+    # The folded-LayerNorm forms (when the run launched them): the residual
+    # GEMM also writes the bf16 operand and 16 bytes of statistics per row
+    # and 192 columns; QKV and Wi read those statistics and a row mean and
+    # write a row mean (72 bytes per row).
+    alg_fold = {"residual": alg["residual"] + 2 * T * H + 16 * T * (H // 192),
+                "wi": alg["wi"] + 72 * T, "qkv": alg["qkv"] + 72 * T}
     kernels = {}
-    for name, tiles in ROOF_TILES.items():
-        cands = [k for k in fetch if list(gemm_params(k) or ())[:5] == tiles[:5]]
+    for name in ROOF_TILES:
+        cands, fold = [], False
+        for fold in (True, False):
+            tiles = roof_tiles(fold)[name]
+            cands = [k for k in fetch if list(gemm_params(k) or ())[:5] == tiles[:5]]
+            if cands:
+                break
         if not cands:
             continue
         k = cands[0]
@@ -1023,8 +1057,9 @@ def summarize_traffic(fetch_dir: str, write_dir: str, out_path: str) -> int:
         wb = float(np.mean(write.get(k, [0.0]))) * write_scale
         kernels[name] = {"symbol": k, "template_args": list(gemm_params(k)), "dispatches": len(fetch[k]),
                          "fetch_bytes_per_launch": round(fb), "write_bytes_per_launch": round(wb),
-                         "hbm_bytes_per_launch": round(fb + wb), "algorithmic_bytes_per_launch": alg[name],
-                         "traffic_over_algorithmic": round((fb + wb) / alg[name], 3)}
+                         "hbm_bytes_per_launch": round(fb + wb),
+                         "algorithmic_bytes_per_launch": (alg_fold if fold else alg)[name],
+                         "traffic_over_algorithmic": round((fb + wb) / (alg_fold if fold else alg)[name], 3)}
     others = {}
     for k, v in fetch.items():
         if "attention_kernel" in k or "ln_kernel" in k:

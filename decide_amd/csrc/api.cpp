@@ -215,6 +215,58 @@ int upload_layout(dn_ctx *c, const HostLayout &hl, const Workspace &w, int nseq,
 
 // The context's own workspace: layout arrays (re-uploaded only when the batch
 // layout changes) and activation buffers for T tokens and R rows.
+// Folded LayerNorm: attn_norm and mlp_norm of the large-batch bf16 forward
+// run inside the GEMMs around them (GemmArgs::fx .. eps): the residual GEMM
+// before the norm writes its operand and row statistics, the GEMM after it
+// applies the row and column terms, and the LayerNorm launch disappears.
+bool fold_geometry(const dn_ctx *c) {
+  const Config &g = c->cfg;
+  return !g.generic && gemm_ln_fold_ok(g.precision, 1025, g.hidden, g.inter);
+}
+
+bool fold_eligible(const dn_ctx *c, int T) {
+  const Config &g = c->cfg;
+  return c->ln_fold && c->fold_cs.p && !g.generic && gemm_ln_fold_ok(g.precision, T, g.hidden, g.inter);
+}
+
+size_t fold_bytes_per_token(const dn_ctx *c) {
+  if (!fold_geometry(c)) return 0;
+  return sizeof(double) * 2 * (c->cfg.hidden / kLnPartCols) + sizeof(float) * 2;
+}
+
+// The consumer GEMMs' column sums of layer l: QKV's (attn_norm, layers >= 1)
+// at fold_cs + l * (3H + 2I), Wi's (mlp_norm) 3H further.
+float *fold_cs_qkv(dn_ctx *c, int l) {
+  const Config &g = c->cfg;
+  return (float *)c->fold_cs.p + (size_t)l * (3 * g.hidden + 2 * g.inter);
+}
+float *fold_cs_wi(dn_ctx *c, int l) { return fold_cs_qkv(c, l) + 3 * c->cfg.hidden; }
+
+int ensure_fold_cs(dn_ctx *c, hipStream_t s) {
+  if (!c->fold_cs.p || c->fold_gen == c->wgen) return DN_OK;
+  const Config &g = c->cfg;
+  const int H = g.hidden, I = g.inter;
+  for (int l = 0; l < g.layers; l++) {
+    const std::string pf = layer_prefix(l);
+    if (l > 0)
+      HIPCHK(c, "fold_colsum", launch_fold_colsum(W(c, pf + "attn.Wqkv.weight"), 3 * H, H,
+                                                  (const float *)W(c, pf + "attn_norm.weight"), fold_cs_qkv(c, l), s));
+    HIPCHK(c, "fold_colsum", launch_fold_colsum(W(c, pf + "mlp.Wi.weight"), 2 * I, H,
+                                                (const float *)W(c, pf + "mlp_norm.weight"), fold_cs_wi(c, l), s));
+  }
+  c->fold_gen = c->wgen;
+  return DN_OK;
+}
+
+// The folded LayerNorm's statistics buffers for T tokens (none when this
+// context never folds).
+int ensure_fold_buffers(dn_ctx *c, size_t T) {
+  if (!fold_geometry(c) || !c->ln_fold) return DN_OK;
+  HIPCHK(c, "hipMalloc", ensure(c->fold_part, sizeof(double) * 2 * (c->cfg.hidden / kLnPartCols) * T));
+  HIPCHK(c, "hipMalloc", ensure(c->fold_mean, sizeof(float) * 2 * T));
+  return DN_OK;
+}
+
 int ctx_workspace(dn_ctx *c, int nseq, const int32_t *seq_len, int R, Workspace *w) {
   std::vector<int> len(seq_len, seq_len + nseq);
   const bool same = len == c->lay_len && c->d_seq_off.p;
@@ -270,6 +322,13 @@ int ctx_workspace(dn_ctx *c, int nseq, const int32_t *seq_len, int R, Workspace 
   if (T <= (size_t)kSmallSplitMaxTokens)
     HIPCHK(c, "hipMalloc", ensure(c->smallpart, sizeof(float) * kSmallSplitParts * T * H));
   o.part = T <= (size_t)kSmallSplitMaxTokens ? (float *)c->smallpart.p : nullptr;
+  if (fold_eligible(c, (int)T)) {
+    const int rc = ensure_fold_buffers(c, T);
+    if (rc) return rc;
+    o.lpart = (double *)c->fold_part.p;
+    o.lmean1 = (float *)c->fold_mean.p;
+    o.lmean2 = (float *)c->fold_mean.p + T;
+  }
   o.h = (float *)c->h.p;
   o.xn = c->xn.p;
   o.qkv = c->qkv.p;
@@ -338,6 +397,9 @@ struct Pass {
   // a large batch); every other forward, training included, uses ATTN_QUERIES
   // items for all layers.
   bool wide_global = false;
+  // The folded LayerNorm (the workspace has its buffers and the pass more
+  // than 1024 tokens).
+  bool fold = false;
   Workspace w;
   const int32_t *ids, *pos, *opt;
   hipStream_t s;
@@ -401,9 +463,14 @@ hipError_t layer_gemm(const Config &g, int epi, const GemmArgs &a0, hipStream_t 
 // its parts into the residual; in_parts > 0: `in` still lacks the previous
 // layer's MlpWo parts, which attn_norm adds; mo_parts non-null: this layer's
 // MlpWo may leave its parts for the next layer's attn_norm the same way and
-// stores their count (0: the residual stream is complete).
+// stores their count (0: the residual stream is complete). With the folded
+// LayerNorm (p.fold): fold_in, the previous layer's MlpWo left attn_norm's
+// operand in the workspace's xn and its statistics (this layer's QKV applies
+// the norm); mlp_norm is folded into Wo and Wi; fold_out, this layer's
+// MlpWo leaves the next layer's attn_norm operand the same way.
 int enqueue_layer(dn_ctx *c, const Pass &p, int l, float *in, float *h1, float *out, void *x1, LayerSave *S,
-                  hipEvent_t *ev, bool attn_only = false, int in_parts = 0, int *mo_parts = nullptr) {
+                  hipEvent_t *ev, bool attn_only = false, int in_parts = 0, int *mo_parts = nullptr,
+                  bool fold_in = false, bool fold_out = false) {
   const Config &g = c->cfg;
   const int H = g.hidden, I = g.inter, prec = g.precision;
   const Workspace &w = p.w;
@@ -412,9 +479,15 @@ int enqueue_layer(dn_ctx *c, const Pass &p, int l, float *in, float *h1, float *
   const std::string pf = layer_prefix(l);
   const bool sliding = g.sliding[l] != 0;
   const bool split = w.part && !S && !g.generic && h1 == in && out == in;
+  const bool fold = p.fold && w.lpart && !S && !split && !g.generic && h1 == in && out == in;
+  fold_in = fold_in && fold && l > 0;
+  fold_out = fold_out && fold && l + 1 < g.layers;
+  const int lparts = H / kLnPartCols;
   if (l > 0) {
     x1 = S ? S->n1.p : w.xn;
-    if (in_parts > 0 && split)
+    if (fold_in) {
+      // the previous layer's MlpWo wrote x1 and the row statistics
+    } else if (in_parts > 0 && split)
       HIPCHK(c, "ln(attn_norm)", launch_ln_parts(prec, in, w.part, in_parts, T, H,
                                                  (const float *)W(c, pf + "attn_norm.weight"), g.eps, x1, s));
     else
@@ -433,7 +506,15 @@ int enqueue_layer(dn_ctx *c, const Pass &p, int l, float *in, float *h1, float *
   q.N = 3 * H;
   q.K = H;
   q.n_store = 3 * H;
-  PROBED(ev, DN_PROBE_QKV, "gemm(Wqkv)", layer_gemm(g, EPI_STORE, q, s));
+  if (fold_in) {
+    q.lpart = w.lpart;
+    q.lparts = lparts;
+    q.mprev = w.lmean2;  // what the previous MlpWo subtracted: its layer's mlp_norm means
+    q.mean_out = w.lmean1;
+    q.lcs = fold_cs_qkv(c, l);
+    q.eps = g.eps;
+  }
+  PROBED(ev, DN_PROBE_QKV, "gemm(Wqkv)", layer_gemm(g, fold_in ? EPI_STORE_LN : EPI_STORE, q, s));
 
   const float *rope = (const float *)c->rope.p;
   const size_t tab = (size_t)kPositions * 32;
@@ -491,6 +572,13 @@ int enqueue_layer(dn_ctx *c, const Pass &p, int l, float *in, float *h1, float *
     PROBED(ev, DN_PROBE_WO, "gemm(Wo)", launch_gemm_small_split(prec, o, wo_parts, w.part, s));
     HIPCHK(c, "ln(mlp_norm)", launch_ln_parts(prec, h1, w.part, wo_parts, T, H,
                                               (const float *)W(c, pf + "mlp_norm.weight"), g.eps, x2, s));
+  } else if (fold) {
+    o.fx = x2;
+    o.lw = (const float *)W(c, pf + "mlp_norm.weight");
+    o.lpart = w.lpart;
+    o.lparts = lparts;
+    o.mprev = fold_in ? w.lmean1 : nullptr;
+    PROBED(ev, DN_PROBE_WO, "gemm(Wo)", layer_gemm(g, EPI_F32_LN, o, s));
   } else {
     PROBED(ev, DN_PROBE_WO, "gemm(Wo)", layer_gemm(g, EPI_F32, o, s));
     HIPCHK(c, "ln(mlp_norm)", launch_ln(prec, h1, T, H, (const float *)W(c, pf + "mlp_norm.weight"), g.eps, x2, s,
@@ -515,7 +603,15 @@ int enqueue_layer(dn_ctx *c, const Pass &p, int l, float *in, float *h1, float *
   } else {
     wi.C = w.act;
     wi.ldc = I;
-    PROBED(ev, DN_PROBE_WI, "gemm(Wi)", layer_gemm(g, EPI_GEGLU, wi, s));
+    if (fold) {
+      wi.lpart = w.lpart;
+      wi.lparts = lparts;
+      wi.mprev = o.mprev;
+      wi.mean_out = w.lmean2;
+      wi.lcs = fold_cs_wi(c, l);
+      wi.eps = g.eps;
+    }
+    PROBED(ev, DN_PROBE_WI, "gemm(Wi)", layer_gemm(g, fold ? EPI_GEGLU_LN : EPI_GEGLU, wi, s));
   }
 
   GemmArgs mo{};
@@ -534,10 +630,17 @@ int enqueue_layer(dn_ctx *c, const Pass &p, int l, float *in, float *h1, float *
   const int parts = split && mo_parts ? small_split_parts(prec, T, H, I) : 1;
   if (mo_parts) *mo_parts = parts > 1 ? parts : 0;
   mo.skinny_regs = g.skinny_regs ? 1 : 0;
+  if (fold_out) {
+    mo.fx = w.xn;
+    mo.lw = (const float *)W(c, layer_prefix(l + 1) + "attn_norm.weight");
+    mo.lpart = w.lpart;
+    mo.lparts = lparts;
+    mo.mprev = w.lmean2;
+  }
   if (parts > 1)
     PROBED(ev, DN_PROBE_MLPWO, "gemm(MlpWo)", launch_gemm_small_split(prec, mo, parts, w.part, s));
   else
-    PROBED(ev, DN_PROBE_MLPWO, "gemm(MlpWo)", layer_gemm(g, EPI_F32, mo, s));
+    PROBED(ev, DN_PROBE_MLPWO, "gemm(MlpWo)", layer_gemm(g, fold_out ? EPI_F32_LN : EPI_F32, mo, s));
   return DN_OK;
 }
 
@@ -872,6 +975,15 @@ int forward_split(dn_ctx *c, int nseq, const int32_t *seq_len, const int32_t *d_
   if (rc) return rc;
   rc = ensure_rope(c);
   if (rc) return rc;
+  // Each part's GEMMs fold when the part has more than 1024 tokens, as the
+  // single-stream forward of the whole batch does (kMinPartTokens).
+  const bool fold = fold_eligible(c, std::min(acc, T_total - acc));
+  if (fold) {
+    rc = ensure_fold_buffers(c, T);
+    if (rc) return rc;
+    rc = ensure_fold_cs(c, st[0]);  // before the fork: both streams read the column sums
+    if (rc) return rc;
+  }
   // The aux stream starts after everything already queued on the context's
   // stream (the caller's uploads of the token arrays among it).
   HIPCHK(c, "hipEventRecord", hipEventRecord(c->ev_fork, st[0]));
@@ -891,6 +1003,12 @@ int forward_split(dn_ctx *c, int nseq, const int32_t *seq_len, const int32_t *d_
     w.ctx = (char *)c->ctxb.p + es * t0 * H;
     w.act = (char *)c->act.p + es * t0 * I;
     w.kinfo = (int *)c->kinfo.p + t0;
+    if (fold) {
+      w.lpart = (double *)c->fold_part.p + t0 * 2 * (H / kLnPartCols);
+      w.lmean1 = (float *)c->fold_mean.p + t0;
+      w.lmean2 = (float *)c->fold_mean.p + T + t0;
+    }
+    ps[k].fold = fold;
     ps[k].ids = d_ids + t0;
     ps[k].pos = d_pos + t0;
     ps[k].opt = d_opt ? d_opt + t0 : nullptr;
@@ -901,10 +1019,11 @@ int forward_split(dn_ctx *c, int nseq, const int32_t *seq_len, const int32_t *d_
   }
   const bool rows_tail = tail_on_rows(c, T_total, R, false);
   const bool rows_layer = rows_tail && rows_layer_fits(c, T_total, R, nseq);
-  for (int l = 0; l < (rows_layer ? L - 1 : L); l++)
+  const int nfull = rows_layer ? L - 1 : L;
+  for (int l = 0; l < nfull; l++)
     for (int k = 0; k < 2; k++) {
       rc = enqueue_layer(c, ps[k], l, ps[k].w.h, ps[k].w.h, ps[k].w.h, ps[k].w.xn, nullptr, nullptr,
-                         rows_tail && l == L - 1);
+                         rows_tail && l == L - 1, 0, nullptr, l > 0, l + 1 < nfull);
       if (rc) return rc;
     }
   HIPCHK(c, "hipEventRecord", hipEventRecord(c->ev_join, st[1]));
@@ -999,6 +1118,11 @@ int forward_core(dn_ctx *c, int nseq, const int32_t *seq_len, const int32_t *d_i
   ps.pos = d_pos;
   ps.opt = d_opt;
   ps.s = c->stream;
+  ps.fold = !train && w.lpart && fold_eligible(c, T);
+  if (ps.fold) {
+    rc = ensure_fold_cs(c, ps.s);
+    if (rc) return rc;
+  }
   // Training keeps each saved layer's input in its own buffer (LayerSave::hs)
   // and its post-attention residual in LayerSave::h1: the residual GEMMs read
   // one and write the next, so the residual stream moves through the saved
@@ -1027,7 +1151,7 @@ int forward_core(dn_ctx *c, int nseq, const int32_t *seq_len, const int32_t *d_i
     // or the option-row layer reads it).
     int parts = 0;
     rc = enqueue_layer(c, ps, l, in, h1, out, xn0, S, ev, rows_tail && l == L - 1, pending,
-                       !train && l + 1 < nfull ? &parts : nullptr);
+                       !train && l + 1 < nfull ? &parts : nullptr, l > 0, l + 1 < nfull);
     if (rc) return rc;
     pending = parts;
     cur = out;
@@ -1118,6 +1242,7 @@ int upload_f32(dn_ctx *c, TensorSlot &t, const float *data, int64_t n) {
     HIPCHK(c, "hipMemcpy", hipMemcpy(t.buf.p, data, bytes, hipMemcpyHostToDevice));
   }
   t.set = true;
+  c->wgen++;
   return DN_OK;
 }
 // Validation (forward.go:142-196) and staging of a host batch.
@@ -1285,7 +1410,8 @@ void dn_close(dn_ctx *c) {
                     &c->rope,     &c->kinfo, &c->io,
                     &c->logits,   &c->err_flag, &c->gA,    &c->gB,          &c->gC,       &c->d_seq_off, &c->head_s1, &c->head_d,
                     &c->d_seq_len, &c->d_chunk_off, &c->d_chunk_desc, &c->d_work, &c->d_chunks,
-                    &c->d_codes,   &c->d_first, &c->calib, &c->smallpart};
+                    &c->d_codes,   &c->d_first, &c->calib, &c->smallpart, &c->fold_cs, &c->fold_part,
+                    &c->fold_mean};
   for (DevBuf *b : bufs) release(*b);
   if (c->pin) (void)hipHostFree(c->pin);
   for (PartLayout &P : c->parts)
@@ -1358,6 +1484,12 @@ int dn_set_config(dn_ctx *c, int hidden, int inter, int heads, int layers, int v
   HIPCHK(c, "hipMemcpy", hipMemcpy(c->inv_freq.p, inv, sizeof(inv), hipMemcpyHostToDevice));
   c->rope_ready = false;
   c->configured = true;
+  // The folded LayerNorm's column sums (filled from the weights at the first
+  // forward that folds, and again after they change).
+  release(c->fold_cs);
+  c->fold_gen = 0;
+  if (fold_geometry(c))
+    HIPCHK(c, "hipMalloc", ensure(c->fold_cs, sizeof(float) * (size_t)layers * (3 * hidden + 2 * inter)));
   // Set-up work that forwards would otherwise do on first use: the RoPE
   // tables of these thetas and the device error flag.
   int rc = ensure_rope(c);
@@ -1404,6 +1536,7 @@ static int upload_bf16_impl(dn_ctx *c, const char *name, const uint16_t *bits, i
     HIPCHK(c, "hipMemcpy", hipMemcpy(t->buf.p, bits, (size_t)n * 2, hipMemcpyHostToDevice));
   }
   t->set = true;
+  c->wgen++;
   return DN_OK;
 }
 
@@ -1615,6 +1748,13 @@ int dn_set_row_tail(dn_ctx *c, int min_tokens) {
   if (!c || min_tokens < 0) return DN_INVALID_ARG;
   c->err.clear();
   c->tail_min_tokens = min_tokens;
+  return DN_OK;
+}
+
+int dn_set_ln_fold(dn_ctx *c, int on) {
+  if (!c) return DN_INVALID_ARG;
+  c->err.clear();
+  c->ln_fold = on != 0;
   return DN_OK;
 }
 

@@ -243,6 +243,22 @@ struct GemmArgs {
   const void *gin;  // EPI_GEGLU_BWD: the GeGLU input (the Wi output, M x 2N, row stride ldc)
   int skinny_regs;  // small-M kernel, 16-bit 32 x 32 tiles: operands loaded straight into registers
                     // (0: whole 128-byte rows through LDS by global->LDS DMA)
+  // LayerNorm folded into the GEMMs on either side of it (bf16 inference).
+  // The residual GEMM (EPI_F32_LN) also writes fx = bf16((x - mprev[row]) *
+  // lw[col]) of the new residual x (row stride ldc) and, per row and
+  // 192-column N-tile, the tile's (mean, M2) of x to lpart (lparts pairs per
+  // row). The GEMM that takes fx as A (EPI_STORE_LN, EPI_GEGLU_LN) merges
+  // them into the row's mean and rstd = 1/sqrt(M2/K + eps) and computes
+  // rstd * (A.B^T - (mean - mprev[row]) * lcs[col]) with lcs[n] =
+  // sum_k lw[k] B[n][k], i.e. LayerNorm(x).B^T with the LayerNorm weight in
+  // lcs and in fx; its tiles at n0 = 0 write the row mean to mean_out.
+  // mprev null: 0.
+  void *fx;
+  const float *lw, *lcs, *mprev;
+  double *lpart;
+  float *mean_out;
+  int lparts;
+  float eps;
 };
 
 // GEMM epilogues: fp32 store / accumulate, store in the operand type, GeGLU of
@@ -251,6 +267,15 @@ struct GemmArgs {
 // output (M x N), and C (M x 2N, operand type, the interleaved Wi layout)
 // receives the gradients of its value and gate inputs, read from gin.
 enum { EPI_F32 = 0, EPI_STORE = 1, EPI_GEGLU = 2, EPI_GEGLU_KEEP = 3, EPI_GEGLU_BWD = 4 };
+// The folded-LayerNorm forms (GemmArgs::fx .. eps; bf16, M > 1024): the
+// residual GEMM that produces the LayerNorm's input, and the store / GeGLU
+// GEMMs that consume its output.
+enum { EPI_F32_LN = 5, EPI_STORE_LN = 6, EPI_GEGLU_LN = 7 };
+// Columns per LayerNorm statistics part written by EPI_F32_LN.
+constexpr int kLnPartCols = 192;
+// Whether the folded LayerNorm runs for a bf16 model of this geometry at M
+// rows (the configurations launch_gemm tiles for EPI_*_LN).
+bool gemm_ln_fold_ok(int precision, int M, int hidden, int inter);
 
 hipError_t launch_gemm(int precision, int epi, const GemmArgs &a, hipStream_t s);
 // Any-shape GEMM for model geometries the MFMA kernels do not tile: one thread
@@ -374,6 +399,9 @@ hipError_t launch_prologue(int precision, const int *pos, const int *opt, const 
                            int *kinfo, ChunkInfo *chunks, const int *ids, int Tn, const float *tok, int vocab,
                            const float *w, float eps, int H, float *h, void *xn, int *err, hipStream_t s,
                            float *mean = nullptr, float *rstd = nullptr);
+// Column sums of a LayerNorm-weighted bf16 projection for the folded
+// LayerNorm: cs[n] = sum_k lw[k] * B[n][k] (fp64 sums), B N x K.
+hipError_t launch_fold_colsum(const void *B, int N, int K, const float *lw, float *cs, hipStream_t s);
 // LayerNorm launchers; mean / rstd (optional, [rows]) receive the row statistics.
 hipError_t launch_ln(int precision, const float *x, int rows, int H, const float *w, float eps, void *y, hipStream_t s,
                      float *mean = nullptr, float *rstd = nullptr);

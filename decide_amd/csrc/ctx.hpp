@@ -105,6 +105,11 @@ struct Workspace {
   // [kSmallSplitParts x T x H] split-K partial products of the residual
   // GEMMs for batches of at most kSmallSplitMaxTokens tokens; null otherwise.
   float *part = nullptr;
+  // Folded LayerNorm (bf16, more than 1024 tokens): per row the residual
+  // GEMM's (mean, M2) pairs over each 192 columns ([T x H/192]), and the
+  // row means of a layer's attn_norm and mlp_norm ([T] each); null: no fold.
+  double *lpart = nullptr;
+  float *lmean1 = nullptr, *lmean2 = nullptr;
   int *seq_off = nullptr, *seq_len = nullptr, *chunk_off = nullptr, *first = nullptr;
   int4 *chunk_desc = nullptr, *work = nullptr;
   ChunkInfo *chunks = nullptr;
@@ -166,6 +171,13 @@ struct dn_ctx {
   DevBuf gA, gB, gC;  // dn_gemm_f32 staging
   DevBuf calib;       // dn_mfma_calibrate's result sink
   void *scratch = nullptr;  // this device's static scratch array (noalloc.cpp), from hipGetSymbolAddress
+  // Folded LayerNorm (dn_set_ln_fold): the column sums of the LayerNorm-
+  // weighted QKV and Wi weights per layer ([L x (3H + 2I)] floats, allocated
+  // by dn_set_config), rebuilt when the weights' generation (bumped by every
+  // upload and optimizer step) has moved; the forwards' statistics buffers.
+  DevBuf fold_cs, fold_part, fold_mean;
+  uint64_t wgen = 1, fold_gen = 0;
+  bool ln_fold = true;
   // Forwards of large batches run in two parts of whole sequences, one per
   // stream (the context's and aux_stream, created on first use at the
   // default priority), so the kernels of one part overlap the other's.
@@ -236,6 +248,14 @@ int ensure_rope(dn_ctx *c);
 // its work / codes / first arrays, after the ATTN_QUERIES items' sections.
 void set_work2(Workspace &w, int nwork2);
 int ensure_err_flag(dn_ctx *c);
+// Folded LayerNorm: whether a forward of T tokens on this context takes it,
+// and the column sums brought up to date with the weights (a kernel per
+// projection on stream s when they changed; no allocation).
+bool fold_eligible(const dn_ctx *c, int T);
+int ensure_fold_cs(dn_ctx *c, hipStream_t s);
+// Bytes of the folded LayerNorm's per-token statistics (0 when the context
+// never folds).
+size_t fold_bytes_per_token(const dn_ctx *c);
 // Fills in the context's own scratch pointer for its device (noalloc.cpp;
 // called by dn_open with the device current).
 int noalloc_init(dn_ctx *c);

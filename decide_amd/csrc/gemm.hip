@@ -142,6 +142,44 @@ __device__ __forceinline__ void store_staged(const T *st, T *C, int ldc, int m0,
   }
 }
 
+// Folded LayerNorm, consumer side. ln_fold_load fetches row `row`'s
+// per-part (mean, M2) pairs and mprev (issued before the first stages' DMA,
+// whose issue is not delayed by them); ln_fold_merge combines the pairs by
+// the pairwise update of Chan, Golub and LeVeque for equal counts (the mean
+// of the part means; M2 = the parts' M2 plus the count times the squared
+// deviations of the part means), in fp64 like the LayerNorm kernel's
+// two-pass statistics, and returns (rstd, mean - mprev) with mean and rstd
+// rounded to float as that kernel rounds them; write_mean also stores the
+// row's mean.
+constexpr int kLnMaxParts = 8;  // launch_gemm checks lparts <= 8
+__device__ __forceinline__ void ln_fold_load(const GemmArgs &g, int row, double2 (&v)[kLnMaxParts], float &mp) {
+  const int rr = min(row, g.M - 1), np = g.lparts;
+  const double2 *pp = (const double2 *)g.lpart + (size_t)rr * np;
+#pragma unroll
+  for (int t = 0; t < kLnMaxParts; t++)
+    if (t < np) v[t] = pp[t];
+  mp = g.mprev ? g.mprev[rr] : 0.0f;
+}
+__device__ __forceinline__ float2 ln_fold_merge(const GemmArgs &g, int row, const double2 (&v)[kLnMaxParts], float mp,
+                                                bool write_mean) {
+  const int np = g.lparts;
+  double sum = 0;
+#pragma unroll
+  for (int t = 0; t < kLnMaxParts; t++)
+    if (t < np) sum += v[t].x;
+  const double mu = sum / np;
+  double m2 = 0;
+#pragma unroll
+  for (int t = 0; t < kLnMaxParts; t++)
+    if (t < np) {
+      const double d = v[t].x - mu;
+      m2 += v[t].y + (double)kLnPartCols * d * d;
+    }
+  const float mean = (float)mu;
+  if (write_mean && row < g.M) g.mean_out[row] = mean;
+  return make_float2((float)(1.0 / sqrt(m2 / (double)g.K + (double)g.eps)), mean - mp);
+}
+
 // WGM x WGN waves tile the BM x BN block; each wave owns a WM x WN sub-tile.
 template <class T, int BM, int BN, int RB, int NSTAGE, int EPI, int WPE, int WGM, int WGN>
 __global__ __launch_bounds__(64 * WGM * WGN) __attribute__((amdgpu_waves_per_eu(WPE))) void gemm_nt_kernel(GemmArgs g) {
@@ -156,13 +194,21 @@ __global__ __launch_bounds__(64 * WGM * WGN) __attribute__((amdgpu_waves_per_eu(
   constexpr int STAGE = (BM + BN) * RB;
   constexpr int LOADS = (BM + BN) * CPR / NT;  // 16-byte DMA loads per thread per stage
   static_assert(LOADS * NT == (BM + BN) * CPR, "tile rows must fill whole DMA instructions");
-  static_assert(EPI == EPI_F32 || EPI == EPI_GEGLU_BWD || TN % 2 == 0, "paired epilogues need 64-column wave tiles");
+  static_assert(EPI == EPI_F32 || EPI == EPI_F32_LN || EPI == EPI_GEGLU_BWD || TN % 2 == 0,
+                "paired epilogues need 64-column wave tiles");
+  constexpr bool F32OUT = EPI == EPI_F32 || EPI == EPI_F32_LN;
+  constexpr bool GATED = EPI == EPI_GEGLU || EPI == EPI_GEGLU_LN;
+  constexpr bool LNC = EPI == EPI_STORE_LN || EPI == EPI_GEGLU_LN;  // folded LayerNorm consumer
   static_assert(NSTAGE >= 2 && LOADS * (NSTAGE - 2) < 64, "pipeline depth");
   // fp32 epilogue staged in WGM passes of WM rows; the others in one pass.
-  constexpr int EPI_BYTES = (EPI == EPI_F32 || EPI == EPI_GEGLU_BWD) ? WM * (BN + 4) * 4
-                                             : BM * ((EPI == EPI_GEGLU ? BN / 2 : BN) + 8) * (int)sizeof(T);
-  constexpr int SMEM = NSTAGE * STAGE > EPI_BYTES ? NSTAGE * STAGE : EPI_BYTES;
-  __shared__ __attribute__((aligned(1024))) char smem[SMEM];
+  constexpr int EPI_BYTES = (F32OUT || EPI == EPI_GEGLU_BWD) ? WM * (BN + 4) * 4
+                                                            : BM * ((GATED ? BN / 2 : BN) + 8) * (int)sizeof(T);
+  constexpr int SMEM_RING = NSTAGE * STAGE > EPI_BYTES ? NSTAGE * STAGE : EPI_BYTES;
+  // The folded LayerNorm consumer's row statistics and column sums follow
+  // the ring in the same array: a second LDS object would make the compiler
+  // wait for every DMA (vmcnt(0)) before the main loop's fragment reads.
+  constexpr int LN_BYTES = LNC ? BM * 8 + BN * 4 : 0;
+  __shared__ __attribute__((aligned(1024))) char smem[SMEM_RING + LN_BYTES];
 
   // The wave index is uniform: readfirstlane keeps it (and every LDS-DMA
   // destination, which goes through M0) in scalar registers.
@@ -172,11 +218,23 @@ __global__ __launch_bounds__(64 * WGM * WGN) __attribute__((amdgpu_waves_per_eu(
 
   const TileOrder<BM, BN> to(blockIdx.x, (g.M + BM - 1) / BM, g.N / BN, g.ngroups, g.order);
   const int m0 = to.m0, n0 = to.n0;
+  // Folded LayerNorm consumer: thread t < BM takes block row t's statistics
+  // and thread t < BN column n0 + t's lcs (loaded here, merged while the
+  // first stages land); the epilogue reads (rstd, mean - mprev) of its rows
+  // from ln_st and its columns' lcs from ln_cs.
+  float2 *const ln_st = (float2 *)(smem + SMEM_RING);
+  float *const ln_cs = (float *)(smem + SMEM_RING + BM * 8);
+  double2 ln_v[LNC ? kLnMaxParts : 1];
+  float ln_mp = 0.0f, ln_c = 0.0f;
+  if constexpr (LNC) {
+    if (threadIdx.x < BM) ln_fold_load(g, m0 + (int)threadIdx.x, ln_v, ln_mp);
+    if (threadIdx.x < BN) ln_c = g.lcs[n0 + threadIdx.x];
+  }
   // Split-K: blockIdx.y takes K elements [y*K, (y+1)*K) of A and B and writes
   // its own partial output.
   const size_t koff = (size_t)blockIdx.y * g.K;
   const T *gA = (const T *)g.A + koff, *gB = (const T *)g.B + koff;
-  char *gC = (char *)g.C + (size_t)blockIdx.y * g.c_split * (EPI == EPI_F32 ? 4 : sizeof(T));
+  char *gC = (char *)g.C + (size_t)blockIdx.y * g.c_split * (F32OUT ? 4 : sizeof(T));
 
   // DMA sources: load i of this wave fills tile rows RPI*(wave + NW*i) .. +RPI-1;
   // lane l writes row RPI*(wave+NW*i) + l/CPR, LDS chunk slot l%CPR, which
@@ -216,6 +274,10 @@ __global__ __launch_bounds__(64 * WGM * WGN) __attribute__((amdgpu_waves_per_eu(
   const int nk = g.K / KT;
 #pragma unroll
   for (int s = 0; s < NSTAGE - 1; s++) issue(s, min(s, nk - 1) * KT);
+  if constexpr (LNC) {
+    if (threadIdx.x < BM) ln_st[threadIdx.x] = ln_fold_merge(g, m0 + (int)threadIdx.x, ln_v, ln_mp, n0 == 0);
+    if (threadIdx.x < BN) ln_cs[threadIdx.x] = ln_c;
+  }
 
   constexpr int NKS = KT / MF::KSTEP;                  // MFMA k steps per stage
   constexpr int PER_KS = (LOADS + NKS - 1) / NKS;      // next-stage loads issued per k step
@@ -351,7 +413,8 @@ __global__ __launch_bounds__(64 * WGM * WGN) __attribute__((amdgpu_waves_per_eu(
       }
       if (pass + 1 < WGM) __syncthreads();
     }
-  } else if constexpr (EPI == EPI_F32) {
+  } else if constexpr (F32OUT) {
+    constexpr bool LN = EPI == EPI_F32_LN;  // also the folded LayerNorm's operand and statistics
     constexpr int LD = BN + 4;  // floats per staged row
     constexpr int HM = WM;      // rows per pass: the waves with wm == pass stage theirs
     float *st = (float *)smem;
@@ -360,6 +423,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) __attribute__((amdgpu_waves_per_eu(
     constexpr int V = BN / 4;  // float4 per row
     constexpr int ITER = HM * V / NT;
     static_assert(ITER * NT == HM * V, "epilogue shape");
+    static_assert(!LN || (BN == kLnPartCols && NT == 8 * HM), "LayerNorm statistics: 8 threads per 192-column row");
     const bool vec = (g.ldc & 3) == 0;
     // The residual loads of a pass are issued together (one HBM round trip
     // per pass): pass 0's before its staging, so that their latency overlaps
@@ -378,8 +442,19 @@ __global__ __launch_bounds__(64 * WGM * WGN) __attribute__((amdgpu_waves_per_eu(
       }
     };
     load_old(0);
+    // Folded LayerNorm: thread (row tid / 8 of the pass, part tid % 8) takes
+    // 24 consecutive columns; the LayerNorm weight at them.
+    constexpr int CW = BN / 8;
+    float4 lw4[LN ? CW / 4 : 1];
+    if constexpr (LN) {
+#pragma unroll
+      for (int q = 0; q < CW / 4; q++) lw4[q] = *(const float4 *)(g.lw + n0 + (tid & 7) * CW + 4 * q);
+    }
 #pragma unroll
     for (int pass = 0; pass < WGM; pass++) {
+      float ln_mp = 0.0f;
+      if constexpr (LN)
+        if (g.mprev) ln_mp = g.mprev[min(m0 + pass * HM + (tid >> 3), g.M - 1)];
       stage_f32(st, LD, pass);
       __syncthreads();
 #pragma unroll
@@ -390,12 +465,64 @@ __global__ __launch_bounds__(64 * WGM * WGN) __attribute__((amdgpu_waves_per_eu(
         const float4 v = *(const float4 *)(st + r * LD + c4);
         float *p = C + (size_t)row * g.ldc + col;
         if (vec && col + 4 <= g.n_store) {
-          *(float4 *)p = make_float4(v.x + old[u].x, v.y + old[u].y, v.z + old[u].z, v.w + old[u].w);
+          const float4 x = make_float4(v.x + old[u].x, v.y + old[u].y, v.z + old[u].z, v.w + old[u].w);
+          *(float4 *)p = x;
+          if constexpr (LN)  // read back below (launch_gemm guarantees vec and n_store == N for this form)
+            *(float4 *)(st + r * LD + c4) = x;
         } else {
           const float vv[4] = {v.x, v.y, v.z, v.w};
           const float *pr = R + (size_t)row * g.ldc + col;
           for (int q = 0; q < 4 && col + q < g.n_store; q++) p[q] = g.accumulate ? pr[q] + vv[q] : vv[q];
         }
+      }
+      if constexpr (LN) {
+        // The pass's rows from the staging area: eight threads per row, 24
+        // consecutive columns each. The next LayerNorm's operand
+        // bf16((x - mprev) * w) in three 16-byte stores per thread; the
+        // statistics over this tile's 192 columns: fp32 partial sums, the
+        // eight reduced in fp64 in a fixed order, then the squared
+        // deviations from the tile mean the same way (their fp32 rounding,
+        // ~1e-6 relative, is far below the bf16 operand's).
+        __syncthreads();
+        const int r = tid >> 3, part = tid & 7;
+        float4 xv[CW / 4];
+#pragma unroll
+        for (int q = 0; q < CW / 4; q++) xv[q] = *(const float4 *)(st + r * LD + part * CW + 4 * q);
+        {
+          const int row = m0 + pass * HM + r;
+          if (row < g.M) {
+            T *f = (T *)g.fx + (size_t)row * g.ldc + n0 + part * CW;
+#pragma unroll
+            for (int q = 0; q < CW / 4; q += 2) {
+              const float4 a = xv[q], b = xv[q + 1], wa = lw4[q], wb = lw4[q + 1];
+              *(uint4 *)(f + 4 * q) = make_uint4(pack16<T>((a.x - ln_mp) * wa.x, (a.y - ln_mp) * wa.y),
+                                                 pack16<T>((a.z - ln_mp) * wa.z, (a.w - ln_mp) * wa.w),
+                                                 pack16<T>((b.x - ln_mp) * wb.x, (b.y - ln_mp) * wb.y),
+                                                 pack16<T>((b.z - ln_mp) * wb.z, (b.w - ln_mp) * wb.w));
+            }
+          }
+        }
+        float s32 = 0.0f;
+#pragma unroll
+        for (int q = 0; q < CW / 4; q++) s32 += (xv[q].x + xv[q].y) + (xv[q].z + xv[q].w);
+        double sum = s32;
+        sum += __shfl_xor(sum, 1);
+        sum += __shfl_xor(sum, 2);
+        sum += __shfl_xor(sum, 4);
+        const double mu = sum / BN;
+        const float muf = (float)mu;
+        float q32 = 0.0f;
+#pragma unroll
+        for (int q = 0; q < CW / 4; q++) {
+          const float a = xv[q].x - muf, b = xv[q].y - muf, c = xv[q].z - muf, d = xv[q].w - muf;
+          q32 += (a * a + b * b) + (c * c + d * d);
+        }
+        double m2 = q32;
+        m2 += __shfl_xor(m2, 1);
+        m2 += __shfl_xor(m2, 2);
+        m2 += __shfl_xor(m2, 4);
+        const int row = m0 + pass * HM + r;
+        if (part == 0 && row < g.M) ((double2 *)g.lpart)[(size_t)row * g.lparts + n0 / BN] = make_double2(mu, m2);
       }
       if (pass + 1 < WGM) {
         load_old(pass + 1);
@@ -412,6 +539,34 @@ __global__ __launch_bounds__(64 * WGM * WGN) __attribute__((amdgpu_waves_per_eu(
       constexpr int LD = OC + 8;           // staged row length (elements)
       typedef T T4 __attribute__((ext_vector_type(4)));
       T *st = (T *)smem;
+      // Folded LayerNorm consumer: lcs at this lane's columns (block j, run
+      // q: the 4 columns from cw + 32 j + mfma_row(4 q)).
+      float cs[LNC ? TN : 1][16];
+      if constexpr (LNC) {
+#pragma unroll
+        for (int j = 0; j < TN; j++)
+#pragma unroll
+          for (int q = 0; q < 4; q++) {
+            const float4 c4 = *(const float4 *)(ln_cs + cw + j * 32 + mfma_row(4 * q, lane));
+            cs[j][4 * q] = c4.x, cs[j][4 * q + 1] = c4.y, cs[j][4 * q + 2] = c4.z, cs[j][4 * q + 3] = c4.w;
+          }
+      }
+      // rstd * (product - (mean - mprev) * lcs) for the folded LayerNorm
+      // (ln_st was written before the main loop's first barrier).
+      float ln_rs[LNC ? TM : 1], ln_dm[LNC ? TM : 1];
+      if constexpr (LNC) {
+#pragma unroll
+        for (int i = 0; i < TM; i++) {
+          const float2 t = ln_st[rw + 32 * i + lr];
+          ln_rs[i] = t.x, ln_dm[i] = t.y;
+        }
+      }
+      auto fin = [&](float v, int i, int j, int e) -> float {
+        if constexpr (LNC)
+          return __builtin_fmaf(-ln_dm[i], cs[j][e], v) * ln_rs[i];
+        else
+          return v;
+      };
 #pragma unroll
       for (int i = 0; i < TM; i++) {
 #pragma unroll
@@ -420,15 +575,19 @@ __global__ __launch_bounds__(64 * WGM * WGN) __attribute__((amdgpu_waves_per_eu(
           for (int q = 0; q < 4; q++) {
             const int r = rw + i * 32 + lr, c = mfma_row(4 * q, lane);  // 4 consecutive columns from c
             const f32x16 &a = acc[i][2 * jp], &b = acc[i][2 * jp + 1];
+            const int ja = 2 * jp, jb = 2 * jp + 1;
             if constexpr (!G) {
               *(T4 *)(st + r * LD + cw + jp * 64 + c) =
-                  T4{to_elem<T>(a[4 * q]), to_elem<T>(a[4 * q + 1]), to_elem<T>(a[4 * q + 2]), to_elem<T>(a[4 * q + 3])};
+                  T4{to_elem<T>(fin(a[4 * q], i, ja, 4 * q)), to_elem<T>(fin(a[4 * q + 1], i, ja, 4 * q + 1)),
+                     to_elem<T>(fin(a[4 * q + 2], i, ja, 4 * q + 2)), to_elem<T>(fin(a[4 * q + 3], i, ja, 4 * q + 3))};
               *(T4 *)(st + r * LD + cw + jp * 64 + 32 + c) =
-                  T4{to_elem<T>(b[4 * q]), to_elem<T>(b[4 * q + 1]), to_elem<T>(b[4 * q + 2]), to_elem<T>(b[4 * q + 3])};
+                  T4{to_elem<T>(fin(b[4 * q], i, jb, 4 * q)), to_elem<T>(fin(b[4 * q + 1], i, jb, 4 * q + 1)),
+                     to_elem<T>(fin(b[4 * q + 2], i, jb, 4 * q + 2)), to_elem<T>(fin(b[4 * q + 3], i, jb, 4 * q + 3))};
             } else {
               T4 o;
 #pragma unroll
-              for (int t = 0; t < 4; t++) o[t] = to_elem<T>(gelu_erf<T>(a[4 * q + t]) * b[4 * q + t]);
+              for (int t = 0; t < 4; t++)
+                o[t] = to_elem<T>(gelu_erf<T>(fin(a[4 * q + t], i, ja, 4 * q + t)) * fin(b[4 * q + t], i, jb, 4 * q + t));
               *(T4 *)(st + r * LD + (cw + jp * 64) / 2 + c) = o;
             }
           }
@@ -439,9 +598,9 @@ __global__ __launch_bounds__(64 * WGM * WGN) __attribute__((amdgpu_waves_per_eu(
       constexpr int V = OC / EPV;
       store_staged<T, BM, V, NT, LD>(st, Cout, ldo, m0, oc0, g.M, tid);
     };
-    if constexpr (EPI == EPI_STORE) {
+    if constexpr (EPI == EPI_STORE || EPI == EPI_STORE_LN) {
       emit(std::false_type{}, (T *)gC, g.ldc);
-    } else if constexpr (EPI == EPI_GEGLU) {
+    } else if constexpr (GATED) {
       emit(std::true_type{}, (T *)gC, g.ldc);
     } else {
       emit(std::false_type{}, (T *)gC, g.ldc);
@@ -491,7 +650,7 @@ hipError_t launch_cfg(int epi, const GemmArgs &a, hipStream_t s, int splits = 1)
 // WGM rows of waves (64-row wave tiles when BM = 256 and WGM = 4).
 template <class T, int BM, int BN, int RB, int NSTAGE, int WPE, int EPI = EPI_F32, int WGM = 2>
 hipError_t launch_cfg_one(const GemmArgs &a, hipStream_t s, int splits = 1) {
-  static_assert(EPI == EPI_F32 || EPI == EPI_GEGLU_BWD, "epilogues that take 96-column wave tiles");
+  static_assert(EPI == EPI_F32 || EPI == EPI_F32_LN || EPI == EPI_GEGLU_BWD, "epilogues that take 96-column wave tiles");
   constexpr int WGN = BN / 96;  // 96-column wave tiles: 2 x 2 waves for 192 columns, 2 x 4 for 384
   static_assert(WGN * 96 == BN && (WGN == 2 || WGN == 4), "96-column wave tiles");
   static_assert(WGM * WGN <= 8, "at most 8 waves per workgroup");
@@ -1029,8 +1188,14 @@ bool gemm_shape_ok(int precision, int N, int K) {
 }
 
 bool gemm_epi_ok(int precision, int epi, int M) {
+  if (epi >= EPI_F32_LN) return precision == PREC_BF16 && M > 1024;
   if (epi != EPI_GEGLU_BWD) return true;
   return prec16(precision) ? M > 128 : M > 1024;
+}
+
+bool gemm_ln_fold_ok(int precision, int M, int hidden, int inter) {
+  return precision == PREC_BF16 && M > 1024 && hidden % kLnPartCols == 0 && hidden / kLnPartCols <= 8 &&
+         3 * hidden > 1024 && (3 * hidden) % 128 == 0 && (2 * inter) % 128 == 0 && inter % 64 == 0;
 }
 
 // Any-shape GEMM (model geometries the MFMA kernels do not tile): thread n of
@@ -1134,8 +1299,45 @@ hipError_t launch_gemm(int precision, int epi, const GemmArgs &a0, hipStream_t s
   return launch_cfg<float, 256, 128, 128, 3, 1>(epi, a, s);
 }
 
+// The folded-LayerNorm forms on the tiles launch_gemm16 gives their plain
+// counterparts at M > 1024 (the 192-column residual tiles; the store and
+// GeGLU tiles of N > 1024).
+template <class T, int BM, int BN, int RB, int NSTAGE, int WPE, int EPI>
+hipError_t launch_fold_cfg(const GemmArgs &a, hipStream_t s) {
+  const int tiles = ((a.M + BM - 1) / BM) * (a.N / BN);
+  hipLaunchKernelGGL((gemm_nt_kernel<T, BM, BN, RB, NSTAGE, EPI, WPE, 2, 2>), dim3(tiles), dim3(256), 0, s, a);
+  return hipGetLastError();
+}
+
+template <class T>
+hipError_t launch_gemm_fold(int epi, const GemmArgs &a, hipStream_t s) {
+  const bool medium = a.M <= 4096;
+  if (epi == EPI_F32_LN) {
+    if (a.N % kLnPartCols || a.lparts != a.N / kLnPartCols || !a.accumulate || a.ldc % 4 || a.n_store != a.N ||
+        !a.fx || !a.lw || !a.lpart)
+      return hipErrorInvalidValue;
+    if (medium) return launch_cfg_one<T, 64, 192, 128, 4, 1, EPI_F32_LN>(a, s);
+    return launch_cfg_one<T, 256, 192, 128, 2, 2, EPI_F32_LN, 4>(a, s);
+  }
+  if (a.lparts < 1 || a.lparts > 8 || a.lparts * kLnPartCols != a.K || !a.lpart || !a.lcs ||
+      (epi == EPI_STORE_LN && a.N <= 1024))
+    return hipErrorInvalidValue;
+  if (epi == EPI_STORE_LN) {
+    if (medium) return launch_fold_cfg<T, 128, 128, 64, 3, 3, EPI_STORE_LN>(a, s);
+    return launch_fold_cfg<T, 256, 128, 64, 3, 2, EPI_STORE_LN>(a, s);
+  }
+  if (a.M <= 8192) return launch_fold_cfg<T, 128, 128, 64, 3, 3, EPI_GEGLU_LN>(a, s);
+  return launch_fold_cfg<T, 256, 128, 64, 3, 2, EPI_GEGLU_LN>(a, s);
+}
+
 template <class T>
 hipError_t launch_gemm16(int epi, const GemmArgs &a, hipStream_t s) {
+  if (epi >= EPI_F32_LN) {
+    if constexpr (std::is_same<T, bf16>::value)
+      return launch_gemm_fold<T>(epi, a, s);
+    else
+      return hipErrorInvalidValue;
+  }
   const bool small = a.M <= 1024;
   {
     if (small) return launch_cfg<T, 64, 128, 128, 4, 1>(epi, a, s);

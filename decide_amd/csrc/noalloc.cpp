@@ -6,8 +6,9 @@
 // inputs and outputs (the activations, the batch layout, the head's
 // scratch) is carved out of one static device array per GPU, `scratch`, of
 // kScratchBytes. The call makes no hipMalloc / hipFree and uses no
-// allocating library routine; the RoPE tables and the error flag come from
-// set-up (dn_set_config).
+// allocating library routine; the RoPE tables, the error flag and the
+// folded LayerNorm's column-sum array come from set-up (dn_set_config; the
+// column sums are refilled by a kernel when the weights have changed).
 //
 // Every call on a GPU shares that GPU's array and it keeps the last call's
 // contents: calls that overlap on one GPU (two contexts, two streams) race.
@@ -102,6 +103,11 @@ extern "C" int dn_forward_device_noalloc(dn_ctx *c, int nseq, const int32_t *seq
   w.head_s1 = (float *)take(sizeof(float) * R1 * H);
   w.head_d = (float *)take(sizeof(float) * R1 * (H / 2));
   if (T <= kSmallSplitMaxTokens) w.part = (float *)take(sizeof(float) * kSmallSplitParts * Tz * H);
+  if (fold_eligible(c, T)) {  // the folded LayerNorm's statistics, as dn_forward_device has them
+    w.lpart = (double *)take(sizeof(double) * 2 * (H / kLnPartCols) * Tz);
+    w.lmean1 = (float *)take(sizeof(float) * Tz);
+    w.lmean2 = (float *)take(sizeof(float) * Tz);
+  }
   w.seq_off = (int *)take(sizeof(int) * (nseq + 1));
   w.seq_len = (int *)take(sizeof(int) * (nseq + 1));
   w.chunk_off = (int *)take(sizeof(int) * (nseq + 1));
@@ -111,7 +117,7 @@ extern "C" int dn_forward_device_noalloc(dn_ctx *c, int nseq, const int32_t *seq
   w.codes = (uint32_t *)take(sizeof(uint32_t) * ATTN_MAXKT * (2 * nwork + nwork2 + 1));
   w.first = (int *)take(sizeof(int) * (2 * nwork + nwork2 + 1));
   if (off > kScratchBytes) {
-    const size_t per_token = sizeof(float) * H + es * (5 * H + I) + sizeof(int);
+    const size_t per_token = sizeof(float) * H + es * (5 * H + I) + sizeof(int) + fold_bytes_per_token(c);
     return fail(c, DN_INVALID_ARG, "decide_hip: dn_forward_device_noalloc: this batch (" + std::to_string(T) +
                                        " tokens, " + std::to_string(nrows) + " rows) needs " + std::to_string(off) +
                                        " bytes of scratch; the maximum is " + std::to_string(kScratchBytes) +

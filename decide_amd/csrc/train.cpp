@@ -652,6 +652,7 @@ int dn_adamw_step(dn_ctx *c, float lr, float head_lr, float weight_decay, float 
                                         inv_sqrt_b2c, c->stream));
   for (auto &kv : c->w)
     if (!frozen(tr, kv.first)) kv.second.train.wt_valid = false;
+  c->wgen++;  // the folded LayerNorm's column sums follow the new weights
   HIPCHK(c, "hipStreamSynchronize", hipStreamSynchronize(c->stream));
   return DN_OK;
 }

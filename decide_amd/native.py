@@ -71,6 +71,7 @@ _SIGS = {
     "dn_synchronize": ([_vp], _i),
     "dn_set_stream_split": ([_vp, _i], _i),
     "dn_set_row_tail": ([_vp, _i], _i),
+    "dn_set_ln_fold": ([_vp, _i], _i),
     "dn_set_certify": ([_vp, _c.c_float], _i),
     "dn_set_small_m_loads": ([_vp, _i], _i),
     "dn_read_certify": ([_vp, _c.POINTER(_c.c_int64), _c.POINTER(_c.c_int64)], _i),

@@ -274,6 +274,11 @@ class Engine:
         quarter of them) finish the last layer on the option rows only (0: off)."""
         check(lib.dn_set_row_tail(self._h, int(min_tokens)), self._h)
 
+    def set_ln_fold(self, on: bool) -> None:
+        """dn_set_ln_fold: bf16 forwards of more than 1024 tokens run attn_norm
+        and mlp_norm inside the GEMMs around them (default on)."""
+        check(lib.dn_set_ln_fold(self._h, int(bool(on))), self._h)
+
     def set_small_m_loads(self, mode: int) -> None:
         """dn_set_small_m_loads: 1 operands of the small-M GEMMs through LDS (default), 0 into registers."""
         check(lib.dn_set_small_m_loads(self._h, int(mode)), self._h)

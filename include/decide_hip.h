@@ -207,6 +207,21 @@ int dn_set_stream_split(dn_ctx *ctx, int min_tokens);
  * (forward.go:212-243 runs every layer over all tokens, then gathers). */
 int dn_set_row_tail(dn_ctx *ctx, int min_tokens);
 
+/* bf16 inference forwards of more than 1024 tokens (or parts of a two-stream
+ * forward) run attn_norm and mlp_norm folded into the GEMMs around them: the
+ * residual GEMM before a LayerNorm (Wo, MlpWo) also writes the norm's operand
+ * bf16((x - m) * w) of the new residual row x, with m the row mean of the
+ * previous LayerNorm and w the norm weight, and per 192 columns the row's
+ * fp64 (mean, M2); the GEMM after it (QKV, Wi) merges those into the row's
+ * mean and rstd and computes rstd * (A.B^T - (mean - m) * sum_k w[k] B[n][k]),
+ * i.e. LayerNorm(x).B^T, so the LayerNorm launches (a read of the fp32
+ * residual stream each) disappear. The logits move by the bf16 rounding of
+ * the operand (x - m) * w instead of the normalised row, the same size of
+ * error. on = 0 runs the LayerNorm kernels; the default is on. No
+ * counterpart in the reference (forward.go:289-294, :324 normalise, then
+ * project). */
+int dn_set_ln_fold(dn_ctx *ctx, int on);
+
 /* How the small-M GEMM kernel (batches of at most 128 tokens, 16-bit modes,
  * 32 x 32 output tiles) loads its operands: 1 (the default) whole 128-byte
  * rows into LDS by global->LDS DMA, then the MFMA fragments from LDS; 0 each

@@ -105,6 +105,10 @@ def set_workers(n: int) -> None:
 # them; they exist to attribute the bf16 path's logit error to its stages and
 # are not part of the reference's arithmetic.
 ROUND_XN, ROUND_QKV, ROUND_QK, ROUND_P, ROUND_CTX, ROUND_ACT = 1, 2, 4, 8, 16, 32
+# The folded LayerNorm's operand instead of ROUND_XN's: the norm input x
+# rounded (XFOLD), or x less the previous LayerNorm's row mean (XFOLDC),
+# with the statistics of the unrounded rows.
+ROUND_XFOLD, ROUND_XFOLDC = 256, 512
 
 
 def set_rounding(mask: int, layers=(0, 1 << 30)) -> None:

@@ -143,6 +143,9 @@ enum : int {
   RND_CTX = 16,   // attention output (Wo's operand)
   RND_ACT = 32,   // GeGLU output (MlpWo's operand)
   RND_FP16 = 128, // round the stages above to IEEE binary16 instead of bfloat16
+  RND_XFOLD = 256, // LayerNorm folded into the GEMM after it: the LayerNorm input x rounded,
+                   // the statistics taken from the unrounded x, the output not rounded
+  RND_XFOLDC = 512, // as RND_XFOLD, x less the previous LayerNorm's row mean rounded
 };
 inline float bf16_round(float x) {
   uint32_t u;
@@ -169,6 +172,24 @@ void round_if(int bit, float *x, size_t n) {
     for (size_t i = 0; i < n; i++) x[i] = fp16_round(x[i]);
   else
     for (size_t i = 0; i < n; i++) x[i] = bf16_round(x[i]);
+}
+
+// RND_XFOLD: y = (round(x) - mean) * rstd * w with the statistics of the
+// unrounded rows, as a device path that multiplies the rounded residual
+// stream by w-scaled weights and subtracts mean * (column sums) afterwards
+// computes it.
+void fold_if(float *y, const float *x, int rows, int dim, const float *w, const float *mean, const float *rstd,
+             const float *prev_mean) {
+  if (!(g_round_now & (RND_XFOLD | RND_XFOLDC))) return;
+  const bool centred = (g_round_now & RND_XFOLDC) != 0;
+  for (int r = 0; r < rows; r++) {
+    const float mp = centred && prev_mean ? prev_mean[r] : 0.0f;
+    for (int i = 0; i < dim; i++) {
+      float v = x[(size_t)r * dim + i] - mp;
+      v = (g_round_now & RND_FP16) ? fp16_round(v) : bf16_round(v);
+      y[(size_t)r * dim + i] = (v - (mean[r] - mp)) * rstd[r] * w[i];
+    }
+  }
 }
 
 // parallelFor, internal/nn/ops.go:13-44.
@@ -735,6 +756,7 @@ int forward_impl(const Model &m, int nseq, const int32_t *seq_len, const int32_t
 
   LayerCache frozen;
   std::vector<float> tmp((size_t)T * H);
+  std::vector<float> fold_prev;  // RND_XFOLDC: the previous LayerNorm's row means
   for (int l = 0; l < L; l++) {
     std::string p = "model.layers." + std::to_string(l) + ".";
     const float *attnNorm = m.get(p + "attn_norm.weight");
@@ -761,6 +783,8 @@ int forward_impl(const Model &m, int nseq, const int32_t *seq_len, const int32_t
       layer_norm(lc.n1.data(), in, T, H, attnNorm, nullptr, cfg.eps, lc.mean1.data(), lc.rstd1.data());
       x1 = lc.n1.data();
       round_if(RND_XN, lc.n1.data(), (size_t)T * H);
+      fold_if(lc.n1.data(), in, T, H, attnNorm, lc.mean1.data(), lc.rstd1.data(),
+              fold_prev.empty() ? nullptr : fold_prev.data());
     } else if (g_round_now & RND_XN) {
       x0r.assign(in, in + (size_t)T * H);
       round_if(RND_XN, x0r.data(), x0r.size());
@@ -789,6 +813,9 @@ int forward_impl(const Model &m, int nseq, const int32_t *seq_len, const int32_t
     lc.rstd2.resize(T);
     layer_norm(lc.n2.data(), lc.h1.data(), T, H, mlpNorm, nullptr, cfg.eps, lc.mean2.data(), lc.rstd2.data());
     round_if(RND_XN, lc.n2.data(), (size_t)T * H);
+    fold_if(lc.n2.data(), lc.h1.data(), T, H, mlpNorm, lc.mean2.data(), lc.rstd2.data(),
+            l > 0 ? lc.mean1.data() : nullptr);
+    fold_prev = lc.mean2;
     lc.wi.resize((size_t)T * 2 * I);
     linear(lc.wi.data(), lc.n2.data(), T, H, Wi, 2 * I);
     lc.act.resize((size_t)T * I);
