@@ -446,10 +446,10 @@ int small_split_parts(int precision, int T, int N, int K) {
 
 // A projection GEMM of the model: the MFMA kernels, or the any-shape kernel
 // for geometries they do not tile.
-hipError_t layer_gemm(const Config &g, int epi, const GemmArgs &a0, hipStream_t s) {
+hipError_t layer_gemm(const Config &g, int epi, const GemmArgs &a0, hipStream_t s, const LnFold *ln = nullptr) {
   GemmArgs a = a0;
   a.skinny_regs = g.skinny_regs ? 1 : 0;
-  return g.generic ? launch_gemm_generic(g.precision, epi, a, s) : launch_gemm(g.precision, epi, a, s);
+  return g.generic ? launch_gemm_generic(g.precision, epi, a, s) : launch_gemm(g.precision, epi, a, s, ln);
 }
 
 // The launches of encoder layer l over the pass's tokens: the residual stream
@@ -506,15 +506,16 @@ int enqueue_layer(dn_ctx *c, const Pass &p, int l, float *in, float *h1, float *
   q.N = 3 * H;
   q.K = H;
   q.n_store = 3 * H;
+  LnFold qf{};
   if (fold_in) {
-    q.lpart = w.lpart;
-    q.lparts = lparts;
-    q.mprev = w.lmean2;  // what the previous MlpWo subtracted: its layer's mlp_norm means
-    q.mean_out = w.lmean1;
-    q.lcs = fold_cs_qkv(c, l);
-    q.eps = g.eps;
+    qf.lpart = w.lpart;
+    qf.lparts = lparts;
+    qf.mprev = w.lmean2;  // what the previous MlpWo subtracted: its layer's mlp_norm means
+    qf.mean_out = w.lmean1;
+    qf.lcs = fold_cs_qkv(c, l);
+    qf.eps = g.eps;
   }
-  PROBED(ev, DN_PROBE_QKV, "gemm(Wqkv)", layer_gemm(g, fold_in ? EPI_STORE_LN : EPI_STORE, q, s));
+  PROBED(ev, DN_PROBE_QKV, "gemm(Wqkv)", layer_gemm(g, fold_in ? EPI_STORE_LN : EPI_STORE, q, s, &qf));
 
   const float *rope = (const float *)c->rope.p;
   const size_t tab = (size_t)kPositions * 32;
@@ -566,6 +567,9 @@ int enqueue_layer(dn_ctx *c, const Pass &p, int l, float *in, float *h1, float *
   o.n_store = H;
   o.accumulate = 1;
   void *x2 = S ? S->n2.p : w.xn;
+  // The row value the folded mlp_norm's operand is taken relative to: this
+  // layer's attn_norm means when its QKV folded too (0 otherwise).
+  float *const mlp_mprev = fold_in ? w.lmean1 : nullptr;
   const int wo_parts = split ? small_split_parts(prec, T, H, H) : 1;
   if (wo_parts > 1) {
     o.skinny_regs = g.skinny_regs ? 1 : 0;
@@ -573,12 +577,13 @@ int enqueue_layer(dn_ctx *c, const Pass &p, int l, float *in, float *h1, float *
     HIPCHK(c, "ln(mlp_norm)", launch_ln_parts(prec, h1, w.part, wo_parts, T, H,
                                               (const float *)W(c, pf + "mlp_norm.weight"), g.eps, x2, s));
   } else if (fold) {
-    o.fx = x2;
-    o.lw = (const float *)W(c, pf + "mlp_norm.weight");
-    o.lpart = w.lpart;
-    o.lparts = lparts;
-    o.mprev = fold_in ? w.lmean1 : nullptr;
-    PROBED(ev, DN_PROBE_WO, "gemm(Wo)", layer_gemm(g, EPI_F32_LN, o, s));
+    LnFold of{};
+    of.fx = x2;
+    of.lw = (const float *)W(c, pf + "mlp_norm.weight");
+    of.lpart = w.lpart;
+    of.lparts = lparts;
+    of.mprev = mlp_mprev;
+    PROBED(ev, DN_PROBE_WO, "gemm(Wo)", layer_gemm(g, EPI_F32_LN, o, s, &of));
   } else {
     PROBED(ev, DN_PROBE_WO, "gemm(Wo)", layer_gemm(g, EPI_F32, o, s));
     HIPCHK(c, "ln(mlp_norm)", launch_ln(prec, h1, T, H, (const float *)W(c, pf + "mlp_norm.weight"), g.eps, x2, s,
@@ -603,15 +608,16 @@ int enqueue_layer(dn_ctx *c, const Pass &p, int l, float *in, float *h1, float *
   } else {
     wi.C = w.act;
     wi.ldc = I;
+    LnFold wf{};
     if (fold) {
-      wi.lpart = w.lpart;
-      wi.lparts = lparts;
-      wi.mprev = o.mprev;
-      wi.mean_out = w.lmean2;
-      wi.lcs = fold_cs_wi(c, l);
-      wi.eps = g.eps;
+      wf.lpart = w.lpart;
+      wf.lparts = lparts;
+      wf.mprev = mlp_mprev;
+      wf.mean_out = w.lmean2;
+      wf.lcs = fold_cs_wi(c, l);
+      wf.eps = g.eps;
     }
-    PROBED(ev, DN_PROBE_WI, "gemm(Wi)", layer_gemm(g, fold ? EPI_GEGLU_LN : EPI_GEGLU, wi, s));
+    PROBED(ev, DN_PROBE_WI, "gemm(Wi)", layer_gemm(g, fold ? EPI_GEGLU_LN : EPI_GEGLU, wi, s, &wf));
   }
 
   GemmArgs mo{};
@@ -630,17 +636,18 @@ int enqueue_layer(dn_ctx *c, const Pass &p, int l, float *in, float *h1, float *
   const int parts = split && mo_parts ? small_split_parts(prec, T, H, I) : 1;
   if (mo_parts) *mo_parts = parts > 1 ? parts : 0;
   mo.skinny_regs = g.skinny_regs ? 1 : 0;
+  LnFold mf{};
   if (fold_out) {
-    mo.fx = w.xn;
-    mo.lw = (const float *)W(c, layer_prefix(l + 1) + "attn_norm.weight");
-    mo.lpart = w.lpart;
-    mo.lparts = lparts;
-    mo.mprev = w.lmean2;
+    mf.fx = w.xn;
+    mf.lw = (const float *)W(c, layer_prefix(l + 1) + "attn_norm.weight");
+    mf.lpart = w.lpart;
+    mf.lparts = lparts;
+    mf.mprev = w.lmean2;
   }
   if (parts > 1)
     PROBED(ev, DN_PROBE_MLPWO, "gemm(MlpWo)", launch_gemm_small_split(prec, mo, parts, w.part, s));
   else
-    PROBED(ev, DN_PROBE_MLPWO, "gemm(MlpWo)", layer_gemm(g, fold_out ? EPI_F32_LN : EPI_F32, mo, s));
+    PROBED(ev, DN_PROBE_MLPWO, "gemm(MlpWo)", layer_gemm(g, fold_out ? EPI_F32_LN : EPI_F32, mo, s, &mf));
   return DN_OK;
 }
 

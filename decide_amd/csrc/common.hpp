@@ -243,16 +243,21 @@ struct GemmArgs {
   const void *gin;  // EPI_GEGLU_BWD: the GeGLU input (the Wi output, M x 2N, row stride ldc)
   int skinny_regs;  // small-M kernel, 16-bit 32 x 32 tiles: operands loaded straight into registers
                     // (0: whole 128-byte rows through LDS by global->LDS DMA)
-  // LayerNorm folded into the GEMMs on either side of it (bf16 inference).
-  // The residual GEMM (EPI_F32_LN) also writes fx = bf16((x - mprev[row]) *
-  // lw[col]) of the new residual x (row stride ldc) and, per row and
-  // 192-column N-tile, the tile's (mean, M2) of x to lpart (lparts pairs per
-  // row). The GEMM that takes fx as A (EPI_STORE_LN, EPI_GEGLU_LN) merges
-  // them into the row's mean and rstd = 1/sqrt(M2/K + eps) and computes
-  // rstd * (A.B^T - (mean - mprev[row]) * lcs[col]) with lcs[n] =
-  // sum_k lw[k] B[n][k], i.e. LayerNorm(x).B^T with the LayerNorm weight in
-  // lcs and in fx; its tiles at n0 = 0 write the row mean to mean_out.
-  // mprev null: 0.
+};
+
+// LayerNorm folded into the GEMMs on either side of it (bf16 inference),
+// the EPI_*_LN forms' second kernel argument (GemmArgs stays at its size:
+// larger kernel arguments cost every launch ~0.6 us, which the small-batch
+// forwards' ~160 launches feel). The residual GEMM (EPI_F32_LN) also writes
+// fx = bf16((x - mprev[row]) * lw[col]) of the new residual x (row stride
+// ldc) and, per row and 192-column N-tile, the tile's (mean, M2) of x to
+// lpart (lparts pairs per row). The GEMM that takes fx as A (EPI_STORE_LN,
+// EPI_GEGLU_LN) merges them into the row's mean and rstd = 1/sqrt(M2/K +
+// eps) and computes rstd * (A.B^T - (mean - mprev[row]) * lcs[col]) with
+// lcs[n] = sum_k lw[k] B[n][k], i.e. LayerNorm(x).B^T with the LayerNorm
+// weight in lcs and in fx; its tiles at n0 = 0 write the row mean to
+// mean_out. mprev null: 0.
+struct LnFold {
   void *fx;
   const float *lw, *lcs, *mprev;
   double *lpart;
@@ -277,7 +282,7 @@ constexpr int kLnPartCols = 192;
 // rows (the configurations launch_gemm tiles for EPI_*_LN).
 bool gemm_ln_fold_ok(int precision, int M, int hidden, int inter);
 
-hipError_t launch_gemm(int precision, int epi, const GemmArgs &a, hipStream_t s);
+hipError_t launch_gemm(int precision, int epi, const GemmArgs &a, hipStream_t s, const LnFold *ln = nullptr);
 // Any-shape GEMM for model geometries the MFMA kernels do not tile: one thread
 // per output element, an fp32 dot product over K in order. EPI_F32,
 // EPI_STORE and EPI_GEGLU, the last over the natural Wi layout (value rows

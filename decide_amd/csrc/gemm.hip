@@ -152,17 +152,18 @@ __device__ __forceinline__ void store_staged(const T *st, T *C, int ldc, int m0,
 // rounded to float as that kernel rounds them; write_mean also stores the
 // row's mean.
 constexpr int kLnMaxParts = 8;  // launch_gemm checks lparts <= 8
-__device__ __forceinline__ void ln_fold_load(const GemmArgs &g, int row, double2 (&v)[kLnMaxParts], float &mp) {
-  const int rr = min(row, g.M - 1), np = g.lparts;
-  const double2 *pp = (const double2 *)g.lpart + (size_t)rr * np;
+__device__ __forceinline__ void ln_fold_load(const GemmArgs &g, const LnFold &lf, int row, double2 (&v)[kLnMaxParts],
+                                             float &mp) {
+  const int rr = min(row, g.M - 1), np = lf.lparts;
+  const double2 *pp = (const double2 *)lf.lpart + (size_t)rr * np;
 #pragma unroll
   for (int t = 0; t < kLnMaxParts; t++)
     if (t < np) v[t] = pp[t];
-  mp = g.mprev ? g.mprev[rr] : 0.0f;
+  mp = lf.mprev ? lf.mprev[rr] : 0.0f;
 }
-__device__ __forceinline__ float2 ln_fold_merge(const GemmArgs &g, int row, const double2 (&v)[kLnMaxParts], float mp,
-                                                bool write_mean) {
-  const int np = g.lparts;
+__device__ __forceinline__ float2 ln_fold_merge(const GemmArgs &g, const LnFold &lf, int row,
+                                                const double2 (&v)[kLnMaxParts], float mp, bool write_mean) {
+  const int np = lf.lparts;
   double sum = 0;
 #pragma unroll
   for (int t = 0; t < kLnMaxParts; t++)
@@ -176,13 +177,15 @@ __device__ __forceinline__ float2 ln_fold_merge(const GemmArgs &g, int row, cons
       m2 += v[t].y + (double)kLnPartCols * d * d;
     }
   const float mean = (float)mu;
-  if (write_mean && row < g.M) g.mean_out[row] = mean;
-  return make_float2((float)(1.0 / sqrt(m2 / (double)g.K + (double)g.eps)), mean - mp);
+  if (write_mean && row < g.M) lf.mean_out[row] = mean;
+  return make_float2((float)(1.0 / sqrt(m2 / (double)g.K + (double)lf.eps)), mean - mp);
 }
 
 // WGM x WGN waves tile the BM x BN block; each wave owns a WM x WN sub-tile.
+// The body of gemm_nt_kernel and gemm_nt_ln_kernel (lf: the folded
+// LayerNorm's arguments, used by the EPI_*_LN forms only).
 template <class T, int BM, int BN, int RB, int NSTAGE, int EPI, int WPE, int WGM, int WGN>
-__global__ __launch_bounds__(64 * WGM * WGN) __attribute__((amdgpu_waves_per_eu(WPE))) void gemm_nt_kernel(GemmArgs g) {
+__device__ __forceinline__ void gemm_nt_tile(const GemmArgs &g, const LnFold &lf) {
   using MF = Mfma<T>;
   typedef typename MF::frag frag;
   constexpr int NW = WGM * WGN, NT = 64 * NW;
@@ -227,8 +230,8 @@ __global__ __launch_bounds__(64 * WGM * WGN) __attribute__((amdgpu_waves_per_eu(
   double2 ln_v[LNC ? kLnMaxParts : 1];
   float ln_mp = 0.0f, ln_c = 0.0f;
   if constexpr (LNC) {
-    if (threadIdx.x < BM) ln_fold_load(g, m0 + (int)threadIdx.x, ln_v, ln_mp);
-    if (threadIdx.x < BN) ln_c = g.lcs[n0 + threadIdx.x];
+    if (threadIdx.x < BM) ln_fold_load(g, lf, m0 + (int)threadIdx.x, ln_v, ln_mp);
+    if (threadIdx.x < BN) ln_c = lf.lcs[n0 + threadIdx.x];
   }
   // Split-K: blockIdx.y takes K elements [y*K, (y+1)*K) of A and B and writes
   // its own partial output.
@@ -275,7 +278,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) __attribute__((amdgpu_waves_per_eu(
 #pragma unroll
   for (int s = 0; s < NSTAGE - 1; s++) issue(s, min(s, nk - 1) * KT);
   if constexpr (LNC) {
-    if (threadIdx.x < BM) ln_st[threadIdx.x] = ln_fold_merge(g, m0 + (int)threadIdx.x, ln_v, ln_mp, n0 == 0);
+    if (threadIdx.x < BM) ln_st[threadIdx.x] = ln_fold_merge(g, lf, m0 + (int)threadIdx.x, ln_v, ln_mp, n0 == 0);
     if (threadIdx.x < BN) ln_cs[threadIdx.x] = ln_c;
   }
 
@@ -448,13 +451,13 @@ __global__ __launch_bounds__(64 * WGM * WGN) __attribute__((amdgpu_waves_per_eu(
     float4 lw4[LN ? CW / 4 : 1];
     if constexpr (LN) {
 #pragma unroll
-      for (int q = 0; q < CW / 4; q++) lw4[q] = *(const float4 *)(g.lw + n0 + (tid & 7) * CW + 4 * q);
+      for (int q = 0; q < CW / 4; q++) lw4[q] = *(const float4 *)(lf.lw + n0 + (tid & 7) * CW + 4 * q);
     }
 #pragma unroll
     for (int pass = 0; pass < WGM; pass++) {
       float ln_mp = 0.0f;
       if constexpr (LN)
-        if (g.mprev) ln_mp = g.mprev[min(m0 + pass * HM + (tid >> 3), g.M - 1)];
+        if (lf.mprev) ln_mp = lf.mprev[min(m0 + pass * HM + (tid >> 3), g.M - 1)];
       stage_f32(st, LD, pass);
       __syncthreads();
 #pragma unroll
@@ -491,7 +494,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) __attribute__((amdgpu_waves_per_eu(
         {
           const int row = m0 + pass * HM + r;
           if (row < g.M) {
-            T *f = (T *)g.fx + (size_t)row * g.ldc + n0 + part * CW;
+            T *f = (T *)lf.fx + (size_t)row * g.ldc + n0 + part * CW;
 #pragma unroll
             for (int q = 0; q < CW / 4; q += 2) {
               const float4 a = xv[q], b = xv[q + 1], wa = lw4[q], wb = lw4[q + 1];
@@ -522,7 +525,7 @@ __global__ __launch_bounds__(64 * WGM * WGN) __attribute__((amdgpu_waves_per_eu(
         m2 += __shfl_xor(m2, 2);
         m2 += __shfl_xor(m2, 4);
         const int row = m0 + pass * HM + r;
-        if (part == 0 && row < g.M) ((double2 *)g.lpart)[(size_t)row * g.lparts + n0 / BN] = make_double2(mu, m2);
+        if (part == 0 && row < g.M) ((double2 *)lf.lpart)[(size_t)row * lf.lparts + n0 / BN] = make_double2(mu, m2);
       }
       if (pass + 1 < WGM) {
         load_old(pass + 1);
@@ -610,6 +613,18 @@ __global__ __launch_bounds__(64 * WGM * WGN) __attribute__((amdgpu_waves_per_eu(
   }
 }
 
+template <class T, int BM, int BN, int RB, int NSTAGE, int EPI, int WPE, int WGM, int WGN>
+__global__ __launch_bounds__(64 * WGM * WGN) __attribute__((amdgpu_waves_per_eu(WPE))) void gemm_nt_kernel(GemmArgs g) {
+  static_assert(EPI < EPI_F32_LN, "the folded-LayerNorm forms run as gemm_nt_ln_kernel");
+  gemm_nt_tile<T, BM, BN, RB, NSTAGE, EPI, WPE, WGM, WGN>(g, LnFold{});
+}
+template <class T, int BM, int BN, int RB, int NSTAGE, int EPI, int WPE, int WGM, int WGN>
+__global__ __launch_bounds__(64 * WGM * WGN) __attribute__((amdgpu_waves_per_eu(WPE))) void gemm_nt_ln_kernel(GemmArgs g,
+                                                                                                            LnFold lf) {
+  static_assert(EPI >= EPI_F32_LN, "plain forms run as gemm_nt_kernel");
+  gemm_nt_tile<T, BM, BN, RB, NSTAGE, EPI, WPE, WGM, WGN>(g, lf);
+}
+
 template <class T, int BM, int BN, int RB, int NSTAGE, int WPE, int WGM = 2, int WGN = 2>
 hipError_t launch_cfg(int epi, const GemmArgs &a, hipStream_t s, int splits = 1) {
   const int tiles = ((a.M + BM - 1) / BM) * (a.N / BN);
@@ -649,14 +664,18 @@ hipError_t launch_cfg(int epi, const GemmArgs &a, hipStream_t s, int splits = 1)
 // wave columns (BN / 2 = 96) do not pair up for the operand-type epilogues.
 // WGM rows of waves (64-row wave tiles when BM = 256 and WGM = 4).
 template <class T, int BM, int BN, int RB, int NSTAGE, int WPE, int EPI = EPI_F32, int WGM = 2>
-hipError_t launch_cfg_one(const GemmArgs &a, hipStream_t s, int splits = 1) {
+hipError_t launch_cfg_one(const GemmArgs &a, hipStream_t s, int splits = 1, const LnFold *ln = nullptr) {
   static_assert(EPI == EPI_F32 || EPI == EPI_F32_LN || EPI == EPI_GEGLU_BWD, "epilogues that take 96-column wave tiles");
   constexpr int WGN = BN / 96;  // 96-column wave tiles: 2 x 2 waves for 192 columns, 2 x 4 for 384
   static_assert(WGN * 96 == BN && (WGN == 2 || WGN == 4), "96-column wave tiles");
   static_assert(WGM * WGN <= 8, "at most 8 waves per workgroup");
   const int tiles = ((a.M + BM - 1) / BM) * (a.N / BN);
-  hipLaunchKernelGGL((gemm_nt_kernel<T, BM, BN, RB, NSTAGE, EPI, WPE, WGM, WGN>), dim3(tiles, splits),
-                     dim3(64 * WGM * WGN), 0, s, a);
+  if constexpr (EPI == EPI_F32_LN)
+    hipLaunchKernelGGL((gemm_nt_ln_kernel<T, BM, BN, RB, NSTAGE, EPI, WPE, WGM, WGN>), dim3(tiles, splits),
+                       dim3(64 * WGM * WGN), 0, s, a, *ln);
+  else
+    hipLaunchKernelGGL((gemm_nt_kernel<T, BM, BN, RB, NSTAGE, EPI, WPE, WGM, WGN>), dim3(tiles, splits),
+                       dim3(64 * WGM * WGN), 0, s, a);
   return hipGetLastError();
 }
 
@@ -1251,9 +1270,9 @@ hipError_t launch_gemm_generic(int precision, int epi, const GemmArgs &a, hipStr
 // The tiled kernel's configuration for 16-bit operands (bf16 or fp16; the
 // same tiles, measured on bf16).
 template <class T>
-hipError_t launch_gemm16(int epi, const GemmArgs &a, hipStream_t s);
+hipError_t launch_gemm16(int epi, const GemmArgs &a, hipStream_t s, const LnFold *ln);
 
-hipError_t launch_gemm(int precision, int epi, const GemmArgs &a0, hipStream_t s) {
+hipError_t launch_gemm(int precision, int epi, const GemmArgs &a0, hipStream_t s, const LnFold *ln) {
   if (a0.M <= 0) return hipSuccess;
   if (!gemm_epi_ok(precision, epi, a0.M) || (epi == EPI_GEGLU_BWD && (!a0.gin || a0.ldc % 8))) return hipErrorInvalidValue;
   // Small M goes to the whole-K kernel (grid: N/32 x M/64 workgroups). In
@@ -1293,8 +1312,8 @@ hipError_t launch_gemm(int precision, int epi, const GemmArgs &a0, hipStream_t s
   //    (isolated launches on the training shapes, 3840 rows: Wi + GeGLU 36.4
   //    -> 31.3 us, dX GEMMs N = 768 K = 2304 32.3 -> 30.4 us, dctx 16.0 ->
   //    12.6 us).
-  if (precision == PREC_BF16) return launch_gemm16<bf16>(epi, a, s);
-  if (precision == PREC_F16) return launch_gemm16<f16>(epi, a, s);
+  if (precision == PREC_BF16) return launch_gemm16<bf16>(epi, a, s, ln);
+  if (precision == PREC_F16) return launch_gemm16<f16>(epi, a, s, ln);
   if (a.M <= 1024) return launch_cfg<float, 64, 128, 128, 4, 1>(epi, a, s);
   return launch_cfg<float, 256, 128, 128, 3, 1>(epi, a, s);
 }
@@ -1303,38 +1322,39 @@ hipError_t launch_gemm(int precision, int epi, const GemmArgs &a0, hipStream_t s
 // counterparts at M > 1024 (the 192-column residual tiles; the store and
 // GeGLU tiles of N > 1024).
 template <class T, int BM, int BN, int RB, int NSTAGE, int WPE, int EPI>
-hipError_t launch_fold_cfg(const GemmArgs &a, hipStream_t s) {
+hipError_t launch_fold_cfg(const GemmArgs &a, const LnFold &ln, hipStream_t s) {
   const int tiles = ((a.M + BM - 1) / BM) * (a.N / BN);
-  hipLaunchKernelGGL((gemm_nt_kernel<T, BM, BN, RB, NSTAGE, EPI, WPE, 2, 2>), dim3(tiles), dim3(256), 0, s, a);
+  hipLaunchKernelGGL((gemm_nt_ln_kernel<T, BM, BN, RB, NSTAGE, EPI, WPE, 2, 2>), dim3(tiles), dim3(256), 0, s, a, ln);
   return hipGetLastError();
 }
 
 template <class T>
-hipError_t launch_gemm_fold(int epi, const GemmArgs &a, hipStream_t s) {
+hipError_t launch_gemm_fold(int epi, const GemmArgs &a, const LnFold *ln, hipStream_t s) {
   const bool medium = a.M <= 4096;
+  if (!ln) return hipErrorInvalidValue;
   if (epi == EPI_F32_LN) {
-    if (a.N % kLnPartCols || a.lparts != a.N / kLnPartCols || !a.accumulate || a.ldc % 4 || a.n_store != a.N ||
-        !a.fx || !a.lw || !a.lpart)
+    if (a.N % kLnPartCols || ln->lparts != a.N / kLnPartCols || !a.accumulate || a.ldc % 4 || a.n_store != a.N ||
+        !ln->fx || !ln->lw || !ln->lpart)
       return hipErrorInvalidValue;
-    if (medium) return launch_cfg_one<T, 64, 192, 128, 4, 1, EPI_F32_LN>(a, s);
-    return launch_cfg_one<T, 256, 192, 128, 2, 2, EPI_F32_LN, 4>(a, s);
+    if (medium) return launch_cfg_one<T, 64, 192, 128, 4, 1, EPI_F32_LN>(a, s, 1, ln);
+    return launch_cfg_one<T, 256, 192, 128, 2, 2, EPI_F32_LN, 4>(a, s, 1, ln);
   }
-  if (a.lparts < 1 || a.lparts > 8 || a.lparts * kLnPartCols != a.K || !a.lpart || !a.lcs ||
+  if (ln->lparts < 1 || ln->lparts > 8 || ln->lparts * kLnPartCols != a.K || !ln->lpart || !ln->lcs ||
       (epi == EPI_STORE_LN && a.N <= 1024))
     return hipErrorInvalidValue;
   if (epi == EPI_STORE_LN) {
-    if (medium) return launch_fold_cfg<T, 128, 128, 64, 3, 3, EPI_STORE_LN>(a, s);
-    return launch_fold_cfg<T, 256, 128, 64, 3, 2, EPI_STORE_LN>(a, s);
+    if (medium) return launch_fold_cfg<T, 128, 128, 64, 3, 3, EPI_STORE_LN>(a, *ln, s);
+    return launch_fold_cfg<T, 256, 128, 64, 3, 2, EPI_STORE_LN>(a, *ln, s);
   }
-  if (a.M <= 8192) return launch_fold_cfg<T, 128, 128, 64, 3, 3, EPI_GEGLU_LN>(a, s);
-  return launch_fold_cfg<T, 256, 128, 64, 3, 2, EPI_GEGLU_LN>(a, s);
+  if (a.M <= 8192) return launch_fold_cfg<T, 128, 128, 64, 3, 3, EPI_GEGLU_LN>(a, *ln, s);
+  return launch_fold_cfg<T, 256, 128, 64, 3, 2, EPI_GEGLU_LN>(a, *ln, s);
 }
 
 template <class T>
-hipError_t launch_gemm16(int epi, const GemmArgs &a, hipStream_t s) {
+hipError_t launch_gemm16(int epi, const GemmArgs &a, hipStream_t s, const LnFold *ln) {
   if (epi >= EPI_F32_LN) {
     if constexpr (std::is_same<T, bf16>::value)
-      return launch_gemm_fold<T>(epi, a, s);
+      return launch_gemm_fold<T>(epi, a, ln, s);
     else
       return hipErrorInvalidValue;
   }
