@@ -1019,10 +1019,12 @@ def summarize_traffic(fetch_dir: str, write_dir: str, out_path: str) -> int:
 
     def gemm_params(name):
         """Template arguments of gemm_nt_kernel<bf16, BM, BN, BK, STAGES, EPI, ...>
-        from a mangled (..Li128ELi192E..) or demangled (<.., 128, 192, ..>) name."""
-        if "gemm_nt_kernel" not in name:
+        (or gemm_nt_ln_kernel, the folded-LayerNorm forms) from a mangled
+        (..Li128ELi192E..) or demangled (<.., 128, 192, ..>) name."""
+        kind = "gemm_nt_ln_kernel" if "gemm_nt_ln_kernel" in name else "gemm_nt_kernel"
+        if kind not in name:
             return None
-        tail = name.split("gemm_nt_kernel", 1)[1]
+        tail = name.split(kind, 1)[1]
         m = re.findall(r"Li(\d+)E", tail)
         if not m:
             m = re.findall(r"(?<=[<,\s])(\d+)(?=[,>])", tail.split(">")[0] + ">")
@@ -1062,7 +1064,7 @@ def summarize_traffic(fetch_dir: str, write_dir: str, out_path: str) -> int:
                          "traffic_over_algorithmic": round((fb + wb) / (alg_fold if fold else alg)[name], 3)}
     others = {}
     for k, v in fetch.items():
-        if "attention_kernel" in k or "ln_kernel" in k:
+        if "attention_kernel" in k or ("ln_kernel" in k and "gemm_nt_ln_kernel" not in k):
             # Per symbol; the summary keeps each family's most-dispatched
             # variant (attention: the full-batch layers, not the last layer's
             # row-tail variant).
