@@ -222,9 +222,10 @@ __device__ __forceinline__ void gemm_nt_tile(const GemmArgs &g, const LnFold &lf
   const TileOrder<BM, BN> to(blockIdx.x, (g.M + BM - 1) / BM, g.N / BN, g.ngroups, g.order);
   const int m0 = to.m0, n0 = to.n0;
   // Folded LayerNorm consumer: thread t < BM takes block row t's statistics
-  // and thread t < BN column n0 + t's lcs (loaded here, merged while the
-  // first stages land); the epilogue reads (rstd, mean - mprev) of its rows
-  // from ln_st and its columns' lcs from ln_cs.
+  // and thread t < BN column n0 + t's lcs (loaded here; merged after the
+  // main loop, when they have landed with the last stage, so the first
+  // stages start without waiting for them); the epilogue reads (rstd, mean -
+  // mprev) of its rows from ln_st and its columns' lcs from ln_cs.
   float2 *const ln_st = (float2 *)(smem + SMEM_RING);
   float *const ln_cs = (float *)(smem + SMEM_RING + BM * 8);
   double2 ln_v[LNC ? kLnMaxParts : 1];
@@ -277,10 +278,6 @@ __device__ __forceinline__ void gemm_nt_tile(const GemmArgs &g, const LnFold &lf
   const int nk = g.K / KT;
 #pragma unroll
   for (int s = 0; s < NSTAGE - 1; s++) issue(s, min(s, nk - 1) * KT);
-  if constexpr (LNC) {
-    if (threadIdx.x < BM) ln_st[threadIdx.x] = ln_fold_merge(g, lf, m0 + (int)threadIdx.x, ln_v, ln_mp, n0 == 0);
-    if (threadIdx.x < BN) ln_cs[threadIdx.x] = ln_c;
-  }
 
   constexpr int NKS = KT / MF::KSTEP;                  // MFMA k steps per stage
   constexpr int PER_KS = (LOADS + NKS - 1) / NKS;      // next-stage loads issued per k step
@@ -354,7 +351,16 @@ __device__ __forceinline__ void gemm_nt_tile(const GemmArgs &g, const LnFold &lf
   }
   // All waves done with the ring and every DMA landed: reuse it for the epilogue.
   wait_vmcnt<0>();
-  __builtin_amdgcn_s_barrier();
+  if constexpr (LNC) {
+    // The folded LayerNorm's row statistics (loaded at the start, landed
+    // with the last stage) and column sums, for every wave's epilogue: the
+    // barrier must also wait for these LDS writes.
+    if (threadIdx.x < BM) ln_st[threadIdx.x] = ln_fold_merge(g, lf, m0 + (int)threadIdx.x, ln_v, ln_mp, n0 == 0);
+    if (threadIdx.x < BN) ln_cs[threadIdx.x] = ln_c;
+    __syncthreads();
+  } else {
+    __builtin_amdgcn_s_barrier();
+  }
   // fp32 staging of the rows of wave row `pass` (LD floats per row).
   auto stage_f32 = [&](float *st, int LD, int pass) {
     if (wm == pass) {
