@@ -452,12 +452,14 @@ __device__ __forceinline__ void gemm_nt_tile(const GemmArgs &g, const LnFold &lf
     };
     load_old(0);
     // Folded LayerNorm: thread (row tid / 8 of the pass, part tid % 8) takes
-    // 24 consecutive columns; the LayerNorm weight at them.
-    constexpr int CW = BN / 8;
-    float4 lw4[LN ? CW / 4 : 1];
+    // the 4-column chunks 4 part + 32 q (q < 6) of the row, so that the eight
+    // threads of a row store 64 contiguous bytes of the bf16 operand per
+    // instruction; the LayerNorm weight at them.
+    constexpr int NQ = BN / 32;
+    float4 lw4[LN ? NQ : 1];
     if constexpr (LN) {
 #pragma unroll
-      for (int q = 0; q < CW / 4; q++) lw4[q] = *(const float4 *)(lf.lw + n0 + (tid & 7) * CW + 4 * q);
+      for (int q = 0; q < NQ; q++) lw4[q] = *(const float4 *)(lf.lw + n0 + 4 * (tid & 7) + 32 * q);
     }
 #pragma unroll
     for (int pass = 0; pass < WGM; pass++) {
@@ -485,35 +487,33 @@ __device__ __forceinline__ void gemm_nt_tile(const GemmArgs &g, const LnFold &lf
         }
       }
       if constexpr (LN) {
-        // The pass's rows from the staging area: eight threads per row, 24
-        // consecutive columns each. The next LayerNorm's operand
-        // bf16((x - mprev) * w) in three 16-byte stores per thread; the
-        // statistics over this tile's 192 columns: fp32 partial sums, the
-        // eight reduced in fp64 in a fixed order, then the squared
-        // deviations from the tile mean the same way (their fp32 rounding,
-        // ~1e-6 relative, is far below the bf16 operand's).
+        // The pass's rows from the staging area: eight threads per row, the
+        // chunks above. The next LayerNorm's operand bf16((x - mprev) * w),
+        // one 8-byte store per chunk; the statistics over this tile's 192
+        // columns: fp32 partial sums, the eight reduced in fp64 in a fixed
+        // order, then the squared deviations from the tile mean the same way
+        // (their fp32 rounding, ~1e-6 relative, is far below the bf16
+        // operand's).
         __syncthreads();
         const int r = tid >> 3, part = tid & 7;
-        float4 xv[CW / 4];
+        float4 xv[NQ];
 #pragma unroll
-        for (int q = 0; q < CW / 4; q++) xv[q] = *(const float4 *)(st + r * LD + part * CW + 4 * q);
+        for (int q = 0; q < NQ; q++) xv[q] = *(const float4 *)(st + r * LD + 4 * part + 32 * q);
         {
           const int row = m0 + pass * HM + r;
           if (row < g.M) {
-            T *f = (T *)lf.fx + (size_t)row * g.ldc + n0 + part * CW;
+            T *f = (T *)lf.fx + (size_t)row * g.ldc + n0 + 4 * part;
 #pragma unroll
-            for (int q = 0; q < CW / 4; q += 2) {
-              const float4 a = xv[q], b = xv[q + 1], wa = lw4[q], wb = lw4[q + 1];
-              *(uint4 *)(f + 4 * q) = make_uint4(pack16<T>((a.x - ln_mp) * wa.x, (a.y - ln_mp) * wa.y),
-                                                 pack16<T>((a.z - ln_mp) * wa.z, (a.w - ln_mp) * wa.w),
-                                                 pack16<T>((b.x - ln_mp) * wb.x, (b.y - ln_mp) * wb.y),
-                                                 pack16<T>((b.z - ln_mp) * wb.z, (b.w - ln_mp) * wb.w));
+            for (int q = 0; q < NQ; q++) {
+              const float4 a = xv[q], wa = lw4[q];
+              *(uint2 *)(f + 32 * q) = make_uint2(pack16<T>((a.x - ln_mp) * wa.x, (a.y - ln_mp) * wa.y),
+                                                  pack16<T>((a.z - ln_mp) * wa.z, (a.w - ln_mp) * wa.w));
             }
           }
         }
         float s32 = 0.0f;
 #pragma unroll
-        for (int q = 0; q < CW / 4; q++) s32 += (xv[q].x + xv[q].y) + (xv[q].z + xv[q].w);
+        for (int q = 0; q < NQ; q++) s32 += (xv[q].x + xv[q].y) + (xv[q].z + xv[q].w);
         double sum = s32;
         sum += __shfl_xor(sum, 1);
         sum += __shfl_xor(sum, 2);
@@ -522,7 +522,7 @@ __device__ __forceinline__ void gemm_nt_tile(const GemmArgs &g, const LnFold &lf
         const float muf = (float)mu;
         float q32 = 0.0f;
 #pragma unroll
-        for (int q = 0; q < CW / 4; q++) {
+        for (int q = 0; q < NQ; q++) {
           const float a = xv[q].x - muf, b = xv[q].y - muf, c = xv[q].z - muf, d = xv[q].w - muf;
           q32 += (a * a + b * b) + (c * c + d * d);
         }
