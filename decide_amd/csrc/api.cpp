@@ -216,7 +216,7 @@ int upload_layout(dn_ctx *c, const HostLayout &hl, const Workspace &w, int nseq,
 // The context's own workspace: layout arrays (re-uploaded only when the batch
 // layout changes) and activation buffers for T tokens and R rows.
 // Folded LayerNorm: attn_norm and mlp_norm of the large-batch bf16 forward
-// run inside the GEMMs around them (GemmArgs::fx .. eps): the residual GEMM
+// run inside the GEMMs around them (LnFold, the EPI_*_LN forms): the residual GEMM
 // before the norm writes its operand and row statistics, the GEMM after it
 // applies the row and column terms, and the LayerNorm launch disappears.
 bool fold_geometry(const dn_ctx *c) {

@@ -561,7 +561,7 @@ __device__ __forceinline__ void gemm_nt_tile(const GemmArgs &g, const LnFold &lf
           }
       }
       // rstd * (product - (mean - mprev) * lcs) for the folded LayerNorm
-      // (ln_st was written before the main loop's first barrier).
+      // (ln_st and ln_cs were written before the epilogue's barrier).
       float ln_rs[LNC ? TM : 1], ln_dm[LNC ? TM : 1];
       if constexpr (LNC) {
 #pragma unroll
