@@ -687,14 +687,14 @@ def main() -> int:
     # algorithmic bytes per launch are A, the weights, and the fp32 residual
     # read and written (T x H each way); with the folded LayerNorm (bf16,
     # T > 1024) also the next norm's bf16 operand (T x H) and the row
-    # statistics (16 bytes per row and 192 columns) it writes. By the roofline
+    # statistics (8 bytes per row and 192 columns) it writes. By the roofline
     # model it is bound by HBM (its bytes take longer at 8 TB/s than its flops
     # at the MFMA peak).
     fold = bool(args.ln_fold) and prec == "bf16" and T > 1024
     res_s = (avg["gemm_wo"] + avg["gemm_mlpwo"]) * 1e-3
     res_bytes = esz * (T * H + H * H) + esz * (T * I + H * I) + 2 * 2 * 4 * T * H
     if fold:
-        res_bytes += 2 * (esz * T * H + 16 * T * (H // 192))
+        res_bytes += 2 * (esz * T * H + 8 * T * (H // 192))
     res_flop = 2.0 * T * H * (H + I)
     wi_flop = 2.0 * T * (2 * I) * H
     wi_bytes = esz * (T * H + 2 * I * H + T * I)
@@ -1039,11 +1039,11 @@ def summarize_traffic(fetch_dir: str, write_dir: str, out_path: str) -> int:
     alg = {"residual": (2 * (T * H + H * H) + 2 * (T * I + H * I) + 16 * T * H) / 2,
            "wi": 2 * (T * H + 2 * I * H + T * I), "qkv": 2 * (T * H + 3 * H * H + 3 * T * H)}
     # The folded-LayerNorm forms (when the run launched them): the residual
-    # GEMM also writes the bf16 operand and 16 bytes of statistics per row
+    # GEMM also writes the bf16 operand and 8 bytes of statistics per row
     # and 192 columns; QKV and Wi read those statistics and a row mean and
-    # write a row mean (72 bytes per row).
-    alg_fold = {"residual": alg["residual"] + 2 * T * H + 16 * T * (H // 192),
-                "wi": alg["wi"] + 72 * T, "qkv": alg["qkv"] + 72 * T}
+    # write a row mean (40 bytes per row).
+    alg_fold = {"residual": alg["residual"] + 2 * T * H + 8 * T * (H // 192),
+                "wi": alg["wi"] + 40 * T, "qkv": alg["qkv"] + 40 * T}
     kernels = {}
     for name in ROOF_TILES:
         cands, fold = [], False

@@ -231,7 +231,7 @@ bool fold_eligible(const dn_ctx *c, int T) {
 
 size_t fold_bytes_per_token(const dn_ctx *c) {
   if (!fold_geometry(c)) return 0;
-  return sizeof(double) * 2 * (c->cfg.hidden / kLnPartCols) + sizeof(float) * 2;
+  return sizeof(float) * 2 * (c->cfg.hidden / kLnPartCols) + sizeof(float) * 2;
 }
 
 // The consumer GEMMs' column sums of layer l: QKV's (attn_norm, layers >= 1)
@@ -262,7 +262,7 @@ int ensure_fold_cs(dn_ctx *c, hipStream_t s) {
 // context never folds).
 int ensure_fold_buffers(dn_ctx *c, size_t T) {
   if (!fold_geometry(c) || !c->ln_fold) return DN_OK;
-  HIPCHK(c, "hipMalloc", ensure(c->fold_part, sizeof(double) * 2 * (c->cfg.hidden / kLnPartCols) * T));
+  HIPCHK(c, "hipMalloc", ensure(c->fold_part, sizeof(float) * 2 * (c->cfg.hidden / kLnPartCols) * T));
   HIPCHK(c, "hipMalloc", ensure(c->fold_mean, sizeof(float) * 2 * T));
   return DN_OK;
 }
@@ -325,7 +325,7 @@ int ctx_workspace(dn_ctx *c, int nseq, const int32_t *seq_len, int R, Workspace 
   if (fold_eligible(c, (int)T)) {
     const int rc = ensure_fold_buffers(c, T);
     if (rc) return rc;
-    o.lpart = (double *)c->fold_part.p;
+    o.lpart = (float *)c->fold_part.p;
     o.lmean1 = (float *)c->fold_mean.p;
     o.lmean2 = (float *)c->fold_mean.p + T;
   }
@@ -1011,7 +1011,7 @@ int forward_split(dn_ctx *c, int nseq, const int32_t *seq_len, const int32_t *d_
     w.act = (char *)c->act.p + es * t0 * I;
     w.kinfo = (int *)c->kinfo.p + t0;
     if (fold) {
-      w.lpart = (double *)c->fold_part.p + t0 * 2 * (H / kLnPartCols);
+      w.lpart = (float *)c->fold_part.p + t0 * 2 * (H / kLnPartCols);
       w.lmean1 = (float *)c->fold_mean.p + t0;
       w.lmean2 = (float *)c->fold_mean.p + T + t0;
     }

@@ -251,7 +251,7 @@ struct GemmArgs {
 // forwards' ~160 launches feel). The residual GEMM (EPI_F32_LN) also writes
 // fx = bf16((x - mprev[row]) * lw[col]) of the new residual x (row stride
 // ldc) and, per row and 192-column N-tile, the tile's (mean, M2) of x to
-// lpart (lparts pairs per row). The GEMM that takes fx as A (EPI_STORE_LN,
+// lpart (lparts float pairs per row). The GEMM that takes fx as A (EPI_STORE_LN,
 // EPI_GEGLU_LN) merges them into the row's mean and rstd = 1/sqrt(M2/K +
 // eps) and computes rstd * (A.B^T - (mean - mprev[row]) * lcs[col]) with
 // lcs[n] = sum_k lw[k] B[n][k], i.e. LayerNorm(x).B^T with the LayerNorm
@@ -260,7 +260,7 @@ struct GemmArgs {
 struct LnFold {
   void *fx;
   const float *lw, *lcs, *mprev;
-  double *lpart;
+  float *lpart;
   float *mean_out;
   int lparts;
   float eps;

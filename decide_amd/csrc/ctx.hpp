@@ -108,7 +108,7 @@ struct Workspace {
   // Folded LayerNorm (bf16, more than 1024 tokens): per row the residual
   // GEMM's (mean, M2) pairs over each 192 columns ([T x H/192]), and the
   // row means of a layer's attn_norm and mlp_norm ([T] each); null: no fold.
-  double *lpart = nullptr;
+  float *lpart = nullptr;
   float *lmean1 = nullptr, *lmean2 = nullptr;
   int *seq_off = nullptr, *seq_len = nullptr, *chunk_off = nullptr, *first = nullptr;
   int4 *chunk_desc = nullptr, *work = nullptr;

@@ -143,7 +143,9 @@ __device__ __forceinline__ void store_staged(const T *st, T *C, int ldc, int m0,
 }
 
 // Folded LayerNorm, consumer side. ln_fold_load fetches row `row`'s
-// per-part (mean, M2) pairs and mprev (issued before the first stages' DMA,
+// per-part (mean, M2) pairs (fp32: each of a row block's N-tiles reads
+// them, so their bytes pass the memory path many times) and mprev (issued
+// before the first stages' DMA,
 // whose issue is not delayed by them); ln_fold_merge combines the pairs by
 // the pairwise update of Chan, Golub and LeVeque for equal counts (the mean
 // of the part means; M2 = the parts' M2 plus the count times the squared
@@ -152,29 +154,29 @@ __device__ __forceinline__ void store_staged(const T *st, T *C, int ldc, int m0,
 // rounded to float as that kernel rounds them; write_mean also stores the
 // row's mean.
 constexpr int kLnMaxParts = 8;  // launch_gemm checks lparts <= 8
-__device__ __forceinline__ void ln_fold_load(const GemmArgs &g, const LnFold &lf, int row, double2 (&v)[kLnMaxParts],
+__device__ __forceinline__ void ln_fold_load(const GemmArgs &g, const LnFold &lf, int row, float2 (&v)[kLnMaxParts],
                                              float &mp) {
   const int rr = min(row, g.M - 1), np = lf.lparts;
-  const double2 *pp = (const double2 *)lf.lpart + (size_t)rr * np;
+  const float2 *pp = (const float2 *)lf.lpart + (size_t)rr * np;
 #pragma unroll
   for (int t = 0; t < kLnMaxParts; t++)
     if (t < np) v[t] = pp[t];
   mp = lf.mprev ? lf.mprev[rr] : 0.0f;
 }
 __device__ __forceinline__ float2 ln_fold_merge(const GemmArgs &g, const LnFold &lf, int row,
-                                                const double2 (&v)[kLnMaxParts], float mp, bool write_mean) {
+                                                const float2 (&v)[kLnMaxParts], float mp, bool write_mean) {
   const int np = lf.lparts;
   double sum = 0;
 #pragma unroll
   for (int t = 0; t < kLnMaxParts; t++)
-    if (t < np) sum += v[t].x;
+    if (t < np) sum += (double)v[t].x;
   const double mu = sum / np;
   double m2 = 0;
 #pragma unroll
   for (int t = 0; t < kLnMaxParts; t++)
     if (t < np) {
-      const double d = v[t].x - mu;
-      m2 += v[t].y + (double)kLnPartCols * d * d;
+      const double d = (double)v[t].x - mu;
+      m2 += (double)v[t].y + (double)kLnPartCols * d * d;
     }
   const float mean = (float)mu;
   if (write_mean && row < g.M) lf.mean_out[row] = mean;
@@ -228,7 +230,7 @@ __device__ __forceinline__ void gemm_nt_tile(const GemmArgs &g, const LnFold &lf
   // mprev) of its rows from ln_st and its columns' lcs from ln_cs.
   float2 *const ln_st = (float2 *)(smem + SMEM_RING);
   float *const ln_cs = (float *)(smem + SMEM_RING + BM * 8);
-  double2 ln_v[LNC ? kLnMaxParts : 1];
+  float2 ln_v[LNC ? kLnMaxParts : 1];
   float ln_mp = 0.0f, ln_c = 0.0f;
   if constexpr (LNC) {
     if (threadIdx.x < BM) ln_fold_load(g, lf, m0 + (int)threadIdx.x, ln_v, ln_mp);
@@ -491,9 +493,9 @@ __device__ __forceinline__ void gemm_nt_tile(const GemmArgs &g, const LnFold &lf
         // chunks above. The next LayerNorm's operand bf16((x - mprev) * w),
         // one 8-byte store per chunk; the statistics over this tile's 192
         // columns: fp32 partial sums, the eight reduced in fp64 in a fixed
-        // order, then the squared deviations from the tile mean the same way
-        // (their fp32 rounding, ~1e-6 relative, is far below the bf16
-        // operand's).
+        // order, then the squared deviations from the tile mean the same way,
+        // stored as an fp32 pair (their fp32 rounding, ~1e-6 relative, is far
+        // below the bf16 operand's).
         __syncthreads();
         const int r = tid >> 3, part = tid & 7;
         float4 xv[NQ];
@@ -531,7 +533,8 @@ __device__ __forceinline__ void gemm_nt_tile(const GemmArgs &g, const LnFold &lf
         m2 += __shfl_xor(m2, 2);
         m2 += __shfl_xor(m2, 4);
         const int row = m0 + pass * HM + r;
-        if (part == 0 && row < g.M) ((double2 *)lf.lpart)[(size_t)row * lf.lparts + n0 / BN] = make_double2(mu, m2);
+        if (part == 0 && row < g.M)
+          ((float2 *)lf.lpart)[(size_t)row * lf.lparts + n0 / BN] = make_float2((float)mu, (float)m2);
       }
       if (pass + 1 < WGM) {
         load_old(pass + 1);

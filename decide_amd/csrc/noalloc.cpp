@@ -104,7 +104,7 @@ extern "C" int dn_forward_device_noalloc(dn_ctx *c, int nseq, const int32_t *seq
   w.head_d = (float *)take(sizeof(float) * R1 * (H / 2));
   if (T <= kSmallSplitMaxTokens) w.part = (float *)take(sizeof(float) * kSmallSplitParts * Tz * H);
   if (fold_eligible(c, T)) {  // the folded LayerNorm's statistics, as dn_forward_device has them
-    w.lpart = (double *)take(sizeof(double) * 2 * (H / kLnPartCols) * Tz);
+    w.lpart = (float *)take(sizeof(float) * 2 * (H / kLnPartCols) * Tz);
     w.lmean1 = (float *)take(sizeof(float) * Tz);
     w.lmean2 = (float *)take(sizeof(float) * Tz);
   }

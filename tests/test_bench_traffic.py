@@ -54,9 +54,9 @@ def test_summary_scales_sums_and_prefers_fold_forms(tmp_path):
     assert k["residual"]["write_bytes_per_launch"] == 700 * 1024
     T, H, I = 32768, bench.H, bench.I
     plain_res = (2 * (T * H + H * H) + 2 * (T * I + H * I) + 16 * T * H) / 2
-    assert k["residual"]["algorithmic_bytes_per_launch"] == plain_res + 2 * T * H + 16 * T * (H // 192)
+    assert k["residual"]["algorithmic_bytes_per_launch"] == plain_res + 2 * T * H + 8 * T * (H // 192)
     assert k["qkv"]["symbol"] == QKV_FOLD
-    assert k["qkv"]["algorithmic_bytes_per_launch"] == 2 * (T * H + 3 * H * H + 3 * T * H) + 72 * T
+    assert k["qkv"]["algorithmic_bytes_per_launch"] == 2 * (T * H + 3 * H * H + 3 * T * H) + 40 * T
     # no folded Wi in this run: the plain form and its algorithmic bytes
     assert k["wi"]["symbol"] == WI_PLAIN and k["wi"]["template_args"][4] == 2
     assert k["wi"]["algorithmic_bytes_per_launch"] == 2 * (T * H + 2 * I * H + T * I)
