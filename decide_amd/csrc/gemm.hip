@@ -434,7 +434,10 @@ __device__ __forceinline__ void gemm_nt_tile(const GemmArgs &g, const LnFold &lf
     constexpr int V = BN / 4;  // float4 per row
     constexpr int ITER = HM * V / NT;
     static_assert(ITER * NT == HM * V, "epilogue shape");
-    static_assert(!LN || (BN == kLnPartCols && NT == 8 * HM), "LayerNorm statistics: 8 threads per 192-column row");
+    // Folded LayerNorm: TPR threads per row of a pass (8 on 256-row tiles).
+    constexpr int TPR = NT / HM, CW = 4 * TPR;
+    static_assert(!LN || (BN == kLnPartCols && TPR * HM == NT && (TPR == 4 || TPR == 8) && BN % CW == 0),
+                  "LayerNorm statistics: 4 or 8 threads per 192-column row");
     const bool vec = (g.ldc & 3) == 0;
     // The residual loads of a pass are issued together (one HBM round trip
     // per pass): pass 0's before its staging, so that their latency overlaps
@@ -453,21 +456,21 @@ __device__ __forceinline__ void gemm_nt_tile(const GemmArgs &g, const LnFold &lf
       }
     };
     load_old(0);
-    // Folded LayerNorm: thread (row tid / 8 of the pass, part tid % 8) takes
-    // the 4-column chunks 4 part + 32 q (q < 6) of the row, so that the eight
-    // threads of a row store 64 contiguous bytes of the bf16 operand per
-    // instruction; the LayerNorm weight at them.
-    constexpr int NQ = BN / 32;
+    // Folded LayerNorm: thread (row tid / TPR of the pass, part tid % TPR)
+    // takes the 4-column chunks 4 part + CW q (q < NQ) of the row, so that
+    // the TPR threads of a row store 8 TPR contiguous bytes of the bf16
+    // operand per instruction; the LayerNorm weight at them.
+    constexpr int NQ = BN / CW;
     float4 lw4[LN ? NQ : 1];
     if constexpr (LN) {
 #pragma unroll
-      for (int q = 0; q < NQ; q++) lw4[q] = *(const float4 *)(lf.lw + n0 + 4 * (tid & 7) + 32 * q);
+      for (int q = 0; q < NQ; q++) lw4[q] = *(const float4 *)(lf.lw + n0 + 4 * (tid % TPR) + CW * q);
     }
 #pragma unroll
     for (int pass = 0; pass < WGM; pass++) {
       float ln_mp = 0.0f;
       if constexpr (LN)
-        if (lf.mprev) ln_mp = lf.mprev[min(m0 + pass * HM + (tid >> 3), g.M - 1)];
+        if (lf.mprev) ln_mp = lf.mprev[min(m0 + pass * HM + tid / TPR, g.M - 1)];
       stage_f32(st, LD, pass);
       __syncthreads();
 #pragma unroll
@@ -489,18 +492,18 @@ __device__ __forceinline__ void gemm_nt_tile(const GemmArgs &g, const LnFold &lf
         }
       }
       if constexpr (LN) {
-        // The pass's rows from the staging area: eight threads per row, the
+        // The pass's rows from the staging area: TPR threads per row, the
         // chunks above. The next LayerNorm's operand bf16((x - mprev) * w),
         // one 8-byte store per chunk; the statistics over this tile's 192
-        // columns: fp32 partial sums, the eight reduced in fp64 in a fixed
+        // columns: fp32 partial sums, the TPR reduced in fp64 in a fixed
         // order, then the squared deviations from the tile mean the same way,
         // stored as an fp32 pair (their fp32 rounding, ~1e-6 relative, is far
         // below the bf16 operand's).
         __syncthreads();
-        const int r = tid >> 3, part = tid & 7;
+        const int r = tid / TPR, part = tid % TPR;
         float4 xv[NQ];
 #pragma unroll
-        for (int q = 0; q < NQ; q++) xv[q] = *(const float4 *)(st + r * LD + 4 * part + 32 * q);
+        for (int q = 0; q < NQ; q++) xv[q] = *(const float4 *)(st + r * LD + 4 * part + CW * q);
         {
           const int row = m0 + pass * HM + r;
           if (row < g.M) {
@@ -508,7 +511,7 @@ __device__ __forceinline__ void gemm_nt_tile(const GemmArgs &g, const LnFold &lf
 #pragma unroll
             for (int q = 0; q < NQ; q++) {
               const float4 a = xv[q], wa = lw4[q];
-              *(uint2 *)(f + 32 * q) = make_uint2(pack16<T>((a.x - ln_mp) * wa.x, (a.y - ln_mp) * wa.y),
+              *(uint2 *)(f + CW * q) = make_uint2(pack16<T>((a.x - ln_mp) * wa.x, (a.y - ln_mp) * wa.y),
                                                   pack16<T>((a.z - ln_mp) * wa.z, (a.w - ln_mp) * wa.w));
             }
           }
@@ -517,9 +520,8 @@ __device__ __forceinline__ void gemm_nt_tile(const GemmArgs &g, const LnFold &lf
 #pragma unroll
         for (int q = 0; q < NQ; q++) s32 += (xv[q].x + xv[q].y) + (xv[q].z + xv[q].w);
         double sum = s32;
-        sum += __shfl_xor(sum, 1);
-        sum += __shfl_xor(sum, 2);
-        sum += __shfl_xor(sum, 4);
+#pragma unroll
+        for (int o = 1; o < TPR; o <<= 1) sum += __shfl_xor(sum, o);
         const double mu = sum / BN;
         const float muf = (float)mu;
         float q32 = 0.0f;
@@ -529,9 +531,8 @@ __device__ __forceinline__ void gemm_nt_tile(const GemmArgs &g, const LnFold &lf
           q32 += (a * a + b * b) + (c * c + d * d);
         }
         double m2 = q32;
-        m2 += __shfl_xor(m2, 1);
-        m2 += __shfl_xor(m2, 2);
-        m2 += __shfl_xor(m2, 4);
+#pragma unroll
+        for (int o = 1; o < TPR; o <<= 1) m2 += __shfl_xor(m2, o);
         const int row = m0 + pass * HM + r;
         if (part == 0 && row < g.M)
           ((float2 *)lf.lpart)[(size_t)row * lf.lparts + n0 / BN] = make_float2((float)mu, (float)m2);
