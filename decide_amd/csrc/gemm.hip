@@ -1350,7 +1350,7 @@ hipError_t launch_gemm_fold(int epi, const GemmArgs &a, const LnFold *ln, hipStr
     return launch_cfg_one<T, 256, 192, 128, 2, 2, EPI_F32_LN, 4>(a, s, 1, ln);
   }
   if (ln->lparts < 1 || ln->lparts > 8 || ln->lparts * kLnPartCols != a.K || !ln->lpart || !ln->lcs ||
-      (epi == EPI_STORE_LN && a.N <= 1024))
+      !ln->mean_out || (epi == EPI_STORE_LN && a.N <= 1024))
     return hipErrorInvalidValue;
   if (epi == EPI_STORE_LN) {
     if (medium) return launch_fold_cfg<T, 128, 128, 64, 3, 3, EPI_STORE_LN>(a, *ln, s);
