@@ -212,7 +212,8 @@ int dn_set_row_tail(dn_ctx *ctx, int min_tokens);
  * residual GEMM before a LayerNorm (Wo, MlpWo) also writes the norm's operand
  * bf16((x - m) * w) of the new residual row x, with m the row mean of the
  * previous LayerNorm and w the norm weight, and per 192 columns the row's
- * fp64 (mean, M2); the GEMM after it (QKV, Wi) merges those into the row's
+ * (mean, M2) as an fp32 pair (reduced in fp64); the GEMM after it (QKV, Wi)
+ * merges those (in fp64) into the row's
  * mean and rstd and computes rstd * (A.B^T - (mean - m) * sum_k w[k] B[n][k]),
  * i.e. LayerNorm(x).B^T, so the LayerNorm launches (a read of the fp32
  * residual stream each) disappear. The logits move by the bf16 rounding of
