@@ -439,9 +439,10 @@ def test_ln_fold_matches_layernorm_kernels(base, engines):
     against the oracle, at the bf16 bar, on batches that take each tile
     configuration of the folded GEMMs: cfg3's 64 x 512 tokens (256 x 192
     residual, 256 x 128 QKV / Wi tiles) on one stream and on two, one cfg4
-    sequence (2,816 tokens: 64 x 192 and 128 x 128 tiles) and 1,025 tokens
-    (the smallest batch that folds; at 1,024 the switch changes nothing, bit
-    for bit). The folded logits are not the unfolded ones (the fold ran);
+    sequence (2,816 tokens: 64 x 192 and 128 x 128 tiles), 4,097 and 6,001
+    tokens (256 x 192 residual, 256 x 128 QKV and 128 x 128 Wi tiles, the last
+    256-row tile holding 1 and 113 rows) and 1,025 tokens (the smallest batch
+    that folds; at 1,024 the switch changes nothing, bit for bit). The folded logits are not the unfolded ones (the fold ran);
     the fp16 and fp32 modes do not fold."""
     from decide_amd.nn import build_sequence
     from decide_amd.synth import config_batch, pack_request
@@ -452,12 +453,16 @@ def test_ln_fold_matches_layernorm_kernels(base, engines):
     b1025 = [build_sequence(pack_request(rng, p, [16] * 8, cfg.vocab), 50284, True) for p in (385, 384)]
     b1024 = [build_sequence(pack_request(rng, 384, [16] * 8, cfg.vocab), 50284, True) for _ in range(2)]
     assert sum(len(s.ids) for s in b1025) == 1025 and sum(len(s.ids) for s in b1024) == 1024
+    b4097 = [build_sequence(pack_request(rng, p, [16] * 8, cfg.vocab), 50284, True) for p in [384] * 7 + [385]]
+    b6001 = [build_sequence(pack_request(rng, p, [16] * 8, cfg.vocab), 50284, True) for p in [384] * 11 + [241]]
+    assert sum(len(s.ids) for s in b4097) == 4097 and sum(len(s.ids) for s in b6001) == 6001
     cfg3 = config_batch("cfg3", vocab=cfg.vocab)
     cfg4 = config_batch("cfg4", vocab=cfg.vocab, nseq=1)
     oracle.set_workers(WORKERS)
     try:
         for name, batch, split, check in (("cfg3 two streams", cfg3, 8192, (0, 37, 63)), ("cfg3 one stream", cfg3, 0, ()),
-                                          ("cfg4 x1", cfg4, 8192, (0,)), ("1025 tokens", b1025, 8192, (0, 1))):
+                                          ("cfg4 x1", cfg4, 8192, (0,)), ("4097 tokens", b4097, 8192, (7,)),
+                                          ("6001 tokens", b6001, 8192, (11,)), ("1025 tokens", b1025, 8192, (0, 1))):
             eng.set_stream_split(split)
             eng.set_ln_fold(False)
             plain = eng.forward(batch)
