@@ -1133,6 +1133,12 @@ hipError_t launch_skinny(int epi, const GemmArgs &a, hipStream_t s) {
   // 32-row tiles while their grid fits one workgroup per CU, else 64-row
   // tiles (QKV at 112 rows: 288 -> 144 workgroups, cfg2 0.917 -> 0.901 ms).
   if (a.M <= 128 && (a.N / 32) * ((a.M + 31) / 32) <= 256) return launch_skinny_cfg<T, 1, 1, 8>(epi, a, s);
+  // fp32 above 128 rows (the validation GEMM, the certification twin's
+  // forward): 32 x 32 tiles for outputs of 2048 columns or more, two
+  // workgroups per CU (512 x 2304 x 768: 39.6 -> 33.5 us; 1024 rows: 64.1 ->
+  // 55.6 us; bit-identical, the same K split over eight waves); the 768-wide
+  // outputs keep 64-row tiles (their 32 x 32 grid: 14.2 -> 15.4 us).
+  if (std::is_same<T, float>::value && a.M > 128 && a.N >= 2048) return launch_skinny_cfg<T, 1, 1, 8>(epi, a, s);
   return launch_skinny_cfg<T, 2, 1, 8>(epi, a, s);
 }
 
