@@ -1128,6 +1128,9 @@ hipError_t launch_skinny(int epi, const GemmArgs &a, hipStream_t s) {
     if (a.M <= 128 && epi == EPI_GEGLU && (a.N / 32) * ((a.M + 31) / 32) <= 256)
       return launch_skinny_cfg<T, 1, 1, 8>(epi, a, s);
     if (a.M <= 128) return launch_skinny_cfg<T, 1, 2, 8>(epi, a, s);
+    // fp32 inference GeGLU above 128 rows also on 32-row tiles (one 512-token
+    // fp32 forward 3.92 -> 3.80 ms against 64 x 64, bit-identical).
+    if (std::is_same<T, float>::value && epi == EPI_GEGLU) return launch_skinny_cfg<T, 1, 2, 8>(epi, a, s);
     return launch_skinny_cfg<T, 2, 2, 8>(epi, a, s);
   }
   // 32-row tiles while their grid fits one workgroup per CU, else 64-row
