@@ -259,14 +259,23 @@ __device__ __forceinline__ void stage_store(const Staging<T, R> &st, char *sK, c
 // LIST: the queries are the option rows of a.items (row_items_kernel): Q
 // read from a.q_rows and the output written at row r, every key tile tested
 // per element.
+// fp32 four-wave workgroups run at two waves per SIMD: at three they spilled
+// 44-62 VGPRs (one 512-token fp32 forward 3.81 -> 3.52 ms without the spills).
 template <class T, int QW, int QT, bool LOCAL, bool LIST = false>
-__global__ __launch_bounds__(64 * QW) __attribute__((amdgpu_waves_per_eu(QT == 1 ? 3 : 2))) void attention_kernel(
+__global__ __launch_bounds__(64 * QW)
+__attribute__((amdgpu_waves_per_eu(sizeof(T) == 4 && QW == ATTN_WAVES ? 2 : QT == 1 ? 3 : 2))) void attention_kernel(
     AttnArgs a) {
   // R staging items per thread; with more than 4 waves only the first 256
   // threads stage. Each wave owns QT 32-query tiles.
   constexpr int NT = 64 * QW, R = QW >= 4 ? 1 : 4 / QW;
   static_assert(QW == 1 || QW == 2 || QW == 4 || QW == 8, "waves per workgroup");
   static_assert(QT * QW <= 8, "tile codes hold 8 query chunks");
+  // Workgroups of fewer than ATTN_WAVES waves (fp32 batches of few work
+  // items) take ATTN_WAVES / QW turns at one work item of ATTN_WAVES 32-query
+  // chunks: part `sub` of the item computes chunks sub * QW .. sub * QW + QW - 1.
+  constexpr int SUB = LIST ? 1 : ATTN_WAVES / QW;
+  static_assert(SUB * QW == ATTN_WAVES || SUB == 1, "work item parts");
+  static_assert(SUB == 1 || QT == 1, "parted work items have one query tile per wave");
   using MF = Mfma<T>;
   typedef typename MF::frag frag;
   constexpr int ROWK = D * sizeof(T) + 16;       // K tile row bytes (key-major)
@@ -292,11 +301,14 @@ __global__ __launch_bounds__(64 * QW) __attribute__((amdgpu_waves_per_eu(QT == 1
   // (work item, head) with the q blocks of one sequence and its 12 heads
   // adjacent: the K/V rows, RoPE factors and chunk summaries they share are
   // reused out of that XCD's L2.
-  const int total = a.nwork * a.heads;
+  const int total = a.nwork * a.heads * SUB;
   const int bid = blockIdx.x;
   int logical = bid;
   if (total % 8 == 0) logical = (bid % 8) * (total / 8) + bid / 8;
+  const int sub = logical % SUB;
+  logical /= SUB;
   const int wi = logical / a.heads, head = logical % a.heads;
+  const int wq = sub * QW + wave;  // this wave's chunk of the work item (QT query tiles each)
   int s, q0 = 0, slot0 = 0, cnt = 0, n, base;
   if constexpr (LIST) {
     if (wi >= *a.nitems) return;  // the grid is sized by an upper bound on the items
@@ -349,7 +361,7 @@ __global__ __launch_bounds__(64 * QW) __attribute__((amdgpu_waves_per_eu(QT == 1
     int qq;
     const T *qrow;
     if constexpr (LIST) {
-      const int idx = (wave * QT + t) * 32 + lr;
+      const int idx = (wq * QT + t) * 32 + lr;
       qvalid[t] = idx < cnt;
       const int r = a.rows[slot0 + (qvalid[t] ? idx : 0)];
       qrow_r[t] = r;
@@ -357,7 +369,7 @@ __global__ __launch_bounds__(64 * QW) __attribute__((amdgpu_waves_per_eu(QT == 1
       qq = min(max(a.row_tok[r] - base, 0), n - 1);
       qrow = (const T *)a.q_rows + (size_t)r * H + head * D;
     } else {
-      const int q = q0 + (wave * QT + t) * 32 + lr;
+      const int q = q0 + (wq * QT + t) * 32 + lr;
       qvalid[t] = q < n;
       qq = qvalid[t] ? q : n - 1;
       qrow = qkv + (size_t)(base + qq) * ld + head * D;
@@ -440,7 +452,7 @@ __global__ __launch_bounds__(64 * QW) __attribute__((amdgpu_waves_per_eu(QT == 1
     // This wave's classes: per query tile t and 32-key half i (uniform
     // across the wave).
     const int mycode =
-        __builtin_amdgcn_readfirstlane((sCode[kt] >> (4 * QT * wave)) & ((1u << (4 * QT)) - 1));
+        __builtin_amdgcn_readfirstlane((sCode[kt] >> (4 * QT * wq)) & ((1u << (4 * QT)) - 1));
     int hcls[QT][2];
 #pragma unroll
     for (int t = 0; t < QT; t++) {
@@ -597,11 +609,11 @@ __global__ __launch_bounds__(64 * QW) __attribute__((amdgpu_waves_per_eu(QT == 1
     const float l_tot = l_run[t] + __shfl_xor(l_run[t], 32);
     const float inv = 1.0f / l_tot;
     if (!LIST && a.lse && qvalid[t] && lh == 0) {
-      const int q = q0 + (wave * QT + t) * 32 + lr;
+      const int q = q0 + (wq * QT + t) * 32 + lr;
       a.lse[(size_t)(base + q) * a.heads + head] = m_run[t] * a.scale_log2 + log2f(l_tot);
     }
     if (qvalid[t]) {
-      const int q = q0 + (wave * QT + t) * 32 + lr;
+      const int q = q0 + (wq * QT + t) * 32 + lr;
       T *out = (T *)a.ctx + (size_t)(LIST ? qrow_r[t] : base + q) * H + head * D;
 #pragma unroll
       for (int i = 0; i < 2; i++)
@@ -1379,6 +1391,19 @@ hipError_t launch_attention_generic(int precision, const AttnArgs &a, hipStream_
 
 template <class T>
 void launch_attention_t(const AttnArgs &a, hipStream_t s) {
+  // fp32 launches of at most 256 (work item, head) pairs (the certification
+  // twin's few sequences, fp32 validation of small requests) leave most CUs
+  // idle: each work item runs as two workgroups of two waves (the same
+  // per-query arithmetic; one 512-token fp32 forward 3.81 -> 3.37 ms, bit-
+  // identical; one-wave parts measured the same).
+  if constexpr (std::is_same<T, float>::value) {
+    if (a.qt == ATTN_QT && a.nwork * a.heads <= 256) {
+      dim3 grid(a.nwork * a.heads * (ATTN_WAVES / 2)), block(128);
+      if (a.sliding) hipLaunchKernelGGL((attention_kernel<T, 2, ATTN_QT, true>), grid, block, 0, s, a);
+      else hipLaunchKernelGGL((attention_kernel<T, 2, ATTN_QT, false>), grid, block, 0, s, a);
+      return;
+    }
+  }
   dim3 grid(a.nwork * a.heads), block(64 * ATTN_WAVES);
   if (a.sliding)
     hipLaunchKernelGGL((attention_kernel<T, ATTN_WAVES, ATTN_QT, true>), grid, block, 0, s, a);
