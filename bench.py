@@ -570,7 +570,7 @@ def main() -> int:
     ap.add_argument("--row-tail", type=int, default=2048, metavar="TOKENS",
                     help="dn_set_row_tail: batches of at least TOKENS finish the last layer on the option rows (0: off)")
     ap.add_argument("--ln-fold", type=int, default=1, choices=(0, 1),
-                    help="dn_set_ln_fold: bf16 batches of more than 1024 tokens run the LayerNorms inside the GEMMs")
+                    help="dn_set_ln_fold: bf16 and fp16 batches of more than 1024 tokens run the LayerNorms inside the GEMMs")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="run one device copy of MIB MiB first (reference kernel for HBM counters)")
     ap.add_argument("--tokenizer", action="store_true",
@@ -685,12 +685,12 @@ def main() -> int:
     # Per-launch roofline views. The kernel with the largest share of GPU
     # time at cfg3 is the fp32-residual GEMM (Wo and MlpWo share its symbol):
     # algorithmic bytes per launch are A, the weights, and the fp32 residual
-    # read and written (T x H each way); with the folded LayerNorm (bf16,
-    # T > 1024) also the next norm's bf16 operand (T x H) and the row
+    # read and written (T x H each way); with the folded LayerNorm (16-bit,
+    # T > 1024) also the next norm's 16-bit operand (T x H) and the row
     # statistics (8 bytes per row and 192 columns) it writes. By the roofline
     # model it is bound by HBM (its bytes take longer at 8 TB/s than its flops
     # at the MFMA peak).
-    fold = bool(args.ln_fold) and prec == "bf16" and T > 1024
+    fold = bool(args.ln_fold) and prec in ("bf16", "fp16") and T > 1024
     res_s = (avg["gemm_wo"] + avg["gemm_mlpwo"]) * 1e-3
     res_bytes = esz * (T * H + H * H) + esz * (T * I + H * I) + 2 * 2 * 4 * T * H
     if fold:
@@ -966,7 +966,7 @@ def extra_configs(eng, cfg, dev, stream, args) -> dict:
 # 32768): the residual GEMMs (N = 768) and the Wi GEMM (N = 2 x 1152).
 ROOF_TILES = {"residual": [256, 192, 128, 2, 0, 2, 4, 2], "wi": [256, 128, 64, 3, 2, 2, 2, 2],
               "qkv": [256, 128, 64, 3, 1, 2, 2, 2]}
-# With the folded LayerNorm (the default bf16 forward above 1024 tokens) the
+# With the folded LayerNorm (the default 16-bit forward above 1024 tokens) the
 # same tiles run the EPI_F32_LN / EPI_GEGLU_LN / EPI_STORE_LN epilogues.
 FOLD_EPI = {"residual": 5, "wi": 7, "qkv": 6}
 

@@ -249,9 +249,9 @@ int ensure_fold_cs(dn_ctx *c, hipStream_t s) {
   for (int l = 0; l < g.layers; l++) {
     const std::string pf = layer_prefix(l);
     if (l > 0)
-      HIPCHK(c, "fold_colsum", launch_fold_colsum(W(c, pf + "attn.Wqkv.weight"), 3 * H, H,
+      HIPCHK(c, "fold_colsum", launch_fold_colsum(g.precision, W(c, pf + "attn.Wqkv.weight"), 3 * H, H,
                                                   (const float *)W(c, pf + "attn_norm.weight"), fold_cs_qkv(c, l), s));
-    HIPCHK(c, "fold_colsum", launch_fold_colsum(W(c, pf + "mlp.Wi.weight"), 2 * I, H,
+    HIPCHK(c, "fold_colsum", launch_fold_colsum(g.precision, W(c, pf + "mlp.Wi.weight"), 2 * I, H,
                                                 (const float *)W(c, pf + "mlp_norm.weight"), fold_cs_wi(c, l), s));
   }
   c->fold_gen = c->wgen;

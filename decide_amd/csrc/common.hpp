@@ -245,11 +245,11 @@ struct GemmArgs {
                     // (0: whole 128-byte rows through LDS by global->LDS DMA)
 };
 
-// LayerNorm folded into the GEMMs on either side of it (bf16 inference),
+// LayerNorm folded into the GEMMs on either side of it (16-bit inference),
 // the EPI_*_LN forms' second kernel argument (GemmArgs stays at its size:
 // larger kernel arguments cost every launch ~0.6 us, which the small-batch
 // forwards' ~160 launches feel). The residual GEMM (EPI_F32_LN) also writes
-// fx = bf16((x - mprev[row]) * lw[col]) of the new residual x (row stride
+// fx = (x - mprev[row]) * lw[col] in the operand type, of the new residual x (row stride
 // ldc) and, per row and 192-column N-tile, the tile's (mean, M2) of x to
 // lpart (lparts float pairs per row). The GEMM that takes fx as A (EPI_STORE_LN,
 // EPI_GEGLU_LN) merges them into the row's mean and rstd = 1/sqrt(M2/K +
@@ -272,13 +272,13 @@ struct LnFold {
 // output (M x N), and C (M x 2N, operand type, the interleaved Wi layout)
 // receives the gradients of its value and gate inputs, read from gin.
 enum { EPI_F32 = 0, EPI_STORE = 1, EPI_GEGLU = 2, EPI_GEGLU_KEEP = 3, EPI_GEGLU_BWD = 4 };
-// The folded-LayerNorm forms (GemmArgs::fx .. eps; bf16, M > 1024): the
+// The folded-LayerNorm forms (LnFold; bf16 or fp16, M > 1024): the
 // residual GEMM that produces the LayerNorm's input, and the store / GeGLU
 // GEMMs that consume its output.
 enum { EPI_F32_LN = 5, EPI_STORE_LN = 6, EPI_GEGLU_LN = 7 };
 // Columns per LayerNorm statistics part written by EPI_F32_LN.
 constexpr int kLnPartCols = 192;
-// Whether the folded LayerNorm runs for a bf16 model of this geometry at M
+// Whether the folded LayerNorm runs for a 16-bit model of this geometry at M
 // rows (the configurations launch_gemm tiles for EPI_*_LN).
 bool gemm_ln_fold_ok(int precision, int M, int hidden, int inter);
 
@@ -404,9 +404,10 @@ hipError_t launch_prologue(int precision, const int *pos, const int *opt, const 
                            int *kinfo, ChunkInfo *chunks, const int *ids, int Tn, const float *tok, int vocab,
                            const float *w, float eps, int H, float *h, void *xn, int *err, hipStream_t s,
                            float *mean = nullptr, float *rstd = nullptr);
-// Column sums of a LayerNorm-weighted bf16 projection for the folded
+// Column sums of a LayerNorm-weighted bf16 or fp16 projection for the folded
 // LayerNorm: cs[n] = sum_k lw[k] * B[n][k] (fp64 sums), B N x K.
-hipError_t launch_fold_colsum(const void *B, int N, int K, const float *lw, float *cs, hipStream_t s);
+hipError_t launch_fold_colsum(int precision, const void *B, int N, int K, const float *lw, float *cs,
+                              hipStream_t s);
 // LayerNorm launchers; mean / rstd (optional, [rows]) receive the row statistics.
 hipError_t launch_ln(int precision, const float *x, int rows, int H, const float *w, float eps, void *y, hipStream_t s,
                      float *mean = nullptr, float *rstd = nullptr);

@@ -105,7 +105,7 @@ struct Workspace {
   // [kSmallSplitParts x T x H] split-K partial products of the residual
   // GEMMs for batches of at most kSmallSplitMaxTokens tokens; null otherwise.
   float *part = nullptr;
-  // Folded LayerNorm (bf16, more than 1024 tokens): per row the residual
+  // Folded LayerNorm (bf16 / fp16, more than 1024 tokens): per row the residual
   // GEMM's (mean, M2) pairs over each 192 columns ([T x H/192]), and the
   // row means of a layer's attn_norm and mlp_norm ([T] each); null: no fold.
   float *lpart = nullptr;

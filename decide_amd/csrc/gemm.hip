@@ -493,7 +493,7 @@ __device__ __forceinline__ void gemm_nt_tile(const GemmArgs &g, const LnFold &lf
       }
       if constexpr (LN) {
         // The pass's rows from the staging area: TPR threads per row, the
-        // chunks above. The next LayerNorm's operand bf16((x - mprev) * w),
+        // chunks above. The next LayerNorm's operand (x - mprev) * w in T,
         // one 8-byte store per chunk; the statistics over this tile's 192
         // columns: fp32 partial sums, the TPR reduced in fp64 in a fixed
         // order, then the squared deviations from the tile mean the same way,
@@ -575,10 +575,17 @@ __device__ __forceinline__ void gemm_nt_tile(const GemmArgs &g, const LnFold &lf
         }
       }
       auto fin = [&](float v, int i, int j, int e) -> float {
-        if constexpr (LNC)
-          return __builtin_fmaf(-ln_dm[i], cs[j][e], v) * ln_rs[i];
-        else
+        if constexpr (LNC) {
+          float r = __builtin_fmaf(-ln_dm[i], cs[j][e], v) * ln_rs[i];
+          // fp16: the compiler would fuse this product into the conversion
+          // for some outputs (v_fma_mixlo_f16, one rounding instead of two)
+          // and not others, so results would depend on the tile shape; the
+          // empty asm keeps every output a rounded fp32 product.
+          if constexpr (std::is_same<T, f16>::value) asm("" : "+v"(r));
+          return r;
+        } else {
           return v;
+        }
       };
 #pragma unroll
       for (int i = 0; i < TM; i++) {
@@ -1226,13 +1233,13 @@ bool gemm_shape_ok(int precision, int N, int K) {
 }
 
 bool gemm_epi_ok(int precision, int epi, int M) {
-  if (epi >= EPI_F32_LN) return precision == PREC_BF16 && M > 1024;
+  if (epi >= EPI_F32_LN) return prec16(precision) && M > 1024;
   if (epi != EPI_GEGLU_BWD) return true;
   return prec16(precision) ? M > 128 : M > 1024;
 }
 
 bool gemm_ln_fold_ok(int precision, int M, int hidden, int inter) {
-  return precision == PREC_BF16 && M > 1024 && hidden % kLnPartCols == 0 && hidden / kLnPartCols <= 8 &&
+  return prec16(precision) && M > 1024 && hidden % kLnPartCols == 0 && hidden / kLnPartCols <= 8 &&
          3 * hidden > 1024 && (3 * hidden) % 128 == 0 && (2 * inter) % 128 == 0 && inter % 64 == 0;
 }
 
@@ -1371,12 +1378,7 @@ hipError_t launch_gemm_fold(int epi, const GemmArgs &a, const LnFold *ln, hipStr
 
 template <class T>
 hipError_t launch_gemm16(int epi, const GemmArgs &a, hipStream_t s, const LnFold *ln) {
-  if (epi >= EPI_F32_LN) {
-    if constexpr (std::is_same<T, bf16>::value)
-      return launch_gemm_fold<T>(epi, a, ln, s);
-    else
-      return hipErrorInvalidValue;
-  }
+  if (epi >= EPI_F32_LN) return launch_gemm_fold<T>(epi, a, ln, s);
   const bool small = a.M <= 1024;
   {
     if (small) return launch_cfg<T, 64, 128, 128, 4, 1>(epi, a, s);

@@ -467,22 +467,29 @@ hipError_t launch_prologue(int precision, const int *pos, const int *opt, const 
   return hipGetLastError();
 }
 
-// cs[n] = sum_k lw[k] * B[n][k] (B bf16, N x K), summed in fp64 and rounded
+// cs[n] = sum_k lw[k] * B[n][k] (B bf16 or fp16, N x K), summed in fp64 and rounded
 // to float: the column sums of the LayerNorm-weighted projection that a
 // folded LayerNorm's consumer GEMM subtracts. One wave per row n.
-__global__ __launch_bounds__(256) void fold_colsum_kernel(const bf16 *B, int N, int K, const float *lw, float *cs) {
+template <class T>
+__global__ __launch_bounds__(256) void fold_colsum_kernel(const T *B, int N, int K, const float *lw, float *cs) {
   const int n = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
   if (n >= N) return;
-  const uint16_t *b = (const uint16_t *)B + (size_t)n * K;
+  const T *b = B + (size_t)n * K;
   double acc = 0;
-  for (int k = lane; k < K; k += 64) acc += (double)lw[k] * (double)__uint_as_float((uint32_t)b[k] << 16);
+  for (int k = lane; k < K; k += 64) acc += (double)lw[k] * (double)(float)b[k];
   acc = wave_sum(acc);
   if (lane == 0) cs[n] = (float)acc;
 }
 
-hipError_t launch_fold_colsum(const void *B, int N, int K, const float *lw, float *cs, hipStream_t s) {
+hipError_t launch_fold_colsum(int precision, const void *B, int N, int K, const float *lw, float *cs,
+                              hipStream_t s) {
   if (N <= 0) return hipSuccess;
-  hipLaunchKernelGGL(fold_colsum_kernel, dim3((N + 3) / 4), dim3(256), 0, s, (const bf16 *)B, N, K, lw, cs);
+  if (precision == PREC_BF16)
+    hipLaunchKernelGGL(fold_colsum_kernel<bf16>, dim3((N + 3) / 4), dim3(256), 0, s, (const bf16 *)B, N, K, lw, cs);
+  else if (precision == PREC_F16)
+    hipLaunchKernelGGL(fold_colsum_kernel<f16>, dim3((N + 3) / 4), dim3(256), 0, s, (const f16 *)B, N, K, lw, cs);
+  else
+    return hipErrorInvalidValue;
   return hipGetLastError();
 }
 

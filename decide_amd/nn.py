@@ -275,7 +275,7 @@ class Engine:
         check(lib.dn_set_row_tail(self._h, int(min_tokens)), self._h)
 
     def set_ln_fold(self, on: bool) -> None:
-        """dn_set_ln_fold: bf16 forwards of more than 1024 tokens run attn_norm
+        """dn_set_ln_fold: bf16 and fp16 forwards of more than 1024 tokens run attn_norm
         and mlp_norm inside the GEMMs around them (default on)."""
         check(lib.dn_set_ln_fold(self._h, int(bool(on))), self._h)
 

@@ -207,10 +207,10 @@ int dn_set_stream_split(dn_ctx *ctx, int min_tokens);
  * (forward.go:212-243 runs every layer over all tokens, then gathers). */
 int dn_set_row_tail(dn_ctx *ctx, int min_tokens);
 
-/* bf16 inference forwards of more than 1024 tokens (or parts of a two-stream
+/* bf16 and fp16 inference forwards of more than 1024 tokens (or parts of a two-stream
  * forward) run attn_norm and mlp_norm folded into the GEMMs around them: the
  * residual GEMM before a LayerNorm (Wo, MlpWo) also writes the norm's operand
- * bf16((x - m) * w) of the new residual row x, with m the row mean of the
+ * ((x - m) * w in the operand type) of the new residual row x, with m the row mean of the
  * previous LayerNorm and w the norm weight, and per 192 columns the row's
  * (mean, M2) as an fp32 pair (reduced in fp64); the GEMM after it (QKV, Wi)
  * merges those (in fp64) into the row's

@@ -442,8 +442,8 @@ def test_ln_fold_matches_layernorm_kernels(base, engines):
     sequence (2,816 tokens: 64 x 192 and 128 x 128 tiles), 4,097 and 6,001
     tokens (256 x 192 residual, 256 x 128 QKV and 128 x 128 Wi tiles, the last
     256-row tile holding 1 and 113 rows) and 1,025 tokens (the smallest batch
-    that folds; at 1,024 the switch changes nothing, bit for bit). The folded logits are not the unfolded ones (the fold ran);
-    the fp16 and fp32 modes do not fold."""
+    that folds; at 1,024 the switch changes nothing, bit for bit). The folded logits are not the unfolded ones (the fold ran).
+    fp16 folds the same way (1,025 tokens); the fp32 mode does not fold."""
     from decide_amd.nn import build_sequence
     from decide_amd.synth import config_batch, pack_request
 
@@ -456,6 +456,7 @@ def test_ln_fold_matches_layernorm_kernels(base, engines):
     b4097 = [build_sequence(pack_request(rng, p, [16] * 8, cfg.vocab), 50284, True) for p in [384] * 7 + [385]]
     b6001 = [build_sequence(pack_request(rng, p, [16] * 8, cfg.vocab), 50284, True) for p in [384] * 11 + [241]]
     assert sum(len(s.ids) for s in b4097) == 4097 and sum(len(s.ids) for s in b6001) == 6001
+    off1025 = np.concatenate([[0], np.cumsum([len(s.mask_pos) for s in b1025])])
     cfg3 = config_batch("cfg3", vocab=cfg.vocab)
     cfg4 = config_batch("cfg4", vocab=cfg.vocab, nseq=1)
     oracle.set_workers(WORKERS)
@@ -480,11 +481,22 @@ def test_ln_fold_matches_layernorm_kernels(base, engines):
         plain = eng.forward(b1024)
         eng.set_ln_fold(True)
         assert np.array_equal(eng.forward(b1024), plain)
+        # fp16 folds as bf16 does (checked at the 16-bit bar against its
+        # LayerNorm kernels and the oracle); fp32 does not fold.
         for p in ("fp16", "fp32"):
             engines[p].set_ln_fold(False)
             plain = engines[p].forward(b1025)
             engines[p].set_ln_fold(True)
-            assert np.array_equal(engines[p].forward(b1025), plain), p
+            folded = engines[p].forward(b1025)
+            if p == "fp32":
+                assert np.array_equal(folded, plain), p
+                continue
+            d = np.abs(folded.astype(np.float64) - plain)
+            print(f"ln fold, fp16 1025 tokens: max |dlogit| folded vs LayerNorm kernels {float(d.max()):.3g}", flush=True)
+            assert not np.array_equal(folded, plain), p
+            compare(folded, plain.astype(np.float64), b1025, p)
+            for i in (0, 1):
+                compare(folded[off1025[i]: off1025[i + 1]], orc.forward([b1025[i]]), [b1025[i]], p)
     finally:
         eng.set_ln_fold(True)
         eng.set_stream_split(8192)
